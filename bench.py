@@ -1,0 +1,357 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X SparseCore embedding path.
+
+A step is one pass of the hot path over one synthetic batch that is already
+resident in HBM: the forward lookup (scemb_sparse_dense_matmul) and the
+backward pass fused with the Adagrad update
+(scemb_sparse_dense_matmul_grad_with_adagrad) of every stacked table. The CSR
+buffers come from the GPU preprocessing, which is timed separately
+(`preprocess_ms`). Default workload: the 26-table DLRM shape (one stack, dim
+128, batch 65,536, one Zipf(1.1) id per feature and sample, sum combiner,
+Adagrad lr 0.01 / accumulator 0.1).
+
+Prints one JSON line (see the field comments in `main`).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "jax-tpu-embedding_amd")):
+  if _p not in sys.path:
+    sys.path.insert(0, _p)
+
+METRIC = ("embedding lookups/sec + achieved HBM GB/s (fwd+bwd+Adagrad), "
+          "26-table DLRM shape")
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg):
+  print(msg, file=sys.stderr, flush=True)
+
+
+def zipf_ids(rng, a, vocab, size):
+  """Truncated Zipf: k ~ zipf(a), rejected when k > vocab, id = k - 1."""
+  out = np.empty(size, np.int64)
+  filled = 0
+  while filled < size:
+    k = rng.zipf(a, size=max(1024, 2 * (size - filled)))
+    k = k[k <= vocab]
+    take = min(size - filled, len(k))
+    out[filled:filled + take] = k[:take] - 1
+    filled += take
+  return out.astype(np.int32)
+
+
+class Workload:
+  """Specs, host inputs and metadata of one benchmark configuration."""
+
+  def __init__(self, name, feature_specs, features, weights, optimizer_name,
+               lr, description):
+    self.name = name
+    self.feature_specs = feature_specs
+    self.features = features
+    self.weights = weights
+    self.optimizer_name = optimizer_name
+    self.lr = lr
+    self.description = description
+
+
+def dlrm26(seed=0, batch=65536, num_tables=26, dim=128):
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
+  from jax_tpu_embedding.sparsecore.lib.nn import table_stacking  # pylint: disable=g-import-not-at-top
+
+  rng = np.random.default_rng(seed)
+  vocabs = np.floor(np.exp(rng.uniform(np.log(10), np.log(4e7),
+                                       size=num_tables))).astype(np.int64)
+  opt = embedding_spec.AdagradOptimizerSpec(learning_rate=0.01,
+                                            initial_accumulator_value=0.1)
+  n_total = num_tables * batch
+  limit = (n_total + 7) // 8 * 8
+  tables = [
+      embedding_spec.TableSpec(
+          name=f"t{t:02d}", vocabulary_size=int(vocabs[t]), embedding_dim=dim,
+          initializer=embedding_spec.normal(0.01), optimizer=opt,
+          combiner="sum", max_ids_per_partition=limit,
+          max_unique_ids_per_partition=limit) for t in range(num_tables)
+  ]
+  feats = [
+      embedding_spec.FeatureSpec(name=f"f{t:02d}", table_spec=tables[t],
+                                 input_shape=[batch, 1],
+                                 output_shape=[batch, dim])
+      for t in range(num_tables)
+  ]
+  table_stacking.stack_tables(
+      feats, [t.name for t in tables], global_device_count=1,
+      num_sc_per_device=1, stack_name="dlrm26",
+      stack_to_max_ids_per_partition=lambda n, b: limit,
+      stack_to_max_unique_ids_per_partition=lambda n, b: limit)
+  features = [zipf_ids(rng, 1.1, int(vocabs[t]), batch).reshape(batch, 1)
+              for t in range(num_tables)]
+  return Workload(
+      "dlrm26", feats, features, None, "adagrad", 0.01,
+      {"workload": "dlrm26: 26 tables dim 128 stacked into one HBM buffer, "
+                   "vocab log-uniform [10, 4e7] (seed 0), batch 65536, "
+                   "1 Zipf(1.1) id per feature, sum, Adagrad lr 0.01",
+       "tables": num_tables, "dim": dim, "batch": batch,
+       "stack_rows": int(sum((v + 7) // 8 * 8 for v in vocabs))})
+
+
+def run_gpu(w: Workload, steps: int, warmup: int):
+  import torch  # pylint: disable=g-import-not-at-top
+
+  from jax_tpu_embedding.sparsecore import _native  # pylint: disable=g-import-not-at-top
+  from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_csr as fwd  # pylint: disable=g-import-not-at-top
+  from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_adagrad as ada  # pylint: disable=g-import-not-at-top
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-import-not-at-top
+
+  torch.cuda.set_device(0)
+  dev = torch.device("cuda", 0)
+  stacked = embedding.get_stacked_table_specs(w.feature_specs)
+  # Inputs resident in HBM before anything is timed.
+  feats_dev = [torch.from_numpy(f).to(dev) for f in w.features]
+  torch.cuda.synchronize()
+  # GPU preprocessing (reported separately): median of 5 after 2 warmups.
+  pre_times = []
+  for i in range(7):
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    pre, stats = embedding.preprocess_sparse_dense_matmul_input(
+        feats_dev, None, w.feature_specs, 1, 1, num_sc_per_device=1)
+    torch.cuda.synchronize()
+    if i >= 2:
+      pre_times.append(time.perf_counter() - t0)
+  preprocess_ms = float(np.median(pre_times) * 1e3)
+  log(f"preprocess: {preprocess_ms:.3f} ms (median of {len(pre_times)})")
+  gen = torch.Generator(device=dev)
+  gen.manual_seed(1234)
+  tables = {}
+  per_stack = {}
+  lookups = 0
+  for name, spec in stacked.items():
+    rows, dim = spec.stack_vocab_size, spec.stack_embedding_dim
+    t = torch.empty((rows, dim), dtype=torch.float32, device=dev)
+    t.normal_(0.0, 0.01, generator=gen)
+    a = torch.full((rows, dim), 0.1, dtype=torch.float32, device=dev)
+    bs = spec.total_sample_count
+    g = torch.empty((bs, dim), dtype=torch.float32, device=dev)
+    g.normal_(0.0, 1.0, generator=gen)
+    tables[name] = (t, a, g)
+    rp = pre.lhs_row_pointers[name]
+    eid = pre.lhs_embedding_ids[name]
+    n_valid = int(rp[0].item())  # S = NS = 1: one partition
+    uniq = int(torch.unique(eid[:n_valid]).numel())
+    per_stack[name] = {"N": n_valid, "U": uniq, "Bs": bs, "D": dim,
+                       "rows": rows}
+    lookups += sum(int(np.asarray(f).size) for f, fs in
+                   zip(w.features, w.feature_specs)
+                   if fs.table_spec.stacked_table_spec.stack_name == name)
+    log(f"stack {name}: rows={rows} dim={dim} N={n_valid} U={uniq} Bs={bs}")
+  lr = torch.tensor(w.lr, dtype=torch.float32, device=dev)
+
+  def step():
+    for name, spec in stacked.items():
+      t, a, g = tables[name]
+      csr = (pre.lhs_row_pointers[name], pre.lhs_embedding_ids[name],
+             pre.lhs_sample_ids[name], pre.lhs_gains[name])
+      fwd.tpu_sparse_dense_matmul_csr_primitive.bind(
+          *csr, 1, t, device_batch_size=spec.total_sample_count,
+          max_ids_per_partition=spec.max_ids_per_partition,
+          max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
+          num_sc_per_device=1)
+      ada.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
+          *csr, 1, t, a, g, lr,
+          max_ids_per_partition=spec.max_ids_per_partition,
+          max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
+          num_sc_per_device=1)
+
+  for _ in range(warmup):
+    step()
+  torch.cuda.synchronize()
+  _native.profile_enable(True)
+  _native.profile_collect(None)
+  torch.cuda.synchronize()
+  t0 = time.perf_counter()
+  for _ in range(steps):
+    step()
+  torch.cuda.synchronize()
+  t1 = time.perf_counter()
+  _native.profile_enable(False)
+  spans = {}
+  for k in ("fwd_gather", "bwd_update", "fwd_call", "bwd_call"):
+    ms, n = _native.profile_collect(k)
+    spans[k] = (ms / n if n else None, n)
+  ms_per_step = (t1 - t0) * 1e3 / steps
+  return {
+      "ms_per_step": ms_per_step,
+      "lookups": lookups,
+      "preprocess_ms": preprocess_ms,
+      "spans": spans,
+      "per_stack": per_stack,
+      "dropped": int(sum(stats.id_drop_counters.values())),
+  }
+
+
+def algorithmic_bytes(per_stack):
+  """Compulsory HBM bytes of the forward and of backward + Adagrad."""
+  fwd = bwd = 0
+  for s in per_stack.values():
+    n, u, bs, d = s["N"], s["U"], s["Bs"], s["D"]
+    fwd += 12 * n + 4 * d * u + 4 * d * bs
+    bwd += 12 * n + 4 * d * bs + 16 * d * u
+  return fwd, bwd
+
+
+def cpu_baseline(w: Workload, sample_batch: int, seconds: float):
+  """The oracle (C++ restatement of the reference CPU path) on host cores,
+  on the first `sample_batch` samples of every feature."""
+  from oracle import refcpu  # pylint: disable=g-import-not-at-top
+
+  threads = min(16, os.cpu_count() or 1)
+  feats = [f[:sample_batch] for f in w.features]
+  # Same stacking geometry with the sample's batch size.
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
+  import copy  # pylint: disable=g-import-not-at-top
+
+  # Same stacking geometry with the sample's batch: each feature keeps its
+  # slot in the stack, its row offset scales with the batch.
+  specs = []
+  for fs in w.feature_specs:
+    nfs = copy.copy(fs)
+    nfs.input_shape = [sample_batch] + list(fs.input_shape[1:])
+    tr = fs.id_transformation
+    slot = tr.row_offset // fs.input_shape[0]
+    nfs._id_transformation = embedding_spec.FeatureIdTransformation(  # pylint: disable=protected-access
+        row_offset=slot * sample_batch, col_offset=tr.col_offset,
+        col_shift=tr.col_shift)
+    specs.append(nfs)
+  stacked = {}
+  for fs in specs:
+    st = fs.table_spec.stacked_table_spec
+    stacked[st.stack_name] = st
+  t0 = time.perf_counter()
+  ref = refcpu.preprocess(feats, None, specs, 1, 1, num_sc_per_device=1)
+  pre_s = time.perf_counter() - t0
+  total_lookups = sum(f.size for f in feats)
+  busy = 0.0
+  iters = 0
+  rng = np.random.default_rng(5)
+  state = {}
+  for name, st in stacked.items():
+    rows, dim = st.stack_vocab_size, st.stack_embedding_dim
+    # calloc'd: only the rows the sample touches are ever paged in.
+    table = np.zeros((rows, dim), np.float32)
+    acc = np.zeros((rows, dim), np.float32)
+    n = int(ref.row_pointers[name][0])
+    touched = np.unique(ref.embedding_ids[name][:n])
+    table[touched] = rng.normal(0, 0.01, size=(len(touched), dim))
+    acc[touched] = 0.1
+    bs = len(feats) * sample_batch
+    grad = rng.normal(0, 1, size=(bs, dim)).astype(np.float32)
+    state[name] = (table, acc, grad, bs)
+  while busy < seconds or iters < 3:
+    t0 = time.perf_counter()
+    for name in stacked:
+      table, acc, grad, bs = state[name]
+      args = (ref.row_pointers[name], ref.embedding_ids[name],
+              ref.sample_ids[name], ref.gains[name])
+      refcpu.sparse_dense_matmul(*args, table, bs, num_sc_per_device=1,
+                                 num_scs=1, threads=threads)
+      refcpu.sparse_dense_matmul_grad(*args, grad, table, acc,
+                                      learning_rate=w.lr, num_sc_per_device=1,
+                                      num_scs=1, threads=threads, inplace=True)
+    busy += time.perf_counter() - t0
+    iters += 1
+  return {
+      "value": total_lookups * iters / busy,
+      "unit": "lookups/s",
+      "cores": threads,
+      "kind": "port",
+      "sample": (f"first {sample_batch} samples of each of the "
+                 f"{len(feats)} features ({total_lookups} lookups), "
+                 f"{iters} fwd+bwd+Adagrad passes in {busy:.1f} s; oracle "
+                 f"preprocessing of the sample {pre_s * 1e3:.1f} ms on 1 "
+                 "thread"),
+      "preprocess_ms_per_1k_lookups": pre_s * 1e3 / total_lookups * 1e3,
+  }
+
+
+def main():
+  ap = argparse.ArgumentParser()
+  ap.add_argument("--gpus", type=int, default=1)
+  ap.add_argument("--steps", type=int, default=20)
+  ap.add_argument("--warmup", type=int, default=5)
+  ap.add_argument("--cpu-seconds", type=float, default=10.0)
+  ap.add_argument("--cpu-sample-batch", type=int, default=8192)
+  ap.add_argument("--no-cpu-baseline", action="store_true")
+  args = ap.parse_args()
+  if args.gpus != 1:
+    print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+          "(this build has no multi-GPU path).", file=sys.stderr)
+    sys.exit(2)
+  t_setup = time.perf_counter()
+  w = dlrm26()
+  log(f"workload built in {time.perf_counter() - t_setup:.1f} s")
+  res = run_gpu(w, args.steps, args.warmup)
+  fwd_bytes, bwd_bytes = algorithmic_bytes(res["per_stack"])
+  step_s = res["ms_per_step"] / 1e3
+  fwd_ms = res["spans"]["fwd_gather"][0]
+  bwd_ms = res["spans"]["bwd_update"][0]
+  if bwd_ms is not None and (fwd_ms is None or bwd_ms >= fwd_ms):
+    dom, dom_ms, dom_bytes = "bwd_update", bwd_ms, bwd_bytes
+  else:
+    dom, dom_ms, dom_bytes = "fwd_gather", fwd_ms, fwd_bytes
+  achieved = dom_bytes / (dom_ms / 1e3) / 1e9
+  roofline = {
+      "bound": "hbm",
+      "kernel": dom,
+      "achieved": round(achieved, 1),
+      "peak": PEAK_HBM_GBS,
+      "unit": "GB/s",
+      "frac": round(achieved / PEAK_HBM_GBS, 4),
+      "traffic": None,
+      "kernel_ms": round(dom_ms, 4),
+      "algorithmic_bytes": int(dom_bytes),
+  }
+  cpu = None
+  if not args.no_cpu_baseline:
+    cpu = cpu_baseline(w, args.cpu_sample_batch, args.cpu_seconds)
+  spans = {k: (round(v[0], 4) if v[0] is not None else None)
+           for k, v in res["spans"].items()}
+  out = {
+      "metric": METRIC,
+      "value": round(res["lookups"] / step_s, 1),
+      "unit": "lookups/s",
+      "n_gpus": 1,
+      "steps": args.steps,
+      "warmup": args.warmup,
+      "ms_per_step": round(res["ms_per_step"], 4),
+      "higher_is_better": True,
+      "scaling": "weak",
+      "vs_baseline": None,
+      "dtype": "f32",
+      "data": "synthetic (seeded numpy ids, N(0,0.01) tables, N(0,1) grads)",
+      "config": w.description,
+      "achieved_step_hbm_gbs": round((fwd_bytes + bwd_bytes) / step_s / 1e9,
+                                     1),
+      "step_hbm_frac": round((fwd_bytes + bwd_bytes) / step_s / 1e9 /
+                             PEAK_HBM_GBS, 4),
+      "algorithmic_bytes_per_step": int(fwd_bytes + bwd_bytes),
+      "kernel_avg_ms": spans,
+      "preprocess_ms": round(res["preprocess_ms"], 3),
+      "csr": res["per_stack"],
+      "roofline": roofline,
+      "cpu_baseline": cpu,
+  }
+  print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+  main()

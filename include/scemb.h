@@ -1,0 +1,212 @@
+/* scemb.h - C ABI of libscemb, the MI355X (gfx950) SparseCore embedding path.
+ *
+ * Plain pointers and sizes only. Device pointers are HIP device memory; the
+ * `stream` arguments are hipStream_t values passed as void*. Every entry point
+ * only enqueues work on `stream` (no host synchronisation, no allocation
+ * beyond the caller's workspace) unless its comment says otherwise, and
+ * returns SCEMB_OK or an error code with a message in scemb_last_error().
+ * Nothing in the library aborts the process.
+ *
+ * Reference interfaces replaced (paths relative to
+ * jax_tpu_embedding/sparsecore/ in jax-ml/jax-tpu-embedding):
+ *   scemb_sparse_dense_matmul              custom call "SparseDenseMatmulOp",
+ *       lowered at lib/core/primitives/sparse_dense_matmul_csr.py:171-201
+ *   scemb_sparse_dense_matmul_grad_with_sgd  custom call
+ *       "SparseDenseMatmulGradOpWithOptimizerUpdate" with the SGD update
+ *       computation, lib/core/primitives/sparse_dense_matmul_grad_with_sgd.py:
+ *       194-227 (update fn :145-192)
+ *   scemb_sparse_dense_matmul_grad_with_adagrad  the same custom call with
+ *       the Adagrad update, lib/core/primitives/
+ *       sparse_dense_matmul_grad_with_adagrad.py:235-275 (update fn :167-233)
+ *   scemb_preprocess_stacked_table         PreprocessSparseDenseMatmulInput
+ *       for one stacked table, lib/core/input_preprocessing.h:62-68 /
+ *       input_preprocessing.cc:800-959, as bound by
+ *       lib/core/pybind_input_preprocessing.cc:124-188
+ *   scemb_compute_*                         size helpers of
+ *       lib/core/pybind_input_preprocessing.cc:203-262 (bound at :311-320)
+ */
+#ifndef SCEMB_H_
+#define SCEMB_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define SCEMB_OK 0
+#define SCEMB_ERR_INVALID_ARGUMENT 1 /* Python: ValueError */
+#define SCEMB_ERR_NOT_IMPLEMENTED 2
+#define SCEMB_ERR_WORKSPACE 3        /* workspace missing or too small */
+#define SCEMB_ERR_DEVICE 4           /* HIP runtime error */
+#define SCEMB_ERR_LIMIT_EXCEEDED 5   /* ids over the partition limits with
+                                        dropping disabled (the reference
+                                        LOG(FATAL)s); Python: RuntimeError */
+
+/* Bits OR-ed into the optional device status word by the kernels. */
+#define SCEMB_STATUS_BAD_ENTRY 1u    /* CSR entry with an embedding id or
+                                        sample id out of range: skipped */
+#define SCEMB_STATUS_BAD_ID 2u       /* preprocessing input id outside
+                                        [0, col_id_bound): skipped */
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* scemb_last_error(void);
+
+/* Library version, (major << 16) | minor. */
+int scemb_version(void);
+
+/* One device's CSR-wrapped COO buffers for one stacked table
+ * (SparseDenseMatmulInput; layout documented at
+ * lib/core/input_preprocessing_util.cc:167-208). For local SparseCore s and
+ * partition p, entries j in [roundup8(rp[s*R + p - 1]) (0 for p = 0),
+ * rp[s*R + p]) of segment s (positions s*coo_size/num_segments + j) hold
+ * (embedding id, sample id, gain). */
+typedef struct scemb_csr {
+  const int32_t* row_pointers;  /* [num_segments * row_pointers_per_segment] */
+  const int32_t* embedding_ids; /* [coo_size] */
+  const int32_t* sample_ids;    /* [coo_size] */
+  const float* gains;           /* [coo_size] */
+  int64_t coo_size;
+  int32_t num_segments;             /* num_sc_per_device */
+  int32_t num_partitions;           /* num_sc_per_device * global devices */
+  int32_t row_pointers_per_segment; /* max(num_partitions, 8) */
+  int32_t reserved;
+} scemb_csr_t;
+
+/* ---- Forward: SparseDenseMatmulOp --------------------------------------
+ * activations[b, :] = sum over entries with s*bps + sample_id == b of
+ *   gain * table[p * (table_rows / num_partitions) + embedding_id, :],
+ * bps = device_batch_size / num_segments; rows without entries are zero.
+ * `table` is [table_rows, dim] row-major (dim 1 for a 1-D table). Entries
+ * whose ids fall outside the table or batch are skipped and flagged in
+ * *device_status (optional, may be NULL). Sums run in CSR order per row. */
+size_t scemb_sparse_dense_matmul_workspace_size(const scemb_csr_t* csr,
+                                                int64_t device_batch_size,
+                                                int64_t table_rows,
+                                                int32_t dim);
+int scemb_sparse_dense_matmul(const scemb_csr_t* csr, const float* table,
+                              int64_t table_rows, int32_t dim,
+                              float* activations, int64_t device_batch_size,
+                              void* workspace, size_t workspace_bytes,
+                              uint32_t* device_status, void* stream);
+
+/* ---- Backward + optimizer: SparseDenseMatmulGradOpWithOptimizerUpdate ----
+ * For every touched table row r:
+ *   g_r = sum over its entries of gain * activations_grad[s*bps + sample_id]
+ * then, once per touched row (untouched rows are not modified),
+ *   SGD:     T[r] = T[r] - g_r * lr
+ *   Adagrad: A[r] = A[r] + g_r * g_r;  T[r] = T[r] - (lr * g_r) / sqrt(A[r])
+ * followed by T[r] = clamp(T[r], min, max) for the bounds that are given
+ * (clip_mask bit 0: min_value, bit 1: max_value). Tables are updated in
+ * place. The learning rate is read from `learning_rate` (device scalar) when
+ * not NULL, else `learning_rate_value` is used. No float atomics: each row is
+ * reduced by one wavefront, long runs split into fixed pieces summed in
+ * order. */
+size_t scemb_sparse_dense_matmul_grad_workspace_size(const scemb_csr_t* csr,
+                                                     int64_t device_batch_size,
+                                                     int64_t table_rows,
+                                                     int32_t dim);
+int scemb_sparse_dense_matmul_grad_with_sgd(
+    const scemb_csr_t* csr, const float* activations_grad,
+    int64_t device_batch_size, float* table, int64_t table_rows, int32_t dim,
+    const float* learning_rate, float learning_rate_value, int32_t clip_mask,
+    float min_value, float max_value, void* workspace, size_t workspace_bytes,
+    uint32_t* device_status, void* stream);
+int scemb_sparse_dense_matmul_grad_with_adagrad(
+    const scemb_csr_t* csr, const float* activations_grad,
+    int64_t device_batch_size, float* table, float* accumulator,
+    int64_t table_rows, int32_t dim, const float* learning_rate,
+    float learning_rate_value, int32_t clip_mask, float min_value,
+    float max_value, void* workspace, size_t workspace_bytes,
+    uint32_t* device_status, void* stream);
+
+/* ---- Preprocessing: PreprocessSparseDenseMatmulInput, one stacked table --
+ * Inputs: the features of one stack, in row_offset order (the order
+ * GetStackedTableMetadata produces, pybind_input_preprocessing.cc:114-120).
+ * Each feature is values + row splits (or a fixed valency) in device memory;
+ * the host copy of the row splits lets the library plan slice offsets
+ * without a device read (if it is NULL and the device splits are given, the
+ * call reads them back synchronously). */
+typedef struct scemb_feature {
+  const int32_t* ids;              /* device [nnz] */
+  const float* weights;            /* device [nnz] or NULL (unity weights) */
+  const int64_t* row_splits;       /* device [num_rows + 1] or NULL */
+  const int64_t* row_splits_host;  /* host [num_rows + 1] or NULL */
+  int64_t num_rows;
+  int64_t nnz;
+  int32_t valency;     /* ids per row when row_splits is NULL */
+  int32_t row_offset;  /* FeatureIdTransformation.row_offset */
+  int32_t col_offset;  /* FeatureIdTransformation.col_offset */
+  int32_t col_shift;   /* FeatureIdTransformation.col_shift */
+} scemb_feature_t;
+
+typedef struct scemb_preprocess_options {
+  int32_t local_device_count;
+  int32_t global_device_count;
+  int32_t num_sc_per_device;
+  int32_t combiner;  /* 0 sum, 1 mean, 2 sqrtn */
+  int32_t max_ids_per_partition;
+  int32_t max_unique_ids_per_partition;
+  int32_t allow_id_dropping;
+  int32_t has_variable_weights; /* weights given for the stack's features */
+  int64_t coo_buffer_size_per_device;
+  int64_t col_id_bound; /* exclusive bound on column ids (stack vocab size) */
+} scemb_preprocess_options_t;
+
+/* Device outputs. The stats block is int32 laid out as
+ *   [L*NS] max_ids_per_partition, [L*NS] max_unique_ids_per_partition,
+ *   [L*S] required_buffer_size, then 4 int64 counters (8-byte aligned by the
+ *   caller): dropped_id_count, limit_exceeded, bad_ids, total_entries. */
+typedef struct scemb_preprocess_output {
+  int32_t* row_pointers;  /* [L * S * max(NS, 8)] */
+  int32_t* embedding_ids; /* [L * coo_buffer_size_per_device] */
+  int32_t* sample_ids;    /* [L * coo_buffer_size_per_device] */
+  float* gains;           /* [L * coo_buffer_size_per_device] */
+  int32_t* stats;         /* scemb_preprocess_stats_size() int32 slots */
+} scemb_preprocess_output_t;
+
+int64_t scemb_preprocess_stats_size(const scemb_preprocess_options_t* opts);
+int64_t scemb_preprocess_stats_counters_offset(
+    const scemb_preprocess_options_t* opts);
+size_t scemb_preprocess_workspace_size(const scemb_feature_t* features,
+                                       int32_t num_features,
+                                       const scemb_preprocess_options_t* opts);
+int scemb_preprocess_stacked_table(const scemb_feature_t* features,
+                                   int32_t num_features,
+                                   const scemb_preprocess_options_t* opts,
+                                   const scemb_preprocess_output_t* out,
+                                   void* workspace, size_t workspace_bytes,
+                                   void* stream);
+
+/* ---- Launch timing (no counterpart in the reference) -------------------
+ * For benchmarks: while enabled, the library records HIP events on the launch
+ * stream around its main kernels ("fwd_gather", "bwd_update") and around
+ * whole calls ("fwd_call", "bwd_call", "preprocess_call").
+ * scemb_profile_collect waits for the recorded events of `name` (all names
+ * when NULL), returns their summed elapsed milliseconds and launch count,
+ * and forgets them. */
+void scemb_profile_enable(int enable);
+int scemb_profile_collect(const char* name, double* total_ms,
+                          int64_t* launches);
+
+/* ---- Size helpers (host only) -----------------------------------------
+ * ComputeTheoreticalMaxCooBufferSize (input_preprocessing_util.cc:223-240),
+ * ComputeCooBufferSizePerDevice without minibatching (:256-312; returns -1
+ * when the suggestion exceeds the theoretical maximum), and
+ * GetRowPointersSizePerDevice (input_preprocessing_util.h:497-511). */
+int64_t scemb_compute_theoretical_max_coo_buffer_size(
+    int32_t max_ids_per_partition, int32_t global_device_count,
+    int32_t num_sc_per_device);
+int64_t scemb_compute_coo_buffer_size_per_device(
+    int32_t max_ids_per_partition, int64_t suggested_coo_buffer_size,
+    int32_t global_device_count, int32_t num_sc_per_device);
+int32_t scemb_compute_row_pointers_size_per_device(int32_t global_device_count,
+                                                   int32_t num_sc_per_device);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SCEMB_H_ */

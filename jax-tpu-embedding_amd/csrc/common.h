@@ -1,0 +1,135 @@
+// Shared device helpers for libscemb (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+namespace scemb {
+
+constexpr int kWave = 64;
+constexpr int kAlign = 8;  // CSR partition alignment (8 elements).
+constexpr int32_t kPadInt = 0x7fffffff;
+constexpr uint32_t kNanBits = 0x7fc00000u;  // std::nanf("")
+
+// Status plumbing: every entry point returns a code and leaves a message in a
+// thread-local buffer (scemb_last_error).
+void SetError(const std::string& msg);
+int Fail(int code, const std::string& msg);
+
+// Optional launch timing (scemb_profile_enable): records a pair of HIP events
+// around a span of launches on `stream`. Returns -1 when disabled.
+int ProfileBegin(const char* name, hipStream_t stream);
+void ProfileEnd(int token, hipStream_t stream);
+
+#define SCEMB_HIP(expr)                                                     \
+  do {                                                                      \
+    hipError_t e_ = (expr);                                                 \
+    if (e_ != hipSuccess) {                                                 \
+      return ::scemb::Fail(4, std::string(#expr ": ") + hipGetErrorString(e_)); \
+    }                                                                       \
+  } while (0)
+
+#define SCEMB_LAUNCH_CHECK()                                                 \
+  do {                                                                       \
+    hipError_t e_ = hipGetLastError();                                       \
+    if (e_ != hipSuccess) {                                                  \
+      return ::scemb::Fail(4, std::string("kernel launch: ") +              \
+                                  hipGetErrorString(e_));                    \
+    }                                                                        \
+  } while (0)
+
+inline int64_t CeilDiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t RoundUp(int64_t a, int64_t b) { return CeilDiv(a, b) * b; }
+inline int BitWidth(uint64_t v) {
+  int b = 0;
+  while (v) {
+    ++b;
+    v >>= 1;
+  }
+  return b;
+}
+
+// Simple bump allocator over a caller-provided workspace. All carve-outs are
+// 256-byte aligned. In "measure" mode (base == nullptr) it only sums sizes.
+class Arena {
+ public:
+  Arena(void* base, size_t bytes) : base_(static_cast<char*>(base)), cap_(bytes) {}
+  template <typename T>
+  T* Take(int64_t count) {
+    const size_t bytes = RoundUp(static_cast<int64_t>(sizeof(T)) *
+                                     (count > 0 ? count : 1), 256);
+    T* p = base_ ? reinterpret_cast<T*>(base_ + used_) : nullptr;
+    used_ += bytes;
+    return p;
+  }
+  size_t used() const { return used_; }
+  bool measuring() const { return base_ == nullptr; }
+  bool overflow() const { return base_ != nullptr && used_ > cap_; }
+
+ private:
+  char* base_;
+  size_t cap_;
+  size_t used_ = 0;
+};
+
+// ---------------------------------------------------------------------------
+// Device-side helpers.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int LaneId() { return __lane_id(); }
+
+__device__ __forceinline__ uint64_t LaneMaskLt() {
+  const int lane = __lane_id();
+  return lane == 0 ? 0ull : (~0ull >> (64 - lane));
+}
+
+template <typename T>
+__device__ __forceinline__ T WaveInclusiveScan(T v) {
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const T o = __shfl_up(v, d, kWave);
+    if (__lane_id() >= d) v += o;
+  }
+  return v;
+}
+
+// Exclusive block scan of one value per thread; returns the exclusive prefix
+// and the block total. BLOCK must be a multiple of 64; `smem` holds
+// BLOCK / 64 + 1 entries.
+template <typename T, int BLOCK>
+__device__ __forceinline__ T BlockExclusiveScan(T v, T* smem, T* total) {
+  constexpr int kWaves = BLOCK / kWave;
+  const int lane = __lane_id();
+  const int wave = threadIdx.x / kWave;
+  const T inc = WaveInclusiveScan(v);
+  if (lane == kWave - 1) smem[wave] = inc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    T run = 0;
+    for (int w = 0; w < kWaves; ++w) {
+      const T t = smem[w];
+      smem[w] = run;
+      run += t;
+    }
+    smem[kWaves] = run;
+  }
+  __syncthreads();
+  const T res = smem[wave] + inc - v;
+  *total = smem[kWaves];
+  __syncthreads();
+  return res;
+}
+
+// Non-coherent-free load of data written by other work-groups of the same
+// kernel after an acquire fence.
+__device__ __forceinline__ void AcquireFence() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+__device__ __forceinline__ void ReleaseFence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+}
+
+}  // namespace scemb

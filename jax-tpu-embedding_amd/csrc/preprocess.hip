@@ -1,0 +1,997 @@
+// GPU preprocessing of one stacked table: the reference's
+// PreprocessSparseDenseMatmulInput (jax_tpu_embedding/sparsecore/lib/core/
+// input_preprocessing.cc:800-959) without minibatching, bit-exact.
+//
+// Stages (segment g = local_device * S + local_sc):
+//   plan      (host)  split-then-stack slices, input_preprocessing.cc:312-436
+//   extract           one thread per input row: sample id, column id
+//                     (coo_format.h:120-135), combiner gain
+//                     (process_coo_tensors_impl.h:39-136), sort key
+//                     (segment, partition, local id) = rotr32(col, log2 NS)
+//   sort              stable LSD radix sort of (key, extraction index). The
+//                     reference sorts 64-bit keys whose low field is the row
+//                     id (unity weights) or the extraction index (weighted);
+//                     a stable sort on the column field alone gives the same
+//                     order whenever rows are non-decreasing in extraction
+//                     order, which the planner checks; otherwise row digits
+//                     are sorted first.
+//   group             the sequential grouping loop of
+//                     sort_and_group_coo_tensors_impl.h:196-311 restated as
+//                     scans: run starts (new (col,row)), column starts,
+//                     per-partition ordinals -> keep/drop, merged gains
+//                     summed in sorted order.
+//   fill              FillBufferSegment (input_preprocessing_util.cc:167-208)
+//                     replayed per segment over partition counts (row
+//                     pointers, alignment padding, static-buffer drops), then
+//                     a scatter of the kept runs.
+#include <algorithm>
+#include <vector>
+
+#include "../../include/scemb.h"
+#include "common.h"
+#include "scan.h"
+
+namespace scemb {
+namespace {
+
+constexpr uint32_t kDataMask26 = (1u << 26) - 1;
+
+struct SliceDesc {
+  int64_t id_begin;
+  int64_t out_begin;
+  int64_t row_start;
+  int64_t row_prefix;
+  int32_t num_rows;
+  int32_t sample_base;
+  int32_t feature;
+  int32_t segment;
+};
+
+struct FeatureDev {
+  const int32_t* ids;
+  const float* weights;
+  const int64_t* splits;
+  int64_t valency;
+  int32_t col_offset;
+  int32_t col_shift;
+};
+
+struct KeyLayout {
+  int log2ns;
+  int32_t ns_mask;
+  bool compact;     // (p, local) packed in local_bits + log2ns bits
+  int local_bits;   // compact: bits of the local id
+  int col_bits;     // bits of the column part of the key
+  int seg_bits;
+  int64_t col_bound;
+};
+
+__device__ __forceinline__ uint32_t Rotr32(uint32_t x, int s) {
+  return s == 0 ? x : ((x >> s) | (x << (32 - s)));
+}
+__device__ __forceinline__ uint32_t Rotl32(uint32_t x, int s) {
+  return s == 0 ? x : ((x << s) | (x >> (32 - s)));
+}
+
+template <typename K>
+__device__ __forceinline__ K ColKey(uint32_t col, const KeyLayout& kl) {
+  if (kl.compact) {
+    const uint32_t p = col & static_cast<uint32_t>(kl.ns_mask);
+    const uint32_t local = col >> kl.log2ns;
+    return (static_cast<K>(p) << kl.local_bits) | static_cast<K>(local);
+  }
+  return static_cast<K>(Rotr32(col, kl.log2ns));
+}
+
+// Partition and local id from the column part of a key.
+template <typename K>
+__device__ __forceinline__ void DecodeCol(K ck, const KeyLayout& kl,
+                                          uint32_t* p, uint32_t* local) {
+  if (kl.compact) {
+    *p = static_cast<uint32_t>(ck >> kl.local_bits);
+    *local = static_cast<uint32_t>(ck) &
+             ((kl.local_bits >= 32) ? 0xffffffffu : ((1u << kl.local_bits) - 1u));
+  } else {
+    const uint32_t col = Rotl32(static_cast<uint32_t>(ck), kl.log2ns);
+    *p = col & static_cast<uint32_t>(kl.ns_mask);
+    *local = col >> kl.log2ns;
+  }
+}
+
+template <typename K>
+__device__ __forceinline__ K SentinelKey() {
+  return ~K(0);
+}
+
+// One thread per input row of every slice.
+template <typename K>
+__global__ __launch_bounds__(256) void ExtractRows(
+    const SliceDesc* slices, int num_slices, const FeatureDev* feats,
+    int64_t total_rows, int combiner, int has_weights, KeyLayout kl,
+    K* keys, uint32_t* vals, uint32_t* rows_out, float* gains_out,
+    uint32_t* row_keys, int row_key_bits_seg_shift, int64_t* counters) {
+  const int64_t gr = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gr >= total_rows) return;
+  int lo = 0, hi = num_slices - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (slices[mid].row_prefix <= gr) lo = mid; else hi = mid - 1;
+  }
+  const SliceDesc sl = slices[lo];
+  const FeatureDev f = feats[sl.feature];
+  const int64_t local_row = gr - sl.row_prefix;
+  const int64_t r = sl.row_start + local_row;
+  int64_t b, e;
+  if (f.splits != nullptr) {
+    b = f.splits[r];
+    e = f.splits[r + 1];
+  } else {
+    b = r * f.valency;
+    e = b + f.valency;
+  }
+  const int64_t cnt = e - b;
+  const int64_t out = sl.out_begin + (b - sl.id_begin);
+  const uint32_t sample = static_cast<uint32_t>(sl.sample_base + local_row);
+  float divisor = 1.0f;
+  float unity_gain = 1.0f;
+  if (!has_weights) {
+    if (combiner == 1) {
+      unity_gain = 1.0f / static_cast<float>(static_cast<int>(cnt));
+    } else if (combiner == 2) {
+      unity_gain = 1.0f / sqrtf(static_cast<float>(static_cast<int>(cnt)));
+    }
+  } else if (combiner == 1) {
+    float s = 0.0f;
+    for (int64_t k = 0; k < cnt; ++k) s = s + f.weights[b + k];
+    divisor = s;
+  } else if (combiner == 2) {
+    float s = 0.0f;
+    for (int64_t k = 0; k < cnt; ++k) {
+      const double w = static_cast<double>(f.weights[b + k]);
+      s = static_cast<float>(static_cast<double>(s) + w * w);
+    }
+    divisor = sqrtf(s);
+  }
+  const K seg_part = static_cast<K>(sl.segment) << kl.col_bits;
+  int64_t bad = 0;
+  for (int64_t k = 0; k < cnt; ++k) {
+    const int32_t id = f.ids[b + k];
+    // GetColId: ((id + shift) & mask) + (id & ~mask) + offset.
+    const int32_t col = ((id + f.col_shift) & kl.ns_mask) + (id & ~kl.ns_mask) +
+                        f.col_offset;
+    const bool ok = id >= 0 && col >= 0 &&
+                    (kl.col_bound <= 0 || static_cast<int64_t>(col) < kl.col_bound);
+    const int64_t o = out + k;
+    keys[o] = ok ? (seg_part | ColKey<K>(static_cast<uint32_t>(col), kl))
+                 : SentinelKey<K>();
+    vals[o] = static_cast<uint32_t>(o);
+    rows_out[o] = sample;
+    gains_out[o] = has_weights ? f.weights[b + k] / divisor : unity_gain;
+    if (row_keys != nullptr) {
+      row_keys[o] = (static_cast<uint32_t>(sl.segment) << row_key_bits_seg_shift) |
+                    sample;
+    }
+    if (!ok) ++bad;
+  }
+  if (bad) atomicAdd(reinterpret_cast<unsigned long long*>(&counters[2]),
+                     static_cast<unsigned long long>(bad));
+}
+
+template <typename K>
+__global__ void GatherKeys(const K* keys, const uint32_t* idx, int64_t n,
+                           K* out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = keys[idx[i]];
+}
+
+__global__ void FillI32(int32_t* p, int64_t n, int32_t v) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// Flags and partition boundaries over the sorted sequence.
+template <typename K>
+__global__ __launch_bounds__(256) void GroupFlags(
+    const K* skeys, const uint32_t* sidx, const uint32_t* rows,
+    const float* gains, int64_t n, KeyLayout kl, int num_partitions,
+    uint32_t* srows, float* sgains, uint64_t* flags, int32_t* part_first,
+    int32_t* part_last) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const K key = skeys[i];
+  const bool valid = key != SentinelKey<K>();
+  uint64_t f = 0;
+  if (valid) {
+    const uint32_t idx = sidx[i];
+    const uint32_t row = rows[idx];
+    srows[i] = row;
+    sgains[i] = gains[idx];
+    const K col_mask = kl.col_bits >= 64 ? ~K(0) : ((K(1) << kl.col_bits) - 1);
+    uint32_t p, local;
+    DecodeCol<K>(key & col_mask, kl, &p, &local);
+    const int64_t seg = static_cast<int64_t>(key >> kl.col_bits);
+    const int64_t bucket = seg * num_partitions + p;
+    bool new_col = true, new_run = true, new_bucket = true;
+    if (i > 0) {
+      const K pk = skeys[i - 1];
+      if (pk == key) {
+        new_col = false;
+        new_bucket = false;
+        new_run = rows[sidx[i - 1]] != row;
+      } else {
+        uint32_t pp, pl;
+        DecodeCol<K>(pk & col_mask, kl, &pp, &pl);
+        new_bucket = static_cast<int64_t>(pk >> kl.col_bits) != seg || pp != p;
+      }
+    }
+    f = (new_run ? 1ull : 0ull) | ((new_col ? 1ull : 0ull) << 32);
+    if (new_bucket) part_first[bucket] = static_cast<int32_t>(i);
+    bool last = i + 1 == n;
+    if (!last) {
+      const K nk = skeys[i + 1];
+      if (nk == SentinelKey<K>()) {
+        last = true;
+      } else if (nk != key) {
+        uint32_t np, nl;
+        DecodeCol<K>(nk & col_mask, kl, &np, &nl);
+        last = static_cast<int64_t>(nk >> kl.col_bits) != seg || np != p;
+      }
+    }
+    if (last) part_last[bucket] = static_cast<int32_t>(i);
+  }
+  flags[i] = f;
+}
+
+// run_pos[r] = sorted position where run r starts; run_pos[R] = end.
+template <typename K>
+__global__ __launch_bounds__(256) void RunPositions(const K* skeys,
+                                                    const uint64_t* flags,
+                                                    const uint64_t* scan,
+                                                    int64_t n,
+                                                    uint32_t* run_pos) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t f = flags[i];
+  const uint32_t r = static_cast<uint32_t>(scan[i]);
+  if (f & 1ull) run_pos[r] = static_cast<uint32_t>(i);
+  if (skeys[i] != SentinelKey<K>()) {
+    const bool last = i + 1 == n || skeys[i + 1] == SentinelKey<K>();
+    if (last) run_pos[r + static_cast<uint32_t>(f & 1ull)] =
+        static_cast<uint32_t>(i + 1);
+  }
+}
+
+struct Limits {
+  int32_t max_ids;
+  int32_t max_unique;
+  int32_t allow_dropping;
+};
+
+template <typename K>
+__global__ __launch_bounds__(256) void RunReduce(
+    const K* skeys, const float* sgains, const uint64_t* flags,
+    const uint64_t* scan, const uint32_t* run_pos, const uint64_t* totals,
+    int64_t n_upper, KeyLayout kl, int num_partitions,
+    const int32_t* part_first, Limits lim, float* run_gain,
+    uint32_t* keep, int64_t* counters) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r > n_upper) return;
+  const int64_t runs = static_cast<int64_t>(static_cast<uint32_t>(totals[0]));
+  if (r >= runs) {
+    keep[r] = 0;
+    return;
+  }
+  const int64_t i0 = run_pos[r];
+  const int64_t i1 = run_pos[r + 1];
+  float g = sgains[i0];
+  for (int64_t k = i0 + 1; k < i1; ++k) g = g + sgains[k];
+  run_gain[r] = g;
+  uint32_t k_ok = 1;
+  if (lim.allow_dropping) {
+    const K key = skeys[i0];
+    const K col_mask = kl.col_bits >= 64 ? ~K(0) : ((K(1) << kl.col_bits) - 1);
+    uint32_t p, local;
+    DecodeCol<K>(key & col_mask, kl, &p, &local);
+    const int64_t bucket =
+        static_cast<int64_t>(key >> kl.col_bits) * num_partitions + p;
+    const int64_t first = part_first[bucket];
+    const uint64_t fs = scan[first];
+    const uint64_t si = scan[i0];
+    const int64_t u = r - static_cast<int64_t>(static_cast<uint32_t>(fs)) + 1;
+    const int64_t c = static_cast<int64_t>(si >> 32) +
+                      static_cast<int64_t>(flags[i0] >> 32) -
+                      static_cast<int64_t>(fs >> 32);
+    if (u > lim.max_ids || c > lim.max_unique) {
+      k_ok = 0;
+      atomicAdd(reinterpret_cast<unsigned long long*>(&counters[0]),
+                static_cast<unsigned long long>(i1 - i0));
+    }
+  }
+  keep[r] = k_ok;
+}
+
+struct BucketStats {
+  int32_t obs_ids;
+  int32_t obs_unique;
+  int32_t kept;
+  int32_t kept_first;
+};
+
+__global__ __launch_bounds__(256) void BucketReduce(
+    const int32_t* part_first, const int32_t* part_last,
+    const uint64_t* flags, const uint64_t* scan, const uint32_t* keep_scan,
+    int64_t num_buckets, BucketStats* stats) {
+  const int64_t bkt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (bkt >= num_buckets) return;
+  BucketStats s{0, 0, 0, 0};
+  const int32_t f = part_first[bkt];
+  if (f >= 0) {
+    const int32_t l = part_last[bkt];
+    const uint64_t fs = scan[f];
+    const uint64_t ls = scan[l];
+    const uint64_t lf = flags[l];
+    const uint32_t rf = static_cast<uint32_t>(fs);
+    const uint32_t rend = static_cast<uint32_t>(ls) + static_cast<uint32_t>(lf & 1ull);
+    s.obs_ids = static_cast<int32_t>(rend - rf);
+    s.obs_unique = static_cast<int32_t>(
+        static_cast<uint32_t>(ls >> 32) + static_cast<uint32_t>(lf >> 32) -
+        static_cast<uint32_t>(fs >> 32));
+    s.kept_first = static_cast<int32_t>(keep_scan[rf]);
+    s.kept = static_cast<int32_t>(keep_scan[rend] - keep_scan[rf]);
+  }
+  stats[bkt] = s;
+}
+
+struct FillPlan {
+  int64_t start;      // absolute position of the first kept entry
+  int32_t fit;        // kept entries that fit the static buffer
+  int32_t pad_begin;  // alignment padding written after this partition
+  int32_t pad_end;
+  int32_t pad_seg;    // padding positions are relative to this segment
+};
+
+struct FillParams {
+  int32_t local_devices;
+  int32_t segs_per_device;  // S
+  int32_t num_partitions;   // NS
+  int32_t rp_per_segment;
+  int64_t coo_size;         // per device
+  int32_t max_ids;
+  int32_t max_unique;
+  int32_t allow_dropping;
+};
+
+// One thread per segment replays FillBufferSegment over partition counts; a
+// second loop reduces device stats (max over local SCs).
+__global__ __launch_bounds__(256) void FillPlanKernel(
+    const BucketStats* bstats, FillParams fp, int32_t* rp_out,
+    FillPlan* plans, int32_t* stat_max_ids, int32_t* stat_max_unique,
+    int32_t* stat_required, int64_t* counters) {
+  const int S = fp.segs_per_device;
+  const int NS = fp.num_partitions;
+  const int num_segments = fp.local_devices * S;
+  const int64_t per_sc = fp.coo_size / S;
+  for (int g = threadIdx.x; g < num_segments; g += blockDim.x) {
+    const int s = g % S;
+    const BucketStats* bs = bstats + static_cast<int64_t>(g) * NS;
+    FillPlan* pl = plans + static_cast<int64_t>(g) * NS;
+    int32_t* rp = rp_out + static_cast<int64_t>(g) * fp.rp_per_segment;
+    int64_t total = 0, req = 0;
+    bool over = false;
+    for (int p = 0; p < NS; ++p) {
+      total += bs[p].kept;
+      req += (static_cast<int64_t>(bs[p].obs_ids) + kAlign - 1) / kAlign * kAlign;
+      pl[p].start = 0;
+      pl[p].fit = 0;
+      pl[p].pad_begin = 0;
+      pl[p].pad_end = 0;
+      pl[p].pad_seg = g;
+      if (bs[p].obs_ids > fp.max_ids || bs[p].obs_unique > fp.max_unique) {
+        over = true;
+      }
+    }
+    stat_required[g] = static_cast<int32_t>(req);
+    if (over && !fp.allow_dropping) {
+      atomicMax(reinterpret_cast<unsigned long long*>(&counters[1]), 1ull);
+    }
+    const int64_t coo_begin = min(static_cast<int64_t>(s) * per_sc, fp.coo_size);
+    const int64_t coo_end = coo_begin + per_sc;
+    int64_t coo = coo_begin;
+    int64_t processed = 0;
+    int rpi = 0;
+    int cur = 0;
+    auto valid = [&]() {
+      if (processed == total && coo == coo_end) return true;
+      if (rpi >= fp.rp_per_segment || coo >= coo_end) return false;
+      return true;
+    };
+    auto advance = [&](int target) {
+      while (cur < target) {
+        if (!valid()) return;
+        rp[rpi++] = static_cast<int32_t>(coo - coo_begin);
+        int64_t nc = (coo + kAlign - 1) / kAlign * kAlign;
+        if (nc > coo_end) nc = coo_end;
+        pl[cur].pad_begin = static_cast<int32_t>(coo - coo_begin);
+        pl[cur].pad_end = static_cast<int32_t>(nc - coo_begin);
+        coo = nc;
+        ++cur;
+      }
+    };
+    bool dropped_rest = false;
+    for (int p = 0; p < NS && !dropped_rest; ++p) {
+      const int64_t kp = bs[p].kept;
+      if (kp == 0) continue;
+      advance(p);
+      if (!valid()) {
+        dropped_rest = true;
+        break;
+      }
+      const int64_t room = coo_end - coo;
+      const int64_t take = kp < room ? kp : room;
+      pl[p].start = coo;
+      pl[p].fit = static_cast<int32_t>(take);
+      coo += take;
+      processed += take;
+      if (take < kp) {
+        dropped_rest = true;
+        break;
+      }
+    }
+    advance(NS);
+    while (rpi < fp.rp_per_segment) {
+      rp[rpi++] = static_cast<int32_t>(coo - coo_begin);
+    }
+    if (total > processed) {
+      atomicAdd(reinterpret_cast<unsigned long long*>(&counters[0]),
+                static_cast<unsigned long long>(total - processed));
+    }
+  }
+  for (int dp = threadIdx.x; dp < fp.local_devices * NS; dp += blockDim.x) {
+    const int d = dp / NS, p = dp % NS;
+    int32_t mi = 0, mu = 0;
+    for (int s = 0; s < S; ++s) {
+      const BucketStats& b = bstats[static_cast<int64_t>(d * S + s) * NS + p];
+      mi = max(mi, b.obs_ids);
+      mu = max(mu, b.obs_unique);
+    }
+    stat_max_ids[dp] = mi;
+    stat_max_unique[dp] = mu;
+  }
+}
+
+template <typename K>
+__global__ __launch_bounds__(256) void ScatterRuns(
+    const K* skeys, const uint32_t* srows, const uint32_t* run_pos,
+    const float* run_gain, const uint32_t* keep, const uint32_t* keep_scan,
+    const uint64_t* totals, int64_t n_upper, KeyLayout kl, FillParams fp,
+    int32_t bps, const BucketStats* bstats, const FillPlan* plans,
+    int32_t* eid, int32_t* sid, float* gains) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n_upper) return;
+  const int64_t runs = static_cast<int64_t>(static_cast<uint32_t>(totals[0]));
+  if (r >= runs || !keep[r]) return;
+  const int64_t i0 = run_pos[r];
+  const K key = skeys[i0];
+  const K col_mask = kl.col_bits >= 64 ? ~K(0) : ((K(1) << kl.col_bits) - 1);
+  uint32_t p, local;
+  DecodeCol<K>(key & col_mask, kl, &p, &local);
+  const int64_t seg = static_cast<int64_t>(key >> kl.col_bits);
+  const int64_t bucket = seg * fp.num_partitions + p;
+  const int64_t k = static_cast<int64_t>(keep_scan[r]) - bstats[bucket].kept_first;
+  const FillPlan pl = plans[bucket];
+  if (k >= pl.fit) return;
+  const int64_t d = seg / fp.segs_per_device;
+  const int64_t pos = d * fp.coo_size + pl.start + k;
+  eid[pos] = static_cast<int32_t>(local);
+  sid[pos] = static_cast<int32_t>(srows[i0] % static_cast<uint32_t>(bps));
+  gains[pos] = run_gain[r];
+}
+
+__global__ __launch_bounds__(256) void WritePadding(const FillPlan* plans,
+                                                    int64_t num_buckets,
+                                                    FillParams fp, int32_t* eid,
+                                                    int32_t* sid, float* gains) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t bkt = t / kAlign;
+  const int k = static_cast<int>(t % kAlign);
+  if (bkt >= num_buckets) return;
+  const FillPlan pl = plans[bkt];
+  const int32_t pos_rel = pl.pad_begin + k;
+  if (pos_rel >= pl.pad_end) return;
+  const int64_t seg = pl.pad_seg;
+  const int64_t d = seg / fp.segs_per_device;
+  const int64_t s = seg % fp.segs_per_device;
+  const int64_t per_sc = fp.coo_size / fp.segs_per_device;
+  const int64_t coo_begin =
+      s * per_sc < fp.coo_size ? s * per_sc : fp.coo_size;
+  const int64_t pos = d * fp.coo_size + coo_begin + pos_rel;
+  eid[pos] = kPadInt;
+  sid[pos] = kPadInt;
+  gains[pos] = __uint_as_float(kNanBits);
+}
+
+__global__ void ZeroI64(int64_t* p, int n) {
+  if (threadIdx.x < n) p[threadIdx.x] = 0;
+}
+
+__global__ void StoreTotal(const uint64_t* totals, int64_t* counters) {
+  counters[3] = static_cast<int64_t>(static_cast<uint32_t>(totals[0]));
+}
+
+// ---------------------------------------------------------------------------
+// Host planning.
+// ---------------------------------------------------------------------------
+
+struct Plan {
+  int L, G, S, NS, log2ns, rp_per_seg;
+  int64_t coo_size, bps, batch_for_device;
+  int64_t total_ids, total_rows;
+  std::vector<SliceDesc> slices;
+  bool rows_monotone;
+  KeyLayout kl;
+  bool wide_keys;
+  int row_key_seg_shift;
+  int row_bits;
+};
+
+int MakePlan(const scemb_feature_t* feats, int nf,
+             const scemb_preprocess_options_t* o, Plan* pl,
+             std::vector<std::vector<int64_t>>* splits_cache) {
+  if (o == nullptr || (nf > 0 && feats == nullptr)) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null arguments");
+  }
+  const int L = o->local_device_count, G = o->global_device_count,
+            S = o->num_sc_per_device;
+  if (L <= 0) return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                          "local_device_count must be greater than 0");
+  if (G <= 0) return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                          "global_device_count must be greater than 0");
+  if (G < L) return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                         "global_device_count must be greater than or equal "
+                         "to local_device_count");
+  if (S <= 0) return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                          "num_sc_per_device must be greater than 0");
+  const int64_t ns = static_cast<int64_t>(S) * G;
+  if (ns > (1 << 20) || (ns & (ns - 1)) != 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "Total number of SparseCores must be a power of 2.");
+  }
+  if (nf <= 0) return Fail(SCEMB_ERR_INVALID_ARGUMENT, "no features");
+  if (o->combiner < 0 || o->combiner > 2) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "unknown combiner");
+  }
+  if (o->coo_buffer_size_per_device <= 0 ||
+      o->coo_buffer_size_per_device >= 0x7fffffff) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "coo buffer size is out of the valid range (0, INT_MAX)");
+  }
+  if (o->max_ids_per_partition <= 0 || o->max_unique_ids_per_partition <= 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "id limits must be positive");
+  }
+  pl->L = L;
+  pl->G = G;
+  pl->S = S;
+  pl->NS = static_cast<int>(ns);
+  pl->log2ns = BitWidth(static_cast<uint64_t>(ns)) - 1;
+  pl->rp_per_seg = std::max(pl->NS, kAlign);
+  pl->coo_size = o->coo_buffer_size_per_device;
+  int64_t bfd = 0;
+  for (int f = 0; f < nf; ++f) {
+    if (feats[f].num_rows < 0 || feats[f].nnz < 0) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "negative feature size");
+    }
+    if (feats[f].row_splits == nullptr && feats[f].valency < 0) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "negative valency");
+    }
+    bfd += feats[f].num_rows / L;
+  }
+  if (bfd > kDataMask26) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "The total local batch size for device (including stacked "
+                "tables) exceeds the maximum limit supported by the "
+                "SparseCore CooFormat sorting key (67108863).");
+  }
+  if (bfd % S != 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "batch_size_for_device must be divisible by num_sc_per_device");
+  }
+  if (bfd < static_cast<int64_t>(S) * nf) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "Batch size must be greater or equal to the number of features "
+                "stacked together (per feature slice).");
+  }
+  pl->batch_for_device = bfd;
+  pl->bps = bfd / S;
+  // Host row splits for planning.
+  splits_cache->assign(nf, {});
+  for (int f = 0; f < nf; ++f) {
+    const scemb_feature_t& ft = feats[f];
+    if (ft.row_splits != nullptr && ft.row_splits_host == nullptr) {
+      auto& v = (*splits_cache)[f];
+      v.resize(ft.num_rows + 1);
+      SCEMB_HIP(hipMemcpy(v.data(), ft.row_splits,
+                          sizeof(int64_t) * (ft.num_rows + 1),
+                          hipMemcpyDeviceToHost));
+    }
+  }
+  auto split_at = [&](int f, int64_t r) -> int64_t {
+    const scemb_feature_t& ft = feats[f];
+    if (ft.row_splits == nullptr) return r * ft.valency;
+    if (ft.row_splits_host != nullptr) return ft.row_splits_host[r];
+    return (*splits_cache)[f][r];
+  };
+  pl->slices.clear();
+  int64_t out = 0, rows = 0;
+  pl->rows_monotone = true;
+  for (int d = 0; d < L; ++d) {
+    for (int s = 0; s < S; ++s) {
+      int64_t prev_last = -1;
+      for (int f = 0; f < nf; ++f) {
+        const scemb_feature_t& ft = feats[f];
+        const int64_t per_split = ft.num_rows / (static_cast<int64_t>(L) * S);
+        const int64_t start = (static_cast<int64_t>(d) * S + s) * per_split;
+        const int64_t end = std::min(ft.num_rows, start + per_split);
+        SliceDesc sd;
+        sd.id_begin = split_at(f, start);
+        const int64_t id_end = split_at(f, end);
+        if (id_end < sd.id_begin || id_end > ft.nnz) {
+          return Fail(SCEMB_ERR_INVALID_ARGUMENT, "row splits out of range");
+        }
+        sd.out_begin = out;
+        sd.row_start = start;
+        sd.row_prefix = rows;
+        sd.num_rows = static_cast<int32_t>(end - start);
+        sd.sample_base = static_cast<int32_t>(
+            s * pl->bps + ft.row_offset / (static_cast<int64_t>(G) * S));
+        sd.feature = f;
+        sd.segment = d * S + s;
+        if (sd.num_rows > 0) {
+          if (sd.sample_base < prev_last) pl->rows_monotone = false;
+          prev_last = sd.sample_base + sd.num_rows - 1;
+          pl->slices.push_back(sd);
+        }
+        out += id_end - sd.id_begin;
+        rows += sd.num_rows;
+      }
+    }
+  }
+  pl->total_ids = out;
+  pl->total_rows = rows;
+  if (out >= (int64_t{1} << 31) - 1) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "too many ids in one stack");
+  }
+  KeyLayout& kl = pl->kl;
+  kl.log2ns = pl->log2ns;
+  kl.ns_mask = pl->NS - 1;
+  kl.col_bound = o->col_id_bound;
+  if (o->col_id_bound > 0) {
+    kl.compact = true;
+    kl.local_bits = BitWidth(static_cast<uint64_t>(o->col_id_bound - 1) >> pl->log2ns);
+    kl.col_bits = kl.local_bits + pl->log2ns;
+  } else {
+    kl.compact = false;
+    kl.local_bits = 32 - pl->log2ns;
+    kl.col_bits = 32;
+  }
+  kl.seg_bits = BitWidth(static_cast<uint64_t>(L) * S - 1);
+  pl->wide_keys = kl.col_bits + kl.seg_bits > 31;
+  const int sample_bits = BitWidth(static_cast<uint64_t>(std::max<int64_t>(bfd - 1, 0)));
+  pl->row_key_seg_shift = sample_bits;
+  pl->row_bits = sample_bits + kl.seg_bits;
+  if (pl->row_bits > 32) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "too many segments");
+  }
+  return 0;
+}
+
+struct Buffers {
+  void* keys;
+  void* keys_alt;
+  uint32_t* vals;
+  uint32_t* vals_alt;
+  uint32_t* rows;
+  float* gains;
+  uint32_t* row_keys;
+  uint32_t* row_keys_alt;
+  uint32_t* srows;
+  float* sgains;
+  uint64_t* flags;
+  uint64_t* scan;
+  uint64_t* totals;
+  uint32_t* run_pos;
+  float* run_gain;
+  uint32_t* keep;
+  uint32_t* keep_scan;
+  int32_t* part_first;
+  int32_t* part_last;
+  BucketStats* bstats;
+  FillPlan* plans;
+  SliceDesc* slices;
+  FeatureDev* feats;
+};
+
+template <typename K>
+int RunPipeline(const scemb_feature_t* feats, int nf,
+                const scemb_preprocess_options_t* o,
+                const scemb_preprocess_output_t* out, const Plan& pl,
+                Arena& ws, hipStream_t stream) {
+  const int64_t M = pl.total_ids;
+  const int64_t num_buckets = static_cast<int64_t>(pl.L) * pl.S * pl.NS;
+  const bool need_row_pass = !o->has_variable_weights && !pl.rows_monotone;
+  Buffers b;
+  b.keys = ws.Take<K>(M);
+  b.keys_alt = ws.Take<K>(M);
+  b.vals = ws.Take<uint32_t>(M);
+  b.vals_alt = ws.Take<uint32_t>(M);
+  b.rows = ws.Take<uint32_t>(M);
+  b.gains = ws.Take<float>(M);
+  b.row_keys = need_row_pass ? ws.Take<uint32_t>(M) : nullptr;
+  b.row_keys_alt = need_row_pass ? ws.Take<uint32_t>(M) : nullptr;
+  b.srows = ws.Take<uint32_t>(M);
+  b.sgains = ws.Take<float>(M);
+  b.flags = ws.Take<uint64_t>(M);
+  b.scan = ws.Take<uint64_t>(M);
+  b.totals = ws.Take<uint64_t>(2);
+  b.run_pos = ws.Take<uint32_t>(M + 1);
+  b.run_gain = ws.Take<float>(M);
+  b.keep = ws.Take<uint32_t>(M + 1);
+  b.keep_scan = ws.Take<uint32_t>(M + 1);
+  b.part_first = ws.Take<int32_t>(num_buckets);
+  b.part_last = ws.Take<int32_t>(num_buckets);
+  b.bstats = ws.Take<BucketStats>(num_buckets);
+  b.plans = ws.Take<FillPlan>(num_buckets);
+  b.slices = ws.Take<SliceDesc>(static_cast<int64_t>(pl.slices.size()));
+  b.feats = ws.Take<FeatureDev>(nf);
+  const bool measuring = ws.measuring();
+  const int64_t counters_off = RoundUp(2 * static_cast<int64_t>(pl.L) * pl.NS +
+                                       static_cast<int64_t>(pl.L) * pl.S, 2);
+  int64_t* counters = nullptr;
+  if (!measuring) {
+    if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+    if (out == nullptr || out->row_pointers == nullptr || out->stats == nullptr ||
+        out->embedding_ids == nullptr || out->sample_ids == nullptr ||
+        out->gains == nullptr) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null output buffer");
+    }
+    counters = reinterpret_cast<int64_t*>(out->stats + counters_off);
+    if ((reinterpret_cast<uintptr_t>(counters) & 7u) != 0) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "stats buffer must be 8-byte aligned");
+    }
+    hipLaunchKernelGGL(ZeroI64, dim3(1), dim3(64), 0, stream, counters, 4);
+    SCEMB_LAUNCH_CHECK();
+    std::vector<FeatureDev> fd(nf);
+    for (int f = 0; f < nf; ++f) {
+      fd[f].ids = feats[f].ids;
+      fd[f].weights = o->has_variable_weights ? feats[f].weights : nullptr;
+      fd[f].splits = feats[f].row_splits;
+      fd[f].valency = feats[f].valency;
+      fd[f].col_offset = feats[f].col_offset;
+      fd[f].col_shift = feats[f].col_shift;
+      if (feats[f].nnz > 0 && feats[f].ids == nullptr) {
+        return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null ids");
+      }
+      if (o->has_variable_weights && feats[f].nnz > 0 &&
+          feats[f].weights == nullptr) {
+        return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                    "weights required for every feature of a weighted stack");
+      }
+    }
+    if (!pl.slices.empty()) {
+      SCEMB_HIP(hipMemcpyAsync(b.slices, pl.slices.data(),
+                               sizeof(SliceDesc) * pl.slices.size(),
+                               hipMemcpyHostToDevice, stream));
+    }
+    SCEMB_HIP(hipMemcpyAsync(b.feats, fd.data(), sizeof(FeatureDev) * nf,
+                             hipMemcpyHostToDevice, stream));
+    // The staging copies above read pageable host memory; make sure they are
+    // done before the vectors go out of scope.
+    SCEMB_HIP(hipStreamSynchronize(stream));
+    hipLaunchKernelGGL(FillI32, dim3(CeilDiv(num_buckets, 256)), dim3(256), 0,
+                       stream, b.part_first, num_buckets, -1);
+    SCEMB_LAUNCH_CHECK();
+    hipLaunchKernelGGL(FillI32, dim3(CeilDiv(num_buckets, 256)), dim3(256), 0,
+                       stream, b.part_last, num_buckets, -1);
+    SCEMB_LAUNCH_CHECK();
+    if (pl.total_rows > 0) {
+      hipLaunchKernelGGL((ExtractRows<K>), dim3(CeilDiv(pl.total_rows, 256)),
+                         dim3(256), 0, stream, b.slices,
+                         static_cast<int>(pl.slices.size()), b.feats,
+                         pl.total_rows, o->combiner,
+                         o->has_variable_weights ? 1 : 0, pl.kl,
+                         static_cast<K*>(b.keys), b.vals, b.rows, b.gains,
+                         b.row_keys, pl.row_key_seg_shift, counters);
+      SCEMB_LAUNCH_CHECK();
+    }
+  }
+  // Sort: optional row pass, then the column key. One extra key bit keeps the
+  // all-ones sentinel of rejected ids strictly above every valid key.
+  const int sort_bits = pl.kl.col_bits + pl.kl.seg_bits + 1;
+  K* skeys = static_cast<K*>(b.keys);
+  uint32_t* sidx = b.vals;
+  int st = 0;
+  if (need_row_pass) {
+    bool alt = false;
+    st = RadixSortPairs<uint32_t, uint32_t>(b.row_keys, b.vals, b.row_keys_alt,
+                                            b.vals_alt, M, 0, pl.row_bits, ws,
+                                            stream, &alt);
+    if (st != 0) return st;
+    uint32_t* idx = alt ? b.vals_alt : b.vals;
+    if (!measuring && M > 0) {
+      hipLaunchKernelGGL((GatherKeys<K>), dim3(CeilDiv(M, 256)), dim3(256), 0,
+                         stream, static_cast<K*>(b.keys), idx, M,
+                         static_cast<K*>(b.keys_alt));
+      SCEMB_LAUNCH_CHECK();
+    }
+    // Keys now in keys_alt (row order), indices in idx.
+    uint32_t* idx_other = alt ? b.vals : b.vals_alt;
+    bool alt2 = false;
+    st = RadixSortPairs<K, uint32_t>(static_cast<K*>(b.keys_alt), idx,
+                                     static_cast<K*>(b.keys), idx_other, M, 0,
+                                     sort_bits, ws, stream, &alt2);
+    if (st != 0) return st;
+    skeys = alt2 ? static_cast<K*>(b.keys) : static_cast<K*>(b.keys_alt);
+    sidx = alt2 ? idx_other : idx;
+  } else {
+    bool alt = false;
+    st = RadixSortPairs<K, uint32_t>(static_cast<K*>(b.keys), b.vals,
+                                     static_cast<K*>(b.keys_alt), b.vals_alt,
+                                     M, 0, sort_bits, ws, stream, &alt);
+    if (st != 0) return st;
+    skeys = alt ? static_cast<K*>(b.keys_alt) : static_cast<K*>(b.keys);
+    sidx = alt ? b.vals_alt : b.vals;
+  }
+  if (!measuring && M > 0) {
+    hipLaunchKernelGGL((GroupFlags<K>), dim3(CeilDiv(M, 256)), dim3(256), 0,
+                       stream, skeys, sidx, b.rows, b.gains, M, pl.kl, pl.NS,
+                       b.srows, b.sgains, b.flags, b.part_first, b.part_last);
+    SCEMB_LAUNCH_CHECK();
+  }
+  st = ExclusiveScan<uint64_t>(b.flags, b.scan, M, b.totals, ws, stream);
+  if (st != 0) return st;
+  if (!measuring && M > 0) {
+    hipLaunchKernelGGL((RunPositions<K>), dim3(CeilDiv(M, 256)), dim3(256), 0,
+                       stream, skeys, b.flags, b.scan, M, b.run_pos);
+    SCEMB_LAUNCH_CHECK();
+  }
+  const Limits lim{o->max_ids_per_partition, o->max_unique_ids_per_partition,
+                   o->allow_id_dropping};
+  if (!measuring) {
+    if (M > 0) {
+      hipLaunchKernelGGL((RunReduce<K>), dim3(CeilDiv(M + 1, 256)), dim3(256),
+                         0, stream, skeys, b.sgains, b.flags, b.scan,
+                         b.run_pos, b.totals, M, pl.kl, pl.NS, b.part_first,
+                         lim, b.run_gain, b.keep, counters);
+      SCEMB_LAUNCH_CHECK();
+    } else {
+      hipLaunchKernelGGL(FillI32, dim3(1), dim3(256), 0, stream,
+                         reinterpret_cast<int32_t*>(b.keep), int64_t{1}, 0);
+      SCEMB_LAUNCH_CHECK();
+    }
+  }
+  st = ExclusiveScan<uint32_t>(b.keep, b.keep_scan, M + 1, nullptr, ws,
+                               stream);
+  if (st != 0) return st;
+  if (measuring) return 0;
+  if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+  hipLaunchKernelGGL(BucketReduce, dim3(CeilDiv(num_buckets, 256)), dim3(256),
+                     0, stream, b.part_first, b.part_last, b.flags, b.scan,
+                     b.keep_scan, num_buckets, b.bstats);
+  SCEMB_LAUNCH_CHECK();
+  FillParams fp;
+  fp.local_devices = pl.L;
+  fp.segs_per_device = pl.S;
+  fp.num_partitions = pl.NS;
+  fp.rp_per_segment = pl.rp_per_seg;
+  fp.coo_size = pl.coo_size;
+  fp.max_ids = o->max_ids_per_partition;
+  fp.max_unique = o->max_unique_ids_per_partition;
+  fp.allow_dropping = o->allow_id_dropping;
+  int32_t* stat_max_ids = out->stats;
+  int32_t* stat_max_unique = out->stats + static_cast<int64_t>(pl.L) * pl.NS;
+  int32_t* stat_required = out->stats + 2 * static_cast<int64_t>(pl.L) * pl.NS;
+  hipLaunchKernelGGL(FillPlanKernel, dim3(1), dim3(256), 0, stream, b.bstats,
+                     fp, out->row_pointers, b.plans, stat_max_ids,
+                     stat_max_unique, stat_required, counters);
+  SCEMB_LAUNCH_CHECK();
+  if (M > 0) {
+    hipLaunchKernelGGL((ScatterRuns<K>), dim3(CeilDiv(M, 256)), dim3(256), 0,
+                       stream, skeys, b.srows, b.run_pos, b.run_gain, b.keep,
+                       b.keep_scan, b.totals, M, pl.kl, fp,
+                       static_cast<int32_t>(pl.bps), b.bstats, b.plans,
+                       out->embedding_ids, out->sample_ids, out->gains);
+    SCEMB_LAUNCH_CHECK();
+    hipLaunchKernelGGL(StoreTotal, dim3(1), dim3(1), 0, stream, b.totals,
+                       counters);
+    SCEMB_LAUNCH_CHECK();
+  }
+  hipLaunchKernelGGL(WritePadding, dim3(CeilDiv(num_buckets * kAlign, 256)),
+                     dim3(256), 0, stream, b.plans, num_buckets, fp,
+                     out->embedding_ids, out->sample_ids, out->gains);
+  SCEMB_LAUNCH_CHECK();
+  return 0;
+}
+
+int Preprocess(const scemb_feature_t* feats, int nf,
+               const scemb_preprocess_options_t* o,
+               const scemb_preprocess_output_t* out, Arena& ws,
+               hipStream_t stream) {
+  Plan pl;
+  std::vector<std::vector<int64_t>> cache;
+  int st = MakePlan(feats, nf, o, &pl, &cache);
+  if (st != 0) return st;
+  if (pl.wide_keys) {
+    return RunPipeline<uint64_t>(feats, nf, o, out, pl, ws, stream);
+  }
+  return RunPipeline<uint32_t>(feats, nf, o, out, pl, ws, stream);
+}
+
+}  // namespace
+}  // namespace scemb
+
+using namespace scemb;
+
+extern "C" {
+
+int64_t scemb_preprocess_stats_counters_offset(
+    const scemb_preprocess_options_t* o) {
+  if (o == nullptr) return -1;
+  const int64_t L = o->local_device_count;
+  const int64_t NS = static_cast<int64_t>(o->num_sc_per_device) *
+                     o->global_device_count;
+  return RoundUp(2 * L * NS + L * o->num_sc_per_device, 2);
+}
+
+int64_t scemb_preprocess_stats_size(const scemb_preprocess_options_t* o) {
+  const int64_t off = scemb_preprocess_stats_counters_offset(o);
+  return off < 0 ? -1 : off + 8;
+}
+
+size_t scemb_preprocess_workspace_size(const scemb_feature_t* features,
+                                       int32_t num_features,
+                                       const scemb_preprocess_options_t* o) {
+  Arena ws(nullptr, 0);
+  if (Preprocess(features, num_features, o, nullptr, ws, nullptr) != 0) {
+    return 0;
+  }
+  return ws.used() + 256;
+}
+
+int scemb_preprocess_stacked_table(const scemb_feature_t* features,
+                                   int32_t num_features,
+                                   const scemb_preprocess_options_t* o,
+                                   const scemb_preprocess_output_t* out,
+                                   void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  if (workspace == nullptr) return Fail(SCEMB_ERR_WORKSPACE, "no workspace");
+  Arena ws(workspace, workspace_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int prof = ProfileBegin("preprocess_call", s);
+  const int rc = Preprocess(features, num_features, o, out, ws, s);
+  ProfileEnd(prof, s);
+  return rc;
+}
+
+int64_t scemb_compute_theoretical_max_coo_buffer_size(
+    int32_t max_ids_per_partition, int32_t global_device_count,
+    int32_t num_sc_per_device) {
+  const int64_t num_scs = static_cast<int64_t>(global_device_count) * num_sc_per_device;
+  return RoundUp(max_ids_per_partition, kAlign) * num_sc_per_device * num_scs;
+}
+
+int64_t scemb_compute_coo_buffer_size_per_device(
+    int32_t max_ids_per_partition, int64_t suggested, int32_t global_device_count,
+    int32_t num_sc_per_device) {
+  const int64_t theoretical = scemb_compute_theoretical_max_coo_buffer_size(
+      max_ids_per_partition, global_device_count, num_sc_per_device);
+  if (suggested <= 0) return theoretical;
+  const int64_t v = RoundUp(suggested, static_cast<int64_t>(kAlign) * num_sc_per_device);
+  return v > theoretical ? -1 : v;
+}
+
+int32_t scemb_compute_row_pointers_size_per_device(int32_t global_device_count,
+                                                   int32_t num_sc_per_device) {
+  const int32_t ns = global_device_count * num_sc_per_device;
+  return std::max(ns, kAlign) * num_sc_per_device;
+}
+
+}  // extern "C"

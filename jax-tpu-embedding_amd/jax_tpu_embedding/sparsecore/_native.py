@@ -1,0 +1,340 @@
+"""ctypes binding of libscemb.so (the C ABI declared in include/scemb.h).
+
+This is the only place where Python touches the native library. Device memory
+and streams come from torch: tensors are passed by ``data_ptr()`` and kernels
+are enqueued on ``torch.cuda.current_stream()``. There is no fallback: if the
+library or a GPU is missing, calls raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import threading
+
+import numpy as np
+
+_PKG_ROOT = pathlib.Path(__file__).resolve().parents[2]
+LIB_PATH = pathlib.Path(
+    os.environ.get("SCEMB_LIBRARY", str(_PKG_ROOT / "libscemb.so")))
+
+SCEMB_OK = 0
+SCEMB_ERR_INVALID_ARGUMENT = 1
+SCEMB_ERR_NOT_IMPLEMENTED = 2
+SCEMB_ERR_WORKSPACE = 3
+SCEMB_ERR_DEVICE = 4
+SCEMB_ERR_LIMIT_EXCEEDED = 5
+
+STATUS_BAD_ENTRY = 1
+STATUS_BAD_ID = 2
+
+# Every function declared in include/scemb.h.
+EXPORTED_SYMBOLS = (
+    "scemb_last_error",
+    "scemb_version",
+    "scemb_sparse_dense_matmul_workspace_size",
+    "scemb_sparse_dense_matmul",
+    "scemb_sparse_dense_matmul_grad_workspace_size",
+    "scemb_sparse_dense_matmul_grad_with_sgd",
+    "scemb_sparse_dense_matmul_grad_with_adagrad",
+    "scemb_preprocess_stats_size",
+    "scemb_preprocess_stats_counters_offset",
+    "scemb_preprocess_workspace_size",
+    "scemb_preprocess_stacked_table",
+    "scemb_compute_theoretical_max_coo_buffer_size",
+    "scemb_compute_coo_buffer_size_per_device",
+    "scemb_compute_row_pointers_size_per_device",
+    "scemb_profile_enable",
+    "scemb_profile_collect",
+)
+
+
+class Csr(ctypes.Structure):
+  _fields_ = [
+      ("row_pointers", ctypes.c_void_p),
+      ("embedding_ids", ctypes.c_void_p),
+      ("sample_ids", ctypes.c_void_p),
+      ("gains", ctypes.c_void_p),
+      ("coo_size", ctypes.c_int64),
+      ("num_segments", ctypes.c_int32),
+      ("num_partitions", ctypes.c_int32),
+      ("row_pointers_per_segment", ctypes.c_int32),
+      ("reserved", ctypes.c_int32),
+  ]
+
+
+class Feature(ctypes.Structure):
+  _fields_ = [
+      ("ids", ctypes.c_void_p),
+      ("weights", ctypes.c_void_p),
+      ("row_splits", ctypes.c_void_p),
+      ("row_splits_host", ctypes.c_void_p),
+      ("num_rows", ctypes.c_int64),
+      ("nnz", ctypes.c_int64),
+      ("valency", ctypes.c_int32),
+      ("row_offset", ctypes.c_int32),
+      ("col_offset", ctypes.c_int32),
+      ("col_shift", ctypes.c_int32),
+  ]
+
+
+class PreprocessOptions(ctypes.Structure):
+  _fields_ = [
+      ("local_device_count", ctypes.c_int32),
+      ("global_device_count", ctypes.c_int32),
+      ("num_sc_per_device", ctypes.c_int32),
+      ("combiner", ctypes.c_int32),
+      ("max_ids_per_partition", ctypes.c_int32),
+      ("max_unique_ids_per_partition", ctypes.c_int32),
+      ("allow_id_dropping", ctypes.c_int32),
+      ("has_variable_weights", ctypes.c_int32),
+      ("coo_buffer_size_per_device", ctypes.c_int64),
+      ("col_id_bound", ctypes.c_int64),
+  ]
+
+
+class PreprocessOutput(ctypes.Structure):
+  _fields_ = [
+      ("row_pointers", ctypes.c_void_p),
+      ("embedding_ids", ctypes.c_void_p),
+      ("sample_ids", ctypes.c_void_p),
+      ("gains", ctypes.c_void_p),
+      ("stats", ctypes.c_void_p),
+  ]
+
+
+_lib = None
+_lib_lock = threading.Lock()
+
+
+def load_library() -> ctypes.CDLL:
+  """Loads libscemb.so; raises RuntimeError when it was not built."""
+  global _lib
+  with _lib_lock:
+    if _lib is not None:
+      return _lib
+    if not LIB_PATH.exists():
+      raise RuntimeError(
+          f"libscemb.so not found at {LIB_PATH}; build it with "
+          "`python -c 'import __graft_entry__; __graft_entry__.build()'` or "
+          "`make -C jax-tpu-embedding_amd/csrc`.")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    vp, i32, i64, f32, sz = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
+                             ctypes.c_float, ctypes.c_size_t)
+    csr_p = ctypes.POINTER(Csr)
+    lib.scemb_last_error.restype = ctypes.c_char_p
+    lib.scemb_last_error.argtypes = []
+    lib.scemb_version.restype = ctypes.c_int
+    lib.scemb_version.argtypes = []
+    lib.scemb_sparse_dense_matmul_workspace_size.restype = sz
+    lib.scemb_sparse_dense_matmul_workspace_size.argtypes = [csr_p, i64, i64,
+                                                             i32]
+    lib.scemb_sparse_dense_matmul.restype = ctypes.c_int
+    lib.scemb_sparse_dense_matmul.argtypes = [csr_p, vp, i64, i32, vp, i64, vp,
+                                              sz, vp, vp]
+    lib.scemb_sparse_dense_matmul_grad_workspace_size.restype = sz
+    lib.scemb_sparse_dense_matmul_grad_workspace_size.argtypes = [
+        csr_p, i64, i64, i32]
+    lib.scemb_sparse_dense_matmul_grad_with_sgd.restype = ctypes.c_int
+    lib.scemb_sparse_dense_matmul_grad_with_sgd.argtypes = [
+        csr_p, vp, i64, vp, i64, i32, vp, f32, i32, f32, f32, vp, sz, vp, vp]
+    lib.scemb_sparse_dense_matmul_grad_with_adagrad.restype = ctypes.c_int
+    lib.scemb_sparse_dense_matmul_grad_with_adagrad.argtypes = [
+        csr_p, vp, i64, vp, vp, i64, i32, vp, f32, i32, f32, f32, vp, sz, vp,
+        vp]
+    opts_p = ctypes.POINTER(PreprocessOptions)
+    lib.scemb_preprocess_stats_size.restype = i64
+    lib.scemb_preprocess_stats_size.argtypes = [opts_p]
+    lib.scemb_preprocess_stats_counters_offset.restype = i64
+    lib.scemb_preprocess_stats_counters_offset.argtypes = [opts_p]
+    lib.scemb_preprocess_workspace_size.restype = sz
+    lib.scemb_preprocess_workspace_size.argtypes = [ctypes.POINTER(Feature),
+                                                    i32, opts_p]
+    lib.scemb_preprocess_stacked_table.restype = ctypes.c_int
+    lib.scemb_preprocess_stacked_table.argtypes = [
+        ctypes.POINTER(Feature), i32, opts_p, ctypes.POINTER(PreprocessOutput),
+        vp, sz, vp]
+    lib.scemb_compute_theoretical_max_coo_buffer_size.restype = i64
+    lib.scemb_compute_theoretical_max_coo_buffer_size.argtypes = [i32, i32,
+                                                                  i32]
+    lib.scemb_compute_coo_buffer_size_per_device.restype = i64
+    lib.scemb_compute_coo_buffer_size_per_device.argtypes = [i32, i64, i32,
+                                                             i32]
+    lib.scemb_compute_row_pointers_size_per_device.restype = i32
+    lib.scemb_compute_row_pointers_size_per_device.argtypes = [i32, i32]
+    lib.scemb_profile_enable.restype = None
+    lib.scemb_profile_enable.argtypes = [ctypes.c_int]
+    lib.scemb_profile_collect.restype = ctypes.c_int
+    lib.scemb_profile_collect.argtypes = [ctypes.c_char_p,
+                                          ctypes.POINTER(ctypes.c_double),
+                                          ctypes.POINTER(ctypes.c_int64)]
+    _lib = lib
+    return lib
+
+
+def profile_enable(on: bool) -> None:
+  """Turns the library's launch-timing events on or off."""
+  load_library().scemb_profile_enable(1 if on else 0)
+
+
+def profile_collect(name: str | None) -> tuple[float, int]:
+  """(summed milliseconds, launches) of the spans recorded under `name`."""
+  ms = ctypes.c_double(0.0)
+  n = ctypes.c_int64(0)
+  check(load_library().scemb_profile_collect(
+      None if name is None else name.encode(), ctypes.byref(ms),
+      ctypes.byref(n)))
+  return ms.value, n.value
+
+
+def check(rc: int) -> None:
+  """Maps a libscemb status code to the reference's Python exceptions."""
+  if rc == SCEMB_OK:
+    return
+  msg = load_library().scemb_last_error().decode("utf-8", "replace")
+  if rc == SCEMB_ERR_INVALID_ARGUMENT:
+    raise ValueError(msg)
+  if rc == SCEMB_ERR_NOT_IMPLEMENTED:
+    raise NotImplementedError(msg)
+  raise RuntimeError(f"libscemb error {rc}: {msg}")
+
+
+# ---------------------------------------------------------------------------
+# torch plumbing.
+# ---------------------------------------------------------------------------
+
+
+def torch():
+  import torch as _torch  # pylint: disable=g-import-not-at-top
+
+  return _torch
+
+
+def require_gpu():
+  t = torch()
+  if not t.cuda.is_available():
+    raise RuntimeError(
+        "The SparseCore embedding path runs on the GPU through libscemb.so; "
+        "no GPU is visible to torch.")
+  return t
+
+
+def stream_handle() -> int:
+  t = torch()
+  return t.cuda.current_stream().cuda_stream
+
+
+def device() -> "torch.device":
+  t = require_gpu()
+  return t.device("cuda", t.cuda.current_device())
+
+
+def as_device_tensor(x, dtype, dev=None):
+  """Returns x as a contiguous CUDA tensor of `dtype` (copies if needed)."""
+  t = require_gpu()
+  dev = dev or device()
+  if isinstance(x, t.Tensor):
+    if x.device != dev or x.dtype != dtype:
+      x = x.to(device=dev, dtype=dtype)
+    return x.contiguous()
+  arr = np.asarray(x)
+  np_dtype = {t.int32: np.int32, t.int64: np.int64,
+              t.float32: np.float32}[dtype]
+  arr = np.ascontiguousarray(arr, dtype=np_dtype)
+  return t.from_numpy(arr).to(dev, non_blocking=False)
+
+
+def ptr(x) -> int | None:
+  return None if x is None else x.data_ptr()
+
+
+class _Workspace:
+  """Per-device scratch buffer, grown on demand and reused across calls."""
+
+  def __init__(self):
+    self._buf = {}
+
+  def get(self, nbytes: int):
+    t = torch()
+    dev = device()
+    key = dev.index
+    buf = self._buf.get(key)
+    if buf is None or buf.numel() < nbytes:
+      buf = t.empty(max(int(nbytes * 1.25), 1 << 20), dtype=t.uint8,
+                    device=dev)
+      self._buf[key] = buf
+    return buf
+
+
+WORKSPACE = _Workspace()
+
+
+def make_csr(row_pointers, embedding_ids, sample_ids, gains, num_segments,
+             num_partitions) -> Csr:
+  rp_len = int(row_pointers.numel())
+  if rp_len % num_segments:
+    raise ValueError("row_pointers length must be divisible by "
+                     "num_sc_per_device")
+  return Csr(ptr(row_pointers), ptr(embedding_ids), ptr(sample_ids),
+             ptr(gains), int(embedding_ids.numel()), num_segments,
+             num_partitions, rp_len // num_segments, 0)
+
+
+def sparse_dense_matmul(csr: Csr, table, activations, batch: int,
+                        device_status=None) -> None:
+  lib = load_library()
+  rows = int(table.shape[0])
+  dim = 1 if table.dim() == 1 else int(table.shape[1])
+  need = lib.scemb_sparse_dense_matmul_workspace_size(ctypes.byref(csr), batch,
+                                                      rows, dim)
+  if need == 0:
+    check(SCEMB_ERR_INVALID_ARGUMENT)
+  ws = WORKSPACE.get(need)
+  check(lib.scemb_sparse_dense_matmul(
+      ctypes.byref(csr), ptr(table), rows, dim, ptr(activations), batch,
+      ptr(ws), ws.numel(), ptr(device_status), stream_handle()))
+
+
+def _lr_args(learning_rate):
+  t = torch()
+  if isinstance(learning_rate, t.Tensor):
+    lr = learning_rate.to(device=device(), dtype=t.float32).reshape(())
+    return lr, ptr(lr), 0.0
+  return None, None, float(np.float32(learning_rate))
+
+
+def _clip_args(min_value, max_value):
+  mask = (1 if min_value is not None else 0) | (2 if max_value is not None
+                                                 else 0)
+  return (mask, float(min_value) if min_value is not None else 0.0,
+          float(max_value) if max_value is not None else 0.0)
+
+
+def sparse_dense_matmul_grad(csr: Csr, activations_grad, table,
+                             accumulator, learning_rate, batch: int,
+                             min_value=None, max_value=None,
+                             device_status=None) -> None:
+  """SGD when accumulator is None, Adagrad otherwise; updates in place."""
+  lib = load_library()
+  rows = int(table.shape[0])
+  dim = 1 if table.dim() == 1 else int(table.shape[1])
+  need = lib.scemb_sparse_dense_matmul_grad_workspace_size(
+      ctypes.byref(csr), batch, rows, dim)
+  if need == 0:
+    check(SCEMB_ERR_INVALID_ARGUMENT)
+  ws = WORKSPACE.get(need)
+  keep, lr_ptr, lr_val = _lr_args(learning_rate)
+  mask, lo, hi = _clip_args(min_value, max_value)
+  if accumulator is None:
+    rc = lib.scemb_sparse_dense_matmul_grad_with_sgd(
+        ctypes.byref(csr), ptr(activations_grad), batch, ptr(table), rows, dim,
+        lr_ptr, lr_val, mask, lo, hi, ptr(ws), ws.numel(), ptr(device_status),
+        stream_handle())
+  else:
+    rc = lib.scemb_sparse_dense_matmul_grad_with_adagrad(
+        ctypes.byref(csr), ptr(activations_grad), batch, ptr(table),
+        ptr(accumulator), rows, dim, lr_ptr, lr_val, mask, lo, hi, ptr(ws),
+        ws.numel(), ptr(device_status), stream_handle())
+  del keep
+  check(rc)

@@ -1,0 +1,35 @@
+"""Operand marshalling from primitive ``bind`` arguments to the C ABI."""
+
+from __future__ import annotations
+
+from jax_tpu_embedding.sparsecore import _native
+from jax_tpu_embedding.sparsecore.utils import utils
+
+
+def resolve_sparsecores(num_sc_per_device, global_device_count):
+  """SparseCores (CSR segments) per device and partitions in total."""
+  if num_sc_per_device is None:
+    num_sc_per_device = utils.num_sparsecores_per_device()
+  g = 1 if global_device_count is None else int(global_device_count)
+  return int(num_sc_per_device), int(num_sc_per_device) * g
+
+
+def csr_operands(row_pointers, embedding_ids, sample_ids, gains,
+                 num_sc_per_device, num_partitions):
+  """Device tensors for the CSR buffers plus the C struct that points at
+  them (the tensors must stay alive while the struct is used)."""
+  t = _native.require_gpu()
+  dev = _native.device()
+  rp = _native.as_device_tensor(row_pointers, t.int32, dev).reshape(-1)
+  eid = _native.as_device_tensor(embedding_ids, t.int32, dev).reshape(-1)
+  sid = _native.as_device_tensor(sample_ids, t.int32, dev).reshape(-1)
+  g = _native.as_device_tensor(gains, t.float32, dev).reshape(-1)
+  csr = _native.make_csr(rp, eid, sid, g, num_sc_per_device, num_partitions)
+  return (rp, eid, sid, g), csr
+
+
+def device_table(table):
+  """The table as a contiguous float32 CUDA tensor; a CUDA float32 input is
+  returned as is so updates happen in place."""
+  t = _native.require_gpu()
+  return _native.as_device_tensor(table, t.float32, _native.device())

@@ -1,0 +1,79 @@
+"""Primitive tpu_sparse_dense_matmul_csr: the forward embedding lookup.
+
+Same operands and attributes as the reference primitive
+(``lib/core/primitives/sparse_dense_matmul_csr.py:47-62`` abstract eval,
+``:114-202`` lowering to the ``SparseDenseMatmulOp`` custom call); ``bind``
+validates like the abstract eval and runs ``scemb_sparse_dense_matmul``
+(gfx950 HIP) on the current stream. Result: float32 activations of shape
+``(device_batch_size, dim)`` (``(device_batch_size,)`` for a 1-D table).
+
+Extra keyword arguments (no reference counterpart; the TPU op reads them from
+the hardware): ``num_sc_per_device`` and ``global_device_count`` give the CSR
+segment / partition counts (defaults: the device's SparseCore count, 1).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from jax_tpu_embedding.sparsecore import _native
+from jax_tpu_embedding.sparsecore.lib.core.primitives import _device
+from jax_tpu_embedding.sparsecore.lib.core.primitives import utils
+
+
+def check_single_minibatch(num_minibatches):
+  """Host-side minibatch counts other than 1 are not supported (device
+  scalars are not read back, to keep the call asynchronous)."""
+  if isinstance(num_minibatches, (int, np.integer, np.ndarray)):
+    if int(np.asarray(num_minibatches).reshape(())) != 1:
+      raise NotImplementedError("only one minibatch is supported")
+
+
+def _validate_quantization(quantization_config):
+  if quantization_config is None:
+    return
+  q_min, q_max, q_buckets = quantization_config
+  if q_buckets < 2:
+    raise ValueError(
+        f"quantization_num_buckets must be at least 2, got {q_buckets}")
+  if q_min >= q_max:
+    raise ValueError(
+        "quantization_min_valuemust be less than quantization_max_value,"
+        f" got {q_min} and {q_max}")
+
+
+def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
+          lhs_gains, num_minibatches_per_physical_sparse_core,
+          embedding_table, *, device_batch_size: int,
+          max_ids_per_partition: int, max_unique_ids_per_partition: int,
+          sharding_strategy: int = 1, quantization_config=None,
+          enable_minibatching: bool = False, num_sc_per_device=None,
+          global_device_count=None):
+  utils.validate_abstract_eval_params(
+      lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
+      lhs_gains, num_minibatches_per_physical_sparse_core, embedding_table,
+      activations_grad=None,
+      max_ids_per_partition=max_ids_per_partition,
+      max_unique_ids_per_partition=max_unique_ids_per_partition,
+      computation_name="fwd-pass", sharding_strategy=sharding_strategy)
+  _validate_quantization(quantization_config)
+  if quantization_config is not None:
+    raise NotImplementedError("quantized tables are not supported yet")
+  if enable_minibatching:
+    raise NotImplementedError("minibatching is not supported on this path")
+  check_single_minibatch(num_minibatches_per_physical_sparse_core)
+  t = _native.require_gpu()
+  s, ns = _device.resolve_sparsecores(num_sc_per_device, global_device_count)
+  keep, csr = _device.csr_operands(lhs_row_pointers, lhs_local_embedding_ids,
+                                   lhs_local_sample_ids, lhs_gains, s, ns)
+  table = _device.device_table(embedding_table)
+  shape = ((device_batch_size,) if table.dim() == 1 else
+           (device_batch_size, int(table.shape[1])))
+  out = t.empty(shape, dtype=t.float32, device=table.device)
+  _native.sparse_dense_matmul(csr, table, out, int(device_batch_size))
+  del keep
+  return out
+
+
+tpu_sparse_dense_matmul_csr_primitive = utils.Primitive(
+    "sparse_dense_matmul_csr", _impl)

@@ -1,0 +1,61 @@
+"""Primitive tpu_sparse_dense_matmul_grad_with_adagrad: backward + Adagrad.
+
+Same operands and attributes as the reference primitive
+(``lib/core/primitives/sparse_dense_matmul_grad_with_adagrad.py:63-113``
+abstract eval, ``multiple_results=True``; lowering ``:119-286`` with the
+per-row update ``acc += g * g; table -= (lr * g) / sqrt(acc)`` and optional
+clipping of the table, ``:167-233``). ``bind`` runs
+``scemb_sparse_dense_matmul_grad_with_adagrad`` on the current stream and
+returns ``(table, accumulator)``, updated in place when they are float32 CUDA
+tensors.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from jax_tpu_embedding.sparsecore import _native
+from jax_tpu_embedding.sparsecore.lib.core.primitives import _device
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_csr
+from jax_tpu_embedding.sparsecore.lib.core.primitives import utils
+
+
+def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
+          lhs_gains, num_minibatches_per_physical_sparse_core,
+          embedding_table, accumulator, activations_grad, learning_rate, *_,
+          max_ids_per_partition: int, max_unique_ids_per_partition: int,
+          computation_name: str = "adagrad_optimizer_update",
+          sharding_strategy: int = 1, enable_minibatching: bool = False,
+          min_value=None, max_value=None, num_sc_per_device=None,
+          global_device_count=None):
+  utils.validate_abstract_eval_params(
+      lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
+      lhs_gains, num_minibatches_per_physical_sparse_core, embedding_table,
+      activations_grad, max_ids_per_partition, max_unique_ids_per_partition,
+      computation_name, sharding_strategy, min_value, max_value)
+  utils.ensure_dtype(accumulator, np.float32, "accumulator")
+  utils.ensure_dtype(learning_rate, np.float32, "learning_rate")
+  if tuple(embedding_table.shape) != tuple(accumulator.shape):
+    raise ValueError(
+        "embedding_table and accumulator must have equal shapes, got"
+        f" {tuple(embedding_table.shape)} and {tuple(accumulator.shape)}")
+  if enable_minibatching:
+    raise NotImplementedError("minibatching is not supported on this path")
+  sparse_dense_matmul_csr.check_single_minibatch(
+      num_minibatches_per_physical_sparse_core)
+  t = _native.require_gpu()
+  s, ns = _device.resolve_sparsecores(num_sc_per_device, global_device_count)
+  keep, csr = _device.csr_operands(lhs_row_pointers, lhs_local_embedding_ids,
+                                   lhs_local_sample_ids, lhs_gains, s, ns)
+  table = _device.device_table(embedding_table)
+  acc = _device.device_table(accumulator)
+  grad = _native.as_device_tensor(activations_grad, t.float32, table.device)
+  _native.sparse_dense_matmul_grad(csr, grad, table, acc, learning_rate,
+                                   int(grad.shape[0]), min_value, max_value)
+  del keep
+  return table, acc
+
+
+tpu_sparse_dense_matmul_grad_with_adagrad_primitive = utils.Primitive(
+    "sparse_dense_matmul_grad_with_adagrad_primitive", _impl)
+tpu_sparse_dense_matmul_grad_with_adagrad_primitive.multiple_results = True

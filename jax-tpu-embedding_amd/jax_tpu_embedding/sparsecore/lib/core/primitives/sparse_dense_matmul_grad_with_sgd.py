@@ -1,0 +1,56 @@
+"""Primitive tpu_sparse_dense_matmul_grad_with_sgd: backward pass + SGD.
+
+Same operands and attributes as the reference primitive
+(``lib/core/primitives/sparse_dense_matmul_grad_with_sgd.py:51-69`` abstract
+eval; lowering ``:98-232`` to ``SparseDenseMatmulGradOpWithOptimizerUpdate``
+with the per-row update ``table - grad * lr``, ``:145-192``, and optional
+clipping, ``primitives/utils.py:24-59``). ``bind`` runs
+``scemb_sparse_dense_matmul_grad_with_sgd`` on the current stream.
+
+The table is updated in place when it is already a float32 CUDA tensor (the
+returned tensor is that same tensor, the equivalent of donating the buffer);
+other inputs are copied to the GPU first and the copy is returned.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from jax_tpu_embedding.sparsecore import _native
+from jax_tpu_embedding.sparsecore.lib.core.primitives import _device
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_csr
+from jax_tpu_embedding.sparsecore.lib.core.primitives import utils
+
+
+def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
+          lhs_gains, num_minibatches_per_physical_sparse_core,
+          embedding_table, activations_grad, learning_rate, *_,
+          max_ids_per_partition: int, max_unique_ids_per_partition: int,
+          computation_name: str = "sgd_optimizer_update",
+          sharding_strategy: int = 1, enable_minibatching: bool = False,
+          min_value=None, max_value=None, num_sc_per_device=None,
+          global_device_count=None):
+  utils.ensure_dtype(learning_rate, np.float32, "learning_rate")
+  utils.validate_abstract_eval_params(
+      lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
+      lhs_gains, num_minibatches_per_physical_sparse_core, embedding_table,
+      activations_grad, max_ids_per_partition, max_unique_ids_per_partition,
+      computation_name, sharding_strategy, min_value, max_value)
+  if enable_minibatching:
+    raise NotImplementedError("minibatching is not supported on this path")
+  sparse_dense_matmul_csr.check_single_minibatch(
+      num_minibatches_per_physical_sparse_core)
+  t = _native.require_gpu()
+  s, ns = _device.resolve_sparsecores(num_sc_per_device, global_device_count)
+  keep, csr = _device.csr_operands(lhs_row_pointers, lhs_local_embedding_ids,
+                                   lhs_local_sample_ids, lhs_gains, s, ns)
+  table = _device.device_table(embedding_table)
+  grad = _native.as_device_tensor(activations_grad, t.float32, table.device)
+  _native.sparse_dense_matmul_grad(csr, grad, table, None, learning_rate,
+                                   int(grad.shape[0]), min_value, max_value)
+  del keep
+  return table
+
+
+tpu_sparse_dense_matmul_grad_with_sgd_primitive = utils.Primitive(
+    "sparse_dense_matmul_grad_with_sgd", _impl)

@@ -1,0 +1,363 @@
+"""GPU preprocessing with the interface of the reference's pybind module.
+
+Mirrors ``lib/core/pybind_input_preprocessing.cc`` (functions bound at
+:291-330, stubs in ``pybind_input_preprocessing.pyi:38-86``): same function
+names, argument meaning, output tuple and exceptions (``ValueError`` for
+invalid arguments, ``RuntimeError`` where the reference aborts). The work runs
+on the GPU through ``scemb_preprocess_stacked_table``; outputs are torch CUDA
+tensors (flattened unless ``has_leading_dimension``), stats are numpy.
+
+Not supported on this path (raise ``NotImplementedError``): minibatching
+(``enable_minibatching=True``) and the sparse-COO entry point.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+import enum
+
+import numpy as np
+
+from jax_tpu_embedding.sparsecore import _native
+
+_COMBINERS = {"sum": 0, "mean": 1, "sqrtn": 2}
+
+
+class ShardingStrategy(enum.IntEnum):
+  MOD = 1
+
+
+class AllReduceInterface:  # pylint: disable=too-few-public-methods
+  """Placeholder type: cross-host minibatching is not part of this path."""
+
+
+class SparseDenseMatmulInputStats:
+  """Stats of one preprocessing call (input_preprocessing.h:30-43)."""
+
+  def __init__(self):
+    self.max_ids_per_partition = {}
+    self.max_unique_ids_per_partition = {}
+    self.required_buffer_sizes = {}
+    self.dropped_id_count = {}
+
+  def TotalDroppedIdCount(self) -> int:  # pylint: disable=invalid-name
+    return int(sum(self.dropped_id_count.values()))
+
+
+@dataclasses.dataclass
+class FeatureMetadataInStack:
+  """One feature of a stacked table (input_preprocessing_util.h:524-571)."""
+
+  name: str
+  feature_index: int
+  max_ids_per_partition: int
+  max_unique_ids_per_partition: int
+  row_offset: int
+  col_offset: int
+  col_shift: int
+  batch_size: int
+  suggested_coo_buffer_size_per_device: int | None
+  row_combiner: str
+  max_col_id: int
+  stack_vocab_size: int
+
+
+def get_stacked_table_metadata(feature_specs):
+  """GetStackedTableMetadata (pybind_input_preprocessing.cc:55-122)."""
+  out: dict[str, list[FeatureMetadataInStack]] = {}
+  for i, fs in enumerate(feature_specs):
+    tr = fs._id_transformation  # pylint: disable=protected-access
+    table_spec = fs.table_spec
+    stacked = table_spec.stacked_table_spec
+    if stacked is None:
+      raise ValueError(f"stacked_table_spec is none for table {table_spec.name}")
+    stack_name = table_spec.setting_in_stack.stack_name
+    row_offset = col_offset = col_shift = 0
+    if tr is not None:
+      row_offset, col_offset, col_shift = (int(tr.row_offset),
+                                           int(tr.col_offset),
+                                           int(tr.col_shift))
+    out.setdefault(stack_name, []).append(
+        FeatureMetadataInStack(
+            name=fs.name,
+            feature_index=i,
+            max_ids_per_partition=int(stacked.max_ids_per_partition),
+            max_unique_ids_per_partition=int(
+                stacked.max_unique_ids_per_partition),
+            row_offset=row_offset,
+            col_offset=col_offset,
+            col_shift=col_shift,
+            batch_size=int(fs.input_shape[0]),
+            suggested_coo_buffer_size_per_device=(
+                stacked.suggested_coo_buffer_size_per_device),
+            row_combiner=stacked.combiner,
+            max_col_id=int(table_spec.vocabulary_size),
+            stack_vocab_size=int(stacked.stack_vocab_size)))
+  for metas in out.values():
+    metas.sort(key=lambda m: m.row_offset)
+  return out
+
+
+# ---------------------------------------------------------------------------
+# Size helpers (pybind_input_preprocessing.cc:203-262, bound at :311-320).
+# ---------------------------------------------------------------------------
+
+
+def compute_row_pointers_size_per_device(global_device_count: int,
+                                         num_sc_per_device: int,
+                                         enable_minibatching: bool = False):
+  if enable_minibatching:
+    raise NotImplementedError("minibatching is not supported on this path")
+  return int(_native.load_library().scemb_compute_row_pointers_size_per_device(
+      global_device_count, num_sc_per_device))
+
+
+def compute_theoretical_max_coo_buffer_size(max_ids_per_partition: int,
+                                            global_device_count: int,
+                                            num_sc_per_device: int,
+                                            enable_minibatching: bool = False):
+  if enable_minibatching:
+    raise NotImplementedError("minibatching is not supported on this path")
+  return int(
+      _native.load_library().scemb_compute_theoretical_max_coo_buffer_size(
+          max_ids_per_partition, global_device_count, num_sc_per_device))
+
+
+def _coo_buffer_size(meta: FeatureMetadataInStack, global_device_count,
+                     num_sc_per_device) -> int:
+  v = _native.load_library().scemb_compute_coo_buffer_size_per_device(
+      meta.max_ids_per_partition,
+      meta.suggested_coo_buffer_size_per_device or 0, global_device_count,
+      num_sc_per_device)
+  if v < 0:
+    raise RuntimeError(
+        "Suggested Coo Buffer Size is larger than the theoretical max for "
+        f"table {meta.name}. Adjust the suggested size or the "
+        "max_ids_per_partition values.")
+  if v >= 2**31 - 1:
+    raise RuntimeError(f"Computed Coo Buffer Size ({v}) for table "
+                       f"{meta.name} is out of the valid range (0, INT_MAX).")
+  return int(v)
+
+
+def compute_coo_buffer_size_per_device(feature_specs, global_device_count: int,
+                                       num_sc_per_device: int,
+                                       enable_minibatching: bool = False):
+  if enable_minibatching:
+    raise NotImplementedError("minibatching is not supported on this path")
+  stacks = get_stacked_table_metadata(list(feature_specs))
+  return {
+      name: _coo_buffer_size(metas[0], global_device_count, num_sc_per_device)
+      for name, metas in stacks.items()
+  }
+
+
+# ---------------------------------------------------------------------------
+# Input conversion.
+# ---------------------------------------------------------------------------
+
+
+@dataclasses.dataclass
+class _DeviceFeature:
+  ids: object
+  weights: object | None
+  splits: object | None
+  splits_host: np.ndarray | None
+  num_rows: int
+  nnz: int
+  valency: int
+  max_id: int | None  # known when the input came from host memory
+
+
+def _to_device_feature(feature, weights) -> _DeviceFeature:
+  t = _native.require_gpu()
+  dev = _native.device()
+  if isinstance(feature, t.Tensor):
+    f = feature
+    if f.dim() == 1:
+      f = f.reshape(-1, 1)
+    if f.dim() != 2:
+      raise ValueError("Only 1D and 2D inputs are supported.")
+    ids = _native.as_device_tensor(f.reshape(-1), t.int32, dev)
+    w = None
+    if weights is not None:
+      w = _native.as_device_tensor(
+          weights.reshape(-1) if isinstance(weights, t.Tensor) else
+          np.asarray(weights, np.float32).reshape(-1), t.float32, dev)
+    return _DeviceFeature(ids, w, None, None, int(f.shape[0]), int(f.numel()),
+                          int(f.shape[1]), None)
+  arr = feature if isinstance(feature, np.ndarray) else np.asarray(
+      feature, dtype=object)
+  if arr.dtype != object and arr.ndim == 2:
+    ids_np = np.ascontiguousarray(arr, dtype=np.int32).reshape(-1)
+    w_np = None
+    if weights is not None:
+      w_np = np.ascontiguousarray(np.asarray(weights, dtype=np.float32)
+                                  ).reshape(-1)
+      if w_np.shape != ids_np.shape:
+        raise ValueError("Batch size mismatch for features and weights.")
+    b, k = arr.shape
+    max_id = int(ids_np.max()) if ids_np.size else None
+    return _DeviceFeature(
+        _native.as_device_tensor(ids_np, t.int32, dev),
+        None if w_np is None else _native.as_device_tensor(w_np, t.float32,
+                                                           dev),
+        None, None, b, b * k, k, max_id)
+  if arr.dtype != object and arr.ndim == 1:
+    # One id per sample.
+    return _to_device_feature(arr.reshape(-1, 1),
+                              None if weights is None else
+                              np.asarray(weights, np.float32).reshape(-1, 1))
+  if arr.ndim != 1:
+    raise ValueError("Only 1D and 2D numpy arrays supported as inputs.")
+  rows = [np.asarray(r).reshape(-1) for r in arr]
+  lens = np.fromiter((len(r) for r in rows), dtype=np.int64, count=len(rows))
+  splits = np.zeros(len(rows) + 1, np.int64)
+  np.cumsum(lens, out=splits[1:])
+  ids_np = (np.concatenate(rows).astype(np.int32) if splits[-1] else
+            np.zeros(0, np.int32))
+  w_np = None
+  if weights is not None:
+    wrows = [np.asarray(x, np.float32).reshape(-1) for x in weights]
+    if len(wrows) != len(rows) or any(
+        len(a) != len(b) for a, b in zip(wrows, rows)):
+      raise ValueError("Batch size mismatch for features and weights.")
+    w_np = (np.concatenate(wrows) if splits[-1] else np.zeros(0, np.float32))
+  max_id = int(ids_np.max()) if ids_np.size else None
+  return _DeviceFeature(
+      _native.as_device_tensor(ids_np, t.int32, dev),
+      None if w_np is None else _native.as_device_tensor(w_np, t.float32, dev),
+      _native.as_device_tensor(splits, t.int64, dev), splits, len(rows),
+      int(splits[-1]), 0, max_id)
+
+
+def _preprocess_stack(feats, metas, *, local_device_count,
+                      global_device_count, num_sc_per_device,
+                      allow_id_dropping, has_weights):
+  """Runs one stacked table; returns (rp, eid, sid, gains, stats_np)."""
+  t = _native.require_gpu()
+  lib = _native.load_library()
+  dev = _native.device()
+  ns = num_sc_per_device * global_device_count
+  c = _coo_buffer_size(metas[0], global_device_count, num_sc_per_device)
+  bound = max(m.stack_vocab_size for m in metas)
+  for f, m in zip(feats, metas):
+    if f.max_id is not None:
+      bound = max(bound, m.col_offset + f.max_id + ns + 1)
+  opts = _native.PreprocessOptions(
+      local_device_count, global_device_count, num_sc_per_device,
+      _COMBINERS.get(metas[0].row_combiner, 0),
+      metas[0].max_ids_per_partition, metas[0].max_unique_ids_per_partition,
+      int(bool(allow_id_dropping)), int(bool(has_weights)), c, bound)
+  structs = (_native.Feature * len(feats))()
+  for i, (f, m) in enumerate(zip(feats, metas)):
+    structs[i] = _native.Feature(
+        _native.ptr(f.ids), _native.ptr(f.weights), _native.ptr(f.splits),
+        None if f.splits_host is None else f.splits_host.ctypes.data,
+        f.num_rows, f.nnz, f.valency, m.row_offset, m.col_offset, m.col_shift)
+  need = lib.scemb_preprocess_workspace_size(structs, len(feats),
+                                             ctypes.byref(opts))
+  if need == 0:
+    _native.check(_native.SCEMB_ERR_INVALID_ARGUMENT)
+  ws = _native.WORKSPACE.get(need)
+  L, S = local_device_count, num_sc_per_device
+  rp = t.empty(L * S * max(ns, 8), dtype=t.int32, device=dev)
+  eid = t.empty(L * c, dtype=t.int32, device=dev)
+  sid = t.empty(L * c, dtype=t.int32, device=dev)
+  gains = t.empty(L * c, dtype=t.float32, device=dev)
+  nstats = lib.scemb_preprocess_stats_size(ctypes.byref(opts))
+  stats = t.zeros(nstats + 2, dtype=t.int32, device=dev)
+  out = _native.PreprocessOutput(_native.ptr(rp), _native.ptr(eid),
+                                 _native.ptr(sid), _native.ptr(gains),
+                                 _native.ptr(stats))
+  _native.check(lib.scemb_preprocess_stacked_table(
+      structs, len(feats), ctypes.byref(opts), ctypes.byref(out),
+      _native.ptr(ws), ws.numel(), _native.stream_handle()))
+  stats_np = stats.cpu().numpy()  # synchronises the stream
+  off = int(lib.scemb_preprocess_stats_counters_offset(ctypes.byref(opts)))
+  counters = stats_np[off:off + 8].copy().view(np.int64)
+  return rp, eid, sid, gains, stats_np, counters, (L, S, ns, off)
+
+
+def preprocess_sparse_dense_matmul_input(
+    features,
+    feature_weights,
+    feature_specs,
+    local_device_count: int,
+    global_device_count: int,
+    *,
+    num_sc_per_device: int,
+    sharding_strategy=ShardingStrategy.MOD,
+    has_leading_dimension: bool = False,
+    allow_id_dropping: bool = False,
+    batch_number: int = 0,
+    enable_minibatching: bool = False,
+    all_reduce_interface=None,
+):
+  """PyNumpyPreprocessSparseDenseMatmulInput (pybind_input_preprocessing.cc:
+  190-216 and :124-188) on the GPU.
+
+  Returns (row_pointers, embedding_ids, sample_ids, gains, num_minibatches,
+  stats): four dicts keyed by stacked-table name, the minibatch count (1) and
+  a SparseDenseMatmulInputStats.
+  """
+  del batch_number, all_reduce_interface
+  if enable_minibatching:
+    raise NotImplementedError("minibatching is not supported on this path")
+  if int(sharding_strategy) != int(ShardingStrategy.MOD):
+    raise ValueError("Only mod sharding is supported for now.")
+  features = list(features)
+  feature_specs = list(feature_specs)
+  if feature_weights is not None:
+    feature_weights = list(feature_weights)
+    if len(feature_weights) != len(features):
+      raise ValueError("features and feature_weights must have equal length")
+  if len(features) != len(feature_specs):
+    raise ValueError("features and feature_specs must have equal length")
+  if not features:
+    raise ValueError("input_batches cannot be empty.")
+  stacks = get_stacked_table_metadata(feature_specs)
+  rps, eids, sids, gns = {}, {}, {}, {}
+  stats = SparseDenseMatmulInputStats()
+  for name, metas in stacks.items():
+    feats = [
+        _to_device_feature(
+            features[m.feature_index],
+            None if feature_weights is None else
+            feature_weights[m.feature_index]) for m in metas
+    ]
+    rp, eid, sid, gains, stats_np, counters, (L, S, ns, _) = (
+        _preprocess_stack(feats, metas,
+                          local_device_count=local_device_count,
+                          global_device_count=global_device_count,
+                          num_sc_per_device=num_sc_per_device,
+                          allow_id_dropping=allow_id_dropping,
+                          has_weights=feature_weights is not None))
+    if counters[2] > 0:
+      raise ValueError(
+          f"{int(counters[2])} embedding ids of stacked table {name} are "
+          "negative or beyond the stacked vocabulary.")
+    if counters[1] > 0:
+      raise RuntimeError(
+          f"Observed max ids per partition for table: {name} is greater than "
+          "the set max ids per partition. Use `allow_id_dropping` or increase "
+          "the `max_ids_per_partition`. You could also try to reduce the "
+          "batch size.")
+    stats.max_ids_per_partition[name] = stats_np[:L * ns].copy()
+    stats.max_unique_ids_per_partition[name] = stats_np[L * ns:2 * L *
+                                                        ns].copy()
+    stats.required_buffer_sizes[name] = stats_np[2 * L * ns:2 * L * ns +
+                                                 L * S].copy()
+    stats.dropped_id_count[name] = int(counters[0])
+    if has_leading_dimension:
+      rp, eid, sid, gains = (rp.reshape(L, -1), eid.reshape(L, -1),
+                             sid.reshape(L, -1), gains.reshape(L, -1))
+    rps[name], eids[name], sids[name], gns[name] = rp, eid, sid, gains
+  return rps, eids, sids, gns, 1, stats
+
+
+def preprocess_sparse_dense_matmul_sparse_coo_input(*args, **kwargs):
+  del args, kwargs
+  raise NotImplementedError(
+      "The sparse-COO input entry point is not part of this path yet.")

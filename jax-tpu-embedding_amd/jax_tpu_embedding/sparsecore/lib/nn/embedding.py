@@ -1,0 +1,562 @@
+"""Embedding API for the MI355X SparseCore path (reference: lib/nn/embedding.py).
+
+Same entry points, arguments and results as the reference module:
+  preprocess_sparse_dense_matmul_input   (:608-705)  -> GPU preprocessing
+  tpu_sparse_dense_matmul                (:1047-1184) -> forward lookup
+  tpu_sparse_dense_matmul_grad           (:1297-1529) -> backward + optimizer
+  stack_embedding_gradients / unstack_embedding_activations (:903-1294)
+  prepare_feature_specs_for_training, auto_stack_tables, size helpers,
+  init_embedding_variables, update_preprocessing_parameters.
+Arrays are torch tensors on the GPU (numpy inputs are copied there). Tables
+and slots are updated in place by the gradient step, which returns them.
+"""
+
+from __future__ import annotations
+
+import collections
+import dataclasses
+import warnings
+from typing import Mapping, NamedTuple
+
+import numpy as np
+
+from jax_tpu_embedding.sparsecore import _native
+from jax_tpu_embedding.sparsecore import _tree
+from jax_tpu_embedding.sparsecore.lib.core import pybind_input_preprocessing
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_csr
+from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec
+from jax_tpu_embedding.sparsecore.lib.nn import table_stacking
+from jax_tpu_embedding.sparsecore.utils import utils
+
+LimitsCallable = table_stacking.LimitsCallable
+get_default_limits = table_stacking.get_default_limits
+
+
+def _assert_same_structure(a, b, a_name="a", b_name="b"):
+  if _tree.leaf_paths(a) != _tree.leaf_paths(b):
+    raise ValueError(f"Pytree structures of {a_name} and {b_name} do not "
+                     "match.")
+
+
+class EmbeddingVariables(NamedTuple):
+  table: object
+  slot: tuple
+
+
+class SparseDenseMatmulInput(NamedTuple):
+  """The CSR-wrapped COO buffers per stacked table."""
+
+  lhs_row_pointers: Mapping
+  lhs_embedding_ids: Mapping
+  lhs_sample_ids: Mapping
+  lhs_gains: Mapping
+
+
+@dataclasses.dataclass
+class SparseDenseMatmulInputStats:
+  """Preprocessing stats per stacked table (embedding.py:97-188)."""
+
+  max_ids_per_partition: dict = dataclasses.field(default_factory=dict)
+  max_unique_ids_per_partition: dict = dataclasses.field(default_factory=dict)
+  required_buffer_size_per_sc: dict = dataclasses.field(default_factory=dict)
+  id_drop_counters: dict = dataclasses.field(default_factory=dict)
+
+  @classmethod
+  def from_cc(cls, stats) -> "SparseDenseMatmulInputStats":
+    return cls(
+        max_ids_per_partition=stats.max_ids_per_partition,
+        max_unique_ids_per_partition=stats.max_unique_ids_per_partition,
+        required_buffer_size_per_sc=stats.required_buffer_sizes,
+        id_drop_counters=stats.dropped_id_count,
+    )
+
+  def get_required_buffer_size_per_device(self, table_name: str,
+                                          num_sc_per_device: int | None = None):
+    if table_name not in self.required_buffer_size_per_sc:
+      return None
+    val = self.required_buffer_size_per_sc[table_name]
+    num_sc = num_sc_per_device or np.size(val)
+    return int(np.max(val) * num_sc)
+
+  def set_required_buffer_size_per_device(self, table_name: str,
+                                          required_buffer_size_per_device: int,
+                                          num_sc_per_device: int | None = None):
+    val = self.required_buffer_size_per_sc.get(table_name)
+    num_sc = num_sc_per_device or (np.size(val) if val is not None else 0)
+    if not num_sc:
+      raise ValueError(
+          "num_sc_per_device must be provided if the table is not present.")
+    self.required_buffer_size_per_sc[table_name] = np.full(
+        num_sc, required_buffer_size_per_device / num_sc)
+
+
+@dataclasses.dataclass
+class PreprocessedInput:
+  """Result of preprocessing: the CSR buffers and the minibatch count."""
+
+  sparse_dense_matmul_input: SparseDenseMatmulInput
+  num_minibatches: object = dataclasses.field(
+      default_factory=lambda: np.array(1))
+
+  @property
+  def lhs_row_pointers(self):
+    return self.sparse_dense_matmul_input.lhs_row_pointers
+
+  @property
+  def lhs_embedding_ids(self):
+    return self.sparse_dense_matmul_input.lhs_embedding_ids
+
+  @property
+  def lhs_sample_ids(self):
+    return self.sparse_dense_matmul_input.lhs_sample_ids
+
+  @property
+  def lhs_gains(self):
+    return self.sparse_dense_matmul_input.lhs_gains
+
+  def __iter__(self):
+    warnings.warn(
+        "Please use attributed lookup on sparse_dense_matmul_input attribute.",
+        DeprecationWarning)
+    return iter(self.sparse_dense_matmul_input)
+
+
+def _verify_feature_specs(feature_specs) -> None:
+  seen = set()
+  for fs in _tree.tree_leaves(feature_specs):
+    if fs.name in seen:
+      raise ValueError(f"Feature spec {fs.name} is already defined.")
+    seen.add(fs.name)
+
+
+def _get_num_sc_per_device(num_sc_per_device: int | None) -> int:
+  if num_sc_per_device is None:
+    return utils.num_sparsecores_per_device()
+  if num_sc_per_device not in utils.NUM_SC_PER_DEVICE_MAP.values():
+    raise ValueError(f"Invalid num_sc_per_device: {num_sc_per_device}")
+  return num_sc_per_device
+
+
+def get_table_specs(feature_specs):
+  _verify_feature_specs(feature_specs)
+  out = {}
+  for fs in _tree.tree_leaves(feature_specs):
+    out[fs.table_spec.name] = fs.table_spec
+  return out
+
+
+def get_stacked_table_specs(feature_specs):
+  _verify_feature_specs(feature_specs)
+  leaves = _tree.tree_leaves(feature_specs)
+  if any(not fs.table_spec.is_stacked() for fs in leaves):
+    raise ValueError(
+        "embedding.prepare_feature_specs_for_training was not called")
+  return {fs.table_spec.stacked_table_spec.stack_name:
+          fs.table_spec.stacked_table_spec for fs in leaves}
+
+
+def prepare_feature_specs_for_training(feature_specs, global_device_count: int,
+                                       num_sc_per_device: int | None = None):
+  """Gives every unstacked table a stack of its own and stacks the features
+  that share a table (embedding.py:342-453)."""
+  num_sc_per_device = _get_num_sc_per_device(num_sc_per_device)
+  leaves = _tree.tree_leaves(feature_specs)
+  not_stacked = [f for f in leaves if not f.table_spec.is_stacked()]
+  by_table = collections.defaultdict(list)
+  for f in not_stacked:
+    by_table[f.table_spec.name].append(f)
+  row_offsets = {}
+  for features in by_table.values():
+    offset = 0
+    for f in sorted(features, key=lambda f: f.name):
+      row_offsets[f.name] = offset
+      offset += int(np.prod(f.output_shape[:-1]))
+  ns = num_sc_per_device * global_device_count
+  for f in leaves:
+    if f not in not_stacked:
+      continue
+    t = f.table_spec
+    s = t._setting_in_stack  # pylint: disable=protected-access
+    if s is not None and s.stack_name != t.name:
+      raise ValueError(
+          f"Invalid stacking. Table {t.name} does not have StackedTableSpec "
+          f"populated, but feature.table_spec.setting_in_stack.stack_name "
+          f"({s.stack_name}) is not {t.name}.")
+    dims, vocabs = table_stacking.round_up_dim_and_vocab_size({t.name: t}, ns)
+    total = sum(int(np.prod(g.output_shape[:-1])) for g in by_table[t.name])
+    t.setting_in_stack = embedding_spec.TableSettingInStack(
+        stack_name=t.name, padded_embedding_dim=dims[t.name],
+        padded_vocab_size=vocabs[t.name], row_offset_in_shard=0,
+        shard_rotation=0)
+    t.stacked_table_spec = embedding_spec.StackedTableSpec(
+        stack_name=t.name, stack_vocab_size=vocabs[t.name],
+        stack_embedding_dim=dims[t.name], optimizer=t.optimizer,
+        combiner=t.combiner, total_sample_count=total,
+        max_ids_per_partition=t.max_ids_per_partition,
+        max_unique_ids_per_partition=t.max_unique_ids_per_partition,
+        suggested_coo_buffer_size_per_device=(
+            t.suggested_coo_buffer_size_per_device),
+        quantization_config=t.quantization_config)
+    f.id_transformation = embedding_spec.FeatureIdTransformation(
+        row_offset=row_offsets.get(f.name, 0), col_offset=0, col_shift=0)
+
+
+def auto_stack_tables(feature_specs, global_device_count: int,
+                      num_sc_per_device: int | None = None,
+                      stack_to_max_ids_per_partition=get_default_limits,
+                      stack_to_max_unique_ids_per_partition=get_default_limits,
+                      use_short_stack_names: bool = True, *,
+                      activation_mem_bytes_limit: int | None = None) -> None:
+  num_sc_per_device = _get_num_sc_per_device(num_sc_per_device)
+  table_stacking.auto_stack_tables(
+      feature_specs, global_device_count=global_device_count,
+      num_sc_per_device=num_sc_per_device,
+      stack_to_max_ids_per_partition=stack_to_max_ids_per_partition,
+      stack_to_max_unique_ids_per_partition=(
+          stack_to_max_unique_ids_per_partition),
+      use_short_stack_names=use_short_stack_names,
+      activation_mem_bytes_limit=activation_mem_bytes_limit)
+
+
+def compute_row_pointers_size_per_device(*, global_device_count: int,
+                                         num_sc_per_device: int | None = None,
+                                         enable_minibatching: bool = False):
+  return pybind_input_preprocessing.compute_row_pointers_size_per_device(
+      global_device_count=global_device_count,
+      num_sc_per_device=_get_num_sc_per_device(num_sc_per_device),
+      enable_minibatching=enable_minibatching)
+
+
+def compute_theoretical_max_coo_buffer_size(max_ids_per_partition: int,
+                                            global_device_count: int,
+                                            num_sc_per_device: int | None = None,
+                                            enable_minibatching: bool = False):
+  return pybind_input_preprocessing.compute_theoretical_max_coo_buffer_size(
+      max_ids_per_partition=max_ids_per_partition,
+      global_device_count=global_device_count,
+      num_sc_per_device=_get_num_sc_per_device(num_sc_per_device),
+      enable_minibatching=enable_minibatching)
+
+
+def compute_coo_buffer_size_per_device(feature_specs, global_device_count: int,
+                                       num_sc_per_device: int | None = None,
+                                       enable_minibatching: bool = False):
+  return pybind_input_preprocessing.compute_coo_buffer_size_per_device(
+      feature_specs=_tree.tree_leaves(feature_specs),
+      global_device_count=global_device_count,
+      num_sc_per_device=_get_num_sc_per_device(num_sc_per_device),
+      enable_minibatching=enable_minibatching)
+
+
+def sharding_strategy_to_enum(sharding_strategy: str):
+  if sharding_strategy.upper() == "MOD":
+    return pybind_input_preprocessing.ShardingStrategy.MOD
+  raise ValueError(f"Unsupported sharding strategy: {sharding_strategy}. "
+                   "Only MOD is supported.")
+
+
+def preprocess_sparse_dense_matmul_input(
+    features, features_weights, feature_specs, local_device_count: int,
+    global_device_count: int, *, num_sc_per_device: int | None = None,
+    sharding_strategy: str = "MOD", has_leading_dimension: bool = False,
+    allow_id_dropping: bool = False, batch_number: int = 0,
+    enable_minibatching: bool = False, all_reduce_interface=None):
+  """Preprocesses the input batch on the GPU (embedding.py:608-705).
+
+  Returns (PreprocessedInput, SparseDenseMatmulInputStats); the CSR buffers
+  are torch CUDA tensors.
+  """
+  num_sc_per_device = _get_num_sc_per_device(num_sc_per_device)
+  _assert_same_structure(features, feature_specs, "features", "feature_specs")
+  if features_weights is not None:
+    _assert_same_structure(features_weights, feature_specs,
+                           "features_weights", "feature_specs")
+  if (enable_minibatching and all_reduce_interface is None and
+      local_device_count < global_device_count):
+    raise ValueError("all_reduce_interface must be provided when minibatching "
+                     "is enabled for multi-host.")
+  *csr, num_minibatches, stats = (
+      pybind_input_preprocessing.preprocess_sparse_dense_matmul_input(
+          _tree.tree_leaves(features),
+          (_tree.tree_leaves(features_weights)
+           if features_weights is not None else None),
+          _tree.tree_leaves(feature_specs), local_device_count,
+          global_device_count, num_sc_per_device=num_sc_per_device,
+          sharding_strategy=sharding_strategy_to_enum(sharding_strategy),
+          has_leading_dimension=has_leading_dimension,
+          allow_id_dropping=allow_id_dropping, batch_number=batch_number,
+          enable_minibatching=enable_minibatching,
+          all_reduce_interface=all_reduce_interface))
+  minibatches = np.full(local_device_count, num_minibatches, dtype=np.int32)
+  if has_leading_dimension:
+    minibatches = minibatches.reshape(local_device_count, 1)
+  return (PreprocessedInput(SparseDenseMatmulInput(*csr), minibatches),
+          SparseDenseMatmulInputStats.from_cc(stats))
+
+
+# ---------------------------------------------------------------------------
+# Activation unstacking / gradient stacking (embedding.py:903-1044,
+# :1200-1294): layout changes between the stacked [B_stack, D] buffer and
+# per-feature [b_f, d_f] arrays.
+# ---------------------------------------------------------------------------
+
+
+def _get_activation_for_feature(feature, activations, global_device_count,
+                                num_feature_slices_per_device):
+  if feature.output_shape[-1] > feature.table_spec.embedding_dim:
+    raise ValueError(
+        f"Feature {feature.name} has output shape {feature.output_shape} and "
+        f"embedding dim {feature.table_spec.embedding_dim}. The embedding dim "
+        "in output shape cannot be more than the (original, unpadded) "
+        "embedding dim in the FeatureSpec.")
+  act = activations[feature.table_spec.stacked_table_spec.stack_name]
+  f = num_feature_slices_per_device
+  if act.shape[0] % f:
+    raise ValueError(
+        "The input batch size must be divisible by the number of feature "
+        f"slices per device. Got input shape {tuple(act.shape)} and {f} "
+        f"feature slices per device for feature {feature.name}.")
+  off = feature.id_transformation.row_offset // (global_device_count * f)
+  b1 = feature.output_shape[0] // (global_device_count * f)
+  per = act.reshape(f, act.shape[0] // f, *act.shape[1:])
+  sl = per[:, off:off + b1]
+  if act.dim() > 1:
+    sl = sl[..., :feature.output_shape[-1]]
+  return sl.reshape(f * b1, *sl.shape[2:])
+
+
+def unstack_embedding_activations(activations, feature_specs,
+                                  global_device_count: int,
+                                  num_sc_per_device: int,
+                                  use_activation_unstack_primitive=False):
+  del use_activation_unstack_primitive
+  return _tree.tree_map(
+      lambda fs: _get_activation_for_feature(fs, activations,
+                                             global_device_count,
+                                             num_sc_per_device),
+      feature_specs)
+
+
+def tpu_sparse_dense_matmul(preprocessed_inputs, embedding_variables,
+                            feature_specs, *, global_device_count: int,
+                            sharding_strategy: str = "MOD",
+                            num_sc_per_device: int | None = None,
+                            enable_minibatching: bool = False,
+                            perform_unstacking: bool = True,
+                            use_activation_unstack_primitive: bool = False):
+  """Forward lookup for every stacked table (embedding.py:1047-1184)."""
+  if isinstance(preprocessed_inputs, SparseDenseMatmulInput):
+    warnings.warn("SparseDenseMatmulInput is deprecated. Please use "
+                  "PreprocessedInput instead.", DeprecationWarning)
+    preprocessed_inputs = PreprocessedInput(preprocessed_inputs)
+  rp, eid, sid, gains = preprocessed_inputs.sparse_dense_matmul_input
+  num_sc_per_device = _get_num_sc_per_device(num_sc_per_device)
+  assert rp.keys() == embedding_variables.keys()
+  stacked = get_stacked_table_specs(feature_specs)
+  assert rp.keys() == stacked.keys()
+  strategy = int(sharding_strategy_to_enum(sharding_strategy))
+  nmb = _resolve_scalar_minibatches(preprocessed_inputs.num_minibatches)
+  acts = {}
+  for name, spec in stacked.items():
+    ev = embedding_variables[name]
+    table = ev.table if isinstance(ev, EmbeddingVariables) else ev[0]
+    acts[name] = (sparse_dense_matmul_csr.tpu_sparse_dense_matmul_csr_primitive
+                  .bind(rp[name], eid[name], sid[name], gains[name], nmb,
+                        table,
+                        device_batch_size=(spec.total_sample_count //
+                                           global_device_count),
+                        max_ids_per_partition=spec.max_ids_per_partition,
+                        max_unique_ids_per_partition=(
+                            spec.max_unique_ids_per_partition),
+                        sharding_strategy=strategy,
+                        quantization_config=(
+                            spec.quantization_config.as_tuple()
+                            if spec.quantization_config else None),
+                        enable_minibatching=enable_minibatching,
+                        num_sc_per_device=num_sc_per_device,
+                        global_device_count=global_device_count))
+  if perform_unstacking:
+    acts = unstack_embedding_activations(acts, feature_specs,
+                                         global_device_count,
+                                         num_sc_per_device,
+                                         use_activation_unstack_primitive)
+  return acts
+
+
+def _resolve_scalar_minibatches(val):
+  if isinstance(val, np.ndarray) and val.ndim == 1:
+    return val[0].astype(np.int32)
+  return val
+
+
+def _prepare_gradient_for_stacking(gradient, feature, num_sc_per_device):
+  t = _native.torch()
+  g = gradient
+  if not isinstance(g, t.Tensor):
+    g = _native.as_device_tensor(g, t.float32)
+  g = g.reshape(-1, feature.table_spec.embedding_dim)
+  extra = (feature.table_spec.setting_in_stack.padded_embedding_dim -
+           feature.table_spec.embedding_dim)
+  if extra:
+    g = t.nn.functional.pad(g, (0, extra))
+  if g.shape[0] % num_sc_per_device:
+    raise ValueError(
+        "The input batch size must be divisible by the number of feature "
+        f"slices per device. Got input shape {tuple(g.shape)} and "
+        f"{num_sc_per_device} feature slices per device for feature "
+        f"{feature.name}.")
+  return g
+
+
+def stack_embedding_gradients(activation_gradients, feature_specs,
+                              num_sc_per_device: int,
+                              global_device_count: int | None = None,
+                              use_gradient_stacking_primitive: bool = False):
+  """Per-feature gradients -> one [B_stack, D] gradient per stack."""
+  del global_device_count, use_gradient_stacking_primitive
+  t = _native.torch()
+  by_stack = collections.defaultdict(list)
+  for g, fs in zip(_tree.tree_leaves(activation_gradients),
+                   _tree.tree_leaves(feature_specs)):
+    if fs._id_transformation is None:  # pylint: disable=protected-access
+      raise ValueError("FeatureIdTransformation cannot be None here. It is "
+                       f"None for {fs.name}")
+    by_stack[fs.table_spec.stacked_table_spec.stack_name].append((fs, g))
+  out = {}
+  f = num_sc_per_device
+  for name, items in by_stack.items():
+    items.sort(key=lambda x: x[0].id_transformation.row_offset)
+    parts = []
+    for fs, g in items:
+      g = _prepare_gradient_for_stacking(g, fs, f)
+      parts.append(g.reshape(f, g.shape[0] // f, g.shape[1]))
+    cat = t.cat(parts, dim=1)
+    out[name] = cat.reshape(-1, cat.shape[-1])
+  return out
+
+
+def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
+                                 embedding_variables, feature_specs, *,
+                                 global_device_count: int | None = None,
+                                 sharding_strategy: str = "MOD",
+                                 label: str = "", step=None,
+                                 num_sc_per_device: int | None = None,
+                                 enable_minibatching: bool = False,
+                                 perform_stacking: bool = True,
+                                 use_gradient_stacking_primitive=False,
+                                 embedding_var_limits=None):
+  """Backward pass + optimizer update (embedding.py:1297-1529).
+
+  Returns the updated EmbeddingVariables per stacked table; the tensors are
+  updated in place.
+  """
+  if isinstance(preprocessed_inputs, SparseDenseMatmulInput):
+    warnings.warn("SparseDenseMatmulInput is deprecated. Please use "
+                  "PreprocessedInput instead.", DeprecationWarning)
+    preprocessed_inputs = PreprocessedInput(preprocessed_inputs)
+  rp, eid, sid, gains = preprocessed_inputs.sparse_dense_matmul_input
+  assert rp.keys() == embedding_variables.keys()
+  stacked = get_stacked_table_specs(feature_specs)
+  assert rp.keys() == stacked.keys()
+  num_sc_per_device = _get_num_sc_per_device(num_sc_per_device)
+  if perform_stacking:
+    _assert_same_structure(feature_specs, activation_gradients,
+                           "feature_specs", "activation_gradients")
+    grads = stack_embedding_gradients(activation_gradients, feature_specs,
+                                      num_sc_per_device, global_device_count,
+                                      use_gradient_stacking_primitive)
+  else:
+    grads = activation_gradients
+  assert rp.keys() == grads.keys()
+  strategy = int(sharding_strategy_to_enum(sharding_strategy))
+  nmb = _resolve_scalar_minibatches(preprocessed_inputs.num_minibatches)
+  g_count = 1 if global_device_count is None else global_device_count
+  out = {}
+  for name, spec in stacked.items():
+    ev = embedding_variables[name]
+    opt = spec.optimizer
+    hyper = opt.get_hyperparameters(step)
+    symbol = f"{opt.short_name()}-{spec.stack_name}{label}"
+    kwargs = {}
+    if embedding_var_limits is not None:
+      kwargs["min_value"], kwargs["max_value"] = embedding_var_limits[name]
+    flat = [ev.table, *ev.slot] if isinstance(ev, EmbeddingVariables) else \
+        list(_tree.tree_leaves(ev))
+    res = opt.get_optimizer_primitive().bind(
+        rp[name], eid[name], sid[name], gains[name], nmb, *flat, grads[name],
+        *hyper, max_ids_per_partition=spec.max_ids_per_partition,
+        max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
+        computation_name=symbol, sharding_strategy=strategy,
+        enable_minibatching=enable_minibatching,
+        num_sc_per_device=num_sc_per_device, global_device_count=g_count,
+        **kwargs)
+    res = res if isinstance(res, tuple) else (res,)
+    out[name] = EmbeddingVariables(res[0], tuple(res[1:]))
+  return out
+
+
+def init_embedding_variables(rng, table_specs, global_sharding=None,
+                             num_sparsecore_per_device: int | None = None,
+                             bypass_mesh_check: bool = False):
+  """Allocates every stacked table and its slots on the GPU.
+
+  `rng` is a seed or a torch.Generator. Each table's rows are initialised by
+  its initializer per SparseCore shard and laid out like the reference
+  (embedding.py:1532-1591): for shard s, the tables of the stack in
+  row_offset_in_shard order.
+  """
+  del global_sharding, bypass_mesh_check
+  t = _native.require_gpu()
+  dev = _native.device()
+  s_count = _get_num_sc_per_device(num_sparsecore_per_device)
+  if isinstance(rng, int):
+    gen = t.Generator(device=dev)
+    gen.manual_seed(rng)
+  else:
+    gen = rng
+  stacks = collections.defaultdict(list)
+  for ts in _tree.tree_leaves(table_specs):
+    stacks[ts.setting_in_stack.stack_name].append(ts)
+  out = {}
+  for name, specs in stacks.items():
+    specs.sort(key=lambda x: x.setting_in_stack.row_offset_in_shard)
+    dim = specs[0].setting_in_stack.padded_embedding_dim
+    tables, slots = [], None
+    for _ in range(s_count):
+      for ts in specs:
+        rows = ts.setting_in_stack.padded_vocab_size // s_count
+        init = ts.initializer or embedding_spec.zeros
+        tables.append(init(gen, (rows, dim), device=dev))
+        slot_inits = ts.optimizer.slot_variables_initializers()
+        vals = [si(gen, (rows, dim), device=dev) for si in slot_inits]
+        slots = [[] for _ in vals] if slots is None else slots
+        for k, v in enumerate(vals):
+          slots[k].append(v)
+    table = t.cat(tables, dim=0)
+    slot_vals = tuple(t.cat(s, dim=0) for s in (slots or []))
+    out[name] = EmbeddingVariables(table, slot_vals)
+  return out
+
+
+def update_preprocessing_parameters(feature_specs, updated_params,
+                                    num_sc_per_device: int) -> None:
+  """Writes observed limits / buffer sizes into the StackedTableSpecs."""
+
+  def update(fs):
+    st = fs.table_spec.stacked_table_spec
+    name = st.stack_name
+    max_ids = updated_params.max_ids_per_partition.get(
+        name, st.max_ids_per_partition)
+    max_unique = updated_params.max_unique_ids_per_partition.get(
+        name, st.max_unique_ids_per_partition)
+    size = updated_params.get_required_buffer_size_per_device(
+        name, num_sc_per_device)
+    if size is None:
+      size = st.suggested_coo_buffer_size_per_device
+    fs.table_spec.stacked_table_spec = dataclasses.replace(
+        st, max_ids_per_partition=int(np.max(max_ids)),
+        max_unique_ids_per_partition=int(np.max(max_unique)),
+        suggested_coo_buffer_size_per_device=size)
+
+  for fs in _tree.tree_leaves(feature_specs):
+    update(fs)

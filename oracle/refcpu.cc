@@ -1,0 +1,649 @@
+// refcpu: CPU restatement of jax-tpu-embedding's SparseCore hot path.
+//
+// TEST INFRASTRUCTURE ONLY. This file is the parity oracle and the CPU
+// baseline. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+// leg load it, and only as a checker; the product path (libscemb.so) never
+// links or calls it.
+//
+// It restates the reference algorithm stage by stage, so that every stage can
+// be pinned separately against the reference's own known-answer tests:
+//
+//   extraction        jax_tpu_embedding/sparsecore/lib/core/
+//                       input_preprocessing.cc:79-123, :312-436
+//                       process_coo_tensors_impl.h:39-136
+//                       coo_format.h:120-185
+//   sort/group/dedupe sort_and_group_coo_tensors_impl.h:196-311, :349-646
+//                       partitioned_coo_tensors.h:94-125
+//   CSR fill          input_preprocessing_util.cc:73-208, :331-473
+//   sizes/validation  input_preprocessing_util.cc:223-312, :490-522
+//                       input_preprocessing.cc:757-786
+//   lookup / update   primitives/sparse_dense_matmul_csr.py:171-201 (operand
+//                       meaning), primitives/optimizers_computation.py:22-148,
+//                       primitives/utils.py:24-59 (clip), and the numpy test
+//                       oracles in primitives/tests/
+//                       sparse_dense_matmul_grad_with_adagrad_test.py:356-400.
+//
+// Numeric rules follow the C++ (not the Python reference): float gains,
+// float sums in sorted order, std::pow(float,int) promoting to double in the
+// weighted sqrtn divisor. Build with -ffp-contract=off.
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <limits>
+#include <numeric>
+#include <thread>
+#include <vector>
+
+namespace {
+
+enum Combiner : int { kSum = 0, kMean = 1, kSqrtn = 2 };
+
+constexpr int kAlign = 8;           // TPU_VECTOR_REGISTER_ALIGNMENT_SIZE
+constexpr uint32_t kDataBits = 26;  // coo_format.h:57-62
+constexpr uint32_t kDataMask = (1u << kDataBits) - 1;
+constexpr uint32_t kRotatedColIdOffset = kDataBits;
+
+inline int64_t RoundUp(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+inline int Log2Exact(uint32_t v) {
+  int b = 0;
+  while ((1u << b) < v) ++b;
+  return b;
+}
+inline uint32_t Rotr32(uint32_t x, int s) {
+  s &= 31;
+  return s == 0 ? x : ((x >> s) | (x << (32 - s)));
+}
+inline uint32_t Rotl32(uint32_t x, int s) {
+  s &= 31;
+  return s == 0 ? x : ((x << s) | (x >> (32 - s)));
+}
+
+// coo_format.h:120-135
+inline int GetColId(int embedding_id, int col_shift, int col_offset,
+                    int num_scs_mod) {
+  return ((embedding_id + col_shift) & num_scs_mod) +
+         (embedding_id & ~num_scs_mod) + col_offset;
+}
+
+// coo_format.h:154-185 (no minibatching buckets: bucket id is 0).
+inline uint64_t GroupingKey(uint32_t col_id, uint32_t data, int num_scs_bit) {
+  const uint32_t rotated = Rotr32(col_id, num_scs_bit);
+  return (uint64_t{rotated} << kRotatedColIdOffset) | uint64_t{data};
+}
+
+struct Coo {
+  int32_t row;
+  int32_t col;
+  float gain;
+};
+
+}  // namespace
+
+extern "C" {
+
+// One feature of a stacked table, in values + row-splits form. `weights` is
+// null for unity weights (UnityWeightsStream, unity_weights_stream_impl.h).
+struct RefFeature {
+  const int32_t* ids;
+  const int64_t* row_splits;  // num_rows + 1 entries
+  const float* weights;       // null or parallel to ids
+  int64_t num_rows;
+  int32_t row_offset;
+  int32_t col_offset;
+  int32_t col_shift;
+  int32_t pad_;
+};
+
+int ref_get_col_id(int embedding_id, int col_shift, int col_offset,
+                   int num_scs_mod) {
+  return GetColId(embedding_id, col_shift, col_offset, num_scs_mod);
+}
+
+uint64_t ref_grouping_key(uint32_t col_id, uint32_t data, int num_scs_bit) {
+  return GroupingKey(col_id, data, num_scs_bit);
+}
+
+uint32_t ref_col_id_from_key(uint64_t key, int num_scs_bit) {
+  return Rotl32(static_cast<uint32_t>(key >> kRotatedColIdOffset), num_scs_bit);
+}
+
+uint32_t ref_data_from_key(uint64_t key) {
+  return static_cast<uint32_t>(key) & kDataMask;
+}
+
+// Gains of one row, following process_coo_tensors_impl.h:39-136.
+// Unity weights: sum -> 1; mean -> 1.0f / float(n) (rematerialized from the
+// token count, input_preprocessing_util.h:216-222); sqrtn -> 1.0f /
+// sqrtf(float(n)) (process_coo_tensors_impl.h:48-49, :105-107).
+// Variable weights: divisor = 1 | float running sum | sqrtf(float sum of
+// double squares), gain = w / divisor (:54-74, :118).
+static void RowGains(const float* w, int64_t n, int combiner, float* out) {
+  if (w == nullptr) {
+    float g = 1.0f;
+    if (combiner == kMean) {
+      g = 1.0f / static_cast<float>(static_cast<int>(n));
+    } else if (combiner == kSqrtn) {
+      const float divisor = std::sqrt(static_cast<float>(static_cast<int>(n)));
+      g = 1.0f / divisor;
+    }
+    for (int64_t i = 0; i < n; ++i) out[i] = g;
+    return;
+  }
+  float divisor = 1.0f;
+  if (combiner == kMean) {
+    float sum = 0.0f;
+    for (int64_t i = 0; i < n; ++i) sum += w[i];
+    divisor = sum;
+  } else if (combiner == kSqrtn) {
+    float sum = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+      // std::pow(float, int) is computed in double; the float accumulator
+      // is promoted for the add and rounded back on assignment.
+      sum = static_cast<float>(static_cast<double>(sum) +
+                               static_cast<double>(w[i]) *
+                                   static_cast<double>(w[i]));
+    }
+    divisor = std::sqrt(sum);
+  }
+  for (int64_t i = 0; i < n; ++i) out[i] = w[i] / divisor;
+}
+
+// ExtractCooTensors for one feature slice [slice_start, slice_end)
+// (input_preprocessing.cc:79-123 with ProcessCooTensors). Appends to
+// rows/cols/gains at *count. Returns 0.
+int ref_extract_slice(const RefFeature* f, int slice_start, int slice_end,
+                      int row_offset, int col_offset, int col_shift,
+                      int num_scs, int combiner, int32_t* rows, int32_t* cols,
+                      float* gains, int64_t* count) {
+  const int num_scs_mod = num_scs - 1;
+  std::vector<float> g;
+  int64_t k = *count;
+  for (int row = slice_start; row < slice_end; ++row) {
+    const int sample_id = row - slice_start + row_offset;
+    const int64_t b = f->row_splits[row];
+    const int64_t n = f->row_splits[row + 1] - b;
+    g.resize(static_cast<size_t>(n));
+    RowGains(f->weights ? f->weights + b : nullptr, n, combiner, g.data());
+    for (int64_t i = 0; i < n; ++i) {
+      rows[k] = sample_id;
+      cols[k] = GetColId(f->ids[b + i], col_shift, col_offset, num_scs_mod);
+      gains[k] = g[static_cast<size_t>(i)];
+      ++k;
+    }
+  }
+  *count = k;
+  return 0;
+}
+
+// ExtractCooTensorsForAllFeaturesPerLocalDevice (input_preprocessing.cc:
+// 312-436). `features` must already be in row_offset order
+// (pybind_input_preprocessing.cc:114-120). Output lists are concatenated SC by
+// SC; sc_sizes[s] receives the per-SC counts. Returns 0, or 1 when the device
+// batch is not divisible by num_sc_per_device / smaller than the number of
+// feature slices (CHECK failures in the reference).
+int ref_extract_device(const RefFeature* features, int n_features,
+                       int local_device_id, int local_device_count,
+                       int global_device_count, int num_sc_per_device,
+                       int combiner, int32_t* rows, int32_t* cols,
+                       float* gains, int64_t* sc_sizes,
+                       int32_t* batch_size_for_device_out) {
+  int batch_size_for_device = 0;
+  for (int f = 0; f < n_features; ++f) {
+    batch_size_for_device +=
+        static_cast<int>(features[f].num_rows / local_device_count);
+  }
+  *batch_size_for_device_out = batch_size_for_device;
+  if (batch_size_for_device % num_sc_per_device != 0) return 1;
+  if (batch_size_for_device < num_sc_per_device * n_features) return 1;
+  const int S = num_sc_per_device;
+  const int num_scs = S * global_device_count;
+  const int bps = (batch_size_for_device + S - 1) / S;
+  int64_t k = 0;
+  for (int s = 0; s < S; ++s) {
+    const int64_t before = k;
+    for (int f = 0; f < n_features; ++f) {
+      const RefFeature& ft = features[f];
+      const int num_samples = static_cast<int>(ft.num_rows);
+      const int per_split = num_samples / (local_device_count * S);
+      const int start = (local_device_id * S + s) * per_split;
+      const int end = std::min(num_samples, start + per_split);
+      const int row_offset_per_slice = ft.row_offset / (global_device_count * S);
+      const int row_offset = s * bps + row_offset_per_slice;
+      ref_extract_slice(&ft, start, end, row_offset, ft.col_offset,
+                        ft.col_shift, num_scs, combiner, rows, cols, gains, &k);
+    }
+    sc_sizes[s] = k - before;
+  }
+  return 0;
+}
+
+// SortAndGroupCooTensorsPerLocalDevice without minibatching
+// (sort_and_group_coo_tensors_impl.h:196-311, :349-646). Input: per-SC
+// extraction-order lists. Output: per-SC grouped lists (capacity = input
+// size), stats in the reference's per-device layout:
+//   max_ids[NS], max_unique[NS]  (max over local SCs of per-partition counts)
+//   required[S]                  (sum over partitions of roundup8(ids))
+// Returns 0 on success, 2 when a limit is exceeded and dropping is not allowed
+// (LOG(FATAL) in the reference, :45-89).
+int ref_sort_and_group(int num_sc_per_device, const int64_t* sc_sizes,
+                       const int32_t* rows, const int32_t* cols,
+                       const float* gains, int has_variable_weights,
+                       int num_scs, int max_ids_per_partition,
+                       int max_unique_ids_per_partition, int allow_id_dropping,
+                       int32_t* g_rows, int32_t* g_cols, float* g_gains,
+                       int64_t* g_sizes, int32_t* max_ids, int32_t* max_unique,
+                       int32_t* required_buffer_size, int64_t* dropped) {
+  const int S = num_sc_per_device;
+  const int NS = num_scs;
+  const int num_sc_bits = Log2Exact(static_cast<uint32_t>(NS));
+  for (int p = 0; p < NS; ++p) max_ids[p] = max_unique[p] = 0;
+  for (int s = 0; s < S; ++s) required_buffer_size[s] = 0;
+  int64_t total_dropped = 0;
+  int status = 0;
+  int64_t in_base = 0;
+  for (int s = 0; s < S; ++s) {
+    const int64_t n = sc_sizes[s];
+    const int32_t* r = rows + in_base;
+    const int32_t* c = cols + in_base;
+    const float* g = gains + in_base;
+    // Keys: data = extraction index (variable weights) or row id (unity).
+    std::vector<uint64_t> keys(static_cast<size_t>(n));
+    for (int64_t i = 0; i < n; ++i) {
+      const uint32_t data = has_variable_weights ? static_cast<uint32_t>(i)
+                                                 : static_cast<uint32_t>(r[i]);
+      keys[i] = GroupingKey(static_cast<uint32_t>(c[i]), data, num_sc_bits);
+    }
+    // Unity weights: gain is a function of the row id alone; recover it from
+    // any entry with the same row (all equal by construction).
+    std::vector<float> row_gain;
+    if (!has_variable_weights) {
+      int32_t max_row = -1;
+      for (int64_t i = 0; i < n; ++i) max_row = std::max(max_row, r[i]);
+      row_gain.assign(static_cast<size_t>(max_row + 1), 1.0f);
+      for (int64_t i = 0; i < n; ++i) row_gain[r[i]] = g[i];
+    }
+    // hwy::VQSort(ascending) on uint64 keys: equal keys are bit-identical,
+    // so any correct sort gives the same sequence.
+    std::sort(keys.begin(), keys.end());
+
+    std::vector<int32_t> obs_ids(NS, 0), obs_unique(NS, 0), kept_ids(NS, 0),
+        kept_unique(NS, 0);
+    const uint32_t kNone = std::numeric_limits<uint32_t>::max();
+    uint32_t prev_col = kNone, prev_row = kNone;
+    uint32_t dedup_col = kNone, dedup_row = kNone;
+    bool dropping_current_col = false;
+    const bool perform_dropping = allow_id_dropping != 0;
+    int64_t out = 0;
+    int32_t* orow = g_rows + in_base;
+    int32_t* ocol = g_cols + in_base;
+    float* ogain = g_gains + in_base;
+    for (int64_t i = 0; i < n; ++i) {
+      const uint64_t key = keys[i];
+      const uint32_t col = ref_col_id_from_key(key, num_sc_bits);
+      const uint32_t p = col & static_cast<uint32_t>(NS - 1);
+      uint32_t row;
+      float gain;
+      if (has_variable_weights) {
+        const uint32_t idx = ref_data_from_key(key);
+        row = static_cast<uint32_t>(r[idx]);
+        gain = g[idx];
+      } else {
+        row = ref_data_from_key(key);
+        gain = row_gain[row];
+      }
+      // Merge with the last kept entry (partitioned_coo_tensors.h:102-113).
+      if (row == dedup_row && col == dedup_col) {
+        ogain[out - 1] += gain;
+        continue;
+      }
+      // A repeat of a dropped entry is dropped too.
+      if (perform_dropping && row == prev_row && col == prev_col) {
+        ++total_dropped;
+        continue;
+      }
+      const bool is_new_col = col != prev_col;
+      obs_ids[p] += 1;
+      if (is_new_col) obs_unique[p] += 1;
+      bool add = true;
+      if (perform_dropping) {
+        const bool exceeds = (kept_ids[p] + 1) > max_ids_per_partition;
+        if (is_new_col) {
+          dropping_current_col =
+              (kept_unique[p] + 1) > max_unique_ids_per_partition;
+        }
+        if (exceeds || dropping_current_col) {
+          ++total_dropped;
+          add = false;
+        }
+        kept_ids[p] += 1;
+        if (is_new_col) kept_unique[p] += 1;
+      }
+      if (add) {
+        orow[out] = static_cast<int32_t>(row);
+        ocol[out] = static_cast<int32_t>(col);
+        ogain[out] = gain;
+        ++out;
+        dedup_col = col;
+        dedup_row = row;
+      }
+      prev_col = col;
+      prev_row = row;
+    }
+    g_sizes[s] = out;
+    int32_t obs_max_ids = 0, obs_max_unique = 0;
+    int64_t req = 0;
+    for (int p = 0; p < NS; ++p) {
+      max_ids[p] = std::max(max_ids[p], obs_ids[p]);
+      max_unique[p] = std::max(max_unique[p], obs_unique[p]);
+      obs_max_ids = std::max(obs_max_ids, obs_ids[p]);
+      obs_max_unique = std::max(obs_max_unique, obs_unique[p]);
+      req += RoundUp(obs_ids[p], kAlign);
+    }
+    required_buffer_size[s] = static_cast<int32_t>(req);
+    if (!allow_id_dropping && (obs_max_ids > max_ids_per_partition ||
+                               obs_max_unique > max_unique_ids_per_partition)) {
+      status = 2;
+    }
+    in_base += n;
+  }
+  *dropped = total_dropped;
+  return status;
+}
+
+// FillLocalDeviceBufferAsync / FillBufferSegment without minibatching
+// (input_preprocessing_util.cc:73-208, :331-473). Writes one device's CSR
+// buffers: rp[S * rp_per_sc], eid/sid/gains[coo_size]. Positions past each
+// segment's final index are left untouched (the reference leaves them
+// uninitialised). Returns the statically dropped count in *dropped.
+int ref_fill_device(int num_sc_per_device, const int64_t* g_sizes,
+                    const int32_t* g_rows, const int32_t* g_cols,
+                    const float* g_gains, int num_scs, int batch_size_per_sc,
+                    int64_t coo_size, int rp_per_sc, int32_t* rp,
+                    int32_t* eid, int32_t* sid, float* gains,
+                    int64_t* dropped) {
+  const int S = num_sc_per_device;
+  const int NS = num_scs;
+  const int64_t per_sc = coo_size / S;
+  const float kNan = std::nanf("");
+  int64_t total_dropped = 0;
+  int64_t in_base = 0;
+  for (int s = 0; s < S; ++s) {
+    const int64_t K = g_sizes[s];
+    const int32_t* r = g_rows + in_base;
+    const int32_t* c = g_cols + in_base;
+    const float* g = g_gains + in_base;
+    int64_t coo_begin = std::min<int64_t>(s * per_sc, coo_size);
+    const int64_t coo_end = coo_begin + per_sc;
+    int rp_index = s * rp_per_sc;
+    const int rp_end = rp_index + rp_per_sc;
+    int64_t coo = coo_begin;
+    int cur_p = 0;
+    int64_t processed = 0;
+    auto valid = [&]() {
+      if (processed == K && coo == coo_end) return true;
+      if (rp_index >= rp_end || coo >= coo_end) return false;
+      return true;
+    };
+    auto advance = [&](int target) {
+      while (cur_p < target) {
+        if (!valid()) return;
+        rp[rp_index++] = static_cast<int32_t>(coo - coo_begin);
+        while (coo % kAlign != 0 && coo < coo_end) {
+          eid[coo] = INT_MAX;
+          sid[coo] = INT_MAX;
+          gains[coo] = kNan;
+          ++coo;
+        }
+        ++cur_p;
+      }
+    };
+    for (int64_t i = 0; i < K; ++i) {
+      const int target = static_cast<int>(c[i] % NS);
+      advance(target);
+      if (!valid()) {
+        total_dropped += K - processed;
+        break;
+      }
+      eid[coo] = c[i] / NS;
+      sid[coo] = r[i] % batch_size_per_sc;
+      gains[coo] = g[i];
+      ++coo;
+      ++processed;
+    }
+    advance(NS);
+    while (rp_index < rp_end) rp[rp_index++] = static_cast<int32_t>(coo - coo_begin);
+    in_base += K;
+  }
+  *dropped = total_dropped;
+  return 0;
+}
+
+// Full preprocessing of one stacked table for all local devices
+// (input_preprocessing.cc:800-959 restricted to one stack, no minibatching).
+// features must be in row_offset order. Outputs (leading dimension L):
+//   rp[L * S * rp_per_sc], eid/sid/gains[L * coo_size_per_device],
+//   max_ids/max_unique[L * NS], required[L * S], *dropped (all devices).
+// Returns 0, 1 (invalid batch split), 2 (limit exceeded without dropping).
+int ref_preprocess_stack(const RefFeature* features, int n_features,
+                         int local_device_count, int global_device_count,
+                         int num_sc_per_device, int combiner,
+                         int has_variable_weights, int max_ids_per_partition,
+                         int max_unique_ids_per_partition,
+                         int allow_id_dropping, int64_t coo_size_per_device,
+                         int32_t* rp, int32_t* eid, int32_t* sid,
+                         float* gains, int32_t* max_ids, int32_t* max_unique,
+                         int32_t* required, int64_t* dropped) {
+  const int L = local_device_count;
+  const int S = num_sc_per_device;
+  const int NS = S * global_device_count;
+  const int rp_per_sc = std::max(NS, kAlign);
+  int64_t total_ids = 0;
+  for (int f = 0; f < n_features; ++f) {
+    total_ids += features[f].row_splits[features[f].num_rows];
+  }
+  std::vector<int32_t> rows(total_ids), cols(total_ids), grows(total_ids),
+      gcols(total_ids);
+  std::vector<float> gn(total_ids), ggn(total_ids);
+  std::vector<int64_t> sizes(S), gsizes(S);
+  int64_t all_dropped = 0;
+  int status = 0;
+  for (int d = 0; d < L; ++d) {
+    int32_t bfd = 0;
+    if (ref_extract_device(features, n_features, d, L, global_device_count, S,
+                           combiner, rows.data(), cols.data(), gn.data(),
+                           sizes.data(), &bfd) != 0) {
+      return 1;
+    }
+    int64_t drop_group = 0, drop_fill = 0;
+    const int st = ref_sort_and_group(
+        S, sizes.data(), rows.data(), cols.data(), gn.data(),
+        has_variable_weights, NS, max_ids_per_partition,
+        max_unique_ids_per_partition, allow_id_dropping, grows.data(),
+        gcols.data(), ggn.data(), gsizes.data(), max_ids + d * NS,
+        max_unique + d * NS, required + d * S, &drop_group);
+    if (st != 0) status = st;
+    const int bps = (bfd + S - 1) / S;
+    ref_fill_device(S, gsizes.data(), grows.data(), gcols.data(), ggn.data(),
+                    NS, bps, coo_size_per_device, rp_per_sc,
+                    rp + static_cast<int64_t>(d) * S * rp_per_sc,
+                    eid + d * coo_size_per_device,
+                    sid + d * coo_size_per_device,
+                    gains + d * coo_size_per_device, &drop_fill);
+    all_dropped += drop_group + drop_fill;
+  }
+  *dropped = all_dropped;
+  return status;
+}
+
+// ComputeTheoreticalMaxCooBufferSize (input_preprocessing_util.cc:223-240).
+int64_t ref_theoretical_max_coo_buffer_size(int max_ids_per_partition,
+                                            int global_device_count,
+                                            int num_sc_per_device) {
+  const int64_t num_scs = int64_t{global_device_count} * num_sc_per_device;
+  return RoundUp(max_ids_per_partition, kAlign) * num_sc_per_device * num_scs;
+}
+
+// ComputeCooBufferSizePerDevice (input_preprocessing_util.cc:256-312):
+// returns -1 when the suggestion exceeds the theoretical maximum (CHECK).
+int64_t ref_coo_buffer_size_per_device(int max_ids_per_partition,
+                                       int64_t suggested, int global_device_count,
+                                       int num_sc_per_device) {
+  const int64_t theoretical = ref_theoretical_max_coo_buffer_size(
+      max_ids_per_partition, global_device_count, num_sc_per_device);
+  if (suggested <= 0) return theoretical;
+  const int64_t v = RoundUp(suggested, int64_t{kAlign} * num_sc_per_device);
+  if (v > theoretical) return -1;
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Lookup and update: the semantics the reference's tests hold the TPU ops to.
+// For local SparseCore s and partition p, entries j in
+// [roundup8(rp[p-1]) (0 for p = 0), rp[p]) of segment s contribute
+//   act[s*bps + sid[j]] += gains[j] * T[p*(V/NS) + eid[j]].
+// The gradient of a table row is the sum over all its entries of
+// gains[j] * act_grad[s*bps + sid[j]]; the optimizer runs once per touched
+// row. Work is split over threads by embedding column, so each thread sums in
+// the same (CSR) order as a serial loop: results are deterministic and do not
+// depend on the thread count.
+// ---------------------------------------------------------------------------
+
+}  // extern "C"
+
+namespace {
+
+struct CsrEntry {
+  int64_t act_row;
+  int64_t table_row;
+  float gain;
+};
+
+std::vector<CsrEntry> CollectEntries(const int32_t* rp, const int32_t* eid,
+                                     const int32_t* sid, const float* gains,
+                                     int64_t coo_size, int num_segments,
+                                     int num_partitions, int rp_per_segment,
+                                     int64_t table_rows, int64_t batch) {
+  std::vector<CsrEntry> out;
+  const int64_t per_seg = coo_size / num_segments;
+  const int64_t bps = batch / num_segments;
+  const int64_t rows_per_partition = table_rows / num_partitions;
+  for (int s = 0; s < num_segments; ++s) {
+    const int32_t* r = rp + static_cast<int64_t>(s) * rp_per_segment;
+    const int64_t base = s * per_seg;
+    int64_t start = 0;
+    for (int p = 0; p < num_partitions; ++p) {
+      const int64_t end = r[p];
+      for (int64_t j = start; j < end; ++j) {
+        out.push_back({s * bps + sid[base + j],
+                       p * rows_per_partition + eid[base + j],
+                       gains[base + j]});
+      }
+      start = RoundUp(end, kAlign);
+    }
+  }
+  return out;
+}
+
+template <typename Fn>
+void ParallelColumns(int dim, int threads, Fn fn) {
+  threads = std::max(1, std::min(threads, dim));
+  if (threads == 1) {
+    fn(0, dim);
+    return;
+  }
+  std::vector<std::thread> pool;
+  const int chunk = (dim + threads - 1) / threads;
+  for (int t = 0; t < threads; ++t) {
+    const int lo = t * chunk;
+    const int hi = std::min(dim, lo + chunk);
+    if (lo >= hi) break;
+    pool.emplace_back(fn, lo, hi);
+  }
+  for (auto& th : pool) th.join();
+}
+
+}  // namespace
+
+extern "C" {
+
+int ref_sparse_dense_matmul(const int32_t* rp, const int32_t* eid,
+                            const int32_t* sid, const float* gains,
+                            int64_t coo_size, int num_segments,
+                            int num_partitions, int rp_per_segment,
+                            const float* table, int64_t table_rows, int dim,
+                            float* act, int64_t batch, int threads) {
+  const std::vector<CsrEntry> e =
+      CollectEntries(rp, eid, sid, gains, coo_size, num_segments,
+                     num_partitions, rp_per_segment, table_rows, batch);
+  std::memset(act, 0, sizeof(float) * batch * dim);
+  ParallelColumns(dim, threads, [&](int lo, int hi) {
+    for (const CsrEntry& x : e) {
+      const float* t = table + x.table_row * dim;
+      float* a = act + x.act_row * dim;
+      for (int d = lo; d < hi; ++d) a[d] += x.gain * t[d];
+    }
+  });
+  return 0;
+}
+
+// optimizer: 0 = SGD, 1 = Adagrad. clip_mask bit0: min, bit1: max.
+int ref_sparse_dense_matmul_grad(const int32_t* rp, const int32_t* eid,
+                                 const int32_t* sid, const float* gains,
+                                 int64_t coo_size, int num_segments,
+                                 int num_partitions, int rp_per_segment,
+                                 const float* act_grad, int64_t batch,
+                                 float* table, float* accumulator,
+                                 int64_t table_rows, int dim, int optimizer,
+                                 float learning_rate, int clip_mask,
+                                 float min_value, float max_value,
+                                 int threads) {
+  const std::vector<CsrEntry> e =
+      CollectEntries(rp, eid, sid, gains, coo_size, num_segments,
+                     num_partitions, rp_per_segment, table_rows, batch);
+  // Dense slot per touched row, assigned in first-touch order.
+  std::vector<int64_t> touched;
+  std::vector<int64_t> slot_of(e.size());
+  {
+    std::vector<std::pair<int64_t, int64_t>> order(e.size());
+    for (size_t i = 0; i < e.size(); ++i) order[i] = {e[i].table_row, (int64_t)i};
+    std::sort(order.begin(), order.end());
+    for (size_t i = 0; i < order.size(); ++i) {
+      if (i == 0 || order[i].first != order[i - 1].first) {
+        touched.push_back(order[i].first);
+      }
+      slot_of[order[i].second] = static_cast<int64_t>(touched.size()) - 1;
+    }
+  }
+  std::vector<float> grad(touched.size() * static_cast<size_t>(dim), 0.0f);
+  ParallelColumns(dim, threads, [&](int lo, int hi) {
+    for (size_t i = 0; i < e.size(); ++i) {
+      const float* gr = act_grad + e[i].act_row * dim;
+      float* gs = grad.data() + slot_of[i] * dim;
+      for (int d = lo; d < hi; ++d) gs[d] += e[i].gain * gr[d];
+    }
+    for (size_t u = 0; u < touched.size(); ++u) {
+      float* t = table + touched[u] * dim;
+      float* a = accumulator ? accumulator + touched[u] * dim : nullptr;
+      const float* g = grad.data() + u * dim;
+      for (int d = lo; d < hi; ++d) {
+        float v;
+        if (optimizer == 0) {
+          v = t[d] - g[d] * learning_rate;
+        } else {
+          const float acc = a[d] + g[d] * g[d];
+          a[d] = acc;
+          v = t[d] - (learning_rate * g[d]) / std::sqrt(acc);
+        }
+        if (clip_mask & 1) v = std::max(min_value, v);
+        if (clip_mask & 2) v = std::min(max_value, v);
+        t[d] = v;
+      }
+    }
+  });
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,108 @@
+"""CPU checks of the C-ABI boundary and the host-side API (no GPU needed)."""
+
+import os
+import re
+
+import numpy as np
+import pytest
+
+from jax_tpu_embedding.sparsecore import _native
+from jax_tpu_embedding.sparsecore.lib.core import pybind_input_preprocessing as pip
+from jax_tpu_embedding.sparsecore.lib.core.primitives import utils as prim_utils
+from oracle import refcpu
+
+_HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include",
+                       "scemb.h")
+
+
+def _declared_functions():
+  text = open(_HEADER).read()
+  text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+  return sorted(set(re.findall(r"\b(scemb_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+  assert _declared_functions() == sorted(_native.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+  lib = _native.load_library()
+  for name in _declared_functions():
+    assert hasattr(lib, name), name
+  assert lib.scemb_version() >= 1
+  assert lib.scemb_last_error() is not None
+
+
+@pytest.mark.parametrize("max_ids,g,s", [(16, 1, 4), (1, 1, 1), (100, 2, 2),
+                                         (1703936, 1, 1)])
+def test_size_helpers_match_oracle(max_ids, g, s):
+  lib = refcpu.lib()
+  assert pip.compute_theoretical_max_coo_buffer_size(max_ids, g, s) == \
+      lib.ref_theoretical_max_coo_buffer_size(max_ids, g, s)
+  for suggested in (0, 48, 96, 1024, 10**6):
+    exp = lib.ref_coo_buffer_size_per_device(max_ids, suggested, g, s)
+    got = _native.load_library().scemb_compute_coo_buffer_size_per_device(
+        max_ids, suggested, g, s)
+    assert got == exp
+  assert pip.compute_row_pointers_size_per_device(g, s) == max(g * s, 8) * s
+
+
+def test_size_helper_kats():
+  """input_preprocessing_util_test.cc:99-133; pybind test :1992-2060."""
+  assert pip.compute_theoretical_max_coo_buffer_size(16, 1, 4) == 256
+  lib = _native.load_library()
+  assert lib.scemb_compute_coo_buffer_size_per_device(16, 48, 1, 4) == 64
+  assert lib.scemb_compute_coo_buffer_size_per_device(16, 96, 1, 4) == 96
+  assert lib.scemb_compute_coo_buffer_size_per_device(16, 1024, 1, 4) == -1
+  assert pip.compute_row_pointers_size_per_device(1, 4) == 32
+  assert pip.compute_row_pointers_size_per_device(4, 4) == 64
+
+
+def test_minibatching_not_implemented():
+  with pytest.raises(NotImplementedError):
+    pip.compute_row_pointers_size_per_device(1, 1, enable_minibatching=True)
+
+
+def test_primitive_validation_messages():
+  """Abstract-eval checks of lib/core/primitives/utils.py:79-155."""
+  rp = np.array([0, 1, 2, 4], np.int32)
+  ids = np.array([0, 1, 2, 3], np.int32)
+  gains = np.ones(4, np.float32)
+  table = np.ones((2, 4), np.float32)
+  grad = np.ones((2, 4), np.float32)
+  ok = dict(max_ids_per_partition=16, max_unique_ids_per_partition=16,
+            computation_name="c", sharding_strategy=1)
+  prim_utils.validate_abstract_eval_params(rp, ids, ids, gains, 1, table,
+                                           grad, **ok)
+  with pytest.raises(ValueError, match="lhs_row_pointers must have type"):
+    prim_utils.validate_abstract_eval_params(rp.astype(np.float32), ids, ids,
+                                             gains, 1, table, grad, **ok)
+  with pytest.raises(ValueError, match="lhs_gains must have type"):
+    prim_utils.validate_abstract_eval_params(rp, ids, ids,
+                                             gains.astype(np.int32), 1, table,
+                                             grad, **ok)
+  with pytest.raises(ValueError, match="embedding_table must have dim"):
+    prim_utils.validate_abstract_eval_params(rp, ids, ids, gains, 1,
+                                             np.ones((1, 2, 3), np.float32),
+                                             grad, **ok)
+  with pytest.raises(ValueError, match="equal rank 1 shapes"):
+    prim_utils.validate_abstract_eval_params(rp, ids[:3], ids, gains, 1,
+                                             table, grad, **ok)
+  with pytest.raises(ValueError, match="equal feature"):
+    prim_utils.validate_abstract_eval_params(rp, ids, ids, gains, 1, table,
+                                             np.ones((2, 5), np.float32), **ok)
+  with pytest.raises(ValueError, match="sharding_strategy must be MOD"):
+    prim_utils.validate_abstract_eval_params(
+        rp, ids, ids, gains, 1, table, grad,
+        **{**ok, "sharding_strategy": 2})
+  with pytest.raises(ValueError, match="max_ids_per_partition must be"):
+    prim_utils.validate_abstract_eval_params(
+        rp, ids, ids, gains, 1, table, grad,
+        **{**ok, "max_ids_per_partition": 0})
+  with pytest.raises(ValueError, match="computation_name"):
+    prim_utils.validate_abstract_eval_params(
+        rp, ids, ids, gains, 1, table, grad, **{**ok, "computation_name": ""})
+  with pytest.raises(ValueError, match="min_value must be less"):
+    prim_utils.validate_abstract_eval_params(rp, ids, ids, gains, 1, table,
+                                             grad, **ok, min_value=2.0,
+                                             max_value=1.0)
