@@ -222,8 +222,9 @@ int ref_extract_device(const RefFeature* features, int n_features,
 
 // SortAndGroupCooTensorsPerLocalDevice without minibatching
 // (sort_and_group_coo_tensors_impl.h:196-311, :349-646). Input: per-SC
-// extraction-order lists. Output: per-SC grouped lists (capacity = input
-// size), stats in the reference's per-device layout:
+// extraction-order lists. Output: per-SC grouped lists packed SC after SC
+// (g_sizes[s] entries each; capacity = input size), stats in the reference's
+// per-device layout:
 //   max_ids[NS], max_unique[NS]  (max over local SCs of per-partition counts)
 //   required[S]                  (sum over partitions of roundup8(ids))
 // Returns 0 on success, 2 when a limit is exceeded and dropping is not allowed
@@ -244,6 +245,7 @@ int ref_sort_and_group(int num_sc_per_device, const int64_t* sc_sizes,
   int64_t total_dropped = 0;
   int status = 0;
   int64_t in_base = 0;
+  int64_t out_base = 0;  // grouped lists are written packed, SC after SC
   for (int s = 0; s < S; ++s) {
     const int64_t n = sc_sizes[s];
     const int32_t* r = rows + in_base;
@@ -277,9 +279,9 @@ int ref_sort_and_group(int num_sc_per_device, const int64_t* sc_sizes,
     bool dropping_current_col = false;
     const bool perform_dropping = allow_id_dropping != 0;
     int64_t out = 0;
-    int32_t* orow = g_rows + in_base;
-    int32_t* ocol = g_cols + in_base;
-    float* ogain = g_gains + in_base;
+    int32_t* orow = g_rows + out_base;
+    int32_t* ocol = g_cols + out_base;
+    float* ogain = g_gains + out_base;
     for (int64_t i = 0; i < n; ++i) {
       const uint64_t key = keys[i];
       const uint32_t col = ref_col_id_from_key(key, num_sc_bits);
@@ -348,6 +350,7 @@ int ref_sort_and_group(int num_sc_per_device, const int64_t* sc_sizes,
       status = 2;
     }
     in_base += n;
+    out_base += out;
   }
   *dropped = total_dropped;
   return status;

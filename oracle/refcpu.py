@@ -259,10 +259,9 @@ def sort_and_group(rows, cols, gains, sc_sizes, *, num_scs,
   base = 0
   for s in range(s_count):
     k = int(g_sizes[s])
-    in_n = int(sc_sizes[s])
     per_sc.append((g_rows[base:base + k].copy(), g_cols[base:base + k].copy(),
                    g_gains[base:base + k].copy()))
-    base += in_n
+    base += k
   return GroupResult(per_sc, max_ids, max_unique, required,
                      int(dropped.value), st == 2)
 

@@ -68,6 +68,15 @@ def _make_specs(num_tables, vocabs, dims, combiner, optimizer, batch,
   return tables, feats
 
 
+def _stack(feats, names, global_device_count, num_sc, limit=1 << 20, **kw):
+  """stack_tables with explicit stack limits (the default for a multi-table
+  stack is 256, table_stacking.py:616-645)."""
+  table_stacking.stack_tables(
+      feats, names, global_device_count, num_sc,
+      stack_to_max_ids_per_partition=lambda n, b: limit,
+      stack_to_max_unique_ids_per_partition=lambda n, b: limit, **kw)
+
+
 def _ragged(rng, batch, lo, hi, vocab, zipf_a=None):
   lens = rng.integers(lo, hi + 1, size=batch)
   rows = []
@@ -138,8 +147,7 @@ def test_preprocess_ragged_stacked(combiner, weighted, num_sc):
   _, feats = _make_specs(3, vocabs, [16, 16, 16], combiner,
                          embedding_spec.SGDOptimizerSpec(0.01), batch,
                          features_per_table=2)
-  table_stacking.stack_tables(feats, ["table_0", "table_1", "table_2"], 1,
-                              num_sc)
+  _stack(feats, ["table_0", "table_1", "table_2"], 1, num_sc)
   features = [
       _ragged(rng, batch, 0, 12, vocabs[i // 2], zipf_a=1.2 if i % 2 else None)
       for i in range(len(feats))
@@ -154,8 +162,7 @@ def test_preprocess_dense_dropping_and_rotation():
   _, feats = _make_specs(2, [4000, 300], [8, 8], "sum",
                          embedding_spec.SGDOptimizerSpec(0.01), batch,
                          max_ids=6)
-  table_stacking.stack_tables(feats, ["table_0", "table_1"], 1, 4,
-                              rotation=1)
+  _stack(feats, ["table_0", "table_1"], 1, 4, limit=6, rotation=1)
   features = [_zipf(rng, 1.1, 4000, batch * 5).reshape(batch, 5),
               rng.integers(0, 300, size=(batch, 3)).astype(np.int32)]
   (_, _, _, _, _, stats), ref = _compare_preprocessing(
@@ -181,7 +188,7 @@ def test_preprocess_multi_device_layout():
   batch = 32
   _, feats = _make_specs(2, [500, 80], [8, 8], "mean",
                          embedding_spec.SGDOptimizerSpec(0.01), batch)
-  table_stacking.stack_tables(feats, ["table_0", "table_1"], 2, 2)
+  _stack(feats, ["table_0", "table_1"], 2, 2)
   features = [_ragged(rng, batch, 1, 6, 500), _ragged(rng, batch, 1, 3, 80)]
   _compare_preprocessing(features, None, feats, 2, local_device_count=2,
                          global_device_count=2)
@@ -221,54 +228,88 @@ def test_forward_matches_oracle(dim, num_sc):
   np.testing.assert_array_equal(act.cpu().numpy(), exp)
 
 
+def _run_grad(optimizer, csr, grad, table0, acc0, lr, lo, hi, num_sc):
+  """Runs the GPU primitive and the oracle; returns (got, expected) pairs."""
+  table = torch.from_numpy(table0.copy()).cuda()
+  if optimizer == "sgd":
+    out = sgd_prim.tpu_sparse_dense_matmul_grad_with_sgd_primitive.bind(
+        *csr, 1, table, torch.from_numpy(grad).cuda(), lr,
+        max_ids_per_partition=1 << 20, max_unique_ids_per_partition=1 << 20,
+        min_value=lo, max_value=hi, num_sc_per_device=num_sc)
+    assert out is table
+    exp_t = refcpu.sparse_dense_matmul_grad(
+        *csr, grad, table0, None, learning_rate=lr,
+        num_sc_per_device=num_sc, num_scs=num_sc, min_value=lo, max_value=hi)
+    return [(table.cpu().numpy(), exp_t)]
+  acc = torch.from_numpy(acc0.copy()).cuda()
+  out_t, out_a = (
+      adagrad_prim.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
+          *csr, 1, table, acc, torch.from_numpy(grad).cuda(), np.float32(lr),
+          max_ids_per_partition=1 << 20, max_unique_ids_per_partition=1 << 20,
+          min_value=lo, max_value=hi, num_sc_per_device=num_sc))
+  assert out_t is table and out_a is acc
+  exp_t, exp_a = refcpu.sparse_dense_matmul_grad(
+      *csr, grad, table0, acc0, learning_rate=lr, num_sc_per_device=num_sc,
+      num_scs=num_sc, min_value=lo, max_value=hi)
+  return [(table.cpu().numpy(), exp_t), (acc.cpu().numpy(), exp_a)]
+
+
 @pytest.mark.parametrize("optimizer", ["sgd", "adagrad"])
 @pytest.mark.parametrize("dim", [1, 8, 24, 128, 256, 300])
 @pytest.mark.parametrize("num_sc", [1, 2])
 @pytest.mark.parametrize("clip", [False, True])
-def test_grad_matches_oracle(optimizer, dim, num_sc, clip):
+def test_grad_hot_rows_exact(optimizer, dim, num_sc, clip):
+  """Long runs of hot rows (Zipf 1.05 over 300 rows) cross the backward's
+  chunk boundaries and use the multi-piece reduction. Integer-valued
+  gradients with unit gains make every partial sum exact, so the result may
+  not depend on summation order: GPU and oracle must agree bit for bit."""
   rng = np.random.default_rng(dim * 13 + num_sc + (7 if clip else 0))
   batch = 4096 if dim <= 128 else 512
   vocab = 300
   _, feats = _make_specs(1, [vocab], [dim], "sum",
                          embedding_spec.SGDOptimizerSpec(0.01), batch)
   embedding.prepare_feature_specs_for_training(feats, 1, num_sc)
-  # Zipf ids over a small vocab: long runs of hot rows cross the backward's
-  # chunk boundaries and exercise the multi-piece reduction.
   features = [_ragged(rng, batch, 1, 8, vocab, zipf_a=1.05)]
   name, ref = _csr_from_oracle(features, None, feats, num_sc)
   rows = feats[0].table_spec.stacked_table_spec.stack_vocab_size
   shape = (rows,) if dim == 1 else (rows, dim)
   table0 = rng.normal(0, 0.01, size=shape).astype(np.float32)
   acc0 = np.full(shape, 0.1, np.float32)
-  grad = rng.normal(0, 1, size=(batch,) if dim == 1 else
-                    (batch, dim)).astype(np.float32)
+  grad = rng.integers(-3, 4, size=(batch,) if dim == 1 else
+                      (batch, dim)).astype(np.float32)
   lo, hi = (-0.005, 0.005) if clip else (None, None)
   csr = (ref.row_pointers[name], ref.embedding_ids[name],
          ref.sample_ids[name], ref.gains[name])
-  table = torch.from_numpy(table0.copy()).cuda()
-  if optimizer == "sgd":
-    out = sgd_prim.tpu_sparse_dense_matmul_grad_with_sgd_primitive.bind(
-        *csr, 1, table, torch.from_numpy(grad).cuda(), 0.05,
-        max_ids_per_partition=1 << 20, max_unique_ids_per_partition=1 << 20,
-        min_value=lo, max_value=hi, num_sc_per_device=num_sc)
-    assert out is table
-    exp_t = refcpu.sparse_dense_matmul_grad(
-        *csr, grad, table0, None, learning_rate=0.05,
-        num_sc_per_device=num_sc, num_scs=num_sc, min_value=lo, max_value=hi)
-  else:
-    acc = torch.from_numpy(acc0.copy()).cuda()
-    out_t, out_a = (
-        adagrad_prim.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
-            *csr, 1, table, acc, torch.from_numpy(grad).cuda(),
-            np.float32(0.05), max_ids_per_partition=1 << 20,
-            max_unique_ids_per_partition=1 << 20, min_value=lo, max_value=hi,
-            num_sc_per_device=num_sc))
-    assert out_t is table and out_a is acc
-    exp_t, exp_a = refcpu.sparse_dense_matmul_grad(
-        *csr, grad, table0, acc0, learning_rate=0.05,
-        num_sc_per_device=num_sc, num_scs=num_sc, min_value=lo, max_value=hi)
-    np.testing.assert_allclose(acc.cpu().numpy(), exp_a, rtol=RTOL, atol=ATOL)
-  np.testing.assert_allclose(table.cpu().numpy(), exp_t, rtol=RTOL, atol=ATOL)
+  for got, exp in _run_grad(optimizer, csr, grad, table0, acc0, 0.05, lo, hi,
+                            num_sc):
+    np.testing.assert_array_equal(got, exp)
+
+
+@pytest.mark.parametrize("optimizer", ["sgd", "adagrad"])
+@pytest.mark.parametrize("combiner", ["sum", "mean", "sqrtn"])
+@pytest.mark.parametrize("dim", [8, 64, 128])
+@pytest.mark.parametrize("num_sc", [1, 4])
+def test_grad_float_matches_oracle(optimizer, combiner, dim, num_sc):
+  """Float gains and gradients, short runs: within rtol 1e-5 / atol 1e-6."""
+  rng = np.random.default_rng(zlib.crc32(
+      f"{optimizer}-{combiner}-{dim}-{num_sc}".encode()))
+  batch = 2048
+  vocab = 200_000
+  _, feats = _make_specs(1, [vocab], [dim], combiner,
+                         embedding_spec.SGDOptimizerSpec(0.01), batch)
+  embedding.prepare_feature_specs_for_training(feats, 1, num_sc)
+  features = [_ragged(rng, batch, 1, 30, vocab)]
+  weights = [_weights_like(rng, features[0])]
+  name, ref = _csr_from_oracle(features, weights, feats, num_sc)
+  rows = feats[0].table_spec.stacked_table_spec.stack_vocab_size
+  table0 = rng.normal(0, 0.01, size=(rows, dim)).astype(np.float32)
+  acc0 = np.full((rows, dim), 0.1, np.float32)
+  grad = rng.normal(0, 1, size=(batch, dim)).astype(np.float32)
+  csr = (ref.row_pointers[name], ref.embedding_ids[name],
+         ref.sample_ids[name], ref.gains[name])
+  for got, exp in _run_grad(optimizer, csr, grad, table0, acc0, 0.05, None,
+                            None, num_sc):
+    np.testing.assert_allclose(got, exp, rtol=RTOL, atol=ATOL)
 
 
 def test_end_to_end_api_feature_stacking_adagrad():
@@ -280,7 +321,7 @@ def test_end_to_end_api_feature_stacking_adagrad():
                                             initial_accumulator_value=0.1)
   tables, feats = _make_specs(2, [3000, 50000], [32, 32], "mean", opt, batch,
                               features_per_table=2)
-  table_stacking.stack_tables(feats, ["table_0", "table_1"], 1, 1)
+  _stack(feats, ["table_0", "table_1"], 1, 1)
   features = [_ragged(rng, batch, 1, 20, t.vocabulary_size, zipf_a=1.2)
               for t in (tables[0], tables[0], tables[1], tables[1])]
   pre, _ = embedding.preprocess_sparse_dense_matmul_input(
