@@ -6,7 +6,10 @@ resident in HBM: the forward lookup (scemb_sparse_dense_matmul) and the
 backward pass fused with the Adagrad update
 (scemb_sparse_dense_matmul_grad_with_adagrad) of every stacked table. The CSR
 buffers come from the GPU preprocessing, which is timed separately
-(`preprocess_ms`). Default workload: the 26-table DLRM shape (one stack, dim
+(`preprocess_ms`); it also emits the sample view the forward pass consumes
+and marks the CSR as sorted by row, so the step itself runs no sort. The
+same step fed only the four reference CSR arrays (each call then sorts a
+copy of the entries) is timed too (`csr_only_ms_per_step`). Default workload: the 26-table DLRM shape (one stack, dim
 128, batch 65,536, one Zipf(1.1) id per feature and sample, sum combiner,
 Adagrad lr 0.01 / accumulator 0.1).
 
@@ -156,7 +159,7 @@ def run_gpu(w: Workload, steps: int, warmup: int):
     log(f"stack {name}: rows={rows} dim={dim} N={n_valid} U={uniq} Bs={bs}")
   lr = torch.tensor(w.lr, dtype=torch.float32, device=dev)
 
-  def step():
+  def step(csr_only=False):
     for name, spec in stacked.items():
       t, a, g = tables[name]
       csr = (pre.lhs_row_pointers[name], pre.lhs_embedding_ids[name],
@@ -165,31 +168,43 @@ def run_gpu(w: Workload, steps: int, warmup: int):
           *csr, 1, t, device_batch_size=spec.total_sample_count,
           max_ids_per_partition=spec.max_ids_per_partition,
           max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
-          num_sc_per_device=1)
+          num_sc_per_device=1,
+          lookup_view=None if csr_only else pre.lookup_views[name])
       ada.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
           *csr, 1, t, a, g, lr,
           max_ids_per_partition=spec.max_ids_per_partition,
           max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
-          num_sc_per_device=1)
+          num_sc_per_device=1,
+          csr_sorted_by_row=not csr_only and pre.csr_sorted_by_row)
 
+  def timed(n, csr_only):
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n):
+      step(csr_only)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / n
+
+  for _ in range(warmup):
+    step(True)
+  csr_only_ms = timed(steps, True)
+  log(f"step with the reference CSR arrays only: {csr_only_ms:.4f} ms")
   for _ in range(warmup):
     step()
   torch.cuda.synchronize()
   _native.profile_enable(True)
   _native.profile_collect(None)
-  torch.cuda.synchronize()
-  t0 = time.perf_counter()
-  for _ in range(steps):
-    step()
-  torch.cuda.synchronize()
-  t1 = time.perf_counter()
+  ms_per_step = timed(steps, False)
   _native.profile_enable(False)
   spans = {}
-  for k in ("fwd_gather", "bwd_update", "fwd_call", "bwd_call"):
+  for k in ("fwd_reduce", "fwd_finish", "bwd_reduce", "bwd_finish",
+            "fwd_call", "bwd_call"):
     ms, n = _native.profile_collect(k)
     spans[k] = (ms / n if n else None, n)
-  ms_per_step = (t1 - t0) * 1e3 / steps
+  log(f"step: {ms_per_step:.4f} ms; spans " +
+      ", ".join(f"{k} {v[0]:.4f}" for k, v in spans.items() if v[0]))
   return {
+      "csr_only_ms_per_step": csr_only_ms,
       "ms_per_step": ms_per_step,
       "lookups": lookups,
       "preprocess_ms": preprocess_ms,
@@ -302,12 +317,16 @@ def main():
   res = run_gpu(w, args.steps, args.warmup)
   fwd_bytes, bwd_bytes = algorithmic_bytes(res["per_stack"])
   step_s = res["ms_per_step"] / 1e3
-  fwd_ms = res["spans"]["fwd_gather"][0]
-  bwd_ms = res["spans"]["bwd_update"][0]
-  if bwd_ms is not None and (fwd_ms is None or bwd_ms >= fwd_ms):
-    dom, dom_ms, dom_bytes = "bwd_update", bwd_ms, bwd_bytes
+  sp = res["spans"]
+  # Each op is one SegReduce launch plus one SegFinish launch (the finish
+  # kernel completes the rows whose entries span several blocks).
+  fwd_ms = sp["fwd_reduce"][0] + sp["fwd_finish"][0]
+  bwd_ms = sp["bwd_reduce"][0] + sp["bwd_finish"][0]
+  if bwd_ms >= fwd_ms:
+    dom, dom_ms, dom_bytes = ("bwd: SegReduce+SegFinish (Adagrad)", bwd_ms,
+                              bwd_bytes)
   else:
-    dom, dom_ms, dom_bytes = "fwd_gather", fwd_ms, fwd_bytes
+    dom, dom_ms, dom_bytes = "fwd: SegReduce+SegFinish", fwd_ms, fwd_bytes
   achieved = dom_bytes / (dom_ms / 1e3) / 1e9
   roofline = {
       "bound": "hbm",
@@ -333,6 +352,7 @@ def main():
       "steps": args.steps,
       "warmup": args.warmup,
       "ms_per_step": round(res["ms_per_step"], 4),
+      "csr_only_ms_per_step": round(res["csr_only_ms_per_step"], 4),
       "higher_is_better": True,
       "scaling": "weak",
       "vs_baseline": None,

@@ -11,6 +11,8 @@
  * jax_tpu_embedding/sparsecore/ in jax-ml/jax-tpu-embedding):
  *   scemb_sparse_dense_matmul              custom call "SparseDenseMatmulOp",
  *       lowered at lib/core/primitives/sparse_dense_matmul_csr.py:171-201
+ *   scemb_build_sample_view                no counterpart (the SparseCore
+ *       groups by sample in hardware); optional input of the forward
  *   scemb_sparse_dense_matmul_grad_with_sgd  custom call
  *       "SparseDenseMatmulGradOpWithOptimizerUpdate" with the SGD update
  *       computation, lib/core/primitives/sparse_dense_matmul_grad_with_sgd.py:
@@ -50,6 +52,9 @@ extern "C" {
                                         sample id out of range: skipped */
 #define SCEMB_STATUS_BAD_ID 2u       /* preprocessing input id outside
                                         [0, col_id_bound): skipped */
+#define SCEMB_STATUS_UNSORTED 4u     /* a stream declared sorted (CSR flag
+                                        or sample view) is not: results are
+                                        not valid */
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* scemb_last_error(void);
@@ -72,8 +77,30 @@ typedef struct scemb_csr {
   int32_t num_segments;             /* num_sc_per_device */
   int32_t num_partitions;           /* num_sc_per_device * global devices */
   int32_t row_pointers_per_segment; /* max(num_partitions, 8) */
-  int32_t reserved;
+  uint32_t flags;                   /* SCEMB_CSR_* bits */
 } scemb_csr_t;
+
+/* The entries of each segment are ascending by (partition, embedding id), as
+ * the preprocessing writes them (input_preprocessing_util.cc:167-208 sorts by
+ * the rotated column id). With one segment the backward pass then reads the
+ * CSR in place instead of sorting it; order violations are reported through
+ * SCEMB_STATUS_UNSORTED. */
+#define SCEMB_CSR_SORTED_BY_ROW 1u
+
+/* The CSR entries of one device grouped by activation row (no counterpart
+ * in the reference, where the SparseCore scatters into activations in
+ * hardware): entry i adds gain_i * table[row_i] to activations[keys[i]].
+ * keys are ascending, entries of one key keep CSR order, keys >=
+ * device_batch_size mark unused slots (at the end). entries[i] packs
+ * row_i | (IEEE bits of gain_i) << 32. Built by scemb_build_sample_view for
+ * one (device_batch_size, table_rows) pair; the forward pass checks both. */
+typedef struct scemb_sample_view {
+  const uint32_t* keys;     /* [size] */
+  const uint64_t* entries;  /* [size] */
+  int64_t size;
+  int64_t device_batch_size;
+  int64_t table_rows;
+} scemb_sample_view_t;
 
 /* ---- Forward: SparseDenseMatmulOp --------------------------------------
  * activations[b, :] = sum over entries with s*bps + sample_id == b of
@@ -81,16 +108,35 @@ typedef struct scemb_csr {
  * bps = device_batch_size / num_segments; rows without entries are zero.
  * `table` is [table_rows, dim] row-major (dim 1 for a 1-D table). Entries
  * whose ids fall outside the table or batch are skipped and flagged in
- * *device_status (optional, may be NULL). Sums run in CSR order per row. */
+ * *device_status (optional, may be NULL). When `view` is not NULL the CSR
+ * is not read (csr may be NULL) and the view's entries are used instead;
+ * otherwise the call builds the same grouping itself. Each row is summed in
+ * a fixed order: pieces of consecutive entries in CSR order, added in a
+ * fixed tree, so repeated calls give identical results. */
 size_t scemb_sparse_dense_matmul_workspace_size(const scemb_csr_t* csr,
+                                                const scemb_sample_view_t* view,
                                                 int64_t device_batch_size,
                                                 int64_t table_rows,
                                                 int32_t dim);
-int scemb_sparse_dense_matmul(const scemb_csr_t* csr, const float* table,
-                              int64_t table_rows, int32_t dim,
-                              float* activations, int64_t device_batch_size,
-                              void* workspace, size_t workspace_bytes,
-                              uint32_t* device_status, void* stream);
+int scemb_sparse_dense_matmul(const scemb_csr_t* csr,
+                              const scemb_sample_view_t* view,
+                              const float* table, int64_t table_rows,
+                              int32_t dim, float* activations,
+                              int64_t device_batch_size, void* workspace,
+                              size_t workspace_bytes, uint32_t* device_status,
+                              void* stream);
+
+/* Builds the sample view of a CSR into keys[coo_size] / entries[coo_size]
+ * (device memory owned by the caller). Invalid entries are flagged as in the
+ * forward pass and left out of the view. */
+size_t scemb_build_sample_view_workspace_size(const scemb_csr_t* csr,
+                                              int64_t device_batch_size,
+                                              int64_t table_rows);
+int scemb_build_sample_view(const scemb_csr_t* csr, int64_t device_batch_size,
+                            int64_t table_rows, uint32_t* keys,
+                            uint64_t* entries, void* workspace,
+                            size_t workspace_bytes, uint32_t* device_status,
+                            void* stream);
 
 /* ---- Backward + optimizer: SparseDenseMatmulGradOpWithOptimizerUpdate ----
  * For every touched table row r:
@@ -101,9 +147,11 @@ int scemb_sparse_dense_matmul(const scemb_csr_t* csr, const float* table,
  * followed by T[r] = clamp(T[r], min, max) for the bounds that are given
  * (clip_mask bit 0: min_value, bit 1: max_value). Tables are updated in
  * place. The learning rate is read from `learning_rate` (device scalar) when
- * not NULL, else `learning_rate_value` is used. No float atomics: each row is
- * reduced by one wavefront, long runs split into fixed pieces summed in
- * order. */
+ * not NULL, else `learning_rate_value` is used. No float atomics: every
+ * row's gradient is summed in a fixed order (pieces of consecutive entries,
+ * added in a fixed tree) and the row is updated once. With
+ * SCEMB_CSR_SORTED_BY_ROW and one segment the CSR is read in place; else the
+ * call sorts a copy of the entries by table row. */
 size_t scemb_sparse_dense_matmul_grad_workspace_size(const scemb_csr_t* csr,
                                                      int64_t device_batch_size,
                                                      int64_t table_rows,
@@ -182,8 +230,9 @@ int scemb_preprocess_stacked_table(const scemb_feature_t* features,
 
 /* ---- Launch timing (no counterpart in the reference) -------------------
  * For benchmarks: while enabled, the library records HIP events on the launch
- * stream around its main kernels ("fwd_gather", "bwd_update") and around
- * whole calls ("fwd_call", "bwd_call", "preprocess_call").
+ * stream around its main kernels ("fwd_reduce", "fwd_finish", "bwd_reduce",
+ * "bwd_finish") and around whole calls ("fwd_call", "bwd_call",
+ * "preprocess_call").
  * scemb_profile_collect waits for the recorded events of `name` (all names
  * when NULL), returns their summed elapsed milliseconds and launch count,
  * and forgets them. */

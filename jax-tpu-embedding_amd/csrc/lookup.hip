@@ -3,28 +3,55 @@
 // SparseDenseMatmulGradOpWithOptimizerUpdate custom calls of
 // jax_tpu_embedding/sparsecore/lib/core/primitives/).
 //
-// Both directions start from the reference's CSR-wrapped COO buffers:
-//   1. ExpandCsr resolves every position of the COO buffer to its partition
-//      (row pointers), validates ids, and emits one (key, payload) pair:
-//      forward  key = activation row,  payload = (table row, gain)
-//      backward key = table row,       payload = (activation row, gain)
-//      Padding and invalid slots get a sentinel key that sorts last.
-//   2. A stable LSD radix sort groups the pairs by key (CSR order is kept
-//      inside each group, so sums run in CSR order).
-//   3. Forward: one sub-wave (G lanes, 16-byte loads) per activation row sums
-//      gain * table row over its group and writes the row once.
-//      Backward: one wavefront per fixed chunk of the sorted pairs walks the
-//      runs of equal table rows; a run inside the chunk is reduced and the
-//      optimizer applied directly; a run crossing chunk boundaries leaves one
-//      partial per chunk, and the wave that completes the run (integer
-//      counter, no float atomics) adds the partials in chunk order and
-//      applies the optimizer once.
+// Both directions are one segmented reduction over a stream of entries
+// (key, row, gain) sorted by key:
+//   forward   key = activation row, gathered row = table row
+//             epilogue: store the activation row (rows without entries are
+//             zero-filled)
+//   backward  key = table row, gathered row = activation-gradient row
+//             epilogue: optimizer update of the table row (and accumulator)
+// The stream comes from one of three places:
+//   * the CSR itself when it is already sorted by table row (backward; one
+//     segment, as the preprocessing emits it: partitions in order, embedding
+//     ids ascending inside each partition);
+//   * a sample view built once per preprocessed batch (forward);
+//   * otherwise ExpandCsr + a stable radix sort inside the call.
+//
+// SegReduce gives every 256-thread block a fixed slice of 256 stream entries
+// (perfect load balance however skewed the keys are). A block is split into
+// P = 256 / G sub-groups of G lanes; sub-group s owns entries [s*G, s*G + G)
+// of the slice and its lanes cover G * VEC columns of a row (16-byte loads).
+// A sub-group walks its entries kUnroll at a time, issuing all row loads of a
+// batch (and, for runs that end inside the batch, the table / accumulator
+// loads of the update) before accumulating. A run that is complete inside
+// one sub-group is finished there; pieces of runs that cross sub-groups are
+// combined through LDS in sub-group order; pieces of runs that cross blocks
+// leave one partial row per block and SegFinish adds them in block order.
+// Every row is reduced and written exactly once, in a fixed order: no float
+// atomics and run-to-run identical results.
 #include "../../include/scemb.h"
 #include "common.h"
 #include "scan.h"
 
 namespace scemb {
 namespace {
+
+constexpr int kBlock = 256;  // threads per block = stream entries per block
+constexpr int kUnroll = 4;   // entries in flight per sub-group
+constexpr uint32_t kSkip = 0xffffffffu;  // key of an entry outside any run
+
+// Per-block flags left by SegReduce for SegFinish.
+constexpr uint32_t kFlagHeadEnd = 1;  // a run from earlier blocks ends here
+constexpr uint32_t kFlagOwner = 2;    // a run starts here, continues past
+constexpr uint32_t kFlagMiddle = 4;   // the whole block lies inside one run
+
+// Per-sub-group piece flags (LDS).
+constexpr uint32_t kHasHead = 1;   // first entry continues the previous run
+constexpr uint32_t kHeadEnds = 2;  // ... and that run ends in this range
+constexpr uint32_t kHasTail = 4;   // a run starts here and continues past
+
+enum { kSrcSorted = 0, kSrcCsr = 1 };
+enum { kEpiFwd = 0, kEpiSgd = 1, kEpiAdagrad = 2 };
 
 struct Csr {
   const int32_t* rp;
@@ -48,6 +75,22 @@ __device__ __forceinline__ float PackedGain(uint64_t p) {
   return __uint_as_float(static_cast<uint32_t>(p >> 32));
 }
 
+// Partition of position `off` of a segment whose row pointers are `rp`
+// (partitions start at 8-aligned offsets), or -1 for padding.
+__device__ __forceinline__ int PartitionOf(const int32_t* rp, int nparts,
+                                           int64_t per_segment, int64_t off) {
+  int64_t start = 0;
+  for (int q = 0; q < nparts; ++q) {
+    int64_t end = rp[q];
+    if (end > per_segment) end = per_segment;
+    if (off < end) return off >= start ? q : -1;
+    start = (end + kAlign - 1) / kAlign * kAlign;
+  }
+  return -1;
+}
+
+// One (key, payload) pair per COO position; padding and invalid entries get
+// the sentinel key, which sorts last.
 template <bool kBySample>
 __global__ __launch_bounds__(256) void ExpandCsr(Csr csr, int64_t bps,
                                                  int64_t rows_per_partition,
@@ -60,18 +103,8 @@ __global__ __launch_bounds__(256) void ExpandCsr(Csr csr, int64_t bps,
   if (j >= n) return;
   const int s = static_cast<int>(j / csr.per_segment);
   const int64_t off = j - static_cast<int64_t>(s) * csr.per_segment;
-  const int32_t* rp = csr.rp + static_cast<int64_t>(s) * csr.rp_per_segment;
-  int p = -1;
-  int64_t start = 0;
-  for (int q = 0; q < csr.num_partitions; ++q) {
-    int64_t end = rp[q];
-    if (end > csr.per_segment) end = csr.per_segment;
-    if (off < end) {
-      if (off >= start) p = q;
-      break;
-    }
-    start = (end + kAlign - 1) / kAlign * kAlign;
-  }
+  const int p = PartitionOf(csr.rp + static_cast<int64_t>(s) * csr.rp_per_segment,
+                            csr.num_partitions, csr.per_segment, off);
   uint32_t key = sentinel;
   uint64_t pay = 0;
   if (p >= 0) {
@@ -97,24 +130,6 @@ __global__ __launch_bounds__(256) void ExpandCsr(Csr csr, int64_t bps,
   payload[j] = pay;
 }
 
-// sp[b] = first sorted position whose key is >= b, for b in [0, batch].
-__global__ __launch_bounds__(256) void GroupStarts(const uint32_t* keys,
-                                                   int64_t n, int64_t batch,
-                                                   int32_t* sp) {
-  const int64_t b = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (b > batch) return;
-  int64_t lo = 0, hi = n;
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (static_cast<int64_t>(keys[mid]) < b) {
-      lo = mid + 1;
-    } else {
-      hi = mid;
-    }
-  }
-  sp[b] = static_cast<int32_t>(lo);
-}
-
 template <int VEC>
 struct Vec;
 template <>
@@ -137,10 +152,6 @@ struct Vec<4> {
   __device__ static T Add(T a, T b) {
     return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
   }
-  __device__ static T ShflXor(T v, int m) {
-    return make_float4(__shfl_xor(v.x, m), __shfl_xor(v.y, m),
-                       __shfl_xor(v.z, m), __shfl_xor(v.w, m));
-  }
   __device__ static float Get(const T& v, int k) {
     return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
   }
@@ -159,53 +170,9 @@ struct Vec<1> {
   __device__ static void Store(float* p, T v) { *p = v; }
   __device__ static T Fma(T acc, float g, T v) { return acc + g * v; }
   __device__ static T Add(T a, T b) { return a + b; }
-  __device__ static T ShflXor(T v, int m) { return __shfl_xor(v, m); }
   __device__ static float Get(const T& v, int) { return v; }
   __device__ static void Set(T& v, int, float x) { v = x; }
 };
-
-// Forward: sub-wave of G lanes per activation row.
-template <int G, int VEC>
-__global__ __launch_bounds__(256) void FwdGather(const int32_t* sp,
-                                                 const uint64_t* payload,
-                                                 const float* table,
-                                                 int64_t dim, float* act,
-                                                 int64_t batch) {
-  using V = Vec<VEC>;
-  const int64_t gtid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t row = gtid / G;
-  const int lane = static_cast<int>(gtid % G);
-  if (row >= batch) return;
-  const int32_t lo = sp[row];
-  const int32_t hi = sp[row + 1];
-  for (int64_t c = static_cast<int64_t>(lane) * VEC; c < dim;
-       c += static_cast<int64_t>(G) * VEC) {
-    typename V::T acc = V::Zero();
-    int32_t i = lo;
-    for (; i + 4 <= hi; i += 4) {
-      const uint64_t p0 = payload[i], p1 = payload[i + 1],
-                     p2 = payload[i + 2], p3 = payload[i + 3];
-      const typename V::T v0 =
-          V::Load(table + static_cast<int64_t>(PackedIndex(p0)) * dim + c);
-      const typename V::T v1 =
-          V::Load(table + static_cast<int64_t>(PackedIndex(p1)) * dim + c);
-      const typename V::T v2 =
-          V::Load(table + static_cast<int64_t>(PackedIndex(p2)) * dim + c);
-      const typename V::T v3 =
-          V::Load(table + static_cast<int64_t>(PackedIndex(p3)) * dim + c);
-      acc = V::Fma(acc, PackedGain(p0), v0);
-      acc = V::Fma(acc, PackedGain(p1), v1);
-      acc = V::Fma(acc, PackedGain(p2), v2);
-      acc = V::Fma(acc, PackedGain(p3), v3);
-    }
-    for (; i < hi; ++i) {
-      const uint64_t p0 = payload[i];
-      acc = V::Fma(acc, PackedGain(p0),
-                   V::Load(table + static_cast<int64_t>(PackedIndex(p0)) * dim + c));
-    }
-    V::Store(act + row * dim + c, acc);
-  }
-}
 
 struct OptParams {
   const float* lr_ptr;
@@ -215,11 +182,67 @@ struct OptParams {
   float max_value;
 };
 
+// Where the stream comes from.
+struct StreamArgs {
+  const uint32_t* keys;     // kSrcSorted
+  const uint64_t* entries;  // kSrcSorted: row | gain bits << 32
+  uint32_t sentinel;        // kSrcSorted: keys >= sentinel are unused
+  int64_t src_rows;         // kSrcSorted: rows of the gathered matrix
+  Csr csr;                  // kSrcCsr (one segment)
+  int64_t rows_per_partition;
+  int64_t bps;
+  int64_t n;
+};
+
+// What the reduction reads and writes.
+struct RowArgs {
+  const float* src;  // gathered rows
+  float* dst;        // activations (forward) or table (backward)
+  float* accum;      // Adagrad accumulator
+  int64_t dim;
+  int64_t batch;     // forward: rows of dst
+  OptParams opt;
+  float* partials;   // [2 * num_blocks, dim]
+  uint32_t* block_flags;
+  uint32_t* block_keys;
+  uint32_t* status;
+};
+
+template <int SRC>
+__device__ __forceinline__ uint32_t FetchEntry(const StreamArgs& s, int64_t e,
+                                               uint64_t* ent,
+                                               uint32_t* status) {
+  if (SRC == kSrcSorted) {
+    const uint32_t k = s.keys[e];
+    *ent = s.entries[e];
+    if (k >= s.sentinel) return kSkip;
+    if (PackedIndex(*ent) >= s.src_rows) {
+      // Keeps the key (and so the run structure) but contributes nothing.
+      if (status != nullptr) atomicOr(status, SCEMB_STATUS_BAD_ENTRY);
+      *ent = Pack(0, 0.0f);
+    }
+    return k;
+  } else {
+    *ent = 0;
+    const int p = PartitionOf(s.csr.rp, s.csr.num_partitions,
+                              s.csr.per_segment, e);
+    if (p < 0) return kSkip;
+    const int32_t id = s.csr.eid[e];
+    const int32_t sm = s.csr.sid[e];
+    if (id < 0 || id >= s.rows_per_partition || sm < 0 || sm >= s.bps) {
+      if (status != nullptr) atomicOr(status, SCEMB_STATUS_BAD_ENTRY);
+      return kSkip;
+    }
+    *ent = Pack(static_cast<uint32_t>(sm), s.csr.gains[e]);
+    return static_cast<uint32_t>(p * s.rows_per_partition + id);
+  }
+}
+
 template <int OPT>
 __device__ __forceinline__ float UpdateOne(float t, float* a, float g,
                                            float lr, const OptParams& o) {
   float v;
-  if (OPT == 0) {
+  if (OPT == kEpiSgd) {
     v = t - g * lr;
   } else {
     const float acc = *a + g * g;
@@ -231,166 +254,341 @@ __device__ __forceinline__ float UpdateOne(float t, float* a, float g,
   return v;
 }
 
-template <int VEC, int OPT>
-__device__ __forceinline__ void ApplyUpdate(float* table, float* accum,
-                                            int64_t row, int64_t dim,
-                                            int64_t c, typename Vec<VEC>::T g,
-                                            float lr, const OptParams& o) {
+// Epilogue for the finished row `key` at column `col`, given the table and
+// accumulator values already loaded (backward) -- or the store (forward).
+template <int VEC, int EPI>
+__device__ __forceinline__ void Epilogue(const RowArgs& r, uint32_t key,
+                                         int64_t col, typename Vec<VEC>::T g,
+                                         typename Vec<VEC>::T t,
+                                         typename Vec<VEC>::T a, float lr) {
   using V = Vec<VEC>;
-  float* tp = table + row * dim + c;
-  typename V::T t = V::Load(tp);
-  typename V::T a = V::Zero();
-  float* ap = nullptr;
-  if (OPT == 1) {
-    ap = accum + row * dim + c;
-    a = V::Load(ap);
+  const int64_t off = static_cast<int64_t>(key) * r.dim + col;
+  if (EPI == kEpiFwd) {
+    V::Store(r.dst + off, g);
+    return;
   }
 #pragma unroll
   for (int k = 0; k < VEC; ++k) {
     float ak = V::Get(a, k);
-    const float nv = UpdateOne<OPT>(V::Get(t, k), &ak, V::Get(g, k), lr, o);
-    V::Set(t, k, nv);
+    V::Set(t, k, UpdateOne<EPI>(V::Get(t, k), &ak, V::Get(g, k), lr, r.opt));
     V::Set(a, k, ak);
   }
-  V::Store(tp, t);
-  if (OPT == 1) V::Store(ap, a);
+  V::Store(r.dst + off, t);
+  if (EPI == kEpiAdagrad) V::Store(r.accum + off, a);
 }
 
-// Sum of gain * act_grad rows over sorted positions [a, b) for the column
-// tile starting at `c`, reduced over the P = 64 / G sub-waves of the wave so
-// that every sub-wave holds the total.
+template <int VEC, int EPI>
+__device__ __forceinline__ void EpilogueLoad(const RowArgs& r, uint32_t key,
+                                             int64_t col,
+                                             typename Vec<VEC>::T g,
+                                             float lr) {
+  using V = Vec<VEC>;
+  typename V::T t = V::Zero(), a = V::Zero();
+  const int64_t off = static_cast<int64_t>(key) * r.dim + col;
+  if (EPI != kEpiFwd) t = V::Load(r.dst + off);
+  if (EPI == kEpiAdagrad) a = V::Load(r.accum + off);
+  Epilogue<VEC, EPI>(r, key, col, g, t, a, lr);
+}
+
+__device__ __forceinline__ uint64_t LowBits(int k) {
+  return k >= 64 ? ~0ull : ((1ull << k) - 1);
+}
+
 template <int G, int VEC>
-__device__ __forceinline__ typename Vec<VEC>::T RunSum(
-    const uint64_t* payload, int64_t a, int64_t b, const float* act_grad,
-    int64_t dim, int64_t c, int sub) {
+__device__ __forceinline__ void ZeroRows(float* dst, int64_t dim, int64_t lo,
+                                         int64_t hi, int cl) {
   using V = Vec<VEC>;
-  constexpr int P = kWave / G;
-  typename V::T acc = V::Zero();
-  const bool col_ok = c < dim;
-  int64_t i = a + sub;
-  if (col_ok) {
-    for (; i + 3 * P < b; i += 4 * P) {
-      const uint64_t p0 = payload[i], p1 = payload[i + P],
-                     p2 = payload[i + 2 * P], p3 = payload[i + 3 * P];
-      const typename V::T v0 =
-          V::Load(act_grad + static_cast<int64_t>(PackedIndex(p0)) * dim + c);
-      const typename V::T v1 =
-          V::Load(act_grad + static_cast<int64_t>(PackedIndex(p1)) * dim + c);
-      const typename V::T v2 =
-          V::Load(act_grad + static_cast<int64_t>(PackedIndex(p2)) * dim + c);
-      const typename V::T v3 =
-          V::Load(act_grad + static_cast<int64_t>(PackedIndex(p3)) * dim + c);
-      acc = V::Fma(acc, PackedGain(p0), v0);
-      acc = V::Fma(acc, PackedGain(p1), v1);
-      acc = V::Fma(acc, PackedGain(p2), v2);
-      acc = V::Fma(acc, PackedGain(p3), v3);
-    }
-    for (; i < b; i += P) {
-      const uint64_t p0 = payload[i];
-      acc = V::Fma(acc, PackedGain(p0),
-                   V::Load(act_grad + static_cast<int64_t>(PackedIndex(p0)) * dim + c));
+  for (int64_t row = lo; row < hi; ++row) {
+    for (int64_t col = static_cast<int64_t>(cl) * VEC; col < dim;
+         col += static_cast<int64_t>(G) * VEC) {
+      V::Store(dst + row * dim + col, V::Zero());
     }
   }
-#pragma unroll
-  for (int m = G; m < kWave; m <<= 1) acc = V::Add(acc, V::ShflXor(acc, m));
-  return acc;
 }
 
-// First index in [lo, hi) whose key differs from `key` (keys sorted), or hi.
-__device__ __forceinline__ int64_t RunEnd(const uint32_t* keys, int64_t lo,
-                                          int64_t hi, uint32_t key) {
-  for (int64_t base = lo; base < hi; base += kWave) {
-    const int64_t idx = base + __lane_id();
-    const uint32_t k = idx < hi ? keys[idx] : key;
-    const uint64_t diff = __ballot(k != key);
-    if (diff) return base + (__ffsll(static_cast<long long>(diff)) - 1);
-  }
-  return hi;
-}
-
-__device__ __forceinline__ int64_t LowerBound(const uint32_t* keys, int64_t lo,
-                                              int64_t hi, uint32_t key) {
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (keys[mid] < key) lo = mid + 1; else hi = mid;
-  }
-  return lo;
-}
-__device__ __forceinline__ int64_t UpperBound(const uint32_t* keys, int64_t lo,
-                                              int64_t hi, uint32_t key) {
-  while (lo < hi) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (keys[mid] <= key) lo = mid + 1; else hi = mid;
-  }
-  return lo;
-}
-
-template <int G, int VEC, int OPT>
-__global__ __launch_bounds__(256) void BwdFused(
-    const uint32_t* keys, const uint64_t* payload, int64_t n, int64_t chunk,
-    int64_t num_chunks, const float* act_grad, int64_t dim, float* table,
-    float* accum, uint32_t sentinel, OptParams opt, float* partials,
-    uint32_t* counters) {
+template <int G, int VEC, int SRC, int EPI>
+__global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
   using V = Vec<VEC>;
-  const int64_t c =
-      (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-  if (c >= num_chunks) return;
-  const int lane = __lane_id();
-  const int sub = lane / G;
-  const int col_lane = lane % G;
-  const float lr = opt.lr_ptr != nullptr ? *opt.lr_ptr : opt.lr_value;
-  const int64_t cb = c * chunk;
-  const int64_t ce = cb + chunk < n ? cb + chunk : n;
-  int64_t i = cb;
-  while (i < ce) {
-    const uint32_t key = keys[i];
-    if (key >= sentinel) break;
-    const int64_t j = RunEnd(keys, i + 1, ce, key);
-    const bool head_cont = i == cb && c > 0 && keys[cb - 1] == key;
-    const bool tail_cont = j == ce && ce < n && keys[ce] == key;
-    const int64_t row = key;
-    if (!head_cont && !tail_cont) {
-      for (int64_t col = static_cast<int64_t>(col_lane) * VEC; col < dim;
-           col += static_cast<int64_t>(G) * VEC) {
-        const typename V::T g = RunSum<G, VEC>(payload, i, j, act_grad, dim, col, sub);
-        if (sub == 0) ApplyUpdate<VEC, OPT>(table, accum, row, dim, col, g, lr, opt);
-      }
+  using T = typename V::T;
+  constexpr int P = kBlock / G;
+  __shared__ uint32_t s_key[kBlock + 2];  // [0]: entry before, [257]: after
+  __shared__ uint64_t s_ent[kBlock];
+  __shared__ T s_part[2 * P][G];
+  __shared__ uint32_t s_info[P];
+
+  const int tid = threadIdx.x;
+  const int64_t blk = blockIdx.x;
+  const int64_t cb = blk * kBlock;
+  const int64_t n = st.n;
+  {
+    uint64_t en = 0;
+    uint32_t k = kSkip;
+    if (cb + tid < n) k = FetchEntry<SRC>(st, cb + tid, &en, r.status);
+    s_key[tid + 1] = k;
+    s_ent[tid] = en;
+    if (tid == 0) {
+      uint64_t d;
+      s_key[0] = cb > 0 ? FetchEntry<SRC>(st, cb - 1, &d, nullptr) : kSkip;
+    }
+    if (tid == kBlock - 1) {
+      uint64_t d;
+      s_key[kBlock + 1] =
+          cb + kBlock < n ? FetchEntry<SRC>(st, cb + kBlock, &d, nullptr)
+                          : kSkip;
+    }
+  }
+  __syncthreads();
+
+  const int sub = tid / G;
+  const int cl = tid % G;
+  const int base = sub * G;  // first entry of the sub-group in the block
+  const int64_t left = n - (cb + base);
+  const int cnt = left <= 0 ? 0 : (left < G ? static_cast<int>(left) : G);
+  const uint32_t my_key = s_key[tid + 1];
+  const uint32_t prev_key = s_key[tid];
+  const bool mine = cl < cnt;
+  const bool valid = mine && my_key != kSkip;
+
+  if (r.status != nullptr && mine) {
+    const bool bad = SRC == kSrcCsr
+                         ? (valid && prev_key != kSkip && prev_key > my_key)
+                         : (cb + tid > 0 && prev_key > my_key);
+    if (bad) atomicOr(r.status, SCEMB_STATUS_UNSORTED);
+  }
+
+  const int wshift = (tid % kWave) / G * G;
+  const uint64_t gmask = LowBits(G);
+  const uint64_t valid_m = (__ballot(valid) >> wshift) & gmask;
+  const uint64_t start_m =
+      (__ballot(valid && my_key != prev_key) >> wshift) & gmask;
+  const uint64_t end_m =
+      (__ballot(valid && (cl == cnt - 1 || my_key != s_key[tid + 2])) >>
+       wshift) & gmask;
+
+  if (EPI == kEpiFwd) {
+    // Activation rows without entries: rows strictly between the clamped
+    // keys of consecutive entries, before the first and after the last.
+    const int64_t e = cb + tid;
+    const int64_t ck = my_key == kSkip ? r.batch : my_key;
+    const int64_t cp = e == 0 ? -1 : (prev_key == kSkip ? r.batch : prev_key);
+    const bool gap = mine && ck > cp + 1;
+    uint64_t m = (__ballot(gap) >> wshift) & gmask;
+    while (m) {
+      const int l = __ffsll(static_cast<long long>(m)) - 1;
+      m &= m - 1;
+      const int64_t lo = __shfl(static_cast<int>(cp + 1), wshift + l);
+      const int64_t hi = __shfl(static_cast<int>(ck), wshift + l);
+      ZeroRows<G, VEC>(r.dst, r.dim, lo, hi, cl);
+    }
+    const bool tail_gap = mine && e == n - 1 && ck + 1 < r.batch;
+    m = (__ballot(tail_gap) >> wshift) & gmask;
+    if (m) {
+      const int l = __ffsll(static_cast<long long>(m)) - 1;
+      const int64_t lo = __shfl(static_cast<int>(ck + 1), wshift + l);
+      ZeroRows<G, VEC>(r.dst, r.dim, lo, r.batch, cl);
+    }
+  }
+
+  // Pieces of this sub-group's range that are not whole runs.
+  const bool head_cont = (valid_m & 1) && !(start_m & 1);
+  bool tail_cont = false;
+  if (cnt > 0) {
+    const uint32_t kl = s_key[base + cnt];
+    tail_cont = kl != kSkip && kl == s_key[base + cnt + 1];
+  }
+  const bool whole = head_cont && tail_cont &&
+                     (start_m & ~1ull & LowBits(cnt)) == 0;
+  const uint32_t info = (head_cont ? kHasHead : 0) |
+                        (head_cont && !whole ? kHeadEnds : 0) |
+                        (tail_cont && !whole ? kHasTail : 0);
+  if (cl == 0) s_info[sub] = info;
+  if (tid == 0) {
+    const int last = n - cb < kBlock ? static_cast<int>(n - cb) : kBlock;
+    const uint32_t kf = s_key[1], kl = s_key[last];
+    const bool from_prev = kf != kSkip && kf == s_key[0];
+    const bool to_next = kl != kSkip && kl == s_key[last + 1];
+    uint32_t f;
+    if (from_prev && to_next && kf == kl) {
+      f = kFlagMiddle;
     } else {
-      const int64_t rs = head_cont ? LowerBound(keys, 0, cb, key) : i;
-      const int64_t re = tail_cont ? UpperBound(keys, ce, n, key) : j;
-      const int64_t c0 = rs / chunk;
-      const int64_t c1 = (re - 1) / chunk;
-      const int64_t slot = c == c0 ? 2 * c0 + 1 : 2 * c;
-      for (int64_t col = static_cast<int64_t>(col_lane) * VEC; col < dim;
-           col += static_cast<int64_t>(G) * VEC) {
-        const typename V::T g = RunSum<G, VEC>(payload, i, j, act_grad, dim, col, sub);
-        if (sub == 0) V::Store(partials + slot * dim + col, g);
+      f = (from_prev ? kFlagHeadEnd : 0) | (to_next ? kFlagOwner : 0);
+    }
+    r.block_flags[blk] = f;
+    if (f & kFlagOwner) r.block_keys[blk] = kl;
+  }
+
+  const float lr = EPI == kEpiFwd
+                       ? 0.f
+                       : (r.opt.lr_ptr != nullptr ? *r.opt.lr_ptr
+                                                  : r.opt.lr_value);
+  const int64_t dim = r.dim;
+  for (int64_t col0 = 0; col0 < dim; col0 += static_cast<int64_t>(G) * VEC) {
+    const int64_t col = col0 + static_cast<int64_t>(cl) * VEC;
+    const bool col_ok = col < dim;
+    T acc = V::Zero();
+    for (int q = 0; q < cnt; q += kUnroll) {
+      T v[kUnroll];
+      T tv[kUnroll];
+      T av[kUnroll];
+      float gn[kUnroll];
+      uint32_t kk[kUnroll];
+      bool fin[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int idx = q + u;
+        const bool val = idx < cnt && ((valid_m >> idx) & 1);
+        uint64_t en = 0;
+        kk[u] = kSkip;
+        if (val) {
+          en = s_ent[base + idx];
+          kk[u] = s_key[base + idx + 1];
+        }
+        gn[u] = PackedGain(en);
+        v[u] = V::Zero();
+        if (val && col_ok) {
+          v[u] = V::Load(r.src + static_cast<int64_t>(PackedIndex(en)) * dim +
+                         col);
+        }
+        const bool is_end = val && ((end_m >> idx) & 1);
+        const bool first = (start_m & ~1ull & LowBits(idx + 1)) == 0;
+        const bool head_piece = head_cont && first;
+        const bool tail_piece = idx == cnt - 1 && tail_cont;
+        fin[u] = is_end && !head_piece && !tail_piece;
+        tv[u] = V::Zero();
+        av[u] = V::Zero();
+        if (EPI != kEpiFwd && fin[u] && col_ok) {
+          const int64_t off = static_cast<int64_t>(kk[u]) * dim + col;
+          tv[u] = V::Load(r.dst + off);
+          if (EPI == kEpiAdagrad) av[u] = V::Load(r.accum + off);
+        }
       }
-      ReleaseFence();
-      uint32_t old = 0;
-      if (lane == 0) old = atomicAdd(&counters[c0], 1u);
-      old = __shfl(old, 0);
-      if (static_cast<int64_t>(old) == c1 - c0) {
-        AcquireFence();
-        if (sub == 0) {
-          for (int64_t col = static_cast<int64_t>(col_lane) * VEC; col < dim;
-               col += static_cast<int64_t>(G) * VEC) {
-            typename V::T g = V::Load(partials + (2 * c0 + 1) * dim + col);
-            for (int64_t cc = c0 + 1; cc <= c1; ++cc) {
-              g = V::Add(g, V::Load(partials + (2 * cc) * dim + col));
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int idx = q + u;
+        if (idx < cnt && ((valid_m >> idx) & 1)) {
+          acc = V::Fma(acc, gn[u], v[u]);
+          if ((end_m >> idx) & 1) {
+            if (fin[u]) {
+              if (col_ok) Epilogue<VEC, EPI>(r, kk[u], col, acc, tv[u], av[u], lr);
+            } else {
+              const bool first = (start_m & ~1ull & LowBits(idx + 1)) == 0;
+              s_part[head_cont && first ? 2 * sub : 2 * sub + 1][cl] = acc;
             }
-            ApplyUpdate<VEC, OPT>(table, accum, row, dim, col, g, lr, opt);
+            acc = V::Zero();
           }
         }
       }
     }
-    i = j;
+    __syncthreads();
+    // Runs crossing sub-group boundaries: the sub-group holding a run's first
+    // piece in this block adds the following sub-groups' head pieces.
+    for (int job = 0; job < 2; ++job) {
+      const bool active =
+          job == 0 ? (sub == 0 && (info & kHasHead)) : (info & kHasTail) != 0;
+      if (!active) continue;
+      T g = s_part[job == 0 ? 0 : 2 * sub + 1][cl];
+      bool ended = job == 0 && (info & kHeadEnds);
+      for (int tt = sub + 1; !ended && tt < P; ++tt) {
+        const uint32_t inf = s_info[tt];
+        if (!(inf & kHasHead)) break;
+        g = V::Add(g, s_part[2 * tt][cl]);
+        ended = (inf & kHeadEnds) != 0;
+      }
+      const uint32_t key = job == 0 ? s_key[1] : s_key[base + cnt];
+      if (job == 1 && ended) {
+        if (col_ok) EpilogueLoad<VEC, EPI>(r, key, col, g, lr);
+      } else if (col_ok) {
+        const int64_t slot = job == 1 ? 2 * blk + 1 : 2 * blk;
+        V::Store(r.partials + slot * dim + col, g);
+      }
+    }
+    __syncthreads();
   }
 }
 
-__global__ void FillU32(uint32_t* p, int64_t n, uint32_t v) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
+// Runs that cross blocks: the block where such a run starts (kFlagOwner)
+// finds the block where it ends (the next kFlagHeadEnd; every block between
+// is kFlagMiddle), adds the partial rows in block order and applies the
+// epilogue once.
+template <int G, int VEC, int EPI>
+__global__ __launch_bounds__(kBlock) void SegFinish(int64_t num_blocks,
+                                                    RowArgs r) {
+  using V = Vec<VEC>;
+  using T = typename V::T;
+  constexpr int P = kBlock / G;
+  constexpr int kWaves = kBlock / kWave;
+  __shared__ T s_part[P][G];
+  __shared__ int64_t s_end[kWaves];
+  const int64_t blk = blockIdx.x;
+  if (!(r.block_flags[blk] & kFlagOwner)) return;
+  const int tid = threadIdx.x;
+  const int sub = tid / G;
+  const int cl = tid % G;
+  const uint32_t key = r.block_keys[blk];
+  int64_t c1 = -1;
+  for (int64_t b0 = blk + 1; b0 < num_blocks && c1 < 0; b0 += kBlock) {
+    const int64_t c = b0 + tid;
+    const bool is_end = c < num_blocks && (r.block_flags[c] & kFlagHeadEnd);
+    const uint64_t m = __ballot(is_end);
+    if (tid % kWave == 0) {
+      s_end[tid / kWave] =
+          m ? b0 + (tid / kWave) * kWave +
+                  (__ffsll(static_cast<long long>(m)) - 1)
+            : -1;
+    }
+    __syncthreads();
+    for (int w = 0; w < kWaves; ++w) {
+      if (s_end[w] >= 0) {
+        c1 = s_end[w];
+        break;
+      }
+    }
+    __syncthreads();
+  }
+  if (c1 < 0) {
+    if (tid == 0 && r.status != nullptr) {
+      atomicOr(r.status, SCEMB_STATUS_BAD_ENTRY);
+    }
+    return;
+  }
+  const int64_t m = c1 - blk + 1;  // partial rows: 2*blk+1, then 2*(blk+q)
+  const float lr = EPI == kEpiFwd
+                       ? 0.f
+                       : (r.opt.lr_ptr != nullptr ? *r.opt.lr_ptr
+                                                  : r.opt.lr_value);
+  const int64_t dim = r.dim;
+  for (int64_t col0 = 0; col0 < dim; col0 += static_cast<int64_t>(G) * VEC) {
+    const int64_t col = col0 + static_cast<int64_t>(cl) * VEC;
+    const bool col_ok = col < dim;
+    T acc = V::Zero();
+    if (col_ok) {
+      int64_t q = sub;
+      for (; q + 3 * P < m; q += 4 * P) {
+        const T p0 = V::Load(r.partials +
+                             (q == 0 ? 2 * blk + 1 : 2 * (blk + q)) * dim + col);
+        const T p1 = V::Load(r.partials + 2 * (blk + q + P) * dim + col);
+        const T p2 = V::Load(r.partials + 2 * (blk + q + 2 * P) * dim + col);
+        const T p3 = V::Load(r.partials + 2 * (blk + q + 3 * P) * dim + col);
+        acc = V::Add(acc, p0);
+        acc = V::Add(acc, p1);
+        acc = V::Add(acc, p2);
+        acc = V::Add(acc, p3);
+      }
+      for (; q < m; q += P) {
+        acc = V::Add(acc, V::Load(r.partials +
+                                  (q == 0 ? 2 * blk + 1 : 2 * (blk + q)) * dim +
+                                  col));
+      }
+    }
+    s_part[sub][cl] = acc;
+    __syncthreads();
+    if (sub == 0) {
+      T g = s_part[0][cl];
+      for (int s = 1; s < P; ++s) g = V::Add(g, s_part[s][cl]);
+      if (col_ok) EpilogueLoad<VEC, EPI>(r, key, col, g, lr);
+    }
+    __syncthreads();
+  }
 }
 
 __global__ void FillF32(float* p, int64_t n, float v) {
@@ -403,7 +601,7 @@ __global__ void FillF32(float* p, int64_t n, float v) {
 // ---------------------------------------------------------------------------
 
 struct Geometry {
-  int64_t n;          // expanded positions
+  int64_t n;  // COO positions
   int64_t bps;
   int64_t rows_per_partition;
 };
@@ -461,11 +659,11 @@ Csr MakeCsr(const scemb_csr_t* csr) {
   return c;
 }
 
-// Lanes per row and vector width for a row of `dim` floats.
+// Lanes per row (>= 4) and vector width for a row of `dim` floats.
 void PickLayout(int64_t dim, bool vec4_ok, int* g, int* vec) {
   *vec = vec4_ok && dim % 4 == 0 ? 4 : 1;
   const int64_t lanes = CeilDiv(dim, *vec);
-  int gg = 1;
+  int gg = 4;
   while (gg < lanes && gg < kWave) gg <<= 1;
   *g = gg;
 }
@@ -474,7 +672,6 @@ bool Aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
-// Carves the sort buffers; returns the sort arena usage through `ws`.
 struct SortBuffers {
   uint32_t* keys;
   uint64_t* pay;
@@ -491,130 +688,228 @@ SortBuffers TakeSortBuffers(Arena& ws, int64_t n) {
   return b;
 }
 
-int ForwardImpl(const scemb_csr_t* csr, const float* table, int64_t table_rows,
-                int32_t dim, float* act, int64_t batch, Arena& ws,
-                uint32_t* status, hipStream_t stream) {
-  Geometry geo;
-  int st = CheckCsr(csr, batch, table_rows, dim, &geo);
-  if (st != 0) return st;
+struct SegBuffers {
+  int64_t num_blocks;
+  float* partials;
+  uint32_t* flags;
+  uint32_t* keys;
+};
+
+SegBuffers TakeSegBuffers(Arena& ws, int64_t n, int64_t dim) {
+  SegBuffers b;
+  b.num_blocks = CeilDiv(n, kBlock);
+  b.partials = ws.Take<float>(2 * b.num_blocks * dim);
+  b.flags = ws.Take<uint32_t>(b.num_blocks);
+  b.keys = ws.Take<uint32_t>(b.num_blocks);
+  return b;
+}
+
+// Launches SegReduce + SegFinish for the layout picked for `dim`.
+template <int SRC, int EPI>
+int LaunchSeg(const StreamArgs& st, RowArgs r, const SegBuffers& sb, int g,
+              int vec, const char* reduce_span, const char* finish_span,
+              hipStream_t stream) {
+  r.partials = sb.partials;
+  r.block_flags = sb.flags;
+  r.block_keys = sb.keys;
+  const dim3 grid(static_cast<uint32_t>(sb.num_blocks));
+#define SCEMB_SEG_CASE(GG, VV)                                                \
+  if (g == GG && vec == VV) {                                                \
+    int prof = ProfileBegin(reduce_span, stream);                            \
+    hipLaunchKernelGGL((SegReduce<GG, VV, SRC, EPI>), grid, dim3(kBlock), 0,  \
+                       stream, st, r);                                        \
+    ProfileEnd(prof, stream);                                                 \
+    SCEMB_LAUNCH_CHECK();                                                     \
+    prof = ProfileBegin(finish_span, stream);                                 \
+    hipLaunchKernelGGL((SegFinish<GG, VV, EPI>), grid, dim3(kBlock), 0,       \
+                       stream, sb.num_blocks, r);                             \
+    ProfileEnd(prof, stream);                                                 \
+    SCEMB_LAUNCH_CHECK();                                                     \
+    return 0;                                                                 \
+  }
+  SCEMB_SEG_CASE(4, 1) SCEMB_SEG_CASE(8, 1) SCEMB_SEG_CASE(16, 1)
+  SCEMB_SEG_CASE(32, 1) SCEMB_SEG_CASE(64, 1) SCEMB_SEG_CASE(4, 4)
+  SCEMB_SEG_CASE(8, 4) SCEMB_SEG_CASE(16, 4) SCEMB_SEG_CASE(32, 4)
+  SCEMB_SEG_CASE(64, 4)
+#undef SCEMB_SEG_CASE
+  return Fail(SCEMB_ERR_INVALID_ARGUMENT, "unsupported layout");
+}
+
+// Sample-major stream of a CSR into (keys, entries): expand + stable sort.
+// The result lands in (b.keys, b.pay) or the alt pair (*in_alt).
+int BuildSampleStream(const scemb_csr_t* csr, const Geometry& geo,
+                      int64_t batch, const SortBuffers& b, Arena& ws,
+                      uint32_t* status, hipStream_t stream, bool* in_alt) {
   const int64_t n = geo.n;
-  SortBuffers b = TakeSortBuffers(ws, n);
-  int32_t* sp = ws.Take<int32_t>(batch + 1);
-  const int key_bits = BitWidth(static_cast<uint64_t>(batch));
-  bool in_alt = false;
-  const bool measuring = ws.measuring();
-  if (!measuring) {
-    if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
-    if (batch == 0) return 0;
-    if (n == 0) {
-      hipLaunchKernelGGL(FillF32, dim3(CeilDiv(batch * dim, 256)), dim3(256),
-                         0, stream, act, batch * dim, 0.0f);
-      SCEMB_LAUNCH_CHECK();
-      return 0;
-    }
+  if (!ws.measuring() && n > 0) {
     hipLaunchKernelGGL(ExpandCsr<true>, dim3(CeilDiv(n, 256)), dim3(256), 0,
                        stream, MakeCsr(csr), geo.bps, geo.rows_per_partition,
                        static_cast<uint32_t>(batch), b.keys, b.pay, status);
     SCEMB_LAUNCH_CHECK();
   }
-  st = RadixSortPairs<uint32_t, uint64_t>(b.keys, b.pay, b.keys_alt, b.pay_alt,
-                                          n, 0, key_bits, ws, stream, &in_alt);
-  if (st != 0) return st;
-  if (measuring) return 0;
+  const int key_bits = BitWidth(static_cast<uint64_t>(batch));
+  return RadixSortPairs<uint32_t, uint64_t>(b.keys, b.pay, b.keys_alt,
+                                            b.pay_alt, n, 0, key_bits, ws,
+                                            stream, in_alt);
+}
+
+int ForwardImpl(const scemb_csr_t* csr, const scemb_sample_view_t* view,
+                const float* table, int64_t table_rows, int32_t dim,
+                float* act, int64_t batch, Arena& ws, uint32_t* status,
+                hipStream_t stream) {
+  StreamArgs st{};
+  st.sentinel = static_cast<uint32_t>(batch);
+  st.src_rows = table_rows;
+  if (view != nullptr) {
+    if (view->size < 0 || (view->size > 0 && (view->keys == nullptr ||
+                                              view->entries == nullptr))) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "bad sample view");
+    }
+    if (view->device_batch_size != batch || view->table_rows != table_rows) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "sample view was built for another batch size or table");
+    }
+    if (dim <= 0 || batch < 0 || batch >= (int64_t{1} << 31) - 1 ||
+        view->size >= (int64_t{1} << 31) - 1) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "bad size");
+    }
+    st.n = view->size;
+    st.keys = view->keys;
+    st.entries = view->entries;
+  } else {
+    Geometry geo;
+    const int rc = CheckCsr(csr, batch, table_rows, dim, &geo);
+    if (rc != 0) return rc;
+    st.n = geo.n;
+    SortBuffers b = TakeSortBuffers(ws, geo.n);
+    bool in_alt = false;
+    if (!ws.measuring() && ws.overflow()) {
+      return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+    }
+    if (ws.measuring() || (geo.n > 0 && batch > 0)) {
+      const int rc2 = BuildSampleStream(csr, geo, batch, b, ws, status,
+                                        stream, &in_alt);
+      if (rc2 != 0) return rc2;
+    }
+    st.keys = in_alt ? b.keys_alt : b.keys;
+    st.entries = in_alt ? b.pay_alt : b.pay;
+  }
+  const SegBuffers sb = TakeSegBuffers(ws, st.n, dim);
+  if (ws.measuring()) return 0;
   if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
-  const uint32_t* keys = in_alt ? b.keys_alt : b.keys;
-  const uint64_t* pay = in_alt ? b.pay_alt : b.pay;
-  hipLaunchKernelGGL(GroupStarts, dim3(CeilDiv(batch + 1, 256)), dim3(256), 0,
-                     stream, keys, n, batch, sp);
-  SCEMB_LAUNCH_CHECK();
+  if (batch == 0) return 0;
+  if (st.n == 0 || table_rows == 0) {
+    hipLaunchKernelGGL(FillF32, dim3(CeilDiv(batch * dim, 256)), dim3(256), 0,
+                       stream, act, batch * dim, 0.0f);
+    SCEMB_LAUNCH_CHECK();
+    return 0;
+  }
+  RowArgs r{};
+  r.src = table;
+  r.dst = act;
+  r.dim = dim;
+  r.batch = batch;
+  r.status = status;
   int g, vec;
   PickLayout(dim, Aligned16(table) && Aligned16(act), &g, &vec);
-  const int64_t threads = batch * g;
-  const dim3 grid(static_cast<uint32_t>(CeilDiv(threads, 256)));
-#define SCEMB_FWD_CASE(GG, VV)                                                 \
-  if (g == GG && vec == VV) {                                                 \
-    const int prof = ProfileBegin("fwd_gather", stream);                      \
-    hipLaunchKernelGGL((FwdGather<GG, VV>), grid, dim3(256), 0, stream, sp,    \
-                       pay, table, static_cast<int64_t>(dim), act, batch);     \
-    ProfileEnd(prof, stream);                                                  \
-    SCEMB_LAUNCH_CHECK();                                                      \
-    return 0;                                                                  \
-  }
-  SCEMB_FWD_CASE(1, 1) SCEMB_FWD_CASE(2, 1) SCEMB_FWD_CASE(4, 1)
-  SCEMB_FWD_CASE(8, 1) SCEMB_FWD_CASE(16, 1) SCEMB_FWD_CASE(32, 1)
-  SCEMB_FWD_CASE(64, 1) SCEMB_FWD_CASE(1, 4) SCEMB_FWD_CASE(2, 4)
-  SCEMB_FWD_CASE(4, 4) SCEMB_FWD_CASE(8, 4) SCEMB_FWD_CASE(16, 4)
-  SCEMB_FWD_CASE(32, 4) SCEMB_FWD_CASE(64, 4)
-#undef SCEMB_FWD_CASE
-  return Fail(SCEMB_ERR_INVALID_ARGUMENT, "unsupported layout");
+  return LaunchSeg<kSrcSorted, kEpiFwd>(st, r, sb, g, vec, "fwd_reduce",
+                                        "fwd_finish", stream);
 }
 
-int64_t BwdChunk(int64_t n) {
-  // Enough waves to fill 256 CUs several times over, pieces of >= 32.
-  int64_t chunk = 64;
-  while (chunk > 32 && CeilDiv(n, chunk) < 256 * 16) chunk >>= 1;
-  return chunk;
-}
-
-template <int OPT>
+template <int EPI>
 int GradImpl(const scemb_csr_t* csr, const float* act_grad, int64_t batch,
              float* table, float* accum, int64_t table_rows, int32_t dim,
              const OptParams& opt, Arena& ws, uint32_t* status,
              hipStream_t stream) {
   Geometry geo;
-  int st = CheckCsr(csr, batch, table_rows, dim, &geo);
-  if (st != 0) return st;
+  int rc = CheckCsr(csr, batch, table_rows, dim, &geo);
+  if (rc != 0) return rc;
   const int64_t n = geo.n;
-  SortBuffers b = TakeSortBuffers(ws, n);
-  const int64_t chunk = BwdChunk(n);
-  const int64_t num_chunks = CeilDiv(n, chunk);
-  uint32_t* counters = ws.Take<uint32_t>(num_chunks);
-  float* partials = ws.Take<float>(2 * num_chunks * static_cast<int64_t>(dim));
-  const int key_bits = BitWidth(static_cast<uint64_t>(table_rows));
-  bool in_alt = false;
-  const bool measuring = ws.measuring();
-  if (!measuring) {
-    if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
-    if (n == 0 || batch == 0) return 0;
-    hipLaunchKernelGGL(ExpandCsr<false>, dim3(CeilDiv(n, 256)), dim3(256), 0,
-                       stream, MakeCsr(csr), geo.bps, geo.rows_per_partition,
-                       static_cast<uint32_t>(table_rows), b.keys, b.pay,
-                       status);
-    SCEMB_LAUNCH_CHECK();
+  const bool direct =
+      (csr->flags & SCEMB_CSR_SORTED_BY_ROW) != 0 && csr->num_segments == 1;
+  StreamArgs st{};
+  st.n = n;
+  if (direct) {
+    st.csr = MakeCsr(csr);
+    st.rows_per_partition = geo.rows_per_partition;
+    st.bps = geo.bps;
+  } else {
+    SortBuffers b = TakeSortBuffers(ws, n);
+    bool in_alt = false;
+    if (!ws.measuring()) {
+      if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+      if (n > 0 && batch > 0) {
+        hipLaunchKernelGGL(ExpandCsr<false>, dim3(CeilDiv(n, 256)), dim3(256),
+                           0, stream, MakeCsr(csr), geo.bps,
+                           geo.rows_per_partition,
+                           static_cast<uint32_t>(table_rows), b.keys, b.pay,
+                           status);
+        SCEMB_LAUNCH_CHECK();
+      }
+    }
+    if (n > 0 && batch > 0) {
+      rc = RadixSortPairs<uint32_t, uint64_t>(
+          b.keys, b.pay, b.keys_alt, b.pay_alt, n, 0,
+          BitWidth(static_cast<uint64_t>(table_rows)), ws, stream, &in_alt);
+      if (rc != 0) return rc;
+    }
+    st.keys = in_alt ? b.keys_alt : b.keys;
+    st.entries = in_alt ? b.pay_alt : b.pay;
+    st.sentinel = static_cast<uint32_t>(table_rows);
+    st.src_rows = batch;
   }
-  st = RadixSortPairs<uint32_t, uint64_t>(b.keys, b.pay, b.keys_alt, b.pay_alt,
-                                          n, 0, key_bits, ws, stream, &in_alt);
-  if (st != 0) return st;
-  if (measuring) return 0;
+  const SegBuffers sb = TakeSegBuffers(ws, n, dim);
+  if (ws.measuring()) return 0;
   if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
-  const uint32_t* keys = in_alt ? b.keys_alt : b.keys;
-  const uint64_t* pay = in_alt ? b.pay_alt : b.pay;
-  hipLaunchKernelGGL(FillU32, dim3(CeilDiv(num_chunks, 256)), dim3(256), 0,
-                     stream, counters, num_chunks, 0u);
-  SCEMB_LAUNCH_CHECK();
+  if (n == 0 || batch == 0) return 0;
+  RowArgs r{};
+  r.src = act_grad;
+  r.dst = table;
+  r.accum = accum;
+  r.dim = dim;
+  r.batch = batch;
+  r.opt = opt;
+  r.status = status;
   int g, vec;
   PickLayout(dim, Aligned16(table) && Aligned16(act_grad) &&
-                      (OPT == 0 || Aligned16(accum)), &g, &vec);
-  const dim3 grid(static_cast<uint32_t>(CeilDiv(num_chunks * kWave, 256)));
-#define SCEMB_BWD_CASE(GG, VV)                                                \
-  if (g == GG && vec == VV) {                                                \
-    const int prof = ProfileBegin("bwd_update", stream);                     \
-    hipLaunchKernelGGL((BwdFused<GG, VV, OPT>), grid, dim3(256), 0, stream,  \
-                       keys, pay, n, chunk, num_chunks, act_grad,             \
-                       static_cast<int64_t>(dim), table, accum,               \
-                       static_cast<uint32_t>(table_rows), opt, partials,      \
-                       counters);                                             \
-    ProfileEnd(prof, stream);                                                 \
-    SCEMB_LAUNCH_CHECK();                                                     \
-    return 0;                                                                 \
+                      (EPI != kEpiAdagrad || Aligned16(accum)), &g, &vec);
+  if (direct) {
+    return LaunchSeg<kSrcCsr, EPI>(st, r, sb, g, vec, "bwd_reduce",
+                                   "bwd_finish", stream);
   }
-  SCEMB_BWD_CASE(1, 1) SCEMB_BWD_CASE(2, 1) SCEMB_BWD_CASE(4, 1)
-  SCEMB_BWD_CASE(8, 1) SCEMB_BWD_CASE(16, 1) SCEMB_BWD_CASE(32, 1)
-  SCEMB_BWD_CASE(64, 1) SCEMB_BWD_CASE(1, 4) SCEMB_BWD_CASE(2, 4)
-  SCEMB_BWD_CASE(4, 4) SCEMB_BWD_CASE(8, 4) SCEMB_BWD_CASE(16, 4)
-  SCEMB_BWD_CASE(32, 4) SCEMB_BWD_CASE(64, 4)
-#undef SCEMB_BWD_CASE
-  return Fail(SCEMB_ERR_INVALID_ARGUMENT, "unsupported layout");
+  return LaunchSeg<kSrcSorted, EPI>(st, r, sb, g, vec, "bwd_reduce",
+                                    "bwd_finish", stream);
+}
+
+int BuildViewImpl(const scemb_csr_t* csr, int64_t batch, int64_t table_rows,
+                  uint32_t* keys, uint64_t* entries, Arena& ws,
+                  uint32_t* status, hipStream_t stream) {
+  Geometry geo;
+  const int rc = CheckCsr(csr, batch, table_rows, 1, &geo);
+  if (rc != 0) return rc;
+  SortBuffers b;
+  b.keys = keys;
+  b.pay = entries;
+  b.keys_alt = ws.Take<uint32_t>(geo.n);
+  b.pay_alt = ws.Take<uint64_t>(geo.n);
+  if (!ws.measuring()) {
+    if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+    if (geo.n > 0 && (keys == nullptr || entries == nullptr)) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null view buffer");
+    }
+  }
+  bool in_alt = false;
+  const int rc2 = BuildSampleStream(csr, geo, batch, b, ws, status, stream,
+                                    &in_alt);
+  if (rc2 != 0 || ws.measuring()) return rc2;
+  if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+  if (in_alt && geo.n > 0) {
+    SCEMB_HIP(hipMemcpyAsync(keys, b.keys_alt, geo.n * sizeof(uint32_t),
+                             hipMemcpyDeviceToDevice, stream));
+    SCEMB_HIP(hipMemcpyAsync(entries, b.pay_alt, geo.n * sizeof(uint64_t),
+                             hipMemcpyDeviceToDevice, stream));
+  }
+  return 0;
 }
 
 }  // namespace
@@ -624,23 +919,24 @@ using namespace scemb;
 
 extern "C" {
 
-size_t scemb_sparse_dense_matmul_workspace_size(const scemb_csr_t* csr,
-                                                int64_t device_batch_size,
-                                                int64_t table_rows,
-                                                int32_t dim) {
+size_t scemb_sparse_dense_matmul_workspace_size(
+    const scemb_csr_t* csr, const scemb_sample_view_t* view,
+    int64_t device_batch_size, int64_t table_rows, int32_t dim) {
   Arena ws(nullptr, 0);
-  if (ForwardImpl(csr, nullptr, table_rows, dim, nullptr, device_batch_size,
-                  ws, nullptr, nullptr) != 0) {
+  if (ForwardImpl(csr, view, nullptr, table_rows, dim, nullptr,
+                  device_batch_size, ws, nullptr, nullptr) != 0) {
     return 0;
   }
   return ws.used() + 256;
 }
 
-int scemb_sparse_dense_matmul(const scemb_csr_t* csr, const float* table,
-                              int64_t table_rows, int32_t dim,
-                              float* activations, int64_t device_batch_size,
-                              void* workspace, size_t workspace_bytes,
-                              uint32_t* device_status, void* stream) {
+int scemb_sparse_dense_matmul(const scemb_csr_t* csr,
+                              const scemb_sample_view_t* view,
+                              const float* table, int64_t table_rows,
+                              int32_t dim, float* activations,
+                              int64_t device_batch_size, void* workspace,
+                              size_t workspace_bytes, uint32_t* device_status,
+                              void* stream) {
   if (workspace == nullptr) return Fail(SCEMB_ERR_WORKSPACE, "no workspace");
   if (table == nullptr || activations == nullptr) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null table or activations");
@@ -648,10 +944,32 @@ int scemb_sparse_dense_matmul(const scemb_csr_t* csr, const float* table,
   Arena ws(workspace, workspace_bytes);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int prof = ProfileBegin("fwd_call", s);
-  const int rc = ForwardImpl(csr, table, table_rows, dim, activations,
+  const int rc = ForwardImpl(csr, view, table, table_rows, dim, activations,
                              device_batch_size, ws, device_status, s);
   ProfileEnd(prof, s);
   return rc;
+}
+
+size_t scemb_build_sample_view_workspace_size(const scemb_csr_t* csr,
+                                              int64_t device_batch_size,
+                                              int64_t table_rows) {
+  Arena ws(nullptr, 0);
+  if (BuildViewImpl(csr, device_batch_size, table_rows, nullptr, nullptr, ws,
+                    nullptr, nullptr) != 0) {
+    return 0;
+  }
+  return ws.used() + 256;
+}
+
+int scemb_build_sample_view(const scemb_csr_t* csr, int64_t device_batch_size,
+                            int64_t table_rows, uint32_t* keys,
+                            uint64_t* entries, void* workspace,
+                            size_t workspace_bytes, uint32_t* device_status,
+                            void* stream) {
+  if (workspace == nullptr) return Fail(SCEMB_ERR_WORKSPACE, "no workspace");
+  Arena ws(workspace, workspace_bytes);
+  return BuildViewImpl(csr, device_batch_size, table_rows, keys, entries, ws,
+                       device_status, static_cast<hipStream_t>(stream));
 }
 
 size_t scemb_sparse_dense_matmul_grad_workspace_size(const scemb_csr_t* csr,
@@ -660,8 +978,8 @@ size_t scemb_sparse_dense_matmul_grad_workspace_size(const scemb_csr_t* csr,
                                                      int32_t dim) {
   Arena ws(nullptr, 0);
   OptParams o{nullptr, 0.f, 0, 0.f, 0.f};
-  if (GradImpl<0>(csr, nullptr, device_batch_size, nullptr, nullptr,
-                  table_rows, dim, o, ws, nullptr, nullptr) != 0) {
+  if (GradImpl<kEpiSgd>(csr, nullptr, device_batch_size, nullptr, nullptr,
+                        table_rows, dim, o, ws, nullptr, nullptr) != 0) {
     return 0;
   }
   return ws.used() + 256;
@@ -686,8 +1004,9 @@ int scemb_sparse_dense_matmul_grad_with_sgd(
               max_value};
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int prof = ProfileBegin("bwd_call", s);
-  const int rc = GradImpl<0>(csr, activations_grad, device_batch_size, table,
-                             nullptr, table_rows, dim, o, ws, device_status, s);
+  const int rc = GradImpl<kEpiSgd>(csr, activations_grad, device_batch_size,
+                                   table, nullptr, table_rows, dim, o, ws,
+                                   device_status, s);
   ProfileEnd(prof, s);
   return rc;
 }
@@ -714,9 +1033,10 @@ int scemb_sparse_dense_matmul_grad_with_adagrad(
               max_value};
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int prof = ProfileBegin("bwd_call", s);
-  const int rc = GradImpl<1>(csr, activations_grad, device_batch_size, table,
-                             accumulator, table_rows, dim, o, ws,
-                             device_status, s);
+  const int rc = GradImpl<kEpiAdagrad>(csr, activations_grad,
+                                       device_batch_size, table, accumulator,
+                                       table_rows, dim, o, ws, device_status,
+                                       s);
   ProfileEnd(prof, s);
   return rc;
 }

@@ -28,6 +28,9 @@ SCEMB_ERR_LIMIT_EXCEEDED = 5
 
 STATUS_BAD_ENTRY = 1
 STATUS_BAD_ID = 2
+STATUS_UNSORTED = 4
+
+CSR_SORTED_BY_ROW = 1
 
 # Every function declared in include/scemb.h.
 EXPORTED_SYMBOLS = (
@@ -35,6 +38,8 @@ EXPORTED_SYMBOLS = (
     "scemb_version",
     "scemb_sparse_dense_matmul_workspace_size",
     "scemb_sparse_dense_matmul",
+    "scemb_build_sample_view_workspace_size",
+    "scemb_build_sample_view",
     "scemb_sparse_dense_matmul_grad_workspace_size",
     "scemb_sparse_dense_matmul_grad_with_sgd",
     "scemb_sparse_dense_matmul_grad_with_adagrad",
@@ -60,7 +65,17 @@ class Csr(ctypes.Structure):
       ("num_segments", ctypes.c_int32),
       ("num_partitions", ctypes.c_int32),
       ("row_pointers_per_segment", ctypes.c_int32),
-      ("reserved", ctypes.c_int32),
+      ("flags", ctypes.c_uint32),
+  ]
+
+
+class SampleView(ctypes.Structure):
+  _fields_ = [
+      ("keys", ctypes.c_void_p),
+      ("entries", ctypes.c_void_p),
+      ("size", ctypes.c_int64),
+      ("device_batch_size", ctypes.c_int64),
+      ("table_rows", ctypes.c_int64),
   ]
 
 
@@ -123,16 +138,22 @@ def load_library() -> ctypes.CDLL:
     vp, i32, i64, f32, sz = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
                              ctypes.c_float, ctypes.c_size_t)
     csr_p = ctypes.POINTER(Csr)
+    view_p = ctypes.POINTER(SampleView)
     lib.scemb_last_error.restype = ctypes.c_char_p
     lib.scemb_last_error.argtypes = []
     lib.scemb_version.restype = ctypes.c_int
     lib.scemb_version.argtypes = []
     lib.scemb_sparse_dense_matmul_workspace_size.restype = sz
-    lib.scemb_sparse_dense_matmul_workspace_size.argtypes = [csr_p, i64, i64,
-                                                             i32]
+    lib.scemb_sparse_dense_matmul_workspace_size.argtypes = [
+        csr_p, view_p, i64, i64, i32]
     lib.scemb_sparse_dense_matmul.restype = ctypes.c_int
-    lib.scemb_sparse_dense_matmul.argtypes = [csr_p, vp, i64, i32, vp, i64, vp,
-                                              sz, vp, vp]
+    lib.scemb_sparse_dense_matmul.argtypes = [csr_p, view_p, vp, i64, i32, vp,
+                                              i64, vp, sz, vp, vp]
+    lib.scemb_build_sample_view_workspace_size.restype = sz
+    lib.scemb_build_sample_view_workspace_size.argtypes = [csr_p, i64, i64]
+    lib.scemb_build_sample_view.restype = ctypes.c_int
+    lib.scemb_build_sample_view.argtypes = [csr_p, i64, i64, vp, vp, vp, sz,
+                                            vp, vp]
     lib.scemb_sparse_dense_matmul_grad_workspace_size.restype = sz
     lib.scemb_sparse_dense_matmul_grad_workspace_size.argtypes = [
         csr_p, i64, i64, i32]
@@ -271,28 +292,69 @@ WORKSPACE = _Workspace()
 
 
 def make_csr(row_pointers, embedding_ids, sample_ids, gains, num_segments,
-             num_partitions) -> Csr:
+             num_partitions, sorted_by_row: bool = False) -> Csr:
   rp_len = int(row_pointers.numel())
   if rp_len % num_segments:
     raise ValueError("row_pointers length must be divisible by "
                      "num_sc_per_device")
   return Csr(ptr(row_pointers), ptr(embedding_ids), ptr(sample_ids),
              ptr(gains), int(embedding_ids.numel()), num_segments,
-             num_partitions, rp_len // num_segments, 0)
+             num_partitions, rp_len // num_segments,
+             CSR_SORTED_BY_ROW if sorted_by_row else 0)
 
 
-def sparse_dense_matmul(csr: Csr, table, activations, batch: int,
+class LookupView:
+  """Device buffers of a sample view (scemb_sample_view_t) plus the
+  (device_batch_size, table_rows) pair it was built for."""
+
+  def __init__(self, keys, entries, device_batch_size: int, table_rows: int):
+    self.keys = keys          # int32 tensor holding the uint32 keys
+    self.entries = entries    # int64 tensor holding the packed entries
+    self.device_batch_size = int(device_batch_size)
+    self.table_rows = int(table_rows)
+
+  def as_struct(self) -> SampleView:
+    return SampleView(ptr(self.keys), ptr(self.entries),
+                      int(self.keys.numel()), self.device_batch_size,
+                      self.table_rows)
+
+
+def build_sample_view(csr: Csr, batch: int, table_rows: int,
+                      device_status=None) -> LookupView:
+  """Groups a CSR's entries by activation row (enqueued on the current
+  stream; the CSR tensors must stay alive until it has run)."""
+  t = require_gpu()
+  lib = load_library()
+  need = lib.scemb_build_sample_view_workspace_size(ctypes.byref(csr), batch,
+                                                    table_rows)
+  if need == 0:
+    check(SCEMB_ERR_INVALID_ARGUMENT)
+  n = int(csr.coo_size) // int(csr.num_segments) * int(csr.num_segments)
+  keys = t.empty(n, dtype=t.int32, device=device())
+  entries = t.empty(n, dtype=t.int64, device=device())
+  ws = WORKSPACE.get(need)
+  check(lib.scemb_build_sample_view(
+      ctypes.byref(csr), batch, table_rows, ptr(keys), ptr(entries), ptr(ws),
+      ws.numel(), ptr(device_status), stream_handle()))
+  return LookupView(keys, entries, batch, table_rows)
+
+
+def sparse_dense_matmul(csr: Csr | None, table, activations, batch: int,
+                        view: LookupView | None = None,
                         device_status=None) -> None:
   lib = load_library()
   rows = int(table.shape[0])
   dim = 1 if table.dim() == 1 else int(table.shape[1])
-  need = lib.scemb_sparse_dense_matmul_workspace_size(ctypes.byref(csr), batch,
+  vs = view.as_struct() if view is not None else None
+  csr_ref = ctypes.byref(csr) if csr is not None else None
+  vs_ref = ctypes.byref(vs) if vs is not None else None
+  need = lib.scemb_sparse_dense_matmul_workspace_size(csr_ref, vs_ref, batch,
                                                       rows, dim)
   if need == 0:
     check(SCEMB_ERR_INVALID_ARGUMENT)
   ws = WORKSPACE.get(need)
   check(lib.scemb_sparse_dense_matmul(
-      ctypes.byref(csr), ptr(table), rows, dim, ptr(activations), batch,
+      csr_ref, vs_ref, ptr(table), rows, dim, ptr(activations), batch,
       ptr(ws), ws.numel(), ptr(device_status), stream_handle()))
 
 

@@ -9,7 +9,10 @@ validates like the abstract eval and runs ``scemb_sparse_dense_matmul``
 
 Extra keyword arguments (no reference counterpart; the TPU op reads them from
 the hardware): ``num_sc_per_device`` and ``global_device_count`` give the CSR
-segment / partition counts (defaults: the device's SparseCore count, 1).
+segment / partition counts (defaults: the device's SparseCore count, 1);
+``lookup_view`` is an optional ``_native.LookupView`` of the same CSR (built
+by the preprocessing), which spares the call its grouping sort. A view built
+for another batch size or table height is ignored.
 """
 
 from __future__ import annotations
@@ -48,7 +51,7 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
           max_ids_per_partition: int, max_unique_ids_per_partition: int,
           sharding_strategy: int = 1, quantization_config=None,
           enable_minibatching: bool = False, num_sc_per_device=None,
-          global_device_count=None):
+          global_device_count=None, lookup_view=None):
   utils.validate_abstract_eval_params(
       lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
       lhs_gains, num_minibatches_per_physical_sparse_core, embedding_table,
@@ -70,7 +73,12 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
   shape = ((device_batch_size,) if table.dim() == 1 else
            (device_batch_size, int(table.shape[1])))
   out = t.empty(shape, dtype=t.float32, device=table.device)
-  _native.sparse_dense_matmul(csr, table, out, int(device_batch_size))
+  if lookup_view is not None and (
+      lookup_view.device_batch_size != int(device_batch_size) or
+      lookup_view.table_rows != int(table.shape[0])):
+    lookup_view = None
+  _native.sparse_dense_matmul(csr, table, out, int(device_batch_size),
+                              view=lookup_view)
   del keep
   return out
 

@@ -8,6 +8,12 @@ clipping of the table, ``:167-233``). ``bind`` runs
 ``scemb_sparse_dense_matmul_grad_with_adagrad`` on the current stream and
 returns ``(table, accumulator)``, updated in place when they are float32 CUDA
 tensors.
+
+Extra keyword arguments besides ``num_sc_per_device`` /
+``global_device_count``: ``csr_sorted_by_row`` declares the CSR as the
+preprocessing writes it (entries ascending by partition and embedding id);
+with one SparseCore segment the kernel then reads it in place instead of
+sorting a copy (a violated order is reported, not silently used).
 """
 
 from __future__ import annotations
@@ -27,7 +33,7 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
           computation_name: str = "adagrad_optimizer_update",
           sharding_strategy: int = 1, enable_minibatching: bool = False,
           min_value=None, max_value=None, num_sc_per_device=None,
-          global_device_count=None):
+          global_device_count=None, csr_sorted_by_row: bool = False):
   utils.validate_abstract_eval_params(
       lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
       lhs_gains, num_minibatches_per_physical_sparse_core, embedding_table,
@@ -46,7 +52,8 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
   t = _native.require_gpu()
   s, ns = _device.resolve_sparsecores(num_sc_per_device, global_device_count)
   keep, csr = _device.csr_operands(lhs_row_pointers, lhs_local_embedding_ids,
-                                   lhs_local_sample_ids, lhs_gains, s, ns)
+                                   lhs_local_sample_ids, lhs_gains, s, ns,
+                                   sorted_by_row=csr_sorted_by_row)
   table = _device.device_table(embedding_table)
   acc = _device.device_table(accumulator)
   grad = _native.as_device_tensor(activations_grad, t.float32, table.device)

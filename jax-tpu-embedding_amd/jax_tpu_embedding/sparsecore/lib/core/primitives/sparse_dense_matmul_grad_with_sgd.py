@@ -10,6 +10,12 @@ clipping, ``primitives/utils.py:24-59``). ``bind`` runs
 The table is updated in place when it is already a float32 CUDA tensor (the
 returned tensor is that same tensor, the equivalent of donating the buffer);
 other inputs are copied to the GPU first and the copy is returned.
+
+Extra keyword arguments besides ``num_sc_per_device`` /
+``global_device_count``: ``csr_sorted_by_row`` declares the CSR as the
+preprocessing writes it (entries ascending by partition and embedding id);
+with one SparseCore segment the kernel then reads it in place instead of
+sorting a copy (a violated order is reported, not silently used).
 """
 
 from __future__ import annotations
@@ -29,7 +35,7 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
           computation_name: str = "sgd_optimizer_update",
           sharding_strategy: int = 1, enable_minibatching: bool = False,
           min_value=None, max_value=None, num_sc_per_device=None,
-          global_device_count=None):
+          global_device_count=None, csr_sorted_by_row: bool = False):
   utils.ensure_dtype(learning_rate, np.float32, "learning_rate")
   utils.validate_abstract_eval_params(
       lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
@@ -43,7 +49,8 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
   t = _native.require_gpu()
   s, ns = _device.resolve_sparsecores(num_sc_per_device, global_device_count)
   keep, csr = _device.csr_operands(lhs_row_pointers, lhs_local_embedding_ids,
-                                   lhs_local_sample_ids, lhs_gains, s, ns)
+                                   lhs_local_sample_ids, lhs_gains, s, ns,
+                                   sorted_by_row=csr_sorted_by_row)
   table = _device.device_table(embedding_table)
   grad = _native.as_device_tensor(activations_grad, t.float32, table.device)
   _native.sparse_dense_matmul_grad(csr, grad, table, None, learning_rate,

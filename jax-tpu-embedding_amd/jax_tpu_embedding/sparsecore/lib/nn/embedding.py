@@ -23,6 +23,7 @@ import numpy as np
 from jax_tpu_embedding.sparsecore import _native
 from jax_tpu_embedding.sparsecore import _tree
 from jax_tpu_embedding.sparsecore.lib.core import pybind_input_preprocessing
+from jax_tpu_embedding.sparsecore.lib.core.primitives import _device
 from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_csr
 from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec
 from jax_tpu_embedding.sparsecore.lib.nn import table_stacking
@@ -92,11 +93,23 @@ class SparseDenseMatmulInputStats:
 
 @dataclasses.dataclass
 class PreprocessedInput:
-  """Result of preprocessing: the CSR buffers and the minibatch count."""
+  """Result of preprocessing: the CSR buffers and the minibatch count.
+
+  Two optional fields have no reference counterpart; the GPU preprocessing
+  fills them and the lookup uses them when present:
+    lookup_views: stack name -> _native.LookupView, the CSR entries grouped
+      by activation row (spares the forward pass its grouping sort);
+    csr_sorted_by_row: the CSR entries are ascending by (partition, embedding
+      id) in every segment, as the preprocessing writes them (lets the
+      backward pass read the CSR in place).
+  A PreprocessedInput built from other CSR buffers leaves both unset.
+  """
 
   sparse_dense_matmul_input: SparseDenseMatmulInput
   num_minibatches: object = dataclasses.field(
       default_factory=lambda: np.array(1))
+  lookup_views: dict | None = None
+  csr_sorted_by_row: bool = False
 
   @property
   def lhs_row_pointers(self):
@@ -290,8 +303,30 @@ def preprocess_sparse_dense_matmul_input(
   minibatches = np.full(local_device_count, num_minibatches, dtype=np.int32)
   if has_leading_dimension:
     minibatches = minibatches.reshape(local_device_count, 1)
-  return (PreprocessedInput(SparseDenseMatmulInput(*csr), minibatches),
+  views = None
+  if local_device_count == 1:
+    views = _build_lookup_views(csr, feature_specs, global_device_count,
+                                num_sc_per_device)
+  return (PreprocessedInput(SparseDenseMatmulInput(*csr), minibatches,
+                            lookup_views=views,
+                            csr_sorted_by_row=local_device_count == 1),
           SparseDenseMatmulInputStats.from_cc(stats))
+
+
+def _build_lookup_views(csr, feature_specs, global_device_count: int,
+                        num_sc_per_device: int):
+  """Sample views of one device's CSR buffers, one per stacked table, for a
+  table shard of stack_vocab_size / global_device_count rows."""
+  rp, eid, sid, gains = csr
+  views = {}
+  for name, spec in get_stacked_table_specs(feature_specs).items():
+    batch = spec.total_sample_count // global_device_count
+    rows = spec.stack_vocab_size // global_device_count
+    _, c = _device.csr_operands(rp[name], eid[name], sid[name], gains[name],
+                                num_sc_per_device,
+                                num_sc_per_device * global_device_count)
+    views[name] = _native.build_sample_view(c, batch, rows)
+  return views
 
 
 # ---------------------------------------------------------------------------
@@ -356,6 +391,7 @@ def tpu_sparse_dense_matmul(preprocessed_inputs, embedding_variables,
   assert rp.keys() == stacked.keys()
   strategy = int(sharding_strategy_to_enum(sharding_strategy))
   nmb = _resolve_scalar_minibatches(preprocessed_inputs.num_minibatches)
+  views = getattr(preprocessed_inputs, "lookup_views", None) or {}
   acts = {}
   for name, spec in stacked.items():
     ev = embedding_variables[name]
@@ -374,7 +410,8 @@ def tpu_sparse_dense_matmul(preprocessed_inputs, embedding_variables,
                             if spec.quantization_config else None),
                         enable_minibatching=enable_minibatching,
                         num_sc_per_device=num_sc_per_device,
-                        global_device_count=global_device_count))
+                        global_device_count=global_device_count,
+                        lookup_view=views.get(name)))
   if perform_unstacking:
     acts = unstack_embedding_activations(acts, feature_specs,
                                          global_device_count,
@@ -489,6 +526,8 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
         computation_name=symbol, sharding_strategy=strategy,
         enable_minibatching=enable_minibatching,
         num_sc_per_device=num_sc_per_device, global_device_count=g_count,
+        csr_sorted_by_row=bool(
+            getattr(preprocessed_inputs, "csr_sorted_by_row", False)),
         **kwargs)
     res = res if isinstance(res, tuple) else (res,)
     out[name] = EmbeddingVariables(res[0], tuple(res[1:]))

@@ -34,6 +34,8 @@ from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-i
 from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top,wrong-import-position
 from jax_tpu_embedding.sparsecore.lib.nn import table_stacking  # pylint: disable=g-import-not-at-top,wrong-import-position
 from oracle import refcpu  # pylint: disable=g-import-not-at-top,wrong-import-position
+from jax_tpu_embedding.sparsecore import _native  # pylint: disable=g-import-not-at-top,wrong-import-position
+from jax_tpu_embedding.sparsecore.lib.core.primitives import _device  # pylint: disable=g-import-not-at-top,wrong-import-position
 
 
 def _zipf(rng, a, vocab, size):
@@ -201,41 +203,122 @@ def _csr_from_oracle(features, weights, feats, num_sc):
   return name, ref
 
 
-@pytest.mark.parametrize("dim", [1, 8, 12, 64, 128, 256, 320])
+def _fwd_bind(ref, name, table_t, batch, num_sc, view=None):
+  return fwd_prim.tpu_sparse_dense_matmul_csr_primitive.bind(
+      ref.row_pointers[name], ref.embedding_ids[name], ref.sample_ids[name],
+      ref.gains[name], 1, table_t, device_batch_size=batch,
+      max_ids_per_partition=1 << 20, max_unique_ids_per_partition=1 << 20,
+      num_sc_per_device=num_sc, lookup_view=view)
+
+
+def _view(ref, name, batch, rows, num_sc):
+  keep, c = _device.csr_operands(ref.row_pointers[name],
+                                 ref.embedding_ids[name], ref.sample_ids[name],
+                                 ref.gains[name], num_sc, num_sc)
+  v = _native.build_sample_view(c, batch, rows)
+  torch.cuda.synchronize()
+  del keep
+  return v
+
+
+@pytest.mark.parametrize("dim", [1, 3, 8, 12, 64, 128, 256, 320, 520])
 @pytest.mark.parametrize("num_sc", [1, 4])
-def test_forward_matches_oracle(dim, num_sc):
-  rng = np.random.default_rng(dim * 7 + num_sc)
+@pytest.mark.parametrize("integer", [False, True])
+def test_forward_matches_oracle(dim, num_sc, integer):
+  """Forward through the CSR (grouping sort inside the call) and through a
+  prebuilt sample view. Integer-valued tables with the sum combiner make
+  every partial sum exact, so those results must agree bit for bit; float
+  tables with the mean combiner are held to rtol 1e-5 / atol 1e-6."""
+  rng = np.random.default_rng(dim * 7 + num_sc + (100 if integer else 0))
   batch = 96
   vocab = 2000
-  _, feats = _make_specs(1, [vocab], [dim], "mean",
+  _, feats = _make_specs(1, [vocab], [dim], "sum" if integer else "mean",
                          embedding_spec.SGDOptimizerSpec(0.01), batch)
   embedding.prepare_feature_specs_for_training(feats, 1, num_sc)
   features = [_ragged(rng, batch, 0, 40, vocab, zipf_a=1.1)]
   name, ref = _csr_from_oracle(features, None, feats, num_sc)
   rows = feats[0].table_spec.stacked_table_spec.stack_vocab_size
-  table = rng.normal(0, 0.01, size=(rows, dim)).astype(np.float32)
+  if integer:
+    table = rng.integers(-8, 9, size=(rows, dim)).astype(np.float32)
+  else:
+    table = rng.normal(0, 0.01, size=(rows, dim)).astype(np.float32)
   if dim == 1:
     table = table.reshape(rows)
-  act = fwd_prim.tpu_sparse_dense_matmul_csr_primitive.bind(
-      ref.row_pointers[name], ref.embedding_ids[name], ref.sample_ids[name],
-      ref.gains[name], 1, torch.from_numpy(table).cuda(),
-      device_batch_size=batch, max_ids_per_partition=1 << 20,
-      max_unique_ids_per_partition=1 << 20, num_sc_per_device=num_sc)
+  table_t = torch.from_numpy(table).cuda()
+  act = _fwd_bind(ref, name, table_t, batch, num_sc).cpu().numpy()
+  act_v = _fwd_bind(ref, name, table_t, batch, num_sc,
+                    view=_view(ref, name, batch, rows, num_sc)).cpu().numpy()
   exp = refcpu.sparse_dense_matmul(
       ref.row_pointers[name], ref.embedding_ids[name], ref.sample_ids[name],
       ref.gains[name], table, batch, num_sc_per_device=num_sc, num_scs=num_sc)
-  # Sums run in CSR order on both sides: the results agree bit for bit.
-  np.testing.assert_array_equal(act.cpu().numpy(), exp)
+  # Both routes feed the same kernel the same stream: identical bits.
+  np.testing.assert_array_equal(act, act_v)
+  if integer:
+    np.testing.assert_array_equal(act, exp)
+  else:
+    np.testing.assert_allclose(act, exp, rtol=RTOL, atol=ATOL)
 
 
-def _run_grad(optimizer, csr, grad, table0, acc0, lr, lo, hi, num_sc):
-  """Runs the GPU primitive and the oracle; returns (got, expected) pairs."""
+@pytest.mark.parametrize("dim", [4, 128, 300])
+def test_forward_long_rows_and_empty_rows(dim):
+  """Activation rows of up to 3000 entries span many 256-entry blocks (the
+  cross-block partial path); every third row, the first rows and the last
+  rows have no entries and must come out zero."""
+  rng = np.random.default_rng(dim)
+  batch = 64
+  vocab = 500
+  _, feats = _make_specs(1, [vocab], [dim], "sum",
+                         embedding_spec.SGDOptimizerSpec(0.01), batch,
+                         max_ids=1 << 16)
+  embedding.prepare_feature_specs_for_training(feats, 1, 1)
+  arr = np.empty(batch, dtype=object)
+  for i in range(batch):
+    n = 0 if (i % 3 == 0 or i < 2 or i >= batch - 3) else int(
+        rng.integers(1, 3000))
+    arr[i] = rng.integers(0, vocab, size=n).astype(np.int32)
+  name, ref = _csr_from_oracle([arr], None, feats, 1)
+  rows = feats[0].table_spec.stacked_table_spec.stack_vocab_size
+  table = rng.integers(-4, 5, size=(rows, dim)).astype(np.float32)
+  table_t = torch.from_numpy(table).cuda()
+  exp = refcpu.sparse_dense_matmul(
+      ref.row_pointers[name], ref.embedding_ids[name], ref.sample_ids[name],
+      ref.gains[name], table, batch, num_sc_per_device=1, num_scs=1)
+  for view in (None, _view(ref, name, batch, rows, 1)):
+    # Poison the output allocation first: empty rows must be written.
+    junk = torch.full((batch, dim), float("nan"), device="cuda")
+    del junk
+    act = _fwd_bind(ref, name, table_t, batch, 1, view=view).cpu().numpy()
+    np.testing.assert_array_equal(act, exp)
+    assert not act[0].any() and not act[-1].any()
+
+
+def test_forward_empty_batch_is_zero():
+  rng = np.random.default_rng(2)
+  batch = 40
+  _, feats = _make_specs(1, [100], [16], "sum",
+                         embedding_spec.SGDOptimizerSpec(0.01), batch)
+  embedding.prepare_feature_specs_for_training(feats, 1, 1)
+  arr = np.empty(batch, dtype=object)
+  for i in range(batch):
+    arr[i] = np.zeros(0, np.int32)
+  name, ref = _csr_from_oracle([arr], None, feats, 1)
+  rows = feats[0].table_spec.stacked_table_spec.stack_vocab_size
+  table = torch.from_numpy(rng.normal(size=(rows, 16)).astype(np.float32))
+  act = _fwd_bind(ref, name, table.cuda(), batch, 1).cpu().numpy()
+  assert act.shape == (batch, 16) and not act.any()
+
+
+def _run_grad(optimizer, csr, grad, table0, acc0, lr, lo, hi, num_sc,
+              sorted_by_row=False):
+  """Runs the GPU primitive and the oracle; returns (got, expected) pairs.
+  `sorted_by_row` lets the kernel read the CSR in place (one segment)."""
   table = torch.from_numpy(table0.copy()).cuda()
   if optimizer == "sgd":
     out = sgd_prim.tpu_sparse_dense_matmul_grad_with_sgd_primitive.bind(
         *csr, 1, table, torch.from_numpy(grad).cuda(), lr,
         max_ids_per_partition=1 << 20, max_unique_ids_per_partition=1 << 20,
-        min_value=lo, max_value=hi, num_sc_per_device=num_sc)
+        min_value=lo, max_value=hi, num_sc_per_device=num_sc,
+        csr_sorted_by_row=sorted_by_row)
     assert out is table
     exp_t = refcpu.sparse_dense_matmul_grad(
         *csr, grad, table0, None, learning_rate=lr,
@@ -246,7 +329,8 @@ def _run_grad(optimizer, csr, grad, table0, acc0, lr, lo, hi, num_sc):
       adagrad_prim.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
           *csr, 1, table, acc, torch.from_numpy(grad).cuda(), np.float32(lr),
           max_ids_per_partition=1 << 20, max_unique_ids_per_partition=1 << 20,
-          min_value=lo, max_value=hi, num_sc_per_device=num_sc))
+          min_value=lo, max_value=hi, num_sc_per_device=num_sc,
+          csr_sorted_by_row=sorted_by_row))
   assert out_t is table and out_a is acc
   exp_t, exp_a = refcpu.sparse_dense_matmul_grad(
       *csr, grad, table0, acc0, learning_rate=lr, num_sc_per_device=num_sc,
@@ -256,13 +340,16 @@ def _run_grad(optimizer, csr, grad, table0, acc0, lr, lo, hi, num_sc):
 
 @pytest.mark.parametrize("optimizer", ["sgd", "adagrad"])
 @pytest.mark.parametrize("dim", [1, 8, 24, 128, 256, 300])
-@pytest.mark.parametrize("num_sc", [1, 2])
+@pytest.mark.parametrize("num_sc,sorted_by_row", [(1, False), (1, True),
+                                                  (2, False), (2, True)])
 @pytest.mark.parametrize("clip", [False, True])
-def test_grad_hot_rows_exact(optimizer, dim, num_sc, clip):
-  """Long runs of hot rows (Zipf 1.05 over 300 rows) cross the backward's
-  chunk boundaries and use the multi-piece reduction. Integer-valued
-  gradients with unit gains make every partial sum exact, so the result may
-  not depend on summation order: GPU and oracle must agree bit for bit."""
+def test_grad_hot_rows_exact(optimizer, dim, num_sc, sorted_by_row, clip):
+  """Long runs of hot rows (Zipf 1.05 over 300 rows) cross block boundaries
+  and use the cross-block reduction. Integer-valued gradients with unit
+  gains make every partial sum exact, so the result may not depend on
+  summation order: GPU and oracle must agree bit for bit. With one segment
+  and sorted_by_row the kernel reads the CSR in place (with two segments the
+  flag must be ignored and the entries sorted)."""
   rng = np.random.default_rng(dim * 13 + num_sc + (7 if clip else 0))
   batch = 4096 if dim <= 128 else 512
   vocab = 300
@@ -281,7 +368,7 @@ def test_grad_hot_rows_exact(optimizer, dim, num_sc, clip):
   csr = (ref.row_pointers[name], ref.embedding_ids[name],
          ref.sample_ids[name], ref.gains[name])
   for got, exp in _run_grad(optimizer, csr, grad, table0, acc0, 0.05, lo, hi,
-                            num_sc):
+                            num_sc, sorted_by_row):
     np.testing.assert_array_equal(got, exp)
 
 
@@ -308,8 +395,97 @@ def test_grad_float_matches_oracle(optimizer, combiner, dim, num_sc):
   csr = (ref.row_pointers[name], ref.embedding_ids[name],
          ref.sample_ids[name], ref.gains[name])
   for got, exp in _run_grad(optimizer, csr, grad, table0, acc0, 0.05, None,
-                            None, num_sc):
+                            None, num_sc, sorted_by_row=num_sc == 1):
     np.testing.assert_allclose(got, exp, rtol=RTOL, atol=ATOL)
+
+
+def _hot_float_case(seed, batch=8192, dim=64):
+  rng = np.random.default_rng(seed)
+  _, feats = _make_specs(1, [40], [dim], "sum",
+                         embedding_spec.SGDOptimizerSpec(0.01), batch)
+  embedding.prepare_feature_specs_for_training(feats, 1, 1)
+  features = [_zipf(rng, 1.2, 40, batch * 4).reshape(batch, 4)]
+  name, ref = _csr_from_oracle(features, None, feats, 1)
+  rows = feats[0].table_spec.stacked_table_spec.stack_vocab_size
+  table0 = rng.normal(0, 0.01, size=(rows, dim)).astype(np.float32)
+  acc0 = np.full((rows, dim), 0.1, np.float32)
+  grad = rng.normal(0, 1, size=(batch, dim)).astype(np.float32)
+  csr = (ref.row_pointers[name], ref.embedding_ids[name],
+         ref.sample_ids[name], ref.gains[name])
+  return csr, grad, table0, acc0
+
+
+def test_grad_deterministic_and_modes_agree():
+  """Float gradients on hot rows (runs of thousands of entries): repeated
+  calls give identical bits, and reading the CSR in place gives the same
+  bits as sorting a copy (same stream order, same blocks)."""
+  csr, grad, table0, acc0 = _hot_float_case(17)
+  runs = [_run_grad("adagrad", csr, grad, table0, acc0, 0.05, None, None, 1,
+                    sorted_by_row=s) for s in (False, False, True, True)]
+  for r in runs[1:]:
+    for (got, _), (got0, _) in zip(r, runs[0]):
+      np.testing.assert_array_equal(got, got0)
+
+
+def test_grad_hot_float_close_to_float64():
+  """The same hot-row case against a float64 restatement of the update.
+
+  Each row gradient is an fp32 sum of up to ~20k terms, evaluated as
+  sequential pieces of at most 64 entries added in a tree. The classical
+  bound for such a sum is |err| <= (64 + log2(#pieces) + 1) * eps32 * sum|x|,
+  below e = 3e-6 * sum|x|. The accumulator A = 0.1 + g^2 then errs by at
+  most 2|g|e + e^2, and the table by at most lr * |d/dg g/sqrt(0.1+g^2)| * e
+  <= lr * 0.1**-0.5 * e, each plus a few ulps of its own rounding."""
+  csr, grad, table0, acc0 = _hot_float_case(23)
+  (got_t, _), (got_a, _) = _run_grad("adagrad", csr, grad, table0, acc0, 0.05,
+                                     None, None, 1, sorted_by_row=True)
+  rp, eid, sid, gains = csr
+  n = int(rp[0])
+  terms = grad[sid[:n]].astype(np.float64) * gains[:n, None].astype(np.float64)
+  g64 = np.zeros(table0.shape, np.float64)
+  mag = np.zeros(table0.shape, np.float64)
+  np.add.at(g64, eid[:n], terms)
+  np.add.at(mag, eid[:n], np.abs(terms))
+  touched = np.zeros(table0.shape[0], bool)
+  touched[eid[:n]] = True
+  a64 = acc0.astype(np.float64) + np.where(touched[:, None], g64 * g64, 0)
+  t64 = table0.astype(np.float64) - np.where(
+      touched[:, None], 0.05 * g64 / np.sqrt(a64), 0)
+  e = 3e-6 * mag
+  bound_a = 2 * np.abs(g64) * e + e * e + 4e-7 * a64
+  bound_t = 0.05 * 0.1**-0.5 * e + 4e-7 * np.abs(t64) + 1e-9
+  assert (np.abs(got_a - a64) <= bound_a).all()
+  assert (np.abs(got_t - t64) <= bound_t).all()
+  # The bound is not vacuous: typical errors sit well inside it and the
+  # largest sums carry rounding at all.
+  assert np.abs(got_a - a64).max() > 0
+
+
+def test_unsorted_csr_declared_sorted_is_flagged():
+  """A CSR whose entries are not ascending, passed with the sorted flag:
+  the kernel reports SCEMB_STATUS_UNSORTED instead of failing silently; the
+  same CSR without the flag is sorted and matches the oracle."""
+  rng = np.random.default_rng(4)
+  rows, dim, batch = 64, 8, 32
+  n = 40
+  eid = rng.integers(0, rows, size=n).astype(np.int32)
+  sid = rng.integers(0, batch, size=n).astype(np.int32)
+  assert (np.diff(eid) < 0).any()
+  rp = np.full(8, n, np.int32)
+  gains = np.ones(n, np.float32)
+  grad = rng.integers(-3, 4, size=(batch, dim)).astype(np.float32)
+  table0 = rng.normal(size=(rows, dim)).astype(np.float32)
+  keep, c = _device.csr_operands(rp, eid, sid, gains, 1, 1,
+                                 sorted_by_row=True)
+  status = torch.zeros(1, dtype=torch.int32, device="cuda")
+  table = torch.from_numpy(table0.copy()).cuda()
+  _native.sparse_dense_matmul_grad(c, torch.from_numpy(grad).cuda(), table,
+                                   None, 0.1, batch, device_status=status)
+  assert int(status.item()) & _native.STATUS_UNSORTED
+  del keep
+  (got, exp), = _run_grad("sgd", (rp, eid, sid, gains), grad, table0, None,
+                          0.1, None, None, 1, sorted_by_row=False)
+  np.testing.assert_array_equal(got, exp)
 
 
 def test_end_to_end_api_feature_stacking_adagrad():
