@@ -107,7 +107,23 @@ def dlrm26(seed=0, batch=65536, num_tables=26, dim=128):
        "stack_rows": int(sum((v + 7) // 8 * 8 for v in vocabs))})
 
 
-def run_gpu(w: Workload, steps: int, warmup: int):
+def copy_probe(dev, gib=1):
+  """A plain device copy of `gib` GiB, three times: the calibration kernel
+  for the FETCH_SIZE / WRITE_SIZE counters (each launch must read and write
+  exactly gib GiB)."""
+  import torch  # pylint: disable=g-import-not-at-top
+
+  n = gib * (1 << 30) // 4
+  a = torch.ones(n, dtype=torch.float32, device=dev)
+  b = torch.empty_like(a)
+  for _ in range(3):
+    b.copy_(a)
+  torch.cuda.synchronize()
+  log(f"copy probe: 3 x {gib} GiB device copies")
+  del a, b
+
+
+def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False):
   import torch  # pylint: disable=g-import-not-at-top
 
   from jax_tpu_embedding.sparsecore import _native  # pylint: disable=g-import-not-at-top
@@ -117,6 +133,8 @@ def run_gpu(w: Workload, steps: int, warmup: int):
 
   torch.cuda.set_device(0)
   dev = torch.device("cuda", 0)
+  if probe:
+    copy_probe(dev)
   stacked = embedding.get_stacked_table_specs(w.feature_specs)
   # Inputs resident in HBM before anything is timed.
   feats_dev = [torch.from_numpy(f).to(dev) for f in w.features]
@@ -191,10 +209,13 @@ def run_gpu(w: Workload, steps: int, warmup: int):
   log(f"step with the reference CSR arrays only: {csr_only_ms:.4f} ms")
   for _ in range(warmup):
     step()
-  torch.cuda.synchronize()
+  ms_per_step = timed(steps, False)
+  # Kernel durations from HIP events on the launch stream, in a second pass
+  # of the same steps (the events themselves cost a few microseconds each,
+  # so the timed pass above runs without them).
   _native.profile_enable(True)
   _native.profile_collect(None)
-  ms_per_step = timed(steps, False)
+  timed(steps, False)
   _native.profile_enable(False)
   spans = {}
   for k in ("fwd_reduce", "fwd_finish", "bwd_reduce", "bwd_finish",
@@ -298,6 +319,27 @@ def cpu_baseline(w: Workload, sample_batch: int, seconds: float):
   }
 
 
+def profiled_traffic():
+  """HBM bytes per launch pair from the committed rocprofv3 --pmc summary,
+  if it was measured on the current lookup kernels (the summary names the
+  SHA-256 of lookup.hip it was taken with); else None."""
+  import hashlib  # pylint: disable=g-import-not-at-top
+  import re  # pylint: disable=g-import-not-at-top
+
+  src = os.path.join(ROOT, "jax-tpu-embedding_amd", "csrc", "lookup.hip")
+  summary = os.path.join(ROOT, "profiles", "dlrm26_segreduce_hbm_traffic.md")
+  try:
+    sha = hashlib.sha256(open(src, "rb").read()).hexdigest()
+    text = open(summary).read()
+  except OSError:
+    return None
+  m = re.search(r"bench-traffic: lookup_hip_sha256=(\w+) bwd_bytes=(\d+) "
+                r"fwd_bytes=(\d+)", text)
+  if not m or m.group(1) != sha:
+    return None
+  return {"bwd": int(m.group(2)), "fwd": int(m.group(3))}
+
+
 def main():
   ap = argparse.ArgumentParser()
   ap.add_argument("--gpus", type=int, default=1)
@@ -306,6 +348,8 @@ def main():
   ap.add_argument("--cpu-seconds", type=float, default=10.0)
   ap.add_argument("--cpu-sample-batch", type=int, default=8192)
   ap.add_argument("--no-cpu-baseline", action="store_true")
+  ap.add_argument("--copy-probe", action="store_true",
+                  help="run a 1 GiB device copy first (counter calibration)")
   args = ap.parse_args()
   if args.gpus != 1:
     print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -314,7 +358,7 @@ def main():
   t_setup = time.perf_counter()
   w = dlrm26()
   log(f"workload built in {time.perf_counter() - t_setup:.1f} s")
-  res = run_gpu(w, args.steps, args.warmup)
+  res = run_gpu(w, args.steps, args.warmup, probe=args.copy_probe)
   fwd_bytes, bwd_bytes = algorithmic_bytes(res["per_stack"])
   step_s = res["ms_per_step"] / 1e3
   sp = res["spans"]
@@ -322,11 +366,14 @@ def main():
   # kernel completes the rows whose entries span several blocks).
   fwd_ms = sp["fwd_reduce"][0] + sp["fwd_finish"][0]
   bwd_ms = sp["bwd_reduce"][0] + sp["bwd_finish"][0]
+  traffic = profiled_traffic()
   if bwd_ms >= fwd_ms:
     dom, dom_ms, dom_bytes = ("bwd: SegReduce+SegFinish (Adagrad)", bwd_ms,
                               bwd_bytes)
+    dom_traffic = traffic["bwd"] if traffic else None
   else:
     dom, dom_ms, dom_bytes = "fwd: SegReduce+SegFinish", fwd_ms, fwd_bytes
+    dom_traffic = traffic["fwd"] if traffic else None
   achieved = dom_bytes / (dom_ms / 1e3) / 1e9
   roofline = {
       "bound": "hbm",
@@ -335,7 +382,9 @@ def main():
       "peak": PEAK_HBM_GBS,
       "unit": "GB/s",
       "frac": round(achieved / PEAK_HBM_GBS, 4),
-      "traffic": None,
+      # HBM bytes per launch pair, rocprofv3 FETCH_SIZE + WRITE_SIZE scaled
+      # by a 1 GiB copy (profiles/dlrm26_segreduce_hbm_traffic.md).
+      "traffic": dom_traffic,
       "kernel_ms": round(dom_ms, 4),
       "algorithmic_bytes": int(dom_bytes),
   }

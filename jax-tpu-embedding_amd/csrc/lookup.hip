@@ -36,8 +36,34 @@
 namespace scemb {
 namespace {
 
+#ifndef SCEMB_FWD_UNROLL
+#define SCEMB_FWD_UNROLL 8
+#endif
+#ifndef SCEMB_BWD_UNROLL
+#define SCEMB_BWD_UNROLL 4
+#endif
+#ifndef SCEMB_NT_ACT
+#define SCEMB_NT_ACT 1
+#endif
+#ifndef SCEMB_NT_GRAD
+#define SCEMB_NT_GRAD 1
+#endif
+#ifndef SCEMB_NT_TABLE
+#define SCEMB_NT_TABLE 0
+#endif
+
 constexpr int kBlock = 256;  // threads per block = stream entries per block
-constexpr int kUnroll = 4;   // entries in flight per sub-group
+// Entries whose rows are loaded together per sub-group (memory-level
+// parallelism; the backward also keeps the table / accumulator rows of the
+// runs that end in the batch in registers).
+constexpr int kFwdUnroll = SCEMB_FWD_UNROLL;
+constexpr int kBwdUnroll = SCEMB_BWD_UNROLL;
+// Streaming (nontemporal) access for data touched once per call, so the
+// last-level cache keeps table rows: activations written by the forward,
+// activation gradients read by the backward.
+constexpr bool kNtAct = SCEMB_NT_ACT;
+constexpr bool kNtGrad = SCEMB_NT_GRAD;
+constexpr bool kNtTable = SCEMB_NT_TABLE;
 constexpr uint32_t kSkip = 0xffffffffu;  // key of an entry outside any run
 
 // Per-block flags left by SegReduce for SegFinish.
@@ -132,6 +158,7 @@ __global__ __launch_bounds__(256) void ExpandCsr(Csr csr, int64_t bps,
 
 template <int VEC>
 struct Vec;
+typedef float NativeF4 __attribute__((ext_vector_type(4)));
 template <>
 struct Vec<4> {
   using T = float4;
@@ -141,6 +168,15 @@ struct Vec<4> {
   }
   __device__ static void Store(float* p, T v) {
     *reinterpret_cast<float4*>(p) = v;
+  }
+  __device__ static T LoadNT(const float* p) {
+    const NativeF4 v =
+        __builtin_nontemporal_load(reinterpret_cast<const NativeF4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+  }
+  __device__ static void StoreNT(float* p, T v) {
+    const NativeF4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<NativeF4*>(p));
   }
   __device__ static T Fma(T acc, float g, T v) {
     acc.x = acc.x + g * v.x;
@@ -168,11 +204,30 @@ struct Vec<1> {
   __device__ static T Zero() { return 0.f; }
   __device__ static T Load(const float* p) { return *p; }
   __device__ static void Store(float* p, T v) { *p = v; }
+  __device__ static T LoadNT(const float* p) {
+    return __builtin_nontemporal_load(p);
+  }
+  __device__ static void StoreNT(float* p, T v) {
+    __builtin_nontemporal_store(v, p);
+  }
   __device__ static T Fma(T acc, float g, T v) { return acc + g * v; }
   __device__ static T Add(T a, T b) { return a + b; }
   __device__ static float Get(const T& v, int) { return v; }
   __device__ static void Set(T& v, int, float x) { v = x; }
 };
+
+template <int VEC, bool NT>
+__device__ __forceinline__ typename Vec<VEC>::T LoadRow(const float* p) {
+  return NT ? Vec<VEC>::LoadNT(p) : Vec<VEC>::Load(p);
+}
+template <int VEC, bool NT>
+__device__ __forceinline__ void StoreRow(float* p, typename Vec<VEC>::T v) {
+  if (NT) {
+    Vec<VEC>::StoreNT(p, v);
+  } else {
+    Vec<VEC>::Store(p, v);
+  }
+}
 
 struct OptParams {
   const float* lr_ptr;
@@ -264,7 +319,7 @@ __device__ __forceinline__ void Epilogue(const RowArgs& r, uint32_t key,
   using V = Vec<VEC>;
   const int64_t off = static_cast<int64_t>(key) * r.dim + col;
   if (EPI == kEpiFwd) {
-    V::Store(r.dst + off, g);
+    StoreRow<VEC, kNtAct>(r.dst + off, g);
     return;
   }
 #pragma unroll
@@ -273,8 +328,8 @@ __device__ __forceinline__ void Epilogue(const RowArgs& r, uint32_t key,
     V::Set(t, k, UpdateOne<EPI>(V::Get(t, k), &ak, V::Get(g, k), lr, r.opt));
     V::Set(a, k, ak);
   }
-  V::Store(r.dst + off, t);
-  if (EPI == kEpiAdagrad) V::Store(r.accum + off, a);
+  StoreRow<VEC, kNtTable>(r.dst + off, t);
+  if (EPI == kEpiAdagrad) StoreRow<VEC, kNtTable>(r.accum + off, a);
 }
 
 template <int VEC, int EPI>
@@ -301,7 +356,7 @@ __device__ __forceinline__ void ZeroRows(float* dst, int64_t dim, int64_t lo,
   for (int64_t row = lo; row < hi; ++row) {
     for (int64_t col = static_cast<int64_t>(cl) * VEC; col < dim;
          col += static_cast<int64_t>(G) * VEC) {
-      V::Store(dst + row * dim + col, V::Zero());
+      StoreRow<VEC, kNtAct>(dst + row * dim + col, V::Zero());
     }
   }
 }
@@ -311,6 +366,8 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
   using V = Vec<VEC>;
   using T = typename V::T;
   constexpr int P = kBlock / G;
+  constexpr int kUnroll = EPI == kEpiFwd ? kFwdUnroll : kBwdUnroll;
+  constexpr bool kNtSrc = EPI == kEpiFwd ? false : kNtGrad;
   __shared__ uint32_t s_key[kBlock + 2];  // [0]: entry before, [257]: after
   __shared__ uint64_t s_ent[kBlock];
   __shared__ T s_part[2 * P][G];
@@ -446,8 +503,8 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
         gn[u] = PackedGain(en);
         v[u] = V::Zero();
         if (val && col_ok) {
-          v[u] = V::Load(r.src + static_cast<int64_t>(PackedIndex(en)) * dim +
-                         col);
+          v[u] = LoadRow<VEC, kNtSrc>(
+              r.src + static_cast<int64_t>(PackedIndex(en)) * dim + col);
         }
         const bool is_end = val && ((end_m >> idx) & 1);
         const bool first = (start_m & ~1ull & LowBits(idx + 1)) == 0;
