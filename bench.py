@@ -56,28 +56,87 @@ def zipf_ids(rng, a, vocab, size):
 class Workload:
   """Specs, host inputs and metadata of one benchmark configuration."""
 
-  def __init__(self, name, feature_specs, features, weights, optimizer_name,
-               lr, description):
+  def __init__(self, name, feature_specs, features, weights, description):
     self.name = name
     self.feature_specs = feature_specs
     self.features = features
     self.weights = weights
-    self.optimizer_name = optimizer_name
-    self.lr = lr
     self.description = description
 
 
-def dlrm26(seed=0, batch=65536, num_tables=26, dim=128):
-  from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
+class Ragged:
+  """Ragged feature: flat values plus row splits (the RaggedTensor layout
+  the preprocessing accepts)."""
+
+  def __init__(self, values, row_splits):
+    self.values = values
+    self.row_splits = row_splits
+
+  def head(self, rows):
+    end = int(self.row_splits[rows])
+    return Ragged(self.values[:end], self.row_splits[:rows + 1])
+
+  @property
+  def size(self):
+    return int(self.values.size)
+
+
+def _ragged(rng, lengths, draw):
+  splits = np.zeros(len(lengths) + 1, np.int64)
+  np.cumsum(lengths, out=splits[1:])
+  return Ragged(draw(int(splits[-1])), splits)
+
+
+def _stack_all(feats, names, stack_name, limit, num_sc=1):
   from jax_tpu_embedding.sparsecore.lib.nn import table_stacking  # pylint: disable=g-import-not-at-top
+
+  table_stacking.stack_tables(
+      feats, names, global_device_count=1, num_sc_per_device=num_sc,
+      stack_name=stack_name,
+      stack_to_max_ids_per_partition=lambda n, b: limit,
+      stack_to_max_unique_ids_per_partition=lambda n, b: limit)
+
+
+def _round8(n):
+  return (int(n) + 7) // 8 * 8
+
+
+def c1(seed=1):
+  """Config 1: one table 100,000 x 16, batch 1,024, 1-16 Zipf(1.05) ids per
+  sample, sum, SGD lr 0.01."""
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-import-not-at-top
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
+
+  rng = np.random.default_rng(seed)
+  batch, vocab, dim = 1024, 100_000, 16
+  lens = rng.integers(1, 17, size=batch)
+  f = _ragged(rng, lens, lambda n: zipf_ids(rng, 1.05, vocab, n))
+  table = embedding_spec.TableSpec(
+      name="t0", vocabulary_size=vocab, embedding_dim=dim,
+      initializer=embedding_spec.normal(0.01),
+      optimizer=embedding_spec.SGDOptimizerSpec(learning_rate=0.01),
+      combiner="sum", max_ids_per_partition=_round8(f.size),
+      max_unique_ids_per_partition=_round8(f.size))
+  fs = embedding_spec.FeatureSpec(name="f0", table_spec=table,
+                                  input_shape=[batch, 1],
+                                  output_shape=[batch, dim])
+  embedding.prepare_feature_specs_for_training([fs], 1, 1)
+  return Workload("c1", [fs], [f], None, {
+      "workload": "c1: one table 100,000 x 16, batch 1,024, 1-16 Zipf(1.05) "
+                  "ids per sample, sum, SGD lr 0.01", "batch": batch})
+
+
+def dlrm26(seed=0, batch=65536, num_tables=26, dim=128):
+  """Config 2 (the headline): 26 tables of dim 128, vocab log-uniform in
+  [10, 4e7], batch 65,536, one Zipf(1.1) id per feature, sum, Adagrad."""
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
 
   rng = np.random.default_rng(seed)
   vocabs = np.floor(np.exp(rng.uniform(np.log(10), np.log(4e7),
                                        size=num_tables))).astype(np.int64)
   opt = embedding_spec.AdagradOptimizerSpec(learning_rate=0.01,
                                             initial_accumulator_value=0.1)
-  n_total = num_tables * batch
-  limit = (n_total + 7) // 8 * 8
+  limit = _round8(num_tables * batch)
   tables = [
       embedding_spec.TableSpec(
           name=f"t{t:02d}", vocabulary_size=int(vocabs[t]), embedding_dim=dim,
@@ -91,20 +150,126 @@ def dlrm26(seed=0, batch=65536, num_tables=26, dim=128):
                                  output_shape=[batch, dim])
       for t in range(num_tables)
   ]
-  table_stacking.stack_tables(
-      feats, [t.name for t in tables], global_device_count=1,
-      num_sc_per_device=1, stack_name="dlrm26",
-      stack_to_max_ids_per_partition=lambda n, b: limit,
-      stack_to_max_unique_ids_per_partition=lambda n, b: limit)
+  _stack_all(feats, [t.name for t in tables], "dlrm26", limit)
   features = [zipf_ids(rng, 1.1, int(vocabs[t]), batch).reshape(batch, 1)
               for t in range(num_tables)]
   return Workload(
-      "dlrm26", feats, features, None, "adagrad", 0.01,
+      "dlrm26", feats, features, None,
       {"workload": "dlrm26: 26 tables dim 128 stacked into one HBM buffer, "
                    "vocab log-uniform [10, 4e7] (seed 0), batch 65536, "
                    "1 Zipf(1.1) id per feature, sum, Adagrad lr 0.01",
        "tables": num_tables, "dim": dim, "batch": batch,
        "stack_rows": int(sum((v + 7) // 8 * 8 for v in vocabs))})
+
+
+def c3(seed=3):
+  """Config 3: 8 tables 10M x 64, batch 32,768, 20-80 Zipf(1.2) ids per
+  sample with U(0,1) weights; tables 0-3 sqrtn, 4-7 mean (two stacks of 40M
+  rows); SGD lr 0.05."""
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
+
+  rng = np.random.default_rng(seed)
+  batch, vocab, dim = 32768, 10_000_000, 64
+  opt = embedding_spec.SGDOptimizerSpec(learning_rate=0.05)
+  feats, features, weights = [], [], []
+  tables = []
+  for t in range(8):
+    lens = rng.integers(20, 81, size=batch)
+    f = _ragged(rng, lens, lambda n: zipf_ids(rng, 1.2, vocab, n))
+    features.append(f)
+    weights.append(Ragged(rng.uniform(0, 1, size=f.size).astype(np.float32),
+                          f.row_splits))
+    tables.append(embedding_spec.TableSpec(
+        name=f"t{t}", vocabulary_size=vocab, embedding_dim=dim,
+        initializer=embedding_spec.normal(0.01), optimizer=opt,
+        combiner="sqrtn" if t < 4 else "mean", max_ids_per_partition=1,
+        max_unique_ids_per_partition=1))
+    feats.append(embedding_spec.FeatureSpec(
+        name=f"f{t}", table_spec=tables[-1], input_shape=[batch, 1],
+        output_shape=[batch, dim]))
+  for k, group in enumerate((range(0, 4), range(4, 8))):
+    limit = _round8(sum(features[t].size for t in group))
+    _stack_all([feats[t] for t in group], [f"t{t}" for t in group],
+               f"c3_{'sqrtn' if k == 0 else 'mean'}", limit)
+  return Workload("c3", feats, features, weights, {
+      "workload": "c3: 8 tables 10M x 64 in two stacks (sqrtn, mean), batch "
+                  "32,768, 20-80 Zipf(1.2) ids per sample, U(0,1) weights, "
+                  "SGD lr 0.05", "batch": batch})
+
+
+def c4(seed=4):
+  """Config 4: one table 200M x 128 (102 GB, plus a 102 GB accumulator),
+  batch 131,072, 50 Zipf(1.3) ids per sample, sum, Adagrad."""
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-import-not-at-top
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
+
+  rng = np.random.default_rng(seed)
+  batch, vocab, dim, k = 131072, 200_000_000, 128, 50
+  ids = zipf_ids(rng, 1.3, vocab, batch * k).reshape(batch, k)
+  table = embedding_spec.TableSpec(
+      name="t0", vocabulary_size=vocab, embedding_dim=dim,
+      initializer=embedding_spec.normal(0.01),
+      optimizer=embedding_spec.AdagradOptimizerSpec(
+          learning_rate=0.01, initial_accumulator_value=0.1),
+      combiner="sum", max_ids_per_partition=_round8(ids.size),
+      max_unique_ids_per_partition=_round8(ids.size))
+  fs = embedding_spec.FeatureSpec(name="f0", table_spec=table,
+                                  input_shape=[batch, k],
+                                  output_shape=[batch, dim])
+  embedding.prepare_feature_specs_for_training([fs], 1, 1)
+  return Workload("c4", [fs], [ids], None, {
+      "workload": "c4: one table 200M x 128 (102 GB + 102 GB accumulator), "
+                  "batch 131,072, 50 Zipf(1.3) ids per sample, sum, Adagrad",
+      "batch": batch})
+
+
+def c5(seed=5):
+  """Config 5: 40 features over 12 tables (dims 8..256, vocab log-uniform
+  [1e4, 5e6]), power-law lengths on [1, 500], uniform ids on tables 0-5 and
+  Zipf(1.05) on 6-11, batch 16,384, mean, Adagrad; six stacks (one per
+  dim) with feature stacking."""
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
+
+  rng = np.random.default_rng(seed)
+  batch = 16384
+  dims = [8, 16, 32, 64, 128, 256]
+  vocabs = np.floor(np.exp(rng.uniform(np.log(1e4), np.log(5e6),
+                                       size=12))).astype(np.int64)
+  opt = embedding_spec.AdagradOptimizerSpec(learning_rate=0.01,
+                                            initial_accumulator_value=0.1)
+  support = np.arange(1, 501)
+  p = support.astype(np.float64) ** -1.5
+  p /= p.sum()
+  tables = [embedding_spec.TableSpec(
+      name=f"t{t:02d}", vocabulary_size=int(vocabs[t]),
+      embedding_dim=dims[t % 6], initializer=embedding_spec.normal(0.01),
+      optimizer=opt, combiner="mean", max_ids_per_partition=1,
+      max_unique_ids_per_partition=1) for t in range(12)]
+  feats, features = [], []
+  for f in range(40):
+    t = f % 12
+    lens = rng.choice(support, size=batch, p=p)
+    if t < 6:
+      draw = lambda n, v=int(vocabs[t]): rng.integers(0, v, size=n).astype(
+          np.int32)
+    else:
+      draw = lambda n, v=int(vocabs[t]): zipf_ids(rng, 1.05, v, n)
+    features.append(_ragged(rng, lens, draw))
+    feats.append(embedding_spec.FeatureSpec(
+        name=f"f{f:02d}", table_spec=tables[t], input_shape=[batch, 1],
+        output_shape=[batch, dims[t % 6]]))
+  for d in range(6):
+    group = [f for f in range(40) if f % 12 in (d, d + 6)]
+    limit = _round8(sum(features[f].size for f in group))
+    _stack_all([feats[f] for f in group], [f"t{d:02d}", f"t{d + 6:02d}"],
+               f"c5_d{dims[d]}", limit)
+  return Workload("c5", feats, features, None, {
+      "workload": "c5: 40 features over 12 tables (dims 8-256, vocab "
+                  "log-uniform [1e4, 5e6]) in six stacks, power-law lengths "
+                  "[1, 500], batch 16,384, mean, Adagrad", "batch": batch})
+
+
+WORKLOADS = {"c1": c1, "c2": dlrm26, "c3": c3, "c4": c4, "c5": c5}
 
 
 def copy_probe(dev, gib=1):
@@ -123,21 +288,42 @@ def copy_probe(dev, gib=1):
   del a, b
 
 
+def _stack_batch_ids(w: Workload):
+  """Input ids (lookups) per stack."""
+  out = {}
+  for f, fs in zip(w.features, w.feature_specs):
+    name = fs.table_spec.stacked_table_spec.stack_name
+    out[name] = out.get(name, 0) + int(np.asarray(f).size if not isinstance(
+        f, Ragged) else f.size)
+  return out
+
+
 def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False):
   import torch  # pylint: disable=g-import-not-at-top
 
   from jax_tpu_embedding.sparsecore import _native  # pylint: disable=g-import-not-at-top
   from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_csr as fwd  # pylint: disable=g-import-not-at-top
   from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_adagrad as ada  # pylint: disable=g-import-not-at-top
+  from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_sgd as sgd  # pylint: disable=g-import-not-at-top
   from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-import-not-at-top
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
 
   torch.cuda.set_device(0)
   dev = torch.device("cuda", 0)
   if probe:
     copy_probe(dev)
   stacked = embedding.get_stacked_table_specs(w.feature_specs)
+
+  def resident(x):
+    if isinstance(x, Ragged):
+      return Ragged(torch.from_numpy(np.asarray(x.values)).to(dev),
+                    x.row_splits)
+    return torch.from_numpy(np.asarray(x)).to(dev)
+
   # Inputs resident in HBM before anything is timed.
-  feats_dev = [torch.from_numpy(f).to(dev) for f in w.features]
+  feats_dev = [resident(f) for f in w.features]
+  weights_dev = (None if w.weights is None else
+                 [resident(x) for x in w.weights])
   torch.cuda.synchronize()
   # GPU preprocessing (reported separately): median of 5 after 2 warmups.
   pre_times = []
@@ -145,7 +331,7 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False):
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     pre, stats = embedding.preprocess_sparse_dense_matmul_input(
-        feats_dev, None, w.feature_specs, 1, 1, num_sc_per_device=1)
+        feats_dev, weights_dev, w.feature_specs, 1, 1, num_sc_per_device=1)
     torch.cuda.synchronize()
     if i >= 2:
       pre_times.append(time.perf_counter() - t0)
@@ -153,33 +339,37 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False):
   log(f"preprocess: {preprocess_ms:.3f} ms (median of {len(pre_times)})")
   gen = torch.Generator(device=dev)
   gen.manual_seed(1234)
-  tables = {}
+  state = {}
   per_stack = {}
-  lookups = 0
+  ids_per_stack = _stack_batch_ids(w)
   for name, spec in stacked.items():
     rows, dim = spec.stack_vocab_size, spec.stack_embedding_dim
     t = torch.empty((rows, dim), dtype=torch.float32, device=dev)
     t.normal_(0.0, 0.01, generator=gen)
-    a = torch.full((rows, dim), 0.1, dtype=torch.float32, device=dev)
+    adagrad = isinstance(spec.optimizer, embedding_spec.AdagradOptimizerSpec)
+    a = None
+    if adagrad:
+      a = torch.full((rows, dim), spec.optimizer.initial_accumulator_value,
+                     dtype=torch.float32, device=dev)
     bs = spec.total_sample_count
     g = torch.empty((bs, dim), dtype=torch.float32, device=dev)
     g.normal_(0.0, 1.0, generator=gen)
-    tables[name] = (t, a, g)
-    rp = pre.lhs_row_pointers[name]
+    lr = torch.tensor(spec.optimizer.learning_rate, dtype=torch.float32,
+                      device=dev)
+    state[name] = (t, a, g, lr)
+    rp = pre.lhs_row_pointers[name].cpu().numpy()
     eid = pre.lhs_embedding_ids[name]
-    n_valid = int(rp[0].item())  # S = NS = 1: one partition
+    n_valid = int(rp[0])  # one partition (S = NS = 1)
     uniq = int(torch.unique(eid[:n_valid]).numel())
     per_stack[name] = {"N": n_valid, "U": uniq, "Bs": bs, "D": dim,
-                       "rows": rows}
-    lookups += sum(int(np.asarray(f).size) for f, fs in
-                   zip(w.features, w.feature_specs)
-                   if fs.table_spec.stacked_table_spec.stack_name == name)
+                       "rows": rows, "ids": ids_per_stack[name],
+                       "optimizer": "adagrad" if adagrad else "sgd"}
     log(f"stack {name}: rows={rows} dim={dim} N={n_valid} U={uniq} Bs={bs}")
-  lr = torch.tensor(w.lr, dtype=torch.float32, device=dev)
+  lookups = sum(ids_per_stack.values())
 
   def step(csr_only=False):
     for name, spec in stacked.items():
-      t, a, g = tables[name]
+      t, a, g, lr = state[name]
       csr = (pre.lhs_row_pointers[name], pre.lhs_embedding_ids[name],
              pre.lhs_sample_ids[name], pre.lhs_gains[name])
       fwd.tpu_sparse_dense_matmul_csr_primitive.bind(
@@ -188,12 +378,16 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False):
           max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
           num_sc_per_device=1,
           lookup_view=None if csr_only else pre.lookup_views[name])
-      ada.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
-          *csr, 1, t, a, g, lr,
-          max_ids_per_partition=spec.max_ids_per_partition,
-          max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
-          num_sc_per_device=1,
-          csr_sorted_by_row=not csr_only and pre.csr_sorted_by_row)
+      kw = dict(max_ids_per_partition=spec.max_ids_per_partition,
+                max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
+                num_sc_per_device=1,
+                csr_sorted_by_row=not csr_only and pre.csr_sorted_by_row)
+      if a is not None:
+        ada.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
+            *csr, 1, t, a, g, lr, **kw)
+      else:
+        sgd.tpu_sparse_dense_matmul_grad_with_sgd_primitive.bind(
+            *csr, 1, t, g, lr, **kw)
 
   def timed(n, csr_only):
     torch.cuda.synchronize()
@@ -221,9 +415,10 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False):
   for k in ("fwd_reduce", "fwd_finish", "bwd_reduce", "bwd_finish",
             "fwd_call", "bwd_call"):
     ms, n = _native.profile_collect(k)
-    spans[k] = (ms / n if n else None, n)
-  log(f"step: {ms_per_step:.4f} ms; spans " +
-      ", ".join(f"{k} {v[0]:.4f}" for k, v in spans.items() if v[0]))
+    # Per step, summed over the stacks (one launch per stack and step).
+    spans[k] = (ms / steps if n else 0.0, n)
+  log(f"step: {ms_per_step:.4f} ms; per-step spans " +
+      ", ".join(f"{k} {v[0]:.4f}" for k, v in spans.items()))
   return {
       "csr_only_ms_per_step": csr_only_ms,
       "ms_per_step": ms_per_step,
@@ -236,26 +431,46 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False):
 
 
 def algorithmic_bytes(per_stack):
-  """Compulsory HBM bytes of the forward and of backward + Adagrad."""
+  """Compulsory HBM bytes of the forward and of backward + optimizer."""
   fwd = bwd = 0
   for s in per_stack.values():
     n, u, bs, d = s["N"], s["U"], s["Bs"], s["D"]
     fwd += 12 * n + 4 * d * u + 4 * d * bs
-    bwd += 12 * n + 4 * d * bs + 16 * d * u
+    slot = 16 if s["optimizer"] == "adagrad" else 8
+    bwd += 12 * n + 4 * d * bs + slot * d * u
   return fwd, bwd
+
+
+def _head(x, rows):
+  if isinstance(x, Ragged):
+    return x.head(rows)
+  return np.asarray(x)[:rows]
 
 
 def cpu_baseline(w: Workload, sample_batch: int, seconds: float):
   """The oracle (C++ restatement of the reference CPU path) on host cores,
   on the first `sample_batch` samples of every feature."""
+  import copy  # pylint: disable=g-import-not-at-top
+
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
   from oracle import refcpu  # pylint: disable=g-import-not-at-top
 
   threads = min(16, os.cpu_count() or 1)
-  feats = [f[:sample_batch] for f in w.features]
-  # Same stacking geometry with the sample's batch size.
-  from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
-  import copy  # pylint: disable=g-import-not-at-top
-
+  batch = w.feature_specs[0].input_shape[0]
+  sample_batch = min(sample_batch, batch)
+  feats = [_head(f, sample_batch) for f in w.features]
+  weights = (None if w.weights is None else
+             [_head(x, sample_batch) for x in w.weights])
+  # The oracle takes per-sample arrays for ragged input.
+  def rows(x):
+    if not isinstance(x, Ragged):
+      return x
+    out = np.empty(len(x.row_splits) - 1, dtype=object)
+    for i in range(len(out)):
+      out[i] = np.asarray(x.values[x.row_splits[i]:x.row_splits[i + 1]])
+    return out
+  feats = [rows(f) for f in feats]
+  weights = None if weights is None else [rows(x) for x in weights]
   # Same stacking geometry with the sample's batch: each feature keeps its
   # slot in the stack, its row offset scales with the batch.
   specs = []
@@ -273,35 +488,41 @@ def cpu_baseline(w: Workload, sample_batch: int, seconds: float):
     st = fs.table_spec.stacked_table_spec
     stacked[st.stack_name] = st
   t0 = time.perf_counter()
-  ref = refcpu.preprocess(feats, None, specs, 1, 1, num_sc_per_device=1)
+  ref = refcpu.preprocess(feats, weights, specs, 1, 1, num_sc_per_device=1)
   pre_s = time.perf_counter() - t0
-  total_lookups = sum(f.size for f in feats)
+  total_lookups = sum(int(f.size) if not isinstance(f, np.ndarray) or
+                      f.dtype != object else sum(len(r) for r in f)
+                      for f in feats)
   busy = 0.0
   iters = 0
   rng = np.random.default_rng(5)
   state = {}
   for name, st in stacked.items():
-    rows, dim = st.stack_vocab_size, st.stack_embedding_dim
+    rows_, dim = st.stack_vocab_size, st.stack_embedding_dim
     # calloc'd: only the rows the sample touches are ever paged in.
-    table = np.zeros((rows, dim), np.float32)
-    acc = np.zeros((rows, dim), np.float32)
+    table = np.zeros((rows_, dim), np.float32)
+    adagrad = isinstance(st.optimizer, embedding_spec.AdagradOptimizerSpec)
+    acc = np.zeros((rows_, dim), np.float32) if adagrad else None
     n = int(ref.row_pointers[name][0])
     touched = np.unique(ref.embedding_ids[name][:n])
     table[touched] = rng.normal(0, 0.01, size=(len(touched), dim))
-    acc[touched] = 0.1
-    bs = len(feats) * sample_batch
+    if adagrad:
+      acc[touched] = st.optimizer.initial_accumulator_value
+    bs = sum(1 for fs in specs
+             if fs.table_spec.stacked_table_spec.stack_name == name
+             ) * sample_batch
     grad = rng.normal(0, 1, size=(bs, dim)).astype(np.float32)
-    state[name] = (table, acc, grad, bs)
+    state[name] = (table, acc, grad, bs, st.optimizer.learning_rate)
   while busy < seconds or iters < 3:
     t0 = time.perf_counter()
     for name in stacked:
-      table, acc, grad, bs = state[name]
+      table, acc, grad, bs, lr = state[name]
       args = (ref.row_pointers[name], ref.embedding_ids[name],
               ref.sample_ids[name], ref.gains[name])
       refcpu.sparse_dense_matmul(*args, table, bs, num_sc_per_device=1,
                                  num_scs=1, threads=threads)
       refcpu.sparse_dense_matmul_grad(*args, grad, table, acc,
-                                      learning_rate=w.lr, num_sc_per_device=1,
+                                      learning_rate=lr, num_sc_per_device=1,
                                       num_scs=1, threads=threads, inplace=True)
     busy += time.perf_counter() - t0
     iters += 1
@@ -312,7 +533,7 @@ def cpu_baseline(w: Workload, sample_batch: int, seconds: float):
       "kind": "port",
       "sample": (f"first {sample_batch} samples of each of the "
                  f"{len(feats)} features ({total_lookups} lookups), "
-                 f"{iters} fwd+bwd+Adagrad passes in {busy:.1f} s; oracle "
+                 f"{iters} fwd+bwd+optimizer passes in {busy:.1f} s; oracle "
                  f"preprocessing of the sample {pre_s * 1e3:.1f} ms on 1 "
                  "thread"),
       "preprocess_ms_per_1k_lookups": pre_s * 1e3 / total_lookups * 1e3,
@@ -350,13 +571,16 @@ def main():
   ap.add_argument("--no-cpu-baseline", action="store_true")
   ap.add_argument("--copy-probe", action="store_true",
                   help="run a 1 GiB device copy first (counter calibration)")
+  ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS),
+                  help="BASELINE.json config (c2, the 26-table DLRM shape, "
+                       "is the headline)")
   args = ap.parse_args()
   if args.gpus != 1:
     print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
           "(this build has no multi-GPU path).", file=sys.stderr)
     sys.exit(2)
   t_setup = time.perf_counter()
-  w = dlrm26()
+  w = WORKLOADS[args.workload]()
   log(f"workload built in {time.perf_counter() - t_setup:.1f} s")
   res = run_gpu(w, args.steps, args.warmup, probe=args.copy_probe)
   fwd_bytes, bwd_bytes = algorithmic_bytes(res["per_stack"])
@@ -366,10 +590,11 @@ def main():
   # kernel completes the rows whose entries span several blocks).
   fwd_ms = sp["fwd_reduce"][0] + sp["fwd_finish"][0]
   bwd_ms = sp["bwd_reduce"][0] + sp["bwd_finish"][0]
-  traffic = profiled_traffic()
+  traffic = profiled_traffic() if w.name == "dlrm26" else None
+  opts = sorted({s["optimizer"] for s in res["per_stack"].values()})
   if bwd_ms >= fwd_ms:
-    dom, dom_ms, dom_bytes = ("bwd: SegReduce+SegFinish (Adagrad)", bwd_ms,
-                              bwd_bytes)
+    dom, dom_ms, dom_bytes = (
+        f"bwd: SegReduce+SegFinish ({'/'.join(opts)})", bwd_ms, bwd_bytes)
     dom_traffic = traffic["bwd"] if traffic else None
   else:
     dom, dom_ms, dom_bytes = "fwd: SegReduce+SegFinish", fwd_ms, fwd_bytes
@@ -391,10 +616,10 @@ def main():
   cpu = None
   if not args.no_cpu_baseline:
     cpu = cpu_baseline(w, args.cpu_sample_batch, args.cpu_seconds)
-  spans = {k: (round(v[0], 4) if v[0] is not None else None)
-           for k, v in res["spans"].items()}
+  spans = {k: round(v[0], 4) for k, v in res["spans"].items()}
   out = {
-      "metric": METRIC,
+      "metric": METRIC if w.name == "dlrm26" else METRIC.replace(
+          "Adagrad), 26-table DLRM shape", "optimizer)"),
       "value": round(res["lookups"] / step_s, 1),
       "unit": "lookups/s",
       "n_gpus": 1,
@@ -413,7 +638,8 @@ def main():
       "step_hbm_frac": round((fwd_bytes + bwd_bytes) / step_s / 1e9 /
                              PEAK_HBM_GBS, 4),
       "algorithmic_bytes_per_step": int(fwd_bytes + bwd_bytes),
-      "kernel_avg_ms": spans,
+      # HIP-event time per step of each kernel (summed over stacks).
+      "kernel_ms_per_step": spans,
       "preprocess_ms": round(res["preprocess_ms"], 3),
       "csr": res["per_stack"],
       "roofline": roofline,

@@ -45,8 +45,8 @@ namespace {
 #ifndef SCEMB_NT_ACT
 #define SCEMB_NT_ACT 1
 #endif
-#ifndef SCEMB_NT_GRAD
-#define SCEMB_NT_GRAD 1
+#ifndef SCEMB_NT_GRAD_MAX_REUSE
+#define SCEMB_NT_GRAD_MAX_REUSE 2
 #endif
 #ifndef SCEMB_NT_TABLE
 #define SCEMB_NT_TABLE 0
@@ -59,10 +59,12 @@ constexpr int kBlock = 256;  // threads per block = stream entries per block
 constexpr int kFwdUnroll = SCEMB_FWD_UNROLL;
 constexpr int kBwdUnroll = SCEMB_BWD_UNROLL;
 // Streaming (nontemporal) access for data touched once per call, so the
-// last-level cache keeps table rows: activations written by the forward,
-// activation gradients read by the backward.
+// last-level cache keeps table rows: activations written by the forward
+// always; activation gradients read by the backward when each is read at
+// most kNtGradMaxReuse times on average (entries per activation row; a
+// multi-hot batch re-reads every gradient row from cache many times).
 constexpr bool kNtAct = SCEMB_NT_ACT;
-constexpr bool kNtGrad = SCEMB_NT_GRAD;
+constexpr int64_t kNtGradMaxReuse = SCEMB_NT_GRAD_MAX_REUSE;
 constexpr bool kNtTable = SCEMB_NT_TABLE;
 constexpr uint32_t kSkip = 0xffffffffu;  // key of an entry outside any run
 
@@ -256,6 +258,7 @@ struct RowArgs {
   float* accum;      // Adagrad accumulator
   int64_t dim;
   int64_t batch;     // forward: rows of dst
+  bool stream_src;   // gathered rows are read about once: nontemporal loads
   OptParams opt;
   float* partials;   // [2 * num_blocks, dim]
   uint32_t* block_flags;
@@ -367,7 +370,6 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
   using T = typename V::T;
   constexpr int P = kBlock / G;
   constexpr int kUnroll = EPI == kEpiFwd ? kFwdUnroll : kBwdUnroll;
-  constexpr bool kNtSrc = EPI == kEpiFwd ? false : kNtGrad;
   __shared__ uint32_t s_key[kBlock + 2];  // [0]: entry before, [257]: after
   __shared__ uint64_t s_ent[kBlock];
   __shared__ T s_part[2 * P][G];
@@ -377,6 +379,26 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
   const int64_t blk = blockIdx.x;
   const int64_t cb = blk * kBlock;
   const int64_t n = st.n;
+  // Blocks that lie wholly in the padding after the last entry (CSR buffers
+  // are sized for the worst case) only clear their flag: with the CSR, past
+  // the end of the last partition; with a sorted stream, after an unused key
+  // (unused keys sort last, and the first one still has gaps to fill).
+  {
+    bool tail;
+    if (SRC == kSrcCsr) {
+      int64_t end = 0;
+      for (int q = 0; q < st.csr.num_partitions; ++q) {
+        end = st.csr.rp[q] > end ? st.csr.rp[q] : end;
+      }
+      tail = cb >= end;
+    } else {
+      tail = cb > 0 && st.keys[cb - 1] >= st.sentinel;
+    }
+    if (tail) {
+      if (tid == 0) r.block_flags[blk] = 0;
+      return;
+    }
+  }
   {
     uint64_t en = 0;
     uint32_t k = kSkip;
@@ -503,8 +525,9 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
         gn[u] = PackedGain(en);
         v[u] = V::Zero();
         if (val && col_ok) {
-          v[u] = LoadRow<VEC, kNtSrc>(
-              r.src + static_cast<int64_t>(PackedIndex(en)) * dim + col);
+          const float* p =
+              r.src + static_cast<int64_t>(PackedIndex(en)) * dim + col;
+          v[u] = r.stream_src ? V::LoadNT(p) : V::Load(p);
         }
         const bool is_end = val && ((end_m >> idx) & 1);
         const bool first = (start_m & ~1ull & LowBits(idx + 1)) == 0;
@@ -927,6 +950,8 @@ int GradImpl(const scemb_csr_t* csr, const float* act_grad, int64_t batch,
   r.batch = batch;
   r.opt = opt;
   r.status = status;
+  // Entries per activation row: how often each gradient row is gathered.
+  r.stream_src = n <= kNtGradMaxReuse * batch;
   int g, vec;
   PickLayout(dim, Aligned16(table) && Aligned16(act_grad) &&
                       (EPI != kEpiAdagrad || Aligned16(accum)), &g, &vec);

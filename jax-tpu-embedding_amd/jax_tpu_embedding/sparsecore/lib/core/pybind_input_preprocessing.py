@@ -187,6 +187,34 @@ def _to_device_feature(feature, weights) -> _DeviceFeature:
           np.asarray(weights, np.float32).reshape(-1), t.float32, dev)
     return _DeviceFeature(ids, w, None, None, int(f.shape[0]), int(f.numel()),
                           int(f.shape[1]), None)
+  if hasattr(feature, "values") and hasattr(feature, "row_splits"):
+    # Ragged tensor (tf.RaggedTensor-like: flat values + row splits), the
+    # RaggedTensorInputBatch input of ragged_tensor_input_batch.h:68-127.
+    vals = feature.values
+    splits = np.asarray(feature.row_splits, np.int64).reshape(-1)
+    if isinstance(vals, t.Tensor):
+      vals = vals.reshape(-1)
+    else:
+      vals = np.ascontiguousarray(np.asarray(vals), dtype=np.int32).reshape(-1)
+    if splits.size == 0 or splits[0] != 0 or splits[-1] != vals.shape[0] or (
+        np.diff(splits) < 0).any():
+      raise ValueError("row_splits must start at 0, be non-decreasing and "
+                       "end at the number of values.")
+    w = None
+    if weights is not None:
+      wv = getattr(weights, "values", weights)
+      wv = (wv.reshape(-1) if isinstance(wv, t.Tensor) else
+            np.asarray(wv, np.float32).reshape(-1))
+      if wv.shape[0] != vals.shape[0]:
+        raise ValueError("Batch size mismatch for features and weights.")
+      w = _native.as_device_tensor(wv, t.float32, dev)
+    ids = _native.as_device_tensor(vals, t.int32, dev)
+    max_id = None
+    if not isinstance(vals, t.Tensor) and vals.size:
+      max_id = int(vals.max())
+    return _DeviceFeature(ids, w, _native.as_device_tensor(splits, t.int64,
+                                                           dev),
+                          splits, splits.size - 1, int(splits[-1]), 0, max_id)
   arr = feature if isinstance(feature, np.ndarray) else np.asarray(
       feature, dtype=object)
   if arr.dtype != object and arr.ndim == 2:
