@@ -163,7 +163,15 @@ def ragged_from_rows(rows, weights=None, **kw) -> RaggedFeature:
 
 
 def ragged_from_array(feature, weights=None, **kw) -> RaggedFeature:
-  """Converts a 2-D array or a 1-D object array of rows to RaggedFeature."""
+  """Converts a 2-D array, a 1-D object array of rows, or a ragged object
+  with flat `values` and `row_splits` to RaggedFeature."""
+  if hasattr(feature, "values") and hasattr(feature, "row_splits"):
+    w = None
+    if weights is not None:
+      w = np.asarray(getattr(weights, "values", weights),
+                     np.float32).reshape(-1)
+    return RaggedFeature(np.asarray(feature.values, np.int32).reshape(-1),
+                         np.asarray(feature.row_splits, np.int64), w, **kw)
   feature = np.asarray(feature) if not isinstance(feature, list) else feature
   if isinstance(feature, np.ndarray) and feature.ndim == 2 and \
       feature.dtype != object:

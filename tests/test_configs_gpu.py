@@ -1,0 +1,213 @@
+"""Parity at the full BASELINE.json configurations (bench.py workloads c1-c5).
+
+For every configuration, at its real size on one GPU:
+  * preprocessing: row pointers, embedding ids, sample ids and gains on the
+    compared region and all stats must equal the CPU oracle's bit for bit
+    (the oracle preprocesses the full batch in seconds);
+  * forward: sampled activation rows (and every empty one among them) against
+    a float64 restatement of sum(gain * table[row]) over the CSR, within the
+    fp32 summation bound |err| <= 5e-6 * sum|gain * value| (pieces of at most
+    64 sequential adds joined by a tree of at most log2(#blocks) levels:
+    (64 + 20) * 2^-24 < 5e-6);
+  * backward + optimizer: the hottest rows, random touched rows and random
+    untouched rows of the table (and accumulator) against a float64
+    restatement of the update from the same CSR, within the bound that the
+    gradient error e = 5e-6 * sum|gain * grad| implies; untouched rows must
+    not change at all.
+The float64 restatements run in torch on the GPU (index_add over the sampled
+rows only), the tables never leave HBM.
+"""
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+import bench  # pylint: disable=g-import-not-at-top,wrong-import-position
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_csr as fwd_prim  # pylint: disable=g-import-not-at-top,wrong-import-position
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_adagrad as ada_prim  # pylint: disable=g-import-not-at-top,wrong-import-position
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_sgd as sgd_prim  # pylint: disable=g-import-not-at-top,wrong-import-position
+from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-import-not-at-top,wrong-import-position
+from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top,wrong-import-position
+from oracle import refcpu  # pylint: disable=g-import-not-at-top,wrong-import-position
+
+EPS_SUM = 5e-6
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+  if not torch.cuda.is_available():
+    pytest.skip("no GPU")
+  torch.cuda.set_device(0)
+  yield
+  torch.cuda.empty_cache()
+
+
+def _check_preprocessing(pre, stats, ref, name):
+  rp = pre.lhs_row_pointers[name].cpu().numpy()
+  np.testing.assert_array_equal(rp, ref.row_pointers[name], err_msg=name)
+  n = int(rp[-1])
+  for got, exp in ((pre.lhs_embedding_ids, ref.embedding_ids),
+                   (pre.lhs_sample_ids, ref.sample_ids),
+                   (pre.lhs_gains, ref.gains)):
+    g = got[name].cpu().numpy()[:n]
+    np.testing.assert_array_equal(g.view(np.int32), exp[name][:n].view(
+        np.int32), err_msg=name)
+  np.testing.assert_array_equal(stats.max_ids_per_partition[name],
+                                ref.max_ids_per_partition[name])
+  np.testing.assert_array_equal(stats.max_unique_ids_per_partition[name],
+                                ref.max_unique_ids_per_partition[name])
+  np.testing.assert_array_equal(stats.required_buffer_size_per_sc[name],
+                                ref.required_buffer_sizes[name])
+  return n
+
+
+def _valid_positions(rp):
+  """Positions of the entries of a one-segment CSR: partition p holds
+  [roundup8(rp[p-1]) (0 for p = 0), rp[p]); the rest is alignment padding
+  (embedding and sample ids INT_MAX) or unused tail."""
+  out, start = [], 0
+  for end in rp:
+    end = int(end)
+    if end > start:
+      out.append(np.arange(start, end))
+    start = max(start, (end + 7) // 8 * 8)
+  return np.concatenate(out) if out else np.zeros(0, np.int64)
+
+
+def _sample(rng, pool, k):
+  pool = np.asarray(pool)
+  return pool if len(pool) <= k else rng.choice(pool, size=k, replace=False)
+
+
+def _check_forward(act, table, eid, sid, gains, rows, dim):
+  """act[rows] against float64 sums over the CSR entries of those rows."""
+  dev = act.device
+  rows_t = torch.from_numpy(rows).to(dev)
+  slot = torch.full((act.shape[0],), -1, dtype=torch.int64, device=dev)
+  slot[rows_t] = torch.arange(len(rows), device=dev)
+  sel = slot[sid] >= 0
+  pos = slot[sid[sel]]
+  vals = table[eid[sel]].double() * gains[sel].double()[:, None]
+  exp = torch.zeros((len(rows), dim), dtype=torch.float64, device=dev)
+  mag = torch.zeros_like(exp)
+  exp.index_add_(0, pos, vals)
+  mag.index_add_(0, pos, vals.abs())
+  got = act[rows_t].double()
+  err = (got - exp).abs()
+  assert bool((err <= EPS_SUM * mag).all()), float((err - EPS_SUM * mag).max())
+  empty = mag.sum(1) == 0
+  assert bool((got[empty] == 0).all())
+
+
+def _check_update(before, after, eid, sid, gains, grad, rows, spec):
+  """Updated table (and accumulator) rows against a float64 restatement."""
+  dev = grad.device
+  rows_t = torch.from_numpy(rows).to(dev)
+  slot = torch.full((int(rows.max()) + 1,), -1, dtype=torch.int64,
+                    device=dev)
+  slot[rows_t] = torch.arange(len(rows), device=dev)
+  valid = eid <= int(rows.max())
+  e, s, g = eid[valid], sid[valid], gains[valid]
+  sel = slot[e] >= 0
+  pos = slot[e[sel]]
+  terms = grad[s[sel]].double() * g[sel].double()[:, None]
+  dim = grad.shape[1]
+  g64 = torch.zeros((len(rows), dim), dtype=torch.float64, device=dev)
+  mag = torch.zeros_like(g64)
+  g64.index_add_(0, pos, terms)
+  mag.index_add_(0, pos, terms.abs())
+  touched = torch.zeros(len(rows), dtype=torch.bool, device=dev)
+  touched[pos] = True
+  t0 = before[0].double()
+  t1 = after[0].double()
+  lr = float(spec.optimizer.learning_rate)
+  e_g = EPS_SUM * mag
+  if isinstance(spec.optimizer, embedding_spec.AdagradOptimizerSpec):
+    a0 = before[1].double()
+    a64 = a0 + g64 * g64
+    t64 = t0 - lr * g64 / torch.sqrt(a64)
+    bound_a = 2 * g64.abs() * e_g + e_g * e_g + 4e-7 * a64
+    bound_t = lr * e_g / torch.sqrt(a0) + 4e-7 * t64.abs() + 1e-9
+    a1 = after[1].double()
+    assert bool(((a1 - a64).abs()[touched] <= bound_a[touched]).all())
+    assert bool((a1[~touched] == a0[~touched]).all())
+  else:
+    t64 = t0 - lr * g64
+    bound_t = lr * e_g + 4e-7 * t64.abs() + 1e-9
+  assert bool(((t1 - t64).abs()[touched] <= bound_t[touched]).all()), float(
+      ((t1 - t64).abs() - bound_t)[touched].max())
+  assert bool((t1[~touched] == t0[~touched]).all())
+  return int(touched.sum())
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c2", "c3", "c5", "c4"])
+def test_config_full_size(cfg):
+  w = bench.WORKLOADS[cfg]()
+  pre, stats = embedding.preprocess_sparse_dense_matmul_input(
+      w.features, w.weights, w.feature_specs, 1, 1, num_sc_per_device=1)
+  ref = refcpu.preprocess(w.features, w.weights, w.feature_specs, 1, 1,
+                          num_sc_per_device=1)
+  rng = np.random.default_rng(int(cfg[1:]))
+  gen = torch.Generator(device="cuda")
+  gen.manual_seed(7)
+  dev = torch.device("cuda", 0)
+  for name, spec in embedding.get_stacked_table_specs(
+      w.feature_specs).items():
+    _check_preprocessing(pre, stats, ref, name)
+    rows, dim, bs = (spec.stack_vocab_size, spec.stack_embedding_dim,
+                     spec.total_sample_count)
+    # The CSR entries only (one partition: S = G = 1), bounds-checked on the
+    # host before any of them is used as an index.
+    pos = torch.from_numpy(_valid_positions(
+        pre.lhs_row_pointers[name].cpu().numpy())).cuda()
+    eid = pre.lhs_embedding_ids[name][pos].long()
+    sid = pre.lhs_sample_ids[name][pos].long()
+    gains = pre.lhs_gains[name][pos]
+    assert int(eid.min()) >= 0 and int(eid.max()) < rows
+    assert int(sid.min()) >= 0 and int(sid.max()) < bs
+    table = torch.empty((rows, dim), dtype=torch.float32, device=dev)
+    table.normal_(0.0, 0.01, generator=gen)
+    act = fwd_prim.tpu_sparse_dense_matmul_csr_primitive.bind(
+        pre.lhs_row_pointers[name], pre.lhs_embedding_ids[name],
+        pre.lhs_sample_ids[name], pre.lhs_gains[name], 1, table,
+        device_batch_size=bs, max_ids_per_partition=spec.max_ids_per_partition,
+        max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
+        num_sc_per_device=1, lookup_view=pre.lookup_views[name])
+    _check_forward(act, table, eid, sid, gains,
+                   _sample(rng, np.arange(bs), 1024), dim)
+    del act
+    # Backward: the 8 hottest rows, random touched and untouched rows.
+    counts = torch.bincount(eid, minlength=rows)
+    hot = torch.topk(counts, min(8, rows)).indices.cpu().numpy()
+    touched = torch.nonzero(counts).flatten().cpu().numpy()
+    untouched = rng.integers(0, rows, size=256)
+    sample_rows = np.unique(np.concatenate(
+        [hot, _sample(rng, touched, 1024), untouched])).astype(np.int64)
+    idx = torch.from_numpy(sample_rows).to(dev)
+    adagrad = isinstance(spec.optimizer, embedding_spec.AdagradOptimizerSpec)
+    acc = (torch.full((rows, dim), spec.optimizer.initial_accumulator_value,
+                      dtype=torch.float32, device=dev) if adagrad else None)
+    grad = torch.empty((bs, dim), dtype=torch.float32, device=dev)
+    grad.normal_(0.0, 1.0, generator=gen)
+    before = (table[idx].clone(), acc[idx].clone() if adagrad else None)
+    lr = torch.tensor(spec.optimizer.learning_rate, dtype=torch.float32,
+                      device=dev)
+    csr = (pre.lhs_row_pointers[name], pre.lhs_embedding_ids[name],
+           pre.lhs_sample_ids[name], pre.lhs_gains[name])
+    kw = dict(max_ids_per_partition=spec.max_ids_per_partition,
+              max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
+              num_sc_per_device=1, csr_sorted_by_row=pre.csr_sorted_by_row)
+    if adagrad:
+      ada_prim.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
+          *csr, 1, table, acc, grad, lr, **kw)
+    else:
+      sgd_prim.tpu_sparse_dense_matmul_grad_with_sgd_primitive.bind(
+          *csr, 1, table, grad, lr, **kw)
+    after = (table[idx], acc[idx] if adagrad else None)
+    assert _check_update(before, after, eid, sid, gains, grad, sample_rows,
+                         spec) > 0
+    del table, acc, grad
+    torch.cuda.empty_cache()
