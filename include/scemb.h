@@ -78,6 +78,9 @@ typedef struct scemb_csr {
   int32_t num_partitions;           /* num_sc_per_device * global devices */
   int32_t row_pointers_per_segment; /* max(num_partitions, 8) */
   uint32_t flags;                   /* SCEMB_CSR_* bits */
+  int64_t num_entries; /* valid entries if known (> 0), else 0: only picks
+                          kernel variants (about one entry per activation
+                          row or more); the buffer size stands in when 0 */
 } scemb_csr_t;
 
 /* The entries of each segment are ascending by (partition, embedding id), as
@@ -100,6 +103,7 @@ typedef struct scemb_sample_view {
   int64_t size;
   int64_t device_batch_size;
   int64_t table_rows;
+  int64_t num_entries;      /* as scemb_csr_t.num_entries */
 } scemb_sample_view_t;
 
 /* ---- Forward: SparseDenseMatmulOp --------------------------------------

@@ -36,36 +36,26 @@
 namespace scemb {
 namespace {
 
-#ifndef SCEMB_FWD_UNROLL
-#define SCEMB_FWD_UNROLL 8
-#endif
-#ifndef SCEMB_BWD_UNROLL
-#define SCEMB_BWD_UNROLL 4
-#endif
-#ifndef SCEMB_NT_ACT
-#define SCEMB_NT_ACT 1
-#endif
-#ifndef SCEMB_NT_GRAD_MAX_REUSE
-#define SCEMB_NT_GRAD_MAX_REUSE 2
-#endif
-#ifndef SCEMB_NT_TABLE
-#define SCEMB_NT_TABLE 0
-#endif
-
 constexpr int kBlock = 256;  // threads per block = stream entries per block
-// Entries whose rows are loaded together per sub-group (memory-level
-// parallelism; the backward also keeps the table / accumulator rows of the
-// runs that end in the batch in registers).
-constexpr int kFwdUnroll = SCEMB_FWD_UNROLL;
-constexpr int kBwdUnroll = SCEMB_BWD_UNROLL;
+// Entries whose rows a sub-group loads together (memory-level parallelism;
+// the backward also holds the table / accumulator rows of the runs that end
+// in the batch). Batches of about one entry per activation row ("one-hot")
+// gain from the wide setting; multi-hot batches, whose gathers mostly hit
+// cache, from the higher occupancy of the narrow one (fewer registers).
+constexpr int kFwdUnrollWide = 8;
+constexpr int kFwdUnrollNarrow = 4;
+constexpr int kBwdUnrollWide = 4;
+constexpr int kBwdUnrollNarrow = 2;
+// Entries per activation row up to which a batch counts as one-hot.
+constexpr int64_t kOneHotMaxEntriesPerRow = 2;
 // Streaming (nontemporal) access for data touched once per call, so the
 // last-level cache keeps table rows: activations written by the forward
-// always; activation gradients read by the backward when each is read at
-// most kNtGradMaxReuse times on average (entries per activation row; a
-// multi-hot batch re-reads every gradient row from cache many times).
-constexpr bool kNtAct = SCEMB_NT_ACT;
-constexpr int64_t kNtGradMaxReuse = SCEMB_NT_GRAD_MAX_REUSE;
-constexpr bool kNtTable = SCEMB_NT_TABLE;
+// always; activation gradients read by the backward for one-hot batches
+// only (a multi-hot batch re-reads every gradient row from cache many
+// times). Table and accumulator rows stay cacheable: the next forward reads
+// the rows the backward has just written.
+constexpr bool kNtAct = true;
+constexpr bool kNtTable = false;
 constexpr uint32_t kSkip = 0xffffffffu;  // key of an entry outside any run
 
 // Per-block flags left by SegReduce for SegFinish.
@@ -364,12 +354,11 @@ __device__ __forceinline__ void ZeroRows(float* dst, int64_t dim, int64_t lo,
   }
 }
 
-template <int G, int VEC, int SRC, int EPI>
+template <int G, int VEC, int SRC, int EPI, int kUnroll>
 __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
   using V = Vec<VEC>;
   using T = typename V::T;
   constexpr int P = kBlock / G;
-  constexpr int kUnroll = EPI == kEpiFwd ? kFwdUnroll : kBwdUnroll;
   __shared__ uint32_t s_key[kBlock + 2];  // [0]: entry before, [257]: after
   __shared__ uint64_t s_ent[kBlock];
   __shared__ T s_part[2 * P][G];
@@ -784,11 +773,14 @@ SegBuffers TakeSegBuffers(Arena& ws, int64_t n, int64_t dim) {
   return b;
 }
 
-// Launches SegReduce + SegFinish for the layout picked for `dim`.
+// Launches SegReduce + SegFinish for the layout picked for `dim`; `one_hot`
+// selects the wide unroll.
 template <int SRC, int EPI>
 int LaunchSeg(const StreamArgs& st, RowArgs r, const SegBuffers& sb, int g,
-              int vec, const char* reduce_span, const char* finish_span,
-              hipStream_t stream) {
+              int vec, bool one_hot, const char* reduce_span,
+              const char* finish_span, hipStream_t stream) {
+  constexpr int kWide = EPI == kEpiFwd ? kFwdUnrollWide : kBwdUnrollWide;
+  constexpr int kNarrow = EPI == kEpiFwd ? kFwdUnrollNarrow : kBwdUnrollNarrow;
   r.partials = sb.partials;
   r.block_flags = sb.flags;
   r.block_keys = sb.keys;
@@ -796,8 +788,13 @@ int LaunchSeg(const StreamArgs& st, RowArgs r, const SegBuffers& sb, int g,
 #define SCEMB_SEG_CASE(GG, VV)                                                \
   if (g == GG && vec == VV) {                                                \
     int prof = ProfileBegin(reduce_span, stream);                            \
-    hipLaunchKernelGGL((SegReduce<GG, VV, SRC, EPI>), grid, dim3(kBlock), 0,  \
-                       stream, st, r);                                        \
+    if (one_hot) {                                                           \
+      hipLaunchKernelGGL((SegReduce<GG, VV, SRC, EPI, kWide>), grid,          \
+                         dim3(kBlock), 0, stream, st, r);                     \
+    } else {                                                                 \
+      hipLaunchKernelGGL((SegReduce<GG, VV, SRC, EPI, kNarrow>), grid,        \
+                         dim3(kBlock), 0, stream, st, r);                     \
+    }                                                                        \
     ProfileEnd(prof, stream);                                                 \
     SCEMB_LAUNCH_CHECK();                                                     \
     prof = ProfileBegin(finish_span, stream);                                 \
@@ -892,8 +889,12 @@ int ForwardImpl(const scemb_csr_t* csr, const scemb_sample_view_t* view,
   r.status = status;
   int g, vec;
   PickLayout(dim, Aligned16(table) && Aligned16(act), &g, &vec);
-  return LaunchSeg<kSrcSorted, kEpiFwd>(st, r, sb, g, vec, "fwd_reduce",
-                                        "fwd_finish", stream);
+  const int64_t hint = view != nullptr ? view->num_entries
+                                        : csr->num_entries;
+  const int64_t entries = hint > 0 && hint < st.n ? hint : st.n;
+  const bool one_hot = entries <= kOneHotMaxEntriesPerRow * batch;
+  return LaunchSeg<kSrcSorted, kEpiFwd>(st, r, sb, g, vec, one_hot,
+                                        "fwd_reduce", "fwd_finish", stream);
 }
 
 template <int EPI>
@@ -951,15 +952,18 @@ int GradImpl(const scemb_csr_t* csr, const float* act_grad, int64_t batch,
   r.opt = opt;
   r.status = status;
   // Entries per activation row: how often each gradient row is gathered.
-  r.stream_src = n <= kNtGradMaxReuse * batch;
+  const int64_t entries =
+      csr->num_entries > 0 && csr->num_entries < n ? csr->num_entries : n;
+  const bool one_hot = entries <= kOneHotMaxEntriesPerRow * batch;
+  r.stream_src = one_hot;
   int g, vec;
   PickLayout(dim, Aligned16(table) && Aligned16(act_grad) &&
                       (EPI != kEpiAdagrad || Aligned16(accum)), &g, &vec);
   if (direct) {
-    return LaunchSeg<kSrcCsr, EPI>(st, r, sb, g, vec, "bwd_reduce",
+    return LaunchSeg<kSrcCsr, EPI>(st, r, sb, g, vec, one_hot, "bwd_reduce",
                                    "bwd_finish", stream);
   }
-  return LaunchSeg<kSrcSorted, EPI>(st, r, sb, g, vec, "bwd_reduce",
+  return LaunchSeg<kSrcSorted, EPI>(st, r, sb, g, vec, one_hot, "bwd_reduce",
                                     "bwd_finish", stream);
 }
 

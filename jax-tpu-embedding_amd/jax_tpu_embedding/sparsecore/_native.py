@@ -66,6 +66,7 @@ class Csr(ctypes.Structure):
       ("num_partitions", ctypes.c_int32),
       ("row_pointers_per_segment", ctypes.c_int32),
       ("flags", ctypes.c_uint32),
+      ("num_entries", ctypes.c_int64),
   ]
 
 
@@ -76,6 +77,7 @@ class SampleView(ctypes.Structure):
       ("size", ctypes.c_int64),
       ("device_batch_size", ctypes.c_int64),
       ("table_rows", ctypes.c_int64),
+      ("num_entries", ctypes.c_int64),
   ]
 
 
@@ -292,7 +294,10 @@ WORKSPACE = _Workspace()
 
 
 def make_csr(row_pointers, embedding_ids, sample_ids, gains, num_segments,
-             num_partitions, sorted_by_row: bool = False) -> Csr:
+             num_partitions, sorted_by_row: bool = False,
+             num_entries: int | None = None) -> Csr:
+  """`num_entries`: the valid entries of the buffers when known (it only
+  picks kernel variants)."""
   rp_len = int(row_pointers.numel())
   if rp_len % num_segments:
     raise ValueError("row_pointers length must be divisible by "
@@ -300,23 +305,26 @@ def make_csr(row_pointers, embedding_ids, sample_ids, gains, num_segments,
   return Csr(ptr(row_pointers), ptr(embedding_ids), ptr(sample_ids),
              ptr(gains), int(embedding_ids.numel()), num_segments,
              num_partitions, rp_len // num_segments,
-             CSR_SORTED_BY_ROW if sorted_by_row else 0)
+             CSR_SORTED_BY_ROW if sorted_by_row else 0,
+             int(num_entries) if num_entries else 0)
 
 
 class LookupView:
   """Device buffers of a sample view (scemb_sample_view_t) plus the
   (device_batch_size, table_rows) pair it was built for."""
 
-  def __init__(self, keys, entries, device_batch_size: int, table_rows: int):
+  def __init__(self, keys, entries, device_batch_size: int, table_rows: int,
+               num_entries: int = 0):
     self.keys = keys          # int32 tensor holding the uint32 keys
     self.entries = entries    # int64 tensor holding the packed entries
     self.device_batch_size = int(device_batch_size)
     self.table_rows = int(table_rows)
+    self.num_entries = int(num_entries)
 
   def as_struct(self) -> SampleView:
     return SampleView(ptr(self.keys), ptr(self.entries),
                       int(self.keys.numel()), self.device_batch_size,
-                      self.table_rows)
+                      self.table_rows, self.num_entries)
 
 
 def build_sample_view(csr: Csr, batch: int, table_rows: int,
@@ -336,7 +344,7 @@ def build_sample_view(csr: Csr, batch: int, table_rows: int,
   check(lib.scemb_build_sample_view(
       ctypes.byref(csr), batch, table_rows, ptr(keys), ptr(entries), ptr(ws),
       ws.numel(), ptr(device_status), stream_handle()))
-  return LookupView(keys, entries, batch, table_rows)
+  return LookupView(keys, entries, batch, table_rows, csr.num_entries)
 
 
 def sparse_dense_matmul(csr: Csr | None, table, activations, batch: int,

@@ -15,11 +15,13 @@ def resolve_sparsecores(num_sc_per_device, global_device_count):
 
 
 def csr_operands(row_pointers, embedding_ids, sample_ids, gains,
-                 num_sc_per_device, num_partitions, sorted_by_row=False):
+                 num_sc_per_device, num_partitions, sorted_by_row=False,
+                 num_entries=None):
   """Device tensors for the CSR buffers plus the C struct that points at
   them (the tensors must stay alive while the struct is used).
   `sorted_by_row` declares the entries ascending by (partition, embedding
-  id) inside each segment, as the preprocessing writes them."""
+  id) inside each segment, as the preprocessing writes them; `num_entries`
+  the count of valid entries when known (it only picks kernel variants)."""
   t = _native.require_gpu()
   dev = _native.device()
   rp = _native.as_device_tensor(row_pointers, t.int32, dev).reshape(-1)
@@ -27,7 +29,7 @@ def csr_operands(row_pointers, embedding_ids, sample_ids, gains,
   sid = _native.as_device_tensor(sample_ids, t.int32, dev).reshape(-1)
   g = _native.as_device_tensor(gains, t.float32, dev).reshape(-1)
   csr = _native.make_csr(rp, eid, sid, g, num_sc_per_device, num_partitions,
-                         sorted_by_row=sorted_by_row)
+                         sorted_by_row=sorted_by_row, num_entries=num_entries)
   return (rp, eid, sid, g), csr
 
 

@@ -12,7 +12,9 @@ the hardware): ``num_sc_per_device`` and ``global_device_count`` give the CSR
 segment / partition counts (defaults: the device's SparseCore count, 1);
 ``lookup_view`` is an optional ``_native.LookupView`` of the same CSR (built
 by the preprocessing), which spares the call its grouping sort. A view built
-for another batch size or table height is ignored.
+for another batch size or table height is ignored. ``csr_num_entries``, the
+CSR's entry count when known, picks the kernel variant (one-hot or
+multi-hot batches) and changes no result.
 """
 
 from __future__ import annotations
@@ -51,7 +53,7 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
           max_ids_per_partition: int, max_unique_ids_per_partition: int,
           sharding_strategy: int = 1, quantization_config=None,
           enable_minibatching: bool = False, num_sc_per_device=None,
-          global_device_count=None, lookup_view=None):
+          global_device_count=None, lookup_view=None, csr_num_entries=None):
   utils.validate_abstract_eval_params(
       lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
       lhs_gains, num_minibatches_per_physical_sparse_core, embedding_table,
@@ -68,7 +70,8 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
   t = _native.require_gpu()
   s, ns = _device.resolve_sparsecores(num_sc_per_device, global_device_count)
   keep, csr = _device.csr_operands(lhs_row_pointers, lhs_local_embedding_ids,
-                                   lhs_local_sample_ids, lhs_gains, s, ns)
+                                   lhs_local_sample_ids, lhs_gains, s, ns,
+                                   num_entries=csr_num_entries)
   table = _device.device_table(embedding_table)
   shape = ((device_batch_size,) if table.dim() == 1 else
            (device_batch_size, int(table.shape[1])))

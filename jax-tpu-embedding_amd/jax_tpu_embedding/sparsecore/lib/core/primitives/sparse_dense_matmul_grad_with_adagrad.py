@@ -14,6 +14,8 @@ Extra keyword arguments besides ``num_sc_per_device`` /
 preprocessing writes it (entries ascending by partition and embedding id);
 with one SparseCore segment the kernel then reads it in place instead of
 sorting a copy (a violated order is reported, not silently used).
+``csr_num_entries``, the CSR's entry count when known, picks the kernel
+variant (one-hot or multi-hot batches) and changes no result.
 """
 
 from __future__ import annotations
@@ -33,7 +35,8 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
           computation_name: str = "adagrad_optimizer_update",
           sharding_strategy: int = 1, enable_minibatching: bool = False,
           min_value=None, max_value=None, num_sc_per_device=None,
-          global_device_count=None, csr_sorted_by_row: bool = False):
+          global_device_count=None, csr_sorted_by_row: bool = False,
+          csr_num_entries=None):
   utils.validate_abstract_eval_params(
       lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
       lhs_gains, num_minibatches_per_physical_sparse_core, embedding_table,
@@ -53,7 +56,8 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
   s, ns = _device.resolve_sparsecores(num_sc_per_device, global_device_count)
   keep, csr = _device.csr_operands(lhs_row_pointers, lhs_local_embedding_ids,
                                    lhs_local_sample_ids, lhs_gains, s, ns,
-                                   sorted_by_row=csr_sorted_by_row)
+                                   sorted_by_row=csr_sorted_by_row,
+                                   num_entries=csr_num_entries)
   table = _device.device_table(embedding_table)
   acc = _device.device_table(accumulator)
   grad = _native.as_device_tensor(activations_grad, t.float32, table.device)

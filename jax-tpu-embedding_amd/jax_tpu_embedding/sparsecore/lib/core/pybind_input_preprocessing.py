@@ -40,6 +40,9 @@ class SparseDenseMatmulInputStats:
     self.max_unique_ids_per_partition = {}
     self.required_buffer_sizes = {}
     self.dropped_id_count = {}
+    # No reference counterpart: grouped CSR entries per stacked table (an
+    # upper bound on the valid entries; lets the lookup pick its kernels).
+    self.num_entries = {}
 
   def TotalDroppedIdCount(self) -> int:  # pylint: disable=invalid-name
     return int(sum(self.dropped_id_count.values()))
@@ -378,6 +381,7 @@ def preprocess_sparse_dense_matmul_input(
     stats.required_buffer_sizes[name] = stats_np[2 * L * ns:2 * L * ns +
                                                  L * S].copy()
     stats.dropped_id_count[name] = int(counters[0])
+    stats.num_entries[name] = int(counters[3])
     if has_leading_dimension:
       rp, eid, sid, gains = (rp.reshape(L, -1), eid.reshape(L, -1),
                              sid.reshape(L, -1), gains.reshape(L, -1))

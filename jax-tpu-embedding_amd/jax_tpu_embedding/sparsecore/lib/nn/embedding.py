@@ -101,7 +101,9 @@ class PreprocessedInput:
       by activation row (spares the forward pass its grouping sort);
     csr_sorted_by_row: the CSR entries are ascending by (partition, embedding
       id) in every segment, as the preprocessing writes them (lets the
-      backward pass read the CSR in place).
+      backward pass read the CSR in place);
+    csr_num_entries: stack name -> number of CSR entries (lets the lookup
+      pick the kernel variant for one-hot or multi-hot batches).
   A PreprocessedInput built from other CSR buffers leaves both unset.
   """
 
@@ -110,6 +112,7 @@ class PreprocessedInput:
       default_factory=lambda: np.array(1))
   lookup_views: dict | None = None
   csr_sorted_by_row: bool = False
+  csr_num_entries: dict | None = None
 
   @property
   def lhs_row_pointers(self):
@@ -304,17 +307,19 @@ def preprocess_sparse_dense_matmul_input(
   if has_leading_dimension:
     minibatches = minibatches.reshape(local_device_count, 1)
   views = None
+  counts = dict(stats.num_entries) if local_device_count == 1 else None
   if local_device_count == 1:
     views = _build_lookup_views(csr, feature_specs, global_device_count,
-                                num_sc_per_device)
+                                num_sc_per_device, counts)
   return (PreprocessedInput(SparseDenseMatmulInput(*csr), minibatches,
                             lookup_views=views,
-                            csr_sorted_by_row=local_device_count == 1),
+                            csr_sorted_by_row=local_device_count == 1,
+                            csr_num_entries=counts),
           SparseDenseMatmulInputStats.from_cc(stats))
 
 
 def _build_lookup_views(csr, feature_specs, global_device_count: int,
-                        num_sc_per_device: int):
+                        num_sc_per_device: int, counts):
   """Sample views of one device's CSR buffers, one per stacked table, for a
   table shard of stack_vocab_size / global_device_count rows."""
   rp, eid, sid, gains = csr
@@ -324,7 +329,8 @@ def _build_lookup_views(csr, feature_specs, global_device_count: int,
     rows = spec.stack_vocab_size // global_device_count
     _, c = _device.csr_operands(rp[name], eid[name], sid[name], gains[name],
                                 num_sc_per_device,
-                                num_sc_per_device * global_device_count)
+                                num_sc_per_device * global_device_count,
+                                num_entries=counts.get(name))
     views[name] = _native.build_sample_view(c, batch, rows)
   return views
 
@@ -392,6 +398,7 @@ def tpu_sparse_dense_matmul(preprocessed_inputs, embedding_variables,
   strategy = int(sharding_strategy_to_enum(sharding_strategy))
   nmb = _resolve_scalar_minibatches(preprocessed_inputs.num_minibatches)
   views = getattr(preprocessed_inputs, "lookup_views", None) or {}
+  counts = getattr(preprocessed_inputs, "csr_num_entries", None) or {}
   acts = {}
   for name, spec in stacked.items():
     ev = embedding_variables[name]
@@ -411,7 +418,8 @@ def tpu_sparse_dense_matmul(preprocessed_inputs, embedding_variables,
                         enable_minibatching=enable_minibatching,
                         num_sc_per_device=num_sc_per_device,
                         global_device_count=global_device_count,
-                        lookup_view=views.get(name)))
+                        lookup_view=views.get(name),
+                        csr_num_entries=counts.get(name)))
   if perform_unstacking:
     acts = unstack_embedding_activations(acts, feature_specs,
                                          global_device_count,
@@ -528,6 +536,8 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
         num_sc_per_device=num_sc_per_device, global_device_count=g_count,
         csr_sorted_by_row=bool(
             getattr(preprocessed_inputs, "csr_sorted_by_row", False)),
+        csr_num_entries=(getattr(preprocessed_inputs, "csr_num_entries",
+                                 None) or {}).get(name),
         **kwargs)
     res = res if isinstance(res, tuple) else (res,)
     out[name] = EmbeddingVariables(res[0], tuple(res[1:]))

@@ -175,7 +175,8 @@ def test_config_full_size(cfg):
         pre.lhs_sample_ids[name], pre.lhs_gains[name], 1, table,
         device_batch_size=bs, max_ids_per_partition=spec.max_ids_per_partition,
         max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
-        num_sc_per_device=1, lookup_view=pre.lookup_views[name])
+        num_sc_per_device=1, lookup_view=pre.lookup_views[name],
+        csr_num_entries=pre.csr_num_entries[name])
     _check_forward(act, table, eid, sid, gains,
                    _sample(rng, np.arange(bs), 1024), dim)
     del act
@@ -199,7 +200,8 @@ def test_config_full_size(cfg):
            pre.lhs_sample_ids[name], pre.lhs_gains[name])
     kw = dict(max_ids_per_partition=spec.max_ids_per_partition,
               max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
-              num_sc_per_device=1, csr_sorted_by_row=pre.csr_sorted_by_row)
+              num_sc_per_device=1, csr_sorted_by_row=pre.csr_sorted_by_row,
+              csr_num_entries=pre.csr_num_entries[name])
     if adagrad:
       ada_prim.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
           *csr, 1, table, acc, grad, lr, **kw)

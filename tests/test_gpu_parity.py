@@ -203,18 +203,32 @@ def _csr_from_oracle(features, weights, feats, num_sc):
   return name, ref
 
 
-def _fwd_bind(ref, name, table_t, batch, num_sc, view=None):
+def _entry_count(rp, num_sc):
+  """Valid entries of a CSR: per segment, partition p holds
+  [roundup8(rp[p-1]), rp[p])."""
+  total = 0
+  for seg in np.split(np.asarray(rp), num_sc):
+    start = 0
+    for end in seg:
+      total += max(0, int(end) - start)
+      start = max(start, (int(end) + 7) // 8 * 8)
+  return total
+
+
+def _fwd_bind(ref, name, table_t, batch, num_sc, view=None,
+              num_entries=None):
   return fwd_prim.tpu_sparse_dense_matmul_csr_primitive.bind(
       ref.row_pointers[name], ref.embedding_ids[name], ref.sample_ids[name],
       ref.gains[name], 1, table_t, device_batch_size=batch,
       max_ids_per_partition=1 << 20, max_unique_ids_per_partition=1 << 20,
-      num_sc_per_device=num_sc, lookup_view=view)
+      num_sc_per_device=num_sc, lookup_view=view, csr_num_entries=num_entries)
 
 
-def _view(ref, name, batch, rows, num_sc):
+def _view(ref, name, batch, rows, num_sc, num_entries=None):
   keep, c = _device.csr_operands(ref.row_pointers[name],
                                  ref.embedding_ids[name], ref.sample_ids[name],
-                                 ref.gains[name], num_sc, num_sc)
+                                 ref.gains[name], num_sc, num_sc,
+                                 num_entries=num_entries)
   v = _native.build_sample_view(c, batch, rows)
   torch.cuda.synchronize()
   del keep
@@ -235,7 +249,9 @@ def test_forward_matches_oracle(dim, num_sc, integer):
   _, feats = _make_specs(1, [vocab], [dim], "sum" if integer else "mean",
                          embedding_spec.SGDOptimizerSpec(0.01), batch)
   embedding.prepare_feature_specs_for_training(feats, 1, num_sc)
-  features = [_ragged(rng, batch, 0, 40, vocab, zipf_a=1.1)]
+  # Integer cases: one id per sample (one-hot kernels), float: 0-40 ids.
+  features = [_ragged(rng, batch, 1 if integer else 0, 1 if integer else 40,
+                      vocab, zipf_a=1.1)]
   name, ref = _csr_from_oracle(features, None, feats, num_sc)
   rows = feats[0].table_spec.stacked_table_spec.stack_vocab_size
   if integer:
@@ -245,9 +261,14 @@ def test_forward_matches_oracle(dim, num_sc, integer):
   if dim == 1:
     table = table.reshape(rows)
   table_t = torch.from_numpy(table).cuda()
-  act = _fwd_bind(ref, name, table_t, batch, num_sc).cpu().numpy()
+  # The entry count (known to the preprocessing) selects the one-hot kernel
+  # variants for the one-id-per-sample cases.
+  count = _entry_count(ref.row_pointers[name], num_sc)
+  act = _fwd_bind(ref, name, table_t, batch, num_sc,
+                  num_entries=count).cpu().numpy()
   act_v = _fwd_bind(ref, name, table_t, batch, num_sc,
-                    view=_view(ref, name, batch, rows, num_sc)).cpu().numpy()
+                    view=_view(ref, name, batch, rows, num_sc, count),
+                    num_entries=count).cpu().numpy()
   exp = refcpu.sparse_dense_matmul(
       ref.row_pointers[name], ref.embedding_ids[name], ref.sample_ids[name],
       ref.gains[name], table, batch, num_sc_per_device=num_sc, num_scs=num_sc)
@@ -311,14 +332,16 @@ def test_forward_empty_batch_is_zero():
 def _run_grad(optimizer, csr, grad, table0, acc0, lr, lo, hi, num_sc,
               sorted_by_row=False):
   """Runs the GPU primitive and the oracle; returns (got, expected) pairs.
-  `sorted_by_row` lets the kernel read the CSR in place (one segment)."""
+  `sorted_by_row` lets the kernel read the CSR in place (one segment); the
+  entry count is passed as the preprocessing would."""
   table = torch.from_numpy(table0.copy()).cuda()
+  count = _entry_count(csr[0], num_sc)
   if optimizer == "sgd":
     out = sgd_prim.tpu_sparse_dense_matmul_grad_with_sgd_primitive.bind(
         *csr, 1, table, torch.from_numpy(grad).cuda(), lr,
         max_ids_per_partition=1 << 20, max_unique_ids_per_partition=1 << 20,
         min_value=lo, max_value=hi, num_sc_per_device=num_sc,
-        csr_sorted_by_row=sorted_by_row)
+        csr_sorted_by_row=sorted_by_row, csr_num_entries=count)
     assert out is table
     exp_t = refcpu.sparse_dense_matmul_grad(
         *csr, grad, table0, None, learning_rate=lr,
@@ -330,7 +353,7 @@ def _run_grad(optimizer, csr, grad, table0, acc0, lr, lo, hi, num_sc,
           *csr, 1, table, acc, torch.from_numpy(grad).cuda(), np.float32(lr),
           max_ids_per_partition=1 << 20, max_unique_ids_per_partition=1 << 20,
           min_value=lo, max_value=hi, num_sc_per_device=num_sc,
-          csr_sorted_by_row=sorted_by_row))
+          csr_sorted_by_row=sorted_by_row, csr_num_entries=count))
   assert out_t is table and out_a is acc
   exp_t, exp_a = refcpu.sparse_dense_matmul_grad(
       *csr, grad, table0, acc0, learning_rate=lr, num_sc_per_device=num_sc,
@@ -356,7 +379,10 @@ def test_grad_hot_rows_exact(optimizer, dim, num_sc, sorted_by_row, clip):
   _, feats = _make_specs(1, [vocab], [dim], "sum",
                          embedding_spec.SGDOptimizerSpec(0.01), batch)
   embedding.prepare_feature_specs_for_training(feats, 1, num_sc)
-  features = [_ragged(rng, batch, 1, 8, vocab, zipf_a=1.05)]
+  # Clipped cases use one id per sample (the kernels' one-hot variants),
+  # unclipped ones 1-8 ids (the multi-hot variants).
+  hi_len = 1 if clip else 8
+  features = [_ragged(rng, batch, 1, hi_len, vocab, zipf_a=1.05)]
   name, ref = _csr_from_oracle(features, None, feats, num_sc)
   rows = feats[0].table_spec.stacked_table_spec.stack_vocab_size
   shape = (rows,) if dim == 1 else (rows, dim)
