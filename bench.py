@@ -298,7 +298,8 @@ def _stack_batch_ids(w: Workload):
   return out
 
 
-def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False):
+def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
+            api: bool = True):
   import torch  # pylint: disable=g-import-not-at-top
 
   from jax_tpu_embedding.sparsecore import _native  # pylint: disable=g-import-not-at-top
@@ -414,6 +415,12 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False):
   _native.profile_collect(None)
   timed(steps, False)
   _native.profile_enable(False)
+  api_ms = api_copy_ms = None
+  if api:
+    api_ms, api_copy_ms = _api_steps(w, pre, state, stacked, steps, warmup,
+                                     timed_fn=torch.cuda.synchronize)
+    log(f"API step (per-feature tensors): fused stacking {api_ms:.4f} ms, "
+        f"with stacking copies {api_copy_ms:.4f} ms")
   spans = {}
   for k in ("fwd_reduce", "fwd_finish", "bwd_reduce", "bwd_finish",
             "fwd_call", "bwd_call"):
@@ -423,6 +430,8 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False):
   log(f"step: {ms_per_step:.4f} ms; per-step spans " +
       ", ".join(f"{k} {v[0]:.4f}" for k, v in spans.items()))
   return {
+      "api_ms_per_step": api_ms,
+      "api_copy_ms_per_step": api_copy_ms,
       "csr_only_ms_per_step": csr_only_ms,
       "ms_per_step": ms_per_step,
       "lookups": lookups,
@@ -431,6 +440,62 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False):
       "per_stack": per_stack,
       "dropped": int(sum(stats.id_drop_counters.values())),
   }
+
+
+def _api_steps(w, pre, state, stacked, steps, warmup, timed_fn):
+  """The same step through the embedding API with per-feature activations
+  and gradients (what a training loop sees): once with the stacking fused
+  into the kernels (the default), once with the stacked-matrix path and the
+  unstack / stack copies. Returns (fused ms, copy ms) per step."""
+  import torch  # pylint: disable=g-import-not-at-top
+
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-import-not-at-top
+
+  specs = w.feature_specs
+  variables = {}
+  grads = []
+  for name in stacked:
+    t, a, _, _ = state[name]
+    variables[name] = embedding.EmbeddingVariables(
+        t, (a,) if a is not None else ())
+  for fs in specs:
+    _, _, g, _ = state[fs.table_spec.stacked_table_spec.stack_name]
+    rows = fs.output_shape[0]
+    off = fs.id_transformation.row_offset
+    grads.append(g[off:off + rows, :fs.table_spec.embedding_dim].contiguous())
+
+  def fused():
+    embedding.tpu_sparse_dense_matmul(pre, variables, specs,
+                                      global_device_count=1,
+                                      num_sc_per_device=1)
+    embedding.tpu_sparse_dense_matmul_grad(grads, pre, variables, specs,
+                                           global_device_count=1,
+                                           num_sc_per_device=1)
+
+  def copies():
+    acts = embedding.tpu_sparse_dense_matmul(
+        pre, variables, specs, global_device_count=1, num_sc_per_device=1,
+        perform_unstacking=False)
+    outs = embedding.unstack_embedding_activations(acts, specs, 1, 1)
+    for o in outs:  # a training loop consumes contiguous activations
+      o.contiguous()
+    sg = embedding.stack_embedding_gradients(grads, specs, 1)
+    embedding.tpu_sparse_dense_matmul_grad(
+        sg, pre, variables, specs, global_device_count=1,
+        num_sc_per_device=1, perform_stacking=False)
+
+  out = []
+  for fn in (fused, copies):
+    for _ in range(warmup):
+      fn()
+    timed_fn()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+      fn()
+    timed_fn()
+    out.append((time.perf_counter() - t0) * 1e3 / steps)
+  del torch
+  return tuple(out)
 
 
 def algorithmic_bytes(per_stack):
@@ -574,6 +639,8 @@ def main():
   ap.add_argument("--no-cpu-baseline", action="store_true")
   ap.add_argument("--copy-probe", action="store_true",
                   help="run a 1 GiB device copy first (counter calibration)")
+  ap.add_argument("--no-api-steps", action="store_true",
+                  help="skip timing the step through the embedding API")
   ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS),
                   help="BASELINE.json config (c2, the 26-table DLRM shape, "
                        "is the headline)")
@@ -585,7 +652,8 @@ def main():
   t_setup = time.perf_counter()
   w = WORKLOADS[args.workload]()
   log(f"workload built in {time.perf_counter() - t_setup:.1f} s")
-  res = run_gpu(w, args.steps, args.warmup, probe=args.copy_probe)
+  res = run_gpu(w, args.steps, args.warmup, probe=args.copy_probe,
+                api=not args.no_api_steps)
   fwd_bytes, bwd_bytes = algorithmic_bytes(res["per_stack"])
   step_s = res["ms_per_step"] / 1e3
   sp = res["spans"]
@@ -630,6 +698,12 @@ def main():
       "warmup": args.warmup,
       "ms_per_step": round(res["ms_per_step"], 4),
       "csr_only_ms_per_step": round(res["csr_only_ms_per_step"], 4),
+      # The same step through the embedding API with per-feature tensors:
+      # stacking fused into the kernels, and with unstack / stack copies.
+      "api_ms_per_step": (round(res["api_ms_per_step"], 4)
+                          if res["api_ms_per_step"] else None),
+      "api_copy_ms_per_step": (round(res["api_copy_ms_per_step"], 4)
+                               if res["api_copy_ms_per_step"] else None),
       "higher_is_better": True,
       "scaling": "weak",
       "vs_baseline": None,

@@ -13,6 +13,10 @@
  *       lowered at lib/core/primitives/sparse_dense_matmul_csr.py:171-201
  *   scemb_build_sample_view                no counterpart (the SparseCore
  *       groups by sample in hardware); optional input of the forward
+ *   scemb_*_to_blocks / *_from_blocks       the same ops with the activation
+ *       unstacking (lib/nn/embedding.py:903-1044) and gradient stacking
+ *       (:1200-1294) fused in: per-feature row blocks instead of one stacked
+ *       matrix
  *   scemb_sparse_dense_matmul_grad_with_sgd  custom call
  *       "SparseDenseMatmulGradOpWithOptimizerUpdate" with the SGD update
  *       computation, lib/core/primitives/sparse_dense_matmul_grad_with_sgd.py:
@@ -106,6 +110,23 @@ typedef struct scemb_sample_view {
   int64_t num_entries;      /* as scemb_csr_t.num_entries */
 } scemb_sample_view_t;
 
+/* One feature's rows of a stacked activation (or activation-gradient)
+ * matrix of device_batch_size x dim: stacked rows [first_row, first_row +
+ * num_rows) are rows 0.. of `data`, row_stride floats apart, holding the
+ * first `width` columns (the feature's own dim; the remaining dim - width
+ * are stacking padding: the forward does not write them, the backward reads
+ * them as zero). Blocks are ascending in first_row and disjoint; rows in no
+ * block are not written (forward) or contribute nothing (backward). */
+typedef struct scemb_row_block {
+  int64_t first_row;
+  int64_t num_rows;
+  float* data;
+  int64_t row_stride;
+  int32_t width;
+  int32_t reserved;
+} scemb_row_block_t;
+#define SCEMB_MAX_ROW_BLOCKS 32
+
 /* ---- Forward: SparseDenseMatmulOp --------------------------------------
  * activations[b, :] = sum over entries with s*bps + sample_id == b of
  *   gain * table[p * (table_rows / num_partitions) + embedding_id, :],
@@ -129,6 +150,14 @@ int scemb_sparse_dense_matmul(const scemb_csr_t* csr,
                               int64_t device_batch_size, void* workspace,
                               size_t workspace_bytes, uint32_t* device_status,
                               void* stream);
+/* The same, writing each activation row into its feature's block (the
+ * unstacked per-feature outputs); workspace as for the call above. */
+int scemb_sparse_dense_matmul_to_blocks(
+    const scemb_csr_t* csr, const scemb_sample_view_t* view,
+    const float* table, int64_t table_rows, int32_t dim,
+    const scemb_row_block_t* outputs, int32_t num_outputs,
+    int64_t device_batch_size, void* workspace, size_t workspace_bytes,
+    uint32_t* device_status, void* stream);
 
 /* Builds the sample view of a CSR into keys[coo_size] / entries[coo_size]
  * (device memory owned by the caller). Invalid entries are flagged as in the
@@ -172,6 +201,22 @@ int scemb_sparse_dense_matmul_grad_with_adagrad(
     int64_t table_rows, int32_t dim, const float* learning_rate,
     float learning_rate_value, int32_t clip_mask, float min_value,
     float max_value, void* workspace, size_t workspace_bytes,
+    uint32_t* device_status, void* stream);
+/* The same two updates reading the activation gradients from per-feature
+ * blocks (no stacked gradient matrix); workspace as above. */
+int scemb_sparse_dense_matmul_grad_with_sgd_from_blocks(
+    const scemb_csr_t* csr, const scemb_row_block_t* activation_grads,
+    int32_t num_blocks, int64_t device_batch_size, float* table,
+    int64_t table_rows, int32_t dim, const float* learning_rate,
+    float learning_rate_value, int32_t clip_mask, float min_value,
+    float max_value, void* workspace, size_t workspace_bytes,
+    uint32_t* device_status, void* stream);
+int scemb_sparse_dense_matmul_grad_with_adagrad_from_blocks(
+    const scemb_csr_t* csr, const scemb_row_block_t* activation_grads,
+    int32_t num_blocks, int64_t device_batch_size, float* table,
+    float* accumulator, int64_t table_rows, int32_t dim,
+    const float* learning_rate, float learning_rate_value, int32_t clip_mask,
+    float min_value, float max_value, void* workspace, size_t workspace_bytes,
     uint32_t* device_status, void* stream);
 
 /* ---- Preprocessing: PreprocessSparseDenseMatmulInput, one stacked table --

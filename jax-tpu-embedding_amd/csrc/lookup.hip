@@ -241,6 +241,22 @@ struct StreamArgs {
   int64_t n;
 };
 
+constexpr int kMaxRowBlocks = SCEMB_MAX_ROW_BLOCKS;
+
+// The activation matrix (forward output, backward input) as per-feature row
+// blocks: stacked rows [first, end) of block b live at data[b] with
+// stride[b] floats between rows and width[b] leading columns (the rest of
+// the dim columns are padding: not written, read as zero). n == 0: one
+// dense [batch, dim] matrix.
+struct RowMap {
+  int32_t n;
+  int64_t first[kMaxRowBlocks];
+  int64_t end[kMaxRowBlocks];
+  int64_t stride[kMaxRowBlocks];
+  int32_t width[kMaxRowBlocks];
+  float* data[kMaxRowBlocks];
+};
+
 // What the reduction reads and writes.
 struct RowArgs {
   const float* src;  // gathered rows
@@ -249,6 +265,7 @@ struct RowArgs {
   int64_t dim;
   int64_t batch;     // forward: rows of dst
   bool stream_src;   // gathered rows are read about once: nontemporal loads
+  RowMap act;        // activation layout (dst forward, src backward)
   OptParams opt;
   float* partials;   // [2 * num_blocks, dim]
   uint32_t* block_flags;
@@ -302,17 +319,63 @@ __device__ __forceinline__ float UpdateOne(float t, float* a, float g,
   return v;
 }
 
+// The row map staged in LDS by every block that reads or writes
+// activations through it.
+struct RowMapLds {
+  int32_t n;
+  int64_t first[kMaxRowBlocks];
+  int64_t end[kMaxRowBlocks];
+  int64_t stride[kMaxRowBlocks];
+  int32_t width[kMaxRowBlocks];
+  float* data[kMaxRowBlocks];
+};
+
+// Copies the row map into LDS; the caller synchronises the block after.
+__device__ __forceinline__ void StageRowMap(const RowMap& m, RowMapLds* s) {
+  const int t = threadIdx.x;
+  if (t == 0) s->n = m.n;
+  if (t < m.n) {
+    s->first[t] = m.first[t];
+    s->end[t] = m.end[t];
+    s->stride[t] = m.stride[t];
+    s->width[t] = m.width[t];
+    s->data[t] = m.data[t];
+  }
+}
+
+// Address of columns [col, col + VEC) of activation row `row`, or null when
+// the row lies in no block or the columns in its padding. Without a map
+// (kMapped false) the activations are one dense matrix.
+template <bool kMapped>
+__device__ __forceinline__ float* ActAddr(const RowMapLds& m, float* dense,
+                                          int64_t dim, int64_t row,
+                                          int64_t col) {
+  if (!kMapped) return dense + row * dim + col;
+  if (m.n == 0) return nullptr;
+  int lo = 0, hi = m.n;  // last block whose first row is <= row
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (m.first[mid] <= row) lo = mid; else hi = mid;
+  }
+  if (row < m.first[lo] || row >= m.end[lo] || col >= m.width[lo]) {
+    return nullptr;
+  }
+  return m.data[lo] + (row - m.first[lo]) * m.stride[lo] + col;
+}
+
 // Epilogue for the finished row `key` at column `col`, given the table and
 // accumulator values already loaded (backward) -- or the store (forward).
-template <int VEC, int EPI>
-__device__ __forceinline__ void Epilogue(const RowArgs& r, uint32_t key,
+template <int VEC, int EPI, bool kMapped>
+__device__ __forceinline__ void Epilogue(const RowArgs& r,
+                                         const RowMapLds& m, uint32_t key,
                                          int64_t col, typename Vec<VEC>::T g,
                                          typename Vec<VEC>::T t,
                                          typename Vec<VEC>::T a, float lr) {
   using V = Vec<VEC>;
   const int64_t off = static_cast<int64_t>(key) * r.dim + col;
   if (EPI == kEpiFwd) {
-    StoreRow<VEC, kNtAct>(r.dst + off, g);
+    float* p = ActAddr<kMapped>(m, r.dst, r.dim, key, col);
+    if (p != nullptr) StoreRow<VEC, kNtAct>(p, g);
     return;
   }
 #pragma unroll
@@ -325,8 +388,9 @@ __device__ __forceinline__ void Epilogue(const RowArgs& r, uint32_t key,
   if (EPI == kEpiAdagrad) StoreRow<VEC, kNtTable>(r.accum + off, a);
 }
 
-template <int VEC, int EPI>
-__device__ __forceinline__ void EpilogueLoad(const RowArgs& r, uint32_t key,
+template <int VEC, int EPI, bool kMapped>
+__device__ __forceinline__ void EpilogueLoad(const RowArgs& r,
+                                             const RowMapLds& m, uint32_t key,
                                              int64_t col,
                                              typename Vec<VEC>::T g,
                                              float lr) {
@@ -335,26 +399,28 @@ __device__ __forceinline__ void EpilogueLoad(const RowArgs& r, uint32_t key,
   const int64_t off = static_cast<int64_t>(key) * r.dim + col;
   if (EPI != kEpiFwd) t = V::Load(r.dst + off);
   if (EPI == kEpiAdagrad) a = V::Load(r.accum + off);
-  Epilogue<VEC, EPI>(r, key, col, g, t, a, lr);
+  Epilogue<VEC, EPI, kMapped>(r, m, key, col, g, t, a, lr);
 }
 
 __device__ __forceinline__ uint64_t LowBits(int k) {
   return k >= 64 ? ~0ull : ((1ull << k) - 1);
 }
 
-template <int G, int VEC>
-__device__ __forceinline__ void ZeroRows(float* dst, int64_t dim, int64_t lo,
-                                         int64_t hi, int cl) {
+template <int G, int VEC, bool kMapped>
+__device__ __forceinline__ void ZeroRows(const RowMapLds& m, float* dst,
+                                         int64_t dim, int64_t lo, int64_t hi,
+                                         int cl) {
   using V = Vec<VEC>;
   for (int64_t row = lo; row < hi; ++row) {
     for (int64_t col = static_cast<int64_t>(cl) * VEC; col < dim;
          col += static_cast<int64_t>(G) * VEC) {
-      StoreRow<VEC, kNtAct>(dst + row * dim + col, V::Zero());
+      float* p = ActAddr<kMapped>(m, dst, dim, row, col);
+      if (p != nullptr) StoreRow<VEC, kNtAct>(p, V::Zero());
     }
   }
 }
 
-template <int G, int VEC, int SRC, int EPI, int kUnroll>
+template <int G, int VEC, int SRC, int EPI, int kUnroll, bool kMapped>
 __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
   using V = Vec<VEC>;
   using T = typename V::T;
@@ -363,6 +429,7 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
   __shared__ uint64_t s_ent[kBlock];
   __shared__ T s_part[2 * P][G];
   __shared__ uint32_t s_info[P];
+  __shared__ RowMapLds s_map;
 
   const int tid = threadIdx.x;
   const int64_t blk = blockIdx.x;
@@ -388,6 +455,7 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
       return;
     }
   }
+  if (kMapped) StageRowMap(r.act, &s_map);
   {
     uint64_t en = 0;
     uint32_t k = kSkip;
@@ -446,14 +514,14 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
       m &= m - 1;
       const int64_t lo = __shfl(static_cast<int>(cp + 1), wshift + l);
       const int64_t hi = __shfl(static_cast<int>(ck), wshift + l);
-      ZeroRows<G, VEC>(r.dst, r.dim, lo, hi, cl);
+      ZeroRows<G, VEC, kMapped>(s_map, r.dst, r.dim, lo, hi, cl);
     }
     const bool tail_gap = mine && e == n - 1 && ck + 1 < r.batch;
     m = (__ballot(tail_gap) >> wshift) & gmask;
     if (m) {
       const int l = __ffsll(static_cast<long long>(m)) - 1;
       const int64_t lo = __shfl(static_cast<int>(ck + 1), wshift + l);
-      ZeroRows<G, VEC>(r.dst, r.dim, lo, r.batch, cl);
+      ZeroRows<G, VEC, kMapped>(s_map, r.dst, r.dim, lo, r.batch, cl);
     }
   }
 
@@ -514,9 +582,14 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
         gn[u] = PackedGain(en);
         v[u] = V::Zero();
         if (val && col_ok) {
+          // Forward: table rows (dense); backward: activation-gradient rows
+          // through the row map.
           const float* p =
-              r.src + static_cast<int64_t>(PackedIndex(en)) * dim + col;
-          v[u] = r.stream_src ? V::LoadNT(p) : V::Load(p);
+              EPI == kEpiFwd
+                  ? r.src + static_cast<int64_t>(PackedIndex(en)) * dim + col
+                  : ActAddr<kMapped>(s_map, const_cast<float*>(r.src), dim,
+                                     PackedIndex(en), col);
+          if (p != nullptr) v[u] = r.stream_src ? V::LoadNT(p) : V::Load(p);
         }
         const bool is_end = val && ((end_m >> idx) & 1);
         const bool first = (start_m & ~1ull & LowBits(idx + 1)) == 0;
@@ -538,7 +611,10 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
           acc = V::Fma(acc, gn[u], v[u]);
           if ((end_m >> idx) & 1) {
             if (fin[u]) {
-              if (col_ok) Epilogue<VEC, EPI>(r, kk[u], col, acc, tv[u], av[u], lr);
+              if (col_ok) {
+                Epilogue<VEC, EPI, kMapped>(r, s_map, kk[u], col, acc, tv[u],
+                                            av[u], lr);
+              }
             } else {
               const bool first = (start_m & ~1ull & LowBits(idx + 1)) == 0;
               s_part[head_cont && first ? 2 * sub : 2 * sub + 1][cl] = acc;
@@ -565,7 +641,7 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
       }
       const uint32_t key = job == 0 ? s_key[1] : s_key[base + cnt];
       if (job == 1 && ended) {
-        if (col_ok) EpilogueLoad<VEC, EPI>(r, key, col, g, lr);
+        if (col_ok) EpilogueLoad<VEC, EPI, kMapped>(r, s_map, key, col, g, lr);
       } else if (col_ok) {
         const int64_t slot = job == 1 ? 2 * blk + 1 : 2 * blk;
         V::Store(r.partials + slot * dim + col, g);
@@ -579,7 +655,7 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
 // finds the block where it ends (the next kFlagHeadEnd; every block between
 // is kFlagMiddle), adds the partial rows in block order and applies the
 // epilogue once.
-template <int G, int VEC, int EPI>
+template <int G, int VEC, int EPI, bool kMapped>
 __global__ __launch_bounds__(kBlock) void SegFinish(int64_t num_blocks,
                                                     RowArgs r) {
   using V = Vec<VEC>;
@@ -588,9 +664,14 @@ __global__ __launch_bounds__(kBlock) void SegFinish(int64_t num_blocks,
   constexpr int kWaves = kBlock / kWave;
   __shared__ T s_part[P][G];
   __shared__ int64_t s_end[kWaves];
+  __shared__ RowMapLds s_map;
   const int64_t blk = blockIdx.x;
   if (!(r.block_flags[blk] & kFlagOwner)) return;
   const int tid = threadIdx.x;
+  if (kMapped) {
+    StageRowMap(r.act, &s_map);
+    __syncthreads();
+  }
   const int sub = tid / G;
   const int cl = tid % G;
   const uint32_t key = r.block_keys[blk];
@@ -654,7 +735,7 @@ __global__ __launch_bounds__(kBlock) void SegFinish(int64_t num_blocks,
     if (sub == 0) {
       T g = s_part[0][cl];
       for (int s = 1; s < P; ++s) g = V::Add(g, s_part[s][cl]);
-      if (col_ok) EpilogueLoad<VEC, EPI>(r, key, col, g, lr);
+      if (col_ok) EpilogueLoad<VEC, EPI, kMapped>(r, s_map, key, col, g, lr);
     }
     __syncthreads();
   }
@@ -773,12 +854,10 @@ SegBuffers TakeSegBuffers(Arena& ws, int64_t n, int64_t dim) {
   return b;
 }
 
-// Launches SegReduce + SegFinish for the layout picked for `dim`; `one_hot`
-// selects the wide unroll.
-template <int SRC, int EPI>
-int LaunchSeg(const StreamArgs& st, RowArgs r, const SegBuffers& sb, int g,
-              int vec, bool one_hot, const char* reduce_span,
-              const char* finish_span, hipStream_t stream) {
+template <int SRC, int EPI, bool kMapped>
+int LaunchSegMapped(const StreamArgs& st, RowArgs r, const SegBuffers& sb,
+                    int g, int vec, bool one_hot, const char* reduce_span,
+                    const char* finish_span, hipStream_t stream) {
   constexpr int kWide = EPI == kEpiFwd ? kFwdUnrollWide : kBwdUnrollWide;
   constexpr int kNarrow = EPI == kEpiFwd ? kFwdUnrollNarrow : kBwdUnrollNarrow;
   r.partials = sb.partials;
@@ -789,17 +868,17 @@ int LaunchSeg(const StreamArgs& st, RowArgs r, const SegBuffers& sb, int g,
   if (g == GG && vec == VV) {                                                \
     int prof = ProfileBegin(reduce_span, stream);                            \
     if (one_hot) {                                                           \
-      hipLaunchKernelGGL((SegReduce<GG, VV, SRC, EPI, kWide>), grid,          \
+      hipLaunchKernelGGL((SegReduce<GG, VV, SRC, EPI, kWide, kMapped>), grid, \
                          dim3(kBlock), 0, stream, st, r);                     \
     } else {                                                                 \
-      hipLaunchKernelGGL((SegReduce<GG, VV, SRC, EPI, kNarrow>), grid,        \
-                         dim3(kBlock), 0, stream, st, r);                     \
+      hipLaunchKernelGGL((SegReduce<GG, VV, SRC, EPI, kNarrow, kMapped>),     \
+                         grid, dim3(kBlock), 0, stream, st, r);               \
     }                                                                        \
     ProfileEnd(prof, stream);                                                 \
     SCEMB_LAUNCH_CHECK();                                                     \
     prof = ProfileBegin(finish_span, stream);                                 \
-    hipLaunchKernelGGL((SegFinish<GG, VV, EPI>), grid, dim3(kBlock), 0,       \
-                       stream, sb.num_blocks, r);                             \
+    hipLaunchKernelGGL((SegFinish<GG, VV, EPI, kMapped>), grid, dim3(kBlock), \
+                       0, stream, sb.num_blocks, r);                          \
     ProfileEnd(prof, stream);                                                 \
     SCEMB_LAUNCH_CHECK();                                                     \
     return 0;                                                                 \
@@ -810,6 +889,22 @@ int LaunchSeg(const StreamArgs& st, RowArgs r, const SegBuffers& sb, int g,
   SCEMB_SEG_CASE(64, 4)
 #undef SCEMB_SEG_CASE
   return Fail(SCEMB_ERR_INVALID_ARGUMENT, "unsupported layout");
+}
+
+// Launches SegReduce + SegFinish for the layout picked for `dim`; `one_hot`
+// selects the wide unroll, `mapped` the kernels that address activations
+// through the row map in `r.act` (which may hold no block at all).
+template <int SRC, int EPI>
+int LaunchSeg(const StreamArgs& st, const RowArgs& r, const SegBuffers& sb,
+              int g, int vec, bool one_hot, bool mapped,
+              const char* reduce_span, const char* finish_span,
+              hipStream_t stream) {
+  if (mapped) {
+    return LaunchSegMapped<SRC, EPI, true>(st, r, sb, g, vec, one_hot,
+                                           reduce_span, finish_span, stream);
+  }
+  return LaunchSegMapped<SRC, EPI, false>(st, r, sb, g, vec, one_hot,
+                                          reduce_span, finish_span, stream);
 }
 
 // Sample-major stream of a CSR into (keys, entries): expand + stable sort.
@@ -830,9 +925,58 @@ int BuildSampleStream(const scemb_csr_t* csr, const Geometry& geo,
                                             stream, in_alt);
 }
 
+// Checks per-feature row blocks against a [batch, dim] activation matrix and
+// packs them for the kernels; *vec4_ok tells whether every block allows
+// 16-byte row accesses.
+int MakeRowMap(const scemb_row_block_t* blocks, int32_t num_blocks,
+               int64_t batch, int32_t dim, RowMap* m, bool* vec4_ok) {
+  if (num_blocks < 0 || num_blocks > kMaxRowBlocks ||
+      (num_blocks > 0 && blocks == nullptr)) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "between 0 and SCEMB_MAX_ROW_BLOCKS row blocks required");
+  }
+  *m = RowMap{};
+  m->n = num_blocks;
+  *vec4_ok = true;
+  int64_t prev_end = 0;
+  for (int32_t b = 0; b < num_blocks; ++b) {
+    const scemb_row_block_t& k = blocks[b];
+    if (k.first_row < prev_end || k.num_rows < 0 ||
+        k.first_row + k.num_rows > batch) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "row blocks must be ascending, disjoint and inside the "
+                  "batch");
+    }
+    if (k.width <= 0 || k.width > dim || k.row_stride < k.width ||
+        (k.num_rows > 0 && k.data == nullptr)) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "row block needs data, 0 < width <= dim and "
+                  "row_stride >= width");
+    }
+    m->first[b] = k.first_row;
+    m->end[b] = k.first_row + k.num_rows;
+    m->stride[b] = k.row_stride;
+    m->width[b] = k.width;
+    m->data[b] = k.data;
+    *vec4_ok = *vec4_ok && k.width % 4 == 0 && k.row_stride % 4 == 0 &&
+               Aligned16(k.data);
+    prev_end = m->end[b];
+  }
+  return 0;
+}
+
+__global__ void FillStrided(float* p, int64_t rows, int64_t width,
+                            int64_t stride, float v) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < rows * width) p[(i / width) * stride + i % width] = v;
+}
+
+// `map` (may be null): the activations as per-feature row blocks instead of
+// the dense `act`.
 int ForwardImpl(const scemb_csr_t* csr, const scemb_sample_view_t* view,
                 const float* table, int64_t table_rows, int32_t dim,
-                float* act, int64_t batch, Arena& ws, uint32_t* status,
+                float* act, const RowMap* map, bool map_vec4,
+                int64_t batch, Arena& ws, uint32_t* status,
                 hipStream_t stream) {
   StreamArgs st{};
   st.sentinel = static_cast<uint32_t>(batch);
@@ -876,9 +1020,21 @@ int ForwardImpl(const scemb_csr_t* csr, const scemb_sample_view_t* view,
   if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
   if (batch == 0) return 0;
   if (st.n == 0 || table_rows == 0) {
-    hipLaunchKernelGGL(FillF32, dim3(CeilDiv(batch * dim, 256)), dim3(256), 0,
-                       stream, act, batch * dim, 0.0f);
-    SCEMB_LAUNCH_CHECK();
+    if (map == nullptr) {
+      hipLaunchKernelGGL(FillF32, dim3(CeilDiv(batch * dim, 256)), dim3(256),
+                         0, stream, act, batch * dim, 0.0f);
+      SCEMB_LAUNCH_CHECK();
+    }
+    for (int32_t b = 0; map != nullptr && b < map->n; ++b) {
+      const int64_t rows = map->end[b] - map->first[b];
+      if (rows == 0) continue;
+      hipLaunchKernelGGL(FillStrided,
+                         dim3(CeilDiv(rows * map->width[b], 256)), dim3(256),
+                         0, stream, map->data[b], rows,
+                         static_cast<int64_t>(map->width[b]), map->stride[b],
+                         0.0f);
+      SCEMB_LAUNCH_CHECK();
+    }
     return 0;
   }
   RowArgs r{};
@@ -887,21 +1043,27 @@ int ForwardImpl(const scemb_csr_t* csr, const scemb_sample_view_t* view,
   r.dim = dim;
   r.batch = batch;
   r.status = status;
+  if (map != nullptr) r.act = *map;
   int g, vec;
-  PickLayout(dim, Aligned16(table) && Aligned16(act), &g, &vec);
+  PickLayout(dim, Aligned16(table) && (map != nullptr ? map_vec4
+                                                      : Aligned16(act)),
+             &g, &vec);
   const int64_t hint = view != nullptr ? view->num_entries
                                         : csr->num_entries;
   const int64_t entries = hint > 0 && hint < st.n ? hint : st.n;
   const bool one_hot = entries <= kOneHotMaxEntriesPerRow * batch;
   return LaunchSeg<kSrcSorted, kEpiFwd>(st, r, sb, g, vec, one_hot,
-                                        "fwd_reduce", "fwd_finish", stream);
+                                        map != nullptr, "fwd_reduce",
+                                        "fwd_finish", stream);
 }
 
+// `map` (may be null): the activation gradients as per-feature row blocks
+// instead of the dense `act_grad`.
 template <int EPI>
-int GradImpl(const scemb_csr_t* csr, const float* act_grad, int64_t batch,
-             float* table, float* accum, int64_t table_rows, int32_t dim,
-             const OptParams& opt, Arena& ws, uint32_t* status,
-             hipStream_t stream) {
+int GradImpl(const scemb_csr_t* csr, const float* act_grad, const RowMap* map,
+             bool map_vec4, int64_t batch, float* table, float* accum,
+             int64_t table_rows, int32_t dim, const OptParams& opt, Arena& ws,
+             uint32_t* status, hipStream_t stream) {
   Geometry geo;
   int rc = CheckCsr(csr, batch, table_rows, dim, &geo);
   if (rc != 0) return rc;
@@ -951,19 +1113,22 @@ int GradImpl(const scemb_csr_t* csr, const float* act_grad, int64_t batch,
   r.batch = batch;
   r.opt = opt;
   r.status = status;
+  if (map != nullptr) r.act = *map;
   // Entries per activation row: how often each gradient row is gathered.
   const int64_t entries =
       csr->num_entries > 0 && csr->num_entries < n ? csr->num_entries : n;
   const bool one_hot = entries <= kOneHotMaxEntriesPerRow * batch;
   r.stream_src = one_hot;
   int g, vec;
-  PickLayout(dim, Aligned16(table) && Aligned16(act_grad) &&
+  PickLayout(dim, Aligned16(table) &&
+                      (map != nullptr ? map_vec4 : Aligned16(act_grad)) &&
                       (EPI != kEpiAdagrad || Aligned16(accum)), &g, &vec);
   if (direct) {
-    return LaunchSeg<kSrcCsr, EPI>(st, r, sb, g, vec, one_hot, "bwd_reduce",
-                                   "bwd_finish", stream);
+    return LaunchSeg<kSrcCsr, EPI>(st, r, sb, g, vec, one_hot, map != nullptr,
+                                   "bwd_reduce", "bwd_finish", stream);
   }
-  return LaunchSeg<kSrcSorted, EPI>(st, r, sb, g, vec, one_hot, "bwd_reduce",
+  return LaunchSeg<kSrcSorted, EPI>(st, r, sb, g, vec, one_hot,
+                                    map != nullptr, "bwd_reduce",
                                     "bwd_finish", stream);
 }
 
@@ -1001,6 +1166,74 @@ int BuildViewImpl(const scemb_csr_t* csr, int64_t batch, int64_t table_rows,
 }  // namespace
 }  // namespace scemb
 
+namespace scemb {
+namespace {
+
+int ForwardEntry(const scemb_csr_t* csr, const scemb_sample_view_t* view,
+                 const float* table, int64_t table_rows, int32_t dim,
+                 float* activations, const scemb_row_block_t* blocks,
+                 int32_t num_blocks, bool mapped, int64_t batch,
+                 void* workspace, size_t workspace_bytes,
+                 uint32_t* device_status, void* stream) {
+  if (workspace == nullptr) return Fail(SCEMB_ERR_WORKSPACE, "no workspace");
+  if (table == nullptr || (!mapped && activations == nullptr)) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null table or activations");
+  }
+  RowMap map;
+  bool vec4 = false;
+  if (mapped) {
+    const int rc = MakeRowMap(blocks, num_blocks, batch, dim, &map, &vec4);
+    if (rc != 0) return rc;
+  }
+  Arena ws(workspace, workspace_bytes);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int prof = ProfileBegin("fwd_call", s);
+  const int rc = ForwardImpl(csr, view, table, table_rows, dim, activations,
+                             mapped ? &map : nullptr, vec4, batch, ws,
+                             device_status, s);
+  ProfileEnd(prof, s);
+  return rc;
+}
+
+template <int EPI>
+int GradEntry(const scemb_csr_t* csr, const float* activations_grad,
+              const scemb_row_block_t* blocks, int32_t num_blocks,
+              bool mapped, int64_t batch, float* table, float* accumulator,
+              int64_t table_rows, int32_t dim, const float* learning_rate,
+              float learning_rate_value, int32_t clip_mask, float min_value,
+              float max_value, void* workspace, size_t workspace_bytes,
+              uint32_t* device_status, void* stream) {
+  if (workspace == nullptr) return Fail(SCEMB_ERR_WORKSPACE, "no workspace");
+  if (table == nullptr || (EPI == kEpiAdagrad && accumulator == nullptr) ||
+      (!mapped && activations_grad == nullptr)) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "null table, accumulator or gradient");
+  }
+  if ((clip_mask & 3) == 3 && min_value > max_value) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "min_value must be less than or equal to max_value");
+  }
+  RowMap map;
+  bool vec4 = false;
+  if (mapped) {
+    const int rc = MakeRowMap(blocks, num_blocks, batch, dim, &map, &vec4);
+    if (rc != 0) return rc;
+  }
+  Arena ws(workspace, workspace_bytes);
+  OptParams o{learning_rate, learning_rate_value, clip_mask, min_value,
+              max_value};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int prof = ProfileBegin("bwd_call", s);
+  const int rc = GradImpl<EPI>(csr, activations_grad, mapped ? &map : nullptr,
+                               vec4, batch, table, accumulator, table_rows,
+                               dim, o, ws, device_status, s);
+  ProfileEnd(prof, s);
+  return rc;
+}
+
+}  // namespace
+}  // namespace scemb
+
 using namespace scemb;
 
 extern "C" {
@@ -1009,8 +1242,8 @@ size_t scemb_sparse_dense_matmul_workspace_size(
     const scemb_csr_t* csr, const scemb_sample_view_t* view,
     int64_t device_batch_size, int64_t table_rows, int32_t dim) {
   Arena ws(nullptr, 0);
-  if (ForwardImpl(csr, view, nullptr, table_rows, dim, nullptr,
-                  device_batch_size, ws, nullptr, nullptr) != 0) {
+  if (ForwardImpl(csr, view, nullptr, table_rows, dim, nullptr, nullptr,
+                  false, device_batch_size, ws, nullptr, nullptr) != 0) {
     return 0;
   }
   return ws.used() + 256;
@@ -1023,17 +1256,20 @@ int scemb_sparse_dense_matmul(const scemb_csr_t* csr,
                               int64_t device_batch_size, void* workspace,
                               size_t workspace_bytes, uint32_t* device_status,
                               void* stream) {
-  if (workspace == nullptr) return Fail(SCEMB_ERR_WORKSPACE, "no workspace");
-  if (table == nullptr || activations == nullptr) {
-    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null table or activations");
-  }
-  Arena ws(workspace, workspace_bytes);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int prof = ProfileBegin("fwd_call", s);
-  const int rc = ForwardImpl(csr, view, table, table_rows, dim, activations,
-                             device_batch_size, ws, device_status, s);
-  ProfileEnd(prof, s);
-  return rc;
+  return ForwardEntry(csr, view, table, table_rows, dim, activations, nullptr,
+                      0, false, device_batch_size, workspace, workspace_bytes,
+                      device_status, stream);
+}
+
+int scemb_sparse_dense_matmul_to_blocks(
+    const scemb_csr_t* csr, const scemb_sample_view_t* view,
+    const float* table, int64_t table_rows, int32_t dim,
+    const scemb_row_block_t* outputs, int32_t num_outputs,
+    int64_t device_batch_size, void* workspace, size_t workspace_bytes,
+    uint32_t* device_status, void* stream) {
+  return ForwardEntry(csr, view, table, table_rows, dim, nullptr, outputs,
+                      num_outputs, true, device_batch_size, workspace,
+                      workspace_bytes, device_status, stream);
 }
 
 size_t scemb_build_sample_view_workspace_size(const scemb_csr_t* csr,
@@ -1064,8 +1300,9 @@ size_t scemb_sparse_dense_matmul_grad_workspace_size(const scemb_csr_t* csr,
                                                      int32_t dim) {
   Arena ws(nullptr, 0);
   OptParams o{nullptr, 0.f, 0, 0.f, 0.f};
-  if (GradImpl<kEpiSgd>(csr, nullptr, device_batch_size, nullptr, nullptr,
-                        table_rows, dim, o, ws, nullptr, nullptr) != 0) {
+  if (GradImpl<kEpiSgd>(csr, nullptr, nullptr, false, device_batch_size,
+                        nullptr, nullptr, table_rows, dim, o, ws, nullptr,
+                        nullptr) != 0) {
     return 0;
   }
   return ws.used() + 256;
@@ -1077,24 +1314,25 @@ int scemb_sparse_dense_matmul_grad_with_sgd(
     const float* learning_rate, float learning_rate_value, int32_t clip_mask,
     float min_value, float max_value, void* workspace, size_t workspace_bytes,
     uint32_t* device_status, void* stream) {
-  if (workspace == nullptr) return Fail(SCEMB_ERR_WORKSPACE, "no workspace");
-  if (table == nullptr || activations_grad == nullptr) {
-    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null table or gradient");
-  }
-  if ((clip_mask & 3) == 3 && min_value > max_value) {
-    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
-                "min_value must be less than or equal to max_value");
-  }
-  Arena ws(workspace, workspace_bytes);
-  OptParams o{learning_rate, learning_rate_value, clip_mask, min_value,
-              max_value};
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int prof = ProfileBegin("bwd_call", s);
-  const int rc = GradImpl<kEpiSgd>(csr, activations_grad, device_batch_size,
-                                   table, nullptr, table_rows, dim, o, ws,
-                                   device_status, s);
-  ProfileEnd(prof, s);
-  return rc;
+  return GradEntry<kEpiSgd>(csr, activations_grad, nullptr, 0, false,
+                            device_batch_size, table, nullptr, table_rows,
+                            dim, learning_rate, learning_rate_value,
+                            clip_mask, min_value, max_value, workspace,
+                            workspace_bytes, device_status, stream);
+}
+
+int scemb_sparse_dense_matmul_grad_with_sgd_from_blocks(
+    const scemb_csr_t* csr, const scemb_row_block_t* activation_grads,
+    int32_t num_blocks, int64_t device_batch_size, float* table,
+    int64_t table_rows, int32_t dim, const float* learning_rate,
+    float learning_rate_value, int32_t clip_mask, float min_value,
+    float max_value, void* workspace, size_t workspace_bytes,
+    uint32_t* device_status, void* stream) {
+  return GradEntry<kEpiSgd>(csr, nullptr, activation_grads, num_blocks, true,
+                            device_batch_size, table, nullptr, table_rows,
+                            dim, learning_rate, learning_rate_value,
+                            clip_mask, min_value, max_value, workspace,
+                            workspace_bytes, device_status, stream);
 }
 
 int scemb_sparse_dense_matmul_grad_with_adagrad(
@@ -1104,27 +1342,27 @@ int scemb_sparse_dense_matmul_grad_with_adagrad(
     float learning_rate_value, int32_t clip_mask, float min_value,
     float max_value, void* workspace, size_t workspace_bytes,
     uint32_t* device_status, void* stream) {
-  if (workspace == nullptr) return Fail(SCEMB_ERR_WORKSPACE, "no workspace");
-  if (table == nullptr || accumulator == nullptr ||
-      activations_grad == nullptr) {
-    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
-                "null table, accumulator or gradient");
-  }
-  if ((clip_mask & 3) == 3 && min_value > max_value) {
-    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
-                "min_value must be less than or equal to max_value");
-  }
-  Arena ws(workspace, workspace_bytes);
-  OptParams o{learning_rate, learning_rate_value, clip_mask, min_value,
-              max_value};
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const int prof = ProfileBegin("bwd_call", s);
-  const int rc = GradImpl<kEpiAdagrad>(csr, activations_grad,
-                                       device_batch_size, table, accumulator,
-                                       table_rows, dim, o, ws, device_status,
-                                       s);
-  ProfileEnd(prof, s);
-  return rc;
+  return GradEntry<kEpiAdagrad>(csr, activations_grad, nullptr, 0, false,
+                                device_batch_size, table, accumulator,
+                                table_rows, dim, learning_rate,
+                                learning_rate_value, clip_mask, min_value,
+                                max_value, workspace, workspace_bytes,
+                                device_status, stream);
+}
+
+int scemb_sparse_dense_matmul_grad_with_adagrad_from_blocks(
+    const scemb_csr_t* csr, const scemb_row_block_t* activation_grads,
+    int32_t num_blocks, int64_t device_batch_size, float* table,
+    float* accumulator, int64_t table_rows, int32_t dim,
+    const float* learning_rate, float learning_rate_value, int32_t clip_mask,
+    float min_value, float max_value, void* workspace, size_t workspace_bytes,
+    uint32_t* device_status, void* stream) {
+  return GradEntry<kEpiAdagrad>(csr, nullptr, activation_grads, num_blocks,
+                                true, device_batch_size, table, accumulator,
+                                table_rows, dim, learning_rate,
+                                learning_rate_value, clip_mask, min_value,
+                                max_value, workspace, workspace_bytes,
+                                device_status, stream);
 }
 
 }  // extern "C"

@@ -38,11 +38,14 @@ EXPORTED_SYMBOLS = (
     "scemb_version",
     "scemb_sparse_dense_matmul_workspace_size",
     "scemb_sparse_dense_matmul",
+    "scemb_sparse_dense_matmul_to_blocks",
     "scemb_build_sample_view_workspace_size",
     "scemb_build_sample_view",
     "scemb_sparse_dense_matmul_grad_workspace_size",
     "scemb_sparse_dense_matmul_grad_with_sgd",
     "scemb_sparse_dense_matmul_grad_with_adagrad",
+    "scemb_sparse_dense_matmul_grad_with_sgd_from_blocks",
+    "scemb_sparse_dense_matmul_grad_with_adagrad_from_blocks",
     "scemb_preprocess_stats_size",
     "scemb_preprocess_stats_counters_offset",
     "scemb_preprocess_workspace_size",
@@ -79,6 +82,20 @@ class SampleView(ctypes.Structure):
       ("table_rows", ctypes.c_int64),
       ("num_entries", ctypes.c_int64),
   ]
+
+
+class RowBlock(ctypes.Structure):
+  _fields_ = [
+      ("first_row", ctypes.c_int64),
+      ("num_rows", ctypes.c_int64),
+      ("data", ctypes.c_void_p),
+      ("row_stride", ctypes.c_int64),
+      ("width", ctypes.c_int32),
+      ("reserved", ctypes.c_int32),
+  ]
+
+
+MAX_ROW_BLOCKS = 32
 
 
 class Feature(ctypes.Structure):
@@ -151,6 +168,20 @@ def load_library() -> ctypes.CDLL:
     lib.scemb_sparse_dense_matmul.restype = ctypes.c_int
     lib.scemb_sparse_dense_matmul.argtypes = [csr_p, view_p, vp, i64, i32, vp,
                                               i64, vp, sz, vp, vp]
+    blk_p = ctypes.POINTER(RowBlock)
+    lib.scemb_sparse_dense_matmul_to_blocks.restype = ctypes.c_int
+    lib.scemb_sparse_dense_matmul_to_blocks.argtypes = [
+        csr_p, view_p, vp, i64, i32, blk_p, i32, i64, vp, sz, vp, vp]
+    lib.scemb_sparse_dense_matmul_grad_with_sgd_from_blocks.restype = (
+        ctypes.c_int)
+    lib.scemb_sparse_dense_matmul_grad_with_sgd_from_blocks.argtypes = [
+        csr_p, blk_p, i32, i64, vp, i64, i32, vp, f32, i32, f32, f32, vp, sz,
+        vp, vp]
+    lib.scemb_sparse_dense_matmul_grad_with_adagrad_from_blocks.restype = (
+        ctypes.c_int)
+    lib.scemb_sparse_dense_matmul_grad_with_adagrad_from_blocks.argtypes = [
+        csr_p, blk_p, i32, i64, vp, vp, i64, i32, vp, f32, i32, f32, f32, vp,
+        sz, vp, vp]
     lib.scemb_build_sample_view_workspace_size.restype = sz
     lib.scemb_build_sample_view_workspace_size.argtypes = [csr_p, i64, i64]
     lib.scemb_build_sample_view.restype = ctypes.c_int
@@ -234,12 +265,20 @@ def torch():
   return _torch
 
 
+_gpu_seen = False
+
+
 def require_gpu():
+  """torch, once a GPU has been seen (the check is not repeated: it costs
+  more host time than a kernel launch)."""
+  global _gpu_seen
   t = torch()
-  if not t.cuda.is_available():
-    raise RuntimeError(
-        "The SparseCore embedding path runs on the GPU through libscemb.so; "
-        "no GPU is visible to torch.")
+  if not _gpu_seen:
+    if not t.cuda.is_available():
+      raise RuntimeError(
+          "The SparseCore embedding path runs on the GPU through "
+          "libscemb.so; no GPU is visible to torch.")
+    _gpu_seen = True
   return t
 
 
@@ -366,6 +405,38 @@ def sparse_dense_matmul(csr: Csr | None, table, activations, batch: int,
       ptr(ws), ws.numel(), ptr(device_status), stream_handle()))
 
 
+def row_blocks(blocks) -> tuple:
+  """ctypes array of RowBlock from (first_row, tensor, width) triples; each
+  tensor is a CUDA float32 matrix whose rows are the block's rows."""
+  arr = (RowBlock * max(len(blocks), 1))()
+  for i, (first, t, width) in enumerate(blocks):
+    arr[i] = RowBlock(int(first), int(t.shape[0]), ptr(t), int(t.stride(0)),
+                      int(width), 0)
+  return arr, len(blocks)
+
+
+def sparse_dense_matmul_to_blocks(csr: Csr | None, table, blocks, batch: int,
+                                  view: LookupView | None = None,
+                                  device_status=None) -> None:
+  """Forward lookup writing each activation row into its block (see
+  scemb_row_block_t); `blocks` as for row_blocks."""
+  lib = load_library()
+  rows = int(table.shape[0])
+  dim = 1 if table.dim() == 1 else int(table.shape[1])
+  vs = view.as_struct() if view is not None else None
+  csr_ref = ctypes.byref(csr) if csr is not None else None
+  vs_ref = ctypes.byref(vs) if vs is not None else None
+  need = lib.scemb_sparse_dense_matmul_workspace_size(csr_ref, vs_ref, batch,
+                                                      rows, dim)
+  if need == 0:
+    check(SCEMB_ERR_INVALID_ARGUMENT)
+  ws = WORKSPACE.get(need)
+  arr, n = row_blocks(blocks)
+  check(lib.scemb_sparse_dense_matmul_to_blocks(
+      csr_ref, vs_ref, ptr(table), rows, dim, arr, n, batch, ptr(ws),
+      ws.numel(), ptr(device_status), stream_handle()))
+
+
 def _lr_args(learning_rate):
   t = torch()
   if isinstance(learning_rate, t.Tensor):
@@ -384,8 +455,11 @@ def _clip_args(min_value, max_value):
 def sparse_dense_matmul_grad(csr: Csr, activations_grad, table,
                              accumulator, learning_rate, batch: int,
                              min_value=None, max_value=None,
-                             device_status=None) -> None:
-  """SGD when accumulator is None, Adagrad otherwise; updates in place."""
+                             device_status=None, grad_blocks=None) -> None:
+  """SGD when accumulator is None, Adagrad otherwise; updates in place.
+  With `grad_blocks` ((first_row, tensor, width) triples, see row_blocks)
+  the gradients are read from those per-feature blocks and
+  `activations_grad` is ignored."""
   lib = load_library()
   rows = int(table.shape[0])
   dim = 1 if table.dim() == 1 else int(table.shape[1])
@@ -396,6 +470,21 @@ def sparse_dense_matmul_grad(csr: Csr, activations_grad, table,
   ws = WORKSPACE.get(need)
   keep, lr_ptr, lr_val = _lr_args(learning_rate)
   mask, lo, hi = _clip_args(min_value, max_value)
+  if grad_blocks is not None:
+    arr, n = row_blocks(grad_blocks)
+    if accumulator is None:
+      rc = lib.scemb_sparse_dense_matmul_grad_with_sgd_from_blocks(
+          ctypes.byref(csr), arr, n, batch, ptr(table), rows, dim, lr_ptr,
+          lr_val, mask, lo, hi, ptr(ws), ws.numel(), ptr(device_status),
+          stream_handle())
+    else:
+      rc = lib.scemb_sparse_dense_matmul_grad_with_adagrad_from_blocks(
+          ctypes.byref(csr), arr, n, batch, ptr(table), ptr(accumulator),
+          rows, dim, lr_ptr, lr_val, mask, lo, hi, ptr(ws), ws.numel(),
+          ptr(device_status), stream_handle())
+    del keep
+    check(rc)
+    return
   if accumulator is None:
     rc = lib.scemb_sparse_dense_matmul_grad_with_sgd(
         ctypes.byref(csr), ptr(activations_grad), batch, ptr(table), rows, dim,

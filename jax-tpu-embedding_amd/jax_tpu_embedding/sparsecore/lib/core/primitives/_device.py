@@ -2,6 +2,8 @@
 
 from __future__ import annotations
 
+import numpy as np
+
 from jax_tpu_embedding.sparsecore import _native
 from jax_tpu_embedding.sparsecore.utils import utils
 
@@ -31,6 +33,25 @@ def csr_operands(row_pointers, embedding_ids, sample_ids, gains,
   csr = _native.make_csr(rp, eid, sid, g, num_sc_per_device, num_partitions,
                          sorted_by_row=sorted_by_row, num_entries=num_entries)
   return (rp, eid, sid, g), csr
+
+
+class RowBlocks:
+  """A [rows, dim] float32 activation (or activation-gradient) matrix held as
+  per-feature row blocks instead of one stacked tensor: `blocks` lists
+  (first_row, tensor, width) with each tensor a CUDA float32 matrix whose
+  rows are stacked rows first_row.. and whose first `width` columns are the
+  feature's (the rest of dim is stacking padding). The primitives accept it
+  in place of the stacked matrix and read or write the blocks directly."""
+
+  dtype = np.float32
+
+  def __init__(self, rows: int, dim: int, blocks):
+    self.shape = (int(rows), int(dim))
+    self.blocks = list(blocks)
+
+  @property
+  def ndim(self) -> int:
+    return 2
 
 
 def device_table(table):

@@ -12,7 +12,11 @@ the hardware): ``num_sc_per_device`` and ``global_device_count`` give the CSR
 segment / partition counts (defaults: the device's SparseCore count, 1);
 ``lookup_view`` is an optional ``_native.LookupView`` of the same CSR (built
 by the preprocessing), which spares the call its grouping sort. A view built
-for another batch size or table height is ignored. ``csr_num_entries``, the
+for another batch size or table height is ignored. ``activation_blocks``
+(a ``_device.RowBlocks``) makes the call write every activation row into its
+feature's block (the unstacking of ``embedding.py:903-1044`` fused into the
+kernel) and return that object instead of a stacked matrix.
+``csr_num_entries``, the
 CSR's entry count when known, picks the kernel variant (one-hot or
 multi-hot batches) and changes no result.
 """
@@ -53,7 +57,8 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
           max_ids_per_partition: int, max_unique_ids_per_partition: int,
           sharding_strategy: int = 1, quantization_config=None,
           enable_minibatching: bool = False, num_sc_per_device=None,
-          global_device_count=None, lookup_view=None, csr_num_entries=None):
+          global_device_count=None, lookup_view=None, csr_num_entries=None,
+          activation_blocks=None):
   utils.validate_abstract_eval_params(
       lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
       lhs_gains, num_minibatches_per_physical_sparse_core, embedding_table,
@@ -75,11 +80,23 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
   table = _device.device_table(embedding_table)
   shape = ((device_batch_size,) if table.dim() == 1 else
            (device_batch_size, int(table.shape[1])))
-  out = t.empty(shape, dtype=t.float32, device=table.device)
   if lookup_view is not None and (
       lookup_view.device_batch_size != int(device_batch_size) or
       lookup_view.table_rows != int(table.shape[0])):
     lookup_view = None
+  if activation_blocks is not None:
+    if tuple(activation_blocks.shape) != (int(device_batch_size),
+                                          int(table.shape[-1])) or (
+                                              table.dim() != 2):
+      raise ValueError(
+          f"activation_blocks of shape {activation_blocks.shape} do not match "
+          f"the activations ({device_batch_size}, {table.shape[-1]})")
+    _native.sparse_dense_matmul_to_blocks(csr, table, activation_blocks.blocks,
+                                          int(device_batch_size),
+                                          view=lookup_view)
+    del keep
+    return activation_blocks
+  out = t.empty(shape, dtype=t.float32, device=table.device)
   _native.sparse_dense_matmul(csr, table, out, int(device_batch_size),
                               view=lookup_view)
   del keep

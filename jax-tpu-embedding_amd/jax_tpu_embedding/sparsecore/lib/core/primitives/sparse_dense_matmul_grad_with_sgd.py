@@ -18,6 +18,9 @@ with one SparseCore segment the kernel then reads it in place instead of
 sorting a copy (a violated order is reported, not silently used).
 ``csr_num_entries``, the CSR's entry count when known, picks the kernel
 variant (one-hot or multi-hot batches) and changes no result.
+``activations_grad`` may be a ``_device.RowBlocks``: the per-feature
+gradients are then read in place (the gradient stacking of
+``embedding.py:1200-1294`` fused into the kernel).
 """
 
 from __future__ import annotations
@@ -56,9 +59,17 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
                                    sorted_by_row=csr_sorted_by_row,
                                    num_entries=csr_num_entries)
   table = _device.device_table(embedding_table)
-  grad = _native.as_device_tensor(activations_grad, t.float32, table.device)
+  blocks = None
+  if isinstance(activations_grad, _device.RowBlocks):
+    blocks, grad = activations_grad.blocks, None
+    batch = activations_grad.shape[0]
+  else:
+    grad = _native.as_device_tensor(activations_grad, t.float32,
+                                    table.device)
+    batch = int(grad.shape[0])
   _native.sparse_dense_matmul_grad(csr, grad, table, None, learning_rate,
-                                   int(grad.shape[0]), min_value, max_value)
+                                   batch, min_value, max_value,
+                                   grad_blocks=blocks)
   del keep
   return table
 

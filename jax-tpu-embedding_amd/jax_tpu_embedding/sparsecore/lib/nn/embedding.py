@@ -366,6 +366,88 @@ def _get_activation_for_feature(feature, activations, global_device_count,
   return sl.reshape(f * b1, *sl.shape[2:])
 
 
+def _activation_blocks(stack_spec, features, global_device_count: int,
+                       num_sc_per_device: int, dev):
+  """Per-feature outputs of one stacked table and the RowBlocks that let the
+  forward kernel write them directly (the layout _get_activation_for_feature
+  slices out of the stacked activations). None when plain views of the
+  stacked activations already are the outputs (one SparseCore, every feature
+  at the full stacked dim) or the stack needs more blocks than the kernels
+  take."""
+  t = _native.torch()
+  f = num_sc_per_device
+  rows = stack_spec.total_sample_count // global_device_count
+  dim = stack_spec.stack_embedding_dim
+  if len(features) * f > _native.MAX_ROW_BLOCKS or rows % f:
+    return None
+  if f == 1 and all(fs.output_shape[-1] == dim for fs in features):
+    return None
+  widths = []
+  for fs in features:
+    if fs.output_shape[-1] > fs.table_spec.embedding_dim:
+      raise ValueError(
+          f"Feature {fs.name} has output shape {fs.output_shape} and "
+          f"embedding dim {fs.table_spec.embedding_dim}. The embedding dim "
+          "in output shape cannot be more than the (original, unpadded) "
+          "embedding dim in the FeatureSpec.")
+    widths.append(fs.output_shape[-1])
+  # One allocation per stack; each feature's output is a contiguous slice.
+  sizes = [f * (fs.output_shape[0] // (global_device_count * f)) * w
+           for fs, w in zip(features, widths)]
+  flat = t.empty(sum(sizes), dtype=t.float32, device=dev)
+  outs, blocks, start = {}, [], 0
+  for fs, width, size in zip(features, widths, sizes):
+    off = fs.id_transformation.row_offset // (global_device_count * f)
+    b1 = fs.output_shape[0] // (global_device_count * f)
+    out = flat[start:start + size].view(f * b1, width)
+    start += size
+    outs[fs.name] = out
+    for s in range(f):
+      blocks.append((s * (rows // f) + off, out[s * b1:(s + 1) * b1], width))
+  blocks.sort(key=lambda b: b[0])
+  return outs, _device.RowBlocks(rows, dim, blocks)
+
+
+def _gradient_blocks(stack_spec, items, num_sc_per_device: int,
+                     num_entries=None):
+  """RowBlocks over the per-feature gradients of one stacked table, in the
+  layout stack_embedding_gradients builds; None when the stack needs more
+  blocks than the kernels take or is multi-hot (`num_entries`, the CSR's
+  entries, above twice its rows)."""
+  f = num_sc_per_device
+  if len(items) * f > _native.MAX_ROW_BLOCKS:
+    return None
+  if num_entries is not None and num_entries > 2 * sum(
+      int(fs.output_shape[0]) for fs, _ in items):
+    # Multi-hot: every gradient row is gathered many times; one stacking
+    # copy costs less than resolving the row blocks per gather.
+    return None
+  t = _native.torch()
+  grads = []
+  for fs, g in items:
+    if not isinstance(g, t.Tensor):
+      g = _native.as_device_tensor(g, t.float32)
+    g = _native.as_device_tensor(g, t.float32, _native.device()).reshape(
+        -1, fs.table_spec.embedding_dim)
+    if g.shape[0] % f:
+      raise ValueError(
+          "The input batch size must be divisible by the number of feature "
+          f"slices per device. Got input shape {tuple(g.shape)} and "
+          f"{f} feature slices per device for feature {fs.name}.")
+    grads.append((fs, g))
+  rows = sum(g.shape[0] for _, g in grads)
+  per_sc = rows // f
+  blocks, cum = [], 0
+  for fs, g in grads:
+    b1 = g.shape[0] // f
+    for s in range(f):
+      blocks.append((s * per_sc + cum, g[s * b1:(s + 1) * b1],
+                     fs.table_spec.embedding_dim))
+    cum += b1
+  blocks.sort(key=lambda b: b[0])
+  return _device.RowBlocks(rows, stack_spec.stack_embedding_dim, blocks)
+
+
 def unstack_embedding_activations(activations, feature_specs,
                                   global_device_count: int,
                                   num_sc_per_device: int,
@@ -399,10 +481,21 @@ def tpu_sparse_dense_matmul(preprocessed_inputs, embedding_variables,
   nmb = _resolve_scalar_minibatches(preprocessed_inputs.num_minibatches)
   views = getattr(preprocessed_inputs, "lookup_views", None) or {}
   counts = getattr(preprocessed_inputs, "csr_num_entries", None) or {}
+  leaves = _tree.tree_leaves(feature_specs)
+  by_stack = collections.defaultdict(list)
+  for fs in leaves:
+    by_stack[fs.table_spec.stacked_table_spec.stack_name].append(fs)
   acts = {}
+  per_feature = {}
   for name, spec in stacked.items():
     ev = embedding_variables[name]
     table = ev.table if isinstance(ev, EmbeddingVariables) else ev[0]
+    fused = None
+    if perform_unstacking and len(getattr(table, "shape", ())) == 2:
+      # Unstacking fused into the kernel: activation rows go straight to
+      # the per-feature outputs.
+      fused = _activation_blocks(spec, by_stack[name], global_device_count,
+                                 num_sc_per_device, _native.device())
     acts[name] = (sparse_dense_matmul_csr.tpu_sparse_dense_matmul_csr_primitive
                   .bind(rp[name], eid[name], sid[name], gains[name], nmb,
                         table,
@@ -419,13 +512,21 @@ def tpu_sparse_dense_matmul(preprocessed_inputs, embedding_variables,
                         num_sc_per_device=num_sc_per_device,
                         global_device_count=global_device_count,
                         lookup_view=views.get(name),
-                        csr_num_entries=counts.get(name)))
-  if perform_unstacking:
-    acts = unstack_embedding_activations(acts, feature_specs,
-                                         global_device_count,
-                                         num_sc_per_device,
-                                         use_activation_unstack_primitive)
-  return acts
+                        csr_num_entries=counts.get(name),
+                        activation_blocks=fused[1] if fused else None))
+    if fused:
+      per_feature.update(fused[0])
+  if not perform_unstacking:
+    return acts
+  rest = [fs for fs in leaves if fs.name not in per_feature]
+  if rest:
+    stacked_acts = {k: v for k, v in acts.items()
+                    if not isinstance(v, _device.RowBlocks)}
+    unstacked = unstack_embedding_activations(
+        stacked_acts, rest, global_device_count, num_sc_per_device,
+        use_activation_unstack_primitive)
+    per_feature.update({fs.name: a for fs, a in zip(rest, unstacked)})
+  return _tree.tree_map(lambda fs: per_feature[fs.name], feature_specs)
 
 
 def _resolve_scalar_minibatches(val):
@@ -507,9 +608,33 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
   if perform_stacking:
     _assert_same_structure(feature_specs, activation_gradients,
                            "feature_specs", "activation_gradients")
-    grads = stack_embedding_gradients(activation_gradients, feature_specs,
-                                      num_sc_per_device, global_device_count,
-                                      use_gradient_stacking_primitive)
+    # Gradient stacking fused into the kernel: each stack's update reads the
+    # per-feature gradients in place (stack_embedding_gradients copies them
+    # into one matrix; it remains the path for stacks with too many blocks).
+    by_stack = collections.defaultdict(list)
+    for g, fs in zip(_tree.tree_leaves(activation_gradients),
+                     _tree.tree_leaves(feature_specs)):
+      if fs._id_transformation is None:  # pylint: disable=protected-access
+        raise ValueError("FeatureIdTransformation cannot be None here. It is "
+                         f"None for {fs.name}")
+      by_stack[fs.table_spec.stacked_table_spec.stack_name].append((fs, g))
+    grads = {}
+    for name, items in by_stack.items():
+      items.sort(key=lambda x: x[0].id_transformation.row_offset)
+      ev = embedding_variables[name]
+      table = ev.table if isinstance(ev, EmbeddingVariables) else ev[0]
+      blocks = None
+      if len(getattr(table, "shape", ())) == 2:
+        blocks = _gradient_blocks(
+            stacked[name], items, num_sc_per_device,
+            (getattr(preprocessed_inputs, "csr_num_entries", None) or
+             {}).get(name))
+      if blocks is None:
+        blocks = stack_embedding_gradients(
+            [g for _, g in items], [fs for fs, _ in items],
+            num_sc_per_device, global_device_count,
+            use_gradient_stacking_primitive)[name]
+      grads[name] = blocks
   else:
     grads = activation_gradients
   assert rp.keys() == grads.keys()

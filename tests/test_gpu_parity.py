@@ -559,3 +559,99 @@ def test_end_to_end_api_feature_stacking_adagrad():
                              atol=ATOL)
   np.testing.assert_allclose(out[name].slot[0].cpu().numpy(), exp_a,
                              rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("num_sc", [1, 2])
+@pytest.mark.parametrize("integer", [True, False])
+def test_fused_unstack_and_gradient_stack_match_copy_paths(num_sc, integer):
+  """The embedding API writes activations straight into per-feature outputs
+  and reads per-feature gradients in place (row blocks). Same results as the
+  stacked-matrix path plus unstack_embedding_activations /
+  stack_embedding_gradients: bit for bit with integer data (every sum is
+  exact whatever the kernel layout), within rtol 1e-5 / atol 1e-6 with float
+  data. Dims 12 (padded to 16: the padding columns are neither written nor
+  read) and 16 share one stack; one feature takes only 10 of its 12 dims."""
+  rng = np.random.default_rng(31 + num_sc + (5 if integer else 0))
+  batch = 128
+  opt = embedding_spec.AdagradOptimizerSpec(learning_rate=0.02,
+                                            initial_accumulator_value=0.1)
+  def specs(out_dim_f1):
+    t0 = embedding_spec.TableSpec(
+        name="t0", vocabulary_size=700, embedding_dim=12,
+        initializer=embedding_spec.zeros, optimizer=opt, combiner="sum",
+        max_ids_per_partition=1 << 16, max_unique_ids_per_partition=1 << 16)
+    t1 = embedding_spec.TableSpec(
+        name="t1", vocabulary_size=300, embedding_dim=16,
+        initializer=embedding_spec.zeros, optimizer=opt, combiner="sum",
+        max_ids_per_partition=1 << 16, max_unique_ids_per_partition=1 << 16)
+    return [
+        embedding_spec.FeatureSpec(name="f0", table_spec=t0,
+                                   input_shape=[batch, 1],
+                                   output_shape=[batch, 12]),
+        embedding_spec.FeatureSpec(name="f1", table_spec=t0,
+                                   input_shape=[batch, 1],
+                                   output_shape=[batch, out_dim_f1]),
+        embedding_spec.FeatureSpec(name="f2", table_spec=t1,
+                                   input_shape=[batch, 1],
+                                   output_shape=[batch, 16]),
+    ]
+
+  features = [_ragged(rng, batch, 1, 6, 700, zipf_a=1.1),
+              _ragged(rng, batch, 0, 4, 700),
+              _ragged(rng, batch, 1, 3, 300, zipf_a=1.3)]
+  for out_dim_f1, check_grad in ((10, False), (12, True)):
+    feats = specs(out_dim_f1)
+    _stack(feats, ["t0", "t1"], 1, num_sc, limit=1 << 16)
+    pre, _ = embedding.preprocess_sparse_dense_matmul_input(
+        features, None, feats, 1, 1, num_sc_per_device=num_sc)
+    name = feats[0].table_spec.stacked_table_spec.stack_name
+    spec = feats[0].table_spec.stacked_table_spec
+    shape = (spec.stack_vocab_size, spec.stack_embedding_dim)
+    table0 = (rng.integers(-4, 5, size=shape) if integer else
+              rng.normal(0, 0.01, size=shape)).astype(np.float32)
+
+    def variables():
+      return {name: embedding.EmbeddingVariables(
+          torch.from_numpy(table0.copy()).cuda(),
+          (torch.full(shape, 0.1, dtype=torch.float32, device="cuda"),))}
+
+    v = variables()
+    fused = embedding.tpu_sparse_dense_matmul(
+        pre, v, feats, global_device_count=1, num_sc_per_device=num_sc)
+    stacked = embedding.tpu_sparse_dense_matmul(
+        pre, v, feats, global_device_count=1, num_sc_per_device=num_sc,
+        perform_unstacking=False)
+    copied = embedding.unstack_embedding_activations(stacked, feats, 1,
+                                                     num_sc)
+    for a, b in zip(fused, copied):
+      assert tuple(a.shape) == tuple(b.shape)
+      if integer:
+        np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy())
+      else:
+        np.testing.assert_allclose(a.cpu().numpy(), b.cpu().numpy(),
+                                   rtol=RTOL, atol=ATOL)
+    if not check_grad:
+      continue
+    grads = [torch.from_numpy(
+        (rng.integers(-3, 4, size=(batch, fs.table_spec.embedding_dim))
+         if integer else rng.normal(size=(batch, fs.table_spec.embedding_dim))
+         ).astype(np.float32)).cuda() for fs in feats]
+    v_fused, v_copy = variables(), variables()
+    embedding.tpu_sparse_dense_matmul_grad(
+        grads, pre, v_fused, feats, global_device_count=1,
+        num_sc_per_device=num_sc)
+    stacked_grads = embedding.stack_embedding_gradients(grads, feats, num_sc)
+    embedding.tpu_sparse_dense_matmul_grad(
+        stacked_grads, pre, v_copy, feats, global_device_count=1,
+        num_sc_per_device=num_sc, perform_stacking=False)
+    for x, y in ((v_fused[name].table, v_copy[name].table),
+                 (v_fused[name].slot[0], v_copy[name].slot[0])):
+      if integer:
+        np.testing.assert_array_equal(x.cpu().numpy(), y.cpu().numpy())
+      else:
+        np.testing.assert_allclose(x.cpu().numpy(), y.cpu().numpy(),
+                                   rtol=RTOL, atol=ATOL)
+    # The stacking padding of the table (columns 12..15 of t0's rows) only
+    # ever sees zero gradient.
+    assert bool((v_fused[name].slot[0][:, 12:16] ==
+                 v_copy[name].slot[0][:, 12:16]).all())
