@@ -25,6 +25,7 @@
 //                     pointers, alignment padding, static-buffer drops), then
 //                     a scatter of the kept runs.
 #include <algorithm>
+#include <cstring>
 #include <vector>
 
 #include "../../include/scemb.h"
@@ -55,6 +56,8 @@ struct FeatureDev {
   int32_t col_offset;
   int32_t col_shift;
 };
+static_assert(sizeof(SliceDesc) % 4 == 0 && sizeof(FeatureDev) % 4 == 0,
+              "descriptors are uploaded as 32-bit words");
 
 struct KeyLayout {
   int log2ns;
@@ -710,6 +713,42 @@ struct Buffers {
   FeatureDev* feats;
 };
 
+// Copies of small host arrays into device memory through kernel arguments
+// (up to kUploadWords words per launch), ordered on `stream` like any
+// kernel: nothing waits on the host side and the source may be released as
+// soon as the launch call returns.
+constexpr int kUploadWords = 768;
+struct UploadChunk {
+  uint32_t words[kUploadWords];
+};
+
+__global__ __launch_bounds__(256) void UploadKernel(UploadChunk c, int n,
+                                                    uint32_t* dst) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = c.words[i];
+}
+
+int UploadBytes(const void* src, size_t bytes, void* dst,
+                hipStream_t stream) {
+  if (bytes == 0) return 0;
+  if (bytes % 4 != 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "upload size not word aligned");
+  }
+  const uint32_t* w = static_cast<const uint32_t*>(src);
+  uint32_t* d = static_cast<uint32_t*>(dst);
+  const size_t total = bytes / 4;
+  for (size_t off = 0; off < total; off += kUploadWords) {
+    const int n = static_cast<int>(
+        total - off < static_cast<size_t>(kUploadWords) ? total - off
+                                                         : kUploadWords);
+    UploadChunk c;
+    std::memcpy(c.words, w + off, sizeof(uint32_t) * n);
+    hipLaunchKernelGGL(UploadKernel, dim3(1), dim3(256), 0, stream, c, n,
+                       d + off);
+    SCEMB_LAUNCH_CHECK();
+  }
+  return 0;
+}
+
 template <typename K>
 int RunPipeline(const scemb_feature_t* feats, int nf,
                 const scemb_preprocess_options_t* o,
@@ -776,16 +815,14 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                     "weights required for every feature of a weighted stack");
       }
     }
-    if (!pl.slices.empty()) {
-      SCEMB_HIP(hipMemcpyAsync(b.slices, pl.slices.data(),
-                               sizeof(SliceDesc) * pl.slices.size(),
-                               hipMemcpyHostToDevice, stream));
-    }
-    SCEMB_HIP(hipMemcpyAsync(b.feats, fd.data(), sizeof(FeatureDev) * nf,
-                             hipMemcpyHostToDevice, stream));
-    // The staging copies above read pageable host memory; make sure they are
-    // done before the vectors go out of scope.
-    SCEMB_HIP(hipStreamSynchronize(stream));
+    // The slice and feature descriptors travel as kernel arguments: no
+    // pageable host copy, no host synchronisation.
+    int st = UploadBytes(pl.slices.data(),
+                         sizeof(SliceDesc) * pl.slices.size(), b.slices,
+                         stream);
+    if (st != 0) return st;
+    st = UploadBytes(fd.data(), sizeof(FeatureDev) * nf, b.feats, stream);
+    if (st != 0) return st;
     hipLaunchKernelGGL(FillI32, dim3(CeilDiv(num_buckets, 256)), dim3(256), 0,
                        stream, b.part_first, num_buckets, -1);
     SCEMB_LAUNCH_CHECK();

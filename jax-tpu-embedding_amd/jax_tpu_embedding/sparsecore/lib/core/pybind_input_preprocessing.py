@@ -305,10 +305,9 @@ def _preprocess_stack(feats, metas, *, local_device_count,
   _native.check(lib.scemb_preprocess_stacked_table(
       structs, len(feats), ctypes.byref(opts), ctypes.byref(out),
       _native.ptr(ws), ws.numel(), _native.stream_handle()))
-  stats_np = stats.cpu().numpy()  # synchronises the stream
   off = int(lib.scemb_preprocess_stats_counters_offset(ctypes.byref(opts)))
-  counters = stats_np[off:off + 8].copy().view(np.int64)
-  return rp, eid, sid, gains, stats_np, counters, (L, S, ns, off)
+  # The stats stay on the device until every stack has been enqueued.
+  return rp, eid, sid, gains, stats, (L, S, ns, off)
 
 
 def preprocess_sparse_dense_matmul_input(
@@ -334,6 +333,21 @@ def preprocess_sparse_dense_matmul_input(
   a SparseDenseMatmulInputStats.
   """
   del batch_number, all_reduce_interface
+  features, feature_weights, feature_specs = check_arguments(
+      features, feature_weights, feature_specs, sharding_strategy,
+      enable_minibatching)
+  rps, eids, sids, gns, pending = enqueue_preprocessing(
+      features, feature_weights, feature_specs, local_device_count,
+      global_device_count, num_sc_per_device=num_sc_per_device,
+      has_leading_dimension=has_leading_dimension,
+      allow_id_dropping=allow_id_dropping)
+  return rps, eids, sids, gns, 1, collect_stats(pending)
+
+
+def check_arguments(features, feature_weights, feature_specs,
+                    sharding_strategy, enable_minibatching: bool):
+  """Argument checks of the preprocessing entry; returns the inputs as
+  lists."""
   if enable_minibatching:
     raise NotImplementedError("minibatching is not supported on this path")
   if int(sharding_strategy) != int(ShardingStrategy.MOD):
@@ -348,9 +362,20 @@ def preprocess_sparse_dense_matmul_input(
     raise ValueError("features and feature_specs must have equal length")
   if not features:
     raise ValueError("input_batches cannot be empty.")
+  return features, feature_weights, feature_specs
+
+
+def enqueue_preprocessing(features, feature_weights, feature_specs,
+                          local_device_count: int, global_device_count: int,
+                          *, num_sc_per_device: int,
+                          has_leading_dimension: bool = False,
+                          allow_id_dropping: bool = False):
+  """Enqueues the preprocessing of every stack on the current stream without
+  waiting for it. Returns the CSR dicts and the pending stats, which
+  collect_stats turns into a SparseDenseMatmulInputStats (one wait)."""
   stacks = get_stacked_table_metadata(feature_specs)
   rps, eids, sids, gns = {}, {}, {}, {}
-  stats = SparseDenseMatmulInputStats()
+  pending = []
   for name, metas in stacks.items():
     feats = [
         _to_device_feature(
@@ -358,13 +383,33 @@ def preprocess_sparse_dense_matmul_input(
             None if feature_weights is None else
             feature_weights[m.feature_index]) for m in metas
     ]
-    rp, eid, sid, gains, stats_np, counters, (L, S, ns, _) = (
-        _preprocess_stack(feats, metas,
-                          local_device_count=local_device_count,
-                          global_device_count=global_device_count,
-                          num_sc_per_device=num_sc_per_device,
-                          allow_id_dropping=allow_id_dropping,
-                          has_weights=feature_weights is not None))
+    rp, eid, sid, gains, stats_dev, (L, S, ns, off) = _preprocess_stack(
+        feats, metas, local_device_count=local_device_count,
+        global_device_count=global_device_count,
+        num_sc_per_device=num_sc_per_device,
+        allow_id_dropping=allow_id_dropping,
+        has_weights=feature_weights is not None)
+    pending.append((name, stats_dev, L, S, ns, off, feats))
+    if has_leading_dimension:
+      rp, eid, sid, gains = (rp.reshape(L, -1), eid.reshape(L, -1),
+                             sid.reshape(L, -1), gains.reshape(L, -1))
+    rps[name], eids[name], sids[name], gns[name] = rp, eid, sid, gains
+  return rps, eids, sids, gns, pending
+
+
+def collect_stats(pending) -> SparseDenseMatmulInputStats:
+  """Waits for the enqueued preprocessing and returns its stats; raises as
+  the reference does on bad ids or exceeded limits."""
+  stats = SparseDenseMatmulInputStats()
+  if not pending:
+    return stats
+  t = _native.torch()
+  host = t.cat([p[1] for p in pending]).cpu().numpy()  # one wait
+  pos = 0
+  for name, stats_dev, L, S, ns, off, _ in pending:
+    stats_np = host[pos:pos + stats_dev.numel()]
+    pos += stats_dev.numel()
+    counters = stats_np[off:off + 8].copy().view(np.int64)
     if counters[2] > 0:
       raise ValueError(
           f"{int(counters[2])} embedding ids of stacked table {name} are "
@@ -382,11 +427,7 @@ def preprocess_sparse_dense_matmul_input(
                                                  L * S].copy()
     stats.dropped_id_count[name] = int(counters[0])
     stats.num_entries[name] = int(counters[3])
-    if has_leading_dimension:
-      rp, eid, sid, gains = (rp.reshape(L, -1), eid.reshape(L, -1),
-                             sid.reshape(L, -1), gains.reshape(L, -1))
-    rps[name], eids[name], sids[name], gns[name] = rp, eid, sid, gains
-  return rps, eids, sids, gns, 1, stats
+  return stats
 
 
 def preprocess_sparse_dense_matmul_sparse_coo_input(*args, **kwargs):

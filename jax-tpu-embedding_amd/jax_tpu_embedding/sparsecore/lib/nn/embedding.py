@@ -291,26 +291,33 @@ def preprocess_sparse_dense_matmul_input(
       local_device_count < global_device_count):
     raise ValueError("all_reduce_interface must be provided when minibatching "
                      "is enabled for multi-host.")
-  *csr, num_minibatches, stats = (
-      pybind_input_preprocessing.preprocess_sparse_dense_matmul_input(
-          _tree.tree_leaves(features),
-          (_tree.tree_leaves(features_weights)
-           if features_weights is not None else None),
-          _tree.tree_leaves(feature_specs), local_device_count,
-          global_device_count, num_sc_per_device=num_sc_per_device,
-          sharding_strategy=sharding_strategy_to_enum(sharding_strategy),
-          has_leading_dimension=has_leading_dimension,
-          allow_id_dropping=allow_id_dropping, batch_number=batch_number,
-          enable_minibatching=enable_minibatching,
-          all_reduce_interface=all_reduce_interface))
-  minibatches = np.full(local_device_count, num_minibatches, dtype=np.int32)
-  if has_leading_dimension:
-    minibatches = minibatches.reshape(local_device_count, 1)
+  del batch_number
+  feats, weights, specs = pybind_input_preprocessing.check_arguments(
+      _tree.tree_leaves(features),
+      (_tree.tree_leaves(features_weights)
+       if features_weights is not None else None),
+      _tree.tree_leaves(feature_specs),
+      sharding_strategy_to_enum(sharding_strategy), enable_minibatching)
+  # Everything is enqueued (CSR build, then the lookup views) before the one
+  # wait for the stats.
+  *csr, pending = pybind_input_preprocessing.enqueue_preprocessing(
+      feats, weights, specs, local_device_count, global_device_count,
+      num_sc_per_device=num_sc_per_device,
+      has_leading_dimension=has_leading_dimension,
+      allow_id_dropping=allow_id_dropping)
   views = None
-  counts = dict(stats.num_entries) if local_device_count == 1 else None
   if local_device_count == 1:
     views = _build_lookup_views(csr, feature_specs, global_device_count,
-                                num_sc_per_device, counts)
+                                num_sc_per_device)
+  stats = pybind_input_preprocessing.collect_stats(pending)
+  counts = None
+  if local_device_count == 1:
+    counts = dict(stats.num_entries)
+    for name, view in views.items():
+      view.num_entries = counts.get(name, 0)
+  minibatches = np.full(local_device_count, 1, dtype=np.int32)
+  if has_leading_dimension:
+    minibatches = minibatches.reshape(local_device_count, 1)
   return (PreprocessedInput(SparseDenseMatmulInput(*csr), minibatches,
                             lookup_views=views,
                             csr_sorted_by_row=local_device_count == 1,
@@ -319,7 +326,7 @@ def preprocess_sparse_dense_matmul_input(
 
 
 def _build_lookup_views(csr, feature_specs, global_device_count: int,
-                        num_sc_per_device: int, counts):
+                        num_sc_per_device: int):
   """Sample views of one device's CSR buffers, one per stacked table, for a
   table shard of stack_vocab_size / global_device_count rows."""
   rp, eid, sid, gains = csr
@@ -329,8 +336,7 @@ def _build_lookup_views(csr, feature_specs, global_device_count: int,
     rows = spec.stack_vocab_size // global_device_count
     _, c = _device.csr_operands(rp[name], eid[name], sid[name], gains[name],
                                 num_sc_per_device,
-                                num_sc_per_device * global_device_count,
-                                num_entries=counts.get(name))
+                                num_sc_per_device * global_device_count)
     views[name] = _native.build_sample_view(c, batch, rows)
   return views
 
