@@ -219,6 +219,70 @@ int scemb_sparse_dense_matmul_grad_with_adagrad_from_blocks(
     float min_value, float max_value, void* workspace, size_t workspace_bytes,
     uint32_t* device_status, void* stream);
 
+/* ---- Backward + any built-in optimizer ----------------------------------
+ * The reference lowers every optimizer to the same custom call,
+ * SparseDenseMatmulGradOpWithOptimizerUpdate, with num_slot_variables,
+ * num_hyperparameters and a row-wise update function
+ * (primitives/sparse_dense_matmul_grad_with_{sgd,adagrad,adam,
+ * adagrad_momentum,ftrl,laprop,f2a}.py, the `operands` lists of each
+ * lowering). These two entry points are that call: `optimizer` names the
+ * update, its slot variables (same shape as the table, updated in place) and
+ * hyperparameters, in the order of the primitive's operands:
+ *   SGD              slots -;  (learning_rate)
+ *   ADAGRAD          slots (accumulator);  (learning_rate)
+ *   ADAM             slots (momentum, velocity);
+ *                    (alpha_t, beta_1, beta_2, epsilon_hat)
+ *   ADAGRAD_MOMENTUM slots (accumulator, momentum);
+ *                    (learning_rate, momentum, beta2, epsilon, exponent,
+ *                     use_nesterov != 0)
+ *   FTRL             slots (accumulator, linear);
+ *                    (learning_rate, learning_rate_power, l1, l2, beta);
+ *                    flag MULTIPLY_LINEAR_BY_LR
+ *   LAPROP           slots (mu, nu);  (learning_rate, b1, decay_rate, eps)
+ *   F2A              slots (accumulator, local_step);
+ *                    (learning_rate, rho, l1, l2, max_lr_multiplier,
+ *                     global_step)
+ * Hyperparameter i is read from the device scalar hyperparameter_ptrs[i]
+ * when that is not NULL, else hyperparameters[i] is used. The update of each
+ * touched row applies the reference's row-wise function in its operation
+ * order, then the clipping as above; the gradient sum is the same fixed-order
+ * reduction as the calls above. Workspace:
+ * scemb_sparse_dense_matmul_grad_workspace_size. */
+#define SCEMB_OPTIMIZER_SGD 0
+#define SCEMB_OPTIMIZER_ADAGRAD 1
+#define SCEMB_OPTIMIZER_ADAM 2
+#define SCEMB_OPTIMIZER_ADAGRAD_MOMENTUM 3
+#define SCEMB_OPTIMIZER_FTRL 4
+#define SCEMB_OPTIMIZER_LAPROP 5
+#define SCEMB_OPTIMIZER_F2A 6
+#define SCEMB_MAX_HYPERPARAMETERS 8
+/* FTRL's multiply_linear_by_learning_rate (a static attribute of the
+ * reference primitive, sparse_dense_matmul_grad_with_ftrl.py). */
+#define SCEMB_OPTIMIZER_FLAG_MULTIPLY_LINEAR_BY_LR 1u
+
+typedef struct scemb_optimizer {
+  int32_t kind;   /* SCEMB_OPTIMIZER_* */
+  uint32_t flags; /* SCEMB_OPTIMIZER_FLAG_* */
+  float* slots[2];
+  const float* hyperparameter_ptrs[SCEMB_MAX_HYPERPARAMETERS];
+  float hyperparameters[SCEMB_MAX_HYPERPARAMETERS];
+  int32_t clip_mask; /* bit 0: min_value, bit 1: max_value */
+  float min_value;
+  float max_value;
+} scemb_optimizer_t;
+
+int scemb_sparse_dense_matmul_grad_with_optimizer(
+    const scemb_csr_t* csr, const float* activations_grad,
+    int64_t device_batch_size, float* table, int64_t table_rows, int32_t dim,
+    const scemb_optimizer_t* optimizer, void* workspace,
+    size_t workspace_bytes, uint32_t* device_status, void* stream);
+int scemb_sparse_dense_matmul_grad_with_optimizer_from_blocks(
+    const scemb_csr_t* csr, const scemb_row_block_t* activation_grads,
+    int32_t num_blocks, int64_t device_batch_size, float* table,
+    int64_t table_rows, int32_t dim, const scemb_optimizer_t* optimizer,
+    void* workspace, size_t workspace_bytes, uint32_t* device_status,
+    void* stream);
+
 /* ---- Preprocessing: PreprocessSparseDenseMatmulInput, one stacked table --
  * Inputs: the features of one stack, in row_offset order (the order
  * GetStackedTableMetadata produces, pybind_input_preprocessing.cc:114-120).

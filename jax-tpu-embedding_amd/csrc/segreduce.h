@@ -1,0 +1,1156 @@
+// Segmented reduction kernels shared by the forward lookup and every fused
+// backward + optimizer update (one translation unit per optimizer), for the
+// SparseDenseMatmulOp and SparseDenseMatmulGradOpWithOptimizerUpdate custom
+// calls of jax_tpu_embedding/sparsecore/lib/core/primitives/.
+//
+// Both directions are one segmented reduction over a stream of entries
+// (key, row, gain) sorted by key:
+//   forward   key = activation row, gathered row = table row
+//             epilogue: store the activation row (rows without entries are
+//             zero-filled)
+//   backward  key = table row, gathered row = activation-gradient row
+//             epilogue: optimizer update of the table row and its slot rows
+// The stream comes from one of three places:
+//   * the CSR itself when it is already sorted by table row (backward; one
+//     segment, as the preprocessing emits it: partitions in order, embedding
+//     ids ascending inside each partition);
+//   * a sample view built once per preprocessed batch (forward);
+//   * otherwise ExpandCsr + a stable radix sort inside the call.
+//
+// SegReduce gives every 256-thread block a fixed slice of 256 stream entries
+// (perfect load balance however skewed the keys are). A block is split into
+// P = 256 / G sub-groups of G lanes; sub-group s owns entries [s*G, s*G + G)
+// of the slice and its lanes cover G * VEC columns of a row (16-byte loads).
+// A sub-group walks its entries kUnroll at a time, issuing all row loads of a
+// batch (and, for runs that end inside the batch, the table / accumulator
+// loads of the update) before accumulating. A run that is complete inside
+// one sub-group is finished there; pieces of runs that cross sub-groups are
+// combined through LDS in sub-group order; pieces of runs that cross blocks
+// leave one partial row per block and SegFinish adds them in block order.
+// Every row is reduced and written exactly once, in a fixed order: no float
+// atomics and run-to-run identical results.
+#pragma once
+
+#include "../../include/scemb.h"
+#include "common.h"
+#include "scan.h"
+
+namespace scemb {
+
+// Which update the backward epilogue applies (the forward stores instead).
+enum {
+  kEpiFwd = 0,
+  kEpiSgd = 1,
+  kEpiAdagrad = 2,
+  kEpiAdam = 3,
+  kEpiAdagradMomentum = 4,
+  kEpiFtrl = 5,
+  kEpiLaprop = 6,
+  kEpiF2a = 7,
+};
+
+constexpr int kMaxHyper = SCEMB_MAX_HYPERPARAMETERS;
+
+// Hyperparameters of the update: value i is *ptr[i] (a device scalar, read
+// once per block) when ptr[i] is set, else value[i]. Clipping of the updated
+// table values, then the optimizer's flags.
+struct OptParams {
+  const float* ptr[kMaxHyper];
+  float value[kMaxHyper];
+  int32_t clip_mask;  // bit 0: min_value, bit 1: max_value
+  float min_value;
+  float max_value;
+  uint32_t flags;     // SCEMB_OPTIMIZER_FLAG_*
+};
+
+constexpr int kMaxRowBlocks = SCEMB_MAX_ROW_BLOCKS;
+
+// The activation matrix (forward output, backward input) as per-feature row
+// blocks: stacked rows [first, end) of block b live at data[b] with
+// stride[b] floats between rows and width[b] leading columns (the rest of
+// the dim columns are padding: not written, read as zero). n == 0: one
+// dense [batch, dim] matrix.
+struct RowMap {
+  int32_t n;
+  int64_t first[kMaxRowBlocks];
+  int64_t end[kMaxRowBlocks];
+  int64_t stride[kMaxRowBlocks];
+  int32_t width[kMaxRowBlocks];
+  float* data[kMaxRowBlocks];
+};
+
+// One backward call: the CSR, the activation gradients (dense, or through
+// `map` when it is set), the table and up to two slot variables updated in
+// place, the hyperparameters, and where temporaries and problems go.
+struct GradCall {
+  const scemb_csr_t* csr;
+  const float* act_grad;
+  const RowMap* map;
+  bool map_vec4;  // every block of `map` allows 16-byte accesses
+  int64_t batch;
+  float* table;
+  float* slot0;
+  float* slot1;
+  int64_t table_rows;
+  int32_t dim;
+  OptParams opt;
+  Arena* ws;  // sizing pass when ws->measuring()
+  uint32_t* status;
+  hipStream_t stream;
+};
+
+// Backward + optimizer for the optimizers with two slot variables, each in a
+// translation unit of its own (optimizer_*.hip).
+int GradWithAdam(const GradCall& c);
+int GradWithAdagradMomentum(const GradCall& c);
+int GradWithFtrl(const GradCall& c);
+int GradWithLaprop(const GradCall& c);
+int GradWithF2a(const GradCall& c);
+
+namespace {
+
+
+constexpr int kBlock = 256;  // threads per block = stream entries per block
+// Entries whose rows a sub-group loads together (memory-level parallelism;
+// the backward also holds the table / accumulator rows of the runs that end
+// in the batch). Batches of about one entry per activation row ("one-hot")
+// gain from the wide setting; multi-hot batches, whose gathers mostly hit
+// cache, from the higher occupancy of the narrow one (fewer registers).
+constexpr int kFwdUnrollWide = 8;
+constexpr int kFwdUnrollNarrow = 4;
+constexpr int kBwdUnrollWide = 4;
+constexpr int kBwdUnrollNarrow = 2;
+// Entries per activation row up to which a batch counts as one-hot.
+constexpr int64_t kOneHotMaxEntriesPerRow = 2;
+// Streaming (nontemporal) access for data touched once per call, so the
+// last-level cache keeps table rows: activations written by the forward
+// always; activation gradients read by the backward for one-hot batches
+// only (a multi-hot batch re-reads every gradient row from cache many
+// times). Table and accumulator rows stay cacheable: the next forward reads
+// the rows the backward has just written.
+constexpr bool kNtAct = true;
+constexpr bool kNtTable = false;
+constexpr uint32_t kSkip = 0xffffffffu;  // key of an entry outside any run
+
+// Per-block flags left by SegReduce for SegFinish.
+constexpr uint32_t kFlagHeadEnd = 1;  // a run from earlier blocks ends here
+constexpr uint32_t kFlagOwner = 2;    // a run starts here, continues past
+constexpr uint32_t kFlagMiddle = 4;   // the whole block lies inside one run
+
+// Per-sub-group piece flags (LDS).
+constexpr uint32_t kHasHead = 1;   // first entry continues the previous run
+constexpr uint32_t kHeadEnds = 2;  // ... and that run ends in this range
+constexpr uint32_t kHasTail = 4;   // a run starts here and continues past
+
+enum { kSrcSorted = 0, kSrcCsr = 1 };
+
+struct Csr {
+  const int32_t* rp;
+  const int32_t* eid;
+  const int32_t* sid;
+  const float* gains;
+  int64_t per_segment;  // coo_size / num_segments
+  int32_t num_segments;
+  int32_t num_partitions;
+  int32_t rp_per_segment;
+};
+
+__device__ __forceinline__ uint64_t Pack(uint32_t lo, float g) {
+  return static_cast<uint64_t>(lo) |
+         (static_cast<uint64_t>(__float_as_uint(g)) << 32);
+}
+__device__ __forceinline__ uint32_t PackedIndex(uint64_t p) {
+  return static_cast<uint32_t>(p);
+}
+__device__ __forceinline__ float PackedGain(uint64_t p) {
+  return __uint_as_float(static_cast<uint32_t>(p >> 32));
+}
+
+// Partition of position `off` of a segment whose row pointers are `rp`
+// (partitions start at 8-aligned offsets), or -1 for padding.
+__device__ __forceinline__ int PartitionOf(const int32_t* rp, int nparts,
+                                           int64_t per_segment, int64_t off) {
+  int64_t start = 0;
+  for (int q = 0; q < nparts; ++q) {
+    int64_t end = rp[q];
+    if (end > per_segment) end = per_segment;
+    if (off < end) return off >= start ? q : -1;
+    start = (end + kAlign - 1) / kAlign * kAlign;
+  }
+  return -1;
+}
+
+// One (key, payload) pair per COO position; padding and invalid entries get
+// the sentinel key, which sorts last.
+template <bool kBySample>
+__global__ __launch_bounds__(256) void ExpandCsr(Csr csr, int64_t bps,
+                                                 int64_t rows_per_partition,
+                                                 uint32_t sentinel,
+                                                 uint32_t* keys,
+                                                 uint64_t* payload,
+                                                 uint32_t* status) {
+  const int64_t n = csr.per_segment * csr.num_segments;
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const int s = static_cast<int>(j / csr.per_segment);
+  const int64_t off = j - static_cast<int64_t>(s) * csr.per_segment;
+  const int p = PartitionOf(csr.rp + static_cast<int64_t>(s) * csr.rp_per_segment,
+                            csr.num_partitions, csr.per_segment, off);
+  uint32_t key = sentinel;
+  uint64_t pay = 0;
+  if (p >= 0) {
+    const int32_t e = csr.eid[j];
+    const int32_t sm = csr.sid[j];
+    if (e >= 0 && e < rows_per_partition && sm >= 0 && sm < bps) {
+      const uint32_t trow =
+          static_cast<uint32_t>(p * rows_per_partition + e);
+      const uint32_t arow = static_cast<uint32_t>(s * bps + sm);
+      const float g = csr.gains[j];
+      if (kBySample) {
+        key = arow;
+        pay = Pack(trow, g);
+      } else {
+        key = trow;
+        pay = Pack(arow, g);
+      }
+    } else if (status != nullptr) {
+      atomicOr(status, SCEMB_STATUS_BAD_ENTRY);
+    }
+  }
+  keys[j] = key;
+  payload[j] = pay;
+}
+
+template <int VEC>
+struct Vec;
+typedef float NativeF4 __attribute__((ext_vector_type(4)));
+template <>
+struct Vec<4> {
+  using T = float4;
+  __device__ static T Zero() { return make_float4(0.f, 0.f, 0.f, 0.f); }
+  __device__ static T Load(const float* p) {
+    return *reinterpret_cast<const float4*>(p);
+  }
+  __device__ static void Store(float* p, T v) {
+    *reinterpret_cast<float4*>(p) = v;
+  }
+  __device__ static T LoadNT(const float* p) {
+    const NativeF4 v =
+        __builtin_nontemporal_load(reinterpret_cast<const NativeF4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+  }
+  __device__ static void StoreNT(float* p, T v) {
+    const NativeF4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, reinterpret_cast<NativeF4*>(p));
+  }
+  __device__ static T Fma(T acc, float g, T v) {
+    acc.x = acc.x + g * v.x;
+    acc.y = acc.y + g * v.y;
+    acc.z = acc.z + g * v.z;
+    acc.w = acc.w + g * v.w;
+    return acc;
+  }
+  __device__ static T Add(T a, T b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+  }
+  __device__ static float Get(const T& v, int k) {
+    return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
+  }
+  __device__ static void Set(T& v, int k, float x) {
+    if (k == 0) v.x = x;
+    else if (k == 1) v.y = x;
+    else if (k == 2) v.z = x;
+    else v.w = x;
+  }
+};
+template <>
+struct Vec<1> {
+  using T = float;
+  __device__ static T Zero() { return 0.f; }
+  __device__ static T Load(const float* p) { return *p; }
+  __device__ static void Store(float* p, T v) { *p = v; }
+  __device__ static T LoadNT(const float* p) {
+    return __builtin_nontemporal_load(p);
+  }
+  __device__ static void StoreNT(float* p, T v) {
+    __builtin_nontemporal_store(v, p);
+  }
+  __device__ static T Fma(T acc, float g, T v) { return acc + g * v; }
+  __device__ static T Add(T a, T b) { return a + b; }
+  __device__ static float Get(const T& v, int) { return v; }
+  __device__ static void Set(T& v, int, float x) { v = x; }
+};
+
+template <int VEC, bool NT>
+__device__ __forceinline__ typename Vec<VEC>::T LoadRow(const float* p) {
+  return NT ? Vec<VEC>::LoadNT(p) : Vec<VEC>::Load(p);
+}
+template <int VEC, bool NT>
+__device__ __forceinline__ void StoreRow(float* p, typename Vec<VEC>::T v) {
+  if (NT) {
+    Vec<VEC>::StoreNT(p, v);
+  } else {
+    Vec<VEC>::Store(p, v);
+  }
+}
+
+
+// Where the stream comes from.
+struct StreamArgs {
+  const uint32_t* keys;     // kSrcSorted
+  const uint64_t* entries;  // kSrcSorted: row | gain bits << 32
+  uint32_t sentinel;        // kSrcSorted: keys >= sentinel are unused
+  int64_t src_rows;         // kSrcSorted: rows of the gathered matrix
+  Csr csr;                  // kSrcCsr (one segment)
+  int64_t rows_per_partition;
+  int64_t bps;
+  int64_t n;
+};
+
+// What the reduction reads and writes.
+struct RowArgs {
+  const float* src;  // gathered rows
+  float* dst;        // activations (forward) or table (backward)
+  float* slot0;      // slot variables of the optimizer (backward)
+  float* slot1;
+  int64_t dim;
+  int64_t batch;     // forward: rows of dst
+  bool stream_src;   // gathered rows are read about once: nontemporal loads
+  RowMap act;        // activation layout (dst forward, src backward)
+  OptParams opt;
+  float* partials;   // [2 * num_blocks, dim]
+  uint32_t* block_flags;
+  uint32_t* block_keys;
+  uint32_t* status;
+};
+
+template <int SRC>
+__device__ __forceinline__ uint32_t FetchEntry(const StreamArgs& s, int64_t e,
+                                               uint64_t* ent,
+                                               uint32_t* status) {
+  if (SRC == kSrcSorted) {
+    const uint32_t k = s.keys[e];
+    *ent = s.entries[e];
+    if (k >= s.sentinel) return kSkip;
+    if (PackedIndex(*ent) >= s.src_rows) {
+      // Keeps the key (and so the run structure) but contributes nothing.
+      if (status != nullptr) atomicOr(status, SCEMB_STATUS_BAD_ENTRY);
+      *ent = Pack(0, 0.0f);
+    }
+    return k;
+  } else {
+    *ent = 0;
+    const int p = PartitionOf(s.csr.rp, s.csr.num_partitions,
+                              s.csr.per_segment, e);
+    if (p < 0) return kSkip;
+    const int32_t id = s.csr.eid[e];
+    const int32_t sm = s.csr.sid[e];
+    if (id < 0 || id >= s.rows_per_partition || sm < 0 || sm >= s.bps) {
+      if (status != nullptr) atomicOr(status, SCEMB_STATUS_BAD_ENTRY);
+      return kSkip;
+    }
+    *ent = Pack(static_cast<uint32_t>(sm), s.csr.gains[e]);
+    return static_cast<uint32_t>(p * s.rows_per_partition + id);
+  }
+}
+
+// Slot variables and hyperparameters per optimizer, in the order of the
+// reference's *SlotVariables and get_hyperparameters()
+// (lib/nn/embedding_spec.py:377-916).
+template <int EPI>
+__host__ __device__ constexpr int NumSlots() {
+  return EPI == kEpiFwd || EPI == kEpiSgd ? 0 : EPI == kEpiAdagrad ? 1 : 2;
+}
+template <int EPI>
+__host__ __device__ constexpr int NumHyper() {
+  return EPI == kEpiFwd                                 ? 0
+         : EPI == kEpiSgd || EPI == kEpiAdagrad         ? 1
+         : EPI == kEpiAdam || EPI == kEpiLaprop         ? 4
+         : EPI == kEpiFtrl                              ? 5
+                                                        : 6;
+}
+
+// The hyperparameters as the update reads them, plus what is constant for
+// the whole call.
+struct Hyper {
+  float h[kMaxHyper];
+  float derived;
+};
+
+template <int EPI>
+__device__ __forceinline__ Hyper LoadHyper(const OptParams& o) {
+  Hyper H{};
+#pragma unroll
+  for (int i = 0; i < NumHyper<EPI>(); ++i) {
+    H.h[i] = o.ptr[i] != nullptr ? *o.ptr[i] : o.value[i];
+  }
+  if (EPI == kEpiAdagradMomentum) {
+    H.derived = -1.0f / H.h[4];  // the power applied to accumulator + eps
+  } else if (EPI == kEpiLaprop) {
+    H.derived = powf(1.0f - powf(H.h[1], 2.0f), 0.5f);  // sqrt(1 - b1^2)
+  }
+  return H;
+}
+
+// Update of one table value t with its summed gradient g and slot values
+// s0, s1 (updated in place), followed by the optional clipping of the new
+// table value (primitives/utils.py:24-59). Each form follows the row-wise
+// update function the reference lowers (lib/core/primitives/, the update
+// body of each file):
+//   SGD              optimizers_computation.py:22-69
+//   Adagrad          sparse_dense_matmul_grad_with_adagrad.py:205-233
+//   Adam             sparse_dense_matmul_grad_with_adam.py:283-338
+//   AdagradMomentum  sparse_dense_matmul_grad_with_adagrad_momentum.py:256-311
+//   FTRL             sparse_dense_matmul_grad_with_ftrl.py:260-335
+//   LaProp           sparse_dense_matmul_grad_with_laprop.py:282-340
+//   F2A              sparse_dense_matmul_grad_with_f2a.py:244-290
+// with the operations in the same order and association, so that only the
+// rounding of the library sqrt and pow can differ.
+template <int EPI>
+__device__ __forceinline__ float UpdateOne(float t, float& s0, float& s1,
+                                           float g, const Hyper& H,
+                                           const OptParams& o) {
+  float v;
+  if (EPI == kEpiSgd) {
+    v = t - g * H.h[0];
+  } else if (EPI == kEpiAdagrad) {
+    const float acc = s0 + g * g;
+    s0 = acc;
+    v = t - (H.h[0] * g) / sqrtf(acc);
+  } else if (EPI == kEpiAdam) {
+    // (alpha_t, beta_1, beta_2, epsilon_hat); slots (momentum, velocity).
+    const float m = s0 + (1.0f - H.h[1]) * (g - s0);
+    const float vel = s1 + (1.0f - H.h[2]) * (g * g - s1);
+    s0 = m;
+    s1 = vel;
+    v = t - (H.h[0] * m) / (sqrtf(vel) + H.h[3]);
+  } else if (EPI == kEpiAdagradMomentum) {
+    // (lr, momentum, beta2, epsilon, exponent, use_nesterov); slots
+    // (accumulator, momentum).
+    const float g2 = g * g;
+    const float a = H.h[2] == 1.0f ? s0 + g2
+                                   : H.h[2] * s0 + (1.0f - H.h[2]) * g2;
+    const float sg = powf(a + H.h[3], H.derived) * g;
+    const float m = H.h[1] * s1 + sg;
+    const float upd = H.h[5] != 0.0f ? H.h[1] * m + sg : m;
+    s0 = a;
+    s1 = m;
+    v = t - H.h[0] * upd;
+  } else if (EPI == kEpiFtrl) {
+    // (lr, lr_power, l1, l2, beta); slots (accumulator, linear).
+    const float lr = H.h[0];
+    const float a = s0 + g * g;
+    const float p_old = powf(s0, -H.h[1]);
+    const float p_new = powf(a, -H.h[1]);
+    const float dp = p_new - p_old;
+    const bool by_lr =
+        (o.flags & SCEMB_OPTIMIZER_FLAG_MULTIPLY_LINEAR_BY_LR) != 0;
+    const float lin = by_lr ? (s1 + lr * g) - dp * t
+                            : (s1 + g) - (dp / lr) * t;
+    const float l1s = H.h[2] * (by_lr ? lr : 1.0f);
+    const float num =
+        H.h[2] == 0.0f ? -lin : fminf(fmaxf(lin, -l1s), l1s) - lin;
+    const float den = by_lr ? (p_new + 2.0f * (lr * H.h[3])) + H.h[4]
+                            : (p_new + H.h[4]) / lr + 2.0f * H.h[3];
+    s0 = a;
+    s1 = lin;
+    v = num / den;
+  } else if (EPI == kEpiLaprop) {
+    // (lr, b1, decay_rate, eps); slots (mu, nu).
+    const float gs = g * g + H.h[3];
+    const float nu = s1 * H.h[2] + (1.0f - H.h[2]) * gs;
+    const float u = H.h[1] * s0 + H.derived * (g / sqrtf(nu));
+    s0 = u;
+    s1 = nu;
+    v = t - H.h[0] * u;
+  } else {
+    // F2A: (lr, rho, l1, l2, max_lr_multiplier, global_step); slots
+    // (accumulator, local_step). sign() keeps zeros (and NaN) as they are.
+    const float ls = s1 + 1.0f;
+    const float ratio = fmaxf(H.h[5], 1.0f) / ls;
+    const float fa = fminf(powf(ratio, H.h[1]), H.h[4]);
+    const float a = s0 + g * g;
+    const float sgn = t > 0.0f ? 1.0f : (t < 0.0f ? -1.0f : t);
+    const float upd = (g * fa) / sqrtf(a) + (H.h[2] * sgn + H.h[3] * t);
+    s0 = a;
+    s1 = ls;
+    v = t - H.h[0] * upd;
+  }
+  if (o.clip_mask & 1) v = fmaxf(o.min_value, v);
+  if (o.clip_mask & 2) v = fminf(o.max_value, v);
+  return v;
+}
+
+// The row map staged in LDS by every block that reads or writes
+// activations through it.
+struct RowMapLds {
+  int32_t n;
+  int64_t first[kMaxRowBlocks];
+  int64_t end[kMaxRowBlocks];
+  int64_t stride[kMaxRowBlocks];
+  int32_t width[kMaxRowBlocks];
+  float* data[kMaxRowBlocks];
+};
+
+// Copies the row map into LDS; the caller synchronises the block after.
+__device__ __forceinline__ void StageRowMap(const RowMap& m, RowMapLds* s) {
+  const int t = threadIdx.x;
+  if (t == 0) s->n = m.n;
+  if (t < m.n) {
+    s->first[t] = m.first[t];
+    s->end[t] = m.end[t];
+    s->stride[t] = m.stride[t];
+    s->width[t] = m.width[t];
+    s->data[t] = m.data[t];
+  }
+}
+
+// Address of columns [col, col + VEC) of activation row `row`, or null when
+// the row lies in no block or the columns in its padding. Without a map
+// (kMapped false) the activations are one dense matrix.
+template <bool kMapped>
+__device__ __forceinline__ float* ActAddr(const RowMapLds& m, float* dense,
+                                          int64_t dim, int64_t row,
+                                          int64_t col) {
+  if (!kMapped) return dense + row * dim + col;
+  if (m.n == 0) return nullptr;
+  int lo = 0, hi = m.n;  // last block whose first row is <= row
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (m.first[mid] <= row) lo = mid; else hi = mid;
+  }
+  if (row < m.first[lo] || row >= m.end[lo] || col >= m.width[lo]) {
+    return nullptr;
+  }
+  return m.data[lo] + (row - m.first[lo]) * m.stride[lo] + col;
+}
+
+// Epilogue for the finished row `key` at column `col`, given the table and
+// slot values already loaded (backward) -- or the store (forward).
+template <int VEC, int EPI, bool kMapped>
+__device__ __forceinline__ void Epilogue(const RowArgs& r,
+                                         const RowMapLds& m, uint32_t key,
+                                         int64_t col, typename Vec<VEC>::T g,
+                                         typename Vec<VEC>::T t,
+                                         typename Vec<VEC>::T a,
+                                         typename Vec<VEC>::T b,
+                                         const Hyper& H) {
+  using V = Vec<VEC>;
+  const int64_t off = static_cast<int64_t>(key) * r.dim + col;
+  if (EPI == kEpiFwd) {
+    float* p = ActAddr<kMapped>(m, r.dst, r.dim, key, col);
+    if (p != nullptr) StoreRow<VEC, kNtAct>(p, g);
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    float ak = V::Get(a, k);
+    float bk = V::Get(b, k);
+    V::Set(t, k, UpdateOne<EPI>(V::Get(t, k), ak, bk, V::Get(g, k), H,
+                                r.opt));
+    V::Set(a, k, ak);
+    V::Set(b, k, bk);
+  }
+  StoreRow<VEC, kNtTable>(r.dst + off, t);
+  if (NumSlots<EPI>() >= 1) StoreRow<VEC, kNtTable>(r.slot0 + off, a);
+  if (NumSlots<EPI>() >= 2) StoreRow<VEC, kNtTable>(r.slot1 + off, b);
+}
+
+template <int VEC, int EPI, bool kMapped>
+__device__ __forceinline__ void EpilogueLoad(const RowArgs& r,
+                                             const RowMapLds& m, uint32_t key,
+                                             int64_t col,
+                                             typename Vec<VEC>::T g,
+                                             const Hyper& H) {
+  using V = Vec<VEC>;
+  typename V::T t = V::Zero(), a = V::Zero(), b = V::Zero();
+  const int64_t off = static_cast<int64_t>(key) * r.dim + col;
+  if (EPI != kEpiFwd) t = V::Load(r.dst + off);
+  if (NumSlots<EPI>() >= 1) a = V::Load(r.slot0 + off);
+  if (NumSlots<EPI>() >= 2) b = V::Load(r.slot1 + off);
+  Epilogue<VEC, EPI, kMapped>(r, m, key, col, g, t, a, b, H);
+}
+
+__device__ __forceinline__ uint64_t LowBits(int k) {
+  return k >= 64 ? ~0ull : ((1ull << k) - 1);
+}
+
+template <int G, int VEC, bool kMapped>
+__device__ __forceinline__ void ZeroRows(const RowMapLds& m, float* dst,
+                                         int64_t dim, int64_t lo, int64_t hi,
+                                         int cl) {
+  using V = Vec<VEC>;
+  for (int64_t row = lo; row < hi; ++row) {
+    for (int64_t col = static_cast<int64_t>(cl) * VEC; col < dim;
+         col += static_cast<int64_t>(G) * VEC) {
+      float* p = ActAddr<kMapped>(m, dst, dim, row, col);
+      if (p != nullptr) StoreRow<VEC, kNtAct>(p, V::Zero());
+    }
+  }
+}
+
+template <int G, int VEC, int SRC, int EPI, int kUnroll, bool kMapped>
+__global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
+  using V = Vec<VEC>;
+  using T = typename V::T;
+  constexpr int P = kBlock / G;
+  __shared__ uint32_t s_key[kBlock + 2];  // [0]: entry before, [257]: after
+  __shared__ uint64_t s_ent[kBlock];
+  __shared__ T s_part[2 * P][G];
+  __shared__ uint32_t s_info[P];
+  __shared__ RowMapLds s_map;
+
+  const int tid = threadIdx.x;
+  const int64_t blk = blockIdx.x;
+  const int64_t cb = blk * kBlock;
+  const int64_t n = st.n;
+  // Blocks that lie wholly in the padding after the last entry (CSR buffers
+  // are sized for the worst case) only clear their flag: with the CSR, past
+  // the end of the last partition; with a sorted stream, after an unused key
+  // (unused keys sort last, and the first one still has gaps to fill).
+  {
+    bool tail;
+    if (SRC == kSrcCsr) {
+      int64_t end = 0;
+      for (int q = 0; q < st.csr.num_partitions; ++q) {
+        end = st.csr.rp[q] > end ? st.csr.rp[q] : end;
+      }
+      tail = cb >= end;
+    } else {
+      tail = cb > 0 && st.keys[cb - 1] >= st.sentinel;
+    }
+    if (tail) {
+      if (tid == 0) r.block_flags[blk] = 0;
+      return;
+    }
+  }
+  if (kMapped) StageRowMap(r.act, &s_map);
+  {
+    uint64_t en = 0;
+    uint32_t k = kSkip;
+    if (cb + tid < n) k = FetchEntry<SRC>(st, cb + tid, &en, r.status);
+    s_key[tid + 1] = k;
+    s_ent[tid] = en;
+    if (tid == 0) {
+      uint64_t d;
+      s_key[0] = cb > 0 ? FetchEntry<SRC>(st, cb - 1, &d, nullptr) : kSkip;
+    }
+    if (tid == kBlock - 1) {
+      uint64_t d;
+      s_key[kBlock + 1] =
+          cb + kBlock < n ? FetchEntry<SRC>(st, cb + kBlock, &d, nullptr)
+                          : kSkip;
+    }
+  }
+  __syncthreads();
+
+  const int sub = tid / G;
+  const int cl = tid % G;
+  const int base = sub * G;  // first entry of the sub-group in the block
+  const int64_t left = n - (cb + base);
+  const int cnt = left <= 0 ? 0 : (left < G ? static_cast<int>(left) : G);
+  const uint32_t my_key = s_key[tid + 1];
+  const uint32_t prev_key = s_key[tid];
+  const bool mine = cl < cnt;
+  const bool valid = mine && my_key != kSkip;
+
+  if (r.status != nullptr && mine) {
+    const bool bad = SRC == kSrcCsr
+                         ? (valid && prev_key != kSkip && prev_key > my_key)
+                         : (cb + tid > 0 && prev_key > my_key);
+    if (bad) atomicOr(r.status, SCEMB_STATUS_UNSORTED);
+  }
+
+  const int wshift = (tid % kWave) / G * G;
+  const uint64_t gmask = LowBits(G);
+  const uint64_t valid_m = (__ballot(valid) >> wshift) & gmask;
+  const uint64_t start_m =
+      (__ballot(valid && my_key != prev_key) >> wshift) & gmask;
+  const uint64_t end_m =
+      (__ballot(valid && (cl == cnt - 1 || my_key != s_key[tid + 2])) >>
+       wshift) & gmask;
+
+  if (EPI == kEpiFwd) {
+    // Activation rows without entries: rows strictly between the clamped
+    // keys of consecutive entries, before the first and after the last.
+    const int64_t e = cb + tid;
+    const int64_t ck = my_key == kSkip ? r.batch : my_key;
+    const int64_t cp = e == 0 ? -1 : (prev_key == kSkip ? r.batch : prev_key);
+    const bool gap = mine && ck > cp + 1;
+    uint64_t m = (__ballot(gap) >> wshift) & gmask;
+    while (m) {
+      const int l = __ffsll(static_cast<long long>(m)) - 1;
+      m &= m - 1;
+      const int64_t lo = __shfl(static_cast<int>(cp + 1), wshift + l);
+      const int64_t hi = __shfl(static_cast<int>(ck), wshift + l);
+      ZeroRows<G, VEC, kMapped>(s_map, r.dst, r.dim, lo, hi, cl);
+    }
+    const bool tail_gap = mine && e == n - 1 && ck + 1 < r.batch;
+    m = (__ballot(tail_gap) >> wshift) & gmask;
+    if (m) {
+      const int l = __ffsll(static_cast<long long>(m)) - 1;
+      const int64_t lo = __shfl(static_cast<int>(ck + 1), wshift + l);
+      ZeroRows<G, VEC, kMapped>(s_map, r.dst, r.dim, lo, r.batch, cl);
+    }
+  }
+
+  // Pieces of this sub-group's range that are not whole runs.
+  const bool head_cont = (valid_m & 1) && !(start_m & 1);
+  bool tail_cont = false;
+  if (cnt > 0) {
+    const uint32_t kl = s_key[base + cnt];
+    tail_cont = kl != kSkip && kl == s_key[base + cnt + 1];
+  }
+  const bool whole = head_cont && tail_cont &&
+                     (start_m & ~1ull & LowBits(cnt)) == 0;
+  const uint32_t info = (head_cont ? kHasHead : 0) |
+                        (head_cont && !whole ? kHeadEnds : 0) |
+                        (tail_cont && !whole ? kHasTail : 0);
+  if (cl == 0) s_info[sub] = info;
+  if (tid == 0) {
+    const int last = n - cb < kBlock ? static_cast<int>(n - cb) : kBlock;
+    const uint32_t kf = s_key[1], kl = s_key[last];
+    const bool from_prev = kf != kSkip && kf == s_key[0];
+    const bool to_next = kl != kSkip && kl == s_key[last + 1];
+    uint32_t f;
+    if (from_prev && to_next && kf == kl) {
+      f = kFlagMiddle;
+    } else {
+      f = (from_prev ? kFlagHeadEnd : 0) | (to_next ? kFlagOwner : 0);
+    }
+    r.block_flags[blk] = f;
+    if (f & kFlagOwner) r.block_keys[blk] = kl;
+  }
+
+  const Hyper H = LoadHyper<EPI>(r.opt);
+  const int64_t dim = r.dim;
+  for (int64_t col0 = 0; col0 < dim; col0 += static_cast<int64_t>(G) * VEC) {
+    const int64_t col = col0 + static_cast<int64_t>(cl) * VEC;
+    const bool col_ok = col < dim;
+    T acc = V::Zero();
+    for (int q = 0; q < cnt; q += kUnroll) {
+      T v[kUnroll];
+      T tv[kUnroll];
+      T av[kUnroll];
+      T bv[kUnroll];
+      float gn[kUnroll];
+      uint32_t kk[kUnroll];
+      bool fin[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int idx = q + u;
+        const bool val = idx < cnt && ((valid_m >> idx) & 1);
+        uint64_t en = 0;
+        kk[u] = kSkip;
+        if (val) {
+          en = s_ent[base + idx];
+          kk[u] = s_key[base + idx + 1];
+        }
+        gn[u] = PackedGain(en);
+        v[u] = V::Zero();
+        if (val && col_ok) {
+          // Forward: table rows (dense); backward: activation-gradient rows
+          // through the row map.
+          const float* p =
+              EPI == kEpiFwd
+                  ? r.src + static_cast<int64_t>(PackedIndex(en)) * dim + col
+                  : ActAddr<kMapped>(s_map, const_cast<float*>(r.src), dim,
+                                     PackedIndex(en), col);
+          if (p != nullptr) v[u] = r.stream_src ? V::LoadNT(p) : V::Load(p);
+        }
+        const bool is_end = val && ((end_m >> idx) & 1);
+        const bool first = (start_m & ~1ull & LowBits(idx + 1)) == 0;
+        const bool head_piece = head_cont && first;
+        const bool tail_piece = idx == cnt - 1 && tail_cont;
+        fin[u] = is_end && !head_piece && !tail_piece;
+        tv[u] = V::Zero();
+        av[u] = V::Zero();
+        bv[u] = V::Zero();
+        if (EPI != kEpiFwd && fin[u] && col_ok) {
+          const int64_t off = static_cast<int64_t>(kk[u]) * dim + col;
+          tv[u] = V::Load(r.dst + off);
+          if (NumSlots<EPI>() >= 1) av[u] = V::Load(r.slot0 + off);
+          if (NumSlots<EPI>() >= 2) bv[u] = V::Load(r.slot1 + off);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        const int idx = q + u;
+        if (idx < cnt && ((valid_m >> idx) & 1)) {
+          acc = V::Fma(acc, gn[u], v[u]);
+          if ((end_m >> idx) & 1) {
+            if (fin[u]) {
+              if (col_ok) {
+                Epilogue<VEC, EPI, kMapped>(r, s_map, kk[u], col, acc, tv[u],
+                                            av[u], bv[u], H);
+              }
+            } else {
+              const bool first = (start_m & ~1ull & LowBits(idx + 1)) == 0;
+              s_part[head_cont && first ? 2 * sub : 2 * sub + 1][cl] = acc;
+            }
+            acc = V::Zero();
+          }
+        }
+      }
+    }
+    __syncthreads();
+    // Runs crossing sub-group boundaries: the sub-group holding a run's first
+    // piece in this block adds the following sub-groups' head pieces.
+    for (int job = 0; job < 2; ++job) {
+      const bool active =
+          job == 0 ? (sub == 0 && (info & kHasHead)) : (info & kHasTail) != 0;
+      if (!active) continue;
+      T g = s_part[job == 0 ? 0 : 2 * sub + 1][cl];
+      bool ended = job == 0 && (info & kHeadEnds);
+      for (int tt = sub + 1; !ended && tt < P; ++tt) {
+        const uint32_t inf = s_info[tt];
+        if (!(inf & kHasHead)) break;
+        g = V::Add(g, s_part[2 * tt][cl]);
+        ended = (inf & kHeadEnds) != 0;
+      }
+      const uint32_t key = job == 0 ? s_key[1] : s_key[base + cnt];
+      if (job == 1 && ended) {
+        if (col_ok) EpilogueLoad<VEC, EPI, kMapped>(r, s_map, key, col, g, H);
+      } else if (col_ok) {
+        const int64_t slot = job == 1 ? 2 * blk + 1 : 2 * blk;
+        V::Store(r.partials + slot * dim + col, g);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Runs that cross blocks: the block where such a run starts (kFlagOwner)
+// finds the block where it ends (the next kFlagHeadEnd; every block between
+// is kFlagMiddle), adds the partial rows in block order and applies the
+// epilogue once.
+template <int G, int VEC, int EPI, bool kMapped>
+__global__ __launch_bounds__(kBlock) void SegFinish(int64_t num_blocks,
+                                                    RowArgs r) {
+  using V = Vec<VEC>;
+  using T = typename V::T;
+  constexpr int P = kBlock / G;
+  constexpr int kWaves = kBlock / kWave;
+  __shared__ T s_part[P][G];
+  __shared__ int64_t s_end[kWaves];
+  __shared__ RowMapLds s_map;
+  const int64_t blk = blockIdx.x;
+  if (!(r.block_flags[blk] & kFlagOwner)) return;
+  const int tid = threadIdx.x;
+  if (kMapped) {
+    StageRowMap(r.act, &s_map);
+    __syncthreads();
+  }
+  const int sub = tid / G;
+  const int cl = tid % G;
+  const uint32_t key = r.block_keys[blk];
+  int64_t c1 = -1;
+  for (int64_t b0 = blk + 1; b0 < num_blocks && c1 < 0; b0 += kBlock) {
+    const int64_t c = b0 + tid;
+    const bool is_end = c < num_blocks && (r.block_flags[c] & kFlagHeadEnd);
+    const uint64_t m = __ballot(is_end);
+    if (tid % kWave == 0) {
+      s_end[tid / kWave] =
+          m ? b0 + (tid / kWave) * kWave +
+                  (__ffsll(static_cast<long long>(m)) - 1)
+            : -1;
+    }
+    __syncthreads();
+    for (int w = 0; w < kWaves; ++w) {
+      if (s_end[w] >= 0) {
+        c1 = s_end[w];
+        break;
+      }
+    }
+    __syncthreads();
+  }
+  if (c1 < 0) {
+    if (tid == 0 && r.status != nullptr) {
+      atomicOr(r.status, SCEMB_STATUS_BAD_ENTRY);
+    }
+    return;
+  }
+  const int64_t m = c1 - blk + 1;  // partial rows: 2*blk+1, then 2*(blk+q)
+  const Hyper H = LoadHyper<EPI>(r.opt);
+  const int64_t dim = r.dim;
+  for (int64_t col0 = 0; col0 < dim; col0 += static_cast<int64_t>(G) * VEC) {
+    const int64_t col = col0 + static_cast<int64_t>(cl) * VEC;
+    const bool col_ok = col < dim;
+    T acc = V::Zero();
+    if (col_ok) {
+      int64_t q = sub;
+      for (; q + 3 * P < m; q += 4 * P) {
+        const T p0 = V::Load(r.partials +
+                             (q == 0 ? 2 * blk + 1 : 2 * (blk + q)) * dim + col);
+        const T p1 = V::Load(r.partials + 2 * (blk + q + P) * dim + col);
+        const T p2 = V::Load(r.partials + 2 * (blk + q + 2 * P) * dim + col);
+        const T p3 = V::Load(r.partials + 2 * (blk + q + 3 * P) * dim + col);
+        acc = V::Add(acc, p0);
+        acc = V::Add(acc, p1);
+        acc = V::Add(acc, p2);
+        acc = V::Add(acc, p3);
+      }
+      for (; q < m; q += P) {
+        acc = V::Add(acc, V::Load(r.partials +
+                                  (q == 0 ? 2 * blk + 1 : 2 * (blk + q)) * dim +
+                                  col));
+      }
+    }
+    s_part[sub][cl] = acc;
+    __syncthreads();
+    if (sub == 0) {
+      T g = s_part[0][cl];
+      for (int s = 1; s < P; ++s) g = V::Add(g, s_part[s][cl]);
+      if (col_ok) EpilogueLoad<VEC, EPI, kMapped>(r, s_map, key, col, g, H);
+    }
+    __syncthreads();
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+
+struct Geometry {
+  int64_t n;  // COO positions
+  int64_t bps;
+  int64_t rows_per_partition;
+};
+
+int CheckCsr(const scemb_csr_t* csr, int64_t batch, int64_t table_rows,
+             int32_t dim, Geometry* geo) {
+  if (csr == nullptr) return Fail(SCEMB_ERR_INVALID_ARGUMENT, "csr is null");
+  if (csr->num_segments <= 0 || csr->num_partitions <= 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "num_segments and num_partitions must be positive");
+  }
+  if (csr->row_pointers_per_segment < csr->num_partitions) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "row_pointers_per_segment must be >= num_partitions");
+  }
+  if (csr->coo_size < 0 || dim <= 0 || batch < 0 || table_rows < 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "negative size");
+  }
+  if (batch % csr->num_segments != 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "device_batch_size must be divisible by num_segments");
+  }
+  if (table_rows % csr->num_partitions != 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "table rows must be divisible by num_partitions");
+  }
+  if (table_rows >= (int64_t{1} << 32) - 1 || batch >= (int64_t{1} << 31) - 1) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "table or batch too large");
+  }
+  const int64_t per_seg = csr->coo_size / csr->num_segments;
+  geo->n = per_seg * csr->num_segments;
+  if (geo->n >= (int64_t{1} << 31) - 1) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "coo buffer too large");
+  }
+  geo->bps = batch / csr->num_segments;
+  geo->rows_per_partition = table_rows / csr->num_partitions;
+  if (geo->n > 0 && (csr->row_pointers == nullptr ||
+                     csr->embedding_ids == nullptr ||
+                     csr->sample_ids == nullptr || csr->gains == nullptr)) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null CSR buffer");
+  }
+  return 0;
+}
+
+Csr MakeCsr(const scemb_csr_t* csr) {
+  Csr c;
+  c.rp = csr->row_pointers;
+  c.eid = csr->embedding_ids;
+  c.sid = csr->sample_ids;
+  c.gains = csr->gains;
+  c.per_segment = csr->coo_size / csr->num_segments;
+  c.num_segments = csr->num_segments;
+  c.num_partitions = csr->num_partitions;
+  c.rp_per_segment = csr->row_pointers_per_segment;
+  return c;
+}
+
+// Lanes per row (>= 4) and vector width for a row of `dim` floats.
+void PickLayout(int64_t dim, bool vec4_ok, int* g, int* vec) {
+  *vec = vec4_ok && dim % 4 == 0 ? 4 : 1;
+  const int64_t lanes = CeilDiv(dim, *vec);
+  int gg = 4;
+  while (gg < lanes && gg < kWave) gg <<= 1;
+  *g = gg;
+}
+
+bool Aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+struct SortBuffers {
+  uint32_t* keys;
+  uint64_t* pay;
+  uint32_t* keys_alt;
+  uint64_t* pay_alt;
+};
+
+SortBuffers TakeSortBuffers(Arena& ws, int64_t n) {
+  SortBuffers b;
+  b.keys = ws.Take<uint32_t>(n);
+  b.pay = ws.Take<uint64_t>(n);
+  b.keys_alt = ws.Take<uint32_t>(n);
+  b.pay_alt = ws.Take<uint64_t>(n);
+  return b;
+}
+
+struct SegBuffers {
+  int64_t num_blocks;
+  float* partials;
+  uint32_t* flags;
+  uint32_t* keys;
+};
+
+SegBuffers TakeSegBuffers(Arena& ws, int64_t n, int64_t dim) {
+  SegBuffers b;
+  b.num_blocks = CeilDiv(n, kBlock);
+  b.partials = ws.Take<float>(2 * b.num_blocks * dim);
+  b.flags = ws.Take<uint32_t>(b.num_blocks);
+  b.keys = ws.Take<uint32_t>(b.num_blocks);
+  return b;
+}
+
+template <int SRC, int EPI, bool kMapped>
+int LaunchSegMapped(const StreamArgs& st, RowArgs r, const SegBuffers& sb,
+                    int g, int vec, bool one_hot, const char* reduce_span,
+                    const char* finish_span, hipStream_t stream) {
+  constexpr int kWide = EPI == kEpiFwd ? kFwdUnrollWide : kBwdUnrollWide;
+  constexpr int kNarrow = EPI == kEpiFwd ? kFwdUnrollNarrow : kBwdUnrollNarrow;
+  r.partials = sb.partials;
+  r.block_flags = sb.flags;
+  r.block_keys = sb.keys;
+  const dim3 grid(static_cast<uint32_t>(sb.num_blocks));
+#define SCEMB_SEG_CASE(GG, VV)                                                \
+  if (g == GG && vec == VV) {                                                \
+    int prof = ProfileBegin(reduce_span, stream);                            \
+    if (one_hot) {                                                           \
+      hipLaunchKernelGGL((SegReduce<GG, VV, SRC, EPI, kWide, kMapped>), grid, \
+                         dim3(kBlock), 0, stream, st, r);                     \
+    } else {                                                                 \
+      hipLaunchKernelGGL((SegReduce<GG, VV, SRC, EPI, kNarrow, kMapped>),     \
+                         grid, dim3(kBlock), 0, stream, st, r);               \
+    }                                                                        \
+    ProfileEnd(prof, stream);                                                 \
+    SCEMB_LAUNCH_CHECK();                                                     \
+    prof = ProfileBegin(finish_span, stream);                                 \
+    hipLaunchKernelGGL((SegFinish<GG, VV, EPI, kMapped>), grid, dim3(kBlock), \
+                       0, stream, sb.num_blocks, r);                          \
+    ProfileEnd(prof, stream);                                                 \
+    SCEMB_LAUNCH_CHECK();                                                     \
+    return 0;                                                                 \
+  }
+  SCEMB_SEG_CASE(4, 1) SCEMB_SEG_CASE(8, 1) SCEMB_SEG_CASE(16, 1)
+  SCEMB_SEG_CASE(32, 1) SCEMB_SEG_CASE(64, 1) SCEMB_SEG_CASE(4, 4)
+  SCEMB_SEG_CASE(8, 4) SCEMB_SEG_CASE(16, 4) SCEMB_SEG_CASE(32, 4)
+  SCEMB_SEG_CASE(64, 4)
+#undef SCEMB_SEG_CASE
+  return Fail(SCEMB_ERR_INVALID_ARGUMENT, "unsupported layout");
+}
+
+// Launches SegReduce + SegFinish for the layout picked for `dim`; `one_hot`
+// selects the wide unroll, `mapped` the kernels that address activations
+// through the row map in `r.act` (which may hold no block at all).
+template <int SRC, int EPI>
+int LaunchSeg(const StreamArgs& st, const RowArgs& r, const SegBuffers& sb,
+              int g, int vec, bool one_hot, bool mapped,
+              const char* reduce_span, const char* finish_span,
+              hipStream_t stream) {
+  if (mapped) {
+    return LaunchSegMapped<SRC, EPI, true>(st, r, sb, g, vec, one_hot,
+                                           reduce_span, finish_span, stream);
+  }
+  return LaunchSegMapped<SRC, EPI, false>(st, r, sb, g, vec, one_hot,
+                                          reduce_span, finish_span, stream);
+}
+
+// Backward + optimizer update for one call; with ws->measuring() it only
+// sizes the workspace. `c.map` (may be null): the activation gradients as
+// per-feature row blocks instead of the dense `c.act_grad`.
+template <int EPI>
+int GradImpl(const GradCall& c) {
+  const scemb_csr_t* csr = c.csr;
+  const int64_t batch = c.batch;
+  const int64_t table_rows = c.table_rows;
+  const int32_t dim = c.dim;
+  Arena& ws = *c.ws;
+  hipStream_t stream = c.stream;
+  Geometry geo;
+  int rc = CheckCsr(csr, batch, table_rows, dim, &geo);
+  if (rc != 0) return rc;
+  const int64_t n = geo.n;
+  const bool direct =
+      (csr->flags & SCEMB_CSR_SORTED_BY_ROW) != 0 && csr->num_segments == 1;
+  StreamArgs st{};
+  st.n = n;
+  if (direct) {
+    st.csr = MakeCsr(csr);
+    st.rows_per_partition = geo.rows_per_partition;
+    st.bps = geo.bps;
+  } else {
+    SortBuffers b = TakeSortBuffers(ws, n);
+    bool in_alt = false;
+    if (!ws.measuring()) {
+      if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+      if (n > 0 && batch > 0) {
+        hipLaunchKernelGGL(ExpandCsr<false>, dim3(CeilDiv(n, 256)), dim3(256),
+                           0, stream, MakeCsr(csr), geo.bps,
+                           geo.rows_per_partition,
+                           static_cast<uint32_t>(table_rows), b.keys, b.pay,
+                           c.status);
+        SCEMB_LAUNCH_CHECK();
+      }
+    }
+    if (n > 0 && batch > 0) {
+      rc = RadixSortPairs<uint32_t, uint64_t>(
+          b.keys, b.pay, b.keys_alt, b.pay_alt, n, 0,
+          BitWidth(static_cast<uint64_t>(table_rows)), ws, stream, &in_alt);
+      if (rc != 0) return rc;
+    }
+    st.keys = in_alt ? b.keys_alt : b.keys;
+    st.entries = in_alt ? b.pay_alt : b.pay;
+    st.sentinel = static_cast<uint32_t>(table_rows);
+    st.src_rows = batch;
+  }
+  const SegBuffers sb = TakeSegBuffers(ws, n, dim);
+  if (ws.measuring()) return 0;
+  if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+  if (n == 0 || batch == 0) return 0;
+  RowArgs r{};
+  r.src = c.act_grad;
+  r.dst = c.table;
+  r.slot0 = c.slot0;
+  r.slot1 = c.slot1;
+  r.dim = dim;
+  r.batch = batch;
+  r.opt = c.opt;
+  r.status = c.status;
+  if (c.map != nullptr) r.act = *c.map;
+  // Entries per activation row: how often each gradient row is gathered.
+  const int64_t entries =
+      csr->num_entries > 0 && csr->num_entries < n ? csr->num_entries : n;
+  const bool one_hot = entries <= kOneHotMaxEntriesPerRow * batch;
+  r.stream_src = one_hot;
+  int g, vec;
+  PickLayout(dim,
+             Aligned16(c.table) &&
+                 (c.map != nullptr ? c.map_vec4 : Aligned16(c.act_grad)) &&
+                 (NumSlots<EPI>() < 1 || Aligned16(c.slot0)) &&
+                 (NumSlots<EPI>() < 2 || Aligned16(c.slot1)),
+             &g, &vec);
+  const bool mapped = c.map != nullptr;
+  if (direct) {
+    return LaunchSeg<kSrcCsr, EPI>(st, r, sb, g, vec, one_hot, mapped,
+                                   "bwd_reduce", "bwd_finish", stream);
+  }
+  return LaunchSeg<kSrcSorted, EPI>(st, r, sb, g, vec, one_hot, mapped,
+                                    "bwd_reduce", "bwd_finish", stream);
+}
+
+}  // namespace
+}  // namespace scemb

@@ -32,6 +32,17 @@ STATUS_UNSORTED = 4
 
 CSR_SORTED_BY_ROW = 1
 
+# scemb_optimizer_t kinds and flags.
+OPTIMIZER_SGD = 0
+OPTIMIZER_ADAGRAD = 1
+OPTIMIZER_ADAM = 2
+OPTIMIZER_ADAGRAD_MOMENTUM = 3
+OPTIMIZER_FTRL = 4
+OPTIMIZER_LAPROP = 5
+OPTIMIZER_F2A = 6
+MAX_HYPERPARAMETERS = 8
+OPTIMIZER_FLAG_MULTIPLY_LINEAR_BY_LR = 1
+
 # Every function declared in include/scemb.h.
 EXPORTED_SYMBOLS = (
     "scemb_last_error",
@@ -46,6 +57,8 @@ EXPORTED_SYMBOLS = (
     "scemb_sparse_dense_matmul_grad_with_adagrad",
     "scemb_sparse_dense_matmul_grad_with_sgd_from_blocks",
     "scemb_sparse_dense_matmul_grad_with_adagrad_from_blocks",
+    "scemb_sparse_dense_matmul_grad_with_optimizer",
+    "scemb_sparse_dense_matmul_grad_with_optimizer_from_blocks",
     "scemb_preprocess_stats_size",
     "scemb_preprocess_stats_counters_offset",
     "scemb_preprocess_workspace_size",
@@ -96,6 +109,19 @@ class RowBlock(ctypes.Structure):
 
 
 MAX_ROW_BLOCKS = 32
+
+
+class Optimizer(ctypes.Structure):
+  _fields_ = [
+      ("kind", ctypes.c_int32),
+      ("flags", ctypes.c_uint32),
+      ("slots", ctypes.c_void_p * 2),
+      ("hyperparameter_ptrs", ctypes.c_void_p * MAX_HYPERPARAMETERS),
+      ("hyperparameters", ctypes.c_float * MAX_HYPERPARAMETERS),
+      ("clip_mask", ctypes.c_int32),
+      ("min_value", ctypes.c_float),
+      ("max_value", ctypes.c_float),
+  ]
 
 
 class Feature(ctypes.Structure):
@@ -197,6 +223,14 @@ def load_library() -> ctypes.CDLL:
     lib.scemb_sparse_dense_matmul_grad_with_adagrad.argtypes = [
         csr_p, vp, i64, vp, vp, i64, i32, vp, f32, i32, f32, f32, vp, sz, vp,
         vp]
+    opt_p = ctypes.POINTER(Optimizer)
+    lib.scemb_sparse_dense_matmul_grad_with_optimizer.restype = ctypes.c_int
+    lib.scemb_sparse_dense_matmul_grad_with_optimizer.argtypes = [
+        csr_p, vp, i64, vp, i64, i32, opt_p, vp, sz, vp, vp]
+    lib.scemb_sparse_dense_matmul_grad_with_optimizer_from_blocks.restype = (
+        ctypes.c_int)
+    lib.scemb_sparse_dense_matmul_grad_with_optimizer_from_blocks.argtypes = [
+        csr_p, blk_p, i32, i64, vp, i64, i32, opt_p, vp, sz, vp, vp]
     opts_p = ctypes.POINTER(PreprocessOptions)
     lib.scemb_preprocess_stats_size.restype = i64
     lib.scemb_preprocess_stats_size.argtypes = [opts_p]
@@ -495,5 +529,66 @@ def sparse_dense_matmul_grad(csr: Csr, activations_grad, table,
         ctypes.byref(csr), ptr(activations_grad), batch, ptr(table),
         ptr(accumulator), rows, dim, lr_ptr, lr_val, mask, lo, hi, ptr(ws),
         ws.numel(), ptr(device_status), stream_handle())
+  del keep
+  check(rc)
+
+
+def _hyper_args(values):
+  """Device scalars stay on the device (passed by pointer, read by the
+  kernels); anything else becomes a float32 value."""
+  t = torch()
+  keep, ptrs, vals = [], [], []
+  for v in values:
+    if isinstance(v, t.Tensor):
+      d = v.to(device=device(), dtype=t.float32).reshape(())
+      keep.append(d)
+      ptrs.append(ptr(d))
+      vals.append(0.0)
+    else:
+      ptrs.append(None)
+      vals.append(float(np.float32(np.asarray(v, np.float32))))
+  return keep, ptrs, vals
+
+
+def sparse_dense_matmul_grad_with_optimizer(
+    csr: Csr, activations_grad, table, kind: int, slots, hyperparameters,
+    batch: int, min_value=None, max_value=None, flags: int = 0,
+    device_status=None, grad_blocks=None) -> None:
+  """Backward + the optimizer `kind` (OPTIMIZER_*), updating `table` and the
+  slot tensors in place. `hyperparameters` in the order of the reference
+  primitive's operands (floats, numpy scalars or 0-d tensors).
+  `grad_blocks`: as for sparse_dense_matmul_grad."""
+  lib = load_library()
+  if len(hyperparameters) > MAX_HYPERPARAMETERS or len(slots) > 2:
+    check(SCEMB_ERR_INVALID_ARGUMENT)
+  rows = int(table.shape[0])
+  dim = 1 if table.dim() == 1 else int(table.shape[1])
+  need = lib.scemb_sparse_dense_matmul_grad_workspace_size(
+      ctypes.byref(csr), batch, rows, dim)
+  if need == 0:
+    check(SCEMB_ERR_INVALID_ARGUMENT)
+  ws = WORKSPACE.get(need)
+  keep, hp_ptrs, hp_vals = _hyper_args(hyperparameters)
+  opt = Optimizer()
+  opt.kind = kind
+  opt.flags = flags
+  for i, s in enumerate(slots):
+    opt.slots[i] = ptr(s)
+  for i, (p, v) in enumerate(zip(hp_ptrs, hp_vals)):
+    opt.hyperparameter_ptrs[i] = p
+    opt.hyperparameters[i] = v
+  opt.clip_mask, opt.min_value, opt.max_value = _clip_args(min_value,
+                                                           max_value)
+  if grad_blocks is not None:
+    arr, n = row_blocks(grad_blocks)
+    rc = lib.scemb_sparse_dense_matmul_grad_with_optimizer_from_blocks(
+        ctypes.byref(csr), arr, n, batch, ptr(table), rows, dim,
+        ctypes.byref(opt), ptr(ws), ws.numel(), ptr(device_status),
+        stream_handle())
+  else:
+    rc = lib.scemb_sparse_dense_matmul_grad_with_optimizer(
+        ctypes.byref(csr), ptr(activations_grad), batch, ptr(table), rows,
+        dim, ctypes.byref(opt), ptr(ws), ws.numel(), ptr(device_status),
+        stream_handle())
   del keep
   check(rc)

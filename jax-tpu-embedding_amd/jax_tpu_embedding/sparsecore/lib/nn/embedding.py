@@ -654,6 +654,9 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
     hyper = opt.get_hyperparameters(step)
     symbol = f"{opt.short_name()}-{spec.stack_name}{label}"
     kwargs = {}
+    if isinstance(opt, embedding_spec.FTRLOptimizerSpec):
+      kwargs["multiply_linear_by_learning_rate"] = (
+          opt.multiply_linear_by_learning_rate)
     if embedding_var_limits is not None:
       kwargs["min_value"], kwargs["max_value"] = embedding_var_limits[name]
     flat = [ev.table, *ev.slot] if isinstance(ev, EmbeddingVariables) else \
@@ -671,7 +674,10 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
                                  None) or {}).get(name),
         **kwargs)
     res = res if isinstance(res, tuple) else (res,)
-    out[name] = EmbeddingVariables(res[0], tuple(res[1:]))
+    slot_type = (type(ev.slot) if isinstance(ev, EmbeddingVariables) and
+                 hasattr(type(ev.slot), "_fields") else None)
+    slots = slot_type(*res[1:]) if slot_type else tuple(res[1:])
+    out[name] = EmbeddingVariables(res[0], slots)
   return out
 
 
@@ -714,6 +720,9 @@ def init_embedding_variables(rng, table_specs, global_sharding=None,
           slots[k].append(v)
     table = t.cat(tables, dim=0)
     slot_vals = tuple(t.cat(s, dim=0) for s in (slots or []))
+    slot_type = type(specs[0].optimizer.slot_variables_initializers())
+    if hasattr(slot_type, "_fields"):  # the optimizer's *SlotVariables
+      slot_vals = slot_type(*slot_vals)
     out[name] = EmbeddingVariables(table, slot_vals)
   return out
 

@@ -4,9 +4,11 @@ The dataclasses keep the reference's field names, defaults and stacking
 rules (``FeatureIdTransformation`` :918-938, ``TableSettingInStack``
 :940-977, ``TableSpec`` :979-1118, ``FeatureSpec`` :1120-1166,
 ``StackedTableSpec`` :1169-1205, ``QuantizationConfig`` :1207-1223) so feature
-specs written for the reference work unchanged. Optimizers in scope are SGD
-(:377-412) and Adagrad (:415-460); learning rates may be numbers, 0-d torch
-tensors or callables of the step.
+specs written for the reference work unchanged. The optimizers are those of
+the reference: SGD (:377-412), Adagrad (:415-460), Adam (:463-557),
+AdagradMomentum (:560-649), FTRL (:652-741), LaProp (:744-830) and F2A
+(:833-916), with the same hyperparameters, slot variables and defaults.
+Learning rates may be numbers, 0-d torch tensors or callables of the step.
 
 Initializers are callables ``init(generator, shape)`` returning a float32
 array; ``init_embedding_variables`` calls them with a ``torch.Generator`` on
@@ -20,7 +22,14 @@ import dataclasses
 import inspect
 from typing import Any, Callable, NamedTuple, Sequence
 
+import numpy as np
+
 from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_adagrad
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_adagrad_momentum
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_adam
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_f2a
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_ftrl
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_laprop
 from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_sgd
 
 DEFAULT_ACTIVATION_MEM_BYTES_LIMIT: int = 2048 * 1024
@@ -81,6 +90,31 @@ class SGDSlotVariables(NamedTuple):
 
 class AdagradSlotVariables(NamedTuple):
   accumulator: Any
+
+
+class F2ASlotVariables(NamedTuple):
+  accumulator: Any
+  local_step: Any
+
+
+class AdamSlotVariables(NamedTuple):
+  momentum: Any
+  velocity: Any
+
+
+class AdagradMomentumSlotVariables(NamedTuple):
+  accumulator: Any
+  momentum: Any
+
+
+class FTRLSlotVariables(NamedTuple):
+  accumulator: Any
+  linear: Any
+
+
+class LaPropSlotVariables(NamedTuple):
+  mu: Any
+  nu: Any
 
 
 class OptimizerSpec:
@@ -187,6 +221,259 @@ class AdagradOptimizerSpec(OptimizerSpec):
   def get_optimizer_primitive(self):
     return (sparse_dense_matmul_grad_with_adagrad
             .tpu_sparse_dense_matmul_grad_with_adagrad_primitive)
+
+
+def _f32(x):
+  return np.float32(x)
+
+
+def _step_value(step) -> float:
+  """The step as a number (0-d tensors are read back)."""
+  if step is None:
+    return 0.0
+  if hasattr(step, "item"):
+    return float(step.item())
+  return float(step)
+
+
+class AdamOptimizerSpec(OptimizerSpec):
+  """Adam (Kingma et al., 2014) with the bias correction folded into the
+  hyperparameters (embedding_spec.py:463-557)."""
+
+  _float_params = ("beta_1", "beta_2", "epsilon")
+
+  def __init__(self, learning_rate: LearningRate = 0.001,
+               beta_1: float = 0.9, beta_2: float = 0.999,
+               epsilon: float = 1e-8):
+    super().__init__(learning_rate=learning_rate)
+    self.beta_1 = beta_1
+    self.beta_2 = beta_2
+    self.epsilon = epsilon
+
+  def slot_variables_initializers(self) -> tuple:
+    return AdamSlotVariables(momentum=constant(0.0), velocity=constant(0.0))
+
+  def get_hyperparameters(self, step=None) -> tuple:
+    """(alpha_t, beta_1, beta_2, epsilon_hat) with
+    alpha_t = lr * sqrt(1 - beta_2^t) / (1 - beta_1^t) and
+    epsilon_hat = epsilon * sqrt(1 - beta_2^t), t = step + 1, in float32
+    (embedding_spec.py:506-539)."""
+    t = _step_value(step) + 1.0
+    beta_1 = _f32(self.beta_1)
+    beta_2 = _f32(self.beta_2)
+    beta_1_t = np.power(beta_1, _f32(t))
+    beta_2_t = np.power(beta_2, _f32(t))
+    c_2 = np.sqrt(_f32(1.0) - beta_2_t)
+    lr = self.get_learning_rate(step)
+    if hasattr(lr, "data_ptr"):  # a 0-d torch tensor stays a tensor
+      alpha_t = lr * float(c_2) / float(_f32(1.0) - beta_1_t)
+    else:
+      alpha_t = _f32(lr) * c_2 / (_f32(1.0) - beta_1_t)
+    epsilon_hat = _f32(self.epsilon) * c_2
+    return (alpha_t, beta_1, beta_2, epsilon_hat)
+
+  def __hash__(self) -> int:
+    return hash((_hashable(self.learning_rate), self.beta_1, self.beta_2,
+                 self.epsilon))
+
+  def short_name(self) -> str:
+    return "adam"
+
+  def get_optimizer_primitive(self):
+    return (sparse_dense_matmul_grad_with_adam
+            .tpu_sparse_dense_matmul_grad_with_adam_primitive)
+
+
+class AdagradMomentumOptimizerSpec(OptimizerSpec):
+  """Adagrad with momentum (embedding_spec.py:560-649)."""
+
+  _float_params = ("momentum", "beta2", "epsilon", "exponent",
+                   "initial_accumulator_value", "initial_momentum_value")
+  _bool_params = ("use_nesterov",)
+
+  def __init__(self, learning_rate: LearningRate = 0.001,
+               momentum: float = 0.9, beta2: float = 1.0,
+               epsilon: float = 1e-10, exponent: float = 2.0,
+               use_nesterov: bool = False,
+               initial_accumulator_value: float = 0.1,
+               initial_momentum_value: float = 0.0):
+    super().__init__(learning_rate=learning_rate)
+    self.momentum = momentum
+    self.beta2 = beta2
+    self.epsilon = epsilon
+    self.exponent = exponent
+    self.use_nesterov = use_nesterov
+    self.initial_accumulator_value = initial_accumulator_value
+    self.initial_momentum_value = initial_momentum_value
+
+  def slot_variables_initializers(self) -> tuple:
+    return AdagradMomentumSlotVariables(
+        accumulator=constant(self.initial_accumulator_value),
+        momentum=constant(self.initial_momentum_value))
+
+  def get_hyperparameters(self, step=None) -> tuple:
+    return (self.get_learning_rate(step), _f32(self.momentum),
+            _f32(self.beta2), _f32(self.epsilon), _f32(self.exponent),
+            np.bool_(self.use_nesterov))
+
+  def __hash__(self) -> int:
+    return hash((_hashable(self.learning_rate), self.momentum, self.beta2,
+                 self.epsilon, self.exponent, self.use_nesterov,
+                 self.initial_accumulator_value,
+                 self.initial_momentum_value))
+
+  def short_name(self) -> str:
+    return "adagrad_momentum"
+
+  def get_optimizer_primitive(self):
+    return (sparse_dense_matmul_grad_with_adagrad_momentum
+            .tpu_sparse_dense_matmul_grad_with_adagrad_momentum_primitive)
+
+
+class FTRLOptimizerSpec(OptimizerSpec):
+  """Follow The Regularized Leader (embedding_spec.py:652-741)."""
+
+  _float_params = ("learning_rate_power", "l1_regularization_strength",
+                   "l2_regularization_strength", "beta",
+                   "initial_accumulator_value", "initial_linear_value")
+  _bool_params = ("multiply_linear_by_learning_rate",)
+
+  def __init__(self, learning_rate: LearningRate = 0.01,
+               learning_rate_power: float = -0.5,
+               l1_regularization_strength: float = 0.0,
+               l2_regularization_strength: float = 0.0, beta: float = 0.0,
+               initial_accumulator_value: float = 0.1,
+               initial_linear_value: float = 0.0,
+               multiply_linear_by_learning_rate: bool = False):
+    super().__init__(learning_rate=learning_rate)
+    self.learning_rate_power = learning_rate_power
+    self.l1_regularization_strength = l1_regularization_strength
+    self.l2_regularization_strength = l2_regularization_strength
+    self.beta = beta
+    self.initial_accumulator_value = initial_accumulator_value
+    self.initial_linear_value = initial_linear_value
+    self.multiply_linear_by_learning_rate = multiply_linear_by_learning_rate
+
+  def slot_variables_initializers(self) -> tuple:
+    return FTRLSlotVariables(
+        accumulator=constant(self.initial_accumulator_value),
+        linear=constant(self.initial_linear_value))
+
+  def get_hyperparameters(self, step=None) -> tuple:
+    return (self.get_learning_rate(step), _f32(self.learning_rate_power),
+            _f32(self.l1_regularization_strength),
+            _f32(self.l2_regularization_strength), _f32(self.beta))
+
+  def __hash__(self) -> int:
+    return hash((_hashable(self.learning_rate), self.learning_rate_power,
+                 self.l1_regularization_strength,
+                 self.l2_regularization_strength, self.beta,
+                 self.initial_accumulator_value, self.initial_linear_value,
+                 self.multiply_linear_by_learning_rate))
+
+  def short_name(self) -> str:
+    return "ftrl"
+
+  def get_optimizer_primitive(self):
+    return (sparse_dense_matmul_grad_with_ftrl
+            .tpu_sparse_dense_matmul_grad_with_ftrl_primitive)
+
+
+class LaPropOptimizerSpec(OptimizerSpec):
+  """LaProp (arXiv:2002.04839; embedding_spec.py:744-830)."""
+
+  _float_params = ("b1", "b2", "eps", "initial_slot_value")
+
+  def __init__(self, learning_rate: LearningRate = 0.001, b1: float = 0.9,
+               b2: float = 0.95, eps: float = 1e-30,
+               rms_clip_threshold: float | None = None,
+               initial_slot_value: float = 0.0):
+    super().__init__(learning_rate=learning_rate)
+    self.b1 = b1
+    self.b2 = b2
+    self.eps = eps
+    if rms_clip_threshold is not None:
+      raise ValueError(
+          "rms_clip_threshold is not yet supported in LaProp optimizer.")
+    self.initial_slot_value = initial_slot_value
+
+  def slot_variables_initializers(self) -> tuple:
+    return LaPropSlotVariables(mu=constant(self.initial_slot_value),
+                               nu=constant(self.initial_slot_value))
+
+  def get_decay_rate(self, step=None):
+    """b2 without a step, else b2 (1 - b2^step) / (1 - b2^(step + 1)) in
+    float32 (embedding_spec.py:788-800)."""
+    b2 = _f32(self.b2)
+    if step is None:
+      return b2
+    st = _f32(_step_value(step))
+    return _f32(b2 * (_f32(1.0) - np.power(b2, st)) /
+                (_f32(1.0) - np.power(b2, st + _f32(1.0))))
+
+  def get_hyperparameters(self, step=None) -> tuple:
+    return (self.get_learning_rate(step), _f32(self.b1),
+            self.get_decay_rate(step), _f32(self.eps))
+
+  def __hash__(self) -> int:
+    return hash((_hashable(self.learning_rate), self.b1, self.b2, self.eps,
+                 self.initial_slot_value))
+
+  def short_name(self) -> str:
+    return "laprop"
+
+  def get_optimizer_primitive(self):
+    return (sparse_dense_matmul_grad_with_laprop
+            .tpu_sparse_dense_matmul_grad_with_laprop_primitive)
+
+
+class F2AOptimizerSpec(OptimizerSpec):
+  """Frequency-aware Adagrad (embedding_spec.py:833-916)."""
+
+  _float_params = ("rho", "initial_accumulator_value",
+                   "initial_local_step_value", "l1_regularization_strength",
+                   "l2_regularization_strength", "max_lr_multiplier")
+
+  def __init__(self, learning_rate: LearningRate = 0.01, rho: float = 0.5,
+               initial_accumulator_value: float = 0.1,
+               initial_local_step_value: float = 0.0,
+               l1_regularization_strength: float = 0.0,
+               l2_regularization_strength: float = 0.0,
+               max_lr_multiplier: float = 1e6):
+    super().__init__(learning_rate=learning_rate)
+    self.rho = rho
+    self.initial_accumulator_value = initial_accumulator_value
+    self.initial_local_step_value = initial_local_step_value
+    self.l1_regularization_strength = l1_regularization_strength
+    self.l2_regularization_strength = l2_regularization_strength
+    self.max_lr_multiplier = max_lr_multiplier
+
+  def slot_variables_initializers(self) -> tuple:
+    return F2ASlotVariables(
+        accumulator=constant(self.initial_accumulator_value),
+        local_step=constant(self.initial_local_step_value))
+
+  def get_hyperparameters(self, step=None) -> tuple:
+    if step is None:
+      step = 0
+    return (self.get_learning_rate(step), _f32(self.rho),
+            _f32(self.l1_regularization_strength),
+            _f32(self.l2_regularization_strength),
+            _f32(self.max_lr_multiplier), _f32(_step_value(step)))
+
+  def __hash__(self) -> int:
+    return hash((_hashable(self.learning_rate), self.rho,
+                 self.initial_accumulator_value,
+                 self.initial_local_step_value,
+                 self.l1_regularization_strength,
+                 self.l2_regularization_strength, self.max_lr_multiplier))
+
+  def short_name(self) -> str:
+    return "f2a"
+
+  def get_optimizer_primitive(self):
+    return (sparse_dense_matmul_grad_with_f2a
+            .tpu_sparse_dense_matmul_grad_with_f2a_primitive)
 
 
 def _hashable(v):

@@ -22,6 +22,10 @@
 //                       primitives/utils.py:24-59 (clip), and the numpy test
 //                       oracles in primitives/tests/
 //                       sparse_dense_matmul_grad_with_adagrad_test.py:356-400.
+//   optimizers        the row-wise update bodies of primitives/
+//                       sparse_dense_matmul_grad_with_adam.py:283-338,
+//                       _adagrad_momentum.py:256-311, _ftrl.py:260-335,
+//                       _laprop.py:282-340, _f2a.py:244-290.
 //
 // Numeric rules follow the C++ (not the Python reference): float gains,
 // float sums in sorted order, std::pow(float,int) promoting to double in the
@@ -592,17 +596,147 @@ int ref_sparse_dense_matmul(const int32_t* rp, const int32_t* eid,
   return 0;
 }
 
-// optimizer: 0 = SGD, 1 = Adagrad. clip_mask bit0: min, bit1: max.
-int ref_sparse_dense_matmul_grad(const int32_t* rp, const int32_t* eid,
-                                 const int32_t* sid, const float* gains,
-                                 int64_t coo_size, int num_segments,
-                                 int num_partitions, int rp_per_segment,
-                                 const float* act_grad, int64_t batch,
-                                 float* table, float* accumulator,
-                                 int64_t table_rows, int dim, int optimizer,
-                                 float learning_rate, int clip_mask,
-                                 float min_value, float max_value,
-                                 int threads) {
+// Optimizer kinds (as SCEMB_OPTIMIZER_* of include/scemb.h).
+enum {
+  kSgd = 0,
+  kAdagrad = 1,
+  kAdam = 2,
+  kAdagradMomentum = 3,
+  kFtrl = 4,
+  kLaprop = 5,
+  kF2a = 6,
+};
+
+}  // extern "C"
+
+namespace {
+
+// One table value t with its summed gradient g and slot values s0, s1, for
+// the hyperparameters h in the order of the reference primitive's operands;
+// then clipping (primitives/utils.py:24-59). Each branch restates the
+// reference's row-wise update body, operation by operation.
+float ApplyUpdate(int kind, const float* h, int flags, float t, float* s0,
+                  float* s1, float g, int clip_mask, float min_value,
+                  float max_value) {
+  float v;
+  switch (kind) {
+    case kSgd:  // optimizers_computation.py:22-69
+      v = t - g * h[0];
+      break;
+    case kAdagrad: {  // sparse_dense_matmul_grad_with_adagrad.py:205-233
+      const float acc = *s0 + g * g;
+      *s0 = acc;
+      v = t - (h[0] * g) / std::sqrt(acc);
+      break;
+    }
+    case kAdam: {  // sparse_dense_matmul_grad_with_adam.py:283-338
+      // h: alpha_t, beta_1, beta_2, epsilon_hat; slots momentum, velocity.
+      const float grad_square = g * g;
+      const float m = *s0 + (1.0f - h[1]) * (g - *s0);
+      const float vel = *s1 + (1.0f - h[2]) * (grad_square - *s1);
+      const float update = (h[0] * m) / (std::sqrt(vel) + h[3]);
+      *s0 = m;
+      *s1 = vel;
+      v = t - update;
+      break;
+    }
+    case kAdagradMomentum: {
+      // sparse_dense_matmul_grad_with_adagrad_momentum.py:256-311
+      // h: lr, momentum, beta2, epsilon, exponent, use_nesterov; slots
+      // accumulator, momentum.
+      const float grad_sq = g * g;
+      const float accum_plus = *s0 + grad_sq;
+      const float scaled_accum = h[2] * *s0 + (1.0f - h[2]) * grad_sq;
+      const float a = h[2] == 1.0f ? accum_plus : scaled_accum;
+      const float neg_inv_exp = -1.0f / h[4];
+      const float p = std::pow(a + h[3], neg_inv_exp);
+      const float scaled_grad = p * g;
+      const float m = h[1] * *s1 + scaled_grad;
+      const float nesterov_update = h[1] * m + scaled_grad;
+      const float update = h[5] != 0.0f ? nesterov_update : m;
+      *s0 = a;
+      *s1 = m;
+      v = t - h[0] * update;
+      break;
+    }
+    case kFtrl: {  // sparse_dense_matmul_grad_with_ftrl.py:260-335
+      // h: lr, lr_power, l1, l2, beta; slots accumulator, linear.
+      const bool by_lr = (flags & 1) != 0;
+      const float a = *s0 + g * g;
+      const float neg_lr_pow = -h[1];
+      const float p_old = std::pow(*s0, neg_lr_pow);
+      const float p_new = std::pow(a, neg_lr_pow);
+      const float delta_p = p_new - p_old;
+      const float linear =
+          by_lr ? (*s1 + h[0] * g) - delta_p * t
+                : (*s1 + g) - (delta_p / h[0]) * t;
+      const float scale = by_lr ? h[0] : 1.0f;
+      const float l1_scaled = h[2] * scale;
+      // stablehlo.clamp(min, x, max) = min(max(x, min), max)
+      const float clamped = std::min(std::max(linear, -l1_scaled), l1_scaled);
+      const float numerator = h[2] == 0.0f ? -linear : clamped - linear;
+      const float denominator =
+          by_lr ? (p_new + 2.0f * (h[0] * h[3])) + h[4]
+                : (p_new + h[4]) / h[0] + 2.0f * h[3];
+      *s0 = a;
+      *s1 = linear;
+      v = numerator / denominator;
+      break;
+    }
+    case kLaprop: {  // sparse_dense_matmul_grad_with_laprop.py:282-340
+      // h: lr, b1, decay_rate, eps; slots mu, nu.
+      const float grad_square = g * g + h[3];
+      const float nu = *s1 * h[2] + (1.0f - h[2]) * grad_square;
+      const float update = g / std::sqrt(nu);
+      const float term_2 = std::pow(1.0f - std::pow(h[1], 2.0f), 0.5f);
+      const float u = h[1] * *s0 + term_2 * update;
+      *s0 = u;
+      *s1 = nu;
+      v = t - h[0] * u;
+      break;
+    }
+    default: {  // kF2a: sparse_dense_matmul_grad_with_f2a.py:244-290
+      // h: lr, rho, l1, l2, max_lr_multiplier, global_step; slots
+      // accumulator, local_step.
+      const float local_step = *s1 + 1.0f;
+      const float safe_global_step = std::max(h[5], 1.0f);
+      const float frequency_ratio = safe_global_step / local_step;
+      const float fa =
+          std::min(std::pow(frequency_ratio, h[1]), h[4]);
+      const float a = *s0 + g * g;
+      const float denominator = std::sqrt(a);
+      // stablehlo.sign: -1, +1, or the value itself for +-0 and NaN.
+      const float sign = t > 0.0f ? 1.0f : (t < 0.0f ? -1.0f : t);
+      const float l1_decay = h[2] * sign;
+      const float l2_shrinkage = h[3] * t;
+      const float grad_scaled = (g * fa) / denominator;
+      const float update_sum = grad_scaled + (l1_decay + l2_shrinkage);
+      *s0 = a;
+      *s1 = local_step;
+      v = t - h[0] * update_sum;
+      break;
+    }
+  }
+  if (clip_mask & 1) v = std::max(min_value, v);
+  if (clip_mask & 2) v = std::min(max_value, v);
+  return v;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Backward + optimizer `kind` (kSgd ...). slot0 / slot1: the optimizer's
+// slot variables (null when it has fewer), hp: its hyperparameters. flags
+// bit 0: FTRL's multiply_linear_by_learning_rate. clip_mask bit 0: min,
+// bit 1: max.
+int ref_sparse_dense_matmul_grad_optimizer(
+    const int32_t* rp, const int32_t* eid, const int32_t* sid,
+    const float* gains, int64_t coo_size, int num_segments,
+    int num_partitions, int rp_per_segment, const float* act_grad,
+    int64_t batch, float* table, float* slot0, float* slot1,
+    int64_t table_rows, int dim, int kind, const float* hp, int flags,
+    int clip_mask, float min_value, float max_value, int threads) {
   const std::vector<CsrEntry> e =
       CollectEntries(rp, eid, sid, gains, coo_size, num_segments,
                      num_partitions, rp_per_segment, table_rows, batch);
@@ -627,26 +761,40 @@ int ref_sparse_dense_matmul_grad(const int32_t* rp, const int32_t* eid,
       float* gs = grad.data() + slot_of[i] * dim;
       for (int d = lo; d < hi; ++d) gs[d] += e[i].gain * gr[d];
     }
+    float unused0 = 0.0f, unused1 = 0.0f;
     for (size_t u = 0; u < touched.size(); ++u) {
-      float* t = table + touched[u] * dim;
-      float* a = accumulator ? accumulator + touched[u] * dim : nullptr;
+      const int64_t off = touched[u] * dim;
       const float* g = grad.data() + u * dim;
       for (int d = lo; d < hi; ++d) {
-        float v;
-        if (optimizer == 0) {
-          v = t[d] - g[d] * learning_rate;
-        } else {
-          const float acc = a[d] + g[d] * g[d];
-          a[d] = acc;
-          v = t[d] - (learning_rate * g[d]) / std::sqrt(acc);
-        }
-        if (clip_mask & 1) v = std::max(min_value, v);
-        if (clip_mask & 2) v = std::min(max_value, v);
-        t[d] = v;
+        float* a = slot0 ? slot0 + off + d : &unused0;
+        float* b = slot1 ? slot1 + off + d : &unused1;
+        table[off + d] = ApplyUpdate(kind, hp, flags, table[off + d], a, b,
+                                     g[d], clip_mask, min_value, max_value);
       }
     }
   });
   return 0;
+}
+
+// optimizer: 0 = SGD, 1 = Adagrad (accumulator). clip_mask bit0: min,
+// bit1: max.
+int ref_sparse_dense_matmul_grad(const int32_t* rp, const int32_t* eid,
+                                 const int32_t* sid, const float* gains,
+                                 int64_t coo_size, int num_segments,
+                                 int num_partitions, int rp_per_segment,
+                                 const float* act_grad, int64_t batch,
+                                 float* table, float* accumulator,
+                                 int64_t table_rows, int dim, int optimizer,
+                                 float learning_rate, int clip_mask,
+                                 float min_value, float max_value,
+                                 int threads) {
+  const float hp[1] = {learning_rate};
+  return ref_sparse_dense_matmul_grad_optimizer(
+      rp, eid, sid, gains, coo_size, num_segments, num_partitions,
+      rp_per_segment, act_grad, batch, table,
+      optimizer == kSgd ? nullptr : accumulator, nullptr, table_rows, dim,
+      optimizer == kSgd ? kSgd : kAdagrad, hp, 0, clip_mask, min_value,
+      max_value, threads);
 }
 
 }  // extern "C"

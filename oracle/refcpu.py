@@ -88,9 +88,13 @@ def lib() -> ctypes.CDLL:
   l.ref_sparse_dense_matmul_grad.argtypes = [vp, vp, vp, vp, i64, i32, i32,
                                              i32, vp, i64, vp, vp, i64, i32,
                                              i32, f32, i32, f32, f32, i32]
+  l.ref_sparse_dense_matmul_grad_optimizer.argtypes = [
+      vp, vp, vp, vp, i64, i32, i32, i32, vp, i64, vp, vp, vp, i64, i32, i32,
+      vp, i32, i32, f32, f32, i32]
   for fn in ("ref_extract_slice", "ref_extract_device", "ref_sort_and_group",
              "ref_fill_device", "ref_preprocess_stack",
-             "ref_sparse_dense_matmul", "ref_sparse_dense_matmul_grad"):
+             "ref_sparse_dense_matmul", "ref_sparse_dense_matmul_grad",
+             "ref_sparse_dense_matmul_grad_optimizer"):
     getattr(l, fn).restype = i32
   _lib = l
   return l
@@ -482,3 +486,49 @@ def sparse_dense_matmul_grad(rp, eid, sid, gains, act_grad, table,
       float(min_value if min_value is not None else 0.0),
       float(max_value if max_value is not None else 0.0), _threads(threads))
   return (table, acc) if acc is not None else table
+
+
+# Optimizer kinds of ref_sparse_dense_matmul_grad_optimizer.
+OPTIMIZERS = {"sgd": 0, "adagrad": 1, "adam": 2, "adagrad_momentum": 3,
+              "ftrl": 4, "laprop": 5, "f2a": 6}
+OPTIMIZER_SLOTS = {"sgd": 0, "adagrad": 1, "adam": 2, "adagrad_momentum": 2,
+                   "ftrl": 2, "laprop": 2, "f2a": 2}
+
+
+def sparse_dense_matmul_grad_optimizer(rp, eid, sid, gains, act_grad, table,
+                                       slots, *, optimizer: str,
+                                       hyperparameters, num_sc_per_device,
+                                       num_scs, multiply_linear_by_lr=False,
+                                       min_value=None, max_value=None,
+                                       threads=None):
+  """Backward + any optimizer (`optimizer` a key of OPTIMIZERS), on copies.
+
+  `slots` in the order of the optimizer's slot variables, `hyperparameters`
+  in the order of the reference primitive's operands. Returns
+  (table, *slots).
+  """
+  n_slots = OPTIMIZER_SLOTS[optimizer]
+  assert len(slots) == n_slots, (optimizer, len(slots))
+  table = np.array(table, np.float32, copy=True, order="C")
+  slots = [np.array(x, np.float32, copy=True, order="C") for x in slots]
+  hp = np.zeros(8, np.float32)
+  hp[:len(hyperparameters)] = [np.float32(np.asarray(h, np.float32))
+                               for h in hyperparameters]
+  dim = 1 if table.ndim == 1 else table.shape[1]
+  act_grad = np.ascontiguousarray(act_grad, np.float32)
+  batch = act_grad.shape[0]
+  rp, eid, sid, gains = (np.ascontiguousarray(rp, np.int32).reshape(-1),
+                         np.ascontiguousarray(eid, np.int32).reshape(-1),
+                         np.ascontiguousarray(sid, np.int32).reshape(-1),
+                         np.ascontiguousarray(gains, np.float32).reshape(-1))
+  clip = (1 if min_value is not None else 0) | (2 if max_value is not None
+                                                 else 0)
+  lib().ref_sparse_dense_matmul_grad_optimizer(
+      _p(rp), _p(eid), _p(sid), _p(gains), len(eid), num_sc_per_device,
+      num_scs, len(rp) // num_sc_per_device, _p(act_grad), batch, _p(table),
+      _p(slots[0]) if n_slots > 0 else None,
+      _p(slots[1]) if n_slots > 1 else None, table.shape[0], dim,
+      OPTIMIZERS[optimizer], _p(hp), 1 if multiply_linear_by_lr else 0, clip,
+      float(min_value if min_value is not None else 0.0),
+      float(max_value if max_value is not None else 0.0), _threads(threads))
+  return (table, *slots)
