@@ -430,7 +430,94 @@ def collect_stats(pending) -> SparseDenseMatmulInputStats:
   return stats
 
 
-def preprocess_sparse_dense_matmul_sparse_coo_input(*args, **kwargs):
-  del args, kwargs
-  raise NotImplementedError(
-      "The sparse-COO input entry point is not part of this path yet.")
+class RaggedIds:
+  """Ids of one feature as flat values plus row splits (row r holds
+  values[row_splits[r]:row_splits[r + 1]]); accepted wherever a feature is.
+  `values` may be a numpy array or a CUDA tensor, `row_splits` is host
+  int64 [batch + 1]."""
+
+  def __init__(self, values, row_splits):
+    self.values = values
+    self.row_splits = row_splits
+
+
+def sparse_coo_to_ragged(indices, values, dense_shape) -> RaggedIds:
+  """A 2-D sparse tensor in COO form (tf.sparse.SparseTensor layout: indices
+  [N, 2] row-major, values [N], dense_shape [batch, width]) as RaggedIds.
+
+  Row splits as ConstructRowPointers builds them
+  (lib/core/sparse_coo_input_batch.cc:30-66): row_splits[r] is the first
+  entry whose row index is >= r, for r = 0..batch. The column index only
+  orders the ids of a row. The reference DCHECKs row-major order; here a
+  violation (decreasing row, non-increasing column within a row) or a row
+  outside [0, batch) raises ValueError.
+  """
+  batch = int(np.asarray(
+      dense_shape.cpu() if hasattr(dense_shape, "cpu") else dense_shape,
+      np.int64).reshape(-1)[0])
+  if hasattr(indices, "cpu"):  # a tensor: the checks read back once
+    idx = indices.reshape(-1, 2)
+    rows, cols = idx[:, 0], idx[:, 1]
+    t = _native.torch()
+    n = int(rows.shape[0])
+    if n:
+      same = rows[1:] == rows[:-1]
+      bad = ((rows[1:] < rows[:-1]) | (same & (cols[1:] <= cols[:-1]))).any()
+      flags = t.stack([bad, rows.min() < 0, rows.max() >= batch]).cpu()
+      if bool(flags[0]):
+        raise ValueError("sparse indices must be sorted in row-major order")
+      if bool(flags[1]) or bool(flags[2]):
+        raise ValueError(f"sparse row index outside [0, {batch})")
+    splits = t.searchsorted(
+        rows.contiguous(),
+        t.arange(batch + 1, device=rows.device, dtype=rows.dtype))
+    return RaggedIds(values.reshape(-1), splits.cpu().numpy().astype(np.int64))
+  idx = np.asarray(indices, np.int64).reshape(-1, 2)
+  rows, cols = idx[:, 0], idx[:, 1]
+  if rows.size:
+    d_row = np.diff(rows)
+    if (d_row < 0).any() or ((d_row == 0) & (np.diff(cols) <= 0)).any():
+      raise ValueError("sparse indices must be sorted in row-major order")
+    if rows[0] < 0 or rows[-1] >= batch:
+      raise ValueError(f"sparse row index outside [0, {batch})")
+  splits = np.searchsorted(rows, np.arange(batch + 1), side="left")
+  vals = values.reshape(-1) if hasattr(values, "data_ptr") else np.asarray(
+      values, np.int32).reshape(-1)
+  if vals.shape[0] != rows.shape[0]:
+    raise ValueError("indices and values must have the same length")
+  return RaggedIds(vals, splits.astype(np.int64))
+
+
+def preprocess_sparse_dense_matmul_sparse_coo_input(
+    indices,
+    values,
+    dense_shapes,
+    feature_specs,
+    local_device_count: int,
+    global_device_count: int,
+    *,
+    num_sc_per_device: int,
+    sharding_strategy=ShardingStrategy.MOD,
+    has_leading_dimension: bool = False,
+    allow_id_dropping: bool = False,
+    batch_number: int = 0,
+    enable_minibatching: bool = False,
+    all_reduce_interface=None,
+):
+  """PySparseCooPreprocessSparseDenseMatmulInput
+  (pybind_input_preprocessing.cc:250-276): one sparse COO tensor per feature,
+  unity weights; same outputs as preprocess_sparse_dense_matmul_input."""
+  indices, values, dense_shapes = list(indices), list(values), list(
+      dense_shapes)
+  if not len(indices) == len(values) == len(dense_shapes):
+    raise ValueError("indices, values and dense_shapes must have equal length")
+  features = [sparse_coo_to_ragged(i, v, d)
+              for i, v, d in zip(indices, values, dense_shapes)]
+  return preprocess_sparse_dense_matmul_input(
+      features, None, feature_specs, local_device_count, global_device_count,
+      num_sc_per_device=num_sc_per_device,
+      sharding_strategy=sharding_strategy,
+      has_leading_dimension=has_leading_dimension,
+      allow_id_dropping=allow_id_dropping, batch_number=batch_number,
+      enable_minibatching=enable_minibatching,
+      all_reduce_interface=all_reduce_interface)

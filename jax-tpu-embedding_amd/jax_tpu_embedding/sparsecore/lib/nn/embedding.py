@@ -57,10 +57,16 @@ class SparseDenseMatmulInput(NamedTuple):
 class SparseDenseMatmulInputStats:
   """Preprocessing stats per stacked table (embedding.py:97-188)."""
 
-  max_ids_per_partition: dict = dataclasses.field(default_factory=dict)
-  max_unique_ids_per_partition: dict = dataclasses.field(default_factory=dict)
-  required_buffer_size_per_sc: dict = dataclasses.field(default_factory=dict)
-  id_drop_counters: dict = dataclasses.field(default_factory=dict)
+  # The suffixes name each field's entries in FDO stats files
+  # (lib/fdo/file_fdo_client.py: "<table><suffix>").
+  max_ids_per_partition: dict = dataclasses.field(
+      default_factory=dict, metadata={"suffix": "_max_ids"})
+  max_unique_ids_per_partition: dict = dataclasses.field(
+      default_factory=dict, metadata={"suffix": "_max_unique_ids"})
+  required_buffer_size_per_sc: dict = dataclasses.field(
+      default_factory=dict, metadata={"suffix": "_required_buffer_size"})
+  id_drop_counters: dict = dataclasses.field(
+      default_factory=dict, metadata={"suffix": "_id_drop_counters"})
 
   @classmethod
   def from_cc(cls, stats) -> "SparseDenseMatmulInputStats":
@@ -323,6 +329,40 @@ def preprocess_sparse_dense_matmul_input(
                             csr_sorted_by_row=local_device_count == 1,
                             csr_num_entries=counts),
           SparseDenseMatmulInputStats.from_cc(stats))
+
+
+def preprocess_sparse_dense_matmul_input_from_sparse_tensor(
+    indices, values, dense_shapes, feature_specs, local_device_count: int,
+    global_device_count: int, *, num_sc_per_device: int | None = None,
+    sharding_strategy: str = "MOD", has_leading_dimension: bool = False,
+    allow_id_dropping: bool = False, batch_number: int = 0,
+    enable_minibatching: bool = False, all_reduce_interface=None):
+  """Preprocesses sparse COO features on the GPU (embedding.py:708-806).
+
+  `indices` ([N, 2] row-major), `values` ([N] ids) and `dense_shapes`
+  ([batch, width]) share the structure of `feature_specs`; weights are 1.
+  Each feature becomes flat ids plus row splits
+  (pybind_input_preprocessing.sparse_coo_to_ragged) and goes through the same
+  preprocessing as preprocess_sparse_dense_matmul_input.
+  """
+  _assert_same_structure(indices, feature_specs, "indices", "feature_specs")
+  _assert_same_structure(values, feature_specs, "values", "feature_specs")
+  _assert_same_structure(dense_shapes, feature_specs, "dense_shapes",
+                         "feature_specs")
+  specs = _tree.tree_leaves(feature_specs)
+  features = [
+      pybind_input_preprocessing.sparse_coo_to_ragged(i, v, d)
+      for i, v, d in zip(_tree.tree_leaves(indices), _tree.tree_leaves(values),
+                         _tree.tree_leaves(dense_shapes))
+  ]
+  return preprocess_sparse_dense_matmul_input(
+      features, None, specs, local_device_count, global_device_count,
+      num_sc_per_device=num_sc_per_device,
+      sharding_strategy=sharding_strategy,
+      has_leading_dimension=has_leading_dimension,
+      allow_id_dropping=allow_id_dropping, batch_number=batch_number,
+      enable_minibatching=enable_minibatching,
+      all_reduce_interface=all_reduce_interface)
 
 
 def _build_lookup_views(csr, feature_specs, global_device_count: int,
