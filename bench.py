@@ -608,21 +608,36 @@ def cpu_baseline(w: Workload, sample_batch: int, seconds: float):
   }
 
 
+KERNEL_SOURCES = ("segreduce.h", "lookup.hip")
+
+
+def kernel_sources_sha256() -> str:
+  """SHA-256 over the sources of the measured kernels (the SegReduce /
+  SegFinish templates and their launches), in KERNEL_SOURCES order."""
+  import hashlib  # pylint: disable=g-import-not-at-top
+
+  h = hashlib.sha256()
+  for name in KERNEL_SOURCES:
+    with open(os.path.join(ROOT, "jax-tpu-embedding_amd", "csrc", name),
+              "rb") as f:
+      h.update(f.read())
+  return h.hexdigest()
+
+
 def profiled_traffic():
   """HBM bytes per launch pair from the committed rocprofv3 --pmc summary,
-  if it was measured on the current lookup kernels (the summary names the
-  SHA-256 of lookup.hip it was taken with); else None."""
-  import hashlib  # pylint: disable=g-import-not-at-top
+  if it was measured on the current kernel sources (the summary names their
+  SHA-256); else None."""
   import re  # pylint: disable=g-import-not-at-top
 
-  src = os.path.join(ROOT, "jax-tpu-embedding_amd", "csrc", "lookup.hip")
   summary = os.path.join(ROOT, "profiles", "dlrm26_segreduce_hbm_traffic.md")
   try:
-    sha = hashlib.sha256(open(src, "rb").read()).hexdigest()
-    text = open(summary).read()
+    sha = kernel_sources_sha256()
+    with open(summary) as f:
+      text = f.read()
   except OSError:
     return None
-  m = re.search(r"bench-traffic: lookup_hip_sha256=(\w+) bwd_bytes=(\d+) "
+  m = re.search(r"bench-traffic: kernel_sources_sha256=(\w+) bwd_bytes=(\d+) "
                 r"fwd_bytes=(\d+)", text)
   if not m or m.group(1) != sha:
     return None
