@@ -299,7 +299,7 @@ def _stack_batch_ids(w: Workload):
 
 
 def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
-            api: bool = True):
+            api: bool = True, other_optimizers: bool = True):
   import torch  # pylint: disable=g-import-not-at-top
 
   from jax_tpu_embedding.sparsecore import _native  # pylint: disable=g-import-not-at-top
@@ -421,6 +421,11 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
                                      timed_fn=torch.cuda.synchronize)
     log(f"API step (per-feature tensors): fused stacking {api_ms:.4f} ms, "
         f"with stacking copies {api_copy_ms:.4f} ms")
+  opt_ms = None
+  if other_optimizers and len(stacked) == 1:
+    opt_ms = _optimizer_steps(pre, state, stacked, steps, warmup)
+    log("backward + optimizer: " + ", ".join(
+        f"{k} {v:.4f} ms" for k, v in opt_ms.items()))
   spans = {}
   for k in ("fwd_reduce", "fwd_finish", "bwd_reduce", "bwd_finish",
             "fwd_call", "bwd_call"):
@@ -439,7 +444,67 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
       "spans": spans,
       "per_stack": per_stack,
       "dropped": int(sum(stats.id_drop_counters.values())),
+      "optimizer_bwd_ms": opt_ms,
   }
+
+
+# Every built-in optimizer spec with two slot variables, at its defaults.
+OTHER_OPTIMIZERS = ("adam", "adagrad_momentum", "ftrl", "laprop", "f2a")
+
+
+def _optimizer_steps(pre, state, stacked, steps, warmup):
+  """Backward + each two-slot optimizer on the headline stack (the step's
+  backward with another update): ms per call, event-free wall time over
+  `steps` calls. Slots start at the spec's initial values; the table is the
+  step's own (updated in place, as in training)."""
+  import torch  # pylint: disable=g-import-not-at-top
+
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
+
+  specs = {
+      "adam": embedding_spec.AdamOptimizerSpec(learning_rate=0.001),
+      "adagrad_momentum": embedding_spec.AdagradMomentumOptimizerSpec(
+          learning_rate=0.01),
+      "ftrl": embedding_spec.FTRLOptimizerSpec(learning_rate=0.01),
+      "laprop": embedding_spec.LaPropOptimizerSpec(learning_rate=0.001),
+      "f2a": embedding_spec.F2AOptimizerSpec(learning_rate=0.01),
+  }
+  (name, spec), = stacked.items()
+  t, _, g, _ = state[name]
+  slots = [torch.empty_like(t), torch.empty_like(t)]
+  csr = (pre.lhs_row_pointers[name], pre.lhs_embedding_ids[name],
+         pre.lhs_sample_ids[name], pre.lhs_gains[name])
+  kw = dict(max_ids_per_partition=spec.max_ids_per_partition,
+            max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
+            num_sc_per_device=1, csr_sorted_by_row=pre.csr_sorted_by_row,
+            csr_num_entries=pre.csr_num_entries[name])
+  out = {}
+  for key in OTHER_OPTIMIZERS:
+    opt = specs[key]
+    for s, init in zip(slots, opt.slot_variables_initializers()):
+      s.fill_(init.constant_value)
+    hyper = [h if isinstance(h, (bool, np.bool_)) else
+             torch.tensor(float(h), dtype=torch.float32, device=t.device)
+             for h in opt.get_hyperparameters(0)]
+    extra = ({"multiply_linear_by_learning_rate":
+              opt.multiply_linear_by_learning_rate}
+             if key == "ftrl" else {})
+    prim = opt.get_optimizer_primitive()
+
+    def call():
+      prim.bind(*csr, 1, t, *slots, g, *hyper, **kw, **extra)  # pylint: disable=cell-var-from-loop
+
+    for _ in range(warmup):
+      call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+      call()
+    torch.cuda.synchronize()
+    out[key] = (time.perf_counter() - t0) * 1e3 / steps
+  del slots
+  torch.cuda.empty_cache()
+  return out
 
 
 def _api_steps(w, pre, state, stacked, steps, warmup, timed_fn):
@@ -656,6 +721,8 @@ def main():
                   help="run a 1 GiB device copy first (counter calibration)")
   ap.add_argument("--no-api-steps", action="store_true",
                   help="skip timing the step through the embedding API")
+  ap.add_argument("--no-optimizer-steps", action="store_true",
+                  help="skip timing the backward with the other optimizers")
   ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS),
                   help="BASELINE.json config (c2, the 26-table DLRM shape, "
                        "is the headline)")
@@ -668,7 +735,8 @@ def main():
   w = WORKLOADS[args.workload]()
   log(f"workload built in {time.perf_counter() - t_setup:.1f} s")
   res = run_gpu(w, args.steps, args.warmup, probe=args.copy_probe,
-                api=not args.no_api_steps)
+                api=not args.no_api_steps,
+                other_optimizers=not args.no_optimizer_steps)
   fwd_bytes, bwd_bytes = algorithmic_bytes(res["per_stack"])
   step_s = res["ms_per_step"] / 1e3
   sp = res["spans"]
@@ -737,6 +805,15 @@ def main():
       "roofline": roofline,
       "cpu_baseline": cpu,
   }
+  if res["optimizer_bwd_ms"]:
+    # The same backward with each two-slot optimizer: compulsory bytes
+    # 12N + 4D*Bs + 24D*U (table and two slots read and written).
+    (s,) = res["per_stack"].values()
+    two_slot = 12 * s["N"] + 4 * s["D"] * s["Bs"] + 24 * s["D"] * s["U"]
+    out["optimizer_bwd"] = {
+        k: {"ms": round(v, 4),
+            "hbm_frac": round(two_slot / (v / 1e3) / 1e9 / PEAK_HBM_GBS, 4)}
+        for k, v in res["optimizer_bwd_ms"].items()}
   print(json.dumps(out), flush=True)
 
 

@@ -4,9 +4,10 @@
 //
 // Stages (segment g = local_device * S + local_sc):
 //   plan      (host)  split-then-stack slices, input_preprocessing.cc:312-436
-//   extract           one thread per input row: sample id, column id
-//                     (coo_format.h:120-135), combiner gain
-//                     (process_coo_tensors_impl.h:39-136), sort key
+//   extract           per weighted row its combiner divisor (one thread per
+//                     row, sequential float sums); then one thread per id:
+//                     sample id, column id (coo_format.h:120-135), combiner
+//                     gain (process_coo_tensors_impl.h:39-136), sort key
 //                     (segment, partition, local id) = rotr32(col, log2 NS)
 //   sort              stable LSD radix sort of (key, extraction index). The
 //                     reference sorts 64-bit keys whose low field is the row
@@ -106,78 +107,119 @@ __device__ __forceinline__ K SentinelKey() {
   return ~K(0);
 }
 
-// One thread per input row of every slice.
-template <typename K>
-__global__ __launch_bounds__(256) void ExtractRows(
-    const SliceDesc* slices, int num_slices, const FeatureDev* feats,
-    int64_t total_rows, int combiner, int has_weights, KeyLayout kl,
-    K* keys, uint32_t* vals, uint32_t* rows_out, float* gains_out,
-    uint32_t* row_keys, int row_key_bits_seg_shift, int64_t* counters) {
-  const int64_t gr = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (gr >= total_rows) return;
+// Index of the last slice whose outputs (or rows, with by_rows) start at or
+// before `pos`; slices are in output order and both offsets are
+// non-decreasing.
+__device__ __forceinline__ int FindSlice(const SliceDesc* slices,
+                                         int num_slices, int64_t pos,
+                                         bool by_rows) {
   int lo = 0, hi = num_slices - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (slices[mid].row_prefix <= gr) lo = mid; else hi = mid - 1;
+    const int64_t start =
+        by_rows ? slices[mid].row_prefix : slices[mid].out_begin;
+    if (start <= pos) lo = mid; else hi = mid - 1;
   }
-  const SliceDesc sl = slices[lo];
+  return lo;
+}
+
+// Combiner divisor of every input row with weights (ComputeWeightDivisor,
+// process_coo_tensors_impl.h:60-74): the weights summed in id order in
+// float (mean), or the square root of the float sum of double squares
+// (sqrtn). One thread per row: the sums are sequential, as in the reference.
+__global__ __launch_bounds__(256) void RowDivisors(
+    const SliceDesc* slices, int num_slices, const FeatureDev* feats,
+    int64_t total_rows, int combiner, float* divisor) {
+  const int64_t gr = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gr >= total_rows) return;
+  const SliceDesc sl = slices[FindSlice(slices, num_slices, gr, true)];
   const FeatureDev f = feats[sl.feature];
-  const int64_t local_row = gr - sl.row_prefix;
-  const int64_t r = sl.row_start + local_row;
-  int64_t b, e;
-  if (f.splits != nullptr) {
-    b = f.splits[r];
-    e = f.splits[r + 1];
+  const int64_t r = sl.row_start + (gr - sl.row_prefix);
+  const int64_t b = f.splits != nullptr ? f.splits[r] : r * f.valency;
+  const int64_t e = f.splits != nullptr ? f.splits[r + 1] : b + f.valency;
+  float s = 0.0f;
+  if (combiner == 1) {
+    for (int64_t k = b; k < e; ++k) s = s + f.weights[k];
+    divisor[gr] = s;
   } else {
-    b = r * f.valency;
-    e = b + f.valency;
-  }
-  const int64_t cnt = e - b;
-  const int64_t out = sl.out_begin + (b - sl.id_begin);
-  const uint32_t sample = static_cast<uint32_t>(sl.sample_base + local_row);
-  float divisor = 1.0f;
-  float unity_gain = 1.0f;
-  if (!has_weights) {
-    if (combiner == 1) {
-      unity_gain = 1.0f / static_cast<float>(static_cast<int>(cnt));
-    } else if (combiner == 2) {
-      unity_gain = 1.0f / sqrtf(static_cast<float>(static_cast<int>(cnt)));
-    }
-  } else if (combiner == 1) {
-    float s = 0.0f;
-    for (int64_t k = 0; k < cnt; ++k) s = s + f.weights[b + k];
-    divisor = s;
-  } else if (combiner == 2) {
-    float s = 0.0f;
-    for (int64_t k = 0; k < cnt; ++k) {
-      const double w = static_cast<double>(f.weights[b + k]);
+    for (int64_t k = b; k < e; ++k) {
+      const double w = static_cast<double>(f.weights[k]);
       s = static_cast<float>(static_cast<double>(s) + w * w);
     }
-    divisor = sqrtf(s);
+    divisor[gr] = sqrtf(s);
   }
-  const K seg_part = static_cast<K>(sl.segment) << kl.col_bits;
-  int64_t bad = 0;
-  for (int64_t k = 0; k < cnt; ++k) {
-    const int32_t id = f.ids[b + k];
+}
+
+// One thread per extracted id (output position o, in slice order): finds its
+// slice and input row, then writes the sort key (segment, column) -- or the
+// sentinel for an id outside the table --, the extraction index, the sample
+// id, the gain and, for the optional row pass, the row key. Consecutive
+// threads write consecutive positions. Gains: unit weights give 1, 1/n or
+// 1/sqrt(n) for a row of n ids (process_coo_tensors_impl.h:39-56); weights
+// are divided by the row's divisor (RowDivisors; 1 for sum).
+template <typename K>
+__global__ __launch_bounds__(256) void ExtractIds(
+    const SliceDesc* slices, int num_slices, const FeatureDev* feats,
+    int64_t total_ids, int combiner, int has_weights,
+    const float* divisor, KeyLayout kl, K* keys, uint32_t* vals,
+    uint32_t* rows_out, float* gains_out, uint32_t* row_keys,
+    int row_key_bits_seg_shift, int64_t* counters) {
+  const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  bool bad = false;
+  if (o < total_ids) {
+    const SliceDesc sl = slices[FindSlice(slices, num_slices, o, false)];
+    const FeatureDev f = feats[sl.feature];
+    const int64_t p = sl.id_begin + (o - sl.out_begin);  // input position
+    int64_t r, b, e;
+    if (f.splits != nullptr) {
+      // Last row of the slice starting at or before p.
+      int64_t lo = sl.row_start, hi = sl.row_start + sl.num_rows - 1;
+      while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (f.splits[mid] <= p) lo = mid; else hi = mid - 1;
+      }
+      r = lo;
+      b = f.splits[r];
+      e = f.splits[r + 1];
+    } else {
+      r = p / f.valency;
+      b = r * f.valency;
+      e = b + f.valency;
+    }
+    const int64_t local_row = r - sl.row_start;
+    const uint32_t sample = static_cast<uint32_t>(sl.sample_base + local_row);
+    float gain = 1.0f;
+    if (has_weights) {
+      gain = f.weights[p] /
+             (combiner == 0 ? 1.0f : divisor[sl.row_prefix + local_row]);
+    } else if (combiner == 1) {
+      gain = 1.0f / static_cast<float>(static_cast<int>(e - b));
+    } else if (combiner == 2) {
+      gain = 1.0f / sqrtf(static_cast<float>(static_cast<int>(e - b)));
+    }
+    const int32_t id = f.ids[p];
     // GetColId: ((id + shift) & mask) + (id & ~mask) + offset.
     const int32_t col = ((id + f.col_shift) & kl.ns_mask) + (id & ~kl.ns_mask) +
                         f.col_offset;
     const bool ok = id >= 0 && col >= 0 &&
                     (kl.col_bound <= 0 || static_cast<int64_t>(col) < kl.col_bound);
-    const int64_t o = out + k;
+    const K seg_part = static_cast<K>(sl.segment) << kl.col_bits;
     keys[o] = ok ? (seg_part | ColKey<K>(static_cast<uint32_t>(col), kl))
                  : SentinelKey<K>();
     vals[o] = static_cast<uint32_t>(o);
     rows_out[o] = sample;
-    gains_out[o] = has_weights ? f.weights[b + k] / divisor : unity_gain;
+    gains_out[o] = gain;
     if (row_keys != nullptr) {
       row_keys[o] = (static_cast<uint32_t>(sl.segment) << row_key_bits_seg_shift) |
                     sample;
     }
-    if (!ok) ++bad;
+    bad = !ok;
   }
-  if (bad) atomicAdd(reinterpret_cast<unsigned long long*>(&counters[2]),
-                     static_cast<unsigned long long>(bad));
+  const uint64_t m = __ballot(bad);
+  if (m != 0 && (threadIdx.x % kWave) == 0) {
+    atomicAdd(reinterpret_cast<unsigned long long*>(&counters[2]),
+              static_cast<unsigned long long>(__popcll(m)));
+  }
 }
 
 template <typename K>
@@ -781,6 +823,10 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   b.plans = ws.Take<FillPlan>(num_buckets);
   b.slices = ws.Take<SliceDesc>(static_cast<int64_t>(pl.slices.size()));
   b.feats = ws.Take<FeatureDev>(nf);
+  // Per-row divisors of weighted mean / sqrtn.
+  float* divisors = o->has_variable_weights && o->combiner != 0
+                        ? ws.Take<float>(pl.total_rows)
+                        : nullptr;
   const bool measuring = ws.measuring();
   const int64_t counters_off = RoundUp(2 * static_cast<int64_t>(pl.L) * pl.NS +
                                        static_cast<int64_t>(pl.L) * pl.S, 2);
@@ -829,12 +875,18 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
     hipLaunchKernelGGL(FillI32, dim3(CeilDiv(num_buckets, 256)), dim3(256), 0,
                        stream, b.part_last, num_buckets, -1);
     SCEMB_LAUNCH_CHECK();
-    if (pl.total_rows > 0) {
-      hipLaunchKernelGGL((ExtractRows<K>), dim3(CeilDiv(pl.total_rows, 256)),
+    if (divisors != nullptr && pl.total_rows > 0) {
+      hipLaunchKernelGGL(RowDivisors, dim3(CeilDiv(pl.total_rows, 256)),
                          dim3(256), 0, stream, b.slices,
                          static_cast<int>(pl.slices.size()), b.feats,
-                         pl.total_rows, o->combiner,
-                         o->has_variable_weights ? 1 : 0, pl.kl,
+                         pl.total_rows, o->combiner, divisors);
+      SCEMB_LAUNCH_CHECK();
+    }
+    if (M > 0) {
+      hipLaunchKernelGGL((ExtractIds<K>), dim3(CeilDiv(M, 256)), dim3(256), 0,
+                         stream, b.slices, static_cast<int>(pl.slices.size()),
+                         b.feats, M, o->combiner,
+                         o->has_variable_weights ? 1 : 0, divisors, pl.kl,
                          static_cast<K*>(b.keys), b.vals, b.rows, b.gains,
                          b.row_keys, pl.row_key_seg_shift, counters);
       SCEMB_LAUNCH_CHECK();

@@ -375,7 +375,46 @@ __host__ __device__ constexpr int NumHyper() {
 struct Hyper {
   float h[kMaxHyper];
   float derived;
+  int pow_kind;  // PowKindOf() of the optimizer's per-value exponent
 };
+
+// pow(x, e) for a per-call exponent e. The exponents the optimizers' defaults
+// use (1/2 for FTRL and F2A, -1/2 for AdagradMomentum) and a few others have
+// exact forms that replace the library pow, which costs tens of
+// instructions per value: sqrt and division are correctly rounded, so these
+// differ from pow by at most its own rounding. x + 0.0f maps -0 to +0, as
+// pow(-0, +-1/2) = +0 / +inf requires.
+enum { kPowGeneric = 0, kPowHalf, kPowMinusHalf, kPowOne, kPowMinusOne,
+       kPowTwo, kPowZero };
+
+__device__ __forceinline__ int PowKindOf(float e) {
+  return e == 0.5f    ? kPowHalf
+         : e == -0.5f ? kPowMinusHalf
+         : e == 1.0f  ? kPowOne
+         : e == -1.0f ? kPowMinusOne
+         : e == 2.0f  ? kPowTwo
+         : e == 0.0f  ? kPowZero
+                      : kPowGeneric;
+}
+
+__device__ __forceinline__ float PowBy(float x, float e, int kind) {
+  switch (kind) {
+    case kPowHalf:
+      return sqrtf(x + 0.0f);
+    case kPowMinusHalf:
+      return 1.0f / sqrtf(x + 0.0f);
+    case kPowOne:
+      return x;
+    case kPowMinusOne:
+      return 1.0f / x;
+    case kPowTwo:
+      return x * x;
+    case kPowZero:
+      return 1.0f;
+    default:
+      return powf(x, e);
+  }
+}
 
 template <int EPI>
 __device__ __forceinline__ Hyper LoadHyper(const OptParams& o) {
@@ -386,6 +425,12 @@ __device__ __forceinline__ Hyper LoadHyper(const OptParams& o) {
   }
   if (EPI == kEpiAdagradMomentum) {
     H.derived = -1.0f / H.h[4];  // the power applied to accumulator + eps
+    H.pow_kind = PowKindOf(H.derived);
+  } else if (EPI == kEpiFtrl) {
+    H.derived = -H.h[1];  // the power applied to the accumulators
+    H.pow_kind = PowKindOf(H.derived);
+  } else if (EPI == kEpiF2a) {
+    H.pow_kind = PowKindOf(H.h[1]);  // rho
   } else if (EPI == kEpiLaprop) {
     H.derived = powf(1.0f - powf(H.h[1], 2.0f), 0.5f);  // sqrt(1 - b1^2)
   }
@@ -405,7 +450,7 @@ __device__ __forceinline__ Hyper LoadHyper(const OptParams& o) {
 //   LaProp           sparse_dense_matmul_grad_with_laprop.py:282-340
 //   F2A              sparse_dense_matmul_grad_with_f2a.py:244-290
 // with the operations in the same order and association, so that only the
-// rounding of the library sqrt and pow can differ.
+// rounding of pow (PowBy) can differ.
 template <int EPI>
 __device__ __forceinline__ float UpdateOne(float t, float& s0, float& s1,
                                            float g, const Hyper& H,
@@ -430,7 +475,7 @@ __device__ __forceinline__ float UpdateOne(float t, float& s0, float& s1,
     const float g2 = g * g;
     const float a = H.h[2] == 1.0f ? s0 + g2
                                    : H.h[2] * s0 + (1.0f - H.h[2]) * g2;
-    const float sg = powf(a + H.h[3], H.derived) * g;
+    const float sg = PowBy(a + H.h[3], H.derived, H.pow_kind) * g;
     const float m = H.h[1] * s1 + sg;
     const float upd = H.h[5] != 0.0f ? H.h[1] * m + sg : m;
     s0 = a;
@@ -440,8 +485,8 @@ __device__ __forceinline__ float UpdateOne(float t, float& s0, float& s1,
     // (lr, lr_power, l1, l2, beta); slots (accumulator, linear).
     const float lr = H.h[0];
     const float a = s0 + g * g;
-    const float p_old = powf(s0, -H.h[1]);
-    const float p_new = powf(a, -H.h[1]);
+    const float p_old = PowBy(s0, H.derived, H.pow_kind);
+    const float p_new = PowBy(a, H.derived, H.pow_kind);
     const float dp = p_new - p_old;
     const bool by_lr =
         (o.flags & SCEMB_OPTIMIZER_FLAG_MULTIPLY_LINEAR_BY_LR) != 0;
@@ -468,7 +513,7 @@ __device__ __forceinline__ float UpdateOne(float t, float& s0, float& s1,
     // (accumulator, local_step). sign() keeps zeros (and NaN) as they are.
     const float ls = s1 + 1.0f;
     const float ratio = fmaxf(H.h[5], 1.0f) / ls;
-    const float fa = fminf(powf(ratio, H.h[1]), H.h[4]);
+    const float fa = fminf(PowBy(ratio, H.h[1], H.pow_kind), H.h[4]);
     const float a = s0 + g * g;
     const float sgn = t > 0.0f ? 1.0f : (t < 0.0f ? -1.0f : t);
     const float upd = (g * fa) / sqrtf(a) + (H.h[2] * sgn + H.h[3] * t);

@@ -18,6 +18,7 @@ _NP_OF = {
     "torch.float16": np.float16,
     "torch.bfloat16": None,
     "torch.uint8": np.uint8,
+    "torch.bool": np.bool_,
 }
 
 
