@@ -59,6 +59,9 @@ extern "C" {
 #define SCEMB_STATUS_UNSORTED 4u     /* a stream declared sorted (CSR flag
                                         or sample view) is not: results are
                                         not valid */
+#define SCEMB_STATUS_SHARED_ROW 8u   /* a CSR declared with at most one
+                                        entry per activation row has two:
+                                        results are not valid */
 
 /* Message of the last failing call on this thread ("" if none). */
 const char* scemb_last_error(void);
@@ -93,6 +96,12 @@ typedef struct scemb_csr {
  * CSR in place instead of sorting it; order violations are reported through
  * SCEMB_STATUS_UNSORTED. */
 #define SCEMB_CSR_SORTED_BY_ROW 1u
+
+/* At most one valid entry per activation row (every input row of the stack
+ * holds at most one id: one-hot features). Building the sample view is then
+ * a placement by activation row instead of a sort; a second entry for a row
+ * is reported through SCEMB_STATUS_SHARED_ROW. */
+#define SCEMB_CSR_ONE_ENTRY_PER_ROW 2u
 
 /* The CSR entries of one device grouped by activation row (no counterpart
  * in the reference, where the SparseCore scatters into activations in

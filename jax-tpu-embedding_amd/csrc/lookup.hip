@@ -13,12 +13,95 @@ __global__ void FillF32(float* p, int64_t n, float v) {
   if (i < n) p[i] = v;
 }
 
-// Sample-major stream of a CSR into (keys, entries): expand + stable sort.
-// The result lands in (b.keys, b.pay) or the alt pair (*in_alt).
+// One-entry-per-row CSRs: each valid entry claims its activation row's slot
+// (count 1, packed entry). A second claim is flagged.
+__global__ __launch_bounds__(256) void SlotByRow(Csr csr, int64_t bps,
+                                                 int64_t rows_per_partition,
+                                                 uint32_t* count,
+                                                 uint64_t* slot,
+                                                 uint32_t* status) {
+  const int64_t n = csr.per_segment * csr.num_segments;
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const int s = static_cast<int>(j / csr.per_segment);
+  const int64_t off = j - static_cast<int64_t>(s) * csr.per_segment;
+  const int p = PartitionOf(csr.rp + static_cast<int64_t>(s) * csr.rp_per_segment,
+                            csr.num_partitions, csr.per_segment, off);
+  if (p < 0) return;
+  const int32_t e = csr.eid[j];
+  const int32_t sm = csr.sid[j];
+  if (e < 0 || e >= rows_per_partition || sm < 0 || sm >= bps) {
+    if (status != nullptr) atomicOr(status, SCEMB_STATUS_BAD_ENTRY);
+    return;
+  }
+  const int64_t arow = s * bps + sm;
+  if (atomicAdd(&count[arow], 1u) != 0 && status != nullptr) {
+    atomicOr(status, SCEMB_STATUS_SHARED_ROW);
+  }
+  slot[arow] = Pack(static_cast<uint32_t>(p * rows_per_partition + e),
+                    csr.gains[j]);
+}
+
+// pos = exclusive scan of the slot counts (pos[batch] = entries): row r's
+// entry goes to pos[r]; positions from pos[batch] on get the unused key.
+__global__ __launch_bounds__(256) void CompactSlots(const uint32_t* pos,
+                                                    const uint64_t* slot,
+                                                    int64_t batch, int64_t n,
+                                                    uint32_t* keys,
+                                                    uint64_t* entries) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < batch && pos[i + 1] > pos[i]) {
+    keys[pos[i]] = static_cast<uint32_t>(i);
+    entries[pos[i]] = slot[i];
+  }
+  if (i < n && i >= static_cast<int64_t>(pos[batch])) {
+    keys[i] = static_cast<uint32_t>(batch);
+    entries[i] = 0;
+  }
+}
+
+__global__ void FillU32(uint32_t* p, int64_t n, uint32_t v) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// Sample-major stream of a CSR into (keys, entries). With at most one entry
+// per activation row (SCEMB_CSR_ONE_ENTRY_PER_ROW) the entries are placed by
+// row through a count / scan / compaction; otherwise expand + stable radix
+// sort. The result lands in (b.keys, b.pay) or the alt pair (*in_alt).
 int BuildSampleStream(const scemb_csr_t* csr, const Geometry& geo,
                       int64_t batch, const SortBuffers& b, Arena& ws,
                       uint32_t* status, hipStream_t stream, bool* in_alt) {
   const int64_t n = geo.n;
+  if ((csr->flags & SCEMB_CSR_ONE_ENTRY_PER_ROW) != 0) {
+    *in_alt = false;
+    uint32_t* pos = ws.Take<uint32_t>(batch + 1);
+    uint64_t* slot = ws.Take<uint64_t>(batch);
+    const bool measuring = ws.measuring();
+    if (!measuring) {
+      if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+      hipLaunchKernelGGL(FillU32, dim3(CeilDiv(batch + 1, 256)), dim3(256), 0,
+                         stream, pos, batch + 1, 0u);
+      SCEMB_LAUNCH_CHECK();
+      if (n > 0) {
+        hipLaunchKernelGGL(SlotByRow, dim3(CeilDiv(n, 256)), dim3(256), 0,
+                           stream, MakeCsr(csr), geo.bps,
+                           geo.rows_per_partition, pos, slot, status);
+        SCEMB_LAUNCH_CHECK();
+      }
+    }
+    const int st = ExclusiveScan<uint32_t>(pos, pos, batch + 1, nullptr, ws,
+                                           stream);
+    if (st != 0 || measuring) return st;
+    if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+    const int64_t grid = batch > n ? batch : n;
+    if (grid > 0) {
+      hipLaunchKernelGGL(CompactSlots, dim3(CeilDiv(grid, 256)), dim3(256), 0,
+                         stream, pos, slot, batch, n, b.keys, b.pay);
+      SCEMB_LAUNCH_CHECK();
+    }
+    return 0;
+  }
   if (!ws.measuring() && n > 0) {
     hipLaunchKernelGGL(ExpandCsr<true>, dim3(CeilDiv(n, 256)), dim3(256), 0,
                        stream, MakeCsr(csr), geo.bps, geo.rows_per_partition,

@@ -29,8 +29,10 @@ SCEMB_ERR_LIMIT_EXCEEDED = 5
 STATUS_BAD_ENTRY = 1
 STATUS_BAD_ID = 2
 STATUS_UNSORTED = 4
+STATUS_SHARED_ROW = 8
 
 CSR_SORTED_BY_ROW = 1
+CSR_ONE_ENTRY_PER_ROW = 2
 
 # scemb_optimizer_t kinds and flags.
 OPTIMIZER_SGD = 0
@@ -368,9 +370,11 @@ WORKSPACE = _Workspace()
 
 def make_csr(row_pointers, embedding_ids, sample_ids, gains, num_segments,
              num_partitions, sorted_by_row: bool = False,
-             num_entries: int | None = None) -> Csr:
+             num_entries: int | None = None,
+             one_entry_per_row: bool = False) -> Csr:
   """`num_entries`: the valid entries of the buffers when known (it only
-  picks kernel variants)."""
+  picks kernel variants). `sorted_by_row` / `one_entry_per_row` set
+  CSR_SORTED_BY_ROW / CSR_ONE_ENTRY_PER_ROW."""
   rp_len = int(row_pointers.numel())
   if rp_len % num_segments:
     raise ValueError("row_pointers length must be divisible by "
@@ -378,7 +382,8 @@ def make_csr(row_pointers, embedding_ids, sample_ids, gains, num_segments,
   return Csr(ptr(row_pointers), ptr(embedding_ids), ptr(sample_ids),
              ptr(gains), int(embedding_ids.numel()), num_segments,
              num_partitions, rp_len // num_segments,
-             CSR_SORTED_BY_ROW if sorted_by_row else 0,
+             (CSR_SORTED_BY_ROW if sorted_by_row else 0) |
+             (CSR_ONE_ENTRY_PER_ROW if one_entry_per_row else 0),
              int(num_entries) if num_entries else 0)
 
 

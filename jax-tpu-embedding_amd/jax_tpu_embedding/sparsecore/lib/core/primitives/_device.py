@@ -18,12 +18,14 @@ def resolve_sparsecores(num_sc_per_device, global_device_count):
 
 def csr_operands(row_pointers, embedding_ids, sample_ids, gains,
                  num_sc_per_device, num_partitions, sorted_by_row=False,
-                 num_entries=None):
+                 num_entries=None, one_entry_per_row=False):
   """Device tensors for the CSR buffers plus the C struct that points at
   them (the tensors must stay alive while the struct is used).
   `sorted_by_row` declares the entries ascending by (partition, embedding
   id) inside each segment, as the preprocessing writes them; `num_entries`
-  the count of valid entries when known (it only picks kernel variants)."""
+  the count of valid entries when known (it only picks kernel variants);
+  `one_entry_per_row` at most one entry per activation row (one-hot input
+  rows), which turns the grouping by activation row into a placement."""
   t = _native.require_gpu()
   dev = _native.device()
   rp = _native.as_device_tensor(row_pointers, t.int32, dev).reshape(-1)
@@ -31,7 +33,8 @@ def csr_operands(row_pointers, embedding_ids, sample_ids, gains,
   sid = _native.as_device_tensor(sample_ids, t.int32, dev).reshape(-1)
   g = _native.as_device_tensor(gains, t.float32, dev).reshape(-1)
   csr = _native.make_csr(rp, eid, sid, g, num_sc_per_device, num_partitions,
-                         sorted_by_row=sorted_by_row, num_entries=num_entries)
+                         sorted_by_row=sorted_by_row, num_entries=num_entries,
+                         one_entry_per_row=one_entry_per_row)
   return (rp, eid, sid, g), csr
 
 

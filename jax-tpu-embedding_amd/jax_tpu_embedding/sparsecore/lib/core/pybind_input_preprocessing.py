@@ -397,6 +397,21 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
   return rps, eids, sids, gns, pending
 
 
+def one_id_per_row(pending) -> dict:
+  """Stack name -> whether every input row of the stack holds at most one
+  id (then every activation row gets at most one CSR entry)."""
+  out = {}
+  for name, *_, feats in pending:
+    ok = True
+    for f in feats:
+      if f.splits_host is not None:
+        ok = ok and (f.nnz == 0 or int(np.diff(f.splits_host).max()) <= 1)
+      else:
+        ok = ok and f.valency <= 1
+    out[name] = ok
+  return out
+
+
 def collect_stats(pending) -> SparseDenseMatmulInputStats:
   """Waits for the enqueued preprocessing and returns its stats; raises as
   the reference does on bad ids or exceeded limits."""

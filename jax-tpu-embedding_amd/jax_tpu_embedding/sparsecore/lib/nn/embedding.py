@@ -312,9 +312,10 @@ def preprocess_sparse_dense_matmul_input(
       has_leading_dimension=has_leading_dimension,
       allow_id_dropping=allow_id_dropping)
   views = None
+  one_per_row = pybind_input_preprocessing.one_id_per_row(pending)
   if local_device_count == 1:
     views = _build_lookup_views(csr, feature_specs, global_device_count,
-                                num_sc_per_device)
+                                num_sc_per_device, one_per_row)
   stats = pybind_input_preprocessing.collect_stats(pending)
   counts = None
   if local_device_count == 1:
@@ -366,7 +367,7 @@ def preprocess_sparse_dense_matmul_input_from_sparse_tensor(
 
 
 def _build_lookup_views(csr, feature_specs, global_device_count: int,
-                        num_sc_per_device: int):
+                        num_sc_per_device: int, one_per_row: dict):
   """Sample views of one device's CSR buffers, one per stacked table, for a
   table shard of stack_vocab_size / global_device_count rows."""
   rp, eid, sid, gains = csr
@@ -376,7 +377,8 @@ def _build_lookup_views(csr, feature_specs, global_device_count: int,
     rows = spec.stack_vocab_size // global_device_count
     _, c = _device.csr_operands(rp[name], eid[name], sid[name], gains[name],
                                 num_sc_per_device,
-                                num_sc_per_device * global_device_count)
+                                num_sc_per_device * global_device_count,
+                                one_entry_per_row=one_per_row.get(name, False))
     views[name] = _native.build_sample_view(c, batch, rows)
   return views
 

@@ -655,3 +655,65 @@ def test_fused_unstack_and_gradient_stack_match_copy_paths(num_sc, integer):
     # ever sees zero gradient.
     assert bool((v_fused[name].slot[0][:, 12:16] ==
                  v_copy[name].slot[0][:, 12:16]).all())
+
+
+@pytest.mark.parametrize("num_sc", [1, 4])
+def test_one_entry_per_row_view_matches_sorted_view(num_sc):
+  """With at most one id per input row, the sample view built by placement
+  (CSR_ONE_ENTRY_PER_ROW: count, scan, compaction) is bit for bit the view
+  the radix sort builds, with empty rows (no id) and invalid entries among
+  the samples, and the forward results agree bit for bit."""
+  rng = np.random.default_rng(17 + num_sc)
+  batch, vocab, dim = 512, 3000, 16
+  tables, feats = _make_specs(2, [vocab, 700], [dim, dim], "sum",
+                              embedding_spec.SGDOptimizerSpec(0.01), batch)
+  _stack(feats, ["table_0", "table_1"], 1, num_sc)
+  features = []
+  for t in tables:
+    rows = np.empty(batch, dtype=object)
+    for i in range(batch):
+      rows[i] = (np.array([rng.integers(0, t.vocabulary_size)], np.int32)
+                 if rng.random() < 0.8 else np.zeros(0, np.int32))
+    features.append(rows)
+  name, ref = _csr_from_oracle(features, None, feats, num_sc)
+  spec = feats[0].table_spec.stacked_table_spec
+  bs, rows_ = spec.total_sample_count, spec.stack_vocab_size
+  csr = (ref.row_pointers[name], ref.embedding_ids[name],
+         ref.sample_ids[name], ref.gains[name].copy())
+  # Two entries with an embedding id outside the table: skipped either way.
+  bad = np.nonzero(csr[1] != np.iinfo(np.int32).max)[0][:2]
+  csr[1][bad] = rows_ // num_sc + 5
+  views = []
+  for one in (False, True):
+    keep, c = _device.csr_operands(*csr, num_sc, num_sc,
+                                   one_entry_per_row=one)
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    views.append((_native.build_sample_view(c, bs, rows_,
+                                            device_status=status), status))
+    torch.cuda.synchronize()
+    del keep
+  (v0, s0), (v1, s1) = views
+  np.testing.assert_array_equal(v1.keys.cpu().numpy(), v0.keys.cpu().numpy())
+  np.testing.assert_array_equal(v1.entries.cpu().numpy(),
+                                v0.entries.cpu().numpy())
+  assert int(s0.item()) == int(s1.item()) == _native.STATUS_BAD_ENTRY
+  table = torch.from_numpy(
+      rng.normal(size=(rows_, dim)).astype(np.float32)).cuda()
+  acts = [_fwd_bind(ref, name, table, bs, num_sc, view=v).cpu().numpy()
+          for v in (v0, v1)]
+  np.testing.assert_array_equal(acts[0], acts[1])
+
+
+def test_shared_row_in_one_entry_per_row_csr_is_flagged():
+  """A CSR with two entries for one activation row, declared one entry per
+  row: the placement reports SCEMB_STATUS_SHARED_ROW."""
+  rp = np.full(8, 3, np.int32)
+  eid = np.array([1, 2, 3], np.int32)
+  sid = np.array([0, 5, 0], np.int32)
+  gains = np.ones(3, np.float32)
+  keep, c = _device.csr_operands(rp, eid, sid, gains, 1, 1,
+                                 one_entry_per_row=True)
+  status = torch.zeros(1, dtype=torch.int32, device="cuda")
+  _native.build_sample_view(c, 8, 16, device_status=status)
+  assert int(status.item()) & _native.STATUS_SHARED_ROW
+  del keep
