@@ -323,6 +323,19 @@ typedef struct scemb_preprocess_options {
   int32_t has_variable_weights; /* weights given for the stack's features */
   int64_t coo_buffer_size_per_device;
   int64_t col_id_bound; /* exclusive bound on column ids (stack vocab size) */
+  /* 1: also write the sample view of the CSR (scemb_sample_view_t) into
+   * out->view_keys / view_entries, without a sort: the entries come out of
+   * the preprocessing already grouped by activation row. Needs
+   * local_device_count = global_device_count = 1 and features whose sample
+   * rows do not overlap (row_offset order, as GetStackedTableMetadata gives
+   * them); entries of one activation row are in input order of their first
+   * id (scemb_build_sample_view keeps CSR order instead; both group the same
+   * entries). Entries whose embedding id is outside the table (table_rows /
+   * num_partitions rows per partition) are left out, as the forward skips
+   * them. */
+  int32_t build_sample_view;
+  int32_t reserved;
+  int64_t table_rows; /* rows of the device's table, for the sample view */
 } scemb_preprocess_options_t;
 
 /* Device outputs. The stats block is int32 laid out as
@@ -335,6 +348,8 @@ typedef struct scemb_preprocess_output {
   int32_t* sample_ids;    /* [L * coo_buffer_size_per_device] */
   float* gains;           /* [L * coo_buffer_size_per_device] */
   int32_t* stats;         /* scemb_preprocess_stats_size() int32 slots */
+  uint32_t* view_keys;     /* [coo_buffer_size_per_device], build_sample_view */
+  uint64_t* view_entries;  /* [coo_buffer_size_per_device], build_sample_view */
 } scemb_preprocess_output_t;
 
 int64_t scemb_preprocess_stats_size(const scemb_preprocess_options_t* opts);

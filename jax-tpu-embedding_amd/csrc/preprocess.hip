@@ -504,13 +504,23 @@ __global__ __launch_bounds__(256) void FillPlanKernel(
   }
 }
 
+// What the sample view needs of every run written to the CSR, indexed by
+// the extraction position of the run's first id (null: no view).
+struct ViewParts {
+  const uint32_t* sidx;  // sorted position -> extraction position
+  uint32_t* mark;        // [M + 1] 1 where a written run starts
+  uint32_t* key;         // [M] activation row
+  uint64_t* entry;       // [M] table row | gain bits << 32
+  int64_t rows_per_partition;
+};
+
 template <typename K>
 __global__ __launch_bounds__(256) void ScatterRuns(
     const K* skeys, const uint32_t* srows, const uint32_t* run_pos,
     const float* run_gain, const uint32_t* keep, const uint32_t* keep_scan,
     const uint64_t* totals, int64_t n_upper, KeyLayout kl, FillParams fp,
     int32_t bps, const BucketStats* bstats, const FillPlan* plans,
-    int32_t* eid, int32_t* sid, float* gains) {
+    int32_t* eid, int32_t* sid, float* gains, ViewParts view) {
   const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (r >= n_upper) return;
   const int64_t runs = static_cast<int64_t>(static_cast<uint32_t>(totals[0]));
@@ -530,6 +540,34 @@ __global__ __launch_bounds__(256) void ScatterRuns(
   eid[pos] = static_cast<int32_t>(local);
   sid[pos] = static_cast<int32_t>(srows[i0] % static_cast<uint32_t>(bps));
   gains[pos] = run_gain[r];
+  if (view.mark != nullptr && local < view.rows_per_partition) {
+    // One device: the activation row is the stacked sample id itself.
+    const uint32_t e0 = view.sidx[i0];
+    view.mark[e0] = 1;
+    view.key[e0] = srows[i0];
+    view.entry[e0] =
+        static_cast<uint64_t>(p * view.rows_per_partition + local) |
+        (static_cast<uint64_t>(__float_as_uint(run_gain[r])) << 32);
+  }
+}
+
+// The sample view in extraction order, which is activation-row order: the
+// run starting at extraction position e goes to view position pos[e]
+// (exclusive scan of the marks); positions from pos[m] to n get the unused
+// key.
+__global__ __launch_bounds__(256) void ViewCompact(
+    const uint32_t* pos, const uint32_t* vkey, const uint64_t* ventry,
+    int64_t m, int64_t n, uint32_t unused_key, uint32_t* keys,
+    uint64_t* entries) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < m && pos[i + 1] > pos[i]) {
+    keys[pos[i]] = vkey[i];
+    entries[pos[i]] = ventry[i];
+  }
+  if (i < n && i >= static_cast<int64_t>(pos[m])) {
+    keys[i] = unused_key;
+    entries[i] = 0;
+  }
 }
 
 __global__ __launch_bounds__(256) void WritePadding(const FillPlan* plans,
@@ -827,6 +865,26 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   float* divisors = o->has_variable_weights && o->combiner != 0
                         ? ws.Take<float>(pl.total_rows)
                         : nullptr;
+  ViewParts view{};
+  if (o->build_sample_view) {
+    if (pl.L != 1 || pl.G != 1) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "the sample view needs one local and one global device");
+    }
+    if (!pl.rows_monotone) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "the sample view needs features whose sample rows do not "
+                  "overlap (row_offset order)");
+    }
+    if (o->table_rows <= 0 || o->table_rows % pl.NS != 0) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "table_rows must be a positive multiple of the partitions");
+    }
+    view.mark = ws.Take<uint32_t>(M + 1);
+    view.key = ws.Take<uint32_t>(M);
+    view.entry = ws.Take<uint64_t>(M);
+    view.rows_per_partition = o->table_rows / pl.NS;
+  }
   const bool measuring = ws.measuring();
   const int64_t counters_off = RoundUp(2 * static_cast<int64_t>(pl.L) * pl.NS +
                                        static_cast<int64_t>(pl.L) * pl.S, 2);
@@ -837,6 +895,10 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
         out->embedding_ids == nullptr || out->sample_ids == nullptr ||
         out->gains == nullptr) {
       return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null output buffer");
+    }
+    if (view.mark != nullptr &&
+        (out->view_keys == nullptr || out->view_entries == nullptr)) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null sample view buffer");
     }
     counters = reinterpret_cast<int64_t*>(out->stats + counters_off);
     if ((reinterpret_cast<uintptr_t>(counters) & 7u) != 0) {
@@ -960,7 +1022,13 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   st = ExclusiveScan<uint32_t>(b.keep, b.keep_scan, M + 1, nullptr, ws,
                                stream);
   if (st != 0) return st;
-  if (measuring) return 0;
+  if (measuring) {
+    // The view's scan runs last; size its temporaries at the same point.
+    return view.mark != nullptr
+               ? ExclusiveScan<uint32_t>(nullptr, nullptr, M + 1, nullptr, ws,
+                                         stream)
+               : 0;
+  }
   if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
   hipLaunchKernelGGL(BucketReduce, dim3(CeilDiv(num_buckets, 256)), dim3(256),
                      0, stream, b.part_first, b.part_last, b.flags, b.scan,
@@ -982,12 +1050,19 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                      fp, out->row_pointers, b.plans, stat_max_ids,
                      stat_max_unique, stat_required, counters);
   SCEMB_LAUNCH_CHECK();
+  if (view.mark != nullptr) {
+    view.sidx = sidx;
+    hipLaunchKernelGGL(FillI32, dim3(CeilDiv(M + 1, 256)), dim3(256), 0,
+                       stream, reinterpret_cast<int32_t*>(view.mark), M + 1,
+                       0);
+    SCEMB_LAUNCH_CHECK();
+  }
   if (M > 0) {
     hipLaunchKernelGGL((ScatterRuns<K>), dim3(CeilDiv(M, 256)), dim3(256), 0,
                        stream, skeys, b.srows, b.run_pos, b.run_gain, b.keep,
                        b.keep_scan, b.totals, M, pl.kl, fp,
                        static_cast<int32_t>(pl.bps), b.bstats, b.plans,
-                       out->embedding_ids, out->sample_ids, out->gains);
+                       out->embedding_ids, out->sample_ids, out->gains, view);
     SCEMB_LAUNCH_CHECK();
     hipLaunchKernelGGL(StoreTotal, dim3(1), dim3(1), 0, stream, b.totals,
                        counters);
@@ -997,6 +1072,20 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                      dim3(256), 0, stream, b.plans, num_buckets, fp,
                      out->embedding_ids, out->sample_ids, out->gains);
   SCEMB_LAUNCH_CHECK();
+  if (view.mark != nullptr) {
+    st = ExclusiveScan<uint32_t>(view.mark, view.mark, M + 1, nullptr, ws,
+                                 stream);
+    if (st != 0) return st;
+    const int64_t n = pl.coo_size;
+    const int64_t grid = M > n ? M : n;
+    if (grid > 0) {
+      hipLaunchKernelGGL(ViewCompact, dim3(CeilDiv(grid, 256)), dim3(256), 0,
+                         stream, view.mark, view.key, view.entry, M, n,
+                         static_cast<uint32_t>(pl.batch_for_device),
+                         out->view_keys, out->view_entries);
+      SCEMB_LAUNCH_CHECK();
+    }
+  }
   return 0;
 }
 

@@ -10,6 +10,8 @@
 // (wave-level multisplit), then across waves and chunks through LDS counters.
 #include "scan.h"
 
+#include "../../include/scemb.h"
+
 namespace scemb {
 namespace {
 
@@ -92,6 +94,9 @@ int ExclusiveScan(const T* in, T* out, int64_t n, T* total, Arena& ws,
   }
   T* partial = ws.Take<T>(tiles);
   const bool measuring = ws.measuring();
+  if (!measuring && ws.overflow()) {
+    return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+  }
   if (!measuring) {
     hipLaunchKernelGGL(ScanReduceTiles<T>, dim3(tiles), dim3(kScanBlock), 0,
                        stream, in, n, partial);
@@ -220,6 +225,9 @@ int RadixSortPairs(K* keys, V* vals, K* keys_alt, V* vals_alt, int64_t n,
   const int64_t tiles = CeilDiv(n, kSortTile);
   uint32_t* hist = ws.Take<uint32_t>(tiles * kRadix);
   const bool measuring = ws.measuring();
+  if (!measuring && ws.overflow()) {
+    return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+  }
   K* src_k = keys;
   V* src_v = vals;
   K* dst_k = keys_alt;

@@ -153,6 +153,9 @@ class PreprocessOptions(ctypes.Structure):
       ("has_variable_weights", ctypes.c_int32),
       ("coo_buffer_size_per_device", ctypes.c_int64),
       ("col_id_bound", ctypes.c_int64),
+      ("build_sample_view", ctypes.c_int32),
+      ("reserved", ctypes.c_int32),
+      ("table_rows", ctypes.c_int64),
   ]
 
 
@@ -163,6 +166,8 @@ class PreprocessOutput(ctypes.Structure):
       ("sample_ids", ctypes.c_void_p),
       ("gains", ctypes.c_void_p),
       ("stats", ctypes.c_void_p),
+      ("view_keys", ctypes.c_void_p),
+      ("view_entries", ctypes.c_void_p),
   ]
 
 

@@ -265,8 +265,11 @@ def _to_device_feature(feature, weights) -> _DeviceFeature:
 
 def _preprocess_stack(feats, metas, *, local_device_count,
                       global_device_count, num_sc_per_device,
-                      allow_id_dropping, has_weights):
-  """Runs one stacked table; returns (rp, eid, sid, gains, stats_np)."""
+                      allow_id_dropping, has_weights, build_view=False):
+  """Enqueues one stacked table; returns (rp, eid, sid, gains, stats on the
+  device, (L, S, NS, counters offset), view) where view is the
+  (keys, entries) pair of the CSR's sample view when `build_view`, else
+  None."""
   t = _native.require_gpu()
   lib = _native.load_library()
   dev = _native.device()
@@ -280,7 +283,9 @@ def _preprocess_stack(feats, metas, *, local_device_count,
       local_device_count, global_device_count, num_sc_per_device,
       _COMBINERS.get(metas[0].row_combiner, 0),
       metas[0].max_ids_per_partition, metas[0].max_unique_ids_per_partition,
-      int(bool(allow_id_dropping)), int(bool(has_weights)), c, bound)
+      int(bool(allow_id_dropping)), int(bool(has_weights)), c, bound,
+      int(bool(build_view)), 0,
+      metas[0].stack_vocab_size // global_device_count)
   structs = (_native.Feature * len(feats))()
   for i, (f, m) in enumerate(zip(feats, metas)):
     structs[i] = _native.Feature(
@@ -299,15 +304,20 @@ def _preprocess_stack(feats, metas, *, local_device_count,
   gains = t.empty(L * c, dtype=t.float32, device=dev)
   nstats = lib.scemb_preprocess_stats_size(ctypes.byref(opts))
   stats = t.zeros(nstats + 2, dtype=t.int32, device=dev)
-  out = _native.PreprocessOutput(_native.ptr(rp), _native.ptr(eid),
-                                 _native.ptr(sid), _native.ptr(gains),
-                                 _native.ptr(stats))
+  view = None
+  if build_view:
+    view = (t.empty(c, dtype=t.int32, device=dev),
+            t.empty(c, dtype=t.int64, device=dev))
+  out = _native.PreprocessOutput(
+      _native.ptr(rp), _native.ptr(eid), _native.ptr(sid), _native.ptr(gains),
+      _native.ptr(stats), None if view is None else _native.ptr(view[0]),
+      None if view is None else _native.ptr(view[1]))
   _native.check(lib.scemb_preprocess_stacked_table(
       structs, len(feats), ctypes.byref(opts), ctypes.byref(out),
       _native.ptr(ws), ws.numel(), _native.stream_handle()))
   off = int(lib.scemb_preprocess_stats_counters_offset(ctypes.byref(opts)))
   # The stats stay on the device until every stack has been enqueued.
-  return rp, eid, sid, gains, stats, (L, S, ns, off)
+  return rp, eid, sid, gains, stats, (L, S, ns, off), view
 
 
 def preprocess_sparse_dense_matmul_input(
@@ -369,13 +379,18 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
                           local_device_count: int, global_device_count: int,
                           *, num_sc_per_device: int,
                           has_leading_dimension: bool = False,
-                          allow_id_dropping: bool = False):
+                          allow_id_dropping: bool = False,
+                          sample_views: dict | None = None):
   """Enqueues the preprocessing of every stack on the current stream without
   waiting for it. Returns the CSR dicts and the pending stats, which
-  collect_stats turns into a SparseDenseMatmulInputStats (one wait)."""
+  collect_stats turns into a SparseDenseMatmulInputStats (one wait). With a
+  `sample_views` dict (one local and one global device only), each stack's
+  sample view (keys, entries) is built along and stored there."""
   stacks = get_stacked_table_metadata(feature_specs)
   rps, eids, sids, gns = {}, {}, {}, {}
   pending = []
+  build_view = (sample_views is not None and local_device_count == 1 and
+                global_device_count == 1)
   for name, metas in stacks.items():
     feats = [
         _to_device_feature(
@@ -383,12 +398,14 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
             None if feature_weights is None else
             feature_weights[m.feature_index]) for m in metas
     ]
-    rp, eid, sid, gains, stats_dev, (L, S, ns, off) = _preprocess_stack(
+    rp, eid, sid, gains, stats_dev, (L, S, ns, off), view = _preprocess_stack(
         feats, metas, local_device_count=local_device_count,
         global_device_count=global_device_count,
         num_sc_per_device=num_sc_per_device,
         allow_id_dropping=allow_id_dropping,
-        has_weights=feature_weights is not None)
+        has_weights=feature_weights is not None, build_view=build_view)
+    if view is not None:
+      sample_views[name] = view
     pending.append((name, stats_dev, L, S, ns, off, feats))
     if has_leading_dimension:
       rp, eid, sid, gains = (rp.reshape(L, -1), eid.reshape(L, -1),

@@ -306,16 +306,27 @@ def preprocess_sparse_dense_matmul_input(
       sharding_strategy_to_enum(sharding_strategy), enable_minibatching)
   # Everything is enqueued (CSR build, then the lookup views) before the one
   # wait for the stats.
+  built = {}
   *csr, pending = pybind_input_preprocessing.enqueue_preprocessing(
       feats, weights, specs, local_device_count, global_device_count,
       num_sc_per_device=num_sc_per_device,
       has_leading_dimension=has_leading_dimension,
-      allow_id_dropping=allow_id_dropping)
+      allow_id_dropping=allow_id_dropping, sample_views=built)
   views = None
-  one_per_row = pybind_input_preprocessing.one_id_per_row(pending)
   if local_device_count == 1:
-    views = _build_lookup_views(csr, feature_specs, global_device_count,
-                                num_sc_per_device, one_per_row)
+    # One device: the preprocessing wrote each stack's sample view along with
+    # its CSR; otherwise (several global devices) it is built from the CSR.
+    stacked = get_stacked_table_specs(feature_specs)
+    views = {
+        name: _native.LookupView(
+            keys, entries, stacked[name].total_sample_count,
+            stacked[name].stack_vocab_size)
+        for name, (keys, entries) in built.items()}
+    missing = [n for n in stacked if n not in views]
+    if missing:
+      views.update(_build_lookup_views(
+          csr, feature_specs, global_device_count, num_sc_per_device,
+          pybind_input_preprocessing.one_id_per_row(pending), only=missing))
   stats = pybind_input_preprocessing.collect_stats(pending)
   counts = None
   if local_device_count == 1:
@@ -367,12 +378,16 @@ def preprocess_sparse_dense_matmul_input_from_sparse_tensor(
 
 
 def _build_lookup_views(csr, feature_specs, global_device_count: int,
-                        num_sc_per_device: int, one_per_row: dict):
-  """Sample views of one device's CSR buffers, one per stacked table, for a
-  table shard of stack_vocab_size / global_device_count rows."""
+                        num_sc_per_device: int, one_per_row: dict,
+                        only=None):
+  """Sample views of one device's CSR buffers, one per stacked table (those
+  named in `only`, when given), for a table shard of
+  stack_vocab_size / global_device_count rows."""
   rp, eid, sid, gains = csr
   views = {}
   for name, spec in get_stacked_table_specs(feature_specs).items():
+    if only is not None and name not in only:
+      continue
     batch = spec.total_sample_count // global_device_count
     rows = spec.stack_vocab_size // global_device_count
     _, c = _device.csr_operands(rp[name], eid[name], sid[name], gains[name],

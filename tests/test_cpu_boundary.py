@@ -1,5 +1,6 @@
 """CPU checks of the C-ABI boundary and the host-side API (no GPU needed)."""
 
+import ctypes
 import os
 import re
 
@@ -106,3 +107,29 @@ def test_primitive_validation_messages():
     prim_utils.validate_abstract_eval_params(rp, ids, ids, gains, 1, table,
                                              grad, **ok, min_value=2.0,
                                              max_value=1.0)
+
+
+def _sizing_call(build_view, local_devices, table_rows=1024):
+  """scemb_preprocess_workspace_size for one 64 x 2 dense feature (sizing
+  only: no device memory is touched)."""
+  lib = _native.load_library()
+  feat = (_native.Feature * 1)()
+  feat[0] = _native.Feature(None, None, None, None, 64, 128, 2, 0, 0, 0)
+  opts = _native.PreprocessOptions(local_devices, local_devices, 1, 0, 512,
+                                   512, 0, 0, 512, 1024, int(build_view), 0,
+                                   table_rows)
+  return int(lib.scemb_preprocess_workspace_size(feat, 1, ctypes.byref(opts)))
+
+
+def test_preprocess_sample_view_option():
+  """build_sample_view adds the view temporaries to the workspace and is
+  refused for several devices or a table that does not split into
+  partitions (the options struct layout is read as the header declares)."""
+  plain = _sizing_call(False, 1)
+  with_view = _sizing_call(True, 1)
+  assert plain > 0 and with_view > plain
+  assert _sizing_call(True, 2) == 0
+  assert b"one local and one global device" in \
+      _native.load_library().scemb_last_error()
+  assert _sizing_call(True, 1, table_rows=0) == 0
+  assert _sizing_call(False, 2) > 0

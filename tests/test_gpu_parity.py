@@ -717,3 +717,56 @@ def test_shared_row_in_one_entry_per_row_csr_is_flagged():
   _native.build_sample_view(c, 8, 16, device_status=status)
   assert int(status.item()) & _native.STATUS_SHARED_ROW
   del keep
+
+
+@pytest.mark.parametrize("num_sc", [1, 2])
+@pytest.mark.parametrize("weighted", [False, True])
+def test_preprocessing_view_groups_like_the_csr_view(num_sc, weighted):
+  """The sample view the preprocessing writes along with the CSR holds, for
+  every activation row, the same entries as the view built from the CSR by
+  sorting (only their order inside a row may differ), with ids dropped by
+  the limits, duplicate ids merged and empty rows; the forward gives the
+  same activations bit for bit on integer data."""
+  rng = np.random.default_rng(23 + num_sc + (10 if weighted else 0))
+  batch = 256
+  tables, feats = _make_specs(2, [900, 4000], [8, 8], "sum",
+                              embedding_spec.SGDOptimizerSpec(0.01), batch,
+                              features_per_table=2)
+  _stack(feats, ["table_0", "table_1"], 1, num_sc, limit=48)
+  features = [_ragged(rng, batch, 0, 12, t.vocabulary_size, zipf_a=1.2)
+              for t in (tables[0], tables[0], tables[1], tables[1])]
+  weights = ([_weights_like(rng, f) for f in features] if weighted else None)
+  pre, stats = embedding.preprocess_sparse_dense_matmul_input(
+      features, weights, feats, 1, 1, num_sc_per_device=num_sc,
+      allow_id_dropping=True)
+  name = feats[0].table_spec.stacked_table_spec.stack_name
+  assert sum(stats.id_drop_counters.values()) > 0
+  spec = feats[0].table_spec.stacked_table_spec
+  bs, rows = spec.total_sample_count, spec.stack_vocab_size
+  got = pre.lookup_views[name]
+  keep, c = _device.csr_operands(pre.lhs_row_pointers[name],
+                                 pre.lhs_embedding_ids[name],
+                                 pre.lhs_sample_ids[name],
+                                 pre.lhs_gains[name], num_sc, num_sc)
+  exp = _native.build_sample_view(c, bs, rows)
+  torch.cuda.synchronize()
+  del keep
+  gk, ge = got.keys.cpu().numpy(), got.entries.cpu().numpy()
+  ek, ee = exp.keys.cpu().numpy(), exp.entries.cpu().numpy()
+  np.testing.assert_array_equal(gk, ek)
+  og, oe = np.lexsort((ge, gk)), np.lexsort((ee, ek))
+  np.testing.assert_array_equal(ge[og], ee[oe])
+  table = torch.from_numpy(
+      rng.integers(-4, 5, size=(rows, 8)).astype(np.float32)).cuda()
+  csr = (pre.lhs_row_pointers[name], pre.lhs_embedding_ids[name],
+         pre.lhs_sample_ids[name], pre.lhs_gains[name])
+  acts = []
+  for v in (got, exp):
+    acts.append(fwd_prim.tpu_sparse_dense_matmul_csr_primitive.bind(
+        *csr, 1, table, device_batch_size=bs, max_ids_per_partition=48,
+        max_unique_ids_per_partition=48, num_sc_per_device=num_sc,
+        lookup_view=v).cpu().numpy())
+  if weighted:
+    np.testing.assert_allclose(acts[0], acts[1], rtol=RTOL, atol=ATOL)
+  else:
+    np.testing.assert_array_equal(acts[0], acts[1])
