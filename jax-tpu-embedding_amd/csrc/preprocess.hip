@@ -165,15 +165,59 @@ __global__ __launch_bounds__(256) void ExtractIds(
     uint32_t* rows_out, float* gains_out, uint32_t* row_keys,
     int row_key_bits_seg_shift, int64_t* counters) {
   const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  // The block's first and last positions, and the rows holding them when
+  // both lie in one slice: every thread then searches only between those
+  // rows (a few steps) instead of over the whole slice.
+  __shared__ int64_t s_row_lo, s_row_hi;
+  __shared__ int s_slice;
+  if (threadIdx.x == 0) {
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * blockDim.x;
+    const int64_t last = min(first + blockDim.x, total_ids) - 1;
+    const int a = FindSlice(slices, num_slices, first, false);
+    const int z = FindSlice(slices, num_slices, last, false);
+    s_slice = a == z ? a : -1;
+    if (a == z) {
+      const SliceDesc sl = slices[a];
+      const FeatureDev f = feats[sl.feature];
+      int64_t lo = sl.row_start, hi = sl.row_start + sl.num_rows - 1;
+      if (f.splits != nullptr) {
+        const int64_t pf = sl.id_begin + (first - sl.out_begin);
+        const int64_t pl = sl.id_begin + (last - sl.out_begin);
+        int64_t l = lo, h = hi;
+        while (l < h) {
+          const int64_t mid = (l + h + 1) >> 1;
+          if (f.splits[mid] <= pf) l = mid; else h = mid - 1;
+        }
+        const int64_t row_first = l;
+        l = row_first;
+        h = hi;
+        while (l < h) {
+          const int64_t mid = (l + h + 1) >> 1;
+          if (f.splits[mid] <= pl) l = mid; else h = mid - 1;
+        }
+        lo = row_first;
+        hi = l;
+      }
+      s_row_lo = lo;
+      s_row_hi = hi;
+    }
+  }
+  __syncthreads();
   bool bad = false;
   if (o < total_ids) {
-    const SliceDesc sl = slices[FindSlice(slices, num_slices, o, false)];
+    const int si = s_slice >= 0 ? s_slice
+                                : FindSlice(slices, num_slices, o, false);
+    const SliceDesc sl = slices[si];
     const FeatureDev f = feats[sl.feature];
     const int64_t p = sl.id_begin + (o - sl.out_begin);  // input position
     int64_t r, b, e;
     if (f.splits != nullptr) {
       // Last row of the slice starting at or before p.
       int64_t lo = sl.row_start, hi = sl.row_start + sl.num_rows - 1;
+      if (s_slice >= 0) {
+        lo = s_row_lo;
+        hi = s_row_hi;
+      }
       while (lo < hi) {
         const int64_t mid = (lo + hi + 1) >> 1;
         if (f.splits[mid] <= p) lo = mid; else hi = mid - 1;
@@ -234,23 +278,31 @@ __global__ void FillI32(int32_t* p, int64_t n, int32_t v) {
   if (i < n) p[i] = v;
 }
 
-// Flags and partition boundaries over the sorted sequence.
+// Flags and partition boundaries over the sorted sequence. Each element's
+// row and gain are gathered once (sidx); the previous element's row comes
+// from the neighbouring thread through LDS (from memory at block starts).
 template <typename K>
 __global__ __launch_bounds__(256) void GroupFlags(
     const K* skeys, const uint32_t* sidx, const uint32_t* rows,
     const float* gains, int64_t n, KeyLayout kl, int num_partitions,
     uint32_t* srows, float* sgains, uint64_t* flags, int32_t* part_first,
     int32_t* part_last) {
+  __shared__ uint32_t s_row[256];
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const K key = skeys[i];
+  const K key = i < n ? skeys[i] : SentinelKey<K>();
   const bool valid = key != SentinelKey<K>();
-  uint64_t f = 0;
+  uint32_t row = 0;
   if (valid) {
     const uint32_t idx = sidx[i];
-    const uint32_t row = rows[idx];
+    row = rows[idx];
     srows[i] = row;
     sgains[i] = gains[idx];
+  }
+  s_row[threadIdx.x] = row;
+  __syncthreads();
+  if (i >= n) return;
+  uint64_t f = 0;
+  if (valid) {
     const K col_mask = kl.col_bits >= 64 ? ~K(0) : ((K(1) << kl.col_bits) - 1);
     uint32_t p, local;
     DecodeCol<K>(key & col_mask, kl, &p, &local);
@@ -262,7 +314,10 @@ __global__ __launch_bounds__(256) void GroupFlags(
       if (pk == key) {
         new_col = false;
         new_bucket = false;
-        new_run = rows[sidx[i - 1]] != row;
+        // Same key, so element i - 1 is valid and its row was loaded.
+        const uint32_t prev_row =
+            threadIdx.x > 0 ? s_row[threadIdx.x - 1] : rows[sidx[i - 1]];
+        new_run = prev_row != row;
       } else {
         uint32_t pp, pl;
         DecodeCol<K>(pk & col_mask, kl, &pp, &pl);
@@ -508,11 +563,11 @@ __global__ __launch_bounds__(256) void FillPlanKernel(
 // the extraction position of the run's first id (null: no view).
 struct ViewParts {
   const uint32_t* sidx;  // sorted position -> extraction position
-  uint32_t* mark;        // [M + 1] 1 where a written run starts
-  uint32_t* key;         // [M] activation row
-  uint64_t* entry;       // [M] table row | gain bits << 32
+  uint64_t* entry;       // [M] table row | gain bits << 32, or kNoEntry
+  uint32_t* pos;         // [M + 1] view positions (scan of entry != kNoEntry)
   int64_t rows_per_partition;
 };
+constexpr uint64_t kNoEntry = ~0ull;  // table rows stay below 2^32 - 1
 
 template <typename K>
 __global__ __launch_bounds__(256) void ScatterRuns(
@@ -540,28 +595,40 @@ __global__ __launch_bounds__(256) void ScatterRuns(
   eid[pos] = static_cast<int32_t>(local);
   sid[pos] = static_cast<int32_t>(srows[i0] % static_cast<uint32_t>(bps));
   gains[pos] = run_gain[r];
-  if (view.mark != nullptr && local < view.rows_per_partition) {
-    // One device: the activation row is the stacked sample id itself.
-    const uint32_t e0 = view.sidx[i0];
-    view.mark[e0] = 1;
-    view.key[e0] = srows[i0];
-    view.entry[e0] =
+  if (view.entry != nullptr && local < view.rows_per_partition) {
+    // One 8-byte store per run, at the run's first input position; the
+    // activation row (one device: the stacked sample id) is read back from
+    // the extraction-order rows when the view is compacted.
+    view.entry[view.sidx[i0]] =
         static_cast<uint64_t>(p * view.rows_per_partition + local) |
         (static_cast<uint64_t>(__float_as_uint(run_gain[r])) << 32);
   }
 }
 
+__global__ __launch_bounds__(256) void FillU64(uint64_t* p, int64_t n,
+                                               uint64_t v) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// 1 where a written run starts (input order), 0 elsewhere and at m.
+__global__ __launch_bounds__(256) void MarkEntries(const uint64_t* entry,
+                                                   int64_t m, uint32_t* mark) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i <= m) mark[i] = i < m && entry[i] != kNoEntry ? 1u : 0u;
+}
+
 // The sample view in extraction order, which is activation-row order: the
 // run starting at extraction position e goes to view position pos[e]
-// (exclusive scan of the marks); positions from pos[m] to n get the unused
-// key.
+// (exclusive scan of the marks) with key rows[e]; positions from pos[m] to
+// n get the unused key.
 __global__ __launch_bounds__(256) void ViewCompact(
-    const uint32_t* pos, const uint32_t* vkey, const uint64_t* ventry,
+    const uint32_t* pos, const uint32_t* rows, const uint64_t* ventry,
     int64_t m, int64_t n, uint32_t unused_key, uint32_t* keys,
     uint64_t* entries) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < m && pos[i + 1] > pos[i]) {
-    keys[pos[i]] = vkey[i];
+    keys[pos[i]] = rows[i];
     entries[pos[i]] = ventry[i];
   }
   if (i < n && i >= static_cast<int64_t>(pos[m])) {
@@ -880,9 +947,8 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
       return Fail(SCEMB_ERR_INVALID_ARGUMENT,
                   "table_rows must be a positive multiple of the partitions");
     }
-    view.mark = ws.Take<uint32_t>(M + 1);
-    view.key = ws.Take<uint32_t>(M);
     view.entry = ws.Take<uint64_t>(M);
+    view.pos = ws.Take<uint32_t>(M + 1);
     view.rows_per_partition = o->table_rows / pl.NS;
   }
   const bool measuring = ws.measuring();
@@ -896,7 +962,7 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
         out->gains == nullptr) {
       return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null output buffer");
     }
-    if (view.mark != nullptr &&
+    if (view.entry != nullptr &&
         (out->view_keys == nullptr || out->view_entries == nullptr)) {
       return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null sample view buffer");
     }
@@ -1024,7 +1090,7 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   if (st != 0) return st;
   if (measuring) {
     // The view's scan runs last; size its temporaries at the same point.
-    return view.mark != nullptr
+    return view.entry != nullptr
                ? ExclusiveScan<uint32_t>(nullptr, nullptr, M + 1, nullptr, ws,
                                          stream)
                : 0;
@@ -1050,11 +1116,10 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                      fp, out->row_pointers, b.plans, stat_max_ids,
                      stat_max_unique, stat_required, counters);
   SCEMB_LAUNCH_CHECK();
-  if (view.mark != nullptr) {
+  if (view.entry != nullptr && M > 0) {
     view.sidx = sidx;
-    hipLaunchKernelGGL(FillI32, dim3(CeilDiv(M + 1, 256)), dim3(256), 0,
-                       stream, reinterpret_cast<int32_t*>(view.mark), M + 1,
-                       0);
+    hipLaunchKernelGGL(FillU64, dim3(CeilDiv(M, 256)), dim3(256), 0, stream,
+                       view.entry, M, kNoEntry);
     SCEMB_LAUNCH_CHECK();
   }
   if (M > 0) {
@@ -1072,15 +1137,18 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                      dim3(256), 0, stream, b.plans, num_buckets, fp,
                      out->embedding_ids, out->sample_ids, out->gains);
   SCEMB_LAUNCH_CHECK();
-  if (view.mark != nullptr) {
-    st = ExclusiveScan<uint32_t>(view.mark, view.mark, M + 1, nullptr, ws,
+  if (view.entry != nullptr) {
+    hipLaunchKernelGGL(MarkEntries, dim3(CeilDiv(M + 1, 256)), dim3(256), 0,
+                       stream, view.entry, M, view.pos);
+    SCEMB_LAUNCH_CHECK();
+    st = ExclusiveScan<uint32_t>(view.pos, view.pos, M + 1, nullptr, ws,
                                  stream);
     if (st != 0) return st;
     const int64_t n = pl.coo_size;
     const int64_t grid = M > n ? M : n;
     if (grid > 0) {
       hipLaunchKernelGGL(ViewCompact, dim3(CeilDiv(grid, 256)), dim3(256), 0,
-                         stream, view.mark, view.key, view.entry, M, n,
+                         stream, view.pos, b.rows, view.entry, M, n,
                          static_cast<uint32_t>(pl.batch_for_device),
                          out->view_keys, out->view_entries);
       SCEMB_LAUNCH_CHECK();
