@@ -165,48 +165,61 @@ __global__ __launch_bounds__(256) void ExtractIds(
     uint32_t* rows_out, float* gains_out, uint32_t* row_keys,
     int row_key_bits_seg_shift, int64_t* counters) {
   const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  // The block's first and last positions, and the rows holding them when
-  // both lie in one slice: every thread then searches only between those
-  // rows (a few steps) instead of over the whole slice.
-  __shared__ int64_t s_row_lo, s_row_hi;
-  __shared__ int s_slice;
+  // The block's first and last positions usually lie in one slice and a few
+  // rows: the block finds that slice and those rows together (a parallel
+  // scan of the slice table, then 256-way searches over the row splits), so
+  // that each thread only searches a handful of rows.
+  __shared__ int s_slice_first, s_slice_last, s_best;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * blockDim.x;
+  const int64_t last = min(first + static_cast<int64_t>(blockDim.x), total_ids) - 1;
   if (threadIdx.x == 0) {
-    const int64_t first = static_cast<int64_t>(blockIdx.x) * blockDim.x;
-    const int64_t last = min(first + blockDim.x, total_ids) - 1;
-    const int a = FindSlice(slices, num_slices, first, false);
-    const int z = FindSlice(slices, num_slices, last, false);
-    s_slice = a == z ? a : -1;
-    if (a == z) {
-      const SliceDesc sl = slices[a];
-      const FeatureDev f = feats[sl.feature];
-      int64_t lo = sl.row_start, hi = sl.row_start + sl.num_rows - 1;
-      if (f.splits != nullptr) {
-        const int64_t pf = sl.id_begin + (first - sl.out_begin);
-        const int64_t pl = sl.id_begin + (last - sl.out_begin);
-        int64_t l = lo, h = hi;
-        while (l < h) {
-          const int64_t mid = (l + h + 1) >> 1;
-          if (f.splits[mid] <= pf) l = mid; else h = mid - 1;
-        }
-        const int64_t row_first = l;
-        l = row_first;
-        h = hi;
-        while (l < h) {
-          const int64_t mid = (l + h + 1) >> 1;
-          if (f.splits[mid] <= pl) l = mid; else h = mid - 1;
-        }
-        lo = row_first;
-        hi = l;
-      }
-      s_row_lo = lo;
-      s_row_hi = hi;
-    }
+    s_slice_first = -1;
+    s_slice_last = -1;
   }
   __syncthreads();
+  for (int j = threadIdx.x; j < num_slices; j += blockDim.x) {
+    const int64_t b0 = slices[j].out_begin;
+    const int64_t b1 = j + 1 < num_slices ? slices[j + 1].out_begin : INT64_MAX;
+    if (b0 <= first && first < b1) s_slice_first = j;
+    if (b0 <= last && last < b1) s_slice_last = j;
+  }
+  __syncthreads();
+  const int block_slice = s_slice_first == s_slice_last ? s_slice_first : -1;
+  int64_t row_lo = 0, row_hi = -1;
+  if (block_slice >= 0) {
+    const SliceDesc sl = slices[block_slice];
+    const int64_t* splits = feats[sl.feature].splits;
+    if (splits != nullptr) {
+      int64_t bounds[2];
+      for (int k = 0; k < 2; ++k) {
+        const int64_t target =
+            sl.id_begin + ((k == 0 ? first : last) - sl.out_begin);
+        // Last row of the slice whose start is <= target; splits[lo] <=
+        // target holds throughout.
+        int64_t lo = k == 0 ? sl.row_start : bounds[0];
+        int64_t hi = sl.row_start + sl.num_rows - 1;
+        while (lo < hi) {
+          const int64_t step = (hi - lo + blockDim.x) / blockDim.x;
+          if (threadIdx.x == 0) s_best = 0;
+          __syncthreads();
+          const int64_t r = lo + static_cast<int64_t>(threadIdx.x) * step;
+          if (r <= hi && splits[r] <= target) atomicMax(&s_best, threadIdx.x);
+          __syncthreads();
+          const int64_t nlo = lo + static_cast<int64_t>(s_best) * step;
+          hi = min(nlo + step - 1, hi);
+          lo = nlo;
+          __syncthreads();
+        }
+        bounds[k] = lo;
+      }
+      row_lo = bounds[0];
+      row_hi = bounds[1];
+    }
+  }
   bool bad = false;
   if (o < total_ids) {
-    const int si = s_slice >= 0 ? s_slice
-                                : FindSlice(slices, num_slices, o, false);
+    const int si = block_slice >= 0 ? block_slice
+                                    : FindSlice(slices, num_slices, o, false);
     const SliceDesc sl = slices[si];
     const FeatureDev f = feats[sl.feature];
     const int64_t p = sl.id_begin + (o - sl.out_begin);  // input position
@@ -214,9 +227,9 @@ __global__ __launch_bounds__(256) void ExtractIds(
     if (f.splits != nullptr) {
       // Last row of the slice starting at or before p.
       int64_t lo = sl.row_start, hi = sl.row_start + sl.num_rows - 1;
-      if (s_slice >= 0) {
-        lo = s_row_lo;
-        hi = s_row_hi;
+      if (block_slice >= 0) {
+        lo = row_lo;
+        hi = row_hi;
       }
       while (lo < hi) {
         const int64_t mid = (lo + hi + 1) >> 1;
