@@ -24,6 +24,11 @@
  *   scemb_sparse_dense_matmul_grad_with_adagrad  the same custom call with
  *       the Adagrad update, lib/core/primitives/
  *       sparse_dense_matmul_grad_with_adagrad.py:235-275 (update fn :167-233)
+ *   scemb_sparse_dense_matmul_grad_with_optimizer  the same custom call for
+ *       every built-in optimizer (Adam, AdagradMomentum, FTRL, LaProp, F2A,
+ *       and SGD / Adagrad), lib/core/primitives/
+ *       sparse_dense_matmul_grad_with_{adam,adagrad_momentum,ftrl,laprop,
+ *       f2a}.py (each file's lowering and update function)
  *   scemb_preprocess_stacked_table         PreprocessSparseDenseMatmulInput
  *       for one stacked table, lib/core/input_preprocessing.h:62-68 /
  *       input_preprocessing.cc:800-959, as bound by

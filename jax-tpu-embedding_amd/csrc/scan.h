@@ -13,17 +13,12 @@ int ExclusiveScan(const T* in, T* out, int64_t n, T* total, Arena& ws,
                   hipStream_t stream);
 
 // Stable LSD radix sort of (key, value) pairs on key bits [begin_bit,
-// end_bit), 8 bits per pass, ping-ponging between (keys, vals) and
-// (keys_alt, vals_alt). *in_alt tells where the result ended up.
+// end_bit), in the fewest passes of at most 8 bits (digit widths balanced),
+// ping-ponging between (keys, vals) and (keys_alt, vals_alt). *in_alt tells
+// where the result ended up.
 template <typename K, typename V>
 int RadixSortPairs(K* keys, V* vals, K* keys_alt, V* vals_alt, int64_t n,
                    int begin_bit, int end_bit, Arena& ws, hipStream_t stream,
                    bool* in_alt);
-
-// Number of radix passes for a key span.
-inline int RadixPasses(int begin_bit, int end_bit) {
-  return end_bit > begin_bit ? static_cast<int>(CeilDiv(end_bit - begin_bit, 8))
-                             : 0;
-}
 
 }  // namespace scemb
