@@ -13,8 +13,8 @@ from the same feature specs as the product:
   grouped by ``setting_in_stack.stack_name`` and ordered by ``row_offset``.
 * ``preprocess`` follows ``PyPreprocessSparseDenseMatmulInput``
   (``pybind_input_preprocessing.cc:124-188``) and
-  ``PreprocessSparseDenseMatmulInput`` (``input_preprocessing.cc:800-959``)
-  without minibatching.
+  ``PreprocessSparseDenseMatmulInput`` (``input_preprocessing.cc:800-959``),
+  with minibatching on a single host.
 """
 
 from __future__ import annotations
@@ -83,18 +83,35 @@ def lib() -> ctypes.CDLL:
   l.ref_theoretical_max_coo_buffer_size.restype = i64
   l.ref_coo_buffer_size_per_device.argtypes = [i32, i64, i32, i32]
   l.ref_coo_buffer_size_per_device.restype = i64
+  l.ref_theoretical_max_coo_buffer_size_ex.argtypes = [i32, i32, i32, i32]
+  l.ref_theoretical_max_coo_buffer_size_ex.restype = i64
+  l.ref_coo_buffer_size_per_device_ex.argtypes = [i32, i64, i32, i32, i32]
+  l.ref_coo_buffer_size_per_device_ex.restype = i64
   l.ref_sparse_dense_matmul.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32,
-                                        vp, i64, i32, vp, i64, i32]
+                                        i32, vp, i64, i32, vp, i64, i32]
   l.ref_sparse_dense_matmul_grad.argtypes = [vp, vp, vp, vp, i64, i32, i32,
-                                             i32, vp, i64, vp, vp, i64, i32,
-                                             i32, f32, i32, f32, f32, i32]
+                                             i32, i32, vp, i64, vp, vp, i64,
+                                             i32, i32, f32, i32, f32, f32, i32]
   l.ref_sparse_dense_matmul_grad_optimizer.argtypes = [
-      vp, vp, vp, vp, i64, i32, i32, i32, vp, i64, vp, vp, vp, i64, i32, i32,
-      vp, i32, i32, f32, f32, i32]
+      vp, vp, vp, vp, i64, i32, i32, i32, i32, vp, i64, vp, vp, vp, i64, i32,
+      i32, vp, i32, i32, f32, f32, i32]
+  u32, u64 = ctypes.c_uint32, ctypes.c_uint64
+  l.ref_minibatching_bucket.argtypes = [i32]
+  l.ref_minibatching_bucket.restype = u32
+  l.ref_highway_hash64.argtypes = [vp, i64, vp]
+  l.ref_highway_hash64.restype = u64
+  l.ref_compute_minibatching_split.argtypes = [vp, i32, i32]
+  l.ref_compute_minibatching_split.restype = u64
+  l.ref_merge_buckets.argtypes = [u64, i32, vp]
+  l.ref_merge_partitioned.argtypes = [i32, vp, vp, vp, vp, i32, u64, vp]
+  l.ref_preprocess_stack_minibatching.argtypes = [
+      vp, i32, i32, i32, i32, i32, i32, i32, i32, i32, i64, i32, u64, vp, vp,
+      vp, vp, vp, vp, vp, vp, vp]
   for fn in ("ref_extract_slice", "ref_extract_device", "ref_sort_and_group",
              "ref_fill_device", "ref_preprocess_stack",
              "ref_sparse_dense_matmul", "ref_sparse_dense_matmul_grad",
-             "ref_sparse_dense_matmul_grad_optimizer"):
+             "ref_sparse_dense_matmul_grad_optimizer", "ref_merge_buckets",
+             "ref_merge_partitioned", "ref_preprocess_stack_minibatching"):
     getattr(l, fn).restype = i32
   _lib = l
   return l
@@ -123,6 +140,52 @@ def col_id_from_key(key, num_scs_bit) -> int:
 
 def data_from_key(key) -> int:
   return lib().ref_data_from_key(key)
+
+
+# Minibatching (coo_format.h:31-49, minibatching_splits_impl.h,
+# partitioned_coo_tensors.h:157-215).
+MAX_MINIBATCHING_BUCKETS = 64
+
+
+def highway_hash64(data: bytes, key) -> int:
+  buf = np.frombuffer(bytes(data), np.uint8) if data else np.zeros(1, np.uint8)
+  k = np.ascontiguousarray(np.asarray(key, np.uint64))
+  return int(lib().ref_highway_hash64(_p(buf), len(data), _p(k)))
+
+
+def minibatching_bucket(col_id) -> int:
+  return int(lib().ref_minibatching_bucket(int(col_id)))
+
+
+def compute_minibatching_split(values, max_value) -> tuple[int, np.ndarray]:
+  """ComputeMinibatchingSplit: (split bits, the values as it leaves them)."""
+  v = np.array(values, np.int32)
+  return int(lib().ref_compute_minibatching_split(_p(v), len(v),
+                                                  int(max_value))), v
+
+
+def merge_buckets(split, n) -> list[tuple[int, int]]:
+  """MergeBuckets<n>: the merged (left, right) bucket pairs in call order."""
+  pairs = np.zeros(2 * n, np.int32)
+  k = lib().ref_merge_buckets(int(split), int(n), _p(pairs))
+  return [(int(pairs[2 * i]), int(pairs[2 * i + 1])) for i in range(k)]
+
+
+def merge_partitioned(buckets, num_scs, split):
+  """PartitionedCooTensors::Merge<len(buckets)>: `buckets` is a list of
+  lists of (row, col, gain); returns the list of minibatches (lists of
+  (row, col, gain))."""
+  sizes = np.array([len(b) for b in buckets], np.int32)
+  flat = [c for b in buckets for c in b] or [(0, 0, 0.0)]
+  rows = np.array([c[0] for c in flat], np.int32)
+  cols = np.array([c[1] for c in flat], np.int32)
+  gains = np.array([c[2] for c in flat], np.float32)
+  offsets = np.zeros(len(buckets) + 1, np.int32)
+  n = lib().ref_merge_partitioned(len(buckets), _p(sizes), _p(rows), _p(cols),
+                                  _p(gains), int(num_scs), int(split),
+                                  _p(offsets))
+  return [[(int(rows[i]), int(cols[i]), float(gains[i]))
+           for i in range(offsets[m], offsets[m + 1])] for m in range(n)]
 
 
 @dataclasses.dataclass
@@ -353,17 +416,31 @@ class PreprocessResult:
   max_unique_ids_per_partition: dict
   required_buffer_sizes: dict
   dropped_id_count: dict
+  num_minibatches: int = 1
 
 
 def preprocess(features, features_weights, feature_specs, local_device_count,
                global_device_count, *, num_sc_per_device,
                has_leading_dimension=False, allow_id_dropping=False,
-               fill_value=0):
-  """CPU preprocessing of a list of features (no minibatching).
+               fill_value=0, enable_minibatching=False):
+  """CPU preprocessing of a list of features.
+
+  With `enable_minibatching` (single host), the passes of
+  PreprocessSparseDenseMatmulInput (input_preprocessing.cc:852-957): a first
+  pass over every stack; if one of them exceeds a limit, a bucket pass over
+  every stack whose splits are OR-ed into one, and a second fill with that
+  many minibatches. Row pointers then have 64 * S * max(NS, 8) entries per
+  device.
 
   Raises ValueError on invalid options and RuntimeError where the reference
   aborts (limits exceeded with dropping disabled).
   """
+  if enable_minibatching:
+    return _preprocess_minibatching(
+        features, features_weights, feature_specs, local_device_count,
+        global_device_count, num_sc_per_device=num_sc_per_device,
+        has_leading_dimension=has_leading_dimension,
+        allow_id_dropping=allow_id_dropping, fill_value=fill_value)
   L, G, S = local_device_count, global_device_count, num_sc_per_device
   if L <= 0 or G <= 0 or S <= 0 or G < L:
     raise ValueError("invalid device counts")
@@ -426,6 +503,93 @@ def preprocess(features, features_weights, feature_specs, local_device_count,
   return res
 
 
+def _preprocess_minibatching(features, features_weights, feature_specs,
+                             local_device_count, global_device_count, *,
+                             num_sc_per_device, has_leading_dimension,
+                             allow_id_dropping, fill_value):
+  L, G, S = local_device_count, global_device_count, num_sc_per_device
+  if L <= 0 or G <= 0 or S <= 0 or G < L:
+    raise ValueError("invalid device counts")
+  ns = S * G
+  if ns & (ns - 1):
+    raise ValueError(f"Total number of SparseCores ({ns}) must be a power of 2.")
+  rpb = max(ns, 8)
+  stacks = stacked_table_metadata(feature_specs)
+  has_w = features_weights is not None
+  res = PreprocessResult({}, {}, {}, {}, {}, {}, {}, {})
+  state = {}
+  for stack_name, metas in stacks.items():
+    ragged = []
+    for m in metas:
+      w = None if features_weights is None else \
+          features_weights[m.feature_index]
+      ragged.append(ragged_from_array(features[m.feature_index], w,
+                                      row_offset=m.row_offset,
+                                      col_offset=m.col_offset,
+                                      col_shift=m.col_shift))
+    c = lib().ref_coo_buffer_size_per_device_ex(
+        metas[0].max_ids_per_partition,
+        metas[0].suggested_coo_buffer_size_per_device or 0, G, S, 1)
+    if c < 0:
+      raise RuntimeError("Suggested Coo Buffer Size is larger than the "
+                         "theoretical max")
+    structs = (RefFeature * len(ragged))(*[f.as_struct() for f in ragged])
+    bufs = dict(
+        rp=np.full(L * S * MAX_MINIBATCHING_BUCKETS * rpb, fill_value,
+                   np.int32),
+        eid=np.full(L * c, fill_value, np.int32),
+        sid=np.full(L * c, fill_value, np.int32),
+        gains=np.full(L * c, fill_value, np.float32),
+        max_ids=np.zeros(L * ns, np.int32),
+        max_unique=np.zeros(L * ns, np.int32),
+        required=np.zeros(L * S, np.int32))
+    state[stack_name] = (metas, ragged, structs, c, bufs)
+
+  def run(stack_name, stage, split=0):
+    metas, ragged, structs, c, b = state[stack_name]
+    dropped = ctypes.c_int64(0)
+    flag = ctypes.c_uint64(0)
+    st = lib().ref_preprocess_stack_minibatching(
+        structs, len(ragged), L, G, S, COMBINERS[metas[0].combiner],
+        int(has_w), metas[0].max_ids_per_partition,
+        metas[0].max_unique_ids_per_partition, int(allow_id_dropping), c,
+        stage, split, _p(b["rp"]), _p(b["eid"]), _p(b["sid"]),
+        _p(b["gains"]), _p(b["max_ids"]), _p(b["max_unique"]),
+        _p(b["required"]), ctypes.byref(dropped), ctypes.byref(flag))
+    if st == 1:
+      raise ValueError("batch size not divisible by num_sc_per_device")
+    if st == 2:
+      raise RuntimeError(f"Observed max ids per partition exceeds the limit "
+                         f"for table: {stack_name}")
+    return int(dropped.value), int(flag.value)
+
+  dropped, required = {}, False
+  for name in state:
+    dropped[name], flag = run(name, 0)
+    required = required or flag != 0
+  split = 0
+  if required:
+    for name in state:
+      split |= run(name, 1)[1]
+    for name in state:
+      dropped[name] = run(name, 2, split)[0]
+  res.num_minibatches = bin(split).count("1") + 1
+  for name, (metas, ragged, structs, c, b) in state.items():
+    rp, eid, sid, gains = b["rp"], b["eid"], b["sid"], b["gains"]
+    if has_leading_dimension:
+      rp, eid, sid, gains = (rp.reshape(L, -1), eid.reshape(L, -1),
+                             sid.reshape(L, -1), gains.reshape(L, -1))
+    res.row_pointers[name] = rp
+    res.embedding_ids[name] = eid
+    res.sample_ids[name] = sid
+    res.gains[name] = gains
+    res.max_ids_per_partition[name] = b["max_ids"]
+    res.max_unique_ids_per_partition[name] = b["max_unique"]
+    res.required_buffer_sizes[name] = b["required"]
+    res.dropped_id_count[name] = dropped[name]
+  return res
+
+
 # ---------------------------------------------------------------------------
 # Lookup and update oracle.
 # ---------------------------------------------------------------------------
@@ -435,9 +599,19 @@ def _threads(threads):
   return threads if threads else min(16, os.cpu_count() or 1)
 
 
+def _rp_per_segment(rp, num_sc_per_device, num_minibatches):
+  if num_minibatches:
+    return len(rp) // (num_sc_per_device * MAX_MINIBATCHING_BUCKETS)
+  return len(rp) // num_sc_per_device
+
+
 def sparse_dense_matmul(rp, eid, sid, gains, table, batch, *,
-                        num_sc_per_device, num_scs, threads=None):
-  """Forward: activations[batch, dim] (or [batch] for a 1-D table)."""
+                        num_sc_per_device, num_scs, threads=None,
+                        num_minibatches=0):
+  """Forward: activations[batch, dim] (or [batch] for a 1-D table).
+
+  num_minibatches > 0: the CSR is in the minibatching layout (row pointers
+  of 64 * num_sc_per_device blocks, positions in the whole buffer)."""
   table = np.ascontiguousarray(table, np.float32)
   dim = 1 if table.ndim == 1 else table.shape[1]
   act = np.zeros((batch, dim), np.float32)
@@ -447,7 +621,9 @@ def sparse_dense_matmul(rp, eid, sid, gains, table, batch, *,
                          np.ascontiguousarray(gains, np.float32).reshape(-1))
   lib().ref_sparse_dense_matmul(_p(rp), _p(eid), _p(sid), _p(gains), len(eid),
                                 num_sc_per_device, num_scs,
-                                len(rp) // num_sc_per_device, _p(table),
+                                _rp_per_segment(rp, num_sc_per_device,
+                                                num_minibatches),
+                                int(num_minibatches), _p(table),
                                 table.shape[0], dim, _p(act), batch,
                                 _threads(threads))
   return act.reshape(batch) if table.ndim == 1 else act
@@ -456,7 +632,8 @@ def sparse_dense_matmul(rp, eid, sid, gains, table, batch, *,
 def sparse_dense_matmul_grad(rp, eid, sid, gains, act_grad, table,
                              accumulator=None, *, learning_rate,
                              num_sc_per_device, num_scs, min_value=None,
-                             max_value=None, threads=None, inplace=False):
+                             max_value=None, threads=None, inplace=False,
+                             num_minibatches=0):
   """Backward + SGD (accumulator None) or Adagrad.
 
   Returns updated copies, or updates `table` / `accumulator` (C-contiguous
@@ -480,8 +657,8 @@ def sparse_dense_matmul_grad(rp, eid, sid, gains, act_grad, table,
                                                  else 0)
   lib().ref_sparse_dense_matmul_grad(
       _p(rp), _p(eid), _p(sid), _p(gains), len(eid), num_sc_per_device,
-      num_scs, len(rp) // num_sc_per_device, _p(act_grad), batch, _p(table),
-      _p(acc), table.shape[0], dim, 0 if acc is None else 1,
+      num_scs, _rp_per_segment(rp, num_sc_per_device, num_minibatches),
+      int(num_minibatches), _p(act_grad), batch, _p(table), _p(acc), table.shape[0], dim, 0 if acc is None else 1,
       float(learning_rate), clip,
       float(min_value if min_value is not None else 0.0),
       float(max_value if max_value is not None else 0.0), _threads(threads))
@@ -500,7 +677,7 @@ def sparse_dense_matmul_grad_optimizer(rp, eid, sid, gains, act_grad, table,
                                        hyperparameters, num_sc_per_device,
                                        num_scs, multiply_linear_by_lr=False,
                                        min_value=None, max_value=None,
-                                       threads=None):
+                                       threads=None, num_minibatches=0):
   """Backward + any optimizer (`optimizer` a key of OPTIMIZERS), on copies.
 
   `slots` in the order of the optimizer's slot variables, `hyperparameters`
@@ -525,7 +702,8 @@ def sparse_dense_matmul_grad_optimizer(rp, eid, sid, gains, act_grad, table,
                                                  else 0)
   lib().ref_sparse_dense_matmul_grad_optimizer(
       _p(rp), _p(eid), _p(sid), _p(gains), len(eid), num_sc_per_device,
-      num_scs, len(rp) // num_sc_per_device, _p(act_grad), batch, _p(table),
+      num_scs, _rp_per_segment(rp, num_sc_per_device, num_minibatches),
+      int(num_minibatches), _p(act_grad), batch, _p(table),
       _p(slots[0]) if n_slots > 0 else None,
       _p(slots[1]) if n_slots > 1 else None, table.shape[0], dim,
       OPTIMIZERS[optimizer], _p(hp), 1 if multiply_linear_by_lr else 0, clip,
