@@ -79,9 +79,19 @@ int scemb_version(void);
  * lib/core/input_preprocessing_util.cc:167-208). For local SparseCore s and
  * partition p, entries j in [roundup8(rp[s*R + p - 1]) (0 for p = 0),
  * rp[s*R + p]) of segment s (positions s*coo_size/num_segments + j) hold
- * (embedding id, sample id, gain). */
+ * (embedding id, sample id, gain).
+ *
+ * With num_minibatches > 0 the buffers are in the minibatching layout
+ * (enable_minibatching; input_preprocessing_util.cc:135-143, :331-473, the
+ * operands of "SparseDenseMatmulWithMinibatchingOp",
+ * primitives/sparse_dense_matmul_csr.py:171-192): segment s holds
+ * num_minibatches blocks of R row pointers (block b = s * num_minibatches +
+ * m at rp[b*R]), row pointers are positions in the whole buffer, and each
+ * partition's entries start at the aligned end of the partition before it
+ * in buffer order (the first at 0). */
 typedef struct scemb_csr {
-  const int32_t* row_pointers;  /* [num_segments * row_pointers_per_segment] */
+  const int32_t* row_pointers;  /* [num_segments * row_pointers_per_segment]
+                                   (times num_minibatches when > 0) */
   const int32_t* embedding_ids; /* [coo_size] */
   const int32_t* sample_ids;    /* [coo_size] */
   const float* gains;           /* [coo_size] */
@@ -93,6 +103,9 @@ typedef struct scemb_csr {
   int64_t num_entries; /* valid entries if known (> 0), else 0: only picks
                           kernel variants (about one entry per activation
                           row or more); the buffer size stands in when 0 */
+  int32_t num_minibatches; /* 0: one block per segment (no minibatching);
+                              1..64: the minibatching layout */
+  int32_t reserved;
 } scemb_csr_t;
 
 /* The entries of each segment are ascending by (partition, embedding id), as
@@ -339,16 +352,35 @@ typedef struct scemb_preprocess_options {
    * num_partitions rows per partition) are left out, as the forward skips
    * them. */
   int32_t build_sample_view;
-  int32_t reserved;
+  /* Minibatching (PreprocessSparseDenseMatmulInputOptions.enable_minibatching,
+   * input_preprocessing_util.h:472; single host). One call per pass and
+   * stack, in the order of input_preprocessing.cc:852-929:
+   *   pass 0  the first pass over every stack: the stats (which stay those of
+   *           the call), the CSR of one minibatch, and counter 4 = 1 when a
+   *           partition exceeds a limit (no id is dropped in this pass);
+   *   pass 1  only if some stack set counter 4: the bucket pass, counter 5 =
+   *           this stack's split of the 64 buckets (OR it over all stacks);
+   *   pass 2  the bucket pass writing popcount(split) + 1 minibatches, with
+   *           minibatching_split = that OR; counter 0 = its dropped ids.
+   * Row pointers then take 64 * S * max(NS, 8) entries per device (the first
+   * S * minibatches * max(NS, 8) written) and hold device positions; the
+   * buffer size bound is 64 times larger (scemb_compute_*). */
+  int32_t enable_minibatching;
   int64_t table_rows; /* rows of the device's table, for the sample view */
+  int32_t minibatching_pass;
+  int32_t reserved;
+  uint64_t minibatching_split; /* pass 2: bit i set = tree node i split
+                                  (MinibatchingSplit, input_preprocessing_
+                                  util.h:94) */
 } scemb_preprocess_options_t;
 
 /* Device outputs. The stats block is int32 laid out as
  *   [L*NS] max_ids_per_partition, [L*NS] max_unique_ids_per_partition,
- *   [L*S] required_buffer_size, then 4 int64 counters (8-byte aligned by the
- *   caller): dropped_id_count, limit_exceeded, bad_ids, total_entries. */
+ *   [L*S] required_buffer_size, then 6 int64 counters (8-byte aligned by the
+ *   caller): dropped_id_count, limit_exceeded, bad_ids, total_entries,
+ *   minibatching_required (pass 0), minibatching_split (pass 1). */
 typedef struct scemb_preprocess_output {
-  int32_t* row_pointers;  /* [L * S * max(NS, 8)] */
+  int32_t* row_pointers;  /* [L * S * max(NS, 8)] (times 64, minibatching) */
   int32_t* embedding_ids; /* [L * coo_buffer_size_per_device] */
   int32_t* sample_ids;    /* [L * coo_buffer_size_per_device] */
   float* gains;           /* [L * coo_buffer_size_per_device] */
@@ -383,18 +415,21 @@ int scemb_profile_collect(const char* name, double* total_ms,
                           int64_t* launches);
 
 /* ---- Size helpers (host only) -----------------------------------------
- * ComputeTheoreticalMaxCooBufferSize (input_preprocessing_util.cc:223-240),
- * ComputeCooBufferSizePerDevice without minibatching (:256-312; returns -1
- * when the suggestion exceeds the theoretical maximum), and
- * GetRowPointersSizePerDevice (input_preprocessing_util.h:497-511). */
+ * ComputeTheoreticalMaxCooBufferSize (input_preprocessing_util.cc:244-255),
+ * ComputeCooBufferSizePerDevice (:256-312; returns -1 when the suggestion
+ * exceeds the theoretical maximum), and GetRowPointersSizePerDevice
+ * (input_preprocessing_util.h:497-511), as bound with their
+ * enable_minibatching argument at pybind_input_preprocessing.cc:218-244. */
 int64_t scemb_compute_theoretical_max_coo_buffer_size(
     int32_t max_ids_per_partition, int32_t global_device_count,
-    int32_t num_sc_per_device);
+    int32_t num_sc_per_device, int32_t enable_minibatching);
 int64_t scemb_compute_coo_buffer_size_per_device(
     int32_t max_ids_per_partition, int64_t suggested_coo_buffer_size,
-    int32_t global_device_count, int32_t num_sc_per_device);
+    int32_t global_device_count, int32_t num_sc_per_device,
+    int32_t enable_minibatching);
 int32_t scemb_compute_row_pointers_size_per_device(int32_t global_device_count,
-                                                   int32_t num_sc_per_device);
+                                                   int32_t num_sc_per_device,
+                                                   int32_t enable_minibatching);
 
 #ifdef __cplusplus
 }

@@ -11,6 +11,9 @@ namespace scemb {
 
 constexpr int kWave = 64;
 constexpr int kAlign = 8;  // CSR partition alignment (8 elements).
+// Minibatching buckets per SparseCore, and so the most minibatches
+// (coo_format.h:52-53).
+constexpr int kMaxMinibatches = 64;
 constexpr int32_t kPadInt = 0x7fffffff;
 constexpr uint32_t kNanBits = 0x7fc00000u;  // std::nanf("")
 

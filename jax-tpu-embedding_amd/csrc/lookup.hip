@@ -20,13 +20,11 @@ __global__ __launch_bounds__(256) void SlotByRow(Csr csr, int64_t bps,
                                                  uint32_t* count,
                                                  uint64_t* slot,
                                                  uint32_t* status) {
-  const int64_t n = csr.per_segment * csr.num_segments;
+  const int64_t n = CsrPositions(csr);
   const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (j >= n) return;
-  const int s = static_cast<int>(j / csr.per_segment);
-  const int64_t off = j - static_cast<int64_t>(s) * csr.per_segment;
-  const int p = PartitionOf(csr.rp + static_cast<int64_t>(s) * csr.rp_per_segment,
-                            csr.num_partitions, csr.per_segment, off);
+  int s = 0;
+  const int p = LocateEntry(csr, j, &s);
   if (p < 0) return;
   const int32_t e = csr.eid[j];
   const int32_t sm = csr.sid[j];

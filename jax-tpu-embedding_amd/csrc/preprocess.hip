@@ -1,6 +1,17 @@
 // GPU preprocessing of one stacked table: the reference's
 // PreprocessSparseDenseMatmulInput (jax_tpu_embedding/sparsecore/lib/core/
-// input_preprocessing.cc:800-959) without minibatching, bit-exact.
+// input_preprocessing.cc:800-959), bit-exact, including single-host
+// minibatching as one call per pass:
+//   pass 0   the first pass (no buckets, nothing dropped): stats, the CSR of
+//            one minibatch, and whether a partition exceeds a limit
+//   pass 1   the bucket pass: keys carry the column's HighwayHash bucket
+//            (coo_format.h:140-185); per (SC, partition) the bucket counts
+//            give the split of the 64-bucket tree
+//            (sort_and_group_coo_tensors_impl.h:116-151)
+//   pass 2   the bucket pass again, written as the minibatches of the
+//            split that every stack's pass 1 OR-ed together
+//            (partitioned_coo_tensors.h:157-215,
+//            input_preprocessing_util.cc:331-473)
 //
 // Stages (segment g = local_device * S + local_sc):
 //   plan      (host)  split-then-stack slices, input_preprocessing.cc:312-436
@@ -37,6 +48,10 @@ namespace scemb {
 namespace {
 
 constexpr uint32_t kDataMask26 = (1u << 26) - 1;
+// int64 counters after the stats: dropped ids, limit exceeded, bad ids,
+// grouped entries, minibatching required (pass 0), minibatching split
+// (pass 1).
+constexpr int kNumCounters = 6;
 
 struct SliceDesc {
   int64_t id_begin;
@@ -67,8 +82,83 @@ struct KeyLayout {
   int local_bits;   // compact: bits of the local id
   int col_bits;     // bits of the column part of the key
   int seg_bits;
+  int mb_bits;      // bucket bits between segment and column (0 or 6)
   int64_t col_bound;
 };
+
+// ---------------------------------------------------------------------------
+// Minibatching bucket of a column id: HighwayHash-64 of the id's 4 bytes
+// under the reference's fixed key, modulo 64 (coo_format.h:31-49, :140-145).
+// HighwayHash (google/highwayhash): four 64-bit lanes each of v0, v1, mul0,
+// mul1; a 4-byte input is one remainder packet (length folded into v0, the
+// 32-bit halves of v1 rotated by the length, the bytes at the packet's
+// start), then four permute-and-update rounds.
+// ---------------------------------------------------------------------------
+
+struct HhLanes {
+  uint64_t v0[4], v1[4], mul0[4], mul1[4];
+};
+
+__device__ __forceinline__ void HhZipperAdd(uint64_t v1, uint64_t v0,
+                                            uint64_t& add1, uint64_t& add0) {
+  add0 += (((v0 & 0xff000000ull) | (v1 & 0xff00000000ull)) >> 24) |
+          (((v0 & 0xff0000000000ull) | (v1 & 0xff000000000000ull)) >> 16) |
+          (v0 & 0xff0000ull) | ((v0 & 0xff00ull) << 32) |
+          ((v1 & 0xff00000000000000ull) >> 8) | (v0 << 56);
+  add1 += (((v1 & 0xff000000ull) | (v0 & 0xff00000000ull)) >> 24) |
+          (v1 & 0xff0000ull) | ((v1 & 0xff0000000000ull) >> 16) |
+          ((v1 & 0xff00ull) << 24) | ((v0 & 0xff000000000000ull) >> 8) |
+          ((v1 & 0xffull) << 48) | (v0 & 0xff00000000000000ull);
+}
+
+__device__ __forceinline__ void HhRound(HhLanes& h, const uint64_t (&in)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h.v1[i] += h.mul0[i] + in[i];
+    h.mul0[i] ^= (h.v1[i] & 0xffffffffull) * (h.v0[i] >> 32);
+    h.v0[i] += h.mul1[i];
+    h.mul1[i] ^= (h.v0[i] & 0xffffffffull) * (h.v1[i] >> 32);
+  }
+  HhZipperAdd(h.v1[1], h.v1[0], h.v0[1], h.v0[0]);
+  HhZipperAdd(h.v1[3], h.v1[2], h.v0[3], h.v0[2]);
+  HhZipperAdd(h.v0[1], h.v0[0], h.v1[1], h.v1[0]);
+  HhZipperAdd(h.v0[3], h.v0[2], h.v1[3], h.v1[2]);
+}
+
+__device__ __forceinline__ uint32_t MinibatchingBucket(uint32_t col) {
+  constexpr uint64_t kKey[4] = {0x4451e30f87db9609ull, 0xca7358a1fd2737f8ull,
+                                0x4b2c991fcee4fdeaull, 0x0b2658e18326f6baull};
+  constexpr uint64_t kInit0[4] = {0xdbe6d5d5fe4cce2full, 0xa4093822299f31d0ull,
+                                  0x13198a2e03707344ull, 0x243f6a8885a308d3ull};
+  constexpr uint64_t kInit1[4] = {0x3bd39e10cb0ef593ull, 0xc0acf169b5f18a8cull,
+                                  0xbe5466cf34e90c6cull, 0x452821e638d01377ull};
+  HhLanes h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h.mul0[i] = kInit0[i];
+    h.mul1[i] = kInit1[i];
+    h.v0[i] = kInit0[i] ^ kKey[i];
+    h.v1[i] = kInit1[i] ^ ((kKey[i] >> 32) | (kKey[i] << 32));
+    // Remainder of 4 bytes.
+    h.v0[i] += (uint64_t{4} << 32) + 4;
+    const uint32_t lo = static_cast<uint32_t>(h.v1[i]);
+    const uint32_t hi = static_cast<uint32_t>(h.v1[i] >> 32);
+    h.v1[i] = static_cast<uint64_t>((lo << 4) | (lo >> 28)) |
+              (static_cast<uint64_t>((hi << 4) | (hi >> 28)) << 32);
+  }
+  uint64_t packet[4] = {static_cast<uint64_t>(col), 0, 0, 0};
+  HhRound(h, packet);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint64_t perm[4] = {(h.v0[2] >> 32) | (h.v0[2] << 32),
+                              (h.v0[3] >> 32) | (h.v0[3] << 32),
+                              (h.v0[0] >> 32) | (h.v0[0] << 32),
+                              (h.v0[1] >> 32) | (h.v0[1] << 32)};
+    HhRound(h, perm);
+  }
+  return static_cast<uint32_t>((h.v0[0] + h.v1[0] + h.mul0[0] + h.mul1[0]) &
+                               (kMaxMinibatches - 1));
+}
 
 __device__ __forceinline__ uint32_t Rotr32(uint32_t x, int s) {
   return s == 0 ? x : ((x >> s) | (x << (32 - s)));
@@ -260,7 +350,12 @@ __global__ __launch_bounds__(256) void ExtractIds(
                         f.col_offset;
     const bool ok = id >= 0 && col >= 0 &&
                     (kl.col_bound <= 0 || static_cast<int64_t>(col) < kl.col_bound);
-    const K seg_part = static_cast<K>(sl.segment) << kl.col_bits;
+    K vseg = static_cast<K>(sl.segment);
+    if (kl.mb_bits > 0) {
+      vseg = (vseg << kl.mb_bits) |
+             static_cast<K>(MinibatchingBucket(static_cast<uint32_t>(col)));
+    }
+    const K seg_part = vseg << kl.col_bits;
     keys[o] = ok ? (seg_part | ColKey<K>(static_cast<uint32_t>(col), kl))
                  : SentinelKey<K>();
     vals[o] = static_cast<uint32_t>(o);
@@ -472,6 +567,10 @@ struct FillParams {
   int32_t max_ids;
   int32_t max_unique;
   int32_t allow_dropping;
+  int32_t mb_bits;          // bucket bits of the key (0 or 6)
+  int32_t absolute;         // padding positions are device positions
+  int32_t num_minibatches;  // minibatching layout: minibatches per SC
+  uint8_t minibatch_of[kMaxMinibatches];  // bucket -> minibatch
 };
 
 // One thread per segment replays FillBufferSegment over partition counts; a
@@ -572,6 +671,206 @@ __global__ __launch_bounds__(256) void FillPlanKernel(
   }
 }
 
+// The minibatching layout (input_preprocessing_util.cc:135-143, :331-473):
+// one thread per device replays FillBufferSegment over the (SC, minibatch)
+// segments in order. A segment's partition p takes the kept entries of
+// every bucket of the minibatch in bucket order (the partition-stable merge
+// of partitioned_coo_tensors.h:162-181); row pointers are device positions;
+// with one minibatch SC s starts at the summed required sizes of the SCs
+// before it, with several each segment starts where the previous ended.
+// Pass 0 (one bucket) also writes the stats and flags a partition over a
+// limit (minibatching required); pass 2 flags a bucket over a limit when
+// dropping is off (ValidateMaxIdsOrDie).
+__global__ __launch_bounds__(64) void FillPlanMinibatch(
+    const BucketStats* bstats, FillParams fp, int pass, int32_t* rp_out,
+    FillPlan* plans, int32_t* stat_max_ids, int32_t* stat_max_unique,
+    int32_t* stat_required, int64_t* counters) {
+  const int S = fp.segs_per_device;
+  const int NS = fp.num_partitions;
+  const int B = 1 << fp.mb_bits;
+  const int nmb = fp.num_minibatches;
+  const int RPB = fp.rp_per_segment;
+  const int64_t coo_size = fp.coo_size;
+  for (int d = threadIdx.x; d < fp.local_devices; d += blockDim.x) {
+    int32_t* rp = rp_out + static_cast<int64_t>(d) * S * kMaxMinibatches * RPB;
+    int64_t packed = 0, chained = 0, dropped = 0;
+    int rp_begin = 0;
+    bool required = false, over = false;
+    for (int s = 0; s < S; ++s) {
+      const int64_t g = static_cast<int64_t>(d) * S + s;
+      const BucketStats* bs = bstats + g * B * NS;  // [b][p]
+      FillPlan* pl = plans + g * B * NS;
+      int64_t req = 0;
+      for (int p = 0; p < NS; ++p) {
+        int64_t ids = 0;
+        for (int b = 0; b < B; ++b) {
+          const BucketStats& x = bs[b * NS + p];
+          ids += x.obs_ids;
+          if (x.obs_ids > fp.max_ids || x.obs_unique > fp.max_unique) {
+            over = true;
+          }
+          FillPlan& q = pl[b * NS + p];
+          q.start = 0;
+          q.fit = 0;
+          q.pad_begin = 0;
+          q.pad_end = 0;
+          q.pad_seg = static_cast<int32_t>(g);
+        }
+        req += (ids + kAlign - 1) / kAlign * kAlign;
+      }
+      if (pass == 0) {
+        stat_required[g] = static_cast<int32_t>(req);
+        required = required || over;
+      }
+      for (int m = 0; m < nmb; ++m) {
+        int64_t coo_begin;
+        if (nmb == 1) {
+          coo_begin = min(packed, coo_size);
+          packed = min(packed + req, coo_size);
+        } else {
+          coo_begin = chained;
+        }
+        const int64_t coo_end = coo_size;
+        int64_t total = 0;
+        for (int b = 0; b < B; ++b) {
+          if (fp.minibatch_of[b] != m) continue;
+          for (int p = 0; p < NS; ++p) total += bs[b * NS + p].kept;
+        }
+        int64_t coo = coo_begin, processed = 0;
+        int rpi = rp_begin;
+        const int rp_end = rp_begin + RPB;
+        int cur = 0;
+        auto valid = [&]() {
+          if (processed == total && coo == coo_end) return true;
+          if (rpi >= rp_end || coo >= coo_end) return false;
+          return true;
+        };
+        // The partition's padding is recorded with the minibatch's first
+        // bucket.
+        int first_b = 0;
+        while (first_b < B - 1 && fp.minibatch_of[first_b] != m) ++first_b;
+        auto advance = [&](int target) {
+          while (cur < target) {
+            if (!valid()) return;
+            rp[rpi++] = static_cast<int32_t>(coo);
+            int64_t nc = (coo + kAlign - 1) / kAlign * kAlign;
+            if (nc > coo_end) nc = coo_end;
+            FillPlan& q = pl[first_b * NS + cur];
+            q.pad_begin = static_cast<int32_t>(coo);
+            q.pad_end = static_cast<int32_t>(nc);
+            coo = nc;
+            ++cur;
+          }
+        };
+        for (int p = 0; p < NS; ++p) {
+          int64_t kp = 0;
+          for (int b = 0; b < B; ++b) {
+            if (fp.minibatch_of[b] == m) kp += bs[b * NS + p].kept;
+          }
+          if (kp == 0) continue;
+          advance(p);
+          if (!valid()) break;
+          const int64_t room = coo_end - coo;
+          const int64_t take = kp < room ? kp : room;
+          int64_t off = 0;
+          for (int b = 0; b < B; ++b) {
+            if (fp.minibatch_of[b] != m) continue;
+            const int64_t kb = bs[b * NS + p].kept;
+            FillPlan& q = pl[b * NS + p];
+            q.start = coo + off;
+            int64_t fit = take - off;
+            fit = fit < 0 ? 0 : (fit > kb ? kb : fit);
+            q.fit = static_cast<int32_t>(fit);
+            off += kb;
+          }
+          coo += take;
+          processed += take;
+          if (take < kp) break;
+        }
+        advance(NS);
+        while (rpi < rp_end) rp[rpi++] = static_cast<int32_t>(coo);
+        dropped += total - processed;
+        chained = coo;
+        rp_begin += RPB;
+      }
+    }
+    if (pass == 0 && required) {
+      atomicMax(reinterpret_cast<unsigned long long*>(&counters[4]), 1ull);
+    }
+    if (pass != 0 && over && !fp.allow_dropping) {
+      atomicMax(reinterpret_cast<unsigned long long*>(&counters[1]), 1ull);
+    }
+    if (dropped > 0) {
+      atomicAdd(reinterpret_cast<unsigned long long*>(&counters[0]),
+                static_cast<unsigned long long>(dropped));
+    }
+  }
+  if (pass != 0) return;
+  for (int dp = threadIdx.x; dp < fp.local_devices * NS; dp += blockDim.x) {
+    const int d = dp / NS, p = dp % NS;
+    int32_t mi = 0, mu = 0;
+    for (int s = 0; s < S; ++s) {
+      const BucketStats& b = bstats[static_cast<int64_t>(d * S + s) * NS + p];
+      mi = max(mi, b.obs_ids);
+      mu = max(mu, b.obs_unique);
+    }
+    stat_max_ids[dp] = mi;
+    stat_max_unique[dp] = mu;
+  }
+}
+
+// ComputeMinibatchingSplit (minibatching_splits_impl.h:58-81) over the 64
+// bucket values of v: bottom-up, a node whose children sum past the limit is
+// split and keeps the larger child, otherwise it keeps the sum.
+__device__ uint64_t SplitOf(int32_t* v, int32_t limit) {
+  uint64_t split = 0;
+  int index = 0;
+  for (int size = 2; size <= kMaxMinibatches; size *= 2) {
+    for (int i = 0; i < kMaxMinibatches; i += size, ++index) {
+      const int32_t l = v[i], r = v[i + size / 2];
+      if (l + r > limit) {
+        split |= uint64_t{1} << index;
+        v[i] = l > r ? l : r;
+      } else {
+        v[i] = l + r;
+      }
+    }
+  }
+  return split;
+}
+
+// Pass 1: per (SC, partition) the split of its bucket counts, ids and unique
+// ids, OR-ed into counters[5] (UpdateMinibatchingSplit,
+// sort_and_group_coo_tensors_impl.h:116-151); a bucket over a limit with
+// dropping off sets counters[1].
+__global__ __launch_bounds__(64) void MinibatchSplit(const BucketStats* bstats,
+                                                     FillParams fp,
+                                                     int64_t* counters) {
+  const int NS = fp.num_partitions;
+  const int64_t n = static_cast<int64_t>(fp.local_devices) *
+                    fp.segs_per_device * NS;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  const int64_t g = t / NS;
+  const int p = static_cast<int>(t % NS);
+  int32_t ids[kMaxMinibatches], uniq[kMaxMinibatches];
+  bool over = false;
+  for (int b = 0; b < kMaxMinibatches; ++b) {
+    const BucketStats& x = bstats[(g * kMaxMinibatches + b) * NS + p];
+    ids[b] = x.obs_ids;
+    uniq[b] = x.obs_unique;
+    over = over || x.obs_ids > fp.max_ids || x.obs_unique > fp.max_unique;
+  }
+  const uint64_t split = SplitOf(ids, fp.max_ids) | SplitOf(uniq, fp.max_unique);
+  if (split != 0) {
+    atomicOr(reinterpret_cast<unsigned long long*>(&counters[5]),
+             static_cast<unsigned long long>(split));
+  }
+  if (over && !fp.allow_dropping) {
+    atomicMax(reinterpret_cast<unsigned long long*>(&counters[1]), 1ull);
+  }
+}
+
 // What the sample view needs of every run written to the CSR, indexed by
 // the extraction position of the run's first id (null: no view).
 struct ViewParts {
@@ -603,7 +902,7 @@ __global__ __launch_bounds__(256) void ScatterRuns(
   const int64_t k = static_cast<int64_t>(keep_scan[r]) - bstats[bucket].kept_first;
   const FillPlan pl = plans[bucket];
   if (k >= pl.fit) return;
-  const int64_t d = seg / fp.segs_per_device;
+  const int64_t d = (seg >> kl.mb_bits) / fp.segs_per_device;
   const int64_t pos = d * fp.coo_size + pl.start + k;
   eid[pos] = static_cast<int32_t>(local);
   sid[pos] = static_cast<int32_t>(srows[i0] % static_cast<uint32_t>(bps));
@@ -666,7 +965,7 @@ __global__ __launch_bounds__(256) void WritePadding(const FillPlan* plans,
   const int64_t s = seg % fp.segs_per_device;
   const int64_t per_sc = fp.coo_size / fp.segs_per_device;
   const int64_t coo_begin =
-      s * per_sc < fp.coo_size ? s * per_sc : fp.coo_size;
+      fp.absolute ? 0 : (s * per_sc < fp.coo_size ? s * per_sc : fp.coo_size);
   const int64_t pos = d * fp.coo_size + coo_begin + pos_rel;
   eid[pos] = kPadInt;
   sid[pos] = kPadInt;
@@ -730,6 +1029,16 @@ int MakePlan(const scemb_feature_t* feats, int nf,
   }
   if (o->max_ids_per_partition <= 0 || o->max_unique_ids_per_partition <= 0) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT, "id limits must be positive");
+  }
+  if (o->enable_minibatching) {
+    if (o->minibatching_pass < 0 || o->minibatching_pass > 2) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "minibatching_pass must be 0, 1 or 2");
+    }
+    if (o->build_sample_view) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "the sample view is not built with minibatching");
+    }
   }
   pl->L = L;
   pl->G = G;
@@ -837,7 +1146,10 @@ int MakePlan(const scemb_feature_t* feats, int nf,
     kl.col_bits = 32;
   }
   kl.seg_bits = BitWidth(static_cast<uint64_t>(L) * S - 1);
-  pl->wide_keys = kl.col_bits + kl.seg_bits > 31;
+  kl.mb_bits = o->enable_minibatching && o->minibatching_pass > 0
+                   ? BitWidth(kMaxMinibatches - 1)
+                   : 0;
+  pl->wide_keys = kl.col_bits + kl.mb_bits + kl.seg_bits > 31;
   const int sample_bits = BitWidth(static_cast<uint64_t>(std::max<int64_t>(bfd - 1, 0)));
   pl->row_key_seg_shift = sample_bits;
   pl->row_bits = sample_bits + kl.seg_bits;
@@ -915,7 +1227,10 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                 const scemb_preprocess_output_t* out, const Plan& pl,
                 Arena& ws, hipStream_t stream) {
   const int64_t M = pl.total_ids;
-  const int64_t num_buckets = static_cast<int64_t>(pl.L) * pl.S * pl.NS;
+  const bool minibatching = o->enable_minibatching != 0;
+  const int pass = minibatching ? o->minibatching_pass : 0;
+  const int64_t num_buckets = static_cast<int64_t>(pl.L) * pl.S *
+                              (int64_t{1} << pl.kl.mb_bits) * pl.NS;
   const bool need_row_pass = !o->has_variable_weights && !pl.rows_monotone;
   Buffers b;
   b.keys = ws.Take<K>(M);
@@ -967,6 +1282,16 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   const bool measuring = ws.measuring();
   const int64_t counters_off = RoundUp(2 * static_cast<int64_t>(pl.L) * pl.NS +
                                        static_cast<int64_t>(pl.L) * pl.S, 2);
+  uint64_t split = 0;
+  int num_minibatches = 1;
+  if (minibatching && pass == 2) {
+    split = o->minibatching_split;
+    if ((split >> (kMaxMinibatches - 1)) != 0) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "minibatching_split has at most 63 bits");
+    }
+    num_minibatches = __builtin_popcountll(split) + 1;
+  }
   int64_t* counters = nullptr;
   if (!measuring) {
     if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
@@ -983,7 +1308,8 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
     if ((reinterpret_cast<uintptr_t>(counters) & 7u) != 0) {
       return Fail(SCEMB_ERR_INVALID_ARGUMENT, "stats buffer must be 8-byte aligned");
     }
-    hipLaunchKernelGGL(ZeroI64, dim3(1), dim3(64), 0, stream, counters, 4);
+    hipLaunchKernelGGL(ZeroI64, dim3(1), dim3(64), 0, stream, counters,
+                       kNumCounters);
     SCEMB_LAUNCH_CHECK();
     std::vector<FeatureDev> fd(nf);
     for (int f = 0; f < nf; ++f) {
@@ -1035,7 +1361,7 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   }
   // Sort: optional row pass, then the column key. One extra key bit keeps the
   // all-ones sentinel of rejected ids strictly above every valid key.
-  const int sort_bits = pl.kl.col_bits + pl.kl.seg_bits + 1;
+  const int sort_bits = pl.kl.col_bits + pl.kl.mb_bits + pl.kl.seg_bits + 1;
   K* skeys = static_cast<K*>(b.keys);
   uint32_t* sidx = b.vals;
   int st = 0;
@@ -1083,8 +1409,10 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                        stream, skeys, b.flags, b.scan, M, b.run_pos);
     SCEMB_LAUNCH_CHECK();
   }
+  // The first minibatching pass never drops (it only decides whether
+  // minibatching is needed, sort_and_group_coo_tensors_impl.h:222-226).
   const Limits lim{o->max_ids_per_partition, o->max_unique_ids_per_partition,
-                   o->allow_id_dropping};
+                   minibatching && pass == 0 ? 0 : o->allow_id_dropping};
   if (!measuring) {
     if (M > 0) {
       hipLaunchKernelGGL((RunReduce<K>), dim3(CeilDiv(M + 1, 256)), dim3(256),
@@ -1122,12 +1450,50 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   fp.max_ids = o->max_ids_per_partition;
   fp.max_unique = o->max_unique_ids_per_partition;
   fp.allow_dropping = o->allow_id_dropping;
+  fp.mb_bits = pl.kl.mb_bits;
+  fp.absolute = minibatching ? 1 : 0;
+  fp.num_minibatches = num_minibatches;
+  // Minibatch of each bucket: the boundary between buckets b - 1 and b is
+  // where the two halves of one node of the merge tree meet (level t =
+  // trailing zeros of b plus one, node b >> t); the buckets on either side
+  // fall into different minibatches iff that node is split
+  // (minibatching_splits_impl.h:84-131).
+  {
+    int mb = 0;
+    fp.minibatch_of[0] = 0;
+    for (int bkt = 1; bkt < kMaxMinibatches; ++bkt) {
+      const int t = __builtin_ctz(static_cast<unsigned>(bkt)) + 1;
+      int index = 0;
+      for (int l = 1; l < t; ++l) index += kMaxMinibatches >> l;
+      index += bkt >> t;
+      mb += static_cast<int>((split >> index) & 1u);
+      fp.minibatch_of[bkt] = static_cast<uint8_t>(mb);
+    }
+  }
   int32_t* stat_max_ids = out->stats;
   int32_t* stat_max_unique = out->stats + static_cast<int64_t>(pl.L) * pl.NS;
   int32_t* stat_required = out->stats + 2 * static_cast<int64_t>(pl.L) * pl.NS;
-  hipLaunchKernelGGL(FillPlanKernel, dim3(1), dim3(256), 0, stream, b.bstats,
-                     fp, out->row_pointers, b.plans, stat_max_ids,
-                     stat_max_unique, stat_required, counters);
+  if (minibatching && pass == 1) {
+    const int64_t cells = static_cast<int64_t>(pl.L) * pl.S * pl.NS;
+    hipLaunchKernelGGL(MinibatchSplit, dim3(CeilDiv(cells, 64)), dim3(64), 0,
+                       stream, b.bstats, fp, counters);
+    SCEMB_LAUNCH_CHECK();
+    if (M > 0) {
+      hipLaunchKernelGGL(StoreTotal, dim3(1), dim3(1), 0, stream, b.totals,
+                         counters);
+      SCEMB_LAUNCH_CHECK();
+    }
+    return 0;
+  }
+  if (minibatching) {
+    hipLaunchKernelGGL(FillPlanMinibatch, dim3(1), dim3(64), 0, stream,
+                       b.bstats, fp, pass, out->row_pointers, b.plans,
+                       stat_max_ids, stat_max_unique, stat_required, counters);
+  } else {
+    hipLaunchKernelGGL(FillPlanKernel, dim3(1), dim3(256), 0, stream, b.bstats,
+                       fp, out->row_pointers, b.plans, stat_max_ids,
+                       stat_max_unique, stat_required, counters);
+  }
   SCEMB_LAUNCH_CHECK();
   if (view.entry != nullptr && M > 0) {
     view.sidx = sidx;
@@ -1202,7 +1568,7 @@ int64_t scemb_preprocess_stats_counters_offset(
 
 int64_t scemb_preprocess_stats_size(const scemb_preprocess_options_t* o) {
   const int64_t off = scemb_preprocess_stats_counters_offset(o);
-  return off < 0 ? -1 : off + 8;
+  return off < 0 ? -1 : off + 2 * kNumCounters;
 }
 
 size_t scemb_preprocess_workspace_size(const scemb_feature_t* features,
@@ -1232,25 +1598,29 @@ int scemb_preprocess_stacked_table(const scemb_feature_t* features,
 
 int64_t scemb_compute_theoretical_max_coo_buffer_size(
     int32_t max_ids_per_partition, int32_t global_device_count,
-    int32_t num_sc_per_device) {
+    int32_t num_sc_per_device, int32_t enable_minibatching) {
   const int64_t num_scs = static_cast<int64_t>(global_device_count) * num_sc_per_device;
-  return RoundUp(max_ids_per_partition, kAlign) * num_sc_per_device * num_scs;
+  return RoundUp(max_ids_per_partition, kAlign) * num_sc_per_device * num_scs *
+         (enable_minibatching ? kMaxMinibatches : 1);
 }
 
 int64_t scemb_compute_coo_buffer_size_per_device(
     int32_t max_ids_per_partition, int64_t suggested, int32_t global_device_count,
-    int32_t num_sc_per_device) {
+    int32_t num_sc_per_device, int32_t enable_minibatching) {
   const int64_t theoretical = scemb_compute_theoretical_max_coo_buffer_size(
-      max_ids_per_partition, global_device_count, num_sc_per_device);
+      max_ids_per_partition, global_device_count, num_sc_per_device,
+      enable_minibatching);
   if (suggested <= 0) return theoretical;
   const int64_t v = RoundUp(suggested, static_cast<int64_t>(kAlign) * num_sc_per_device);
   return v > theoretical ? -1 : v;
 }
 
 int32_t scemb_compute_row_pointers_size_per_device(int32_t global_device_count,
-                                                   int32_t num_sc_per_device) {
+                                                   int32_t num_sc_per_device,
+                                                   int32_t enable_minibatching) {
   const int32_t ns = global_device_count * num_sc_per_device;
-  return std::max(ns, kAlign) * num_sc_per_device;
+  return std::max(ns, kAlign) * num_sc_per_device *
+         (enable_minibatching ? kMaxMinibatches : 1);
 }
 
 }  // extern "C"

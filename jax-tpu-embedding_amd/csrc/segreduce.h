@@ -153,6 +153,8 @@ struct Csr {
   int32_t num_segments;
   int32_t num_partitions;
   int32_t rp_per_segment;
+  int32_t num_minibatches;  // 0: one block per segment, relative positions
+  int64_t coo_size;
 };
 
 __device__ __forceinline__ uint64_t Pack(uint32_t lo, float g) {
@@ -180,6 +182,46 @@ __device__ __forceinline__ int PartitionOf(const int32_t* rp, int nparts,
   return -1;
 }
 
+// COO positions of a CSR (the whole buffer in the minibatching layout).
+__device__ __forceinline__ int64_t CsrPositions(const Csr& csr) {
+  return csr.num_minibatches > 0 ? csr.coo_size
+                                 : csr.per_segment * csr.num_segments;
+}
+
+// Segment (local SparseCore) and partition of COO position j, partition -1
+// for padding. In the minibatching layout the (segment, minibatch,
+// partition) ranges follow each other through the buffer, each starting at
+// the aligned end of the one before: the first whose end lies past j holds
+// it, unless j falls in the alignment gap before that range.
+__device__ __forceinline__ int LocateEntry(const Csr& csr, int64_t j,
+                                           int* segment) {
+  if (csr.num_minibatches == 0) {
+    const int s = static_cast<int>(j / csr.per_segment);
+    *segment = s;
+    return PartitionOf(csr.rp + static_cast<int64_t>(s) * csr.rp_per_segment,
+                       csr.num_partitions, csr.per_segment,
+                       j - static_cast<int64_t>(s) * csr.per_segment);
+  }
+  const int ns = csr.num_partitions;
+  const int total = csr.num_segments * csr.num_minibatches * ns;
+  auto end_of = [&](int f) -> int64_t {
+    const int64_t e = csr.rp[static_cast<int64_t>(f / ns) * csr.rp_per_segment +
+                             f % ns];
+    return e < csr.coo_size ? e : csr.coo_size;
+  };
+  int lo = 0, hi = total;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (end_of(mid) > j) hi = mid; else lo = mid + 1;
+  }
+  if (lo == total) return -1;
+  const int64_t start =
+      lo == 0 ? 0 : (end_of(lo - 1) + kAlign - 1) / kAlign * kAlign;
+  if (j < start) return -1;
+  *segment = lo / ns / csr.num_minibatches;
+  return lo % ns;
+}
+
 // One (key, payload) pair per COO position; padding and invalid entries get
 // the sentinel key, which sorts last.
 template <bool kBySample>
@@ -189,13 +231,11 @@ __global__ __launch_bounds__(256) void ExpandCsr(Csr csr, int64_t bps,
                                                  uint32_t* keys,
                                                  uint64_t* payload,
                                                  uint32_t* status) {
-  const int64_t n = csr.per_segment * csr.num_segments;
+  const int64_t n = CsrPositions(csr);
   const int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (j >= n) return;
-  const int s = static_cast<int>(j / csr.per_segment);
-  const int64_t off = j - static_cast<int64_t>(s) * csr.per_segment;
-  const int p = PartitionOf(csr.rp + static_cast<int64_t>(s) * csr.rp_per_segment,
-                            csr.num_partitions, csr.per_segment, off);
+  int s = 0;
+  const int p = LocateEntry(csr, j, &s);
   uint32_t key = sentinel;
   uint64_t pay = 0;
   if (p >= 0) {
@@ -988,8 +1028,13 @@ int CheckCsr(const scemb_csr_t* csr, int64_t batch, int64_t table_rows,
   if (table_rows >= (int64_t{1} << 32) - 1 || batch >= (int64_t{1} << 31) - 1) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT, "table or batch too large");
   }
+  if (csr->num_minibatches < 0 || csr->num_minibatches > kMaxMinibatches) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "num_minibatches must be in [0, 64]");
+  }
   const int64_t per_seg = csr->coo_size / csr->num_segments;
-  geo->n = per_seg * csr->num_segments;
+  geo->n = csr->num_minibatches > 0 ? csr->coo_size
+                                    : per_seg * csr->num_segments;
   if (geo->n >= (int64_t{1} << 31) - 1) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT, "coo buffer too large");
   }
@@ -1013,6 +1058,8 @@ Csr MakeCsr(const scemb_csr_t* csr) {
   c.num_segments = csr->num_segments;
   c.num_partitions = csr->num_partitions;
   c.rp_per_segment = csr->row_pointers_per_segment;
+  c.num_minibatches = csr->num_minibatches;
+  c.coo_size = csr->coo_size;
   return c;
 }
 
@@ -1130,7 +1177,8 @@ int GradImpl(const GradCall& c) {
   if (rc != 0) return rc;
   const int64_t n = geo.n;
   const bool direct =
-      (csr->flags & SCEMB_CSR_SORTED_BY_ROW) != 0 && csr->num_segments == 1;
+      (csr->flags & SCEMB_CSR_SORTED_BY_ROW) != 0 && csr->num_segments == 1 &&
+      csr->num_minibatches == 0;
   StreamArgs st{};
   st.n = n;
   if (direct) {

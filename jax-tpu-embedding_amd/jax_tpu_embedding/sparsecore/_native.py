@@ -85,6 +85,8 @@ class Csr(ctypes.Structure):
       ("row_pointers_per_segment", ctypes.c_int32),
       ("flags", ctypes.c_uint32),
       ("num_entries", ctypes.c_int64),
+      ("num_minibatches", ctypes.c_int32),
+      ("reserved", ctypes.c_int32),
   ]
 
 
@@ -111,6 +113,9 @@ class RowBlock(ctypes.Structure):
 
 
 MAX_ROW_BLOCKS = 32
+# Minibatching buckets per SparseCore, the most minibatches (coo_format.h:
+# 52-53).
+MAX_MINIBATCHES = 64
 
 
 class Optimizer(ctypes.Structure):
@@ -154,8 +159,11 @@ class PreprocessOptions(ctypes.Structure):
       ("coo_buffer_size_per_device", ctypes.c_int64),
       ("col_id_bound", ctypes.c_int64),
       ("build_sample_view", ctypes.c_int32),
-      ("reserved", ctypes.c_int32),
+      ("enable_minibatching", ctypes.c_int32),
       ("table_rows", ctypes.c_int64),
+      ("minibatching_pass", ctypes.c_int32),
+      ("reserved", ctypes.c_int32),
+      ("minibatching_split", ctypes.c_uint64),
   ]
 
 
@@ -252,12 +260,12 @@ def load_library() -> ctypes.CDLL:
         vp, sz, vp]
     lib.scemb_compute_theoretical_max_coo_buffer_size.restype = i64
     lib.scemb_compute_theoretical_max_coo_buffer_size.argtypes = [i32, i32,
-                                                                  i32]
+                                                                  i32, i32]
     lib.scemb_compute_coo_buffer_size_per_device.restype = i64
     lib.scemb_compute_coo_buffer_size_per_device.argtypes = [i32, i64, i32,
-                                                             i32]
+                                                             i32, i32]
     lib.scemb_compute_row_pointers_size_per_device.restype = i32
-    lib.scemb_compute_row_pointers_size_per_device.argtypes = [i32, i32]
+    lib.scemb_compute_row_pointers_size_per_device.argtypes = [i32, i32, i32]
     lib.scemb_profile_enable.restype = None
     lib.scemb_profile_enable.argtypes = [ctypes.c_int]
     lib.scemb_profile_collect.restype = ctypes.c_int
@@ -376,20 +384,36 @@ WORKSPACE = _Workspace()
 def make_csr(row_pointers, embedding_ids, sample_ids, gains, num_segments,
              num_partitions, sorted_by_row: bool = False,
              num_entries: int | None = None,
-             one_entry_per_row: bool = False) -> Csr:
+             one_entry_per_row: bool = False,
+             num_minibatches: int = 0) -> Csr:
   """`num_entries`: the valid entries of the buffers when known (it only
   picks kernel variants). `sorted_by_row` / `one_entry_per_row` set
-  CSR_SORTED_BY_ROW / CSR_ONE_ENTRY_PER_ROW."""
+  CSR_SORTED_BY_ROW / CSR_ONE_ENTRY_PER_ROW. `num_minibatches` > 0: the
+  buffers are in the minibatching layout (row pointers of 64 blocks per
+  segment)."""
   rp_len = int(row_pointers.numel())
-  if rp_len % num_segments:
-    raise ValueError("row_pointers length must be divisible by "
-                     "num_sc_per_device")
+  if not 0 <= num_minibatches <= MAX_MINIBATCHES:
+    raise ValueError("num_minibatches must be in [0, 64]")
+  if num_minibatches:
+    # max(NS, 8) row pointers per (SC, minibatch), packed from the start
+    # (the buffer may be sized for 64 minibatches).
+    per_block = max(num_partitions, 8)
+    if rp_len < num_segments * num_minibatches * per_block:
+      raise ValueError(
+          f"row_pointers has {rp_len} entries; {num_minibatches} minibatches "
+          f"of {num_segments} SparseCores need "
+          f"{num_segments * num_minibatches * per_block}")
+  else:
+    if rp_len % num_segments:
+      raise ValueError("row_pointers length must be divisible by "
+                       "num_sc_per_device")
+    per_block = rp_len // num_segments
   return Csr(ptr(row_pointers), ptr(embedding_ids), ptr(sample_ids),
              ptr(gains), int(embedding_ids.numel()), num_segments,
-             num_partitions, rp_len // num_segments,
+             num_partitions, per_block,
              (CSR_SORTED_BY_ROW if sorted_by_row else 0) |
              (CSR_ONE_ENTRY_PER_ROW if one_entry_per_row else 0),
-             int(num_entries) if num_entries else 0)
+             int(num_entries) if num_entries else 0, int(num_minibatches), 0)
 
 
 class LookupView:

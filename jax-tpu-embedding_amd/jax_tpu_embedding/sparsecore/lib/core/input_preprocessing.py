@@ -14,9 +14,11 @@ Differences from the reference module, all documented behaviour of the C++
 path this build follows: duplicate weights are summed in float32 in sorted
 order (the Python module sums in float64 before the float32 cast), and ids
 must be non-negative. Limits are checked as in the reference
-(``_validate_partition_map``, ``:96-122``) and raise ``ValueError``.
-Minibatching raises ``NotImplementedError``. The returned buffers are torch
-CUDA tensors.
+(``_validate_partition_map``, ``:96-122``) and raise ``ValueError``. With
+``enable_minibatching`` the features (and weights) are a sequence of
+minibatches, each preprocessed on its own and packed into the minibatching
+layout of ``_pack_partitions_to_csr`` (``:190-284``). The returned buffers
+are torch CUDA tensors.
 """
 
 from __future__ import annotations
@@ -107,14 +109,13 @@ def preprocess_sparse_dense_matmul_input(
     max_unique_ids_per_partition: int, num_sc_per_device: int = -1,
     sharding_strategy: str = "MOD", enable_minibatching: bool = False):
   """Returns (row_pointers, embedding_ids, sample_ids, gains) for one feature
-  batch on one device (reference ``input_preprocessing.py:290-383``)."""
+  batch (or, with `enable_minibatching`, a sequence of minibatches) on one
+  device (reference ``input_preprocessing.py:290-383``)."""
   if max_ids_per_partition <= 0:
     raise ValueError(
         f"max_ids_per_partition must be positive, got {max_ids_per_partition}.")
-  if enable_minibatching:
-    raise NotImplementedError("minibatching is not supported on this path")
   ndim = _resolve_feature_input_ndim(features)
-  if ndim not in (1, 2):
+  if not enable_minibatching and ndim not in (1, 2):
     raise ValueError(f"features must be 1D or 2D, got {ndim}D.")
   if features_weights is not None and len(features) != len(features_weights):
     raise ValueError("features and features_weights must have the same length.")
@@ -125,6 +126,69 @@ def preprocess_sparse_dense_matmul_input(
     raise ValueError("global_device_count must be positive.")
   num_sc = (num_sc_per_device if num_sc_per_device > 0 else
             utils.num_sparsecores_per_device())
+  if enable_minibatching:
+    t = _native.torch()
+    if isinstance(features, (np.ndarray, t.Tensor)) or not hasattr(
+        features, "__len__"):
+      raise ValueError("When enable_minibatching is True, features must be a "
+                       "sequence of batches.")
+    weights = (features_weights if features_weights is not None else
+               [None] * len(features))
+    parts = [
+        _preprocess_one(f, w, max_ids_per_partition,
+                        max_unique_ids_per_partition, global_device_count,
+                        num_sc) for f, w in zip(features, weights)
+    ]
+    return _pack_minibatches(parts, num_sc, num_sc * global_device_count)
+  return _preprocess_one(features, features_weights, max_ids_per_partition,
+                         max_unique_ids_per_partition, global_device_count,
+                         num_sc)
+
+
+def _pack_minibatches(parts, num_sc: int, num_scs: int):
+  """The minibatching layout of _pack_partitions_to_csr (reference
+  input_preprocessing.py:190-284): for each local SC (starting at the
+  aligned end of the one before) and each minibatch, the partitions' entries
+  at positions in the whole buffer, row pointers at their ends, each
+  partition starting 8-aligned, max(NS, 8) row pointers per minibatch; every
+  other position holds the padding (INT_MAX, INT_MAX, NaN). The entries are
+  copied on the device; only the minibatches' row pointers are read back."""
+  t = _native.torch()
+  dev = _native.device()
+  per_mb = int(parts[0][1].numel())
+  total = per_mb * len(parts)
+  eid = t.full((total,), np.iinfo(np.int32).max, dtype=t.int32, device=dev)
+  sid = t.full((total,), np.iinfo(np.int32).max, dtype=t.int32, device=dev)
+  gains = t.full((total,), float("nan"), dtype=t.float32, device=dev)
+  rps_host = [p[0].cpu().numpy() for p in parts]
+  rpb = max(num_scs, 8)
+  rp = []
+  coo = 0
+  for s in range(num_sc):
+    coo = -(-coo // 8) * 8
+    for m, (_, e, si, g) in enumerate(parts):
+      seg = int(e.numel()) // num_sc
+      rpm = rps_host[m][s * (len(rps_host[m]) // num_sc):]
+      start = 0
+      for p in range(num_scs):
+        end = int(rpm[p])
+        n = end - start
+        if n > 0:
+          src = slice(s * seg + start, s * seg + end)
+          eid[coo:coo + n] = e[src]
+          sid[coo:coo + n] = si[src]
+          gains[coo:coo + n] = g[src]
+          coo += n
+        rp.append(coo)
+        coo = -(-coo // 8) * 8
+        start = -(-end // 8) * 8
+      rp.extend([coo] * (rpb - num_scs))
+  return (t.tensor(np.array(rp, np.int32), device=dev), eid, sid, gains)
+
+
+def _preprocess_one(features, features_weights, max_ids_per_partition,
+                    max_unique_ids_per_partition, global_device_count, num_sc):
+  """One batch through the stacked pipeline, checked against the limits."""
   ids, wts = _as_samples(features, features_weights)
   batch = len(ids)
   max_id = max((int(r.max()) for r in ids if r.size), default=0)

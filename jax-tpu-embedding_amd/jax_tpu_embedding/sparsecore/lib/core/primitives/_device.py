@@ -18,14 +18,17 @@ def resolve_sparsecores(num_sc_per_device, global_device_count):
 
 def csr_operands(row_pointers, embedding_ids, sample_ids, gains,
                  num_sc_per_device, num_partitions, sorted_by_row=False,
-                 num_entries=None, one_entry_per_row=False):
+                 num_entries=None, one_entry_per_row=False,
+                 num_minibatches=0):
   """Device tensors for the CSR buffers plus the C struct that points at
   them (the tensors must stay alive while the struct is used).
   `sorted_by_row` declares the entries ascending by (partition, embedding
   id) inside each segment, as the preprocessing writes them; `num_entries`
   the count of valid entries when known (it only picks kernel variants);
   `one_entry_per_row` at most one entry per activation row (one-hot input
-  rows), which turns the grouping by activation row into a placement."""
+  rows), which turns the grouping by activation row into a placement;
+  `num_minibatches` > 0 the minibatching layout with that many minibatches
+  per SparseCore."""
   t = _native.require_gpu()
   dev = _native.device()
   rp = _native.as_device_tensor(row_pointers, t.int32, dev).reshape(-1)
@@ -34,7 +37,8 @@ def csr_operands(row_pointers, embedding_ids, sample_ids, gains,
   g = _native.as_device_tensor(gains, t.float32, dev).reshape(-1)
   csr = _native.make_csr(rp, eid, sid, g, num_sc_per_device, num_partitions,
                          sorted_by_row=sorted_by_row, num_entries=num_entries,
-                         one_entry_per_row=one_entry_per_row)
+                         one_entry_per_row=one_entry_per_row,
+                         num_minibatches=num_minibatches)
   return (rp, eid, sid, g), csr
 
 

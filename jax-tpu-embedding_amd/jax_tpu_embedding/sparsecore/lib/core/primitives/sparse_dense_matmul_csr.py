@@ -30,12 +30,25 @@ from jax_tpu_embedding.sparsecore.lib.core.primitives import _device
 from jax_tpu_embedding.sparsecore.lib.core.primitives import utils
 
 
-def check_single_minibatch(num_minibatches):
-  """Host-side minibatch counts other than 1 are not supported (device
-  scalars are not read back, to keep the call asynchronous)."""
-  if isinstance(num_minibatches, (int, np.integer, np.ndarray)):
-    if int(np.asarray(num_minibatches).reshape(())) != 1:
-      raise NotImplementedError("only one minibatch is supported")
+def resolve_minibatches(num_minibatches, enable_minibatching: bool) -> int:
+  """The CSR layout the operands are in: 0 without minibatching (one block
+  of row pointers per SparseCore; the count must then be 1, a device scalar
+  is not read back), else the minibatch count (1 to 64) of the minibatching
+  layout ("SparseDenseMatmulWithMinibatchingOp",
+  sparse_dense_matmul_csr.py:171-192 of the reference)."""
+  if not enable_minibatching:
+    if isinstance(num_minibatches, (int, np.integer, np.ndarray)):
+      if int(np.asarray(num_minibatches).reshape(())) != 1:
+        raise ValueError("num_minibatches must be 1 without minibatching")
+    return 0
+  if hasattr(num_minibatches, "item") and not isinstance(
+      num_minibatches, (np.ndarray, np.generic)):
+    n = int(num_minibatches.reshape(()).item())  # device scalar: one read
+  else:
+    n = int(np.asarray(num_minibatches).reshape(()))
+  if not 1 <= n <= _native.MAX_MINIBATCHES:
+    raise ValueError(f"num_minibatches must be in [1, 64], got {n}")
+  return n
 
 
 def _validate_quantization(quantization_config):
@@ -69,14 +82,16 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
   _validate_quantization(quantization_config)
   if quantization_config is not None:
     raise NotImplementedError("quantized tables are not supported yet")
-  if enable_minibatching:
-    raise NotImplementedError("minibatching is not supported on this path")
-  check_single_minibatch(num_minibatches_per_physical_sparse_core)
+  nmb = resolve_minibatches(num_minibatches_per_physical_sparse_core,
+                            enable_minibatching)
   t = _native.require_gpu()
   s, ns = _device.resolve_sparsecores(num_sc_per_device, global_device_count)
   keep, csr = _device.csr_operands(lhs_row_pointers, lhs_local_embedding_ids,
                                    lhs_local_sample_ids, lhs_gains, s, ns,
-                                   num_entries=csr_num_entries)
+                                   num_entries=csr_num_entries,
+                                   num_minibatches=nmb)
+  if nmb:
+    lookup_view = None  # views are built for the per-SC layout
   table = _device.device_table(embedding_table)
   shape = ((device_batch_size,) if table.dim() == 1 else
            (device_batch_size, int(table.shape[1])))

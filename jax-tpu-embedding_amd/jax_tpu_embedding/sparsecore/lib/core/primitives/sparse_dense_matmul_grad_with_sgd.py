@@ -48,16 +48,15 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
       lhs_gains, num_minibatches_per_physical_sparse_core, embedding_table,
       activations_grad, max_ids_per_partition, max_unique_ids_per_partition,
       computation_name, sharding_strategy, min_value, max_value)
-  if enable_minibatching:
-    raise NotImplementedError("minibatching is not supported on this path")
-  sparse_dense_matmul_csr.check_single_minibatch(
-      num_minibatches_per_physical_sparse_core)
+  nmb = sparse_dense_matmul_csr.resolve_minibatches(
+      num_minibatches_per_physical_sparse_core, enable_minibatching)
   t = _native.require_gpu()
   s, ns = _device.resolve_sparsecores(num_sc_per_device, global_device_count)
   keep, csr = _device.csr_operands(lhs_row_pointers, lhs_local_embedding_ids,
                                    lhs_local_sample_ids, lhs_gains, s, ns,
                                    sorted_by_row=csr_sorted_by_row,
-                                   num_entries=csr_num_entries)
+                                   num_entries=csr_num_entries,
+                                   num_minibatches=nmb)
   table = _device.device_table(embedding_table)
   blocks = None
   if isinstance(activations_grad, _device.RowBlocks):

@@ -7,8 +7,10 @@ invalid arguments, ``RuntimeError`` where the reference aborts). The work runs
 on the GPU through ``scemb_preprocess_stacked_table``; outputs are torch CUDA
 tensors (flattened unless ``has_leading_dimension``), stats are numpy.
 
-Not supported on this path (raise ``NotImplementedError``): minibatching
-(``enable_minibatching=True``) and the sparse-COO entry point.
+Minibatching (``enable_minibatching=True``) is single-host: the passes of
+``PreprocessSparseDenseMatmulInput`` (input_preprocessing.cc:852-929) run as
+one library call per pass and stack, with the OR of the stacks' splits taken
+here (the reference's all-reduce across hosts is not part of this path).
 """
 
 from __future__ import annotations
@@ -29,7 +31,8 @@ class ShardingStrategy(enum.IntEnum):
 
 
 class AllReduceInterface:  # pylint: disable=too-few-public-methods
-  """Placeholder type: cross-host minibatching is not part of this path."""
+  """Placeholder type: cross-host minibatching is not part of this path (one
+  host decides alone, input_preprocessing.cc:535-537, :581-583)."""
 
 
 class SparseDenseMatmulInputStats:
@@ -110,29 +113,26 @@ def get_stacked_table_metadata(feature_specs):
 def compute_row_pointers_size_per_device(global_device_count: int,
                                          num_sc_per_device: int,
                                          enable_minibatching: bool = False):
-  if enable_minibatching:
-    raise NotImplementedError("minibatching is not supported on this path")
   return int(_native.load_library().scemb_compute_row_pointers_size_per_device(
-      global_device_count, num_sc_per_device))
+      global_device_count, num_sc_per_device, int(bool(enable_minibatching))))
 
 
 def compute_theoretical_max_coo_buffer_size(max_ids_per_partition: int,
                                             global_device_count: int,
                                             num_sc_per_device: int,
                                             enable_minibatching: bool = False):
-  if enable_minibatching:
-    raise NotImplementedError("minibatching is not supported on this path")
   return int(
       _native.load_library().scemb_compute_theoretical_max_coo_buffer_size(
-          max_ids_per_partition, global_device_count, num_sc_per_device))
+          max_ids_per_partition, global_device_count, num_sc_per_device,
+          int(bool(enable_minibatching))))
 
 
 def _coo_buffer_size(meta: FeatureMetadataInStack, global_device_count,
-                     num_sc_per_device) -> int:
+                     num_sc_per_device, enable_minibatching=False) -> int:
   v = _native.load_library().scemb_compute_coo_buffer_size_per_device(
       meta.max_ids_per_partition,
       meta.suggested_coo_buffer_size_per_device or 0, global_device_count,
-      num_sc_per_device)
+      num_sc_per_device, int(bool(enable_minibatching)))
   if v < 0:
     raise RuntimeError(
         "Suggested Coo Buffer Size is larger than the theoretical max for "
@@ -147,11 +147,10 @@ def _coo_buffer_size(meta: FeatureMetadataInStack, global_device_count,
 def compute_coo_buffer_size_per_device(feature_specs, global_device_count: int,
                                        num_sc_per_device: int,
                                        enable_minibatching: bool = False):
-  if enable_minibatching:
-    raise NotImplementedError("minibatching is not supported on this path")
   stacks = get_stacked_table_metadata(list(feature_specs))
   return {
-      name: _coo_buffer_size(metas[0], global_device_count, num_sc_per_device)
+      name: _coo_buffer_size(metas[0], global_device_count, num_sc_per_device,
+                             enable_minibatching)
       for name, metas in stacks.items()
   }
 
@@ -265,16 +264,21 @@ def _to_device_feature(feature, weights) -> _DeviceFeature:
 
 def _preprocess_stack(feats, metas, *, local_device_count,
                       global_device_count, num_sc_per_device,
-                      allow_id_dropping, has_weights, build_view=False):
-  """Enqueues one stacked table; returns (rp, eid, sid, gains, stats on the
+                      allow_id_dropping, has_weights, build_view=False,
+                      enable_minibatching=False, minibatching_pass=0,
+                      minibatching_split=0, outputs=None):
+  """Enqueues one stacked table (one minibatching pass of it with
+  `enable_minibatching`); returns (rp, eid, sid, gains, stats on the
   device, (L, S, NS, counters offset), view) where view is the
   (keys, entries) pair of the CSR's sample view when `build_view`, else
-  None."""
+  None. `outputs`: the (rp, eid, sid, gains) of an earlier pass to write
+  into."""
   t = _native.require_gpu()
   lib = _native.load_library()
   dev = _native.device()
   ns = num_sc_per_device * global_device_count
-  c = _coo_buffer_size(metas[0], global_device_count, num_sc_per_device)
+  c = _coo_buffer_size(metas[0], global_device_count, num_sc_per_device,
+                       enable_minibatching)
   bound = max(m.stack_vocab_size for m in metas)
   for f, m in zip(feats, metas):
     if f.max_id is not None:
@@ -284,8 +288,9 @@ def _preprocess_stack(feats, metas, *, local_device_count,
       _COMBINERS.get(metas[0].row_combiner, 0),
       metas[0].max_ids_per_partition, metas[0].max_unique_ids_per_partition,
       int(bool(allow_id_dropping)), int(bool(has_weights)), c, bound,
-      int(bool(build_view)), 0,
-      metas[0].stack_vocab_size // global_device_count)
+      int(bool(build_view)), int(bool(enable_minibatching)),
+      metas[0].stack_vocab_size // global_device_count,
+      int(minibatching_pass), 0, int(minibatching_split))
   structs = (_native.Feature * len(feats))()
   for i, (f, m) in enumerate(zip(feats, metas)):
     structs[i] = _native.Feature(
@@ -298,10 +303,15 @@ def _preprocess_stack(feats, metas, *, local_device_count,
     _native.check(_native.SCEMB_ERR_INVALID_ARGUMENT)
   ws = _native.WORKSPACE.get(need)
   L, S = local_device_count, num_sc_per_device
-  rp = t.empty(L * S * max(ns, 8), dtype=t.int32, device=dev)
-  eid = t.empty(L * c, dtype=t.int32, device=dev)
-  sid = t.empty(L * c, dtype=t.int32, device=dev)
-  gains = t.empty(L * c, dtype=t.float32, device=dev)
+  if outputs is not None:
+    rp, eid, sid, gains = outputs
+  else:
+    rp = t.empty(L * S * max(ns, 8) *
+                 (_native.MAX_MINIBATCHES if enable_minibatching else 1),
+                 dtype=t.int32, device=dev)
+    eid = t.empty(L * c, dtype=t.int32, device=dev)
+    sid = t.empty(L * c, dtype=t.int32, device=dev)
+    gains = t.empty(L * c, dtype=t.float32, device=dev)
   nstats = lib.scemb_preprocess_stats_size(ctypes.byref(opts))
   stats = t.zeros(nstats + 2, dtype=t.int32, device=dev)
   view = None
@@ -339,8 +349,8 @@ def preprocess_sparse_dense_matmul_input(
   190-216 and :124-188) on the GPU.
 
   Returns (row_pointers, embedding_ids, sample_ids, gains, num_minibatches,
-  stats): four dicts keyed by stacked-table name, the minibatch count (1) and
-  a SparseDenseMatmulInputStats.
+  stats): four dicts keyed by stacked-table name, the minibatch count and a
+  SparseDenseMatmulInputStats.
   """
   del batch_number, all_reduce_interface
   features, feature_weights, feature_specs = check_arguments(
@@ -350,16 +360,17 @@ def preprocess_sparse_dense_matmul_input(
       features, feature_weights, feature_specs, local_device_count,
       global_device_count, num_sc_per_device=num_sc_per_device,
       has_leading_dimension=has_leading_dimension,
-      allow_id_dropping=allow_id_dropping)
-  return rps, eids, sids, gns, 1, collect_stats(pending)
+      allow_id_dropping=allow_id_dropping,
+      enable_minibatching=enable_minibatching)
+  return (rps, eids, sids, gns, pending.num_minibatches,
+          collect_stats(pending))
 
 
 def check_arguments(features, feature_weights, feature_specs,
                     sharding_strategy, enable_minibatching: bool):
   """Argument checks of the preprocessing entry; returns the inputs as
   lists."""
-  if enable_minibatching:
-    raise NotImplementedError("minibatching is not supported on this path")
+  del enable_minibatching  # every combination is accepted
   if int(sharding_strategy) != int(ShardingStrategy.MOD):
     raise ValueError("Only mod sharding is supported for now.")
   features = list(features)
@@ -375,22 +386,92 @@ def check_arguments(features, feature_weights, feature_specs,
   return features, feature_weights, feature_specs
 
 
+class PendingStats(list):
+  """Per stack (name, stats on the device, L, S, NS, counters offset,
+  features) of the enqueued first pass, plus what minibatching decided:
+  `num_minibatches` and, per stack, the stats of the pass that wrote the
+  final CSR when it was not the first (its dropped ids count)."""
+
+  def __init__(self):
+    super().__init__()
+    self.num_minibatches = 1
+    self.final_pass_stats = {}
+
+
+def _read_counters(entries):
+  """One wait: the int64 counters of each (stats tensor, offset)."""
+  t = _native.torch()
+  host = t.cat([e[0] for e in entries]).cpu().numpy()
+  out, pos = [], 0
+  for stats_dev, off in entries:
+    chunk = host[pos:pos + stats_dev.numel()]
+    pos += stats_dev.numel()
+    out.append(chunk[off:off + 2 * _NUM_COUNTERS].copy().view(np.int64))
+  return out
+
+
+_NUM_COUNTERS = 6
+
+
+def _raise_on_counters(name, counters):
+  if counters[2] > 0:
+    raise ValueError(
+        f"{int(counters[2])} embedding ids of stacked table {name} are "
+        "negative or beyond the stacked vocabulary.")
+  if counters[1] > 0:
+    raise RuntimeError(
+        f"Observed max ids per partition for table: {name} is greater than "
+        "the set max ids per partition. Use `allow_id_dropping` or increase "
+        "the `max_ids_per_partition`. You could also try to reduce the "
+        "batch size.")
+
+
+def _minibatching_passes(pending, jobs, csr):
+  """Runs the rest of input_preprocessing.cc:852-929 after every stack's
+  first pass: if one of them exceeds a limit, the bucket pass of every
+  stack, the OR of their splits, and the minibatched fill of every stack.
+  Waits for the device twice (the required flags, the splits)."""
+  first = _read_counters([(p[1], p[5]) for p in pending])
+  for p, c in zip(pending, first):
+    _raise_on_counters(p[0], c)
+  if not any(c[4] for c in first):
+    return
+  split = 0
+  second = []
+  for name, kwargs in jobs:
+    out = _preprocess_stack(**kwargs, minibatching_pass=1, outputs=csr[name])
+    second.append((out[4], out[5][3]))
+  for (name, _), c in zip(jobs, _read_counters(second)):
+    _raise_on_counters(name, c)
+    split |= int(np.uint64(c[5]))
+  for name, kwargs in jobs:
+    out = _preprocess_stack(**kwargs, minibatching_pass=2,
+                            minibatching_split=split, outputs=csr[name])
+    pending.final_pass_stats[name] = (out[4], out[5][3])
+  pending.num_minibatches = bin(split).count("1") + 1
+
+
 def enqueue_preprocessing(features, feature_weights, feature_specs,
                           local_device_count: int, global_device_count: int,
                           *, num_sc_per_device: int,
                           has_leading_dimension: bool = False,
                           allow_id_dropping: bool = False,
-                          sample_views: dict | None = None):
+                          sample_views: dict | None = None,
+                          enable_minibatching: bool = False):
   """Enqueues the preprocessing of every stack on the current stream without
   waiting for it. Returns the CSR dicts and the pending stats, which
   collect_stats turns into a SparseDenseMatmulInputStats (one wait). With a
   `sample_views` dict (one local and one global device only), each stack's
-  sample view (keys, entries) is built along and stored there."""
+  sample view (keys, entries) is built along and stored there. With
+  `enable_minibatching` the minibatching passes run here (they wait for the
+  device) and `pending.num_minibatches` holds the outcome; no sample view is
+  built."""
   stacks = get_stacked_table_metadata(feature_specs)
   rps, eids, sids, gns = {}, {}, {}, {}
-  pending = []
+  pending = PendingStats()
+  jobs, flat = [], {}
   build_view = (sample_views is not None and local_device_count == 1 and
-                global_device_count == 1)
+                global_device_count == 1 and not enable_minibatching)
   for name, metas in stacks.items():
     feats = [
         _to_device_feature(
@@ -398,19 +479,26 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
             None if feature_weights is None else
             feature_weights[m.feature_index]) for m in metas
     ]
+    kwargs = dict(feats=feats, metas=metas,
+                  local_device_count=local_device_count,
+                  global_device_count=global_device_count,
+                  num_sc_per_device=num_sc_per_device,
+                  allow_id_dropping=allow_id_dropping,
+                  has_weights=feature_weights is not None,
+                  enable_minibatching=enable_minibatching)
     rp, eid, sid, gains, stats_dev, (L, S, ns, off), view = _preprocess_stack(
-        feats, metas, local_device_count=local_device_count,
-        global_device_count=global_device_count,
-        num_sc_per_device=num_sc_per_device,
-        allow_id_dropping=allow_id_dropping,
-        has_weights=feature_weights is not None, build_view=build_view)
+        **kwargs, build_view=build_view)
     if view is not None:
       sample_views[name] = view
     pending.append((name, stats_dev, L, S, ns, off, feats))
+    jobs.append((name, kwargs))
+    flat[name] = (rp, eid, sid, gains)
     if has_leading_dimension:
       rp, eid, sid, gains = (rp.reshape(L, -1), eid.reshape(L, -1),
                              sid.reshape(L, -1), gains.reshape(L, -1))
     rps[name], eids[name], sids[name], gns[name] = rp, eid, sid, gains
+  if enable_minibatching:
+    _minibatching_passes(pending, jobs, flat)
   return rps, eids, sids, gns, pending
 
 
@@ -436,22 +524,29 @@ def collect_stats(pending) -> SparseDenseMatmulInputStats:
   if not pending:
     return stats
   t = _native.torch()
-  host = t.cat([p[1] for p in pending]).cpu().numpy()  # one wait
+  final = getattr(pending, "final_pass_stats", {})
+  later = [final[p[0]] for p in pending if p[0] in final]
+  # One wait for the first passes' stats and any later pass's counters.
+  host = t.cat([p[1] for p in pending] + [x[0] for x in later]).cpu().numpy()
   pos = 0
+  tail = sum(p[1].numel() for p in pending)
   for name, stats_dev, L, S, ns, off, _ in pending:
     stats_np = host[pos:pos + stats_dev.numel()]
     pos += stats_dev.numel()
-    counters = stats_np[off:off + 8].copy().view(np.int64)
-    if counters[2] > 0:
-      raise ValueError(
-          f"{int(counters[2])} embedding ids of stacked table {name} are "
-          "negative or beyond the stacked vocabulary.")
-    if counters[1] > 0:
-      raise RuntimeError(
-          f"Observed max ids per partition for table: {name} is greater than "
-          "the set max ids per partition. Use `allow_id_dropping` or increase "
-          "the `max_ids_per_partition`. You could also try to reduce the "
-          "batch size.")
+    counters = stats_np[off:off + 2 * _NUM_COUNTERS].copy().view(np.int64)
+    _raise_on_counters(name, counters)
+    if name in final:
+      later_dev, later_off = final[name]
+      chunk = host[tail:tail + later_dev.numel()]
+      tail += later_dev.numel()
+      later_counters = chunk[later_off:later_off +
+                             2 * _NUM_COUNTERS].copy().view(np.int64)
+      _raise_on_counters(name, later_counters)
+      # The stats stay the first pass's (input_preprocessing.cc:268-276);
+      # the dropped ids are the final pass's.
+      counters = counters.copy()
+      counters[0] = later_counters[0]
+      counters[3] = later_counters[3]
     stats.max_ids_per_partition[name] = stats_np[:L * ns].copy()
     stats.max_unique_ids_per_partition[name] = stats_np[L * ns:2 * L *
                                                         ns].copy()

@@ -311,9 +311,10 @@ def preprocess_sparse_dense_matmul_input(
       feats, weights, specs, local_device_count, global_device_count,
       num_sc_per_device=num_sc_per_device,
       has_leading_dimension=has_leading_dimension,
-      allow_id_dropping=allow_id_dropping, sample_views=built)
+      allow_id_dropping=allow_id_dropping, sample_views=built,
+      enable_minibatching=enable_minibatching)
   views = None
-  if local_device_count == 1:
+  if local_device_count == 1 and not enable_minibatching:
     # One device: the preprocessing wrote each stack's sample view along with
     # its CSR; otherwise (several global devices) it is built from the CSR.
     stacked = get_stacked_table_specs(feature_specs)
@@ -331,9 +332,10 @@ def preprocess_sparse_dense_matmul_input(
   counts = None
   if local_device_count == 1:
     counts = dict(stats.num_entries)
-    for name, view in views.items():
+    for name, view in (views or {}).items():
       view.num_entries = counts.get(name, 0)
-  minibatches = np.full(local_device_count, 1, dtype=np.int32)
+  minibatches = np.full(local_device_count, pending.num_minibatches,
+                        dtype=np.int32)
   if has_leading_dimension:
     minibatches = minibatches.reshape(local_device_count, 1)
   return (PreprocessedInput(SparseDenseMatmulInput(*csr), minibatches,

@@ -543,6 +543,11 @@ class StackedTableSpec:
   suggested_coo_buffer_size_per_device: int | None = None
   quantization_config: QuantizationConfig | None = None
 
+  def replace(self, **changes) -> "StackedTableSpec":
+    """A copy with `changes` (flax struct.PyTreeNode.replace of the
+    reference's spec, embedding_spec.py:1169)."""
+    return dataclasses.replace(self, **changes)
+
 
 @dataclasses.dataclass(eq=True, unsafe_hash=True, kw_only=True)
 class TableSpec:

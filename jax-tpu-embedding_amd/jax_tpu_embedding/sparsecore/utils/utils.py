@@ -40,7 +40,14 @@ def _device_kind(device) -> str:
     index = device.index
   if not torch.cuda.is_available():
     raise ValueError("Cannot determine device kind: no GPU is visible.")
-  return torch.cuda.get_device_name(index if index is not None else 0)
+  i = index if index is not None else 0
+  name = torch.cuda.get_device_name(i)
+  # Some ROCm installs report a generic marketing name ("AMD Radeon
+  # Graphics"); the architecture name identifies the MI355X (gfx950).
+  arch = getattr(torch.cuda.get_device_properties(i), "gcnArchName", "") or ""
+  if "MI355" not in name and arch.split(":")[0] == "gfx950":
+    return "AMD Instinct MI355X"
+  return name
 
 
 def num_sparsecores_per_device(device: DeviceLike | None = None) -> int:

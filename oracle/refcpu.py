@@ -599,9 +599,9 @@ def _threads(threads):
   return threads if threads else min(16, os.cpu_count() or 1)
 
 
-def _rp_per_segment(rp, num_sc_per_device, num_minibatches):
+def _rp_per_segment(rp, num_sc_per_device, num_scs, num_minibatches):
   if num_minibatches:
-    return len(rp) // (num_sc_per_device * MAX_MINIBATCHING_BUCKETS)
+    return max(num_scs, 8)
   return len(rp) // num_sc_per_device
 
 
@@ -610,8 +610,9 @@ def sparse_dense_matmul(rp, eid, sid, gains, table, batch, *,
                         num_minibatches=0):
   """Forward: activations[batch, dim] (or [batch] for a 1-D table).
 
-  num_minibatches > 0: the CSR is in the minibatching layout (row pointers
-  of 64 * num_sc_per_device blocks, positions in the whole buffer)."""
+  num_minibatches > 0: the CSR is in the minibatching layout (blocks of
+  max(num_scs, 8) row pointers per SC and minibatch from the start of `rp`,
+  positions in the whole buffer)."""
   table = np.ascontiguousarray(table, np.float32)
   dim = 1 if table.ndim == 1 else table.shape[1]
   act = np.zeros((batch, dim), np.float32)
@@ -621,7 +622,7 @@ def sparse_dense_matmul(rp, eid, sid, gains, table, batch, *,
                          np.ascontiguousarray(gains, np.float32).reshape(-1))
   lib().ref_sparse_dense_matmul(_p(rp), _p(eid), _p(sid), _p(gains), len(eid),
                                 num_sc_per_device, num_scs,
-                                _rp_per_segment(rp, num_sc_per_device,
+                                _rp_per_segment(rp, num_sc_per_device, num_scs,
                                                 num_minibatches),
                                 int(num_minibatches), _p(table),
                                 table.shape[0], dim, _p(act), batch,
@@ -657,7 +658,7 @@ def sparse_dense_matmul_grad(rp, eid, sid, gains, act_grad, table,
                                                  else 0)
   lib().ref_sparse_dense_matmul_grad(
       _p(rp), _p(eid), _p(sid), _p(gains), len(eid), num_sc_per_device,
-      num_scs, _rp_per_segment(rp, num_sc_per_device, num_minibatches),
+      num_scs, _rp_per_segment(rp, num_sc_per_device, num_scs, num_minibatches),
       int(num_minibatches), _p(act_grad), batch, _p(table), _p(acc), table.shape[0], dim, 0 if acc is None else 1,
       float(learning_rate), clip,
       float(min_value if min_value is not None else 0.0),
@@ -702,7 +703,7 @@ def sparse_dense_matmul_grad_optimizer(rp, eid, sid, gains, act_grad, table,
                                                  else 0)
   lib().ref_sparse_dense_matmul_grad_optimizer(
       _p(rp), _p(eid), _p(sid), _p(gains), len(eid), num_sc_per_device,
-      num_scs, _rp_per_segment(rp, num_sc_per_device, num_minibatches),
+      num_scs, _rp_per_segment(rp, num_sc_per_device, num_scs, num_minibatches),
       int(num_minibatches), _p(act_grad), batch, _p(table),
       _p(slots[0]) if n_slots > 0 else None,
       _p(slots[1]) if n_slots > 1 else None, table.shape[0], dim,

@@ -38,30 +38,34 @@ def test_library_exports_every_declared_symbol():
                                          (1703936, 1, 1)])
 def test_size_helpers_match_oracle(max_ids, g, s):
   lib = refcpu.lib()
-  assert pip.compute_theoretical_max_coo_buffer_size(max_ids, g, s) == \
-      lib.ref_theoretical_max_coo_buffer_size(max_ids, g, s)
-  for suggested in (0, 48, 96, 1024, 10**6):
-    exp = lib.ref_coo_buffer_size_per_device(max_ids, suggested, g, s)
-    got = _native.load_library().scemb_compute_coo_buffer_size_per_device(
-        max_ids, suggested, g, s)
-    assert got == exp
+  for mb in (False, True):
+    assert pip.compute_theoretical_max_coo_buffer_size(
+        max_ids, g, s, enable_minibatching=mb) == \
+        lib.ref_theoretical_max_coo_buffer_size_ex(max_ids, g, s, int(mb))
+    for suggested in (0, 48, 96, 1024, 10**6, 10**8):
+      exp = lib.ref_coo_buffer_size_per_device_ex(max_ids, suggested, g, s,
+                                                  int(mb))
+      got = _native.load_library().scemb_compute_coo_buffer_size_per_device(
+          max_ids, suggested, g, s, int(mb))
+      assert got == exp
   assert pip.compute_row_pointers_size_per_device(g, s) == max(g * s, 8) * s
+  # GetRowPointersSizePerDevice: 64 buckets with minibatching
+  # (input_preprocessing_util.h:497-511).
+  assert pip.compute_row_pointers_size_per_device(
+      g, s, enable_minibatching=True) == max(g * s, 8) * s * 64
 
 
 def test_size_helper_kats():
   """input_preprocessing_util_test.cc:99-133; pybind test :1992-2060."""
   assert pip.compute_theoretical_max_coo_buffer_size(16, 1, 4) == 256
   lib = _native.load_library()
-  assert lib.scemb_compute_coo_buffer_size_per_device(16, 48, 1, 4) == 64
-  assert lib.scemb_compute_coo_buffer_size_per_device(16, 96, 1, 4) == 96
-  assert lib.scemb_compute_coo_buffer_size_per_device(16, 1024, 1, 4) == -1
+  assert lib.scemb_compute_coo_buffer_size_per_device(16, 48, 1, 4, 0) == 64
+  assert lib.scemb_compute_coo_buffer_size_per_device(16, 96, 1, 4, 0) == 96
+  assert lib.scemb_compute_coo_buffer_size_per_device(16, 1024, 1, 4, 0) == -1
+  assert lib.scemb_compute_coo_buffer_size_per_device(16, 1024, 1, 4, 1) == \
+      1024
   assert pip.compute_row_pointers_size_per_device(1, 4) == 32
   assert pip.compute_row_pointers_size_per_device(4, 4) == 64
-
-
-def test_minibatching_not_implemented():
-  with pytest.raises(NotImplementedError):
-    pip.compute_row_pointers_size_per_device(1, 1, enable_minibatching=True)
 
 
 def test_primitive_validation_messages():
@@ -109,16 +113,34 @@ def test_primitive_validation_messages():
                                              max_value=1.0)
 
 
-def _sizing_call(build_view, local_devices, table_rows=1024):
+def _sizing_call(build_view, local_devices, table_rows=1024,
+                 enable_minibatching=0, minibatching_pass=0, split=0):
   """scemb_preprocess_workspace_size for one 64 x 2 dense feature (sizing
   only: no device memory is touched)."""
   lib = _native.load_library()
   feat = (_native.Feature * 1)()
   feat[0] = _native.Feature(None, None, None, None, 64, 128, 2, 0, 0, 0)
   opts = _native.PreprocessOptions(local_devices, local_devices, 1, 0, 512,
-                                   512, 0, 0, 512, 1024, int(build_view), 0,
-                                   table_rows)
+                                   512, 0, 0, 512, 1024, int(build_view),
+                                   enable_minibatching, table_rows,
+                                   minibatching_pass, 0, split)
   return int(lib.scemb_preprocess_workspace_size(feat, 1, ctypes.byref(opts)))
+
+
+def test_preprocess_minibatching_options():
+  """The bucket passes size 64 buckets per (SC, partition); a bad pass, a
+  split of 64 bits or a sample view with minibatching are refused."""
+  plain = _sizing_call(False, 1, enable_minibatching=1)
+  bucket = _sizing_call(False, 1, enable_minibatching=1, minibatching_pass=1)
+  assert plain > 0 and bucket > plain
+  assert _sizing_call(False, 1, enable_minibatching=1, minibatching_pass=2,
+                      split=0b101) > 0
+  assert _sizing_call(False, 1, enable_minibatching=1,
+                      minibatching_pass=3) == 0
+  assert b"minibatching_pass" in _native.load_library().scemb_last_error()
+  assert _sizing_call(True, 1, enable_minibatching=1) == 0
+  assert _sizing_call(False, 1, enable_minibatching=1, minibatching_pass=2,
+                      split=1 << 63) == 0
 
 
 def test_preprocess_sample_view_option():
