@@ -299,7 +299,8 @@ def _stack_batch_ids(w: Workload):
 
 
 def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
-            api: bool = True, other_optimizers: bool = True):
+            api: bool = True, other_optimizers: bool = True,
+            minibatching: bool = True):
   import torch  # pylint: disable=g-import-not-at-top
 
   from jax_tpu_embedding.sparsecore import _native  # pylint: disable=g-import-not-at-top
@@ -426,6 +427,13 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
     opt_ms = _optimizer_steps(pre, state, stacked, steps, warmup)
     log("backward + optimizer: " + ", ".join(
         f"{k} {v:.4f} ms" for k, v in opt_ms.items()))
+  mb = None
+  if minibatching and len(stacked) == 1:
+    mb = _minibatching_steps(w, feats_dev, weights_dev, state, stacked,
+                             steps, warmup)
+    log(f"minibatching ({mb['num_minibatches']} minibatches): preprocess "
+        f"{mb['preprocess_ms']:.3f} ms, step {mb['ms_per_step']:.4f} ms, "
+        f"dropped {mb['dropped']}")
   spans = {}
   for k in ("fwd_reduce", "fwd_finish", "bwd_reduce", "bwd_finish",
             "fwd_call", "bwd_call"):
@@ -445,6 +453,7 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
       "per_stack": per_stack,
       "dropped": int(sum(stats.id_drop_counters.values())),
       "optimizer_bwd_ms": opt_ms,
+      "minibatching": mb,
   }
 
 
@@ -505,6 +514,76 @@ def _optimizer_steps(pre, state, stacked, steps, warmup):
   del slots
   torch.cuda.empty_cache()
   return out
+
+
+# Stack limit for the minibatching leg: at the headline shape (1.7M entries
+# in one partition) it splits the 64 buckets into several minibatches without
+# dropping an id.
+MINIBATCH_LIMIT = 1 << 18
+
+
+def _minibatching_steps(w, feats_dev, weights_dev, state, stacked, steps,
+                        warmup):
+  """The headline stack with enable_minibatching and limits of
+  MINIBATCH_LIMIT ids per partition: the three-pass preprocessing (median of
+  5 after 2 warmups, host time including its two device waits) and the
+  forward + Adagrad step over the minibatched CSR (sorted route; the
+  in-place CSR backward and the sample view do not apply to that layout)."""
+  import torch  # pylint: disable=g-import-not-at-top
+
+  from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_csr as fwd  # pylint: disable=g-import-not-at-top
+  from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_adagrad as ada  # pylint: disable=g-import-not-at-top
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-import-not-at-top
+
+  (name, spec), = stacked.items()
+  saved = [fs.table_spec.stacked_table_spec for fs in w.feature_specs]
+  for fs, st in zip(w.feature_specs, saved):
+    fs.table_spec.stacked_table_spec = st.replace(
+        max_ids_per_partition=MINIBATCH_LIMIT,
+        max_unique_ids_per_partition=MINIBATCH_LIMIT,
+        suggested_coo_buffer_size_per_device=None)
+  try:
+    times = []
+    for i in range(7):
+      torch.cuda.synchronize()
+      t0 = time.perf_counter()
+      pre, stats = embedding.preprocess_sparse_dense_matmul_input(
+          feats_dev, weights_dev, w.feature_specs, 1, 1, num_sc_per_device=1,
+          enable_minibatching=True)
+      torch.cuda.synchronize()
+      if i >= 2:
+        times.append(time.perf_counter() - t0)
+  finally:
+    for fs, st in zip(w.feature_specs, saved):
+      fs.table_spec.stacked_table_spec = st
+  nmb = int(pre.num_minibatches[0])
+  t, a, g, lr = state[name]
+  csr = (pre.lhs_row_pointers[name], pre.lhs_embedding_ids[name],
+         pre.lhs_sample_ids[name], pre.lhs_gains[name])
+  kw = dict(max_ids_per_partition=MINIBATCH_LIMIT,
+            max_unique_ids_per_partition=MINIBATCH_LIMIT, num_sc_per_device=1,
+            enable_minibatching=True,
+            csr_num_entries=pre.csr_num_entries[name])
+
+  def step():
+    fwd.tpu_sparse_dense_matmul_csr_primitive.bind(
+        *csr, nmb, t, device_batch_size=spec.total_sample_count, **kw)
+    ada.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
+        *csr, nmb, t, a, g, lr, **kw)
+
+  for _ in range(warmup):
+    step()
+  torch.cuda.synchronize()
+  t0 = time.perf_counter()
+  for _ in range(steps):
+    step()
+  torch.cuda.synchronize()
+  ms = (time.perf_counter() - t0) * 1e3 / steps
+  return {"num_minibatches": nmb,
+          "max_ids_per_partition": MINIBATCH_LIMIT,
+          "preprocess_ms": float(np.median(times) * 1e3),
+          "ms_per_step": ms,
+          "dropped": int(sum(stats.id_drop_counters.values()))}
 
 
 def _api_steps(w, pre, state, stacked, steps, warmup, timed_fn):
@@ -723,6 +802,8 @@ def main():
                   help="skip timing the step through the embedding API")
   ap.add_argument("--no-optimizer-steps", action="store_true",
                   help="skip timing the backward with the other optimizers")
+  ap.add_argument("--no-minibatching", action="store_true",
+                  help="skip the minibatching leg (headline stack only)")
   ap.add_argument("--workload", default="c2", choices=sorted(WORKLOADS),
                   help="BASELINE.json config (c2, the 26-table DLRM shape, "
                        "is the headline)")
@@ -739,7 +820,8 @@ def main():
                 # The headline stack only (two more table-sized slots do not
                 # fit next to config 4's 205 GB table and accumulator).
                 other_optimizers=(not args.no_optimizer_steps and
-                                  w.name == "dlrm26"))
+                                  w.name == "dlrm26"),
+                minibatching=not args.no_minibatching and w.name == "dlrm26")
   fwd_bytes, bwd_bytes = algorithmic_bytes(res["per_stack"])
   step_s = res["ms_per_step"] / 1e3
   sp = res["spans"]
@@ -817,6 +899,19 @@ def main():
         k: {"ms": round(v, 4),
             "hbm_frac": round(two_slot / (v / 1e3) / 1e9 / PEAK_HBM_GBS, 4)}
         for k, v in res["optimizer_bwd_ms"].items()}
+  if res["minibatching"]:
+    # Same entries (nothing dropped), so the same compulsory bytes.
+    mb = res["minibatching"]
+    out["minibatching"] = {
+        "num_minibatches": mb["num_minibatches"],
+        "max_ids_per_partition": mb["max_ids_per_partition"],
+        "preprocess_ms": round(mb["preprocess_ms"], 3),
+        "ms_per_step": round(mb["ms_per_step"], 4),
+        "step_hbm_frac": round((fwd_bytes + bwd_bytes) /
+                               (mb["ms_per_step"] / 1e3) / 1e9 /
+                               PEAK_HBM_GBS, 4),
+        "dropped": mb["dropped"],
+    }
   print(json.dumps(out), flush=True)
 
 

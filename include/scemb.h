@@ -105,7 +105,12 @@ typedef struct scemb_csr {
                           row or more); the buffer size stands in when 0 */
   int32_t num_minibatches; /* 0: one block per segment (no minibatching);
                               1..64: the minibatching layout */
-  int32_t reserved;
+  int32_t positions_used;  /* minibatching layout: every entry lies below
+                              this buffer position (0: anywhere below
+                              coo_size). The buffer is sized for 64
+                              minibatches; a bound from the preprocessing
+                              (entries + 7 per (SC, minibatch, partition),
+                              rounded up to 8) spares the lookup the rest. */
 } scemb_csr_t;
 
 /* The entries of each segment are ascending by (partition, embedding id), as

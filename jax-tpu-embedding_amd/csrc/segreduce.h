@@ -155,6 +155,7 @@ struct Csr {
   int32_t rp_per_segment;
   int32_t num_minibatches;  // 0: one block per segment, relative positions
   int64_t coo_size;
+  int64_t positions;        // minibatching layout: positions holding entries
 };
 
 __device__ __forceinline__ uint64_t Pack(uint32_t lo, float g) {
@@ -184,7 +185,7 @@ __device__ __forceinline__ int PartitionOf(const int32_t* rp, int nparts,
 
 // COO positions of a CSR (the whole buffer in the minibatching layout).
 __device__ __forceinline__ int64_t CsrPositions(const Csr& csr) {
-  return csr.num_minibatches > 0 ? csr.coo_size
+  return csr.num_minibatches > 0 ? csr.positions
                                  : csr.per_segment * csr.num_segments;
 }
 
@@ -1003,6 +1004,8 @@ struct Geometry {
   int64_t rows_per_partition;
 };
 
+int64_t MinibatchPositions(const scemb_csr_t& csr);
+
 int CheckCsr(const scemb_csr_t* csr, int64_t batch, int64_t table_rows,
              int32_t dim, Geometry* geo) {
   if (csr == nullptr) return Fail(SCEMB_ERR_INVALID_ARGUMENT, "csr is null");
@@ -1032,8 +1035,11 @@ int CheckCsr(const scemb_csr_t* csr, int64_t batch, int64_t table_rows,
     return Fail(SCEMB_ERR_INVALID_ARGUMENT,
                 "num_minibatches must be in [0, 64]");
   }
+  if (csr->positions_used < 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "positions_used is negative");
+  }
   const int64_t per_seg = csr->coo_size / csr->num_segments;
-  geo->n = csr->num_minibatches > 0 ? csr->coo_size
+  geo->n = csr->num_minibatches > 0 ? MinibatchPositions(*csr)
                                     : per_seg * csr->num_segments;
   if (geo->n >= (int64_t{1} << 31) - 1) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT, "coo buffer too large");
@@ -1048,6 +1054,12 @@ int CheckCsr(const scemb_csr_t* csr, int64_t batch, int64_t table_rows,
   return 0;
 }
 
+int64_t MinibatchPositions(const scemb_csr_t& csr) {
+  return csr.positions_used > 0 && csr.positions_used < csr.coo_size
+             ? csr.positions_used
+             : csr.coo_size;
+}
+
 Csr MakeCsr(const scemb_csr_t* csr) {
   Csr c;
   c.rp = csr->row_pointers;
@@ -1060,6 +1072,7 @@ Csr MakeCsr(const scemb_csr_t* csr) {
   c.rp_per_segment = csr->row_pointers_per_segment;
   c.num_minibatches = csr->num_minibatches;
   c.coo_size = csr->coo_size;
+  c.positions = MinibatchPositions(*csr);
   return c;
 }
 

@@ -86,7 +86,7 @@ class Csr(ctypes.Structure):
       ("flags", ctypes.c_uint32),
       ("num_entries", ctypes.c_int64),
       ("num_minibatches", ctypes.c_int32),
-      ("reserved", ctypes.c_int32),
+      ("positions_used", ctypes.c_int32),
   ]
 
 
@@ -385,12 +385,13 @@ def make_csr(row_pointers, embedding_ids, sample_ids, gains, num_segments,
              num_partitions, sorted_by_row: bool = False,
              num_entries: int | None = None,
              one_entry_per_row: bool = False,
-             num_minibatches: int = 0) -> Csr:
+             num_minibatches: int = 0, positions_used: int = 0) -> Csr:
   """`num_entries`: the valid entries of the buffers when known (it only
   picks kernel variants). `sorted_by_row` / `one_entry_per_row` set
   CSR_SORTED_BY_ROW / CSR_ONE_ENTRY_PER_ROW. `num_minibatches` > 0: the
   buffers are in the minibatching layout (row pointers of 64 blocks per
-  segment)."""
+  segment); `positions_used` then bounds the positions holding entries (0:
+  the whole buffer)."""
   rp_len = int(row_pointers.numel())
   if not 0 <= num_minibatches <= MAX_MINIBATCHES:
     raise ValueError("num_minibatches must be in [0, 64]")
@@ -413,7 +414,8 @@ def make_csr(row_pointers, embedding_ids, sample_ids, gains, num_segments,
              num_partitions, per_block,
              (CSR_SORTED_BY_ROW if sorted_by_row else 0) |
              (CSR_ONE_ENTRY_PER_ROW if one_entry_per_row else 0),
-             int(num_entries) if num_entries else 0, int(num_minibatches), 0)
+             int(num_entries) if num_entries else 0, int(num_minibatches),
+             int(positions_used) if num_minibatches else 0)
 
 
 class LookupView:

@@ -28,17 +28,26 @@ def csr_operands(row_pointers, embedding_ids, sample_ids, gains,
   `one_entry_per_row` at most one entry per activation row (one-hot input
   rows), which turns the grouping by activation row into a placement;
   `num_minibatches` > 0 the minibatching layout with that many minibatches
-  per SparseCore."""
+  per SparseCore (with `num_entries`, the positions past the bound on what
+  the preprocessing wrote are skipped)."""
   t = _native.require_gpu()
   dev = _native.device()
   rp = _native.as_device_tensor(row_pointers, t.int32, dev).reshape(-1)
   eid = _native.as_device_tensor(embedding_ids, t.int32, dev).reshape(-1)
   sid = _native.as_device_tensor(sample_ids, t.int32, dev).reshape(-1)
   g = _native.as_device_tensor(gains, t.float32, dev).reshape(-1)
+  used = 0
+  if num_minibatches and num_entries:
+    # Entries plus at most 7 alignment positions per (SC, minibatch,
+    # partition), the last rounded up to 8.
+    used = -(-(int(num_entries) + 7 * num_sc_per_device * num_minibatches *
+                num_partitions) // 8) * 8
+    used = used if used < 2**31 - 1 else 0
   csr = _native.make_csr(rp, eid, sid, g, num_sc_per_device, num_partitions,
                          sorted_by_row=sorted_by_row, num_entries=num_entries,
                          one_entry_per_row=one_entry_per_row,
-                         num_minibatches=num_minibatches)
+                         num_minibatches=num_minibatches,
+                         positions_used=used)
   return (rp, eid, sid, g), csr
 
 

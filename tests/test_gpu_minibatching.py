@@ -234,6 +234,39 @@ def test_lookup_and_update_over_minibatches(num_sc, dim):
   np.testing.assert_allclose(acc.cpu().numpy(), exp_a, rtol=RTOL, atol=ATOL)
 
 
+def test_entry_bound_skips_the_unused_buffer():
+  """The buffer is sized for 64 minibatches; with the preprocessing's entry
+  count the lookup and update only visit the positions the minibatches can
+  use. Same results, bit for bit, as over the whole buffer."""
+  rng = np.random.default_rng(17)
+  batch, vocab, dim, limit = 4096, 50000, 16, 4096
+  specs = _specs([("a", vocab, dim)], batch, (limit, limit), 1)
+  feats = [_ragged(rng, batch, 1, 8, vocab)]
+  got, _ = _compare(feats, None, specs, 1, allow=False)
+  name = specs[0].table_spec.stacked_table_spec.stack_name
+  (rp, eid, sid, gains), nmb = _csr_args(got, name)
+  entries = got[5].num_entries[name]
+  assert nmb > 1 and 0 < 8 * entries < eid.numel()
+  table = rng.normal(size=(vocab, dim)).astype(np.float32)
+  grad = torch.tensor(rng.normal(size=(batch, dim)).astype(np.float32)).cuda()
+  kw = dict(max_ids_per_partition=limit, max_unique_ids_per_partition=limit,
+            num_sc_per_device=1, global_device_count=1,
+            enable_minibatching=True)
+  outs = []
+  for n in (None, entries):
+    act = fwd_prim.tpu_sparse_dense_matmul_csr_primitive.bind(
+        rp, eid, sid, gains, nmb, torch.tensor(table).cuda(),
+        device_batch_size=batch, csr_num_entries=n, **kw)
+    tab = torch.tensor(table).cuda()
+    acc = torch.full((vocab, dim), 0.1, device="cuda")
+    adagrad_prim.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
+        rp, eid, sid, gains, nmb, tab, acc, grad, 0.05,
+        computation_name="adagrad", csr_num_entries=n, **kw)
+    outs.append([x.cpu().numpy() for x in (act, tab, acc)])
+  for a, b in zip(*outs):
+    np.testing.assert_array_equal(a, b)
+
+
 # ---------------------------------------------------------------------------
 # The reference's minibatching tests.
 # ---------------------------------------------------------------------------
