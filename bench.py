@@ -527,8 +527,8 @@ def _minibatching_steps(w, feats_dev, weights_dev, state, stacked, steps,
   """The headline stack with enable_minibatching and limits of
   MINIBATCH_LIMIT ids per partition: the three-pass preprocessing (median of
   5 after 2 warmups, host time including its two device waits) and the
-  forward + Adagrad step over the minibatched CSR (sorted route; the
-  in-place CSR backward and the sample view do not apply to that layout)."""
+  forward + Adagrad step over the minibatched CSR (the forward from the
+  preprocessing's sample view, the backward reading the CSR in place)."""
   import torch  # pylint: disable=g-import-not-at-top
 
   from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_csr as fwd  # pylint: disable=g-import-not-at-top
@@ -567,9 +567,10 @@ def _minibatching_steps(w, feats_dev, weights_dev, state, stacked, steps,
 
   def step():
     fwd.tpu_sparse_dense_matmul_csr_primitive.bind(
-        *csr, nmb, t, device_batch_size=spec.total_sample_count, **kw)
+        *csr, nmb, t, device_batch_size=spec.total_sample_count,
+        lookup_view=pre.lookup_views[name], **kw)
     ada.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
-        *csr, nmb, t, a, g, lr, **kw)
+        *csr, nmb, t, a, g, lr, csr_sorted_by_row=pre.csr_sorted_by_row, **kw)
 
   for _ in range(warmup):
     step()

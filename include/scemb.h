@@ -117,7 +117,10 @@ typedef struct scemb_csr {
  * the preprocessing writes them (input_preprocessing_util.cc:167-208 sorts by
  * the rotated column id). With one segment the backward pass then reads the
  * CSR in place instead of sorting it; order violations are reported through
- * SCEMB_STATUS_UNSORTED. */
+ * SCEMB_STATUS_UNSORTED. In the minibatching layout the flag declares that
+ * every table row's entries are contiguous (one local SparseCore: a column
+ * falls in one bucket, so in one minibatch, where it is sorted), which is not
+ * checked. */
 #define SCEMB_CSR_SORTED_BY_ROW 1u
 
 /* At most one valid entry per activation row (every input row of the stack

@@ -1035,10 +1035,6 @@ int MakePlan(const scemb_feature_t* feats, int nf,
       return Fail(SCEMB_ERR_INVALID_ARGUMENT,
                   "minibatching_pass must be 0, 1 or 2");
     }
-    if (o->build_sample_view) {
-      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
-                  "the sample view is not built with minibatching");
-    }
   }
   pl->L = L;
   pl->G = G;
@@ -1261,7 +1257,8 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                         ? ws.Take<float>(pl.total_rows)
                         : nullptr;
   ViewParts view{};
-  if (o->build_sample_view) {
+  // The bucket pass writes no CSR, so no view either.
+  if (o->build_sample_view && !(minibatching && pass == 1)) {
     if (pl.L != 1 || pl.G != 1) {
       return Fail(SCEMB_ERR_INVALID_ARGUMENT,
                   "the sample view needs one local and one global device");

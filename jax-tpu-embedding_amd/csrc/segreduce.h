@@ -381,8 +381,11 @@ __device__ __forceinline__ uint32_t FetchEntry(const StreamArgs& s, int64_t e,
     return k;
   } else {
     *ent = 0;
-    const int p = PartitionOf(s.csr.rp, s.csr.num_partitions,
-                              s.csr.per_segment, e);
+    int seg = 0;
+    const int p = s.csr.num_minibatches > 0
+                      ? LocateEntry(s.csr, e, &seg)
+                      : PartitionOf(s.csr.rp, s.csr.num_partitions,
+                                    s.csr.per_segment, e);
     if (p < 0) return kSkip;
     const int32_t id = s.csr.eid[e];
     const int32_t sm = s.csr.sid[e];
@@ -698,8 +701,12 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
     bool tail;
     if (SRC == kSrcCsr) {
       int64_t end = 0;
-      for (int q = 0; q < st.csr.num_partitions; ++q) {
-        end = st.csr.rp[q] > end ? st.csr.rp[q] : end;
+      if (st.csr.num_minibatches > 0) {
+        end = n;  // entries may lie anywhere below the positions bound
+      } else {
+        for (int q = 0; q < st.csr.num_partitions; ++q) {
+          end = st.csr.rp[q] > end ? st.csr.rp[q] : end;
+        }
       }
       tail = cb >= end;
     } else {
@@ -740,7 +747,10 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
   const bool mine = cl < cnt;
   const bool valid = mine && my_key != kSkip;
 
-  if (r.status != nullptr && mine) {
+  // A minibatched CSR is contiguous by row but not ascending (a minibatch's
+  // buckets follow each other); that cannot be checked locally.
+  if (r.status != nullptr && mine &&
+      (SRC != kSrcCsr || st.csr.num_minibatches == 0)) {
     const bool bad = SRC == kSrcCsr
                          ? (valid && prev_key != kSkip && prev_key > my_key)
                          : (cb + tid > 0 && prev_key > my_key);
@@ -1190,8 +1200,7 @@ int GradImpl(const GradCall& c) {
   if (rc != 0) return rc;
   const int64_t n = geo.n;
   const bool direct =
-      (csr->flags & SCEMB_CSR_SORTED_BY_ROW) != 0 && csr->num_segments == 1 &&
-      csr->num_minibatches == 0;
+      (csr->flags & SCEMB_CSR_SORTED_BY_ROW) != 0 && csr->num_segments == 1;
   StreamArgs st{};
   st.n = n;
   if (direct) {

@@ -90,8 +90,6 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
                                    lhs_local_sample_ids, lhs_gains, s, ns,
                                    num_entries=csr_num_entries,
                                    num_minibatches=nmb)
-  if nmb:
-    lookup_view = None  # views are built for the per-SC layout
   table = _device.device_table(embedding_table)
   shape = ((device_batch_size,) if table.dim() == 1 else
            (device_batch_size, int(table.shape[1])))

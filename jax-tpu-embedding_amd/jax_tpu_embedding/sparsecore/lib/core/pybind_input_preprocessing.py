@@ -266,13 +266,13 @@ def _preprocess_stack(feats, metas, *, local_device_count,
                       global_device_count, num_sc_per_device,
                       allow_id_dropping, has_weights, build_view=False,
                       enable_minibatching=False, minibatching_pass=0,
-                      minibatching_split=0, outputs=None):
+                      minibatching_split=0, outputs=None, view_outputs=None):
   """Enqueues one stacked table (one minibatching pass of it with
   `enable_minibatching`); returns (rp, eid, sid, gains, stats on the
   device, (L, S, NS, counters offset), view) where view is the
   (keys, entries) pair of the CSR's sample view when `build_view`, else
-  None. `outputs`: the (rp, eid, sid, gains) of an earlier pass to write
-  into."""
+  None. `outputs` / `view_outputs`: the (rp, eid, sid, gains) / view of an
+  earlier pass to write into."""
   t = _native.require_gpu()
   lib = _native.load_library()
   dev = _native.device()
@@ -316,8 +316,8 @@ def _preprocess_stack(feats, metas, *, local_device_count,
   stats = t.zeros(nstats + 2, dtype=t.int32, device=dev)
   view = None
   if build_view:
-    view = (t.empty(c, dtype=t.int32, device=dev),
-            t.empty(c, dtype=t.int64, device=dev))
+    view = view_outputs or (t.empty(c, dtype=t.int32, device=dev),
+                            t.empty(c, dtype=t.int64, device=dev))
   out = _native.PreprocessOutput(
       _native.ptr(rp), _native.ptr(eid), _native.ptr(sid), _native.ptr(gains),
       _native.ptr(stats), None if view is None else _native.ptr(view[0]),
@@ -426,7 +426,7 @@ def _raise_on_counters(name, counters):
         "batch size.")
 
 
-def _minibatching_passes(pending, jobs, csr):
+def _minibatching_passes(pending, jobs, csr, views):
   """Runs the rest of input_preprocessing.cc:852-929 after every stack's
   first pass: if one of them exceeds a limit, the bucket pass of every
   stack, the OR of their splits, and the minibatched fill of every stack.
@@ -446,7 +446,9 @@ def _minibatching_passes(pending, jobs, csr):
     split |= int(np.uint64(c[5]))
   for name, kwargs in jobs:
     out = _preprocess_stack(**kwargs, minibatching_pass=2,
-                            minibatching_split=split, outputs=csr[name])
+                            minibatching_split=split, outputs=csr[name],
+                            build_view=name in views,
+                            view_outputs=views.get(name))
     pending.final_pass_stats[name] = (out[4], out[5][3])
   pending.num_minibatches = bin(split).count("1") + 1
 
@@ -464,14 +466,14 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
   `sample_views` dict (one local and one global device only), each stack's
   sample view (keys, entries) is built along and stored there. With
   `enable_minibatching` the minibatching passes run here (they wait for the
-  device) and `pending.num_minibatches` holds the outcome; no sample view is
-  built."""
+  device) and `pending.num_minibatches` holds the outcome; a sample view is
+  rebuilt by the pass that writes the final CSR."""
   stacks = get_stacked_table_metadata(feature_specs)
   rps, eids, sids, gns = {}, {}, {}, {}
   pending = PendingStats()
   jobs, flat = [], {}
   build_view = (sample_views is not None and local_device_count == 1 and
-                global_device_count == 1 and not enable_minibatching)
+                global_device_count == 1)
   for name, metas in stacks.items():
     feats = [
         _to_device_feature(
@@ -498,7 +500,8 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
                              sid.reshape(L, -1), gains.reshape(L, -1))
     rps[name], eids[name], sids[name], gns[name] = rp, eid, sid, gains
   if enable_minibatching:
-    _minibatching_passes(pending, jobs, flat)
+    _minibatching_passes(pending, jobs, flat,
+                         sample_views if sample_views is not None else {})
   return rps, eids, sids, gns, pending
 
 

@@ -106,8 +106,9 @@ class PreprocessedInput:
     lookup_views: stack name -> _native.LookupView, the CSR entries grouped
       by activation row (spares the forward pass its grouping sort);
     csr_sorted_by_row: the CSR entries are ascending by (partition, embedding
-      id) in every segment, as the preprocessing writes them (lets the
-      backward pass read the CSR in place);
+      id) in every segment, as the preprocessing writes them (with
+      minibatching: every row's entries contiguous); lets the backward pass
+      read the CSR in place;
     csr_num_entries: stack name -> number of CSR entries (lets the lookup
       pick the kernel variant for one-hot or multi-hot batches).
   A PreprocessedInput built from other CSR buffers leaves both unset.
@@ -314,7 +315,7 @@ def preprocess_sparse_dense_matmul_input(
       allow_id_dropping=allow_id_dropping, sample_views=built,
       enable_minibatching=enable_minibatching)
   views = None
-  if local_device_count == 1 and not enable_minibatching:
+  if local_device_count == 1:
     # One device: the preprocessing wrote each stack's sample view along with
     # its CSR; otherwise (several global devices) it is built from the CSR.
     stacked = get_stacked_table_specs(feature_specs)
@@ -327,13 +328,21 @@ def preprocess_sparse_dense_matmul_input(
     if missing:
       views.update(_build_lookup_views(
           csr, feature_specs, global_device_count, num_sc_per_device,
-          pybind_input_preprocessing.one_id_per_row(pending), only=missing))
+          pybind_input_preprocessing.one_id_per_row(pending), only=missing,
+          num_minibatches=(pending.num_minibatches if enable_minibatching
+                           else 0)))
   stats = pybind_input_preprocessing.collect_stats(pending)
   counts = None
   if local_device_count == 1:
     counts = dict(stats.num_entries)
     for name, view in (views or {}).items():
       view.num_entries = counts.get(name, 0)
+      if enable_minibatching and view.num_entries:
+        # The view has room for a buffer sized for 64 minibatches; past the
+        # entries it holds only unused keys.
+        used = -(-view.num_entries // 256) * 256
+        if used < view.keys.numel():
+          view.keys, view.entries = view.keys[:used], view.entries[:used]
   minibatches = np.full(local_device_count, pending.num_minibatches,
                         dtype=np.int32)
   if has_leading_dimension:
@@ -381,7 +390,7 @@ def preprocess_sparse_dense_matmul_input_from_sparse_tensor(
 
 def _build_lookup_views(csr, feature_specs, global_device_count: int,
                         num_sc_per_device: int, one_per_row: dict,
-                        only=None):
+                        only=None, num_minibatches: int = 0):
   """Sample views of one device's CSR buffers, one per stacked table (those
   named in `only`, when given), for a table shard of
   stack_vocab_size / global_device_count rows."""
@@ -395,7 +404,8 @@ def _build_lookup_views(csr, feature_specs, global_device_count: int,
     _, c = _device.csr_operands(rp[name], eid[name], sid[name], gains[name],
                                 num_sc_per_device,
                                 num_sc_per_device * global_device_count,
-                                one_entry_per_row=one_per_row.get(name, False))
+                                one_entry_per_row=one_per_row.get(name, False),
+                                num_minibatches=num_minibatches)
     views[name] = _native.build_sample_view(c, batch, rows)
   return views
 

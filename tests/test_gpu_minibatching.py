@@ -253,18 +253,27 @@ def test_entry_bound_skips_the_unused_buffer():
             num_sc_per_device=1, global_device_count=1,
             enable_minibatching=True)
   outs = []
-  for n in (None, entries):
+  # Whole buffer, sorted backward; bounded, sorted (the same sorted stream:
+  # equal bit for bit); bounded, the CSR read in place (one SparseCore: every
+  # row's entries are contiguous; a row is summed in the same order but split
+  # into pieces at other positions, so to rounding).
+  for n, in_place in ((None, False), (entries, False), (entries, True)):
     act = fwd_prim.tpu_sparse_dense_matmul_csr_primitive.bind(
         rp, eid, sid, gains, nmb, torch.tensor(table).cuda(),
         device_batch_size=batch, csr_num_entries=n, **kw)
     tab = torch.tensor(table).cuda()
     acc = torch.full((vocab, dim), 0.1, device="cuda")
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
     adagrad_prim.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
         rp, eid, sid, gains, nmb, tab, acc, grad, 0.05,
-        computation_name="adagrad", csr_num_entries=n, **kw)
+        computation_name="adagrad", csr_num_entries=n,
+        csr_sorted_by_row=in_place, **kw)
     outs.append([x.cpu().numpy() for x in (act, tab, acc)])
-  for a, b in zip(*outs):
+  for a, b in zip(outs[0], outs[1]):
     np.testing.assert_array_equal(a, b)
+  for a, b in zip(outs[0], outs[2]):
+    np.testing.assert_allclose(a, b, rtol=RTOL, atol=ATOL)
+  del status
 
 
 # ---------------------------------------------------------------------------
@@ -380,6 +389,41 @@ def test_nn_id_dropping_counted():
   for limits in ((1, 1), (10, 1)):
     _, _, _, stats, _ = _nn_case(limits, batch=64, max_sample=8)
     assert stats.id_drop_counters["table_a"] > 0
+
+
+def test_nn_views_and_in_place_backward_match_the_plain_csr():
+  """Through the embedding API the minibatched step takes the sample view
+  built by the final pass (trimmed to the entries) and the in-place
+  backward; the same CSR without them (sorting in every call) gives the same
+  tables and activations (rtol 1e-5: the view orders a row's entries by
+  input position, the sorted CSR by column; the in-place backward splits a
+  row's sum at other positions)."""
+  feature, _, pre, _, num_sc = _nn_case((64, 64), batch=64)
+  assert (pre.num_minibatches > 1).all()
+  name = feature.table_spec.stacked_table_spec.stack_name
+  view = pre.lookup_views[name]
+  assert view is not None and view.keys.numel() < (
+      pre.sparse_dense_matmul_input.lhs_embedding_ids[name].numel())
+  rng = np.random.default_rng(2)
+  table = rng.normal(size=(2048, 16)).astype(np.float32)
+  grads = torch.tensor(rng.normal(size=(64, 16)).astype(np.float32)).cuda()
+  results = []
+  for plain in (False, True):
+    p = pre
+    if plain:
+      p = embedding.PreprocessedInput(pre.sparse_dense_matmul_input,
+                                      pre.num_minibatches)
+    variables = {name: embedding.EmbeddingVariables(
+        table=torch.tensor(table).cuda(), slot=())}
+    acts = embedding.tpu_sparse_dense_matmul(
+        p, variables, [feature], global_device_count=1,
+        num_sc_per_device=num_sc, enable_minibatching=True)
+    upd = embedding.tpu_sparse_dense_matmul_grad(
+        [grads], p, variables, [feature], num_sc_per_device=num_sc,
+        enable_minibatching=True)
+    results.append((acts[0].cpu().numpy(), upd[name].table.cpu().numpy()))
+  for a, b in zip(results[0], results[1]):
+    np.testing.assert_allclose(a, b, rtol=RTOL, atol=ATOL)
 
 
 def test_nn_forward_and_backward():
