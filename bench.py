@@ -660,7 +660,8 @@ def _head(x, rows):
   return np.asarray(x)[:rows]
 
 
-def cpu_baseline(w: Workload, sample_batch: int, seconds: float):
+def cpu_baseline(w: Workload, sample_batch: int, seconds: float,
+                 minibatching: bool = False):
   """The oracle (C++ restatement of the reference CPU path) on host cores,
   on the first `sample_batch` samples of every feature."""
   import copy  # pylint: disable=g-import-not-at-top
@@ -703,6 +704,24 @@ def cpu_baseline(w: Workload, sample_batch: int, seconds: float):
   t0 = time.perf_counter()
   ref = refcpu.preprocess(feats, weights, specs, 1, 1, num_sc_per_device=1)
   pre_s = time.perf_counter() - t0
+  mb = None
+  if minibatching and len(stacked) == 1:
+    # The minibatching passes on the sample, with the limit scaled to the
+    # sample so that the split is alike.
+    limit = max(8, MINIBATCH_LIMIT * sample_batch // batch)
+    mb_specs = []
+    for fs in specs:
+      nfs = copy.copy(fs)
+      nfs.table_spec = copy.copy(fs.table_spec)
+      nfs.table_spec.stacked_table_spec = (
+          fs.table_spec.stacked_table_spec.replace(
+              max_ids_per_partition=limit, max_unique_ids_per_partition=limit,
+              suggested_coo_buffer_size_per_device=None))
+      mb_specs.append(nfs)
+    t0 = time.perf_counter()
+    mb_ref = refcpu.preprocess(feats, weights, mb_specs, 1, 1,
+                               num_sc_per_device=1, enable_minibatching=True)
+    mb = (time.perf_counter() - t0, mb_ref.num_minibatches, limit)
   total_lookups = sum(int(f.size) if not isinstance(f, np.ndarray) or
                       f.dtype != object else sum(len(r) for r in f)
                       for f in feats)
@@ -750,6 +769,12 @@ def cpu_baseline(w: Workload, sample_batch: int, seconds: float):
                  f"preprocessing of the sample {pre_s * 1e3:.1f} ms on 1 "
                  "thread"),
       "preprocess_ms_per_1k_lookups": pre_s * 1e3 / total_lookups * 1e3,
+      # The oracle's minibatching passes on the same sample (1 thread).
+      "minibatching_preprocess_ms_per_1k_lookups": (
+          mb[0] * 1e3 / total_lookups * 1e3 if mb else None),
+      "minibatching_sample": (
+          f"limit {mb[2]} ids per partition, {mb[1]} minibatches"
+          if mb else None),
   }
 
 
@@ -855,7 +880,8 @@ def main():
   }
   cpu = None
   if not args.no_cpu_baseline:
-    cpu = cpu_baseline(w, args.cpu_sample_batch, args.cpu_seconds)
+    cpu = cpu_baseline(w, args.cpu_sample_batch, args.cpu_seconds,
+                       minibatching=res["minibatching"] is not None)
   spans = {k: round(v[0], 4) for k, v in res["spans"].items()}
   out = {
       "metric": METRIC if w.name == "dlrm26" else METRIC.replace(
