@@ -409,6 +409,8 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
   for _ in range(warmup):
     step()
   ms_per_step = timed(steps, False)
+  graph_ms = _graph_steps(step, steps, warmup)
+  log(f"step replayed from a HIP graph: {graph_ms:.4f} ms")
   # Kernel durations from HIP events on the launch stream, in a second pass
   # of the same steps (the events themselves cost a few microseconds each,
   # so the timed pass above runs without them).
@@ -447,6 +449,7 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
       "api_copy_ms_per_step": api_copy_ms,
       "csr_only_ms_per_step": csr_only_ms,
       "ms_per_step": ms_per_step,
+      "graph_ms_per_step": graph_ms,
       "lookups": lookups,
       "preprocess_ms": preprocess_ms,
       "spans": spans,
@@ -455,6 +458,32 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
       "optimizer_bwd_ms": opt_ms,
       "minibatching": mb,
   }
+
+
+def _graph_steps(step, steps, warmup):
+  """The same step captured once in a HIP graph (torch.cuda.CUDAGraph) and
+  replayed: the kernels of a step, without the host work of each call (the
+  step only launches kernels, so it captures as is). ms per replay."""
+  import torch  # pylint: disable=g-import-not-at-top
+
+  side = torch.cuda.Stream()
+  side.wait_stream(torch.cuda.current_stream())
+  with torch.cuda.stream(side):
+    step()
+  torch.cuda.current_stream().wait_stream(side)
+  g = torch.cuda.CUDAGraph()
+  with torch.cuda.graph(g):
+    step()
+  for _ in range(warmup):
+    g.replay()
+  torch.cuda.synchronize()
+  t0 = time.perf_counter()
+  for _ in range(steps):
+    g.replay()
+  torch.cuda.synchronize()
+  ms = (time.perf_counter() - t0) * 1e3 / steps
+  del g
+  return ms
 
 
 # Every built-in optimizer spec with two slot variables, at its defaults.
@@ -893,6 +922,8 @@ def main():
       "warmup": args.warmup,
       "ms_per_step": round(res["ms_per_step"], 4),
       "csr_only_ms_per_step": round(res["csr_only_ms_per_step"], 4),
+      # The step replayed from a HIP graph (no per-call host work).
+      "graph_ms_per_step": round(res["graph_ms_per_step"], 4),
       # The same step through the embedding API with per-feature tensors:
       # stacking fused into the kernels, and with unstack / stack copies.
       "api_ms_per_step": (round(res["api_ms_per_step"], 4)

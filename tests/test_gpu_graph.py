@@ -1,0 +1,116 @@
+"""The training step captured in a HIP graph (torch.cuda.CUDAGraph).
+
+The lookup and the fused backward only launch kernels on the current stream
+(no allocation, memset, copy or host wait; the workspace is the caller's), so
+a whole step can be captured once and replayed. Each replay must equal the
+eager step bit for bit: the test replays four times, with eager work and
+synchronisations between the replays, and compares every replay's
+activations, table and accumulator with an eager twin advanced step by step.
+"""
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+  if not torch.cuda.is_available():
+    pytest.skip("no GPU")
+  torch.cuda.set_device(0)
+
+
+from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-import-not-at-top,wrong-import-position
+from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top,wrong-import-position
+
+
+def _workload(one_hot, seed=0):
+  rng = np.random.default_rng(seed)
+  batch, dim = 2048, 32
+  tables = [embedding_spec.TableSpec(
+      name=f"t{i}", vocabulary_size=int(v), embedding_dim=dim,
+      initializer=embedding_spec.zeros,
+      optimizer=embedding_spec.AdagradOptimizerSpec(0.05), combiner="sum",
+      max_ids_per_partition=1 << 16, max_unique_ids_per_partition=1 << 16)
+            for i, v in enumerate((100, 5000, 70000))]
+  feats = [embedding_spec.FeatureSpec(
+      name=f"f{i}", table_spec=t, input_shape=[batch, 1],
+      output_shape=[batch, dim]) for i, t in enumerate(tables)]
+  embedding.prepare_feature_specs_for_training(feats, 1, 1)
+  ids = []
+  for t in tables:
+    if one_hot:
+      ids.append(rng.integers(0, t.vocabulary_size, size=(batch, 1),
+                              dtype=np.int32))
+    else:
+      rows = np.empty(batch, dtype=object)
+      for i in range(batch):
+        rows[i] = rng.integers(0, t.vocabulary_size,
+                               size=int(rng.integers(0, 7))).astype(np.int32)
+      ids.append(rows)
+  pre, _ = embedding.preprocess_sparse_dense_matmul_input(
+      ids, None, feats, 1, 1, num_sc_per_device=1)
+  init = {}
+  for name, spec in embedding.get_stacked_table_specs(feats).items():
+    table = torch.tensor(rng.normal(0, 0.01, size=(spec.stack_vocab_size,
+                                                   dim)).astype(np.float32))
+    init[name] = (table.cuda(), torch.full_like(table, 0.1).cuda())
+  grads = [torch.tensor(rng.normal(size=(batch, dim)).astype(np.float32)
+                        ).cuda() for _ in feats]
+  return feats, pre, init, grads
+
+
+@pytest.mark.parametrize("one_hot", [True, False])
+def test_graph_replays_equal_eager_steps(one_hot):
+  feats, pre, init, grads = _workload(one_hot)
+
+  def make_state():
+    return {n: embedding.EmbeddingVariables(table=t.clone(), slot=(a.clone(),))
+            for n, (t, a) in init.items()}
+
+  def same(x, y, msg):
+    for n in init:
+      np.testing.assert_array_equal(x[n].table.cpu().numpy(),
+                                    y[n].table.cpu().numpy(), err_msg=msg)
+      np.testing.assert_array_equal(x[n].slot[0].cpu().numpy(),
+                                    y[n].slot[0].cpu().numpy(), err_msg=msg)
+
+  def step(variables):
+    acts = embedding.tpu_sparse_dense_matmul(
+        pre, variables, feats, global_device_count=1, num_sc_per_device=1)
+    embedding.tpu_sparse_dense_matmul_grad(
+        grads, pre, variables, feats, global_device_count=1,
+        num_sc_per_device=1)
+    return acts
+
+  eager, graphed = make_state(), make_state()
+  # Warm up on a side stream (sizes the workspace), then restore the state.
+  side = torch.cuda.Stream()
+  side.wait_stream(torch.cuda.current_stream())
+  with torch.cuda.stream(side):
+    step(graphed)
+  torch.cuda.current_stream().wait_stream(side)
+  torch.cuda.synchronize()
+  for n, (t, a) in init.items():
+    graphed[n].table.copy_(t)
+    graphed[n].slot[0].copy_(a)
+  g = torch.cuda.CUDAGraph()
+  with torch.cuda.graph(g):
+    graph_acts = step(graphed)
+  torch.cuda.synchronize()
+  # Capture records without running: the state is still the initial one.
+  same(graphed, make_state(), "after capture")
+  for i in range(4):
+    acts = step(eager)
+    noise = torch.randn(1000, device="cuda").sum()  # eager work in between
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    del noise
+    for a, b in zip(acts, graph_acts):
+      np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy(),
+                                    err_msg=f"replay {i}")
+    same(eager, graphed, f"replay {i}")
