@@ -819,6 +819,192 @@ __global__ __launch_bounds__(64) void FillPlanMinibatch(
   }
 }
 
+// FillPlanMinibatch for one device per block, with the device's bucket counts
+// in LDS: slot totals ((SC, minibatch, partition): the kept entries of the
+// minibatch's buckets) and the per-bucket plans are computed in parallel;
+// one thread replays FillBufferSegment over the slots, as FillPlanMinibatch
+// does. Needs S * 64 * NS <= kLdsPlanCells (bucket counts) slots and cells.
+constexpr int kLdsPlanCells = 2048;
+
+__global__ __launch_bounds__(256) void FillPlanMinibatchLds(
+    const BucketStats* bstats, FillParams fp, int pass, int32_t* rp_out,
+    FillPlan* plans, int32_t* stat_max_ids, int32_t* stat_max_unique,
+    int32_t* stat_required, int64_t* counters) {
+  __shared__ int32_t s_kept[kLdsPlanCells];    // [s][b][p]
+  __shared__ int32_t s_total[kLdsPlanCells];   // [s][m][p], then slot take
+  __shared__ int32_t s_start[kLdsPlanCells];   // [s][m][p]
+  __shared__ int32_t s_pad0[kLdsPlanCells];
+  __shared__ int32_t s_pad1[kLdsPlanCells];
+  __shared__ int32_t s_req[kMaxMinibatches];   // per SC (S <= 64 here)
+  __shared__ int32_t s_first[kMaxMinibatches + 1];
+  const int d = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int S = fp.segs_per_device;
+  const int NS = fp.num_partitions;
+  const int B = 1 << fp.mb_bits;
+  const int nmb = fp.num_minibatches;
+  const int RPB = fp.rp_per_segment;
+  const int64_t coo_size = fp.coo_size;
+  const int cells = S * B * NS;
+  const int slots = S * nmb * NS;
+  const BucketStats* bs = bstats + static_cast<int64_t>(d) * cells;
+  FillPlan* pl = plans + static_cast<int64_t>(d) * cells;
+  int32_t* rp = rp_out + static_cast<int64_t>(d) * S * kMaxMinibatches * RPB;
+  // Bucket counts to LDS; a cell over a limit.
+  bool over = false;
+  for (int c = tid; c < cells; c += blockDim.x) {
+    const BucketStats x = bs[c];
+    s_kept[c] = x.kept;
+    over = over || x.obs_ids > fp.max_ids || x.obs_unique > fp.max_unique;
+  }
+  // First bucket of each minibatch (buckets of one minibatch are a range).
+  for (int b = tid; b < B; b += blockDim.x) {
+    const int m = fp.minibatch_of[b];
+    if (b == 0 || fp.minibatch_of[b - 1] != m) s_first[m] = b;
+  }
+  if (tid == 0) s_first[nmb] = B;
+  // Required sizes: per partition the observed ids of all buckets, aligned.
+  for (int sc = tid; sc < S; sc += blockDim.x) {
+    int64_t req = 0;
+    for (int p = 0; p < NS; ++p) {
+      int64_t ids = 0;
+      for (int b = 0; b < B; ++b) ids += bs[(sc * B + b) * NS + p].obs_ids;
+      req += (ids + kAlign - 1) / kAlign * kAlign;
+    }
+    s_req[sc] = static_cast<int32_t>(req);
+    if (pass == 0) {
+      stat_required[static_cast<int64_t>(d) * S + sc] =
+          static_cast<int32_t>(req);
+    }
+  }
+  const bool any_over = __syncthreads_or(over);
+  // Slot totals and cleared plans.
+  for (int t = tid; t < slots; t += blockDim.x) {
+    const int p = t % NS;
+    const int m = (t / NS) % nmb;
+    const int sc = t / NS / nmb;
+    int32_t k = 0;
+    for (int b = s_first[m]; b < s_first[m + 1]; ++b) {
+      k += s_kept[(sc * B + b) * NS + p];
+    }
+    s_total[t] = k;
+    s_start[t] = 0;
+    s_pad0[t] = 0;
+    s_pad1[t] = 0;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    // FillBufferSegment over the (SC, minibatch) segments; s_total becomes
+    // the slot's take.
+    int64_t packed = 0, chained = 0, dropped = 0;
+    int rp_begin = 0;
+    for (int sc = 0; sc < S; ++sc) {
+      for (int m = 0; m < nmb; ++m) {
+        int64_t coo_begin;
+        if (nmb == 1) {
+          coo_begin = min(packed, coo_size);
+          packed = min(packed + static_cast<int64_t>(s_req[sc]), coo_size);
+        } else {
+          coo_begin = chained;
+        }
+        const int base = (sc * nmb + m) * NS;
+        int64_t total = 0;
+        for (int p = 0; p < NS; ++p) total += s_total[base + p];
+        const int64_t coo_end = coo_size;
+        int64_t coo = coo_begin, processed = 0;
+        int rpi = rp_begin;
+        const int rp_end = rp_begin + RPB;
+        int cur = 0;
+        auto valid = [&]() {
+          if (processed == total && coo == coo_end) return true;
+          if (rpi >= rp_end || coo >= coo_end) return false;
+          return true;
+        };
+        auto advance = [&](int target) {
+          while (cur < target) {
+            if (!valid()) return;
+            rp[rpi++] = static_cast<int32_t>(coo);
+            int64_t nc = (coo + kAlign - 1) / kAlign * kAlign;
+            if (nc > coo_end) nc = coo_end;
+            s_pad0[base + cur] = static_cast<int32_t>(coo);
+            s_pad1[base + cur] = static_cast<int32_t>(nc);
+            coo = nc;
+            ++cur;
+          }
+        };
+        bool stop = false;
+        for (int p = 0; p < NS; ++p) {
+          const int64_t kp = s_total[base + p];
+          s_total[base + p] = 0;
+          if (stop || kp == 0) continue;
+          advance(p);
+          if (!valid()) {
+            stop = true;
+            continue;
+          }
+          const int64_t room = coo_end - coo;
+          const int64_t take = kp < room ? kp : room;
+          s_start[base + p] = static_cast<int32_t>(coo);
+          s_total[base + p] = static_cast<int32_t>(take);
+          coo += take;
+          processed += take;
+          if (take < kp) stop = true;
+        }
+        advance(NS);
+        while (rpi < rp_end) rp[rpi++] = static_cast<int32_t>(coo);
+        dropped += total - processed;
+        chained = coo;
+        rp_begin += RPB;
+      }
+    }
+    if (pass == 0 && any_over) {
+      atomicMax(reinterpret_cast<unsigned long long*>(&counters[4]), 1ull);
+    }
+    if (pass != 0 && any_over && !fp.allow_dropping) {
+      atomicMax(reinterpret_cast<unsigned long long*>(&counters[1]), 1ull);
+    }
+    if (dropped > 0) {
+      atomicAdd(reinterpret_cast<unsigned long long*>(&counters[0]),
+                static_cast<unsigned long long>(dropped));
+    }
+  }
+  __syncthreads();
+  // Per-bucket plans: the bucket's entries follow those of the minibatch's
+  // earlier buckets in the slot; the slot's padding goes with its first
+  // bucket.
+  for (int c = tid; c < cells; c += blockDim.x) {
+    const int p = c % NS;
+    const int b = (c / NS) % B;
+    const int sc = c / NS / B;
+    const int m = fp.minibatch_of[b];
+    const int slot = (sc * nmb + m) * NS + p;
+    int32_t off = 0;
+    for (int b2 = s_first[m]; b2 < b; ++b2) off += s_kept[(sc * B + b2) * NS + p];
+    const int32_t kb = s_kept[c];
+    int32_t fit = s_total[slot] - off;
+    fit = fit < 0 ? 0 : (fit > kb ? kb : fit);
+    FillPlan q;
+    q.start = static_cast<int64_t>(s_start[slot]) + off;
+    q.fit = fit;
+    const bool first = b == s_first[m];
+    q.pad_begin = first ? s_pad0[slot] : 0;
+    q.pad_end = first ? s_pad1[slot] : 0;
+    q.pad_seg = d * S + sc;
+    pl[c] = q;
+  }
+  if (pass != 0) return;
+  for (int p = tid; p < NS; p += blockDim.x) {
+    int32_t mi = 0, mu = 0;
+    for (int sc = 0; sc < S; ++sc) {
+      const BucketStats& x = bs[sc * NS + p];
+      mi = max(mi, x.obs_ids);
+      mu = max(mu, x.obs_unique);
+    }
+    stat_max_ids[static_cast<int64_t>(d) * NS + p] = mi;
+    stat_max_unique[static_cast<int64_t>(d) * NS + p] = mu;
+  }
+}
+
 // ComputeMinibatchingSplit (minibatching_splits_impl.h:58-81) over the 64
 // bucket values of v: bottom-up, a node whose children sum past the limit is
 // split and keeps the larger child, otherwise it keeps the sum.
@@ -1483,9 +1669,19 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
     return 0;
   }
   if (minibatching) {
-    hipLaunchKernelGGL(FillPlanMinibatch, dim3(1), dim3(64), 0, stream,
-                       b.bstats, fp, pass, out->row_pointers, b.plans,
-                       stat_max_ids, stat_max_unique, stat_required, counters);
+    const int64_t cells = static_cast<int64_t>(pl.S) *
+                          (int64_t{1} << pl.kl.mb_bits) * pl.NS;
+    if (cells <= kLdsPlanCells && pl.S <= kMaxMinibatches) {
+      hipLaunchKernelGGL(FillPlanMinibatchLds, dim3(pl.L), dim3(256), 0,
+                         stream, b.bstats, fp, pass, out->row_pointers,
+                         b.plans, stat_max_ids, stat_max_unique,
+                         stat_required, counters);
+    } else {
+      hipLaunchKernelGGL(FillPlanMinibatch, dim3(1), dim3(64), 0, stream,
+                         b.bstats, fp, pass, out->row_pointers, b.plans,
+                         stat_max_ids, stat_max_unique, stat_required,
+                         counters);
+    }
   } else {
     hipLaunchKernelGGL(FillPlanKernel, dim3(1), dim3(256), 0, stream, b.bstats,
                        fp, out->row_pointers, b.plans, stat_max_ids,
