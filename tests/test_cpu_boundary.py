@@ -155,3 +155,20 @@ def test_preprocess_sample_view_option():
       _native.load_library().scemb_last_error()
   assert _sizing_call(True, 1, table_rows=0) == 0
   assert _sizing_call(False, 2) > 0
+
+
+def test_embedding_size_helpers_with_minibatching():
+  """lib/nn/tests/embedding_test.py:964-1000."""
+  from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-import-not-at-top
+  kw = dict(max_ids_per_partition=12, global_device_count=1,
+            num_sc_per_device=4)
+  assert embedding.compute_theoretical_max_coo_buffer_size(
+      **kw, enable_minibatching=False) == 256
+  assert embedding.compute_theoretical_max_coo_buffer_size(
+      **kw, enable_minibatching=True) == 16384
+  assert embedding.compute_row_pointers_size_per_device(
+      global_device_count=1, num_sc_per_device=4,
+      enable_minibatching=False) == 32
+  assert embedding.compute_row_pointers_size_per_device(
+      global_device_count=1, num_sc_per_device=4,
+      enable_minibatching=True) == 2048
