@@ -365,9 +365,11 @@ typedef struct scemb_preprocess_options {
    * stack, in the order of input_preprocessing.cc:852-929:
    *   pass 0  the first pass over every stack: the stats (which stay those of
    *           the call), the CSR of one minibatch, and counter 4 = 1 when a
-   *           partition exceeds a limit (no id is dropped in this pass);
-   *   pass 1  only if some stack set counter 4: the bucket pass, counter 5 =
-   *           this stack's split of the 64 buckets (OR it over all stacks);
+   *           partition exceeds a limit (no id is dropped in this pass); then
+   *           also counter 5 = this stack's split of the 64 buckets, from its
+   *           runs counted per bucket (OR it over all stacks);
+   *   pass 1  the bucket pass itself, counter 5 = the same split (optional:
+   *           pass 0 already gives it);
    *   pass 2  the bucket pass writing popcount(split) + 1 minibatches, with
    *           minibatching_split = that OR; counter 0 = its dropped ids.
    * Row pointers then take 64 * S * max(NS, 8) entries per device (the first

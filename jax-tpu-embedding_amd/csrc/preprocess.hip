@@ -1025,13 +1025,70 @@ __device__ uint64_t SplitOf(int32_t* v, int32_t limit) {
   return split;
 }
 
-// Pass 1: per (SC, partition) the split of its bucket counts, ids and unique
-// ids, OR-ed into counters[5] (UpdateMinibatchingSplit,
+// Pass 0, only when a limit was exceeded (counters[4], set by the fill
+// plan): the bucket pass's observed counts straight from this pass's runs.
+// A run is a distinct (column, row) of one SC, and the bucket pass counts
+// exactly those (merged duplicates and repeats of dropped ones are not
+// observed, sort_and_group_coo_tensors_impl.h:245-274); its distinct
+// columns are the unique ids. So per (SC, bucket, partition): runs, and runs
+// that start a column. Block-local counts in LDS when they fit.
+constexpr int kLdsCountCells = 2048;
+
+template <typename K>
+__global__ __launch_bounds__(256) void BucketCountsOfRuns(
+    const K* skeys, const uint32_t* run_pos, const uint64_t* flags,
+    const uint64_t* totals, KeyLayout kl, int num_partitions, int64_t cells,
+    const int64_t* counters, BucketStats* counts) {
+  __shared__ int32_t s_ids[kLdsCountCells];
+  __shared__ int32_t s_uniq[kLdsCountCells];
+  if (counters[4] == 0) return;
+  const bool lds = cells <= kLdsCountCells;
+  if (lds) {
+    for (int64_t c = threadIdx.x; c < cells; c += blockDim.x) {
+      s_ids[c] = 0;
+      s_uniq[c] = 0;
+    }
+    __syncthreads();
+  }
+  const int64_t runs = static_cast<int64_t>(static_cast<uint32_t>(totals[0]));
+  const K col_mask = kl.col_bits >= 64 ? ~K(0) : ((K(1) << kl.col_bits) - 1);
+  for (int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+       r < runs; r += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t i0 = run_pos[r];
+    const K key = skeys[i0];
+    uint32_t p, local;
+    DecodeCol<K>(key & col_mask, kl, &p, &local);
+    const int64_t seg = static_cast<int64_t>(key >> kl.col_bits);
+    const uint32_t col = (local << kl.log2ns) | p;
+    const int64_t cell =
+        (seg * kMaxMinibatches + MinibatchingBucket(col)) * num_partitions + p;
+    const bool new_col = ((flags[i0] >> 32) & 1ull) != 0;
+    if (lds) {
+      atomicAdd(&s_ids[cell], 1);
+      if (new_col) atomicAdd(&s_uniq[cell], 1);
+    } else {
+      atomicAdd(&counts[cell].obs_ids, 1);
+      if (new_col) atomicAdd(&counts[cell].obs_unique, 1);
+    }
+  }
+  if (!lds) return;
+  __syncthreads();
+  for (int64_t c = threadIdx.x; c < cells; c += blockDim.x) {
+    if (s_ids[c] != 0) atomicAdd(&counts[c].obs_ids, s_ids[c]);
+    if (s_uniq[c] != 0) atomicAdd(&counts[c].obs_unique, s_uniq[c]);
+  }
+}
+
+// Per (SC, partition) the split of its bucket counts, ids and unique ids,
+// OR-ed into counters[5] (UpdateMinibatchingSplit,
 // sort_and_group_coo_tensors_impl.h:116-151); a bucket over a limit with
-// dropping off sets counters[1].
+// dropping off sets counters[1]. Pass 1 runs it on its own counts; pass 0
+// on BucketCountsOfRuns's, and only when a limit was exceeded.
 __global__ __launch_bounds__(64) void MinibatchSplit(const BucketStats* bstats,
                                                      FillParams fp,
+                                                     int only_if_required,
                                                      int64_t* counters) {
+  if (only_if_required && counters[4] == 0) return;
   const int NS = fp.num_partitions;
   const int64_t n = static_cast<int64_t>(fp.local_devices) *
                     fp.segs_per_device * NS;
@@ -1438,6 +1495,12 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   b.plans = ws.Take<FillPlan>(num_buckets);
   b.slices = ws.Take<SliceDesc>(static_cast<int64_t>(pl.slices.size()));
   b.feats = ws.Take<FeatureDev>(nf);
+  // Pass 0 of minibatching: the bucket counts its runs give (used only when
+  // a limit is exceeded).
+  const int64_t split_cells =
+      static_cast<int64_t>(pl.L) * pl.S * kMaxMinibatches * pl.NS;
+  BucketStats* split_counts =
+      minibatching && pass == 0 ? ws.Take<BucketStats>(split_cells) : nullptr;
   // Per-row divisors of weighted mean / sqrtn.
   float* divisors = o->has_variable_weights && o->combiner != 0
                         ? ws.Take<float>(pl.total_rows)
@@ -1525,6 +1588,13 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
     hipLaunchKernelGGL(FillI32, dim3(CeilDiv(num_buckets, 256)), dim3(256), 0,
                        stream, b.part_last, num_buckets, -1);
     SCEMB_LAUNCH_CHECK();
+    if (split_counts != nullptr) {
+      const int64_t words = split_cells * (sizeof(BucketStats) / 4);
+      hipLaunchKernelGGL(FillI32, dim3(CeilDiv(words, 256)), dim3(256), 0,
+                         stream, reinterpret_cast<int32_t*>(split_counts),
+                         words, 0);
+      SCEMB_LAUNCH_CHECK();
+    }
     if (divisors != nullptr && pl.total_rows > 0) {
       hipLaunchKernelGGL(RowDivisors, dim3(CeilDiv(pl.total_rows, 256)),
                          dim3(256), 0, stream, b.slices,
@@ -1659,7 +1729,7 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   if (minibatching && pass == 1) {
     const int64_t cells = static_cast<int64_t>(pl.L) * pl.S * pl.NS;
     hipLaunchKernelGGL(MinibatchSplit, dim3(CeilDiv(cells, 64)), dim3(64), 0,
-                       stream, b.bstats, fp, counters);
+                       stream, b.bstats, fp, 0, counters);
     SCEMB_LAUNCH_CHECK();
     if (M > 0) {
       hipLaunchKernelGGL(StoreTotal, dim3(1), dim3(1), 0, stream, b.totals,
@@ -1688,6 +1758,20 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                        stat_max_unique, stat_required, counters);
   }
   SCEMB_LAUNCH_CHECK();
+  if (split_counts != nullptr && M > 0) {
+    // Both kernels return at once unless the fill plan flagged a limit.
+    const int64_t grid = std::min<int64_t>(CeilDiv(M, 4096), 1024);
+    hipLaunchKernelGGL((BucketCountsOfRuns<K>), dim3(grid), dim3(256), 0,
+                       stream, skeys, b.run_pos, b.flags, b.totals, pl.kl,
+                       pl.NS, split_cells, counters, split_counts);
+    SCEMB_LAUNCH_CHECK();
+    FillParams sp = fp;
+    sp.mb_bits = BitWidth(kMaxMinibatches - 1);
+    const int64_t cells = static_cast<int64_t>(pl.L) * pl.S * pl.NS;
+    hipLaunchKernelGGL(MinibatchSplit, dim3(CeilDiv(cells, 64)), dim3(64), 0,
+                       stream, split_counts, sp, 1, counters);
+    SCEMB_LAUNCH_CHECK();
+  }
   if (view.entry != nullptr && M > 0) {
     view.sidx = sidx;
     hipLaunchKernelGGL(FillU64, dim3(CeilDiv(M, 256)), dim3(256), 0, stream,

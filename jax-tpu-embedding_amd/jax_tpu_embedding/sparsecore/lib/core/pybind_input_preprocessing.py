@@ -428,21 +428,18 @@ def _raise_on_counters(name, counters):
 
 def _minibatching_passes(pending, jobs, csr, views):
   """Runs the rest of input_preprocessing.cc:852-929 after every stack's
-  first pass: if one of them exceeds a limit, the bucket pass of every
-  stack, the OR of their splits, and the minibatched fill of every stack.
-  Waits for the device twice (the required flags, the splits)."""
+  first pass: if one of them exceeds a limit, the OR of the stacks' splits
+  and the minibatched fill of every stack. The first pass already counted
+  its runs per bucket when a limit was exceeded, so its counter 5 is the
+  bucket pass's split (the library's pass 1 gives the same; the tests
+  compare them). Waits for the device once."""
   first = _read_counters([(p[1], p[5]) for p in pending])
   for p, c in zip(pending, first):
     _raise_on_counters(p[0], c)
   if not any(c[4] for c in first):
     return
   split = 0
-  second = []
-  for name, kwargs in jobs:
-    out = _preprocess_stack(**kwargs, minibatching_pass=1, outputs=csr[name])
-    second.append((out[4], out[5][3]))
-  for (name, _), c in zip(jobs, _read_counters(second)):
-    _raise_on_counters(name, c)
+  for c in first:
     split |= int(np.uint64(c[5]))
   for name, kwargs in jobs:
     out = _preprocess_stack(**kwargs, minibatching_pass=2,

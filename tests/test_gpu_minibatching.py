@@ -455,3 +455,33 @@ def test_nn_forward_and_backward():
   got = utils.unshard_emb_table(updated["table_a"].table.cpu().numpy()[None],
                                 num_sc_per_device=num_sc)
   np.testing.assert_allclose(got, exp_logical, rtol=1e-6)
+
+
+@pytest.mark.parametrize("num_sc,limits,weighted", [
+    (1, (8, 6), False), (2, (3, 3), True), (4, (2, 1), False),
+    (1, (1, 1), True)])
+def test_first_pass_split_equals_bucket_pass_split(num_sc, limits, weighted):
+  """The split the first pass counts from its runs is the bucket pass's
+  (library pass 1), stack by stack; the split decides the whole minibatched
+  CSR, which the other tests compare with the oracle."""
+  rng = np.random.default_rng(num_sc * 7 + limits[0])
+  batch = 256
+  specs = _specs([("a", 3000, 8), ("b", 500, 16)], batch, limits, num_sc)
+  feats = [_ragged(rng, batch, 0, 9, 3000), _ragged(rng, batch, 1, 4, 500)]
+  weights = [_weights_like(rng, f) for f in feats] if weighted else None
+  stacks = pip.get_stacked_table_metadata(specs)
+  for name, metas in stacks.items():
+    dev = [pip._to_device_feature(feats[m.feature_index],  # pylint: disable=protected-access
+                                  None if weights is None else
+                                  weights[m.feature_index]) for m in metas]
+    kw = dict(feats=dev, metas=metas, local_device_count=1,
+              global_device_count=1, num_sc_per_device=num_sc,
+              allow_id_dropping=True, has_weights=weighted,
+              enable_minibatching=True)
+    first = pip._preprocess_stack(**kw, minibatching_pass=0)  # pylint: disable=protected-access
+    bucket = pip._preprocess_stack(**kw, minibatching_pass=1,  # pylint: disable=protected-access
+                                   outputs=first[:4])
+    c0, c1 = pip._read_counters([(first[4], first[5][3]),  # pylint: disable=protected-access
+                                 (bucket[4], bucket[5][3])])
+    assert c0[4] == 1, name
+    assert c0[5] == c1[5] and c1[5] != 0, name
