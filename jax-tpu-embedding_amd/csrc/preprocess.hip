@@ -240,72 +240,80 @@ __global__ __launch_bounds__(256) void RowDivisors(
   }
 }
 
+// Last row r in [lo, hi] with splits[r] <= target (splits[lo] <= target).
+// With empty rows several rows share a start; the last of them is the
+// non-empty row holding position `target`.
+__device__ __forceinline__ int64_t LastRowAtOrBefore(const int64_t* splits,
+                                                     int64_t lo, int64_t hi,
+                                                     int64_t target) {
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (splits[mid] <= target) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+constexpr int kExtractBlock = 256;
+
+// Where an ExtractIds block reads from: the slice holding both its first and
+// last output positions (-1 when they lie in different slices) and, for a
+// ragged feature, the input rows of those two positions.
+struct BlockRows {
+  int32_t slice;
+  int32_t pad;
+  int64_t lo;
+  int64_t hi;
+};
+
+// One thread per ExtractIds block: two binary searches over the row splits,
+// run for all blocks at once before the extraction, so that an extraction
+// thread only searches the few rows its block spans.
+__global__ __launch_bounds__(256) void BlockBounds(const SliceDesc* slices,
+                                                   int num_slices,
+                                                   const FeatureDev* feats,
+                                                   int64_t total_ids,
+                                                   int64_t num_blocks,
+                                                   BlockRows* out) {
+  const int64_t blk = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (blk >= num_blocks) return;
+  const int64_t first = blk * kExtractBlock;
+  const int64_t last = min(first + kExtractBlock, total_ids) - 1;
+  BlockRows br{-1, 0, 0, -1};
+  const int sf = FindSlice(slices, num_slices, first, false);
+  if (sf == FindSlice(slices, num_slices, last, false)) {
+    br.slice = sf;
+    const SliceDesc sl = slices[sf];
+    const int64_t* splits = feats[sl.feature].splits;
+    if (splits != nullptr) {
+      const int64_t top = sl.row_start + sl.num_rows - 1;
+      br.lo = LastRowAtOrBefore(splits, sl.row_start, top,
+                                sl.id_begin + (first - sl.out_begin));
+      br.hi = LastRowAtOrBefore(splits, br.lo, top,
+                                sl.id_begin + (last - sl.out_begin));
+    }
+  }
+  out[blk] = br;
+}
+
 // One thread per extracted id (output position o, in slice order): finds its
 // slice and input row, then writes the sort key (segment, column) -- or the
 // sentinel for an id outside the table --, the extraction index, the sample
-// id, the gain and, for the optional row pass, the row key. Consecutive
-// threads write consecutive positions. Gains: unit weights give 1, 1/n or
-// 1/sqrt(n) for a row of n ids (process_coo_tensors_impl.h:39-56); weights
-// are divided by the row's divisor (RowDivisors; 1 for sum).
+// id and gain packed into one word (sample in the low half), and, for the
+// optional row pass, the row key. Consecutive threads write consecutive
+// positions. Gains: unit weights give 1, 1/n or 1/sqrt(n) for a row of n
+// ids (process_coo_tensors_impl.h:39-56); weights are divided by the row's
+// divisor (RowDivisors; 1 for sum).
 template <typename K>
-__global__ __launch_bounds__(256) void ExtractIds(
+__global__ __launch_bounds__(kExtractBlock) void ExtractIds(
     const SliceDesc* slices, int num_slices, const FeatureDev* feats,
-    int64_t total_ids, int combiner, int has_weights,
-    const float* divisor, KeyLayout kl, K* keys, uint32_t* vals,
-    uint32_t* rows_out, float* gains_out, uint32_t* row_keys,
+    const BlockRows* block_rows, int64_t total_ids, int combiner,
+    int has_weights, const float* divisor, KeyLayout kl, K* keys,
+    uint32_t* vals, uint64_t* row_gain, uint32_t* row_keys,
     int row_key_bits_seg_shift, int64_t* counters) {
   const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  // The block's first and last positions usually lie in one slice and a few
-  // rows: the block finds that slice and those rows together (a parallel
-  // scan of the slice table, then 256-way searches over the row splits), so
-  // that each thread only searches a handful of rows.
-  __shared__ int s_slice_first, s_slice_last, s_best;
-  const int64_t first = static_cast<int64_t>(blockIdx.x) * blockDim.x;
-  const int64_t last = min(first + static_cast<int64_t>(blockDim.x), total_ids) - 1;
-  if (threadIdx.x == 0) {
-    s_slice_first = -1;
-    s_slice_last = -1;
-  }
-  __syncthreads();
-  for (int j = threadIdx.x; j < num_slices; j += blockDim.x) {
-    const int64_t b0 = slices[j].out_begin;
-    const int64_t b1 = j + 1 < num_slices ? slices[j + 1].out_begin : INT64_MAX;
-    if (b0 <= first && first < b1) s_slice_first = j;
-    if (b0 <= last && last < b1) s_slice_last = j;
-  }
-  __syncthreads();
-  const int block_slice = s_slice_first == s_slice_last ? s_slice_first : -1;
-  int64_t row_lo = 0, row_hi = -1;
-  if (block_slice >= 0) {
-    const SliceDesc sl = slices[block_slice];
-    const int64_t* splits = feats[sl.feature].splits;
-    if (splits != nullptr) {
-      int64_t bounds[2];
-      for (int k = 0; k < 2; ++k) {
-        const int64_t target =
-            sl.id_begin + ((k == 0 ? first : last) - sl.out_begin);
-        // Last row of the slice whose start is <= target; splits[lo] <=
-        // target holds throughout.
-        int64_t lo = k == 0 ? sl.row_start : bounds[0];
-        int64_t hi = sl.row_start + sl.num_rows - 1;
-        while (lo < hi) {
-          const int64_t step = (hi - lo + blockDim.x) / blockDim.x;
-          if (threadIdx.x == 0) s_best = 0;
-          __syncthreads();
-          const int64_t r = lo + static_cast<int64_t>(threadIdx.x) * step;
-          if (r <= hi && splits[r] <= target) atomicMax(&s_best, threadIdx.x);
-          __syncthreads();
-          const int64_t nlo = lo + static_cast<int64_t>(s_best) * step;
-          hi = min(nlo + step - 1, hi);
-          lo = nlo;
-          __syncthreads();
-        }
-        bounds[k] = lo;
-      }
-      row_lo = bounds[0];
-      row_hi = bounds[1];
-    }
-  }
+  const BlockRows br = block_rows[blockIdx.x];
+  const int block_slice = br.slice;
+  const int64_t row_lo = br.lo, row_hi = br.hi;
   bool bad = false;
   if (o < total_ids) {
     const int si = block_slice >= 0 ? block_slice
@@ -321,11 +329,7 @@ __global__ __launch_bounds__(256) void ExtractIds(
         lo = row_lo;
         hi = row_hi;
       }
-      while (lo < hi) {
-        const int64_t mid = (lo + hi + 1) >> 1;
-        if (f.splits[mid] <= p) lo = mid; else hi = mid - 1;
-      }
-      r = lo;
+      r = LastRowAtOrBefore(f.splits, lo, hi, p);
       b = f.splits[r];
       e = f.splits[r + 1];
     } else {
@@ -359,8 +363,8 @@ __global__ __launch_bounds__(256) void ExtractIds(
     keys[o] = ok ? (seg_part | ColKey<K>(static_cast<uint32_t>(col), kl))
                  : SentinelKey<K>();
     vals[o] = static_cast<uint32_t>(o);
-    rows_out[o] = sample;
-    gains_out[o] = gain;
+    row_gain[o] = static_cast<uint64_t>(sample) |
+                  (static_cast<uint64_t>(__float_as_uint(gain)) << 32);
     if (row_keys != nullptr) {
       row_keys[o] = (static_cast<uint32_t>(sl.segment) << row_key_bits_seg_shift) |
                     sample;
@@ -387,24 +391,24 @@ __global__ void FillI32(int32_t* p, int64_t n, int32_t v) {
 }
 
 // Flags and partition boundaries over the sorted sequence. Each element's
-// row and gain are gathered once (sidx); the previous element's row comes
-// from the neighbouring thread through LDS (from memory at block starts).
+// row and gain are gathered once, as one packed word (sidx); the previous
+// element's row comes from the neighbouring thread through LDS (from memory
+// at block starts).
 template <typename K>
 __global__ __launch_bounds__(256) void GroupFlags(
-    const K* skeys, const uint32_t* sidx, const uint32_t* rows,
-    const float* gains, int64_t n, KeyLayout kl, int num_partitions,
-    uint32_t* srows, float* sgains, uint64_t* flags, int32_t* part_first,
-    int32_t* part_last) {
+    const K* skeys, const uint32_t* sidx, const uint64_t* row_gain, int64_t n,
+    KeyLayout kl, int num_partitions, uint32_t* srows, float* sgains,
+    uint64_t* flags, int32_t* part_first, int32_t* part_last) {
   __shared__ uint32_t s_row[256];
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const K key = i < n ? skeys[i] : SentinelKey<K>();
   const bool valid = key != SentinelKey<K>();
   uint32_t row = 0;
   if (valid) {
-    const uint32_t idx = sidx[i];
-    row = rows[idx];
+    const uint64_t rg = row_gain[sidx[i]];
+    row = static_cast<uint32_t>(rg);
     srows[i] = row;
-    sgains[i] = gains[idx];
+    sgains[i] = __uint_as_float(static_cast<uint32_t>(rg >> 32));
   }
   s_row[threadIdx.x] = row;
   __syncthreads();
@@ -424,7 +428,8 @@ __global__ __launch_bounds__(256) void GroupFlags(
         new_bucket = false;
         // Same key, so element i - 1 is valid and its row was loaded.
         const uint32_t prev_row =
-            threadIdx.x > 0 ? s_row[threadIdx.x - 1] : rows[sidx[i - 1]];
+            threadIdx.x > 0 ? s_row[threadIdx.x - 1]
+                            : static_cast<uint32_t>(row_gain[sidx[i - 1]]);
         new_run = prev_row != row;
       } else {
         uint32_t pp, pl;
@@ -1175,15 +1180,15 @@ __global__ __launch_bounds__(256) void MarkEntries(const uint64_t* entry,
 
 // The sample view in extraction order, which is activation-row order: the
 // run starting at extraction position e goes to view position pos[e]
-// (exclusive scan of the marks) with key rows[e]; positions from pos[m] to
-// n get the unused key.
+// (exclusive scan of the marks) with key row_gain[e]'s row; positions from
+// pos[m] to n get the unused key.
 __global__ __launch_bounds__(256) void ViewCompact(
-    const uint32_t* pos, const uint32_t* rows, const uint64_t* ventry,
+    const uint32_t* pos, const uint64_t* row_gain, const uint64_t* ventry,
     int64_t m, int64_t n, uint32_t unused_key, uint32_t* keys,
     uint64_t* entries) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < m && pos[i + 1] > pos[i]) {
-    keys[pos[i]] = rows[i];
+    keys[pos[i]] = static_cast<uint32_t>(row_gain[i]);
     entries[pos[i]] = ventry[i];
   }
   if (i < n && i >= static_cast<int64_t>(pos[m])) {
@@ -1403,8 +1408,8 @@ struct Buffers {
   void* keys_alt;
   uint32_t* vals;
   uint32_t* vals_alt;
-  uint32_t* rows;
-  float* gains;
+  uint64_t* row_gain;
+  BlockRows* block_rows;
   uint32_t* row_keys;
   uint32_t* row_keys_alt;
   uint32_t* srows;
@@ -1476,8 +1481,9 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   b.keys_alt = ws.Take<K>(M);
   b.vals = ws.Take<uint32_t>(M);
   b.vals_alt = ws.Take<uint32_t>(M);
-  b.rows = ws.Take<uint32_t>(M);
-  b.gains = ws.Take<float>(M);
+  b.row_gain = ws.Take<uint64_t>(M);
+  const int64_t extract_blocks = CeilDiv(M, kExtractBlock);
+  b.block_rows = ws.Take<BlockRows>(extract_blocks);
   b.row_keys = need_row_pass ? ws.Take<uint32_t>(M) : nullptr;
   b.row_keys_alt = need_row_pass ? ws.Take<uint32_t>(M) : nullptr;
   b.srows = ws.Take<uint32_t>(M);
@@ -1603,11 +1609,16 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
       SCEMB_LAUNCH_CHECK();
     }
     if (M > 0) {
-      hipLaunchKernelGGL((ExtractIds<K>), dim3(CeilDiv(M, 256)), dim3(256), 0,
-                         stream, b.slices, static_cast<int>(pl.slices.size()),
-                         b.feats, M, o->combiner,
+      const int num_slices = static_cast<int>(pl.slices.size());
+      hipLaunchKernelGGL(BlockBounds, dim3(CeilDiv(extract_blocks, 256)),
+                         dim3(256), 0, stream, b.slices, num_slices, b.feats,
+                         M, extract_blocks, b.block_rows);
+      SCEMB_LAUNCH_CHECK();
+      hipLaunchKernelGGL((ExtractIds<K>), dim3(extract_blocks),
+                         dim3(kExtractBlock), 0, stream, b.slices, num_slices,
+                         b.feats, b.block_rows, M, o->combiner,
                          o->has_variable_weights ? 1 : 0, divisors, pl.kl,
-                         static_cast<K*>(b.keys), b.vals, b.rows, b.gains,
+                         static_cast<K*>(b.keys), b.vals, b.row_gain,
                          b.row_keys, pl.row_key_seg_shift, counters);
       SCEMB_LAUNCH_CHECK();
     }
@@ -1651,7 +1662,7 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   }
   if (!measuring && M > 0) {
     hipLaunchKernelGGL((GroupFlags<K>), dim3(CeilDiv(M, 256)), dim3(256), 0,
-                       stream, skeys, sidx, b.rows, b.gains, M, pl.kl, pl.NS,
+                       stream, skeys, sidx, b.row_gain, M, pl.kl, pl.NS,
                        b.srows, b.sgains, b.flags, b.part_first, b.part_last);
     SCEMB_LAUNCH_CHECK();
   }
@@ -1804,7 +1815,7 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
     const int64_t grid = M > n ? M : n;
     if (grid > 0) {
       hipLaunchKernelGGL(ViewCompact, dim3(CeilDiv(grid, 256)), dim3(256), 0,
-                         stream, view.pos, b.rows, view.entry, M, n,
+                         stream, view.pos, b.row_gain, view.entry, M, n,
                          static_cast<uint32_t>(pl.batch_for_device),
                          out->view_keys, out->view_entries);
       SCEMB_LAUNCH_CHECK();
