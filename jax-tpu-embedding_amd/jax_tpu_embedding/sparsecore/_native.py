@@ -356,6 +356,64 @@ def as_device_tensor(x, dtype, dev=None):
   return t.from_numpy(arr).to(dev, non_blocking=False)
 
 
+class HostUploads:
+  """Host arrays bound for the device, gathered into one pinned staging
+  buffer and sent with a single asynchronous copy on the current stream.
+
+  add() returns a handle; after flush(), resolve(handle) is the device
+  tensor (anything that is not a handle resolves to itself). The staging
+  buffer comes from torch's pinned-memory cache, which keeps it until the
+  copy has completed; nothing here waits for the device."""
+
+  _ALIGN = 256  # every array starts 256-byte aligned on the device
+
+  class _Handle:
+    __slots__ = ("offset", "count", "dtype", "tensor")
+
+    def __init__(self, offset, count, dtype):
+      self.offset, self.count, self.dtype = offset, count, dtype
+      self.tensor = None
+
+  def __init__(self):
+    self._items = []
+    self._nbytes = 0
+
+  def add(self, x, dtype):
+    t = torch()
+    np_dtype = {t.int32: np.int32, t.int64: np.int64,
+                t.float32: np.float32}[dtype]
+    arr = np.ascontiguousarray(np.asarray(x), dtype=np_dtype).reshape(-1)
+    off = -(-self._nbytes // self._ALIGN) * self._ALIGN
+    self._nbytes = off + arr.nbytes
+    h = HostUploads._Handle(off, arr.size, dtype)
+    self._items.append((arr, h))
+    return h
+
+  def flush(self):
+    if not self._items:
+      return
+    t = torch()
+    dev = device()
+    host = t.empty(self._nbytes, dtype=t.uint8, pin_memory=True)
+    staged = host.numpy()
+    for arr, h in self._items:
+      staged[h.offset:h.offset + arr.nbytes] = arr.view(np.uint8)
+    dst = t.empty(self._nbytes, dtype=t.uint8, device=dev)
+    dst.copy_(host, non_blocking=True)
+    for arr, h in self._items:
+      h.tensor = dst[h.offset:h.offset + arr.nbytes].view(h.dtype)
+    self._items = []
+    self._nbytes = 0
+
+  @staticmethod
+  def resolve(x):
+    if isinstance(x, HostUploads._Handle):
+      if x.tensor is None:
+        raise RuntimeError("HostUploads.flush() has not run")
+      return x.tensor
+    return x
+
+
 def ptr(x) -> int | None:
   return None if x is None else x.data_ptr()
 

@@ -172,21 +172,31 @@ class _DeviceFeature:
   max_id: int | None  # known when the input came from host memory
 
 
-def _to_device_feature(feature, weights) -> _DeviceFeature:
+def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
+  """One feature's ids, weights and row splits as device tensors. With
+  `uploads` (a _native.HostUploads), host arrays are staged there instead of
+  copied one by one: the fields hold handles until _resolve_feature runs
+  after uploads.flush()."""
   t = _native.require_gpu()
   dev = _native.device()
+
+  def on_device(x, dtype):
+    if uploads is None or isinstance(x, t.Tensor):
+      return _native.as_device_tensor(x, dtype, dev)
+    return uploads.add(x, dtype)
+
   if isinstance(feature, t.Tensor):
     f = feature
     if f.dim() == 1:
       f = f.reshape(-1, 1)
     if f.dim() != 2:
       raise ValueError("Only 1D and 2D inputs are supported.")
-    ids = _native.as_device_tensor(f.reshape(-1), t.int32, dev)
+    ids = on_device(f.reshape(-1), t.int32)
     w = None
     if weights is not None:
-      w = _native.as_device_tensor(
+      w = on_device(
           weights.reshape(-1) if isinstance(weights, t.Tensor) else
-          np.asarray(weights, np.float32).reshape(-1), t.float32, dev)
+          np.asarray(weights, np.float32).reshape(-1), t.float32)
     return _DeviceFeature(ids, w, None, None, int(f.shape[0]), int(f.numel()),
                           int(f.shape[1]), None)
   if hasattr(feature, "values") and hasattr(feature, "row_splits"):
@@ -209,13 +219,12 @@ def _to_device_feature(feature, weights) -> _DeviceFeature:
             np.asarray(wv, np.float32).reshape(-1))
       if wv.shape[0] != vals.shape[0]:
         raise ValueError("Batch size mismatch for features and weights.")
-      w = _native.as_device_tensor(wv, t.float32, dev)
-    ids = _native.as_device_tensor(vals, t.int32, dev)
+      w = on_device(wv, t.float32)
+    ids = on_device(vals, t.int32)
     max_id = None
     if not isinstance(vals, t.Tensor) and vals.size:
       max_id = int(vals.max())
-    return _DeviceFeature(ids, w, _native.as_device_tensor(splits, t.int64,
-                                                           dev),
+    return _DeviceFeature(ids, w, on_device(splits, t.int64),
                           splits, splits.size - 1, int(splits[-1]), 0, max_id)
   arr = feature if isinstance(feature, np.ndarray) else np.asarray(
       feature, dtype=object)
@@ -230,15 +239,15 @@ def _to_device_feature(feature, weights) -> _DeviceFeature:
     b, k = arr.shape
     max_id = int(ids_np.max()) if ids_np.size else None
     return _DeviceFeature(
-        _native.as_device_tensor(ids_np, t.int32, dev),
-        None if w_np is None else _native.as_device_tensor(w_np, t.float32,
-                                                           dev),
+        on_device(ids_np, t.int32),
+        None if w_np is None else on_device(w_np, t.float32),
         None, None, b, b * k, k, max_id)
   if arr.dtype != object and arr.ndim == 1:
     # One id per sample.
     return _to_device_feature(arr.reshape(-1, 1),
                               None if weights is None else
-                              np.asarray(weights, np.float32).reshape(-1, 1))
+                              np.asarray(weights, np.float32).reshape(-1, 1),
+                              uploads)
   if arr.ndim != 1:
     raise ValueError("Only 1D and 2D numpy arrays supported as inputs.")
   rows = [np.asarray(r).reshape(-1) for r in arr]
@@ -256,10 +265,17 @@ def _to_device_feature(feature, weights) -> _DeviceFeature:
     w_np = (np.concatenate(wrows) if splits[-1] else np.zeros(0, np.float32))
   max_id = int(ids_np.max()) if ids_np.size else None
   return _DeviceFeature(
-      _native.as_device_tensor(ids_np, t.int32, dev),
-      None if w_np is None else _native.as_device_tensor(w_np, t.float32, dev),
-      _native.as_device_tensor(splits, t.int64, dev), splits, len(rows),
+      on_device(ids_np, t.int32),
+      None if w_np is None else on_device(w_np, t.float32),
+      on_device(splits, t.int64), splits, len(rows),
       int(splits[-1]), 0, max_id)
+
+
+def _resolve_feature(f: _DeviceFeature) -> _DeviceFeature:
+  f.ids = _native.HostUploads.resolve(f.ids)
+  f.weights = _native.HostUploads.resolve(f.weights)
+  f.splits = _native.HostUploads.resolve(f.splits)
+  return f
 
 
 def _preprocess_stack(feats, metas, *, local_device_count,
@@ -471,13 +487,19 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
   jobs, flat = [], {}
   build_view = (sample_views is not None and local_device_count == 1 and
                 global_device_count == 1)
+  # Host inputs of every stack go to the device in one copy.
+  uploads = _native.HostUploads()
+  stack_feats = {
+      name: [
+          _to_device_feature(
+              features[m.feature_index],
+              None if feature_weights is None else
+              feature_weights[m.feature_index], uploads) for m in metas
+      ] for name, metas in stacks.items()
+  }
+  uploads.flush()
   for name, metas in stacks.items():
-    feats = [
-        _to_device_feature(
-            features[m.feature_index],
-            None if feature_weights is None else
-            feature_weights[m.feature_index]) for m in metas
-    ]
+    feats = [_resolve_feature(f) for f in stack_feats[name]]
     kwargs = dict(feats=feats, metas=metas,
                   local_device_count=local_device_count,
                   global_device_count=global_device_count,
