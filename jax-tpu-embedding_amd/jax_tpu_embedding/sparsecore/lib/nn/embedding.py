@@ -434,6 +434,13 @@ def _get_activation_for_feature(feature, activations, global_device_count,
         f"feature slices per device for feature {feature.name}.")
   off = feature.id_transformation.row_offset // (global_device_count * f)
   b1 = feature.output_shape[0] // (global_device_count * f)
+  if f == 1:
+    # One slice per device: a row range (and leading columns) of the
+    # stacked activations.
+    sl = act.narrow(0, off, b1)
+    if act.dim() > 1 and feature.output_shape[-1] < act.shape[-1]:
+      sl = sl.narrow(-1, 0, feature.output_shape[-1])
+    return sl
   per = act.reshape(f, act.shape[0] // f, *act.shape[1:])
   sl = per[:, off:off + b1]
   if act.dim() > 1:
@@ -498,11 +505,10 @@ def _gradient_blocks(stack_spec, items, num_sc_per_device: int,
     # copy costs less than resolving the row blocks per gather.
     return None
   t = _native.torch()
+  dev = _native.device()
   grads = []
   for fs, g in items:
-    if not isinstance(g, t.Tensor):
-      g = _native.as_device_tensor(g, t.float32)
-    g = _native.as_device_tensor(g, t.float32, _native.device()).reshape(
+    g = _native.as_device_tensor(g, t.float32, dev).reshape(
         -1, fs.table_spec.embedding_dim)
     if g.shape[0] % f:
       raise ValueError(
@@ -515,9 +521,12 @@ def _gradient_blocks(stack_spec, items, num_sc_per_device: int,
   blocks, cum = [], 0
   for fs, g in grads:
     b1 = g.shape[0] // f
-    for s in range(f):
-      blocks.append((s * per_sc + cum, g[s * b1:(s + 1) * b1],
-                     fs.table_spec.embedding_dim))
+    if f == 1:
+      blocks.append((cum, g, fs.table_spec.embedding_dim))
+    else:
+      for s in range(f):
+        blocks.append((s * per_sc + cum, g[s * b1:(s + 1) * b1],
+                       fs.table_spec.embedding_dim))
     cum += b1
   blocks.sort(key=lambda b: b[0])
   return _device.RowBlocks(rows, stack_spec.stack_embedding_dim, blocks)
