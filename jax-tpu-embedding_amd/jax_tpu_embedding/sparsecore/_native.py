@@ -419,20 +419,33 @@ def ptr(x) -> int | None:
 
 
 class _Workspace:
-  """Per-device scratch buffer, grown on demand and reused across calls."""
+  """Scratch memory of the library's calls: one buffer per (device, stream),
+  grown on demand and reused by later calls on the same stream, which stream
+  order makes safe. Calls on different streams never share a buffer, so
+  preprocessing on a side stream may overlap a step on another.
+
+  A buffer that a call used while its stream was being captured into a graph
+  stays allocated after it has been outgrown: the graph's replays still
+  address it."""
 
   def __init__(self):
     self._buf = {}
+    self._captured = set()
+    self._retired = []
 
   def get(self, nbytes: int):
     t = torch()
     dev = device()
-    key = dev.index
+    key = (dev.index, t.cuda.current_stream(dev).cuda_stream)
     buf = self._buf.get(key)
     if buf is None or buf.numel() < nbytes:
+      if buf is not None and key in self._captured:
+        self._retired.append(buf)
       buf = t.empty(max(int(nbytes * 1.25), 1 << 20), dtype=t.uint8,
                     device=dev)
       self._buf[key] = buf
+    if t.cuda.is_current_stream_capturing():
+      self._captured.add(key)
     return buf
 
 
