@@ -1,7 +1,8 @@
 // Device-wide scan and stable LSD radix sort.
 //
-// Scan: reduce-then-scan over 2048-element tiles (256 threads x 8 items),
-// recursing on the tile sums.
+// Scan: reduce-then-scan over 2048-element tiles (256 threads x 8 items).
+// Up to 8192 tiles the scanning blocks add up the tile sums before them
+// themselves (two launches); beyond, the tile sums are scanned recursively.
 //
 // Radix sort: per digit pass (up to 8 bits, passes balanced over the key
 // span), (1) per-tile digit histograms, (2) an exclusive scan of the
@@ -71,6 +72,48 @@ __global__ __launch_bounds__(kScanBlock) void ScanTiles(const T* in, T* out,
   }
 }
 
+// ScanTiles whose tile offset is the sum of the partial sums of the tiles
+// before it, added up by the block itself (integer sums: any order gives the
+// same value), so that no separate scan of the partial sums is launched.
+template <typename T>
+__global__ __launch_bounds__(kScanBlock) void ScanTilesPrefix(
+    const T* in, T* out, int64_t n, const T* partial, T* total_out) {
+  __shared__ T smem[kScanBlock / kWave + 1];
+  T pre = 0;
+  for (int64_t j = threadIdx.x; j < static_cast<int64_t>(blockIdx.x);
+       j += kScanBlock) {
+    pre += partial[j];
+  }
+  T off;
+  BlockExclusiveScan<T, kScanBlock>(pre, smem, &off);
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile +
+                       static_cast<int64_t>(threadIdx.x) * kScanItems;
+  T v[kScanItems];
+  T s = 0;
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) {
+    const int64_t i = base + k;
+    v[k] = i < n ? in[i] : T(0);
+    s += v[k];
+  }
+  T total;
+  T run = BlockExclusiveScan<T, kScanBlock>(s, smem, &total) + off;
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) {
+    const int64_t i = base + k;
+    if (i < n) out[i] = run;
+    run += v[k];
+  }
+  if (total_out != nullptr && threadIdx.x == 0 &&
+      blockIdx.x == gridDim.x - 1) {
+    total_out[0] = off + total;
+  }
+}
+
+// Up to this many tiles, each block of the second launch adds up the
+// partial sums before it (at most this many loads spread over 256 threads).
+constexpr int64_t kPrefixTilesMax = 8192;
+
 }  // namespace
 
 template <typename T>
@@ -103,6 +146,14 @@ int ExclusiveScan(const T* in, T* out, int64_t n, T* total, Arena& ws,
     hipLaunchKernelGGL(ScanReduceTiles<T>, dim3(tiles), dim3(kScanBlock), 0,
                        stream, in, n, partial);
     SCEMB_LAUNCH_CHECK();
+  }
+  if (tiles <= kPrefixTilesMax) {
+    if (!measuring) {
+      hipLaunchKernelGGL(ScanTilesPrefix<T>, dim3(tiles), dim3(kScanBlock), 0,
+                         stream, in, out, n, partial, total);
+      SCEMB_LAUNCH_CHECK();
+    }
+    return 0;
   }
   int st = ExclusiveScan<T>(partial, partial, tiles, nullptr, ws, stream);
   if (st != 0) return st;
