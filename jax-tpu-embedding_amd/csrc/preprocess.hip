@@ -48,6 +48,8 @@ namespace scemb {
 namespace {
 
 constexpr uint32_t kDataMask26 = (1u << 26) - 1;
+// Sample-view slot of an extraction position that starts no written run.
+constexpr uint64_t kNoEntry = ~0ull;  // table rows stay below 2^32 - 1
 // int64 counters after the stats: dropped ids, limit exceeded, bad ids,
 // grouped entries, minibatching required (pass 0), minibatching split
 // (pass 1).
@@ -398,9 +400,13 @@ template <typename K>
 __global__ __launch_bounds__(256) void GroupFlags(
     const K* skeys, const uint32_t* sidx, const uint64_t* row_gain, int64_t n,
     KeyLayout kl, int num_partitions, uint32_t* srows, float* sgains,
-    uint64_t* flags, int32_t* part_first, int32_t* part_last) {
+    uint64_t* flags, int32_t* part_first, int32_t* part_last,
+    uint64_t* view_entry) {
   __shared__ uint32_t s_row[256];
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  // The sample view's slots (when built) start empty; ScatterRuns fills the
+  // ones where a written run starts.
+  if (view_entry != nullptr && i < n) view_entry[i] = kNoEntry;
   const K key = i < n ? skeys[i] : SentinelKey<K>();
   const bool valid = key != SentinelKey<K>();
   uint32_t row = 0;
@@ -1127,8 +1133,6 @@ struct ViewParts {
   uint32_t* pos;         // [M + 1] view positions (scan of entry != kNoEntry)
   int64_t rows_per_partition;
 };
-constexpr uint64_t kNoEntry = ~0ull;  // table rows stay below 2^32 - 1
-
 template <typename K>
 __global__ __launch_bounds__(256) void ScatterRuns(
     const K* skeys, const uint32_t* srows, const uint32_t* run_pos,
@@ -1165,12 +1169,6 @@ __global__ __launch_bounds__(256) void ScatterRuns(
   }
 }
 
-__global__ __launch_bounds__(256) void FillU64(uint64_t* p, int64_t n,
-                                               uint64_t v) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = v;
-}
-
 // 1 where a written run starts (input order), 0 elsewhere and at m.
 __global__ __launch_bounds__(256) void MarkEntries(const uint64_t* entry,
                                                    int64_t m, uint32_t* mark) {
@@ -1197,11 +1195,18 @@ __global__ __launch_bounds__(256) void ViewCompact(
   }
 }
 
+// Also copies the grouped-entry total into the counters when `totals` is
+// not null (after ScatterRuns, which reads it).
 __global__ __launch_bounds__(256) void WritePadding(const FillPlan* plans,
                                                     int64_t num_buckets,
                                                     FillParams fp, int32_t* eid,
-                                                    int32_t* sid, float* gains) {
+                                                    int32_t* sid, float* gains,
+                                                    const uint64_t* totals,
+                                                    int64_t* counters) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t == 0 && totals != nullptr) {
+    counters[3] = static_cast<int64_t>(static_cast<uint32_t>(totals[0]));
+  }
   const int64_t bkt = t / kAlign;
   const int k = static_cast<int>(t % kAlign);
   if (bkt >= num_buckets) return;
@@ -1443,6 +1448,38 @@ __global__ __launch_bounds__(256) void UploadKernel(UploadChunk c, int n,
   for (int i = threadIdx.x; i < n; i += blockDim.x) dst[i] = c.words[i];
 }
 
+// The set-up of one call in one launch, when both descriptor arrays fit in
+// one chunk: zeroed counters, partition bounds at -1, zeroed split counts,
+// and the slice and feature descriptors copied from the kernel arguments.
+struct SetupArgs {
+  int64_t* counters;
+  int32_t* part_first;
+  int32_t* part_last;
+  int64_t num_buckets;
+  int32_t* split_words;  // may be null
+  int64_t num_split_words;
+  uint32_t* slices;
+  uint32_t* feats;
+  int32_t slice_words;
+  int32_t feat_words;
+};
+
+__global__ __launch_bounds__(256) void SetupKernel(UploadChunk c,
+                                                   SetupArgs a) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < kNumCounters) a.counters[i] = 0;
+  if (i < a.num_buckets) {
+    a.part_first[i] = -1;
+    a.part_last[i] = -1;
+  }
+  if (a.split_words != nullptr && i < a.num_split_words) a.split_words[i] = 0;
+  if (i < a.slice_words) {
+    a.slices[i] = c.words[i];
+  } else if (i < a.slice_words + a.feat_words) {
+    a.feats[i - a.slice_words] = c.words[i];
+  }
+}
+
 int UploadBytes(const void* src, size_t bytes, void* dst,
                 hipStream_t stream) {
   if (bytes == 0) return 0;
@@ -1560,9 +1597,6 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
     if ((reinterpret_cast<uintptr_t>(counters) & 7u) != 0) {
       return Fail(SCEMB_ERR_INVALID_ARGUMENT, "stats buffer must be 8-byte aligned");
     }
-    hipLaunchKernelGGL(ZeroI64, dim3(1), dim3(64), 0, stream, counters,
-                       kNumCounters);
-    SCEMB_LAUNCH_CHECK();
     std::vector<FeatureDev> fd(nf);
     for (int f = 0; f < nf; ++f) {
       fd[f].ids = feats[f].ids;
@@ -1582,24 +1616,53 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
     }
     // The slice and feature descriptors travel as kernel arguments: no
     // pageable host copy, no host synchronisation.
-    int st = UploadBytes(pl.slices.data(),
-                         sizeof(SliceDesc) * pl.slices.size(), b.slices,
-                         stream);
-    if (st != 0) return st;
-    st = UploadBytes(fd.data(), sizeof(FeatureDev) * nf, b.feats, stream);
-    if (st != 0) return st;
-    hipLaunchKernelGGL(FillI32, dim3(CeilDiv(num_buckets, 256)), dim3(256), 0,
-                       stream, b.part_first, num_buckets, -1);
-    SCEMB_LAUNCH_CHECK();
-    hipLaunchKernelGGL(FillI32, dim3(CeilDiv(num_buckets, 256)), dim3(256), 0,
-                       stream, b.part_last, num_buckets, -1);
-    SCEMB_LAUNCH_CHECK();
-    if (split_counts != nullptr) {
-      const int64_t words = split_cells * (sizeof(BucketStats) / 4);
-      hipLaunchKernelGGL(FillI32, dim3(CeilDiv(words, 256)), dim3(256), 0,
-                         stream, reinterpret_cast<int32_t*>(split_counts),
-                         words, 0);
+    const size_t slice_bytes = sizeof(SliceDesc) * pl.slices.size();
+    const size_t feat_bytes = sizeof(FeatureDev) * nf;
+    const int64_t split_words =
+        split_counts != nullptr ? split_cells * (sizeof(BucketStats) / 4) : 0;
+    if (slice_bytes + feat_bytes <= sizeof(UploadChunk)) {
+      UploadChunk c;
+      std::memcpy(c.words, pl.slices.data(), slice_bytes);
+      std::memcpy(reinterpret_cast<char*>(c.words) + slice_bytes, fd.data(),
+                  feat_bytes);
+      SetupArgs a;
+      a.counters = counters;
+      a.part_first = b.part_first;
+      a.part_last = b.part_last;
+      a.num_buckets = num_buckets;
+      a.split_words = reinterpret_cast<int32_t*>(split_counts);
+      a.num_split_words = split_words;
+      a.slices = reinterpret_cast<uint32_t*>(b.slices);
+      a.feats = reinterpret_cast<uint32_t*>(b.feats);
+      a.slice_words = static_cast<int32_t>(slice_bytes / 4);
+      a.feat_words = static_cast<int32_t>(feat_bytes / 4);
+      const int64_t work = std::max<int64_t>(
+          {int64_t{kNumCounters}, num_buckets, split_words,
+           static_cast<int64_t>((slice_bytes + feat_bytes) / 4)});
+      hipLaunchKernelGGL(SetupKernel, dim3(CeilDiv(work, 256)), dim3(256), 0,
+                         stream, c, a);
       SCEMB_LAUNCH_CHECK();
+    } else {
+      hipLaunchKernelGGL(ZeroI64, dim3(1), dim3(64), 0, stream, counters,
+                         kNumCounters);
+      SCEMB_LAUNCH_CHECK();
+      int st = UploadBytes(pl.slices.data(), slice_bytes, b.slices, stream);
+      if (st != 0) return st;
+      st = UploadBytes(fd.data(), feat_bytes, b.feats, stream);
+      if (st != 0) return st;
+      hipLaunchKernelGGL(FillI32, dim3(CeilDiv(num_buckets, 256)), dim3(256),
+                         0, stream, b.part_first, num_buckets, -1);
+      SCEMB_LAUNCH_CHECK();
+      hipLaunchKernelGGL(FillI32, dim3(CeilDiv(num_buckets, 256)), dim3(256),
+                         0, stream, b.part_last, num_buckets, -1);
+      SCEMB_LAUNCH_CHECK();
+      if (split_counts != nullptr) {
+        hipLaunchKernelGGL(FillI32, dim3(CeilDiv(split_words, 256)),
+                           dim3(256), 0, stream,
+                           reinterpret_cast<int32_t*>(split_counts),
+                           split_words, 0);
+        SCEMB_LAUNCH_CHECK();
+      }
     }
     if (divisors != nullptr && pl.total_rows > 0) {
       hipLaunchKernelGGL(RowDivisors, dim3(CeilDiv(pl.total_rows, 256)),
@@ -1663,7 +1726,8 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   if (!measuring && M > 0) {
     hipLaunchKernelGGL((GroupFlags<K>), dim3(CeilDiv(M, 256)), dim3(256), 0,
                        stream, skeys, sidx, b.row_gain, M, pl.kl, pl.NS,
-                       b.srows, b.sgains, b.flags, b.part_first, b.part_last);
+                       b.srows, b.sgains, b.flags, b.part_first, b.part_last,
+                       view.entry);
     SCEMB_LAUNCH_CHECK();
   }
   st = ExclusiveScan<uint64_t>(b.flags, b.scan, M, b.totals, ws, stream);
@@ -1783,12 +1847,8 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                        stream, split_counts, sp, 1, counters);
     SCEMB_LAUNCH_CHECK();
   }
-  if (view.entry != nullptr && M > 0) {
-    view.sidx = sidx;
-    hipLaunchKernelGGL(FillU64, dim3(CeilDiv(M, 256)), dim3(256), 0, stream,
-                       view.entry, M, kNoEntry);
-    SCEMB_LAUNCH_CHECK();
-  }
+  // GroupFlags cleared the view's slots.
+  if (view.entry != nullptr) view.sidx = sidx;
   if (M > 0) {
     hipLaunchKernelGGL((ScatterRuns<K>), dim3(CeilDiv(M, 256)), dim3(256), 0,
                        stream, skeys, b.srows, b.run_pos, b.run_gain, b.keep,
@@ -1796,13 +1856,11 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                        static_cast<int32_t>(pl.bps), b.bstats, b.plans,
                        out->embedding_ids, out->sample_ids, out->gains, view);
     SCEMB_LAUNCH_CHECK();
-    hipLaunchKernelGGL(StoreTotal, dim3(1), dim3(1), 0, stream, b.totals,
-                       counters);
-    SCEMB_LAUNCH_CHECK();
   }
   hipLaunchKernelGGL(WritePadding, dim3(CeilDiv(num_buckets * kAlign, 256)),
                      dim3(256), 0, stream, b.plans, num_buckets, fp,
-                     out->embedding_ids, out->sample_ids, out->gains);
+                     out->embedding_ids, out->sample_ids, out->gains,
+                     M > 0 ? b.totals : nullptr, counters);
   SCEMB_LAUNCH_CHECK();
   if (view.entry != nullptr) {
     hipLaunchKernelGGL(MarkEntries, dim3(CeilDiv(M + 1, 256)), dim3(256), 0,
