@@ -388,7 +388,8 @@ typedef struct scemb_preprocess_options {
  *   [L*NS] max_ids_per_partition, [L*NS] max_unique_ids_per_partition,
  *   [L*S] required_buffer_size, then 6 int64 counters (8-byte aligned by the
  *   caller): dropped_id_count, limit_exceeded, bad_ids, total_entries,
- *   minibatching_required (pass 0), minibatching_split (pass 1). */
+ *   minibatching_required (pass 0), minibatching_split (pass 1). The call
+ *   initialises the whole block; the caller need not clear it. */
 typedef struct scemb_preprocess_output {
   int32_t* row_pointers;  /* [L * S * max(NS, 8)] (times 64, minibatching) */
   int32_t* embedding_ids; /* [L * coo_buffer_size_per_device] */

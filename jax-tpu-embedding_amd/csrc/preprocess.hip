@@ -1452,6 +1452,8 @@ __global__ __launch_bounds__(256) void UploadKernel(UploadChunk c, int n,
 // one chunk: zeroed counters, partition bounds at -1, zeroed split counts,
 // and the slice and feature descriptors copied from the kernel arguments.
 struct SetupArgs {
+  int32_t* stats;  // the stats slots before the counters
+  int64_t stats_words;
   int64_t* counters;
   int32_t* part_first;
   int32_t* part_last;
@@ -1467,6 +1469,7 @@ struct SetupArgs {
 __global__ __launch_bounds__(256) void SetupKernel(UploadChunk c,
                                                    SetupArgs a) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < a.stats_words) a.stats[i] = 0;
   if (i < kNumCounters) a.counters[i] = 0;
   if (i < a.num_buckets) {
     a.part_first[i] = -1;
@@ -1626,6 +1629,8 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
       std::memcpy(reinterpret_cast<char*>(c.words) + slice_bytes, fd.data(),
                   feat_bytes);
       SetupArgs a;
+      a.stats = out->stats;
+      a.stats_words = counters_off;
       a.counters = counters;
       a.part_first = b.part_first;
       a.part_last = b.part_last;
@@ -1637,12 +1642,15 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
       a.slice_words = static_cast<int32_t>(slice_bytes / 4);
       a.feat_words = static_cast<int32_t>(feat_bytes / 4);
       const int64_t work = std::max<int64_t>(
-          {int64_t{kNumCounters}, num_buckets, split_words,
+          {int64_t{kNumCounters}, counters_off, num_buckets, split_words,
            static_cast<int64_t>((slice_bytes + feat_bytes) / 4)});
       hipLaunchKernelGGL(SetupKernel, dim3(CeilDiv(work, 256)), dim3(256), 0,
                          stream, c, a);
       SCEMB_LAUNCH_CHECK();
     } else {
+      hipLaunchKernelGGL(FillI32, dim3(CeilDiv(counters_off, 256)), dim3(256),
+                         0, stream, out->stats, counters_off, 0);
+      SCEMB_LAUNCH_CHECK();
       hipLaunchKernelGGL(ZeroI64, dim3(1), dim3(64), 0, stream, counters,
                          kNumCounters);
       SCEMB_LAUNCH_CHECK();

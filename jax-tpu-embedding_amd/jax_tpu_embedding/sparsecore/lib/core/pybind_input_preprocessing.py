@@ -170,6 +170,7 @@ class _DeviceFeature:
   nnz: int
   valency: int
   max_id: int | None  # known when the input came from host memory
+  max_row_len: int = 0  # longest row of a ragged input (splits_host)
 
 
 def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
@@ -208,8 +209,9 @@ def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
       vals = vals.reshape(-1)
     else:
       vals = np.ascontiguousarray(np.asarray(vals), dtype=np.int32).reshape(-1)
+    lens = np.diff(splits)
     if splits.size == 0 or splits[0] != 0 or splits[-1] != vals.shape[0] or (
-        np.diff(splits) < 0).any():
+        lens.size and lens.min() < 0):
       raise ValueError("row_splits must start at 0, be non-decreasing and "
                        "end at the number of values.")
     w = None
@@ -225,7 +227,8 @@ def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
     if not isinstance(vals, t.Tensor) and vals.size:
       max_id = int(vals.max())
     return _DeviceFeature(ids, w, on_device(splits, t.int64),
-                          splits, splits.size - 1, int(splits[-1]), 0, max_id)
+                          splits, splits.size - 1, int(splits[-1]), 0, max_id,
+                          int(lens.max()) if lens.size else 0)
   arr = feature if isinstance(feature, np.ndarray) else np.asarray(
       feature, dtype=object)
   if arr.dtype != object and arr.ndim == 2:
@@ -268,7 +271,7 @@ def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
       on_device(ids_np, t.int32),
       None if w_np is None else on_device(w_np, t.float32),
       on_device(splits, t.int64), splits, len(rows),
-      int(splits[-1]), 0, max_id)
+      int(splits[-1]), 0, max_id, int(lens.max()) if lens.size else 0)
 
 
 def _resolve_feature(f: _DeviceFeature) -> _DeviceFeature:
@@ -282,13 +285,15 @@ def _preprocess_stack(feats, metas, *, local_device_count,
                       global_device_count, num_sc_per_device,
                       allow_id_dropping, has_weights, build_view=False,
                       enable_minibatching=False, minibatching_pass=0,
-                      minibatching_split=0, outputs=None, view_outputs=None):
+                      minibatching_split=0, outputs=None, view_outputs=None,
+                      stats_out=None):
   """Enqueues one stacked table (one minibatching pass of it with
   `enable_minibatching`); returns (rp, eid, sid, gains, stats on the
   device, (L, S, NS, counters offset), view) where view is the
   (keys, entries) pair of the CSR's sample view when `build_view`, else
   None. `outputs` / `view_outputs`: the (rp, eid, sid, gains) / view of an
-  earlier pass to write into."""
+  earlier pass to write into. `stats_out`: an int32 device tensor of
+  _stats_words(...) slots to hold the stats (else one is allocated)."""
   t = _native.require_gpu()
   lib = _native.load_library()
   dev = _native.device()
@@ -329,7 +334,13 @@ def _preprocess_stack(feats, metas, *, local_device_count,
     sid = t.empty(L * c, dtype=t.int32, device=dev)
     gains = t.empty(L * c, dtype=t.float32, device=dev)
   nstats = lib.scemb_preprocess_stats_size(ctypes.byref(opts))
-  stats = t.zeros(nstats + 2, dtype=t.int32, device=dev)
+  # The library initialises the whole stats block.
+  if stats_out is not None:
+    if int(stats_out.numel()) < nstats:
+      raise ValueError("stats buffer too small")
+    stats = stats_out
+  else:
+    stats = t.empty(nstats + 2, dtype=t.int32, device=dev)
   view = None
   if build_view:
     view = view_outputs or (t.empty(c, dtype=t.int32, device=dev),
@@ -344,6 +355,17 @@ def _preprocess_stack(feats, metas, *, local_device_count,
   off = int(lib.scemb_preprocess_stats_counters_offset(ctypes.byref(opts)))
   # The stats stay on the device until every stack has been enqueued.
   return rp, eid, sid, gains, stats, (L, S, ns, off), view
+
+
+def _stats_words(local_device_count, global_device_count, num_sc_per_device):
+  """int32 slots of one stack's stats block (scemb_preprocess_stats_size:
+  the per-partition stats rounded up to an even count, then six int64
+  counters), plus two so that consecutive blocks keep the counters 8-byte
+  aligned."""
+  L, S = local_device_count, num_sc_per_device
+  ns = S * global_device_count
+  stats = 2 * L * ns + L * S
+  return stats + stats % 2 + 2 * _NUM_COUNTERS + 2
 
 
 def preprocess_sparse_dense_matmul_input(
@@ -412,12 +434,28 @@ class PendingStats(list):
     super().__init__()
     self.num_minibatches = 1
     self.final_pass_stats = {}
+    self.stats_buffer = None  # the stacks' first-pass stats, one after another
 
 
-def _read_counters(entries):
-  """One wait: the int64 counters of each (stats tensor, offset)."""
+def _to_host(tensors) -> np.ndarray:
+  """The int32 device tensors, one after another, in one pinned host
+  buffer: asynchronous copies on the current stream, then one wait."""
   t = _native.torch()
-  host = t.cat([e[0] for e in entries]).cpu().numpy()
+  host = t.empty(sum(int(x.numel()) for x in tensors), dtype=t.int32,
+                 pin_memory=True)
+  pos = 0
+  for x in tensors:
+    n = int(x.numel())
+    host[pos:pos + n].copy_(x, non_blocking=True)
+    pos += n
+  t.cuda.current_stream().synchronize()
+  return host.numpy()
+
+
+def _read_counters(entries, buffer=None):
+  """One wait: the int64 counters of each (stats tensor, offset); `buffer`
+  (may be None): one device tensor holding the stats tensors in order."""
+  host = _to_host([buffer] if buffer is not None else [e[0] for e in entries])
   out, pos = [], 0
   for stats_dev, off in entries:
     chunk = host[pos:pos + stats_dev.numel()]
@@ -449,7 +487,8 @@ def _minibatching_passes(pending, jobs, csr, views):
   its runs per bucket when a limit was exceeded, so its counter 5 is the
   bucket pass's split (the library's pass 1 gives the same; the tests
   compare them). Waits for the device once."""
-  first = _read_counters([(p[1], p[5]) for p in pending])
+  first = _read_counters([(p[1], p[5]) for p in pending],
+                         pending.stats_buffer)
   for p, c in zip(pending, first):
     _raise_on_counters(p[0], c)
   if not any(c[4] for c in first):
@@ -498,7 +537,14 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
       ] for name, metas in stacks.items()
   }
   uploads.flush()
-  for name, metas in stacks.items():
+  # The stats of every stack's first pass share one device buffer, so that
+  # collect_stats reads them back with one copy.
+  words = _stats_words(local_device_count, global_device_count,
+                       num_sc_per_device)
+  pending.stats_buffer = _native.torch().empty(
+      words * len(stacks), dtype=_native.torch().int32,
+      device=_native.device())
+  for i, (name, metas) in enumerate(stacks.items()):
     feats = [_resolve_feature(f) for f in stack_feats[name]]
     kwargs = dict(feats=feats, metas=metas,
                   local_device_count=local_device_count,
@@ -508,7 +554,8 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
                   has_weights=feature_weights is not None,
                   enable_minibatching=enable_minibatching)
     rp, eid, sid, gains, stats_dev, (L, S, ns, off), view = _preprocess_stack(
-        **kwargs, build_view=build_view)
+        **kwargs, build_view=build_view,
+        stats_out=pending.stats_buffer[i * words:(i + 1) * words])
     if view is not None:
       sample_views[name] = view
     pending.append((name, stats_dev, L, S, ns, off, feats))
@@ -532,7 +579,7 @@ def one_id_per_row(pending) -> dict:
     ok = True
     for f in feats:
       if f.splits_host is not None:
-        ok = ok and (f.nnz == 0 or int(np.diff(f.splits_host).max()) <= 1)
+        ok = ok and f.max_row_len <= 1
       else:
         ok = ok and f.valency <= 1
     out[name] = ok
@@ -545,11 +592,13 @@ def collect_stats(pending) -> SparseDenseMatmulInputStats:
   stats = SparseDenseMatmulInputStats()
   if not pending:
     return stats
-  t = _native.torch()
   final = getattr(pending, "final_pass_stats", {})
   later = [final[p[0]] for p in pending if p[0] in final]
   # One wait for the first passes' stats and any later pass's counters.
-  host = t.cat([p[1] for p in pending] + [x[0] for x in later]).cpu().numpy()
+  # The stacks' stats tensors are consecutive slices of stats_buffer.
+  buffer = getattr(pending, "stats_buffer", None)
+  host = _to_host(([buffer] if buffer is not None else
+                   [p[1] for p in pending]) + [x[0] for x in later])
   pos = 0
   tail = sum(p[1].numel() for p in pending)
   for name, stats_dev, L, S, ns, off, _ in pending:
