@@ -331,6 +331,25 @@ def require_gpu():
   return t
 
 
+# Side streams for independent work within one call (per device, created
+# once, default priority).
+NUM_SIDE_STREAMS = 4
+_side_streams = {}
+
+
+def side_streams(n: int) -> list:
+  """The first n side streams of the current device."""
+  if n <= 0:
+    return []
+  t = torch()
+  dev = t.cuda.current_device()
+  pool = _side_streams.get(dev)
+  if pool is None:
+    pool = [t.cuda.Stream(device=dev) for _ in range(NUM_SIDE_STREAMS)]
+    _side_streams[dev] = pool
+  return pool[:n]
+
+
 def stream_handle() -> int:
   t = torch()
   return t.cuda.current_stream().cuda_stream

@@ -15,6 +15,7 @@ here (the reference's all-reduce across hosts is not part of this path).
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import dataclasses
 import enum
@@ -286,14 +287,17 @@ def _preprocess_stack(feats, metas, *, local_device_count,
                       allow_id_dropping, has_weights, build_view=False,
                       enable_minibatching=False, minibatching_pass=0,
                       minibatching_split=0, outputs=None, view_outputs=None,
-                      stats_out=None):
+                      stats_out=None, stream=None):
   """Enqueues one stacked table (one minibatching pass of it with
   `enable_minibatching`); returns (rp, eid, sid, gains, stats on the
   device, (L, S, NS, counters offset), view) where view is the
   (keys, entries) pair of the CSR's sample view when `build_view`, else
   None. `outputs` / `view_outputs`: the (rp, eid, sid, gains) / view of an
   earlier pass to write into. `stats_out`: an int32 device tensor of
-  _stats_words(...) slots to hold the stats (else one is allocated)."""
+  _stats_words(...) slots to hold the stats (else one is allocated).
+  `stream` (may be None): the stream to enqueue on instead of the current
+  one; the outputs are still allocated on the current stream, which the
+  caller makes wait for `stream` before it uses them."""
   t = _native.require_gpu()
   lib = _native.load_library()
   dev = _native.device()
@@ -322,7 +326,6 @@ def _preprocess_stack(feats, metas, *, local_device_count,
                                              ctypes.byref(opts))
   if need == 0:
     _native.check(_native.SCEMB_ERR_INVALID_ARGUMENT)
-  ws = _native.WORKSPACE.get(need)
   L, S = local_device_count, num_sc_per_device
   if outputs is not None:
     rp, eid, sid, gains = outputs
@@ -349,9 +352,13 @@ def _preprocess_stack(feats, metas, *, local_device_count,
       _native.ptr(rp), _native.ptr(eid), _native.ptr(sid), _native.ptr(gains),
       _native.ptr(stats), None if view is None else _native.ptr(view[0]),
       None if view is None else _native.ptr(view[1]))
-  _native.check(lib.scemb_preprocess_stacked_table(
-      structs, len(feats), ctypes.byref(opts), ctypes.byref(out),
-      _native.ptr(ws), ws.numel(), _native.stream_handle()))
+  with (t.cuda.stream(stream) if stream is not None else
+        contextlib.nullcontext()):
+    # The workspace belongs to the stream the work is enqueued on.
+    ws = _native.WORKSPACE.get(need)
+    _native.check(lib.scemb_preprocess_stacked_table(
+        structs, len(feats), ctypes.byref(opts), ctypes.byref(out),
+        _native.ptr(ws), ws.numel(), _native.stream_handle()))
   off = int(lib.scemb_preprocess_stats_counters_offset(ctypes.byref(opts)))
   # The stats stay on the device until every stack has been enqueued.
   return rp, eid, sid, gains, stats, (L, S, ns, off), view
@@ -541,9 +548,20 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
   # collect_stats reads them back with one copy.
   words = _stats_words(local_device_count, global_device_count,
                        num_sc_per_device)
-  pending.stats_buffer = _native.torch().empty(
-      words * len(stacks), dtype=_native.torch().int32,
-      device=_native.device())
+  t = _native.torch()
+  pending.stats_buffer = t.empty(words * len(stacks), dtype=t.int32,
+                                 device=_native.device())
+  # Stacks are independent: with several, each is enqueued on one of a few
+  # side streams, forked from and joined back into the current stream, so
+  # that their chains of small kernels overlap on the device.
+  sides = _native.side_streams(min(len(stacks), _native.NUM_SIDE_STREAMS)
+                               if len(stacks) > 1 else 0)
+  if sides:
+    main = t.cuda.current_stream()
+    fork = t.cuda.Event()
+    fork.record(main)
+    for s in sides:
+      s.wait_event(fork)
   for i, (name, metas) in enumerate(stacks.items()):
     feats = [_resolve_feature(f) for f in stack_feats[name]]
     kwargs = dict(feats=feats, metas=metas,
@@ -555,7 +573,8 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
                   enable_minibatching=enable_minibatching)
     rp, eid, sid, gains, stats_dev, (L, S, ns, off), view = _preprocess_stack(
         **kwargs, build_view=build_view,
-        stats_out=pending.stats_buffer[i * words:(i + 1) * words])
+        stats_out=pending.stats_buffer[i * words:(i + 1) * words],
+        stream=sides[i % len(sides)] if sides else None)
     if view is not None:
       sample_views[name] = view
     pending.append((name, stats_dev, L, S, ns, off, feats))
@@ -565,6 +584,10 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
       rp, eid, sid, gains = (rp.reshape(L, -1), eid.reshape(L, -1),
                              sid.reshape(L, -1), gains.reshape(L, -1))
     rps[name], eids[name], sids[name], gns[name] = rp, eid, sid, gains
+  for s in sides:
+    done = t.cuda.Event()
+    done.record(s)
+    main.wait_event(done)
   if enable_minibatching:
     _minibatching_passes(pending, jobs, flat,
                          sample_views if sample_views is not None else {})
