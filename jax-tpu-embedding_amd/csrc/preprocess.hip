@@ -270,14 +270,9 @@ struct BlockRows {
 // One thread per ExtractIds block: two binary searches over the row splits,
 // run for all blocks at once before the extraction, so that an extraction
 // thread only searches the few rows its block spans.
-__global__ __launch_bounds__(256) void BlockBounds(const SliceDesc* slices,
-                                                   int num_slices,
-                                                   const FeatureDev* feats,
-                                                   int64_t total_ids,
-                                                   int64_t num_blocks,
-                                                   BlockRows* out) {
-  const int64_t blk = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (blk >= num_blocks) return;
+__device__ __forceinline__ BlockRows ComputeBlockRows(
+    const SliceDesc* slices, int num_slices, const FeatureDev* feats,
+    int64_t total_ids, int64_t blk) {
   const int64_t first = blk * kExtractBlock;
   const int64_t last = min(first + kExtractBlock, total_ids) - 1;
   BlockRows br{-1, 0, 0, -1};
@@ -294,7 +289,18 @@ __global__ __launch_bounds__(256) void BlockBounds(const SliceDesc* slices,
                                 sl.id_begin + (last - sl.out_begin));
     }
   }
-  out[blk] = br;
+  return br;
+}
+
+__global__ __launch_bounds__(256) void BlockBounds(const SliceDesc* slices,
+                                                   int num_slices,
+                                                   const FeatureDev* feats,
+                                                   int64_t total_ids,
+                                                   int64_t num_blocks,
+                                                   BlockRows* out) {
+  const int64_t blk = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (blk >= num_blocks) return;
+  out[blk] = ComputeBlockRows(slices, num_slices, feats, total_ids, blk);
 }
 
 // One thread per extracted id (output position o, in slice order): finds its
@@ -536,12 +542,10 @@ struct BucketStats {
   int32_t kept_first;
 };
 
-__global__ __launch_bounds__(256) void BucketReduce(
+__device__ __forceinline__ BucketStats ReduceBucket(
     const int32_t* part_first, const int32_t* part_last,
     const uint64_t* flags, const uint64_t* scan, const uint32_t* keep_scan,
-    int64_t num_buckets, BucketStats* stats) {
-  const int64_t bkt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (bkt >= num_buckets) return;
+    int64_t bkt) {
   BucketStats s{0, 0, 0, 0};
   const int32_t f = part_first[bkt];
   if (f >= 0) {
@@ -558,8 +562,28 @@ __global__ __launch_bounds__(256) void BucketReduce(
     s.kept_first = static_cast<int32_t>(keep_scan[rf]);
     s.kept = static_cast<int32_t>(keep_scan[rend] - keep_scan[rf]);
   }
-  stats[bkt] = s;
+  return s;
 }
+
+__global__ __launch_bounds__(256) void BucketReduce(
+    const int32_t* part_first, const int32_t* part_last,
+    const uint64_t* flags, const uint64_t* scan, const uint32_t* keep_scan,
+    int64_t num_buckets, BucketStats* stats) {
+  const int64_t bkt = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (bkt >= num_buckets) return;
+  stats[bkt] = ReduceBucket(part_first, part_last, flags, scan, keep_scan, bkt);
+}
+
+// BucketReduce's inputs, for the kernels that fold it in.
+struct BucketReduceArgs {
+  const int32_t* part_first;
+  const int32_t* part_last;
+  const uint64_t* flags;
+  const uint64_t* scan;
+  const uint32_t* keep_scan;
+  int64_t num_buckets;  // 0: the stats were reduced beforehand
+  BucketStats* out;
+};
 
 struct FillPlan {
   int64_t start;      // absolute position of the first kept entry
@@ -585,11 +609,20 @@ struct FillParams {
 };
 
 // One thread per segment replays FillBufferSegment over partition counts; a
-// second loop reduces device stats (max over local SCs).
+// second loop reduces device stats (max over local SCs). With
+// br.num_buckets > 0 the block first reduces the bucket stats itself
+// (BucketReduce folded in; bstats is then br.out).
 __global__ __launch_bounds__(256) void FillPlanKernel(
     const BucketStats* bstats, FillParams fp, int32_t* rp_out,
     FillPlan* plans, int32_t* stat_max_ids, int32_t* stat_max_unique,
-    int32_t* stat_required, int64_t* counters) {
+    int32_t* stat_required, int64_t* counters, BucketReduceArgs br) {
+  if (br.num_buckets > 0) {
+    for (int64_t bkt = threadIdx.x; bkt < br.num_buckets; bkt += blockDim.x) {
+      br.out[bkt] = ReduceBucket(br.part_first, br.part_last, br.flags,
+                                 br.scan, br.keep_scan, bkt);
+    }
+    __syncthreads();
+  }
   const int S = fp.segs_per_device;
   const int NS = fp.num_partitions;
   const int num_segments = fp.local_devices * S;
@@ -1464,6 +1497,11 @@ struct SetupArgs {
   uint32_t* feats;
   int32_t slice_words;
   int32_t feat_words;
+  // BlockBounds of the extraction, read from the descriptors in the chunk.
+  int32_t num_slices;
+  int64_t total_ids;
+  int64_t extract_blocks;
+  BlockRows* block_rows;
 };
 
 __global__ __launch_bounds__(256) void SetupKernel(UploadChunk c,
@@ -1480,6 +1518,12 @@ __global__ __launch_bounds__(256) void SetupKernel(UploadChunk c,
     a.slices[i] = c.words[i];
   } else if (i < a.slice_words + a.feat_words) {
     a.feats[i - a.slice_words] = c.words[i];
+  }
+  if (i < a.extract_blocks) {
+    a.block_rows[i] = ComputeBlockRows(
+        reinterpret_cast<const SliceDesc*>(c.words), a.num_slices,
+        reinterpret_cast<const FeatureDev*>(c.words + a.slice_words),
+        a.total_ids, i);
   }
 }
 
@@ -1619,6 +1663,7 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
     }
     // The slice and feature descriptors travel as kernel arguments: no
     // pageable host copy, no host synchronisation.
+    bool bounds_done = false;  // BlockBounds folded into the set-up
     const size_t slice_bytes = sizeof(SliceDesc) * pl.slices.size();
     const size_t feat_bytes = sizeof(FeatureDev) * nf;
     const int64_t split_words =
@@ -1641,9 +1686,15 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
       a.feats = reinterpret_cast<uint32_t*>(b.feats);
       a.slice_words = static_cast<int32_t>(slice_bytes / 4);
       a.feat_words = static_cast<int32_t>(feat_bytes / 4);
+      a.num_slices = static_cast<int32_t>(pl.slices.size());
+      a.total_ids = M;
+      a.extract_blocks = M > 0 ? extract_blocks : 0;
+      a.block_rows = b.block_rows;
+      bounds_done = true;
       const int64_t work = std::max<int64_t>(
           {int64_t{kNumCounters}, counters_off, num_buckets, split_words,
-           static_cast<int64_t>((slice_bytes + feat_bytes) / 4)});
+           static_cast<int64_t>((slice_bytes + feat_bytes) / 4),
+           a.extract_blocks});
       hipLaunchKernelGGL(SetupKernel, dim3(CeilDiv(work, 256)), dim3(256), 0,
                          stream, c, a);
       SCEMB_LAUNCH_CHECK();
@@ -1681,10 +1732,12 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
     }
     if (M > 0) {
       const int num_slices = static_cast<int>(pl.slices.size());
-      hipLaunchKernelGGL(BlockBounds, dim3(CeilDiv(extract_blocks, 256)),
-                         dim3(256), 0, stream, b.slices, num_slices, b.feats,
-                         M, extract_blocks, b.block_rows);
-      SCEMB_LAUNCH_CHECK();
+      if (!bounds_done) {
+        hipLaunchKernelGGL(BlockBounds, dim3(CeilDiv(extract_blocks, 256)),
+                           dim3(256), 0, stream, b.slices, num_slices,
+                           b.feats, M, extract_blocks, b.block_rows);
+        SCEMB_LAUNCH_CHECK();
+      }
       hipLaunchKernelGGL((ExtractIds<K>), dim3(extract_blocks),
                          dim3(kExtractBlock), 0, stream, b.slices, num_slices,
                          b.feats, b.block_rows, M, o->combiner,
@@ -1773,10 +1826,16 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                : 0;
   }
   if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
-  hipLaunchKernelGGL(BucketReduce, dim3(CeilDiv(num_buckets, 256)), dim3(256),
-                     0, stream, b.part_first, b.part_last, b.flags, b.scan,
-                     b.keep_scan, num_buckets, b.bstats);
-  SCEMB_LAUNCH_CHECK();
+  // Without minibatching the fill plan's single block reduces the bucket
+  // stats first (one launch less).
+  BucketReduceArgs bra{b.part_first, b.part_last, b.flags, b.scan,
+                       b.keep_scan, minibatching ? 0 : num_buckets, b.bstats};
+  if (minibatching) {
+    hipLaunchKernelGGL(BucketReduce, dim3(CeilDiv(num_buckets, 256)),
+                       dim3(256), 0, stream, b.part_first, b.part_last,
+                       b.flags, b.scan, b.keep_scan, num_buckets, b.bstats);
+    SCEMB_LAUNCH_CHECK();
+  }
   FillParams fp;
   fp.local_devices = pl.L;
   fp.segs_per_device = pl.S;
@@ -1838,7 +1897,7 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   } else {
     hipLaunchKernelGGL(FillPlanKernel, dim3(1), dim3(256), 0, stream, b.bstats,
                        fp, out->row_pointers, b.plans, stat_max_ids,
-                       stat_max_unique, stat_required, counters);
+                       stat_max_unique, stat_required, counters, bra);
   }
   SCEMB_LAUNCH_CHECK();
   if (split_counts != nullptr && M > 0) {

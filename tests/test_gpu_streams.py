@@ -195,3 +195,57 @@ def test_graph_replays_after_its_workspace_is_outgrown():
       np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy(),
                                     err_msg=f"replay {i}")
     _assert_same(eager, graphed, f"replay {i}")
+
+
+def _specs_three_stacks(batch):
+  """Three tables of different dims: three stacks in one call."""
+  tables = [embedding_spec.TableSpec(
+      name=f"d{dim}", vocabulary_size=v, embedding_dim=dim,
+      initializer=embedding_spec.zeros,
+      optimizer=embedding_spec.AdagradOptimizerSpec(0.05), combiner="sum",
+      max_ids_per_partition=1 << 20, max_unique_ids_per_partition=1 << 20)
+            for dim, v in ((8, 700), (16, 9000), (32, 120000))]
+  feats = [embedding_spec.FeatureSpec(
+      name=f"f{i}", table_spec=t, input_shape=[batch, 1],
+      output_shape=[batch, t.embedding_dim]) for i, t in enumerate(tables)]
+  embedding.prepare_feature_specs_for_training(feats, 1, 1)
+  return feats
+
+
+@pytest.mark.parametrize("multi_hot", [False, True])
+def test_stacks_on_side_streams_equal_one_stream(multi_hot, monkeypatch):
+  """The stacks of one call are enqueued on forked side streams; the CSR
+  (compared region), the stats and a training step equal those of the same
+  call with every stack on the calling stream."""
+  feats = _specs_three_stacks(4096)
+  assert len(embedding.get_stacked_table_specs(feats)) == 3
+  ids = _ids(np.random.default_rng(21), feats, multi_hot)
+  grads = _grads(feats, 6)
+  init = _state(feats, 4)
+  runs = []
+  for sides in (_native.NUM_SIDE_STREAMS, 0):
+    monkeypatch.setattr(_native, "NUM_SIDE_STREAMS", sides)
+    pre, stats = embedding.preprocess_sparse_dense_matmul_input(
+        ids, None, feats, 1, 1, num_sc_per_device=1)
+    state = _clone(init)
+    acts = _step(pre, state, feats, grads)
+    torch.cuda.synchronize()
+    runs.append((_csr(pre), stats, state,
+                 [a.cpu().numpy() for a in acts]))
+  (csr_a, stats_a, state_a, acts_a), (csr_b, stats_b, state_b, acts_b) = runs
+  rp_a, eid_a, sid_a, gains_a = csr_a
+  rp_b, eid_b, sid_b, gains_b = csr_b
+  for name in rp_a:
+    np.testing.assert_array_equal(rp_a[name], rp_b[name])
+    end = int(rp_a[name][-1])
+    for x, y in ((eid_a, eid_b), (sid_a, sid_b), (gains_a, gains_b)):
+      np.testing.assert_array_equal(x[name][:end], y[name][:end],
+                                    err_msg=name)
+    np.testing.assert_array_equal(stats_a.max_ids_per_partition[name],
+                                  stats_b.max_ids_per_partition[name])
+    np.testing.assert_array_equal(stats_a.required_buffer_size_per_sc[name],
+                                  stats_b.required_buffer_size_per_sc[name])
+    assert stats_a.id_drop_counters[name] == stats_b.id_drop_counters[name]
+  for a, b in zip(acts_a, acts_b):
+    np.testing.assert_array_equal(a, b)
+  _assert_same(state_a, state_b, "side streams vs one stream")
