@@ -143,7 +143,15 @@ typedef struct scemb_sample_view {
   int64_t device_batch_size;
   int64_t table_rows;
   int64_t num_entries;      /* as scemb_csr_t.num_entries */
+  uint32_t flags;           /* SCEMB_VIEW_* bits */
+  int32_t reserved;
 } scemb_sample_view_t;
+
+/* No key appears twice (the view of a CSR with SCEMB_CSR_ONE_ENTRY_PER_ROW):
+ * no activation row's sum crosses a work-group, so the forward pass skips its
+ * cross-block combining launch. A repeated key is reported through
+ * SCEMB_STATUS_SHARED_ROW (results are then not valid). */
+#define SCEMB_VIEW_ONE_ENTRY_PER_KEY 1u
 
 /* One feature's rows of a stacked activation (or activation-gradient)
  * matrix of device_batch_size x dim: stacked rows [first_row, first_row +

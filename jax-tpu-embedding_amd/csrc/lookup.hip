@@ -230,6 +230,12 @@ int ForwardImpl(const scemb_csr_t* csr, const scemb_sample_view_t* view,
   r.dim = dim;
   r.batch = batch;
   r.status = status;
+  // Keys that never repeat: a view that says so, or the placement of a
+  // one-entry-per-row CSR.
+  r.single_runs =
+      view != nullptr
+          ? (view->flags & SCEMB_VIEW_ONE_ENTRY_PER_KEY) != 0
+          : (csr->flags & SCEMB_CSR_ONE_ENTRY_PER_ROW) != 0;
   if (map != nullptr) r.act = *map;
   int g, vec;
   PickLayout(dim, Aligned16(table) && (map != nullptr ? map_vec4

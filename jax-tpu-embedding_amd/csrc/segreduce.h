@@ -363,6 +363,9 @@ struct RowArgs {
   uint32_t* block_flags;
   uint32_t* block_keys;
   uint32_t* status;
+  // Every key has one entry: no run crosses a block, SegFinish is not
+  // launched, and a block that finds one reports SCEMB_STATUS_SHARED_ROW.
+  bool single_runs;
 };
 
 template <int SRC>
@@ -816,6 +819,9 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
     }
     r.block_flags[blk] = f;
     if (f & kFlagOwner) r.block_keys[blk] = kl;
+    if (r.single_runs && f != 0 && r.status != nullptr) {
+      atomicOr(r.status, SCEMB_STATUS_SHARED_ROW);
+    }
   }
 
   const Hyper H = LoadHyper<EPI>(r.opt);
@@ -1153,6 +1159,7 @@ int LaunchSegMapped(const StreamArgs& st, RowArgs r, const SegBuffers& sb,
     }                                                                        \
     ProfileEnd(prof, stream);                                                 \
     SCEMB_LAUNCH_CHECK();                                                     \
+    if (r.single_runs) return 0;                                              \
     prof = ProfileBegin(finish_span, stream);                                 \
     hipLaunchKernelGGL((SegFinish<GG, VV, EPI, kMapped>), grid, dim3(kBlock), \
                        0, stream, sb.num_blocks, r);                          \

@@ -98,7 +98,12 @@ class SampleView(ctypes.Structure):
       ("device_batch_size", ctypes.c_int64),
       ("table_rows", ctypes.c_int64),
       ("num_entries", ctypes.c_int64),
+      ("flags", ctypes.c_uint32),
+      ("reserved", ctypes.c_int32),
   ]
+
+
+VIEW_ONE_ENTRY_PER_KEY = 1
 
 
 class RowBlock(ctypes.Structure):
@@ -513,17 +518,21 @@ class LookupView:
   (device_batch_size, table_rows) pair it was built for."""
 
   def __init__(self, keys, entries, device_batch_size: int, table_rows: int,
-               num_entries: int = 0):
+               num_entries: int = 0, one_entry_per_key: bool = False):
     self.keys = keys          # int32 tensor holding the uint32 keys
     self.entries = entries    # int64 tensor holding the packed entries
     self.device_batch_size = int(device_batch_size)
     self.table_rows = int(table_rows)
     self.num_entries = int(num_entries)
+    # No key twice (one-hot input rows): SCEMB_VIEW_ONE_ENTRY_PER_KEY.
+    self.one_entry_per_key = bool(one_entry_per_key)
 
   def as_struct(self) -> SampleView:
     return SampleView(ptr(self.keys), ptr(self.entries),
                       int(self.keys.numel()), self.device_batch_size,
-                      self.table_rows, self.num_entries)
+                      self.table_rows, self.num_entries,
+                      VIEW_ONE_ENTRY_PER_KEY if self.one_entry_per_key else 0,
+                      0)
 
 
 def build_sample_view(csr: Csr, batch: int, table_rows: int,
@@ -543,7 +552,10 @@ def build_sample_view(csr: Csr, batch: int, table_rows: int,
   check(lib.scemb_build_sample_view(
       ctypes.byref(csr), batch, table_rows, ptr(keys), ptr(entries), ptr(ws),
       ws.numel(), ptr(device_status), stream_handle()))
-  return LookupView(keys, entries, batch, table_rows, csr.num_entries)
+  # A one-entry-per-row CSR is placed by activation row (a repeated row is
+  # reported through STATUS_SHARED_ROW), so its view repeats no key.
+  return LookupView(keys, entries, batch, table_rows, csr.num_entries,
+                    one_entry_per_key=bool(csr.flags & CSR_ONE_ENTRY_PER_ROW))
 
 
 def sparse_dense_matmul(csr: Csr | None, table, activations, batch: int,

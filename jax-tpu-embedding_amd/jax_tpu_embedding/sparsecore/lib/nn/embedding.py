@@ -319,16 +319,18 @@ def preprocess_sparse_dense_matmul_input(
     # One device: the preprocessing wrote each stack's sample view along with
     # its CSR; otherwise (several global devices) it is built from the CSR.
     stacked = get_stacked_table_specs(feature_specs)
+    one_per_row = pybind_input_preprocessing.one_id_per_row(pending)
     views = {
         name: _native.LookupView(
             keys, entries, stacked[name].total_sample_count,
-            stacked[name].stack_vocab_size)
+            stacked[name].stack_vocab_size,
+            one_entry_per_key=one_per_row.get(name, False))
         for name, (keys, entries) in built.items()}
     missing = [n for n in stacked if n not in views]
     if missing:
       views.update(_build_lookup_views(
           csr, feature_specs, global_device_count, num_sc_per_device,
-          pybind_input_preprocessing.one_id_per_row(pending), only=missing,
+          one_per_row, only=missing,
           num_minibatches=(pending.num_minibatches if enable_minibatching
                            else 0)))
   stats = pybind_input_preprocessing.collect_stats(pending)

@@ -770,3 +770,76 @@ def test_preprocessing_view_groups_like_the_csr_view(num_sc, weighted):
     np.testing.assert_allclose(acts[0], acts[1], rtol=RTOL, atol=ATOL)
   else:
     np.testing.assert_array_equal(acts[0], acts[1])
+
+
+@pytest.mark.parametrize("mapped", [False, True])
+def test_one_entry_per_key_view_skips_the_combining_pass(mapped):
+  """A one-hot stack's sample view declares that no key repeats: the
+  forward then skips its cross-block combining launch. Its activations equal
+  those of the same view without the declaration, bit for bit, through
+  the dense output and through per-feature row blocks."""
+  rng = np.random.default_rng(41)
+  batch, rows_, dim = 5000, 3000, 32
+  sid = rng.permutation(batch)[:4000].astype(np.int32)  # rows without ids
+  eid = rng.integers(0, rows_, size=sid.size).astype(np.int32)
+  gains = rng.uniform(0.5, 2.0, size=sid.size).astype(np.float32)
+  order = np.lexsort((sid, eid))
+  eid, sid, gains = eid[order], sid[order], gains[order]
+  n = -(-sid.size // 8) * 8
+  pad = n - sid.size
+  eid = np.concatenate([eid, np.full(pad, 2**31 - 1, np.int32)])
+  sid = np.concatenate([sid, np.full(pad, 2**31 - 1, np.int32)])
+  gains = np.concatenate([gains, np.full(pad, np.nan, np.float32)])
+  rp = np.full(8, 4000, np.int32)
+  keep, c = _device.csr_operands(rp, eid, sid, gains, 1, 1,
+                                 one_entry_per_row=True, num_entries=4000)
+  status = torch.zeros(1, dtype=torch.int32, device="cuda")
+  view = _native.build_sample_view(c, batch, rows_, device_status=status)
+  assert view.one_entry_per_key
+  plain = _native.LookupView(view.keys, view.entries, batch, rows_,
+                             view.num_entries)
+  table = torch.from_numpy(
+      rng.normal(size=(rows_, dim)).astype(np.float32)).cuda()
+  outs = []
+  for v in (view, plain):
+    if mapped:
+      blocks = [torch.full((2600, dim), 7.0, device="cuda"),
+                torch.full((2400, dim), 7.0, device="cuda")]
+      _native.sparse_dense_matmul_to_blocks(
+          None, table, [(0, blocks[0], dim), (2600, blocks[1], dim)],
+          batch, view=v, device_status=status)
+      out = torch.cat(blocks)
+    else:
+      out = torch.full((batch, dim), 7.0, device="cuda")
+      _native.sparse_dense_matmul(None, table, out, batch, view=v,
+                                  device_status=status)
+    outs.append(out.cpu().numpy())
+  torch.cuda.synchronize()
+  assert int(status.item()) == 0
+  np.testing.assert_array_equal(outs[0], outs[1])
+  expect = np.zeros((batch, dim), np.float32)
+  expect[sid[:4000]] = (gains[:4000, None] *
+                        table.cpu().numpy()[eid[:4000]])
+  np.testing.assert_array_equal(outs[0], expect)
+  del keep
+
+
+def test_repeated_key_in_one_entry_per_key_view_is_flagged():
+  """A view declared with no repeated key that has one spanning a block:
+  the forward reports SCEMB_STATUS_SHARED_ROW."""
+  batch, rows_, dim = 400, 16, 8
+  # Every key twice; positions 255 and 256 (two blocks) share key 128.
+  keys = ((np.arange(600) + 1) // 2).astype(np.uint32)
+  entries = (np.arange(600, dtype=np.uint64) % rows_) | (
+      np.uint64(np.float32(1.0).view(np.uint32)) << np.uint64(32))
+  kt = torch.from_numpy(keys.view(np.int32)).cuda()
+  et = torch.from_numpy(entries.view(np.int64)).cuda()
+  view = _native.LookupView(kt, et, batch, rows_, 600,
+                            one_entry_per_key=True)
+  table = torch.ones(rows_, dim, device="cuda")
+  out = torch.empty(batch, dim, device="cuda")
+  status = torch.zeros(1, dtype=torch.int32, device="cuda")
+  _native.sparse_dense_matmul(None, table, out, batch, view=view,
+                              device_status=status)
+  torch.cuda.synchronize()
+  assert int(status.item()) & _native.STATUS_SHARED_ROW
