@@ -171,7 +171,7 @@ class _DeviceFeature:
   nnz: int
   valency: int
   max_id: int | None  # known when the input came from host memory
-  max_row_len: int = 0  # longest row of a ragged input (splits_host)
+  one_id_per_row: bool = True  # no row of a ragged input holds two ids
 
 
 def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
@@ -229,7 +229,7 @@ def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
       max_id = int(vals.max())
     return _DeviceFeature(ids, w, on_device(splits, t.int64),
                           splits, splits.size - 1, int(splits[-1]), 0, max_id,
-                          int(lens.max()) if lens.size else 0)
+                          _one_id_per_row(lens, int(splits[-1])))
   arr = feature if isinstance(feature, np.ndarray) else np.asarray(
       feature, dtype=object)
   if arr.dtype != object and arr.ndim == 2:
@@ -272,7 +272,12 @@ def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
       on_device(ids_np, t.int32),
       None if w_np is None else on_device(w_np, t.float32),
       on_device(splits, t.int64), splits, len(rows),
-      int(splits[-1]), 0, max_id, int(lens.max()) if lens.size else 0)
+      int(splits[-1]), 0, max_id, _one_id_per_row(lens, int(splits[-1])))
+
+
+def _one_id_per_row(lens: np.ndarray, nnz: int) -> bool:
+  """Whether no row length exceeds 1 (more ids than rows settles it)."""
+  return nnz <= lens.size and (lens.size == 0 or int(lens.max()) <= 1)
 
 
 def _resolve_feature(f: _DeviceFeature) -> _DeviceFeature:
@@ -602,7 +607,7 @@ def one_id_per_row(pending) -> dict:
     ok = True
     for f in feats:
       if f.splits_host is not None:
-        ok = ok and f.max_row_len <= 1
+        ok = ok and f.one_id_per_row
       else:
         ok = ok and f.valency <= 1
     out[name] = ok
