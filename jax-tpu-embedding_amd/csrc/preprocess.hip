@@ -1288,23 +1288,41 @@ int MakePlan(const scemb_feature_t* feats, int nf,
   if (o == nullptr || (nf > 0 && feats == nullptr)) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null arguments");
   }
+  // PreprocessSparseDenseMatmulInputOptions::Validate
+  // (input_preprocessing_util.cc:490-522) and the empty-input check of
+  // input_preprocessing.cc:815-817, in their order and with their messages.
   const int L = o->local_device_count, G = o->global_device_count,
             S = o->num_sc_per_device;
-  if (L <= 0) return Fail(SCEMB_ERR_INVALID_ARGUMENT,
-                          "local_device_count must be greater than 0");
-  if (G <= 0) return Fail(SCEMB_ERR_INVALID_ARGUMENT,
-                          "global_device_count must be greater than 0");
-  if (G < L) return Fail(SCEMB_ERR_INVALID_ARGUMENT,
-                         "global_device_count must be greater than or equal "
-                         "to local_device_count");
-  if (S <= 0) return Fail(SCEMB_ERR_INVALID_ARGUMENT,
-                          "num_sc_per_device must be greater than 0");
+  if (L <= 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "local_device_count must be greater than 0, but got " +
+                    std::to_string(L));
+  }
+  if (G <= 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "global_device_count must be greater than 0, but got " +
+                    std::to_string(G));
+  }
+  if (G < L) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "global_device_count must be greater than or equal to "
+                "local_device_count, but got " +
+                    std::to_string(G) + " vs " + std::to_string(L));
+  }
+  if (S <= 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "num_sc_per_device must be greater than 0, but got " +
+                    std::to_string(S));
+  }
   const int64_t ns = static_cast<int64_t>(S) * G;
   if (ns > (1 << 20) || (ns & (ns - 1)) != 0) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT,
-                "Total number of SparseCores must be a power of 2.");
+                "Total number of SparseCores (" + std::to_string(ns) +
+                    ") must be a power of 2.");
   }
-  if (nf <= 0) return Fail(SCEMB_ERR_INVALID_ARGUMENT, "no features");
+  if (nf <= 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "input_batches cannot be empty.");
+  }
   if (o->combiner < 0 || o->combiner > 2) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT, "unknown combiner");
   }
@@ -1411,6 +1429,18 @@ int MakePlan(const scemb_feature_t* feats, int nf,
   }
   pl->total_ids = out;
   pl->total_rows = rows;
+  // With weights the sort key carries the extraction position, not the
+  // sample row, so duplicates of one (row, column) are adjacent after the
+  // sort only when rows ascend in extraction order. The reference merges a
+  // duplicate into the last kept entry even across a dropped one
+  // (sort_and_group_coo_tensors_impl.h:251-259); the grouping here merges
+  // adjacent duplicates, which is the same whenever rows ascend. Features in
+  // row_offset order (as GetStackedTableMetadata gives them) always do.
+  if (o->has_variable_weights && o->allow_id_dropping && !pl->rows_monotone) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "weighted features with id dropping must come in row_offset "
+                "order (sample rows ascending across the stack's features)");
+  }
   if (out >= (int64_t{1} << 31) - 1) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT, "too many ids in one stack");
   }

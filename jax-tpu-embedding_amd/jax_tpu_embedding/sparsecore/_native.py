@@ -308,6 +308,59 @@ def check(rc: int) -> None:
   raise RuntimeError(f"libscemb error {rc}: {msg}")
 
 
+# Validation mode: the lookup and update primitives hand the kernels a
+# device status word and read it back after each call (one host wait per
+# call), raising on what the kernels found: entries out of range (skipped),
+# or a stream declared sorted / with unrepeated keys that is not (results
+# not valid). Off by default; SCEMB_VALIDATE=1 in the environment or
+# set_validation(True) turns it on.
+_validate = os.environ.get("SCEMB_VALIDATE", "0") not in ("", "0")
+
+_STATUS_NAMES = (
+    (STATUS_BAD_ENTRY, "CSR entry with an embedding or sample id out of "
+     "range (skipped)"),
+    (STATUS_BAD_ID, "input id outside the table (skipped)"),
+    (STATUS_UNSORTED, "a stream declared sorted is not (results not valid)"),
+    (STATUS_SHARED_ROW, "a stream declared with one entry per row repeats a "
+     "row (results not valid)"),
+)
+
+
+def set_validation(on: bool) -> bool:
+  """Turns validation mode on or off; returns the previous setting."""
+  global _validate
+  prev, _validate = _validate, bool(on)
+  return prev
+
+
+def validation() -> bool:
+  return _validate
+
+
+def status_word():
+  """A zeroed device status word in validation mode, else None."""
+  if not _validate:
+    return None
+  t = torch()
+  return t.zeros(1, dtype=t.int32, device=device())
+
+
+def raise_on_status(flags: int, what: str) -> None:
+  """RuntimeError naming every status bit set in `flags`."""
+  flags = int(flags) & 0xFFFFFFFF
+  if flags == 0:
+    return
+  found = [text for bit, text in _STATUS_NAMES if flags & bit]
+  raise RuntimeError(f"{what}: device status {flags:#x}: " + "; ".join(found))
+
+
+def check_status_word(word, what: str) -> None:
+  """Waits for the stream and raises on a non-zero status word (None: no
+  check)."""
+  if word is not None:
+    raise_on_status(int(word.item()), what)
+
+
 # ---------------------------------------------------------------------------
 # torch plumbing.
 # ---------------------------------------------------------------------------
@@ -336,22 +389,28 @@ def require_gpu():
   return t
 
 
-# Side streams for independent work within one call (per device, created
-# once, default priority).
-NUM_SIDE_STREAMS = 4
+# Side streams for independent work within one call: a pool per (device,
+# calling stream), created on first use, default priority. Calls made from
+# different streams therefore never queue behind each other's side work nor
+# share its workspaces (one per stream, below). Three side streams plus the
+# calling stream match the four hardware queues a process gets by default.
+NUM_SIDE_STREAMS = 3
 _side_streams = {}
 
 
 def side_streams(n: int) -> list:
-  """The first n side streams of the current device."""
+  """The first n side streams of the current device's current stream."""
   if n <= 0:
     return []
   t = torch()
   dev = t.cuda.current_device()
-  pool = _side_streams.get(dev)
-  if pool is None:
-    pool = [t.cuda.Stream(device=dev) for _ in range(NUM_SIDE_STREAMS)]
-    _side_streams[dev] = pool
+  key = (dev, t.cuda.current_stream(dev).cuda_stream)
+  pool = _side_streams.get(key)
+  if pool is None or len(pool) < n:
+    pool = (pool or []) + [
+        t.cuda.Stream(device=dev)
+        for _ in range(max(n, NUM_SIDE_STREAMS) - len(pool or []))]
+    _side_streams[key] = pool
   return pool[:n]
 
 
@@ -445,8 +504,10 @@ def ptr(x) -> int | None:
 class _Workspace:
   """Scratch memory of the library's calls: one buffer per (device, stream),
   grown on demand and reused by later calls on the same stream, which stream
-  order makes safe. Calls on different streams never share a buffer, so
-  preprocessing on a side stream may overlap a step on another.
+  order makes safe. Calls on different streams never share a buffer (the
+  side streams a call forks to belong to its calling stream, see
+  side_streams), so preprocessing on one stream may overlap a step or
+  another preprocessing on another.
 
   A buffer that a call used while its stream was being captured into a graph
   stays allocated after it has been outgrown: the graph's replays still

@@ -71,8 +71,10 @@ def apply(kind: int, lhs_row_pointers, lhs_local_embedding_ids,
     grad = _native.as_device_tensor(activations_grad, t.float32,
                                     table.device)
     batch = int(grad.shape[0])
+  status = _native.status_word()
   _native.sparse_dense_matmul_grad_with_optimizer(
       csr, grad, table, kind, dev_slots, hyperparameters, batch, min_value,
-      max_value, flags=flags, grad_blocks=blocks)
+      max_value, flags=flags, grad_blocks=blocks, device_status=status)
+  _native.check_status_word(status, computation_name)
   del keep
   return (table, *dev_slots)

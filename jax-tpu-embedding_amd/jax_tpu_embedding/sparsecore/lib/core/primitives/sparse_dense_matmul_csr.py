@@ -15,7 +15,9 @@ by the preprocessing), which spares the call its grouping sort. A view built
 for another batch size or table height is ignored. ``activation_blocks``
 (a ``_device.RowBlocks``) makes the call write every activation row into its
 feature's block (the unstacking of ``embedding.py:903-1044`` fused into the
-kernel) and return that object instead of a stacked matrix.
+kernel) and return that object instead of a stacked matrix. In validation
+mode (``_native.set_validation``) the call checks the kernels' status word
+and raises RuntimeError on out-of-range entries or a mislabelled stream.
 ``csr_num_entries``, the
 CSR's entry count when known, picks the kernel variant (one-hot or
 multi-hot batches) and changes no result.
@@ -104,14 +106,19 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
       raise ValueError(
           f"activation_blocks of shape {activation_blocks.shape} do not match "
           f"the activations ({device_batch_size}, {table.shape[-1]})")
+    status = _native.status_word()
     _native.sparse_dense_matmul_to_blocks(csr, table, activation_blocks.blocks,
                                           int(device_batch_size),
-                                          view=lookup_view)
+                                          view=lookup_view,
+                                          device_status=status)
+    _native.check_status_word(status, "sparse_dense_matmul")
     del keep
     return activation_blocks
   out = t.empty(shape, dtype=t.float32, device=table.device)
+  status = _native.status_word()
   _native.sparse_dense_matmul(csr, table, out, int(device_batch_size),
-                              view=lookup_view)
+                              view=lookup_view, device_status=status)
+  _native.check_status_word(status, "sparse_dense_matmul")
   del keep
   return out
 

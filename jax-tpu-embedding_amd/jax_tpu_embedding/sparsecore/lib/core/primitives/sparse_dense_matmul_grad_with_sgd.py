@@ -66,9 +66,11 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
     grad = _native.as_device_tensor(activations_grad, t.float32,
                                     table.device)
     batch = int(grad.shape[0])
+  status = _native.status_word()
   _native.sparse_dense_matmul_grad(csr, grad, table, None, learning_rate,
                                    batch, min_value, max_value,
-                                   grad_blocks=blocks)
+                                   grad_blocks=blocks, device_status=status)
+  _native.check_status_word(status, computation_name)
   del keep
   return table
 

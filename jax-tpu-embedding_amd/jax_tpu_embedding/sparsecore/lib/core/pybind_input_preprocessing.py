@@ -405,7 +405,9 @@ def preprocess_sparse_dense_matmul_input(
   del batch_number, all_reduce_interface
   features, feature_weights, feature_specs = check_arguments(
       features, feature_weights, feature_specs, sharding_strategy,
-      enable_minibatching)
+      enable_minibatching, local_device_count=local_device_count,
+      global_device_count=global_device_count,
+      num_sc_per_device=num_sc_per_device)
   rps, eids, sids, gns, pending = enqueue_preprocessing(
       features, feature_weights, feature_specs, local_device_count,
       global_device_count, num_sc_per_device=num_sc_per_device,
@@ -417,12 +419,35 @@ def preprocess_sparse_dense_matmul_input(
 
 
 def check_arguments(features, feature_weights, feature_specs,
-                    sharding_strategy, enable_minibatching: bool):
-  """Argument checks of the preprocessing entry; returns the inputs as
-  lists."""
+                    sharding_strategy, enable_minibatching: bool, *,
+                    local_device_count: int, global_device_count: int,
+                    num_sc_per_device: int):
+  """Argument checks of the preprocessing entry, before any device work;
+  returns the inputs as lists. The option checks and their messages are
+  PreprocessSparseDenseMatmulInputOptions::Validate
+  (input_preprocessing_util.cc:490-522), then the empty-input check
+  (input_preprocessing.cc:815-817); the library repeats them."""
   del enable_minibatching  # every combination is accepted
   if int(sharding_strategy) != int(ShardingStrategy.MOD):
     raise ValueError("Only mod sharding is supported for now.")
+  if local_device_count <= 0:
+    raise ValueError("local_device_count must be greater than 0, but got "
+                     f"{local_device_count}")
+  if global_device_count <= 0:
+    raise ValueError("global_device_count must be greater than 0, but got "
+                     f"{global_device_count}")
+  if global_device_count < local_device_count:
+    raise ValueError(
+        "global_device_count must be greater than or equal to "
+        f"local_device_count, but got {global_device_count} vs "
+        f"{local_device_count}")
+  if num_sc_per_device <= 0:
+    raise ValueError("num_sc_per_device must be greater than 0, but got "
+                     f"{num_sc_per_device}")
+  num_scs = num_sc_per_device * global_device_count
+  if num_scs & (num_scs - 1):
+    raise ValueError(f"Total number of SparseCores ({num_scs}) must be a "
+                     "power of 2.")
   features = list(features)
   feature_specs = list(feature_specs)
   if feature_weights is not None:

@@ -304,7 +304,10 @@ def preprocess_sparse_dense_matmul_input(
       (_tree.tree_leaves(features_weights)
        if features_weights is not None else None),
       _tree.tree_leaves(feature_specs),
-      sharding_strategy_to_enum(sharding_strategy), enable_minibatching)
+      sharding_strategy_to_enum(sharding_strategy), enable_minibatching,
+      local_device_count=local_device_count,
+      global_device_count=global_device_count,
+      num_sc_per_device=num_sc_per_device)
   # Everything is enqueued (CSR build, then the lookup views) before the one
   # wait for the stats.
   built = {}
@@ -679,8 +682,9 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
                                  embedding_var_limits=None):
   """Backward pass + optimizer update (embedding.py:1297-1529).
 
-  Returns the updated EmbeddingVariables per stacked table; the tensors are
-  updated in place.
+  Returns the updated variables per stacked table, in the structure each
+  was given in (EmbeddingVariables or a (table, *slots) tuple); the tensors
+  are updated in place.
   """
   if isinstance(preprocessed_inputs, SparseDenseMatmulInput):
     warnings.warn("SparseDenseMatmulInput is deprecated. Please use "
@@ -739,8 +743,7 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
           opt.multiply_linear_by_learning_rate)
     if embedding_var_limits is not None:
       kwargs["min_value"], kwargs["max_value"] = embedding_var_limits[name]
-    flat = [ev.table, *ev.slot] if isinstance(ev, EmbeddingVariables) else \
-        list(_tree.tree_leaves(ev))
+    flat, treedef = _tree.tree_flatten(ev)
     res = opt.get_optimizer_primitive().bind(
         rp[name], eid[name], sid[name], gains[name], nmb, *flat, grads[name],
         *hyper, max_ids_per_partition=spec.max_ids_per_partition,
@@ -754,10 +757,10 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
                                  None) or {}).get(name),
         **kwargs)
     res = res if isinstance(res, tuple) else (res,)
-    slot_type = (type(ev.slot) if isinstance(ev, EmbeddingVariables) and
-                 hasattr(type(ev.slot), "_fields") else None)
-    slots = slot_type(*res[1:]) if slot_type else tuple(res[1:])
-    out[name] = EmbeddingVariables(res[0], slots)
+    # The updated variables in the structure they came in
+    # (embedding.py:1524-1527): EmbeddingVariables stay EmbeddingVariables
+    # (with their slot type), a plain (table, *slots) tuple stays a tuple.
+    out[name] = _tree.tree_unflatten(treedef, list(res))
   return out
 
 
@@ -829,3 +832,15 @@ def update_preprocessing_parameters(feature_specs, updated_params,
 
   for fs in _tree.tree_leaves(feature_specs):
     update(fs)
+
+
+# Spec <-> proto conversion, re-exported as the reference does
+# (embedding.py:1759-1765).
+from jax_tpu_embedding.sparsecore.lib.nn import embedding_proto_utils  # pylint: disable=g-import-not-at-top,g-bad-import-order
+
+get_optimizer_class = embedding_proto_utils.get_optimizer_class
+get_optimizer_type = embedding_proto_utils.get_optimizer_type
+optimizer_spec_to_proto = embedding_proto_utils.optimizer_spec_to_proto
+proto_to_optimizer_spec = embedding_proto_utils.proto_to_optimizer_spec
+create_proto_from_feature_specs = (
+    embedding_proto_utils.create_proto_from_feature_specs)

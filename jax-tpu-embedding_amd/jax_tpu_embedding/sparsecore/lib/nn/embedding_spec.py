@@ -117,6 +117,29 @@ class LaPropSlotVariables(NamedTuple):
   nu: Any
 
 
+class CallablePlaceholder:
+  """Stands in for a callable learning rate read back from a spec proto
+  (embedding_spec.py:53-76): comparable by its tag, not callable."""
+
+  def __init__(self, tag: str):
+    self.tag = tag
+
+  def __call__(self, *args, **kwargs):
+    raise RuntimeError(
+        f"CallablePlaceholder '{self.tag}' cannot be evaluated during model"
+        " execution. It is intended only for spec inspection and table"
+        " stacking.")
+
+  def __eq__(self, other: object) -> bool:
+    return isinstance(other, CallablePlaceholder) and self.tag == other.tag
+
+  def __hash__(self) -> int:
+    return hash(self.tag)
+
+  def __repr__(self) -> str:
+    return f"CallablePlaceholder({self.tag!r})"
+
+
 class OptimizerSpec:
   """Base of the optimizer specs (embedding_spec.py:122-247)."""
 
@@ -175,6 +198,21 @@ class OptimizerSpec:
   def get_bool_params(self) -> dict[str, bool]:
     return {p: bool(getattr(self, p)) for p in self._bool_params
             if hasattr(self, p)}
+
+  @classmethod
+  def from_float_and_bool_params(cls, float_params: dict[str, float],
+                                 bool_params: dict[str, bool],
+                                 learning_rate: LearningRate):
+    """The spec whose get_float_params / get_bool_params gave these
+    values (embedding_spec.py:232-247)."""
+    kwargs: dict[str, Any] = {"learning_rate": learning_rate}
+    for p in cls._float_params:
+      if p in float_params:
+        kwargs[p] = float(float_params[p])
+    for p in cls._bool_params:
+      if p in bool_params:
+        kwargs[p] = bool(bool_params[p])
+    return cls(**kwargs)
 
 
 class SGDOptimizerSpec(OptimizerSpec):

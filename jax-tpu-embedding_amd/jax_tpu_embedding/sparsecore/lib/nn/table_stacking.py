@@ -15,6 +15,9 @@ the reference's, because the CSR ids it produces index the stacked buffer:
   physical rows             compute_physical_row_ids (:1229-1255)
   stack / shard of values   stack_and_shard_tables (:144-221) and its inverse
                             unshard_and_unstack_tables (:226-311)
+  from a spec proto         stack_and_shard_feature_tables (:1080-1226),
+                            unstack_and_unshard_stacked_tables (:963-1077),
+                            get_row_ids_in_stacked_table(s) (:1258-1330)
 Table values here are numpy arrays or torch tensors.
 """
 
@@ -300,6 +303,34 @@ def compute_physical_row_ids(num_sparse_cores: int, stack_vocab_size: int,
   return shard_id * shard_size + sharded_row
 
 
+def get_row_ids_in_stacked_table(stack_table_spec, table_spec,
+                                 row_ids) -> list[int]:
+  """Rows of the stacked buffer holding rows `row_ids` of one table
+  (StackedTableSpecProto, TableSpecProto)."""
+  out = []
+  for row_id in row_ids:
+    if row_id >= table_spec.vocab_size:
+      raise ValueError(f"{row_id} exceeds available vocabulary size "
+                       f"[{table_spec.vocab_size}].")
+    out.append(compute_physical_row_ids(
+        stack_table_spec.num_sparsecores, stack_table_spec.stack_vocab_size,
+        table_spec.shard_rotation, table_spec.row_offset_in_shard, row_id))
+  return out
+
+
+def get_row_ids_in_stacked_tables(embedding_spec_proto,
+                                  row_ids: Mapping) -> dict[str, list[int]]:
+  """Stacked-buffer rows of the tables' rows in `row_ids` (keyed by table
+  name), grouped by stack name in the proto's table order."""
+  out: dict[str, list[int]] = collections.defaultdict(list)
+  for stack in embedding_spec_proto.stacked_table_specs:
+    for table in stack.table_specs:
+      if table.table_name in row_ids:
+        out[stack.stack_name].extend(get_row_ids_in_stacked_table(
+            stack, table, row_ids[table.table_name]))
+  return out
+
+
 # ---------------------------------------------------------------------------
 # Table values.
 # ---------------------------------------------------------------------------
@@ -371,6 +402,26 @@ def stack_and_shard_tables(table_specs, tables, num_shards: int,
   return out
 
 
+def _unshard_one(stacked_3d, row_offset_in_shard: int, per_shard: int,
+                 shard_rotation: int, vocab_size: int, embedding_dim: int):
+  """One table [vocab, dim] out of a stacked buffer viewed as
+  [num_shards, rows_per_shard, dim]: its rows of every shard, shards turned
+  back by the rotation, rows interleaved back (row i of shard s is logical
+  row i * num_shards + s), padding dropped."""
+  dim = stacked_3d.shape[-1]
+  r = row_offset_in_shard
+  part = stacked_3d[:, r:r + per_shard, :]
+  if _is_torch(part):
+    import torch  # pylint: disable=g-import-not-at-top
+
+    part = torch.roll(part, -shard_rotation, dims=0)
+    part = part.transpose(0, 1).reshape(-1, dim)
+  else:
+    part = np.roll(part, -shard_rotation, axis=0)
+    part = np.swapaxes(part, 0, 1).reshape(-1, dim)
+  return part[:vocab_size, :embedding_dim]
+
+
 def unshard_and_unstack_tables(table_specs, stacked_tables: Mapping,
                                num_shards: int):
   """Recovers each table [vocab, dim] from its stacked buffer."""
@@ -380,20 +431,103 @@ def unshard_and_unstack_tables(table_specs, stacked_tables: Mapping,
         spec.name
     st = stacked_tables[name]
     dim = st.shape[-1]
-    st = st.reshape(num_shards, -1, dim)
     per_shard = _next_largest_multiple(spec.vocabulary_size,
                                        8 * num_shards) // num_shards
     setting = spec.setting_in_stack
-    r = setting.row_offset_in_shard
-    part = st[:, r:r + per_shard, :]
-    if _is_torch(part):
-      import torch  # pylint: disable=g-import-not-at-top
-
-      part = torch.roll(part, -setting.shard_rotation, dims=0)
-      part = part.transpose(0, 1).reshape(-1, dim)
-    else:
-      part = np.roll(part, -setting.shard_rotation, axis=0)
-      part = np.swapaxes(part, 0, 1).reshape(-1, dim)
-    return part[:spec.vocabulary_size, :spec.embedding_dim]
+    return _unshard_one(st.reshape(num_shards, -1, dim),
+                        setting.row_offset_in_shard, per_shard,
+                        setting.shard_rotation, spec.vocabulary_size,
+                        spec.embedding_dim)
 
   return _tree.tree_map(one, table_specs)
+
+
+# ---------------------------------------------------------------------------
+# The same, driven by an EmbeddingSpecProto (checkpoint conversion).
+# ---------------------------------------------------------------------------
+
+
+def _unstack_and_unshard_stacked_table(stacked_table, stacked_table_spec,
+                                       donate: bool = False) -> dict:
+  """Tables of one stack, by name, from its stacked buffer [vocab, dim].
+  `donate` is accepted for the reference's signature; the buffer is left
+  to the caller."""
+  del donate
+  ns = stacked_table_spec.num_sparsecores
+  st = stacked_table.reshape(ns, -1, stacked_table_spec.stack_embedding_dim)
+  out = {}
+  for t in stacked_table_spec.table_specs:
+    out[t.table_name] = _unshard_one(st, t.row_offset_in_shard,
+                                     t.padded_vocab_size // ns,
+                                     t.shard_rotation, t.vocab_size,
+                                     t.embedding_dim)
+  return out
+
+
+def unstack_and_unshard_stacked_tables(stacked_tables: Mapping,
+                                       embedding_specs,
+                                       donate: bool = False) -> dict:
+  """Every table of an EmbeddingSpecProto, by name, from the stacked
+  buffers keyed by stack name."""
+  out = {}
+  for spec in embedding_specs.stacked_table_specs:
+    table = stacked_tables.get(spec.stack_name)
+    if table is None:
+      raise ValueError(f"Stacked table '{spec.stack_name}' not found in "
+                       "`stacked_tables`.")
+    out.update(_unstack_and_unshard_stacked_table(table, spec, donate))
+  return out
+
+
+def _shard_one(table, padded_vocab_size: int, padded_embedding_dim: int,
+               num_shards: int, shard_rotation: int):
+  """[num_shards, padded_vocab / num_shards, dim] block of one table:
+  zero padding, then logical row i to shard i % num_shards (row
+  i // num_shards), shards rotated by `shard_rotation`."""
+  rows, cols = table.shape
+  per_shard = padded_vocab_size // num_shards
+  if _is_torch(table):
+    import torch  # pylint: disable=g-import-not-at-top
+
+    padded = torch.zeros((padded_vocab_size, padded_embedding_dim),
+                         dtype=table.dtype, device=table.device)
+    padded[:rows, :cols] = table
+    block = padded.reshape(per_shard, num_shards, -1).transpose(0, 1)
+    return torch.roll(block, shard_rotation, dims=0)
+  padded = np.zeros((padded_vocab_size, padded_embedding_dim),
+                    np.asarray(table).dtype)
+  padded[:rows, :cols] = np.asarray(table)
+  block = np.swapaxes(padded.reshape(per_shard, num_shards, -1), 0, 1)
+  return np.roll(block, shard_rotation, axis=0)
+
+
+def stack_and_shard_feature_tables(feature_tables: Mapping, embedding_specs,
+                                   delete_input: bool = False) -> dict:
+  """The stacked buffer [stack_vocab, dim] of every stack of an
+  EmbeddingSpecProto from the unstacked tables keyed by table name.
+  `delete_input` is accepted for the reference's signature; the inputs are
+  left to the caller."""
+  del delete_input
+  out = {}
+  for spec in embedding_specs.stacked_table_specs:
+    blocks = []
+    for t in spec.table_specs:
+      table = feature_tables.get(t.table_name)
+      if table is None:
+        raise ValueError(f"{t.table_name}' not found in `feature_tables`.")
+      if spec.stack_embedding_dim != t.padded_embedding_dim:
+        raise ValueError(
+            f"Embedding dim of table_spec {t.table_name} is "
+            f"{t.padded_embedding_dim} but the stacked table embedding dim "
+            f"is {spec.stack_embedding_dim}.")
+      blocks.append(_shard_one(table, t.padded_vocab_size,
+                               t.padded_embedding_dim, spec.num_sparsecores,
+                               t.shard_rotation))
+    if blocks and _is_torch(blocks[0]):
+      import torch  # pylint: disable=g-import-not-at-top
+
+      stacked = torch.cat(blocks, dim=1)
+    else:
+      stacked = np.concatenate(blocks, axis=1)
+    out[spec.stack_name] = stacked.reshape(-1, spec.stack_embedding_dim)
+  return out

@@ -172,3 +172,19 @@ def test_embedding_size_helpers_with_minibatching():
   assert embedding.compute_row_pointers_size_per_device(
       global_device_count=1, num_sc_per_device=4,
       enable_minibatching=True) == 2048
+
+
+def test_device_status_decoding():
+  """Validation mode's status check names every bit the kernels set."""
+  _native.raise_on_status(0, "op")
+  with pytest.raises(RuntimeError, match=r"op: device status 0x8: .*repeats"):
+    _native.raise_on_status(_native.STATUS_SHARED_ROW, "op")
+  with pytest.raises(RuntimeError, match="out of range.*not valid"):
+    _native.raise_on_status(
+        _native.STATUS_BAD_ENTRY | _native.STATUS_UNSORTED, "op")
+  prev = _native.set_validation(False)
+  try:
+    assert _native.status_word() is None
+    _native.check_status_word(None, "op")
+  finally:
+    _native.set_validation(prev)

@@ -249,3 +249,55 @@ def test_stacks_on_side_streams_equal_one_stream(multi_hot, monkeypatch):
   for a, b in zip(acts_a, acts_b):
     np.testing.assert_array_equal(a, b)
   _assert_same(state_a, state_b, "side streams vs one stream")
+
+
+@pytest.mark.parametrize("multi_hot", [False, True])
+def test_two_user_streams_preprocess_multi_stack_batches(multi_hot):
+  """Two user streams each enqueue a multi-stack preprocessing (forking to
+  side streams of their own) before either is waited for; each CSR and its
+  stats equal the same call made alone on the default stream."""
+  from jax_tpu_embedding.sparsecore.lib.core import pybind_input_preprocessing as pip  # pylint: disable=g-import-not-at-top
+
+  feats = _specs_three_stacks(4096)
+  rng = np.random.default_rng(31)
+  ids = [_ids(rng, feats, multi_hot), _ids(rng, feats, multi_hot)]
+  serial = []
+  for batch in ids:
+    *csr, pending = pip.enqueue_preprocessing(batch, None, feats, 1, 1,
+                                              num_sc_per_device=1)
+    serial.append((csr, pip.collect_stats(pending)))
+  torch.cuda.synchronize()
+  streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+  for s in streams:
+    s.wait_stream(torch.cuda.current_stream())
+  enqueued = []
+  for s, batch in zip(streams, ids):
+    with torch.cuda.stream(s):
+      enqueued.append(pip.enqueue_preprocessing(batch, None, feats, 1, 1,
+                                                num_sc_per_device=1))
+  sides = [_native.side_streams(_native.NUM_SIDE_STREAMS)]
+  with torch.cuda.stream(streams[0]):
+    sides.append(_native.side_streams(_native.NUM_SIDE_STREAMS))
+  with torch.cuda.stream(streams[1]):
+    sides.append(_native.side_streams(_native.NUM_SIDE_STREAMS))
+  handles = [{x.cuda_stream for x in p} for p in sides]
+  assert not handles[1] & handles[2] and not handles[0] & handles[1]
+  got = []
+  for s, (*csr, pending) in zip(streams, enqueued):
+    with torch.cuda.stream(s):
+      got.append((csr, pip.collect_stats(pending)))
+  torch.cuda.synchronize()
+  for (csr_g, st_g), (csr_e, st_e) in zip(got, serial):
+    rp_g, rp_e = csr_g[0], csr_e[0]
+    for name in rp_e:
+      a, b = rp_g[name].cpu().numpy(), rp_e[name].cpu().numpy()
+      np.testing.assert_array_equal(a, b, err_msg=name)
+      end = int(b.max())
+      for x, y in zip(csr_g[1:], csr_e[1:]):
+        np.testing.assert_array_equal(x[name].cpu().numpy()[:end],
+                                      y[name].cpu().numpy()[:end],
+                                      err_msg=name)
+      np.testing.assert_array_equal(st_g.max_ids_per_partition[name],
+                                    st_e.max_ids_per_partition[name])
+      np.testing.assert_array_equal(st_g.required_buffer_sizes[name],
+                                    st_e.required_buffer_sizes[name])
