@@ -193,6 +193,23 @@ int scemb_sparse_dense_matmul(const scemb_csr_t* csr,
                               int64_t device_batch_size, void* workspace,
                               size_t workspace_bytes, uint32_t* device_status,
                               void* stream);
+/* No counterpart in the reference. The same lookup for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc): no workspace argument and no allocation; its
+ * scratch is a library-owned device array of SCEMB_NO_ALLOC_SCRATCH_BYTES
+ * per GPU, held until the process ends. A lookup whose workspace
+ * (scemb_sparse_dense_matmul_workspace_size) exceeds that returns
+ * SCEMB_ERR_INVALID_ARGUMENT. Every call on a GPU uses that GPU's one
+ * array: calls that overlap on one GPU (different streams or host threads)
+ * race and must be serialised by the caller. Results equal those of
+ * scemb_sparse_dense_matmul bit for bit. */
+#define SCEMB_NO_ALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int scemb_sparse_dense_matmul_no_alloc(const scemb_csr_t* csr,
+                                       const scemb_sample_view_t* view,
+                                       const float* table, int64_t table_rows,
+                                       int32_t dim, float* activations,
+                                       int64_t device_batch_size,
+                                       uint32_t* device_status, void* stream);
 /* The same, writing each activation row into its feature's block (the
  * unstacked per-feature outputs); workspace as for the call above. */
 int scemb_sparse_dense_matmul_to_blocks(

@@ -428,9 +428,83 @@ scemb_optimizer_t LrOptimizer(int32_t kind, float* accumulator,
 }  // namespace
 }  // namespace scemb
 
+// ---------------------------------------------------------------------------
+// The allocation-free forward (scemb_sparse_dense_matmul_no_alloc): the same
+// call as scemb_sparse_dense_matmul, with its workspace in a file-scope
+// device array instead of caller memory. Each GPU holds its own copy of the
+// array, at its own address, for the life of the process; every call on a
+// GPU uses that GPU's copy, so calls that overlap on one GPU race. Nothing
+// in it must start at zero: every kernel writes what it later reads.
+// ---------------------------------------------------------------------------
+
+#include <mutex>
+#include <vector>
+
+namespace scemb {
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = SCEMB_NO_ALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;  // per device, from hipGetSymbolAddress
+
+// The device address of the current device's scratch array, looked up once
+// per device with that device current. In host code `scratch` names a
+// host-side stand-in, never the device memory.
+int ScratchAddress(void** out) {
+  int dev = 0;
+  SCEMB_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (dev >= static_cast<int>(g_scratch_ptr.size())) {
+    g_scratch_ptr.resize(dev + 1, nullptr);
+  }
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    SCEMB_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (p == nullptr) {
+      return Fail(SCEMB_ERR_DEVICE, "no device address for the scratch array");
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+}  // namespace scemb
+
 using namespace scemb;
 
 extern "C" {
+
+int scemb_sparse_dense_matmul_no_alloc(const scemb_csr_t* csr,
+                                       const scemb_sample_view_t* view,
+                                       const float* table, int64_t table_rows,
+                                       int32_t dim, float* activations,
+                                       int64_t device_batch_size,
+                                       uint32_t* device_status,
+                                       void* stream) {
+  // The sizing pass of the workspace entry point: host arithmetic only.
+  Arena sizing(nullptr, 0);
+  int rc = ForwardImpl(csr, view, nullptr, table_rows, dim, nullptr, nullptr,
+                       false, device_batch_size, sizing, nullptr, nullptr);
+  if (rc != 0) return rc;
+  const size_t need = sizing.used();
+  if (need > kNoAllocScratchBytes) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "this lookup needs " + std::to_string(need) +
+                    " bytes of scratch; the allocation-free entry point has " +
+                    std::to_string(kNoAllocScratchBytes) +
+                    " (use scemb_sparse_dense_matmul with a workspace)");
+  }
+  void* ws = nullptr;
+  rc = ScratchAddress(&ws);
+  if (rc != 0) return rc;
+  return ForwardEntry(csr, view, table, table_rows, dim, activations, nullptr,
+                      0, false, device_batch_size, ws, kNoAllocScratchBytes,
+                      device_status, stream);
+}
 
 size_t scemb_sparse_dense_matmul_workspace_size(
     const scemb_csr_t* csr, const scemb_sample_view_t* view,

@@ -51,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "scemb_version",
     "scemb_sparse_dense_matmul_workspace_size",
     "scemb_sparse_dense_matmul",
+    "scemb_sparse_dense_matmul_no_alloc",
     "scemb_sparse_dense_matmul_to_blocks",
     "scemb_build_sample_view_workspace_size",
     "scemb_build_sample_view",
@@ -214,6 +215,9 @@ def load_library() -> ctypes.CDLL:
     lib.scemb_sparse_dense_matmul.restype = ctypes.c_int
     lib.scemb_sparse_dense_matmul.argtypes = [csr_p, view_p, vp, i64, i32, vp,
                                               i64, vp, sz, vp, vp]
+    lib.scemb_sparse_dense_matmul_no_alloc.restype = ctypes.c_int
+    lib.scemb_sparse_dense_matmul_no_alloc.argtypes = [
+        csr_p, view_p, vp, i64, i32, vp, i64, vp, vp]
     blk_p = ctypes.POINTER(RowBlock)
     lib.scemb_sparse_dense_matmul_to_blocks.restype = ctypes.c_int
     lib.scemb_sparse_dense_matmul_to_blocks.argtypes = [
