@@ -384,7 +384,8 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
       kw = dict(max_ids_per_partition=spec.max_ids_per_partition,
                 max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
                 num_sc_per_device=1,
-                csr_sorted_by_row=not csr_only and pre.csr_sorted_by_row,
+                csr_sorted_by_row=None if csr_only else
+                pre.csr_sorted_by_row,
                 csr_num_entries=None if csr_only else
                 pre.csr_num_entries[name])
       if a is not None:

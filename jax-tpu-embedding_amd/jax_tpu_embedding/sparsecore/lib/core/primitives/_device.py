@@ -17,13 +17,18 @@ def resolve_sparsecores(num_sc_per_device, global_device_count):
 
 
 def csr_operands(row_pointers, embedding_ids, sample_ids, gains,
-                 num_sc_per_device, num_partitions, sorted_by_row=False,
+                 num_sc_per_device, num_partitions, sorted_by_row=None,
                  num_entries=None, one_entry_per_row=False,
                  num_minibatches=0):
   """Device tensors for the CSR buffers plus the C struct that points at
   them (the tensors must stay alive while the struct is used).
   `sorted_by_row` declares the entries ascending by (partition, embedding
-  id) inside each segment, as the preprocessing writes them; `num_entries`
+  id) inside each segment, as the preprocessing writes them; None (the
+  default) takes that order from the format: the reference's CSR always has
+  it (input_preprocessing_util.cc:167-208 fills each partition from the
+  sorted keys), and a violation is reported through the status word. Pass
+  False for buffers in another order (the backward then sorts a copy);
+  `num_entries`
   the count of valid entries when known (it only picks kernel variants);
   `one_entry_per_row` at most one entry per activation row (one-hot input
   rows), which turns the grouping by activation row into a placement;
@@ -43,6 +48,8 @@ def csr_operands(row_pointers, embedding_ids, sample_ids, gains,
     used = -(-(int(num_entries) + 7 * num_sc_per_device * num_minibatches *
                 num_partitions) // 8) * 8
     used = used if used < 2**31 - 1 else 0
+  if sorted_by_row is None:
+    sorted_by_row = True
   csr = _native.make_csr(rp, eid, sid, g, num_sc_per_device, num_partitions,
                          sorted_by_row=sorted_by_row, num_entries=num_entries,
                          one_entry_per_row=one_entry_per_row,

@@ -16,7 +16,8 @@ returned.
 
 Extra keyword arguments, as for the SGD and Adagrad primitives:
 ``num_sc_per_device`` / ``global_device_count``, ``csr_sorted_by_row`` (the
-CSR is in the preprocessing's order, so it is read in place) and
+CSR is in the reference format's order, so one segment is read in place;
+None, the default, assumes it, False sorts a copy) and
 ``csr_num_entries`` (entry count; picks a kernel variant, changes no
 result). ``activations_grad`` may be a ``_device.RowBlocks`` (the per-feature
 gradients, read in place).
@@ -44,7 +45,7 @@ def apply(kind: int, lhs_row_pointers, lhs_local_embedding_ids,
           max_unique_ids_per_partition: int, computation_name: str,
           sharding_strategy: int = 1, enable_minibatching: bool = False,
           min_value=None, max_value=None, num_sc_per_device=None,
-          global_device_count=None, csr_sorted_by_row: bool = False,
+          global_device_count=None, csr_sorted_by_row=None,
           csr_num_entries=None, flags: int = 0):
   """Checks shared by all primitives (utils.py:79-155), then the update."""
   utils.validate_abstract_eval_params(

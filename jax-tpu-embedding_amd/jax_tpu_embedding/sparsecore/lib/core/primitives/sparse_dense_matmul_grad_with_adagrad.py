@@ -10,10 +10,12 @@ returns ``(table, accumulator)``, updated in place when they are float32 CUDA
 tensors.
 
 Extra keyword arguments besides ``num_sc_per_device`` /
-``global_device_count``: ``csr_sorted_by_row`` declares the CSR as the
-preprocessing writes it (entries ascending by partition and embedding id);
-with one SparseCore segment the kernel then reads it in place instead of
-sorting a copy (a violated order is reported, not silently used).
+``global_device_count``: ``csr_sorted_by_row`` declares the CSR in the
+order the reference's format has (entries ascending by partition and
+embedding id in each segment), with which one SparseCore segment is read in
+place instead of a sorted copy; by default (None) the operands are taken to
+be in that order, as every CSR the preprocessing writes is (a violated order
+is reported through the status word); False makes the call sort a copy.
 ``csr_num_entries``, the CSR's entry count when known, picks the kernel
 variant (one-hot or multi-hot batches) and changes no result.
 ``activations_grad`` may be a ``_device.RowBlocks``: the per-feature
@@ -38,7 +40,7 @@ def _impl(lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
           computation_name: str = "adagrad_optimizer_update",
           sharding_strategy: int = 1, enable_minibatching: bool = False,
           min_value=None, max_value=None, num_sc_per_device=None,
-          global_device_count=None, csr_sorted_by_row: bool = False,
+          global_device_count=None, csr_sorted_by_row=None,
           csr_num_entries=None):
   utils.validate_abstract_eval_params(
       lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,

@@ -105,20 +105,21 @@ class PreprocessedInput:
   fills them and the lookup uses them when present:
     lookup_views: stack name -> _native.LookupView, the CSR entries grouped
       by activation row (spares the forward pass its grouping sort);
-    csr_sorted_by_row: the CSR entries are ascending by (partition, embedding
-      id) in every segment, as the preprocessing writes them (with
-      minibatching: every row's entries contiguous); lets the backward pass
-      read the CSR in place;
+    csr_sorted_by_row: whether the CSR entries are ascending by (partition,
+      embedding id) in every segment (with minibatching: every row's
+      entries contiguous), which lets the backward pass read the CSR in
+      place; None (the default) takes that order from the reference's
+      format, which always has it;
     csr_num_entries: stack name -> number of CSR entries (lets the lookup
       pick the kernel variant for one-hot or multi-hot batches).
-  A PreprocessedInput built from other CSR buffers leaves both unset.
+  A PreprocessedInput built from other CSR buffers leaves them unset.
   """
 
   sparse_dense_matmul_input: SparseDenseMatmulInput
   num_minibatches: object = dataclasses.field(
       default_factory=lambda: np.array(1))
   lookup_views: dict | None = None
-  csr_sorted_by_row: bool = False
+  csr_sorted_by_row: bool | None = None
   csr_num_entries: dict | None = None
 
   @property
@@ -354,7 +355,8 @@ def preprocess_sparse_dense_matmul_input(
     minibatches = minibatches.reshape(local_device_count, 1)
   return (PreprocessedInput(SparseDenseMatmulInput(*csr), minibatches,
                             lookup_views=views,
-                            csr_sorted_by_row=local_device_count == 1,
+                            csr_sorted_by_row=(None if local_device_count == 1
+                                               else False),
                             csr_num_entries=counts),
           SparseDenseMatmulInputStats.from_cc(stats))
 
@@ -751,8 +753,8 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
         computation_name=symbol, sharding_strategy=strategy,
         enable_minibatching=enable_minibatching,
         num_sc_per_device=num_sc_per_device, global_device_count=g_count,
-        csr_sorted_by_row=bool(
-            getattr(preprocessed_inputs, "csr_sorted_by_row", False)),
+        csr_sorted_by_row=getattr(preprocessed_inputs, "csr_sorted_by_row",
+                                  None),
         csr_num_entries=(getattr(preprocessed_inputs, "csr_num_entries",
                                  None) or {}).get(name),
         **kwargs)

@@ -212,16 +212,17 @@ def test_optimizer_routes_and_hyperparameter_sources_agree(name):
     out = _bind(name, ref, sname, t, s, g, 1, **kw)
     return [x.cpu().numpy() for x in out]
 
-  base = run()
+  base = run(csr_sorted_by_row=False)  # a sorted copy of the entries
   variants = {
       "sorted_by_row": run(csr_sorted_by_row=True),
+      "format_order": run(),  # the default reads the CSR in place too
       "device_hyper": run(hyper=[
           torch.tensor(float(h), dtype=torch.float32, device="cuda")
           for h in HYPER[name]]),
       "blocks": run(grad=_device.RowBlocks(
           grad.shape[0], shape[1],
           [(0, grad[:300], shape[1]), (300, grad[300:], shape[1])])),
-      "again": run(),
+      "again": run(csr_sorted_by_row=False),
   }
   for what, got in variants.items():
     for g, b in zip(got, base):
