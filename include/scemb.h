@@ -302,6 +302,9 @@ int scemb_sparse_dense_matmul_grad_with_adagrad_from_blocks(
  *   F2A              slots (accumulator, local_step);
  *                    (learning_rate, rho, l1, l2, max_lr_multiplier,
  *                     global_step)
+ *   CUSTOM           slots and hyperparameters as `program` declares them
+ *                    (primitives/sparse_dense_matmul_optimizer_grad.py:
+ *                    147-260, CustomOptimizerSpec)
  * Hyperparameter i is read from the device scalar hyperparameter_ptrs[i]
  * when that is not NULL, else hyperparameters[i] is used. The update of each
  * touched row applies the reference's row-wise function in its operation
@@ -315,10 +318,51 @@ int scemb_sparse_dense_matmul_grad_with_adagrad_from_blocks(
 #define SCEMB_OPTIMIZER_FTRL 4
 #define SCEMB_OPTIMIZER_LAPROP 5
 #define SCEMB_OPTIMIZER_F2A 6
+#define SCEMB_OPTIMIZER_CUSTOM 7 /* `program` below; slots 0-2 */
 #define SCEMB_MAX_HYPERPARAMETERS 8
 /* FTRL's multiply_linear_by_learning_rate (a static attribute of the
  * reference primitive, sparse_dense_matmul_grad_with_ftrl.py). */
 #define SCEMB_OPTIMIZER_FLAG_MULTIPLY_LINEAR_BY_LR 1u
+
+/* A custom optimizer's row-wise update: CustomOptimizerSpec's function of
+ * (gradient, table, *slots, *hyperparameters) returning (table, *slots)
+ * (lib/nn/custom_optimizer_lowering.py, lowered to StableHLO by the
+ * reference and run by the SparseCore compiler per embedding row), here as
+ * a straight-line program applied to every value of each touched row.
+ * Registers hold floats; before the first instruction register 0 holds the
+ * row's summed gradient, register 1 the table value, registers 2..
+ * 1 + num_slots the slot values and the next num_hyperparameters registers
+ * the hyperparameters. Instruction i sets register dst[i] to
+ * op[i](a[i], b[i], c[i]) (CONST: the value imm[i]; comparisons give 1 or
+ * 0, SELECT(a, b, c) is b where a != 0 else c, CLAMP(a, b, c) is
+ * min(max(b, a), c)). Afterwards register out[0] is the new table value
+ * (the optimizer's clipping then applies) and out[1 + k] the new value of
+ * slot k. Arithmetic is float32 with correctly rounded division and square
+ * root; EXP, LOG, POW, TANH, LOG1P and EXPM1 are the device library's. */
+#define SCEMB_PROGRAM_MAX_OPS 48
+#define SCEMB_PROGRAM_MAX_REGISTERS 24
+enum {
+  SCEMB_OP_CONST = 0, SCEMB_OP_ADD, SCEMB_OP_SUB, SCEMB_OP_MUL, SCEMB_OP_DIV,
+  SCEMB_OP_NEG, SCEMB_OP_SQRT, SCEMB_OP_RSQRT, SCEMB_OP_ABS, SCEMB_OP_EXP,
+  SCEMB_OP_LOG, SCEMB_OP_POW, SCEMB_OP_MAX, SCEMB_OP_MIN, SCEMB_OP_SIGN,
+  SCEMB_OP_TANH, SCEMB_OP_LOG1P, SCEMB_OP_EXPM1, SCEMB_OP_FLOOR,
+  SCEMB_OP_CEIL, SCEMB_OP_SELECT, SCEMB_OP_CMP_EQ, SCEMB_OP_CMP_NE,
+  SCEMB_OP_CMP_LT, SCEMB_OP_CMP_LE, SCEMB_OP_CMP_GT, SCEMB_OP_CMP_GE,
+  SCEMB_OP_CLAMP, SCEMB_OP_AND, SCEMB_OP_OR, SCEMB_OP_NOT, SCEMB_OP_COUNT
+};
+typedef struct scemb_update_program {
+  int32_t num_ops;
+  int32_t num_slots;           /* slot variables (0..2) */
+  int32_t num_hyperparameters; /* 0..SCEMB_MAX_HYPERPARAMETERS */
+  uint8_t op[SCEMB_PROGRAM_MAX_OPS];
+  uint8_t dst[SCEMB_PROGRAM_MAX_OPS];
+  uint8_t a[SCEMB_PROGRAM_MAX_OPS];
+  uint8_t b[SCEMB_PROGRAM_MAX_OPS];
+  uint8_t c[SCEMB_PROGRAM_MAX_OPS];
+  float imm[SCEMB_PROGRAM_MAX_OPS];
+  uint8_t out[3];
+  uint8_t reserved;
+} scemb_update_program_t;
 
 typedef struct scemb_optimizer {
   int32_t kind;   /* SCEMB_OPTIMIZER_* */
@@ -329,6 +373,8 @@ typedef struct scemb_optimizer {
   int32_t clip_mask; /* bit 0: min_value, bit 1: max_value */
   float min_value;
   float max_value;
+  /* SCEMB_OPTIMIZER_CUSTOM: the update (copied at the call, not kept) */
+  const scemb_update_program_t* program;
 } scemb_optimizer_t;
 
 int scemb_sparse_dense_matmul_grad_with_optimizer(

@@ -315,15 +315,76 @@ int ForwardEntry(const scemb_csr_t* csr, const scemb_sample_view_t* view,
 }
 
 // Slot variables each optimizer kind updates.
-int SlotsOf(int32_t kind) {
-  switch (kind) {
+int SlotsOf(const scemb_optimizer_t& o) {
+  switch (o.kind) {
     case SCEMB_OPTIMIZER_SGD:
       return 0;
     case SCEMB_OPTIMIZER_ADAGRAD:
       return 1;
+    case SCEMB_OPTIMIZER_CUSTOM:
+      return o.program != nullptr ? o.program->num_slots : 0;
     default:
       return 2;
   }
+}
+
+// A custom update program that the interpreter can run: counts and register
+// indices in range, every register read before it is written holds an
+// input, the outputs are set.
+int CheckProgram(const scemb_update_program_t* p) {
+  if (p == nullptr) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "custom optimizer without program");
+  }
+  if (p->num_ops < 0 || p->num_ops > SCEMB_PROGRAM_MAX_OPS ||
+      p->num_slots < 0 || p->num_slots > 2 || p->num_hyperparameters < 0 ||
+      p->num_hyperparameters > kMaxHyper) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "custom optimizer program: at most " +
+                    std::to_string(SCEMB_PROGRAM_MAX_OPS) +
+                    " operations, 2 slot variables and " +
+                    std::to_string(kMaxHyper) + " hyperparameters");
+  }
+  const int inputs = 2 + p->num_slots + p->num_hyperparameters;
+  if (inputs > SCEMB_PROGRAM_MAX_REGISTERS) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "too many program inputs");
+  }
+  bool set[SCEMB_PROGRAM_MAX_REGISTERS] = {};
+  for (int r = 0; r < inputs; ++r) set[r] = true;
+  for (int i = 0; i < p->num_ops; ++i) {
+    const int op = p->op[i];
+    if (op >= SCEMB_OP_COUNT || p->dst[i] >= SCEMB_PROGRAM_MAX_REGISTERS ||
+        p->a[i] >= SCEMB_PROGRAM_MAX_REGISTERS ||
+        p->b[i] >= SCEMB_PROGRAM_MAX_REGISTERS ||
+        p->c[i] >= SCEMB_PROGRAM_MAX_REGISTERS) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "custom optimizer program: bad opcode or register");
+    }
+    const bool unary = op == SCEMB_OP_NEG || op == SCEMB_OP_SQRT ||
+                       op == SCEMB_OP_RSQRT || op == SCEMB_OP_ABS ||
+                       op == SCEMB_OP_EXP || op == SCEMB_OP_LOG ||
+                       op == SCEMB_OP_SIGN || op == SCEMB_OP_TANH ||
+                       op == SCEMB_OP_LOG1P || op == SCEMB_OP_EXPM1 ||
+                       op == SCEMB_OP_FLOOR || op == SCEMB_OP_CEIL ||
+                       op == SCEMB_OP_NOT;
+    const bool ternary = op == SCEMB_OP_SELECT || op == SCEMB_OP_CLAMP;
+    const int reads = op == SCEMB_OP_CONST ? 0 : unary ? 1 : ternary ? 3 : 2;
+    const uint8_t src[3] = {p->a[i], p->b[i], p->c[i]};
+    for (int k = 0; k < reads; ++k) {
+      if (!set[src[k]]) {
+        return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                    "custom optimizer program reads a register before "
+                    "setting it");
+      }
+    }
+    set[p->dst[i]] = true;
+  }
+  for (int k = 0; k <= p->num_slots; ++k) {
+    if (p->out[k] >= SCEMB_PROGRAM_MAX_REGISTERS || !set[p->out[k]]) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "custom optimizer program: bad output register");
+    }
+  }
+  return 0;
 }
 
 int GradEntry(const scemb_csr_t* csr, const float* activations_grad,
@@ -333,14 +394,18 @@ int GradEntry(const scemb_csr_t* csr, const float* activations_grad,
               size_t workspace_bytes, uint32_t* device_status, void* stream) {
   if (workspace == nullptr) return Fail(SCEMB_ERR_WORKSPACE, "no workspace");
   if (opt == nullptr || opt->kind < SCEMB_OPTIMIZER_SGD ||
-      opt->kind > SCEMB_OPTIMIZER_F2A) {
+      opt->kind > SCEMB_OPTIMIZER_CUSTOM) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT, "unknown optimizer");
+  }
+  if (opt->kind == SCEMB_OPTIMIZER_CUSTOM) {
+    const int rc = CheckProgram(opt->program);
+    if (rc != 0) return rc;
   }
   if ((opt->flags & ~SCEMB_OPTIMIZER_FLAG_MULTIPLY_LINEAR_BY_LR) != 0 ||
       (opt->flags != 0 && opt->kind != SCEMB_OPTIMIZER_FTRL)) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT, "unknown optimizer flags");
   }
-  const int nslots = SlotsOf(opt->kind);
+  const int nslots = SlotsOf(*opt);
   if (table == nullptr || (nslots >= 1 && opt->slots[0] == nullptr) ||
       (nslots >= 2 && opt->slots[1] == nullptr) ||
       (!mapped && activations_grad == nullptr)) {
@@ -377,6 +442,7 @@ int GradEntry(const scemb_csr_t* csr, const float* activations_grad,
   c.opt.min_value = opt->min_value;
   c.opt.max_value = opt->max_value;
   c.opt.flags = opt->flags;
+  if (opt->kind == SCEMB_OPTIMIZER_CUSTOM) c.opt.prog = *opt->program;
   c.ws = &ws;
   c.status = device_status;
   c.stream = static_cast<hipStream_t>(stream);
@@ -400,6 +466,9 @@ int GradEntry(const scemb_csr_t* csr, const float* activations_grad,
       break;
     case SCEMB_OPTIMIZER_LAPROP:
       rc = GradWithLaprop(c);
+      break;
+    case SCEMB_OPTIMIZER_CUSTOM:
+      rc = GradWithCustom(c);
       break;
     default:
       rc = GradWithF2a(c);

@@ -47,6 +47,7 @@ enum {
   kEpiFtrl = 5,
   kEpiLaprop = 6,
   kEpiF2a = 7,
+  kEpiCustom = 8,  // a CustomOptimizerSpec update, run as a program
 };
 
 constexpr int kMaxHyper = SCEMB_MAX_HYPERPARAMETERS;
@@ -61,6 +62,7 @@ struct OptParams {
   float min_value;
   float max_value;
   uint32_t flags;     // SCEMB_OPTIMIZER_FLAG_*
+  scemb_update_program_t prog;  // kEpiCustom only
 };
 
 constexpr int kMaxRowBlocks = SCEMB_MAX_ROW_BLOCKS;
@@ -106,6 +108,7 @@ int GradWithAdagradMomentum(const GradCall& c);
 int GradWithFtrl(const GradCall& c);
 int GradWithLaprop(const GradCall& c);
 int GradWithF2a(const GradCall& c);
+int GradWithCustom(const GradCall& c);
 
 namespace {
 
@@ -404,6 +407,8 @@ __device__ __forceinline__ uint32_t FetchEntry(const StreamArgs& s, int64_t e,
 // Slot variables and hyperparameters per optimizer, in the order of the
 // reference's *SlotVariables and get_hyperparameters()
 // (lib/nn/embedding_spec.py:377-916).
+// (A custom update has up to 2 slots and kMaxHyper hyperparameters; how
+// many it uses is in its program: HasSlot.)
 template <int EPI>
 __host__ __device__ constexpr int NumSlots() {
   return EPI == kEpiFwd || EPI == kEpiSgd ? 0 : EPI == kEpiAdagrad ? 1 : 2;
@@ -414,7 +419,13 @@ __host__ __device__ constexpr int NumHyper() {
          : EPI == kEpiSgd || EPI == kEpiAdagrad         ? 1
          : EPI == kEpiAdam || EPI == kEpiLaprop         ? 4
          : EPI == kEpiFtrl                              ? 5
+         : EPI == kEpiCustom                            ? kMaxHyper
                                                         : 6;
+}
+// Whether slot k is read and written.
+template <int EPI>
+__device__ __forceinline__ bool HasSlot(const OptParams& o, int k) {
+  return NumSlots<EPI>() > k && (EPI != kEpiCustom || o.prog.num_slots > k);
 }
 
 // The hyperparameters as the update reads them, plus what is constant for
@@ -482,6 +493,85 @@ __device__ __forceinline__ Hyper LoadHyper(const OptParams& o) {
     H.derived = powf(1.0f - powf(H.h[1], 2.0f), 0.5f);  // sqrt(1 - b1^2)
   }
   return H;
+}
+
+// Transcendentals of a custom update program, evaluated in double and
+// rounded once: correctly rounded but for the rarest double-rounding ties,
+// so the result matches a correctly rounded float library (glibc's powf,
+// numpy's float32 power) rather than differing in the last bit. Kept out of
+// line: inlined for every vector element, the double-precision code would
+// double the interpreter's registers.
+__device__ __noinline__ float ProgTranscendental(int op, float x, float y) {
+  const double a = static_cast<double>(x);
+  switch (op) {
+    case SCEMB_OP_EXP: return static_cast<float>(exp(a));
+    case SCEMB_OP_LOG: return static_cast<float>(log(a));
+    case SCEMB_OP_POW: return static_cast<float>(pow(a, static_cast<double>(y)));
+    case SCEMB_OP_TANH: return static_cast<float>(tanh(a));
+    case SCEMB_OP_LOG1P: return static_cast<float>(log1p(a));
+    default: return static_cast<float>(expm1(a));  // SCEMB_OP_EXPM1
+  }
+}
+
+// A custom update (scemb_update_program_t): registers 0, 1 hold the summed
+// gradient and the table value, then the slot values, then the
+// hyperparameters; each instruction sets one register. The program is the
+// same for every thread (kernel arguments), so every branch is uniform.
+__device__ __forceinline__ float ProgOp(int op, float x, float y, float z,
+                                        float imm) {
+  switch (op) {
+    case SCEMB_OP_CONST: return imm;
+    case SCEMB_OP_ADD: return x + y;
+    case SCEMB_OP_SUB: return x - y;
+    case SCEMB_OP_MUL: return x * y;
+    case SCEMB_OP_DIV: return x / y;
+    case SCEMB_OP_NEG: return -x;
+    case SCEMB_OP_SQRT: return sqrtf(x);
+    case SCEMB_OP_RSQRT: return 1.0f / sqrtf(x);
+    case SCEMB_OP_ABS: return fabsf(x);
+    case SCEMB_OP_EXP:
+    case SCEMB_OP_LOG:
+    case SCEMB_OP_POW:
+    case SCEMB_OP_TANH:
+    case SCEMB_OP_LOG1P:
+    case SCEMB_OP_EXPM1:
+      return ProgTranscendental(op, x, y);
+    // maximum / minimum propagate NaN, as StableHLO's do.
+    case SCEMB_OP_MAX: return (x != x || y != y) ? x + y : fmaxf(x, y);
+    case SCEMB_OP_MIN: return (x != x || y != y) ? x + y : fminf(x, y);
+    case SCEMB_OP_SIGN: return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : x);
+    case SCEMB_OP_FLOOR: return floorf(x);
+    case SCEMB_OP_CEIL: return ceilf(x);
+    case SCEMB_OP_SELECT: return x != 0.0f ? y : z;
+    case SCEMB_OP_CMP_EQ: return x == y ? 1.0f : 0.0f;
+    case SCEMB_OP_CMP_NE: return x != y ? 1.0f : 0.0f;
+    case SCEMB_OP_CMP_LT: return x < y ? 1.0f : 0.0f;
+    case SCEMB_OP_CMP_LE: return x <= y ? 1.0f : 0.0f;
+    case SCEMB_OP_CMP_GT: return x > y ? 1.0f : 0.0f;
+    case SCEMB_OP_CMP_GE: return x >= y ? 1.0f : 0.0f;
+    case SCEMB_OP_CLAMP: return fminf(fmaxf(y, x), z);
+    case SCEMB_OP_AND: return (x != 0.0f && y != 0.0f) ? 1.0f : 0.0f;
+    case SCEMB_OP_OR: return (x != 0.0f || y != 0.0f) ? 1.0f : 0.0f;
+    default: return x == 0.0f ? 1.0f : 0.0f;  // SCEMB_OP_NOT
+  }
+}
+
+__device__ __forceinline__ void RunProgram(const scemb_update_program_t& p,
+                                           float g, float& t, float& s0,
+                                           float& s1, const float* h) {
+  float R[SCEMB_PROGRAM_MAX_REGISTERS];
+  R[0] = g;
+  R[1] = t;
+  const int ns = p.num_slots;
+  if (ns >= 1) R[2] = s0;
+  if (ns >= 2) R[3] = s1;
+  for (int i = 0; i < p.num_hyperparameters; ++i) R[2 + ns + i] = h[i];
+  for (int i = 0; i < p.num_ops; ++i) {
+    R[p.dst[i]] = ProgOp(p.op[i], R[p.a[i]], R[p.b[i]], R[p.c[i]], p.imm[i]);
+  }
+  t = R[p.out[0]];
+  if (ns >= 1) s0 = R[p.out[1]];
+  if (ns >= 2) s1 = R[p.out[2]];
 }
 
 // Update of one table value t with its summed gradient g and slot values
@@ -555,6 +645,9 @@ __device__ __forceinline__ float UpdateOne(float t, float& s0, float& s1,
     s0 = u;
     s1 = nu;
     v = t - H.h[0] * u;
+  } else if (EPI == kEpiCustom) {
+    v = t;
+    RunProgram(o.prog, g, v, s0, s1, H.h);
   } else {
     // F2A: (lr, rho, l1, l2, max_lr_multiplier, global_step); slots
     // (accumulator, local_step). sign() keeps zeros (and NaN) as they are.
@@ -644,8 +737,8 @@ __device__ __forceinline__ void Epilogue(const RowArgs& r,
     V::Set(b, k, bk);
   }
   StoreRow<VEC, kNtTable>(r.dst + off, t);
-  if (NumSlots<EPI>() >= 1) StoreRow<VEC, kNtTable>(r.slot0 + off, a);
-  if (NumSlots<EPI>() >= 2) StoreRow<VEC, kNtTable>(r.slot1 + off, b);
+  if (HasSlot<EPI>(r.opt, 0)) StoreRow<VEC, kNtTable>(r.slot0 + off, a);
+  if (HasSlot<EPI>(r.opt, 1)) StoreRow<VEC, kNtTable>(r.slot1 + off, b);
 }
 
 template <int VEC, int EPI, bool kMapped>
@@ -658,8 +751,8 @@ __device__ __forceinline__ void EpilogueLoad(const RowArgs& r,
   typename V::T t = V::Zero(), a = V::Zero(), b = V::Zero();
   const int64_t off = static_cast<int64_t>(key) * r.dim + col;
   if (EPI != kEpiFwd) t = V::Load(r.dst + off);
-  if (NumSlots<EPI>() >= 1) a = V::Load(r.slot0 + off);
-  if (NumSlots<EPI>() >= 2) b = V::Load(r.slot1 + off);
+  if (HasSlot<EPI>(r.opt, 0)) a = V::Load(r.slot0 + off);
+  if (HasSlot<EPI>(r.opt, 1)) b = V::Load(r.slot1 + off);
   Epilogue<VEC, EPI, kMapped>(r, m, key, col, g, t, a, b, H);
 }
 
@@ -871,8 +964,8 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
         if (EPI != kEpiFwd && fin[u] && col_ok) {
           const int64_t off = static_cast<int64_t>(kk[u]) * dim + col;
           tv[u] = V::Load(r.dst + off);
-          if (NumSlots<EPI>() >= 1) av[u] = V::Load(r.slot0 + off);
-          if (NumSlots<EPI>() >= 2) bv[u] = V::Load(r.slot1 + off);
+          if (HasSlot<EPI>(r.opt, 0)) av[u] = V::Load(r.slot0 + off);
+          if (HasSlot<EPI>(r.opt, 1)) bv[u] = V::Load(r.slot1 + off);
         }
       }
 #pragma unroll
@@ -1262,8 +1355,8 @@ int GradImpl(const GradCall& c) {
   PickLayout(dim,
              Aligned16(c.table) &&
                  (c.map != nullptr ? c.map_vec4 : Aligned16(c.act_grad)) &&
-                 (NumSlots<EPI>() < 1 || Aligned16(c.slot0)) &&
-                 (NumSlots<EPI>() < 2 || Aligned16(c.slot1)),
+                 (c.slot0 == nullptr || Aligned16(c.slot0)) &&
+                 (c.slot1 == nullptr || Aligned16(c.slot1)),
              &g, &vec);
   const bool mapped = c.map != nullptr;
   if (direct) {

@@ -42,7 +42,9 @@ OPTIMIZER_ADAGRAD_MOMENTUM = 3
 OPTIMIZER_FTRL = 4
 OPTIMIZER_LAPROP = 5
 OPTIMIZER_F2A = 6
+OPTIMIZER_CUSTOM = 7
 MAX_HYPERPARAMETERS = 8
+PROGRAM_MAX_OPS = 48
 OPTIMIZER_FLAG_MULTIPLY_LINEAR_BY_LR = 1
 
 # Every function declared in include/scemb.h.
@@ -124,6 +126,37 @@ MAX_ROW_BLOCKS = 32
 MAX_MINIBATCHES = 64
 
 
+class UpdateProgram(ctypes.Structure):
+  _fields_ = [
+      ("num_ops", ctypes.c_int32),
+      ("num_slots", ctypes.c_int32),
+      ("num_hyperparameters", ctypes.c_int32),
+      ("op", ctypes.c_uint8 * PROGRAM_MAX_OPS),
+      ("dst", ctypes.c_uint8 * PROGRAM_MAX_OPS),
+      ("a", ctypes.c_uint8 * PROGRAM_MAX_OPS),
+      ("b", ctypes.c_uint8 * PROGRAM_MAX_OPS),
+      ("c", ctypes.c_uint8 * PROGRAM_MAX_OPS),
+      ("imm", ctypes.c_float * PROGRAM_MAX_OPS),
+      ("out", ctypes.c_uint8 * 3),
+      ("reserved", ctypes.c_uint8),
+  ]
+
+
+def update_program(fields: dict) -> UpdateProgram:
+  """scemb_update_program_t from UpdateProgram.compile()'s fields."""
+  p = UpdateProgram()
+  p.num_ops = len(fields["op"])
+  p.num_slots = fields["num_slots"]
+  p.num_hyperparameters = fields["num_hyperparameters"]
+  for k in ("op", "dst", "a", "b", "c", "imm"):
+    arr = getattr(p, k)
+    for i, v in enumerate(fields[k]):
+      arr[i] = v
+  for i, v in enumerate(fields["out"]):
+    p.out[i] = v
+  return p
+
+
 class Optimizer(ctypes.Structure):
   _fields_ = [
       ("kind", ctypes.c_int32),
@@ -134,6 +167,7 @@ class Optimizer(ctypes.Structure):
       ("clip_mask", ctypes.c_int32),
       ("min_value", ctypes.c_float),
       ("max_value", ctypes.c_float),
+      ("program", ctypes.POINTER(UpdateProgram)),
   ]
 
 
@@ -756,11 +790,12 @@ def _hyper_args(values):
 def sparse_dense_matmul_grad_with_optimizer(
     csr: Csr, activations_grad, table, kind: int, slots, hyperparameters,
     batch: int, min_value=None, max_value=None, flags: int = 0,
-    device_status=None, grad_blocks=None) -> None:
+    device_status=None, grad_blocks=None, program=None) -> None:
   """Backward + the optimizer `kind` (OPTIMIZER_*), updating `table` and the
   slot tensors in place. `hyperparameters` in the order of the reference
   primitive's operands (floats, numpy scalars or 0-d tensors).
-  `grad_blocks`: as for sparse_dense_matmul_grad."""
+  `grad_blocks`: as for sparse_dense_matmul_grad. `program`: the
+  UpdateProgram struct of OPTIMIZER_CUSTOM."""
   lib = load_library()
   if len(hyperparameters) > MAX_HYPERPARAMETERS or len(slots) > 2:
     check(SCEMB_ERR_INVALID_ARGUMENT)
@@ -782,6 +817,8 @@ def sparse_dense_matmul_grad_with_optimizer(
     opt.hyperparameters[i] = v
   opt.clip_mask, opt.min_value, opt.max_value = _clip_args(min_value,
                                                            max_value)
+  if program is not None:
+    opt.program = ctypes.pointer(program)
   if grad_blocks is not None:
     arr, n = row_blocks(grad_blocks)
     rc = lib.scemb_sparse_dense_matmul_grad_with_optimizer_from_blocks(

@@ -46,7 +46,7 @@ def apply(kind: int, lhs_row_pointers, lhs_local_embedding_ids,
           sharding_strategy: int = 1, enable_minibatching: bool = False,
           min_value=None, max_value=None, num_sc_per_device=None,
           global_device_count=None, csr_sorted_by_row=None,
-          csr_num_entries=None, flags: int = 0):
+          csr_num_entries=None, flags: int = 0, program=None):
   """Checks shared by all primitives (utils.py:79-155), then the update."""
   utils.validate_abstract_eval_params(
       lhs_row_pointers, lhs_local_embedding_ids, lhs_local_sample_ids,
@@ -75,7 +75,8 @@ def apply(kind: int, lhs_row_pointers, lhs_local_embedding_ids,
   status = _native.status_word()
   _native.sparse_dense_matmul_grad_with_optimizer(
       csr, grad, table, kind, dev_slots, hyperparameters, batch, min_value,
-      max_value, flags=flags, grad_blocks=blocks, device_status=status)
+      max_value, flags=flags, grad_blocks=blocks, device_status=status,
+      program=program)
   _native.check_status_word(status, computation_name)
   del keep
   return (table, *dev_slots)

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import collections
 import dataclasses
+import functools
 import warnings
 from typing import Mapping, NamedTuple
 
@@ -25,6 +26,7 @@ from jax_tpu_embedding.sparsecore import _tree
 from jax_tpu_embedding.sparsecore.lib.core import pybind_input_preprocessing
 from jax_tpu_embedding.sparsecore.lib.core.primitives import _device
 from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_csr
+from jax_tpu_embedding.sparsecore.lib.nn import custom_optimizer_lowering
 from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec
 from jax_tpu_embedding.sparsecore.lib.nn import table_stacking
 from jax_tpu_embedding.sparsecore.utils import utils
@@ -746,24 +748,64 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
     if embedding_var_limits is not None:
       kwargs["min_value"], kwargs["max_value"] = embedding_var_limits[name]
     flat, treedef = _tree.tree_flatten(ev)
-    res = opt.get_optimizer_primitive().bind(
-        rp[name], eid[name], sid[name], gains[name], nmb, *flat, grads[name],
-        *hyper, max_ids_per_partition=spec.max_ids_per_partition,
-        max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
-        computation_name=symbol, sharding_strategy=strategy,
-        enable_minibatching=enable_minibatching,
+    extra = dict(
         num_sc_per_device=num_sc_per_device, global_device_count=g_count,
         csr_sorted_by_row=getattr(preprocessed_inputs, "csr_sorted_by_row",
                                   None),
         csr_num_entries=(getattr(preprocessed_inputs, "csr_num_entries",
-                                 None) or {}).get(name),
-        **kwargs)
+                                 None) or {}).get(name))
+    if isinstance(opt, embedding_spec.CustomOptimizerSpec):
+      # The update as StableHLO text, clipped to the limits
+      # (embedding.py:1441-1495); operands in the custom primitive's order.
+      limits = (embedding_var_limits or {}).get(name, (None, None))
+      text = _custom_update_text(
+          opt, spec.stack_embedding_dim,
+          len(opt.slot_variables_initializers()), len(hyper), *limits)
+      res = opt.get_optimizer_primitive().bind(
+          rp[name], eid[name], sid[name], gains[name], nmb, grads[name],
+          *hyper, *flat, num_hyperparameters=len(hyper), stablehlo=text,
+          max_ids_per_partition=spec.max_ids_per_partition,
+          max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
+          computation_name=symbol, sharding_strategy=strategy,
+          enable_minibatching=enable_minibatching, **extra)
+    else:
+      res = opt.get_optimizer_primitive().bind(
+          rp[name], eid[name], sid[name], gains[name], nmb, *flat,
+          grads[name], *hyper,
+          max_ids_per_partition=spec.max_ids_per_partition,
+          max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
+          computation_name=symbol, sharding_strategy=strategy,
+          enable_minibatching=enable_minibatching, **extra, **kwargs)
     res = res if isinstance(res, tuple) else (res,)
     # The updated variables in the structure they came in
     # (embedding.py:1524-1527): EmbeddingVariables stay EmbeddingVariables
     # (with their slot type), a plain (table, *slots) tuple stays a tuple.
     out[name] = _tree.tree_unflatten(treedef, list(res))
   return out
+
+
+@functools.lru_cache(maxsize=64)
+def _custom_text(fn, stablehlo, dim, num_slots, num_hyper, lo, hi):
+  if stablehlo is not None:
+    return custom_optimizer_lowering.wrap_stablehlo_with_limits(
+        stablehlo, dim, num_slots, num_hyper, lo, hi)
+  return custom_optimizer_lowering.lower_to_stablehlo(
+      fn, dim, num_slots, num_hyper, lo, hi)
+
+
+def _custom_update_text(opt, dim, num_slots, num_hyper, lo, hi) -> str:
+  """StableHLO text of a CustomOptimizerSpec's update (cached per spec
+  contents)."""
+  if opt.stablehlo is None and opt.custom_computation_fn is None:
+    raise ValueError("Either stablehlo or custom_computation_fn must be "
+                     "provided for CustomOptimizerSpec")
+  stablehlo = opt.stablehlo
+  if isinstance(stablehlo, bytes):
+    stablehlo = stablehlo.decode("utf-8")
+  return _custom_text(opt.custom_computation_fn if stablehlo is None else
+                      None, stablehlo, int(dim), num_slots, num_hyper,
+                      None if lo is None else float(lo),
+                      None if hi is None else float(hi))
 
 
 def init_embedding_variables(rng, table_specs, global_sharding=None,

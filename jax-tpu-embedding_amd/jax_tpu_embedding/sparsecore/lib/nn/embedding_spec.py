@@ -7,7 +7,8 @@ rules (``FeatureIdTransformation`` :918-938, ``TableSettingInStack``
 specs written for the reference work unchanged. The optimizers are those of
 the reference: SGD (:377-412), Adagrad (:415-460), Adam (:463-557),
 AdagradMomentum (:560-649), FTRL (:652-741), LaProp (:744-830) and F2A
-(:833-916), with the same hyperparameters, slot variables and defaults.
+(:833-916), with the same hyperparameters, slot variables and defaults, and
+the custom optimizer (:250-374) given by its update function.
 Learning rates may be numbers, 0-d torch tensors or callables of the step.
 
 Initializers are callables ``init(generator, shape)`` returning a float32
@@ -31,6 +32,7 @@ from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul
 from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_ftrl
 from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_laprop
 from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_sgd
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_optimizer_grad
 
 DEFAULT_ACTIVATION_MEM_BYTES_LIMIT: int = 2048 * 1024
 
@@ -213,6 +215,73 @@ class OptimizerSpec:
       if p in bool_params:
         kwargs[p] = bool(bool_params[p])
     return cls(**kwargs)
+
+
+class CustomOptimizerSpec(OptimizerSpec):
+  """An optimizer given by its row-wise update (embedding_spec.py:250-374).
+
+  `custom_computation_fn(gradient, table, *slots, *hyperparameters)` returns
+  the new table, or (new table, *new slots); the hyperparameters are those of
+  get_hyperparameters() (the learning rate). Alternatively `stablehlo` holds
+  the update as a StableHLO module. Either is run per touched row by the
+  tpu_sparse_dense_matmul_optimizer_grad primitive; see
+  custom_optimizer_lowering for what the function may use.
+  """
+
+  def __init__(self, learning_rate: LearningRate = 0.001,
+               custom_computation_fn: Callable[..., Any] | None = None,
+               stablehlo: str | bytes | Any | None = None,
+               slot_variable_initializers_tuple: tuple[
+                   CallableTableInitializer, ...] = (),
+               short_name_str: str = "custom"):
+    super().__init__(learning_rate=learning_rate)
+    self.custom_computation_fn = custom_computation_fn
+    self.stablehlo = stablehlo
+    self.slot_variable_initializers_tuple = slot_variable_initializers_tuple
+    self.short_name_str = short_name_str
+
+  def slot_variables_initializers(self) -> tuple:
+    return self.slot_variable_initializers_tuple
+
+  def __hash__(self) -> int:
+    return hash((_hashable(self.learning_rate), self.custom_computation_fn,
+                 self.stablehlo, self.slot_variable_initializers_tuple,
+                 self.short_name_str))
+
+  def short_name(self) -> str:
+    return self.short_name_str
+
+  def get_optimizer_primitive(self):
+    return (sparse_dense_matmul_optimizer_grad
+            .tpu_sparse_dense_matmul_optimizer_grad_primitive)
+
+  @classmethod
+  def lower_to_stablehlo(cls, custom_computation_fn, embedding_dim: int = 1,
+                         num_slot_variables: int = 0,
+                         num_hyperparameters: int = 1,
+                         min_value: float | None = None,
+                         max_value: float | None = None) -> str:
+    from jax_tpu_embedding.sparsecore.lib.nn import custom_optimizer_lowering  # pylint: disable=g-import-not-at-top
+
+    return custom_optimizer_lowering.lower_to_stablehlo(
+        custom_computation_fn, embedding_dim=embedding_dim,
+        num_slot_variables=num_slot_variables,
+        num_hyperparameters=num_hyperparameters, min_value=min_value,
+        max_value=max_value)
+
+  @classmethod
+  def wrap_stablehlo_with_limits(cls, stablehlo, embedding_dim: int,
+                                 num_slot_variables: int,
+                                 num_hyperparameters: int,
+                                 min_value: float | None = None,
+                                 max_value: float | None = None) -> str:
+    from jax_tpu_embedding.sparsecore.lib.nn import custom_optimizer_lowering  # pylint: disable=g-import-not-at-top
+
+    return custom_optimizer_lowering.wrap_stablehlo_with_limits(
+        stablehlo, embedding_dim=embedding_dim,
+        num_slot_variables=num_slot_variables,
+        num_hyperparameters=num_hyperparameters, min_value=min_value,
+        max_value=max_value)
 
 
 class SGDOptimizerSpec(OptimizerSpec):

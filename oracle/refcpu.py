@@ -15,6 +15,15 @@ from the same feature specs as the product:
   (``pybind_input_preprocessing.cc:124-188``) and
   ``PreprocessSparseDenseMatmulInput`` (``input_preprocessing.cc:800-959``),
   with minibatching on a single host.
+
+``sparse_dense_matmul_grad_custom`` restates the custom-optimizer update
+(``lib/core/primitives/sparse_dense_matmul_optimizer_grad.py``; the test-side
+expectation of ``tests/sparse_dense_matmul_optimizer_grad_test.py:81-140``):
+per-row gradient sums from the C backward, then the user's function in numpy
+float32 on the touched rows. It is pinned by equality with the oracle's
+built-in SGD and Adagrad (bit for bit) and by the reference's custom-Adagrad
+literal table (``tpu_sparse_dense_matmul_grad_test.py:1324-1486``), in
+``tests/test_custom_optimizer.py``.
 """
 
 from __future__ import annotations
@@ -710,4 +719,66 @@ def sparse_dense_matmul_grad_optimizer(rp, eid, sid, gains, act_grad, table,
       OPTIMIZERS[optimizer], _p(hp), 1 if multiply_linear_by_lr else 0, clip,
       float(min_value if min_value is not None else 0.0),
       float(max_value if max_value is not None else 0.0), _threads(threads))
+  return (table, *slots)
+
+
+def touched_rows(rp, eid, *, num_sc_per_device, num_scs, table_rows,
+                 num_minibatches=0) -> np.ndarray:
+  """Table rows the CSR names (entries of every segment and partition up to
+  its row pointer; padding and ids outside the table left out)."""
+  rp = np.asarray(rp, np.int64).reshape(-1)
+  eid = np.asarray(eid, np.int64).reshape(-1)
+  rows_per_part = table_rows // num_scs
+  per_seg = len(eid) // num_sc_per_device
+  rp_per = _rp_per_segment(rp, num_sc_per_device, num_scs, num_minibatches)
+  out = np.zeros(table_rows, bool)
+  blocks = (num_sc_per_device * (num_minibatches or 1))
+  for blk in range(blocks):
+    seg = blk // (num_minibatches or 1)
+    base = 0 if num_minibatches else seg * per_seg
+    start = 0 if not num_minibatches or blk == 0 else None
+    for p in range(num_scs):
+      end = int(rp[blk * rp_per + p])
+      if start is None:
+        prev = int(rp[blk * rp_per - rp_per + num_scs - 1])
+        start = (prev + 7) // 8 * 8
+      lo, hi = base + start, base + min(end, per_seg if not num_minibatches
+                                        else len(eid))
+      ids = eid[lo:hi]
+      ids = ids[(ids >= 0) & (ids < rows_per_part)]
+      out[p * rows_per_part + ids] = True
+      start = (end + 7) // 8 * 8
+  return out
+
+
+def sparse_dense_matmul_grad_custom(rp, eid, sid, gains, act_grad, table,
+                                    slots, *, update_fn, hyperparameters,
+                                    num_sc_per_device, num_scs,
+                                    min_value=None, max_value=None,
+                                    threads=None):
+  """Backward + a custom update: each touched row's gradient summed by the C
+  oracle (its SGD with learning rate -1 on a zero table returns the sums),
+  then `update_fn(grad, table, *slots, *hyperparameters)` evaluated in numpy
+  float32 on the touched rows, then the clipping of the table. Returns
+  (table, *slots)."""
+  table = np.array(table, np.float32, copy=True)
+  slots = [np.array(x, np.float32, copy=True) for x in slots]
+  sums = sparse_dense_matmul_grad(rp, eid, sid, gains, act_grad,
+                                  np.zeros_like(table), learning_rate=-1.0,
+                                  num_sc_per_device=num_sc_per_device,
+                                  num_scs=num_scs, threads=threads)
+  rows = touched_rows(rp, eid, num_sc_per_device=num_sc_per_device,
+                      num_scs=num_scs, table_rows=table.shape[0])
+  hyper = [np.float32(np.asarray(h, np.float32).reshape(())) for h in
+           hyperparameters]
+  out = update_fn(sums[rows], table[rows], *[s[rows] for s in slots], *hyper)
+  outs = list(out) if isinstance(out, (list, tuple)) else [out]
+  new_table = np.asarray(outs[0], np.float32)
+  if min_value is not None:
+    new_table = np.maximum(new_table, np.float32(min_value))
+  if max_value is not None:
+    new_table = np.minimum(new_table, np.float32(max_value))
+  table[rows] = new_table
+  for s, v in zip(slots, outs[1:]):
+    s[rows] = np.asarray(v, np.float32)
   return (table, *slots)
