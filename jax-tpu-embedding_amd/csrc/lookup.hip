@@ -4,6 +4,7 @@
 // view, SGD and Adagrad here; the optimizers with two slot variables in
 // optimizer_*.hip.
 #include "segreduce.h"
+#include "radix.h"
 
 namespace scemb {
 namespace {
@@ -63,10 +64,135 @@ __global__ void FillU32(uint32_t* p, int64_t n, uint32_t v) {
   if (i < n) p[i] = v;
 }
 
+// --- Grouping a CSR by activation row --------------------------------------
+//
+// A stable LSD radix sort by activation row whose first pass reads the CSR
+// itself (padding and invalid entries dropped, the packed (table row, gain)
+// as payload), so no expanded copy is written first; each row's entries
+// keep their CSR order. Keys span BitWidth(batch - 1) bits (no sentinel
+// value to make room for); the last pass fills the positions past the
+// entries with the unused key.
+
+struct CsrRowSource {
+  Csr csr;
+  int64_t bps;
+  int64_t rows_per_partition;
+  uint32_t* status;
+  __device__ bool Valid(int64_t j, int* p, uint32_t* k) const {
+    int s = 0;
+    *p = LocateEntry(csr, j, &s);
+    if (*p < 0) return false;
+    const int32_t e = csr.eid[j];
+    const int32_t sm = csr.sid[j];
+    if (e < 0 || e >= rows_per_partition || sm < 0 || sm >= bps) {
+      if (status != nullptr) atomicOr(status, SCEMB_STATUS_BAD_ENTRY);
+      return false;
+    }
+    *k = static_cast<uint32_t>(s * bps + sm);
+    return true;
+  }
+  __device__ bool LoadKey(int64_t j, uint32_t* k) const {
+    int p;
+    return Valid(j, &p, k);
+  }
+  __device__ bool Load(int64_t j, uint32_t* k, uint64_t* v) const {
+    int p;
+    if (!Valid(j, &p, k)) return false;
+    *v = Pack(static_cast<uint32_t>(p * rows_per_partition + csr.eid[j]),
+              csr.gains[j]);
+    return true;
+  }
+};
+
+// The stream arrays; positions past the entries get the unused key.
+struct StreamSink {
+  uint32_t* keys;
+  uint64_t* entries;
+  uint32_t sentinel;
+  __device__ void Store(uint32_t pos, uint32_t k, uint64_t v) const {
+    keys[pos] = k;
+    entries[pos] = v;
+  }
+  __device__ void Fill(int64_t pos) const {
+    keys[pos] = sentinel;
+    entries[pos] = 0;
+  }
+};
+
+int GroupByRow(const scemb_csr_t* csr, const Geometry& geo, int64_t batch,
+               const SortBuffers& b, Arena& ws, uint32_t* status,
+               hipStream_t stream) {
+  using radix::kSortBlock;
+  using radix::kSortTile;
+  using Arr = radix::ArraySource<uint32_t, uint64_t>;
+  const int64_t n = geo.n;
+  const int bits = batch > 1 ? BitWidth(static_cast<uint64_t>(batch - 1)) : 1;
+  const radix::DigitPlan plan = radix::PlanDigits(bits);
+  const int64_t tiles = CeilDiv(n, kSortTile);
+  uint32_t* hist = ws.Take<uint32_t>(tiles * (int64_t{1} << plan.digit));
+  uint32_t* totals = ws.Take<uint32_t>(plan.passes);
+  const bool measuring = ws.measuring();
+  if (!measuring && ws.overflow()) {
+    return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+  }
+  const CsrRowSource csr_src{MakeCsr(csr), geo.bps, geo.rows_per_partition,
+                             status};
+  const uint32_t* taken = totals;  // entries kept by the first pass
+  const uint32_t* in_keys = nullptr;
+  const uint64_t* in_pay = nullptr;
+  for (int pass = 0; pass < plan.passes; ++pass) {
+    const int shift = pass * plan.digit;
+    const int pbits = bits - shift < plan.digit ? bits - shift : plan.digit;
+    const uint32_t mask = (1u << pbits) - 1u;
+    const int64_t cells = tiles * (int64_t{1} << pbits);
+    const bool first = pass == 0;
+    const bool last = pass == plan.passes - 1;
+    // Passes alternate so that the last one writes (b.keys, b.pay).
+    const bool to_final = (plan.passes - 1 - pass) % 2 == 0;
+    const StreamSink sink{to_final ? b.keys : b.keys_alt,
+                          to_final ? b.pay : b.pay_alt,
+                          static_cast<uint32_t>(batch)};
+    const Arr arr{in_keys, in_pay};
+    if (!measuring) {
+      if (first) {
+        hipLaunchKernelGGL((radix::RadixHistogramK<uint32_t, CsrRowSource>),
+                           dim3(tiles), dim3(kSortBlock), 0, stream, csr_src,
+                           n, nullptr, shift, mask, tiles, hist);
+      } else {
+        hipLaunchKernelGGL((radix::RadixHistogramK<uint32_t, Arr>),
+                           dim3(tiles), dim3(kSortBlock), 0, stream, arr, n,
+                           taken, shift, mask, tiles, hist);
+      }
+      SCEMB_LAUNCH_CHECK();
+    }
+    const int st = ExclusiveScan<uint32_t>(hist, hist, cells, totals + pass,
+                                           ws, stream);
+    if (st != 0) return st;
+    if (!measuring) {
+      if (first) {
+        hipLaunchKernelGGL(
+            (radix::RadixScatterK<uint32_t, uint64_t, CsrRowSource,
+                                  StreamSink>),
+            dim3(tiles), dim3(kSortBlock), 0, stream, csr_src, sink, n,
+            nullptr, shift, mask, pbits, tiles, hist, totals + pass, last);
+      } else {
+        hipLaunchKernelGGL(
+            (radix::RadixScatterK<uint32_t, uint64_t, Arr, StreamSink>),
+            dim3(tiles), dim3(kSortBlock), 0, stream, arr, sink, n, taken,
+            shift, mask, pbits, tiles, hist, totals + pass, last);
+      }
+      SCEMB_LAUNCH_CHECK();
+    }
+    in_keys = sink.keys;
+    in_pay = sink.entries;
+  }
+  return 0;
+}
+
 // Sample-major stream of a CSR into (keys, entries). With at most one entry
 // per activation row (SCEMB_CSR_ONE_ENTRY_PER_ROW) the entries are placed by
-// row through a count / scan / compaction; otherwise expand + stable radix
-// sort. The result lands in (b.keys, b.pay) or the alt pair (*in_alt).
+// row through a count / scan / compaction; otherwise GroupByRow sorts them.
+// The result lands in (b.keys, b.pay) (*in_alt is false).
 int BuildSampleStream(const scemb_csr_t* csr, const Geometry& geo,
                       int64_t batch, const SortBuffers& b, Arena& ws,
                       uint32_t* status, hipStream_t stream, bool* in_alt) {
@@ -100,16 +226,9 @@ int BuildSampleStream(const scemb_csr_t* csr, const Geometry& geo,
     }
     return 0;
   }
-  if (!ws.measuring() && n > 0) {
-    hipLaunchKernelGGL(ExpandCsr<true>, dim3(CeilDiv(n, 256)), dim3(256), 0,
-                       stream, MakeCsr(csr), geo.bps, geo.rows_per_partition,
-                       static_cast<uint32_t>(batch), b.keys, b.pay, status);
-    SCEMB_LAUNCH_CHECK();
-  }
-  const int key_bits = BitWidth(static_cast<uint64_t>(batch));
-  return RadixSortPairs<uint32_t, uint64_t>(b.keys, b.pay, b.keys_alt,
-                                            b.pay_alt, n, 0, key_bits, ws,
-                                            stream, in_alt);
+  *in_alt = false;
+  if (n == 0) return 0;
+  return GroupByRow(csr, geo, batch, b, ws, status, stream);
 }
 
 // Checks per-feature row blocks against a [batch, dim] activation matrix and

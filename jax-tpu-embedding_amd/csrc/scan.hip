@@ -7,11 +7,10 @@
 // Radix sort: per digit pass (up to 8 bits, passes balanced over the key
 // span), (1) per-tile digit histograms, (2) an exclusive scan of the
 // digit-major histogram matrix, (3) a stable scatter, staged through LDS so
-// that the writes of a tile come out bucket by bucket.
-// Stability inside a tile comes from processing it in 256-element chunks in
-// position order and ranking equal digits within each wave with 8 ballots
-// (wave-level multisplit), then across waves and chunks through LDS counters.
+// that the writes of a tile come out bucket by bucket (radix.h).
 #include "scan.h"
+
+#include "radix.h"
 
 #include "../../include/scemb.h"
 
@@ -173,180 +172,24 @@ template int ExclusiveScan<int64_t>(const int64_t*, int64_t*, int64_t,
                                     int64_t*, Arena&, hipStream_t);
 
 // ---------------------------------------------------------------------------
-// Radix sort.
+// Radix sort (kernels in radix.h).
 // ---------------------------------------------------------------------------
-
-namespace {
-
-constexpr int kSortBlock = 256;
-constexpr int kSortChunks = 8;
-constexpr int kSortTile = kSortBlock * kSortChunks;
-constexpr int kMaxDigitBits = 8;
-constexpr int kMaxRadix = 1 << kMaxDigitBits;
-constexpr int kSortWaves = kSortBlock / kWave;
-
-template <typename K>
-__device__ __forceinline__ uint32_t Digit(K key, int shift, uint32_t mask) {
-  return static_cast<uint32_t>(key >> shift) & mask;
-}
-
-// hist[d * tiles + tile] = keys of digit d in the tile.
-template <typename K>
-__global__ __launch_bounds__(kSortBlock) void RadixHistogram(
-    const K* keys, int64_t n, int shift, uint32_t mask, int64_t tiles,
-    uint32_t* hist) {
-  __shared__ uint32_t h[kMaxRadix];
-  const int radix = static_cast<int>(mask) + 1;
-  for (int d = threadIdx.x; d < radix; d += kSortBlock) h[d] = 0;
-  __syncthreads();
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
-#pragma unroll
-  for (int c = 0; c < kSortChunks; ++c) {
-    const int64_t i = base + c * kSortBlock + threadIdx.x;
-    if (i < n) atomicAdd(&h[Digit(keys[i], shift, mask)], 1u);
-  }
-  __syncthreads();
-  for (int d = threadIdx.x; d < radix; d += kSortBlock) {
-    hist[static_cast<int64_t>(d) * tiles + blockIdx.x] = h[d];
-  }
-}
-
-// Stable scatter of one tile (kSortTile consecutive elements) into the
-// digit buckets. Each element's rank inside its bucket comes from the chunks
-// (256 elements, in position order) before it, the waves before it in its
-// chunk and the lanes before it in its wave with the same digit (ballots).
-// The tile is first reordered by digit in LDS, then written out in that
-// order: consecutive threads then write consecutive positions of a bucket,
-// instead of one element per bucket and store.
-template <typename K, typename V>
-__global__ __launch_bounds__(kSortBlock) void RadixScatter(
-    const K* keys, const V* vals, K* keys_out, V* vals_out, int64_t n,
-    int shift, uint32_t mask, int digit_bits, int64_t tiles,
-    const uint32_t* offsets) {
-  __shared__ uint32_t run_base[kMaxRadix];    // bucket fill so far (tile)
-  __shared__ uint32_t wave_cnt[kSortWaves][kMaxRadix];
-  __shared__ uint32_t global_off[kMaxRadix];  // bucket start (output)
-  __shared__ uint32_t tile_off[kMaxRadix];    // bucket start (tile)
-  __shared__ uint32_t scan_tmp[kSortBlock / kWave + 1];
-  __shared__ K s_keys[kSortTile];
-  __shared__ V s_vals[kSortTile];
-  const int t = threadIdx.x;
-  const int wave = t / kWave;
-  const int radix = static_cast<int>(mask) + 1;
-  const int64_t blk = blockIdx.x;
-  const int64_t base = blk * kSortTile;
-  const int tile_n =
-      static_cast<int>(n - base < kSortTile ? n - base : kSortTile);
-  // Bucket sizes of this tile from the scanned histogram: the next cell's
-  // offset minus this one's (the last cell: n minus it).
-  uint32_t cnt_local[kMaxRadix / kSortBlock];
-#pragma unroll
-  for (int k = 0; k < kMaxRadix / kSortBlock; ++k) {
-    const int d = t + k * kSortBlock;
-    cnt_local[k] = 0;
-    if (d < radix) {
-      const int64_t cell = static_cast<int64_t>(d) * tiles + blk;
-      const uint32_t off = offsets[cell];
-      const uint32_t next = cell + 1 < static_cast<int64_t>(radix) * tiles
-                                ? offsets[cell + 1]
-                                : static_cast<uint32_t>(n);
-      global_off[d] = off;
-      run_base[d] = 0;
-      cnt_local[k] = next - off;
-    }
-  }
-  // Tile offsets of the buckets: exclusive scan over digits, thread t holding
-  // digits t, t + 256, ... (one round per 256 digits).
-#pragma unroll
-  for (int k = 0; k < kMaxRadix / kSortBlock; ++k) {
-    uint32_t total;
-    const uint32_t ex =
-        BlockExclusiveScan<uint32_t, kSortBlock>(cnt_local[k], scan_tmp,
-                                                 &total);
-    const int d = t + k * kSortBlock;
-    // Digits of round k follow all digits of earlier rounds.
-    __shared__ uint32_t round_base;
-    if (k == 0 && t == 0) round_base = 0;
-    __syncthreads();
-    if (d < radix) tile_off[d] = round_base + ex;
-    __syncthreads();
-    if (t == 0) round_base += total;
-    __syncthreads();
-  }
-  const uint64_t lt = LaneMaskLt();
-  for (int c = 0; c < kSortChunks; ++c) {
-    const int li = c * kSortBlock + t;  // position inside the tile
-    const bool active = li < tile_n;
-    K key = 0;
-    V val = 0;
-    uint32_t d = 0;
-    if (active) {
-      key = keys[base + li];
-      val = vals[base + li];
-      d = Digit(key, shift, mask);
-    }
-    for (int b = t; b < radix; b += kSortBlock) {
-#pragma unroll
-      for (int w = 0; w < kSortWaves; ++w) wave_cnt[w][b] = 0;
-    }
-    __syncthreads();
-    uint64_t match = __ballot(active);
-    for (int b = 0; b < digit_bits; ++b) {
-      const uint64_t bits = __ballot((d >> b) & 1u);
-      match &= ((d >> b) & 1u) ? bits : ~bits;
-    }
-    const uint32_t rank = static_cast<uint32_t>(__popcll(match & lt));
-    if (active && (match & lt) == 0) {
-      wave_cnt[wave][d] = static_cast<uint32_t>(__popcll(match));
-    }
-    __syncthreads();
-    for (int b = t; b < radix; b += kSortBlock) {
-      uint32_t r = run_base[b];
-#pragma unroll
-      for (int w = 0; w < kSortWaves; ++w) {
-        const uint32_t cnt = wave_cnt[w][b];
-        wave_cnt[w][b] = r;
-        r += cnt;
-      }
-      run_base[b] = r;
-    }
-    __syncthreads();
-    if (active) {
-      const uint32_t pos = tile_off[d] + wave_cnt[wave][d] + rank;
-      s_keys[pos] = key;
-      s_vals[pos] = val;
-    }
-    __syncthreads();
-  }
-  // Write out in tile-sorted order: element j of digit d goes to
-  // global_off[d] + (j - tile_off[d]).
-  for (int j = t; j < tile_n; j += kSortBlock) {
-    const K key = s_keys[j];
-    const uint32_t d = Digit(key, shift, mask);
-    const uint32_t pos = global_off[d] + (static_cast<uint32_t>(j) - tile_off[d]);
-    keys_out[pos] = key;
-    vals_out[pos] = s_vals[j];
-  }
-}
-
-}  // namespace
 
 template <typename K, typename V>
 int RadixSortPairs(K* keys, V* vals, K* keys_alt, V* vals_alt, int64_t n,
                    int begin_bit, int end_bit, Arena& ws, hipStream_t stream,
                    bool* in_alt) {
+  using radix::kSortBlock;
+  using radix::kSortTile;
   *in_alt = false;
   if (n <= 1 || end_bit <= begin_bit) return 0;
   if (n > (int64_t{1} << 32) - 1) {
     return Fail(1, "radix sort: more than 2^32-1 elements");
   }
-  // Fewest passes of at most kMaxDigitBits bits, balanced (27 bits: four
-  // passes of 7; 21: three of 7; 16: two of 8).
-  const int span = end_bit - begin_bit;
-  const int passes = (span + kMaxDigitBits - 1) / kMaxDigitBits;
-  const int digit = (span + passes - 1) / passes;
+  const radix::DigitPlan plan = radix::PlanDigits(end_bit - begin_bit);
   const int64_t tiles = CeilDiv(n, kSortTile);
-  uint32_t* hist = ws.Take<uint32_t>(tiles * (int64_t{1} << digit));
+  uint32_t* hist = ws.Take<uint32_t>(tiles * (int64_t{1} << plan.digit));
+  uint32_t* total = ws.Take<uint32_t>(1);
   const bool measuring = ws.measuring();
   if (!measuring && ws.overflow()) {
     return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
@@ -355,22 +198,28 @@ int RadixSortPairs(K* keys, V* vals, K* keys_alt, V* vals_alt, int64_t n,
   V* src_v = vals;
   K* dst_k = keys_alt;
   V* dst_v = vals_alt;
-  for (int shift = begin_bit; shift < end_bit; shift += digit) {
-    const int bits = end_bit - shift < digit ? end_bit - shift : digit;
+  for (int shift = begin_bit; shift < end_bit; shift += plan.digit) {
+    const int bits = end_bit - shift < plan.digit ? end_bit - shift
+                                                  : plan.digit;
     const uint32_t mask = (1u << bits) - 1u;
     const int64_t cells = tiles * (int64_t{1} << bits);
+    const radix::ArraySource<K, V> src{src_k, src_v};
     if (!measuring) {
-      hipLaunchKernelGGL(RadixHistogram<K>, dim3(tiles), dim3(kSortBlock), 0,
-                         stream, src_k, n, shift, mask, tiles, hist);
+      hipLaunchKernelGGL((radix::RadixHistogramK<K, radix::ArraySource<K, V>>),
+                         dim3(tiles), dim3(kSortBlock), 0, stream, src, n,
+                         nullptr, shift, mask, tiles, hist);
       SCEMB_LAUNCH_CHECK();
     }
-    const int st = ExclusiveScan<uint32_t>(hist, hist, cells, nullptr, ws,
+    const int st = ExclusiveScan<uint32_t>(hist, hist, cells, total, ws,
                                            stream);
     if (st != 0) return st;
     if (!measuring) {
-      hipLaunchKernelGGL((RadixScatter<K, V>), dim3(tiles), dim3(kSortBlock),
-                         0, stream, src_k, src_v, dst_k, dst_v, n, shift, mask,
-                         bits, tiles, hist);
+      const radix::ArraySink<K, V> sink{dst_k, dst_v};
+      hipLaunchKernelGGL(
+          (radix::RadixScatterK<K, V, radix::ArraySource<K, V>,
+                                radix::ArraySink<K, V>>),
+          dim3(tiles), dim3(kSortBlock), 0, stream, src, sink, n, nullptr,
+          shift, mask, bits, tiles, hist, total, false);
       SCEMB_LAUNCH_CHECK();
     }
     K* tk = src_k;

@@ -200,7 +200,12 @@ __device__ __forceinline__ int64_t CsrPositions(const Csr& csr) {
 __device__ __forceinline__ int LocateEntry(const Csr& csr, int64_t j,
                                            int* segment) {
   if (csr.num_minibatches == 0) {
-    const int s = static_cast<int>(j / csr.per_segment);
+    // Positions fit 32 bits (the row pointers are int32): a 32-bit divide.
+    const int s = csr.num_segments == 1
+                      ? 0
+                      : static_cast<int>(static_cast<uint32_t>(j) /
+                                         static_cast<uint32_t>(
+                                             csr.per_segment));
     *segment = s;
     return PartitionOf(csr.rp + static_cast<int64_t>(s) * csr.rp_per_segment,
                        csr.num_partitions, csr.per_segment,

@@ -18,7 +18,7 @@ from the same feature specs as the product:
 
 ``sparse_dense_matmul_grad_custom`` restates the custom-optimizer update
 (``lib/core/primitives/sparse_dense_matmul_optimizer_grad.py``; the test-side
-expectation of ``tests/sparse_dense_matmul_optimizer_grad_test.py:81-140``):
+expectation of ``primitives/tests/sparse_dense_matmul_optimizer_grad_test.py:81-140``):
 per-row gradient sums from the C backward, then the user's function in numpy
 float32 on the touched rows. It is pinned by equality with the oracle's
 built-in SGD and Adagrad (bit for bit) and by the reference's custom-Adagrad

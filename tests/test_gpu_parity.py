@@ -843,3 +843,93 @@ def test_repeated_key_in_one_entry_per_key_view_is_flagged():
                               device_status=status)
   torch.cuda.synchronize()
   assert int(status.item()) & _native.STATUS_SHARED_ROW
+
+
+def _expected_sample_stream(rp, eid, sid, gains, num_sc, bps, rpp):
+  """The CSR's valid entries grouped by activation row, each row in CSR
+  order (a stable sort by row), as (keys, packed entries) with the entry
+  packed as (partition * rows_per_partition + id) | gain bits << 32."""
+  rp = np.asarray(rp).reshape(num_sc, -1)
+  eid, sid = np.asarray(eid), np.asarray(sid)
+  g = np.asarray(gains, np.float32).view(np.uint32).astype(np.uint64)
+  per_seg = eid.size // num_sc
+  keys, ents = [], []
+  for s in range(num_sc):
+    start = 0
+    for p, end in enumerate(rp[s]):
+      end = min(int(end), per_seg)
+      for j in range(s * per_seg + start, s * per_seg + max(start, end)):
+        if 0 <= eid[j] < rpp and 0 <= sid[j] < bps:
+          keys.append(s * bps + sid[j])
+          ents.append(np.uint64(p * rpp + eid[j]) | (g[j] << np.uint64(32)))
+      start = max(start, (end + 7) // 8 * 8)
+  keys = np.asarray(keys, np.int64)
+  ents = np.asarray(ents, np.uint64)
+  order = np.argsort(keys, kind="stable")
+  return keys[order], ents[order]
+
+
+@pytest.mark.parametrize("num_sc", [1, 4])
+def test_sample_stream_is_csr_order_within_rows(num_sc):
+  """The CSR-only forward groups the entries by activation row inside the
+  call. Its stream must equal a stable sort by row of the CSR's valid
+  entries exactly (each row in CSR order, the order in which the oracle
+  sums), for rows of 0 to 6000 entries over one and four segments, with
+  float gains (weights) so that any order change would also move the
+  activations' bits."""
+  rng = np.random.default_rng(41 + num_sc)
+  vocab = 24000
+  sizes = [0, 1, 2, 7, 63, 64, 65, 200, 511, 512, 513, 1000, 4095, 4096, 4097,
+           6000, 3, 0, 40, 90]
+  batch = len(sizes)
+  _, feats = _make_specs(1, [vocab], [8], "sum",
+                         embedding_spec.SGDOptimizerSpec(0.01), batch,
+                         max_ids=1 << 16)
+  embedding.prepare_feature_specs_for_training(feats, 1, num_sc)
+  arr = np.empty(batch, dtype=object)
+  warr = np.empty(batch, dtype=object)
+  for i, n in enumerate(sizes):
+    arr[i] = rng.permutation(vocab)[:n].astype(np.int32)
+    warr[i] = rng.uniform(0.5, 1.5, size=n).astype(np.float32)
+  ref = refcpu.preprocess([arr], [warr], feats, 1, 1,
+                          num_sc_per_device=num_sc)
+  name = next(iter(ref.row_pointers))
+  rows = feats[0].table_spec.stacked_table_spec.stack_vocab_size
+  bps = batch // num_sc
+  keep, c = _device.csr_operands(ref.row_pointers[name],
+                                 ref.embedding_ids[name], ref.sample_ids[name],
+                                 ref.gains[name], num_sc, num_sc)
+  status = torch.zeros(1, dtype=torch.int32, device="cuda")
+  view = _native.build_sample_view(c, batch, rows, device_status=status)
+  torch.cuda.synchronize()
+  del keep
+  assert int(status.item()) == 0
+  ek, ee = _expected_sample_stream(ref.row_pointers[name],
+                                   ref.embedding_ids[name],
+                                   ref.sample_ids[name], ref.gains[name],
+                                   num_sc, bps, rows // num_sc)
+  gk = view.keys.cpu().numpy().astype(np.int64)
+  ge = view.entries.cpu().numpy().view(np.uint64)
+  total = ek.size
+  np.testing.assert_array_equal(gk[:total], ek)
+  np.testing.assert_array_equal(ge[:total], ee)
+  assert (gk[total:] == batch).all()
+  # The forward through the CSR alone feeds the kernel the same stream.
+  table = rng.normal(size=(rows, 8)).astype(np.float32)
+  table_t = torch.from_numpy(table).cuda()
+  act = _fwd_bind(ref, name, table_t, batch, num_sc).cpu().numpy()
+  act_v = _fwd_bind(ref, name, table_t, batch, num_sc,
+                    view=view).cpu().numpy()
+  np.testing.assert_array_equal(act, act_v)
+  args = (ref.row_pointers[name], ref.embedding_ids[name],
+          ref.sample_ids[name])
+  common = dict(num_sc_per_device=num_sc, num_scs=num_sc)
+  exp = refcpu.sparse_dense_matmul(*args, ref.gains[name], table, batch,
+                                   **common)
+  # Rows of thousands of terms are summed by blocks on the GPU and in one
+  # sequence by the oracle: the difference is bounded by a few dozen ulp of
+  # the sum of the terms' magnitudes.
+  mag = refcpu.sparse_dense_matmul(*args, np.abs(ref.gains[name]),
+                                   np.abs(table), batch, **common)
+  bound = 32 * np.finfo(np.float32).eps * mag + ATOL
+  assert (np.abs(act - exp) <= bound).all()
