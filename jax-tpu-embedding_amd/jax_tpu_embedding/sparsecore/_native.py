@@ -436,6 +436,33 @@ NUM_SIDE_STREAMS = 3
 _side_streams = {}
 
 
+_hip = None
+
+
+def _new_stream(dev: int):
+  """A HIP stream of its own (non-blocking, default priority), wrapped for
+  torch. torch.cuda.Stream() hands out a fixed pool of streams round robin,
+  so two pools built from it can share a stream, and a side stream can be
+  the very stream another caller uses; these are never shared. They live
+  until the process ends."""
+  global _hip
+  t = torch()
+  if _hip is None:
+    # The HIP runtime torch runs on (its own copy when it ships one), so
+    # that the stream belongs to the same runtime instance.
+    own = pathlib.Path(t.__file__).parent / "lib" / "libamdhip64.so"
+    _hip = ctypes.CDLL(str(own) if own.exists() else "libamdhip64.so")
+    _hip.hipStreamCreateWithFlags.argtypes = [
+        ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+    _hip.hipStreamCreateWithFlags.restype = ctypes.c_int
+  with t.cuda.device(dev):
+    h = ctypes.c_void_p()
+    rc = _hip.hipStreamCreateWithFlags(ctypes.byref(h), 1)  # NonBlocking
+    if rc != 0:
+      raise RuntimeError(f"hipStreamCreateWithFlags failed ({rc})")
+    return t.cuda.ExternalStream(h.value, device=dev)
+
+
 def side_streams(n: int) -> list:
   """The first n side streams of the current device's current stream."""
   if n <= 0:
@@ -446,10 +473,62 @@ def side_streams(n: int) -> list:
   pool = _side_streams.get(key)
   if pool is None or len(pool) < n:
     pool = (pool or []) + [
-        t.cuda.Stream(device=dev)
+        _new_stream(dev)
         for _ in range(max(n, NUM_SIDE_STREAMS) - len(pool or []))]
     _side_streams[key] = pool
   return pool[:n]
+
+
+def _tensors_in(obj, out):
+  t = torch()
+  if isinstance(obj, t.Tensor):
+    out.append(obj)
+  elif isinstance(obj, dict):
+    for v in obj.values():
+      _tensors_in(v, out)
+  elif isinstance(obj, (list, tuple)):
+    for v in obj:
+      _tensors_in(v, out)
+  elif hasattr(obj, "__dict__"):
+    for v in vars(obj).values():
+      _tensors_in(v, out)
+  return out
+
+
+def run_per_stack(names, fn, width=None) -> dict:
+  """{name: fn(name)} for independent per-stack calls (their own tables,
+  inputs and outputs). Stacks of different widths (width(name), e.g. the
+  embedding dimension) run concurrently, each width on its own side stream
+  of the current stream (round robin): the narrow stacks' latency-bound
+  kernels then fill the gaps and tails of the wide stacks' bandwidth-bound
+  ones. Stacks of one width run one after another on their stream, as
+  concurrent copies of the same bandwidth-bound kernel only compete for the
+  same L2 and HBM. The current stream then waits for all of them; results
+  allocated on a side stream are marked as used by the current stream, so
+  their memory is not recycled before the caller's later work. A single
+  width, no side streams (NUM_SIDE_STREAMS = 0) or no GPU: inline."""
+  names = list(names)
+  t = torch()
+  widths = [width(n) if width else n for n in names]
+  distinct = list(dict.fromkeys(widths))
+  if (len(distinct) <= 1 or NUM_SIDE_STREAMS <= 0 or
+      not t.cuda.is_available()):
+    return {n: fn(n) for n in names}
+  main = t.cuda.current_stream()
+  sides = side_streams(min(len(distinct), NUM_SIDE_STREAMS))
+  for s in sides:
+    s.wait_stream(main)
+  out = {}
+  for n, w in zip(names, widths):
+    with t.cuda.stream(sides[distinct.index(w) % len(sides)]):
+      out[n] = fn(n)
+  for s in sides:
+    main.wait_stream(s)
+  if not t.cuda.is_current_stream_capturing():
+    for x in _tensors_in(out, []):
+      if x.is_cuda:
+        x.record_stream(main)
+  return out
 
 
 def stream_handle() -> int:

@@ -578,9 +578,10 @@ def tpu_sparse_dense_matmul(preprocessed_inputs, embedding_variables,
   by_stack = collections.defaultdict(list)
   for fs in leaves:
     by_stack[fs.table_spec.stacked_table_spec.stack_name].append(fs)
-  acts = {}
   per_feature = {}
-  for name, spec in stacked.items():
+
+  def lookup(name):
+    spec = stacked[name]
     ev = embedding_variables[name]
     table = ev.table if isinstance(ev, EmbeddingVariables) else ev[0]
     fused = None
@@ -589,24 +590,32 @@ def tpu_sparse_dense_matmul(preprocessed_inputs, embedding_variables,
       # the per-feature outputs.
       fused = _activation_blocks(spec, by_stack[name], global_device_count,
                                  num_sc_per_device, _native.device())
-    acts[name] = (sparse_dense_matmul_csr.tpu_sparse_dense_matmul_csr_primitive
-                  .bind(rp[name], eid[name], sid[name], gains[name], nmb,
-                        table,
-                        device_batch_size=(spec.total_sample_count //
-                                           global_device_count),
-                        max_ids_per_partition=spec.max_ids_per_partition,
-                        max_unique_ids_per_partition=(
-                            spec.max_unique_ids_per_partition),
-                        sharding_strategy=strategy,
-                        quantization_config=(
-                            spec.quantization_config.as_tuple()
-                            if spec.quantization_config else None),
-                        enable_minibatching=enable_minibatching,
-                        num_sc_per_device=num_sc_per_device,
-                        global_device_count=global_device_count,
-                        lookup_view=views.get(name),
-                        csr_num_entries=counts.get(name),
-                        activation_blocks=fused[1] if fused else None))
+    act = (sparse_dense_matmul_csr.tpu_sparse_dense_matmul_csr_primitive
+           .bind(rp[name], eid[name], sid[name], gains[name], nmb, table,
+                 device_batch_size=(spec.total_sample_count //
+                                    global_device_count),
+                 max_ids_per_partition=spec.max_ids_per_partition,
+                 max_unique_ids_per_partition=(
+                     spec.max_unique_ids_per_partition),
+                 sharding_strategy=strategy,
+                 quantization_config=(
+                     spec.quantization_config.as_tuple()
+                     if spec.quantization_config else None),
+                 enable_minibatching=enable_minibatching,
+                 num_sc_per_device=num_sc_per_device,
+                 global_device_count=global_device_count,
+                 lookup_view=views.get(name),
+                 csr_num_entries=counts.get(name),
+                 activation_blocks=fused[1] if fused else None))
+    return act, fused
+
+  # Independent stacks of different widths run concurrently (one side
+  # stream per width); a quantized stack is refused inside its call.
+  results = _native.run_per_stack(
+      stacked.keys(), lookup, lambda n: stacked[n].stack_embedding_dim)
+  acts = {}
+  for name in stacked:
+    acts[name], fused = results[name]
     if fused:
       per_feature.update(fused[0])
   if not perform_unstacking:
@@ -735,8 +744,8 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
   strategy = int(sharding_strategy_to_enum(sharding_strategy))
   nmb = _resolve_scalar_minibatches(preprocessed_inputs.num_minibatches)
   g_count = 1 if global_device_count is None else global_device_count
-  out = {}
-  for name, spec in stacked.items():
+  def update(name):
+    spec = stacked[name]
     ev = embedding_variables[name]
     opt = spec.optimizer
     hyper = opt.get_hyperparameters(step)
@@ -780,8 +789,12 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
     # The updated variables in the structure they came in
     # (embedding.py:1524-1527): EmbeddingVariables stay EmbeddingVariables
     # (with their slot type), a plain (table, *slots) tuple stays a tuple.
-    out[name] = _tree.tree_unflatten(treedef, list(res))
-  return out
+    return _tree.tree_unflatten(treedef, list(res))
+
+  # Independent stacks of different widths update concurrently.
+  results = _native.run_per_stack(
+      stacked.keys(), update, lambda n: stacked[n].stack_embedding_dim)
+  return {name: results[name] for name in stacked}
 
 
 @functools.lru_cache(maxsize=64)

@@ -157,7 +157,9 @@ def test_preprocessing_on_a_side_stream_overlaps_steps(multi_hot):
 
 def test_graph_replays_after_its_workspace_is_outgrown():
   """A step captured on stream cs, then a larger step run eagerly on cs
-  (its workspace grows); the replays still equal an eager twin."""
+  (the workspaces its calls use grow); the replays still equal an eager
+  twin. The workspaces checked are those of cs and of its side streams
+  (stacks of different widths would run there)."""
   small, large = _specs(512), _specs(32768, dim=128)
   rng = np.random.default_rng(21)
   pre_s, _ = embedding.preprocess_sparse_dense_matmul_input(
@@ -177,14 +179,18 @@ def test_graph_replays_after_its_workspace_is_outgrown():
   with torch.cuda.graph(g, stream=cs):
     graph_acts = _step(pre_s, graphed, small, g_s)
   torch.cuda.synchronize()
-  key = (torch.cuda.current_device(), cs.cuda_stream)
-  captured = _native.WORKSPACE._buf[key]  # pylint: disable=protected-access
+  dev = torch.cuda.current_device()
+  sides = _native._side_streams.get((dev, cs.cuda_stream), [])  # pylint: disable=protected-access
+  keys = [(dev, s.cuda_stream) for s in [cs] + list(sides)]
+  bufs = _native.WORKSPACE._buf  # pylint: disable=protected-access
+  captured = {k: bufs[k] for k in keys if k in bufs}
+  assert captured
   with torch.cuda.stream(cs):
-    _step(pre_l, big, large, g_l)  # needs a larger workspace on cs
+    _step(pre_l, big, large, g_l)  # needs larger workspaces
   torch.cuda.synchronize()
-  grown = _native.WORKSPACE._buf[key]  # pylint: disable=protected-access
-  assert grown.data_ptr() != captured.data_ptr()
-  assert grown.numel() > captured.numel()
+  grown = {k: bufs[k] for k in captured}
+  assert any(grown[k].data_ptr() != captured[k].data_ptr() and
+             grown[k].numel() > captured[k].numel() for k in captured)
   del captured, grown
   for i in range(3):
     acts = _step(pre_s, eager, small, g_s)
@@ -214,9 +220,10 @@ def _specs_three_stacks(batch):
 
 @pytest.mark.parametrize("multi_hot", [False, True])
 def test_stacks_on_side_streams_equal_one_stream(multi_hot, monkeypatch):
-  """The stacks of one call are enqueued on forked side streams; the CSR
-  (compared region), the stats and a training step equal those of the same
-  call with every stack on the calling stream."""
+  """The stacks of one call are enqueued on forked side streams (the
+  preprocessing, the lookups and the updates); the CSR (compared region),
+  the stats and a training step equal those of the same calls with every
+  stack on the calling stream."""
   feats = _specs_three_stacks(4096)
   assert len(embedding.get_stacked_table_specs(feats)) == 3
   ids = _ids(np.random.default_rng(21), feats, multi_hot)
