@@ -775,7 +775,8 @@ def cpu_baseline(w: Workload, sample_batch: int, seconds: float,
   from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top
   from oracle import refcpu  # pylint: disable=g-import-not-at-top
 
-  threads = min(16, os.cpu_count() or 1)
+  # A one-GPU box's CPU share is 16 cores, whatever the host has in all.
+  threads = min(CPU_SHARE, _usable_cpus())
   batch = w.feature_specs[0].input_shape[0]
   sample_batch = min(sample_batch, batch)
   feats = [_head(f, sample_batch) for f in w.features]
@@ -868,6 +869,9 @@ def cpu_baseline(w: Workload, sample_batch: int, seconds: float,
       "value": total_lookups * iters / busy,
       "unit": "lookups/s",
       "cores": threads,
+      "host_cpus": os.cpu_count(),
+      "usable_cpus": _usable_cpus(),
+      "cpu_model": _cpu_model(),
       "kind": "port",
       "sample": (f"first {sample_batch} samples of each of the "
                  f"{len(feats)} features ({total_lookups} lookups), "
@@ -882,6 +886,27 @@ def cpu_baseline(w: Workload, sample_batch: int, seconds: float,
           f"limit {mb[2]} ids per partition, {mb[1]} minibatches"
           if mb else None),
   }
+
+
+CPU_SHARE = 16  # host cores a one-GPU job may use on the GPU boxes
+
+
+def _usable_cpus() -> int:
+  try:
+    return len(os.sched_getaffinity(0))
+  except (AttributeError, OSError):
+    return os.cpu_count() or 1
+
+
+def _cpu_model() -> str | None:
+  try:
+    with open("/proc/cpuinfo") as f:
+      for line in f:
+        if line.startswith("model name"):
+          return line.split(":", 1)[1].strip()
+  except OSError:
+    pass
+  return None
 
 
 KERNEL_SOURCES = ("segreduce.h", "lookup.hip")
