@@ -27,18 +27,18 @@ from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-i
 from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top,wrong-import-position
 
 
-def _workload(one_hot, seed=0):
+def _workload(one_hot, seed=0, dims=(32, 32, 32)):
   rng = np.random.default_rng(seed)
-  batch, dim = 2048, 32
+  batch = 2048
   tables = [embedding_spec.TableSpec(
-      name=f"t{i}", vocabulary_size=int(v), embedding_dim=dim,
+      name=f"t{i}", vocabulary_size=int(v), embedding_dim=dims[i],
       initializer=embedding_spec.zeros,
       optimizer=embedding_spec.AdagradOptimizerSpec(0.05), combiner="sum",
       max_ids_per_partition=1 << 16, max_unique_ids_per_partition=1 << 16)
             for i, v in enumerate((100, 5000, 70000))]
   feats = [embedding_spec.FeatureSpec(
       name=f"f{i}", table_spec=t, input_shape=[batch, 1],
-      output_shape=[batch, dim]) for i, t in enumerate(tables)]
+      output_shape=[batch, t.embedding_dim]) for i, t in enumerate(tables)]
   embedding.prepare_feature_specs_for_training(feats, 1, 1)
   ids = []
   for t in tables:
@@ -55,17 +55,21 @@ def _workload(one_hot, seed=0):
       ids, None, feats, 1, 1, num_sc_per_device=1)
   init = {}
   for name, spec in embedding.get_stacked_table_specs(feats).items():
-    table = torch.tensor(rng.normal(0, 0.01, size=(spec.stack_vocab_size,
-                                                   dim)).astype(np.float32))
+    table = torch.tensor(rng.normal(0, 0.01, size=(
+        spec.stack_vocab_size, spec.stack_embedding_dim)).astype(np.float32))
     init[name] = (table.cuda(), torch.full_like(table, 0.1).cuda())
-  grads = [torch.tensor(rng.normal(size=(batch, dim)).astype(np.float32)
-                        ).cuda() for _ in feats]
+  grads = [torch.tensor(rng.normal(size=(batch, fs.table_spec.embedding_dim)
+                                   ).astype(np.float32)).cuda()
+           for fs in feats]
   return feats, pre, init, grads
 
 
+@pytest.mark.parametrize("dims", [(32, 32, 32), (8, 16, 32)])
 @pytest.mark.parametrize("one_hot", [True, False])
-def test_graph_replays_equal_eager_steps(one_hot):
-  feats, pre, init, grads = _workload(one_hot)
+def test_graph_replays_equal_eager_steps(one_hot, dims):
+  """With stacks of three widths the lookups and updates run on forked side
+  streams (run_per_stack), so the graph also holds their fork and join."""
+  feats, pre, init, grads = _workload(one_hot, dims=dims)
 
   def make_state():
     return {n: embedding.EmbeddingVariables(table=t.clone(), slot=(a.clone(),))
