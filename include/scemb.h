@@ -407,7 +407,29 @@ typedef struct scemb_feature {
   int32_t row_offset;  /* FeatureIdTransformation.row_offset */
   int32_t col_offset;  /* FeatureIdTransformation.col_offset */
   int32_t col_shift;   /* FeatureIdTransformation.col_shift */
+  /* With row_splits: the most ids of one row, or 0 when not known (the
+   * library then reads it off the row splits). A hint that picks the
+   * grouping route (scemb_preprocess_options_t.flags); any value gives the
+   * same outputs. */
+  int64_t max_row_length;
 } scemb_feature_t;
+
+/* Checks host row splits [num_rows + 1] (start at 0, non-decreasing, end at
+ * nnz; the RaggedTensorInputBatch contract, ragged_tensor_input_batch.h:
+ * 68-127) in one pass and returns the most ids of one row in
+ * *max_row_length. SCEMB_ERR_INVALID_ARGUMENT when they do not hold. */
+int scemb_check_row_splits(const int64_t* row_splits, int64_t num_rows,
+                           int64_t nnz, int64_t* max_row_length);
+
+/* scemb_preprocess_options_t.flags. Where the features' sample rows are
+ * disjoint and neither id dropping nor minibatching is on, the library merges
+ * the copies of an id within one input row while extracting (the only
+ * duplicates such an input can hold) and sorts the distinct entries; a
+ * sample view then also needs a static buffer of at least the theoretical
+ * size (scemb_compute_theoretical_max_coo_buffer_size). Otherwise it sorts
+ * every id and merges duplicates after the sort. Both routes give the same
+ * outputs; this flag forces the second, for comparison. */
+#define SCEMB_PREPROCESS_GROUP_AFTER_SORT 1
 
 typedef struct scemb_preprocess_options {
   int32_t local_device_count;
@@ -449,7 +471,7 @@ typedef struct scemb_preprocess_options {
   int32_t enable_minibatching;
   int64_t table_rows; /* rows of the device's table, for the sample view */
   int32_t minibatching_pass;
-  int32_t reserved;
+  int32_t flags; /* SCEMB_PREPROCESS_* bits; 0 for the default route */
   uint64_t minibatching_split; /* pass 2: bit i set = tree node i split
                                   (MinibatchingSplit, input_preprocessing_
                                   util.h:94) */

@@ -42,6 +42,7 @@
 
 #include "../../include/scemb.h"
 #include "common.h"
+#include "radix.h"
 #include "scan.h"
 
 namespace scemb {
@@ -607,7 +608,28 @@ struct BucketReduceArgs {
   const uint32_t* keep_scan;
   int64_t num_buckets;  // 0: the stats were reduced beforehand
   BucketStats* out;
+  // Not null: every sorted entry is its own run (grouped at extraction) and
+  // col_heads[b] counts bucket b's distinct columns; flags, scan and
+  // keep_scan are unused.
+  const int32_t* col_heads;
 };
+
+// Stats of one bucket whose entries are all distinct (row, column) pairs
+// and all kept: part_first..part_last of the sorted entries.
+__device__ __forceinline__ BucketStats UniqueBucket(const int32_t* part_first,
+                                                    const int32_t* part_last,
+                                                    const int32_t* col_heads,
+                                                    int64_t bkt) {
+  BucketStats s{0, 0, 0, 0};
+  const int32_t f = part_first[bkt];
+  if (f >= 0) {
+    s.obs_ids = part_last[bkt] - f + 1;
+    s.obs_unique = col_heads[bkt];
+    s.kept = s.obs_ids;
+    s.kept_first = f;
+  }
+  return s;
+}
 
 struct FillPlan {
   int64_t start;      // absolute position of the first kept entry
@@ -642,8 +664,11 @@ __global__ __launch_bounds__(256) void FillPlanKernel(
     int32_t* stat_required, int64_t* counters, BucketReduceArgs br) {
   if (br.num_buckets > 0) {
     for (int64_t bkt = threadIdx.x; bkt < br.num_buckets; bkt += blockDim.x) {
-      br.out[bkt] = ReduceBucket(br.part_first, br.part_last, br.flags,
-                                 br.scan, br.keep_scan, bkt);
+      br.out[bkt] = br.col_heads != nullptr
+                        ? UniqueBucket(br.part_first, br.part_last,
+                                       br.col_heads, bkt)
+                        : ReduceBucket(br.part_first, br.part_last, br.flags,
+                                       br.scan, br.keep_scan, bkt);
     }
     __syncthreads();
   }
@@ -1252,17 +1277,22 @@ __global__ __launch_bounds__(256) void ViewCompact(
   }
 }
 
-// Also copies the grouped-entry total into the counters when `totals` is
-// not null (after ScatterRuns, which reads it).
+// Also copies the grouped-entry total into the counters when `totals` (low
+// half of a 64-bit scan total) or `total32` is not null (after the scatter,
+// which reads it).
 __global__ __launch_bounds__(256) void WritePadding(const FillPlan* plans,
                                                     int64_t num_buckets,
                                                     FillParams fp, int32_t* eid,
                                                     int32_t* sid, float* gains,
                                                     const uint64_t* totals,
+                                                    const uint32_t* total32,
                                                     int64_t* counters) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (t == 0 && totals != nullptr) {
     counters[3] = static_cast<int64_t>(static_cast<uint32_t>(totals[0]));
+  }
+  if (t == 0 && total32 != nullptr) {
+    counters[3] = static_cast<int64_t>(total32[0]);
   }
   const int64_t bkt = t / kAlign;
   const int k = static_cast<int>(t % kAlign);
@@ -1291,6 +1321,418 @@ __global__ void StoreTotal(const uint64_t* totals, int64_t* counters) {
 }
 
 // ---------------------------------------------------------------------------
+// Grouping at extraction. Where the sample rows of a stack's features are
+// disjoint, two ids share (row, column) only if one input row holds the same
+// id twice; the grouping of sort_and_group_coo_tensors_impl.h:196-311 then
+// merges exactly the copies of an id within one input row, summing their
+// gains in input order. ExtractUnique does that while it extracts, so that
+// the sort sees one entry per (row, column) and every sorted entry is its
+// own run. The sample view is the extraction-order compaction of those
+// entries (ViewWrite); the CSR is the sorted entries (GroupUnique,
+// ScatterUnique).
+// ---------------------------------------------------------------------------
+
+// Input positions of one ExtractUnique block's rows staged in LDS, and the
+// longest row the route is taken for: a block of kExtractBlock consecutive
+// ids then spans at most kExtractBlock + 2 * (kDedupMaxRow - 1) positions,
+// which fit the staging.
+constexpr int kDedupStage = 2048;
+constexpr int64_t kDedupMaxRow = 896;
+static_assert(kExtractBlock + 2 * (kDedupMaxRow - 1) <= kDedupStage,
+              "a block's rows must fit the staging");
+
+// Combiner divisor of one row (ComputeWeightDivisor,
+// process_coo_tensors_impl.h:60-74): the weights summed in order in float
+// (mean, combiner 1), or the square root of the float sum of double squares
+// (sqrtn, combiner 2). Weights are loaded eight at a time ahead of the
+// sequential sum.
+template <typename W>
+__device__ __forceinline__ float RowDivisor(const W* w, int n, int combiner) {
+  float s = 0.0f;
+  int k = 0;
+  if (combiner == 1) {
+    for (; k + 8 <= n; k += 8) {
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = w[k + j];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s = s + x[j];
+    }
+    for (; k < n; ++k) s = s + w[k];
+    return s;
+  }
+  for (; k + 8 <= n; k += 8) {
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = w[k + j];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const double d = static_cast<double>(x[j]);
+      s = static_cast<float>(static_cast<double>(s) + d * d);
+    }
+  }
+  for (; k < n; ++k) {
+    const double d = static_cast<double>(w[k]);
+    s = static_cast<float>(static_cast<double>(s) + d * d);
+  }
+  return sqrtf(s);
+}
+
+// The id at position q of a row of n ids (ids, weights w): whether it is the
+// row's first copy of that id, and its gain summed with the gains of the
+// later copies in input order. Weighted gains are w / div, with div the
+// row's divisor (computed here unless `have_div`); unit weights give the
+// combiner's 1, 1/n or 1/sqrt(n). One pass, eight ids at a time, counts the
+// copies before and after q; only a first copy with later copies walks the
+// row again to add their gains.
+template <typename T, typename W>
+__device__ __forceinline__ bool ScanRow(const T* ids, const W* w, int n, int q,
+                                        bool has_weights, int combiner,
+                                        bool have_div, float* div,
+                                        int32_t* id_out, float* gain_out) {
+  const int32_t id = ids[q];
+  *id_out = id;
+  if (has_weights && !have_div) *div = RowDivisor(w, n, combiner);
+  float unit = 1.0f;
+  if (!has_weights && combiner == 1) {
+    unit = 1.0f / static_cast<float>(n);
+  } else if (!has_weights && combiner == 2) {
+    unit = 1.0f / sqrtf(static_cast<float>(n));
+  }
+  int before = 0, after = 0;
+  int k = 0;
+  for (; k + 8 <= n; k += 8) {
+    int32_t a[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j] = ids[k + j];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const bool eq = a[j] == id;
+      before += eq && k + j < q;
+      after += eq && k + j > q;
+    }
+  }
+  for (; k < n; ++k) {
+    const bool eq = ids[k] == id;
+    before += eq && k < q;
+    after += eq && k > q;
+  }
+  float gain = has_weights ? w[q] / *div : unit;
+  if (before == 0 && after > 0) {
+    for (k = q + 1; k < n; ++k) {
+      if (ids[k] == id) gain = gain + (has_weights ? w[k] / *div : unit);
+    }
+  }
+  *gain_out = gain;
+  return before == 0;
+}
+
+// One thread per extracted id, laid out as ExtractIds. The block stages the
+// ids (and weights) of the rows it spans in LDS and, for a weighted mean or
+// sqrtn, each row's divisor (one thread per row, the sequential sums of
+// RowDivisors). An id then scans its row: an earlier copy makes it a
+// duplicate; a first copy adds the gains of the later copies to its own, in
+// input order. The first copy of an id writes its key and (sample, summed
+// gain); later copies and ids outside the table write the sentinel key.
+// Blocks whose rows do not fit the staging read them from memory. With
+// `view_counts`, each block also counts its entries that enter the sample
+// view (a first copy whose local row is below `view_rows`).
+template <typename K>
+__global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
+    const SliceDesc* slices, int num_slices, const FeatureDev* feats,
+    const BlockRows* block_rows, int64_t total_ids, int combiner,
+    int has_weights, KeyLayout kl, int64_t view_rows, K* keys, uint64_t* pay,
+    uint32_t* view_counts, int64_t* counters) {
+  __shared__ int64_t s_splits[kExtractStagedSplits];
+  __shared__ int32_t s_ids[kDedupStage];
+  __shared__ float s_w[kDedupStage];
+  __shared__ float s_div[kExtractStagedSplits];
+  const int64_t blk_first = static_cast<int64_t>(blockIdx.x) * blockDim.x;
+  const int64_t o = blk_first + threadIdx.x;
+  const BlockRows br = block_rows[blockIdx.x];
+  const int block_slice = br.slice;
+  const int64_t row_lo = br.lo, row_hi = br.hi;
+  const bool need_div = has_weights && combiner != 0;
+  bool staged = false;       // row splits [row_lo, row_hi + 1] in s_splits
+  bool ids_staged = false;   // ids (and weights) [span_b, span_e) in LDS
+  int64_t span_b = 0, span_e = 0;
+  int64_t div_row0 = 0;      // row of s_div[0]
+  int div_rows = 0;          // rows with a divisor in s_div
+  int64_t valency = 0;       // dense feature of the block
+  if (block_slice >= 0) {  // uniform over the block
+    const SliceDesc bsl = slices[block_slice];
+    const FeatureDev bf = feats[bsl.feature];
+    if (bf.splits != nullptr) {
+      const int64_t cnt = row_hi - row_lo + 2;
+      if (cnt <= kExtractStagedSplits) {
+        for (int64_t i = threadIdx.x; i < cnt; i += blockDim.x) {
+          s_splits[i] = bf.splits[row_lo + i];
+        }
+        staged = true;
+      }
+      span_b = bf.splits[row_lo];
+      span_e = bf.splits[row_hi + 1];
+    } else if (bf.valency > 0) {
+      valency = bf.valency;
+      const int64_t o_last = min(blk_first + kExtractBlock, total_ids) - 1;
+      const int64_t p_first = bsl.id_begin + (blk_first - bsl.out_begin);
+      const int64_t p_last = bsl.id_begin + (o_last - bsl.out_begin);
+      span_b = p_first / valency * valency;
+      span_e = (p_last / valency + 1) * valency;
+    }
+    if (span_e > span_b && span_e - span_b <= kDedupStage) {
+      const int n = static_cast<int>(span_e - span_b);
+      for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        s_ids[i] = bf.ids[span_b + i];
+        if (has_weights) s_w[i] = bf.weights[span_b + i];
+      }
+      ids_staged = true;
+      if (need_div) {
+        const int64_t rows =
+            valency > 0 ? (span_e - span_b) / valency
+                        : (staged ? row_hi - row_lo + 1 : 0);
+        if (rows <= kExtractStagedSplits) {
+          div_rows = static_cast<int>(rows);
+          div_row0 = valency > 0 ? span_b / valency : row_lo;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < div_rows; t += blockDim.x) {
+    const int64_t b = valency > 0 ? t * valency : s_splits[t] - span_b;
+    const int64_t e = valency > 0 ? b + valency : s_splits[t + 1] - span_b;
+    s_div[t] = RowDivisor(s_w + b, e - b, combiner);
+  }
+  __syncthreads();
+  bool bad = false;
+  bool view_entry = false;
+  if (o < total_ids) {
+    const int si = block_slice >= 0 ? block_slice
+                                    : FindSlice(slices, num_slices, o, false);
+    const SliceDesc sl = slices[si];
+    const FeatureDev f = feats[sl.feature];
+    const int64_t p = sl.id_begin + (o - sl.out_begin);  // input position
+    int64_t r, b, e;
+    if (staged) {
+      const int64_t k = LastRowAtOrBefore(s_splits, 0, row_hi - row_lo, p);
+      r = row_lo + k;
+      b = s_splits[k];
+      e = s_splits[k + 1];
+    } else if (f.splits != nullptr) {
+      int64_t lo = sl.row_start, hi = sl.row_start + sl.num_rows - 1;
+      if (block_slice >= 0) {
+        lo = row_lo;
+        hi = row_hi;
+      }
+      r = LastRowAtOrBefore(f.splits, lo, hi, p);
+      b = f.splits[r];
+      e = f.splits[r + 1];
+    } else {
+      r = p / f.valency;
+      b = r * f.valency;
+      e = b + f.valency;
+    }
+    // The row in LDS (a staged block holds all of its rows) or in memory;
+    // two inlined copies, so that each reads through a pointer of one
+    // address space.
+    const int n = static_cast<int>(e - b);
+    const int q = static_cast<int>(p - b);  // position in the row
+    float div = 1.0f;
+    if (need_div && r - div_row0 >= 0 && r - div_row0 < div_rows) {
+      div = s_div[r - div_row0];
+    }
+    const bool table_div = !need_div || (r - div_row0 >= 0 &&
+                                         r - div_row0 < div_rows);
+    int32_t id;
+    float gain;
+    bool first;
+    if (ids_staged) {
+      const int64_t off = b - span_b;
+      first = ScanRow(s_ids + off, s_w + off, n, q, has_weights != 0,
+                      combiner, table_div, &div, &id, &gain);
+    } else {
+      first = ScanRow(f.ids + b, has_weights ? f.weights + b : nullptr, n, q,
+                      has_weights != 0, combiner, table_div, &div, &id, &gain);
+    }
+    const int32_t col = ((id + f.col_shift) & kl.ns_mask) + (id & ~kl.ns_mask) +
+                        f.col_offset;
+    const bool ok = id >= 0 && col >= 0 &&
+                    (kl.col_bound <= 0 || static_cast<int64_t>(col) < kl.col_bound);
+    const bool take = ok && first;
+    const K seg_part = static_cast<K>(sl.segment) << kl.col_bits;
+    keys[o] = take ? (seg_part | ColKey<K>(static_cast<uint32_t>(col), kl))
+                   : SentinelKey<K>();
+    if (take) {
+      const uint32_t sample =
+          static_cast<uint32_t>(sl.sample_base + (r - sl.row_start));
+      pay[o] = static_cast<uint64_t>(sample) |
+               (static_cast<uint64_t>(__float_as_uint(gain)) << 32);
+    }
+    view_entry = take && (static_cast<int64_t>(static_cast<uint32_t>(col) >>
+                                               kl.log2ns) < view_rows);
+    bad = !ok;
+  }
+  const uint64_t m = __ballot(bad);
+  if (m != 0 && (threadIdx.x % kWave) == 0) {
+    atomicAdd(reinterpret_cast<unsigned long long*>(&counters[2]),
+              static_cast<unsigned long long>(__popcll(m)));
+  }
+  if (view_counts != nullptr) {
+    const int c = __syncthreads_count(view_entry);
+    if (threadIdx.x == 0) view_counts[blockIdx.x] = static_cast<uint32_t>(c);
+  }
+}
+
+// The sample view from ExtractUnique's arrays: the entries a block counted
+// go, in extraction order, to view_off[block] onwards (positions at or past
+// n are not written); positions from *view_total to n get the unused key.
+// The grid covers max(extraction blocks, n / 256).
+template <typename K>
+__global__ __launch_bounds__(kExtractBlock) void ViewWrite(
+    const K* keys, const uint64_t* pay, const uint32_t* view_off,
+    const uint32_t* view_total, int64_t m, int64_t n, KeyLayout kl,
+    int64_t view_rows, uint32_t unused_key, uint32_t* vkeys,
+    uint64_t* ventries) {
+  __shared__ uint32_t smem[kExtractBlock / kWave + 1];
+  const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (static_cast<int64_t>(blockIdx.x) * blockDim.x < m) {  // uniform
+    bool in_view = false;
+    uint32_t p = 0, local = 0;
+    if (o < m) {
+      const K key = keys[o];
+      if (key != SentinelKey<K>()) {
+        const K col_mask =
+            kl.col_bits >= 64 ? ~K(0) : ((K(1) << kl.col_bits) - 1);
+        DecodeCol<K>(key & col_mask, kl, &p, &local);
+        in_view = static_cast<int64_t>(local) < view_rows;
+      }
+    }
+    uint32_t count;
+    const uint32_t rank =
+        BlockExclusiveScan<uint32_t, kExtractBlock>(in_view ? 1u : 0u, smem,
+                                                    &count);
+    if (in_view) {
+      const int64_t q = static_cast<int64_t>(view_off[blockIdx.x]) + rank;
+      if (q < n) {
+        const uint64_t v = pay[o];
+        vkeys[q] = static_cast<uint32_t>(v);
+        ventries[q] = static_cast<uint64_t>(
+                          static_cast<int64_t>(p) * view_rows + local) |
+                      (v & 0xffffffff00000000ull);
+      }
+    }
+  }
+  if (o < n && o >= static_cast<int64_t>(view_total[0])) {
+    vkeys[o] = unused_key;
+    ventries[o] = 0;
+  }
+}
+
+// First pass source of the sort: the extraction arrays, sentinel keys left
+// out (duplicates and ids outside the table), so that the later passes and
+// the CSR see only the *total entries the first pass took.
+template <typename K>
+struct UniqueSource {
+  const K* keys;
+  const uint64_t* pay;
+  __device__ bool LoadKey(int64_t i, K* k) const {
+    *k = keys[i];
+    return *k != SentinelKey<K>();
+  }
+  __device__ bool Load(int64_t i, K* k, uint64_t* v) const {
+    *k = keys[i];
+    if (*k == SentinelKey<K>()) return false;
+    *v = pay[i];
+    return true;
+  }
+};
+
+constexpr int kGroupItems = 8;  // sorted entries per GroupUnique thread
+
+// Over the *total sorted entries: each bucket's first and last position, and
+// its distinct columns (counted per block in LDS, then one atomic per bucket
+// and block; integer sums, so the order does not matter). col_heads starts
+// at zero.
+template <typename K>
+__global__ __launch_bounds__(256) void GroupUnique(
+    const K* skeys, const uint32_t* total, KeyLayout kl, int num_partitions,
+    int32_t* part_first, int32_t* part_last, int32_t* col_heads) {
+  __shared__ int32_t s_cnt[256];
+  const int64_t n = static_cast<int64_t>(total[0]);
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * 256 * kGroupItems;
+  if (base >= n) return;  // uniform
+  const K col_mask = kl.col_bits >= 64 ? ~K(0) : ((K(1) << kl.col_bits) - 1);
+  auto bucket_of = [&](K key) -> int64_t {
+    uint32_t p, local;
+    DecodeCol<K>(key & col_mask, kl, &p, &local);
+    return static_cast<int64_t>(key >> kl.col_bits) * num_partitions + p;
+  };
+  s_cnt[threadIdx.x] = 0;
+  const int64_t b0 = bucket_of(skeys[base]);
+  __syncthreads();
+  for (int it = 0; it < kGroupItems; ++it) {
+    const int64_t i = base + static_cast<int64_t>(it) * 256 + threadIdx.x;
+    if (i >= n) break;
+    const K key = skeys[i];
+    const int64_t bkt = bucket_of(key);
+    bool new_col = true, new_bucket = true;
+    if (i > 0) {
+      const K pk = skeys[i - 1];
+      new_col = pk != key;
+      new_bucket = new_col && bucket_of(pk) != bkt;
+    }
+    if (new_bucket) part_first[bkt] = static_cast<int32_t>(i);
+    bool last = i + 1 == n;
+    if (!last) {
+      const K nk = skeys[i + 1];
+      last = nk != key && bucket_of(nk) != bkt;
+    }
+    if (last) part_last[bkt] = static_cast<int32_t>(i);
+    if (new_col) {
+      const int64_t rel = bkt - b0;  // >= 0: buckets ascend with the key
+      if (rel < 256) {
+        atomicAdd(&s_cnt[rel], 1);
+      } else {
+        atomicAdd(&col_heads[bkt], 1);
+      }
+    }
+  }
+  __syncthreads();
+  if (s_cnt[threadIdx.x] != 0) {
+    atomicAdd(&col_heads[b0 + threadIdx.x], s_cnt[threadIdx.x]);
+  }
+}
+
+// One thread per sorted entry: the CSR position is the bucket's planned
+// start plus the entry's rank in its bucket (every entry is kept; those
+// past the bucket's room in the static buffer are not written).
+template <typename K>
+__global__ __launch_bounds__(256) void ScatterUnique(
+    const K* skeys, const uint64_t* spay, const uint32_t* total, KeyLayout kl,
+    FillParams fp, int32_t bps, const int32_t* part_first,
+    const FillPlan* plans, int32_t* eid, int32_t* sid, float* gains) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<int64_t>(total[0])) return;
+  const K key = skeys[i];
+  const K col_mask = kl.col_bits >= 64 ? ~K(0) : ((K(1) << kl.col_bits) - 1);
+  uint32_t p, local;
+  DecodeCol<K>(key & col_mask, kl, &p, &local);
+  const int64_t seg = static_cast<int64_t>(key >> kl.col_bits);
+  const int64_t bucket = seg * fp.num_partitions + p;
+  const int64_t k = i - part_first[bucket];
+  const FillPlan pl = plans[bucket];
+  if (k >= pl.fit) return;
+  const int64_t d = seg / fp.segs_per_device;
+  const int64_t pos = d * fp.coo_size + pl.start + k;
+  const uint64_t v = spay[i];
+  eid[pos] = static_cast<int32_t>(local);
+  sid[pos] = static_cast<int32_t>(static_cast<uint32_t>(v) %
+                                  static_cast<uint32_t>(bps));
+  gains[pos] = __uint_as_float(static_cast<uint32_t>(v >> 32));
+}
+
+// ---------------------------------------------------------------------------
 // Host planning.
 // ---------------------------------------------------------------------------
 
@@ -1299,7 +1741,8 @@ struct Plan {
   int64_t coo_size, bps, batch_for_device;
   int64_t total_ids, total_rows;
   std::vector<SliceDesc> slices;
-  bool rows_monotone;
+  bool rows_monotone;  // features' sample rows non-decreasing per segment
+  bool rows_disjoint;  // and no sample row shared by two features
   KeyLayout kl;
   bool wide_keys;
   int row_key_seg_shift;
@@ -1419,6 +1862,7 @@ int MakePlan(const scemb_feature_t* feats, int nf,
   pl->slices.clear();
   int64_t out = 0, rows = 0;
   pl->rows_monotone = true;
+  pl->rows_disjoint = true;
   for (int d = 0; d < L; ++d) {
     for (int s = 0; s < S; ++s) {
       int64_t prev_last = -1;
@@ -1443,6 +1887,7 @@ int MakePlan(const scemb_feature_t* feats, int nf,
         sd.segment = d * S + s;
         if (sd.num_rows > 0) {
           if (sd.sample_base < prev_last) pl->rows_monotone = false;
+          if (sd.sample_base <= prev_last) pl->rows_disjoint = false;
           prev_last = sd.sample_base + sd.num_rows - 1;
           pl->slices.push_back(sd);
         }
@@ -1603,6 +2048,112 @@ int UploadBytes(const void* src, size_t bytes, void* dst,
   return 0;
 }
 
+// What the set-up of one call prepares besides the stats and counters.
+struct SetupTargets {
+  int32_t* part_first;  // [num_buckets] set to -1
+  int32_t* part_last;
+  int64_t num_buckets;
+  int32_t* zero_words;  // [num_zero_words] cleared (may be null)
+  int64_t num_zero_words;
+  SliceDesc* slices;    // descriptor copies
+  FeatureDev* feats;
+  BlockRows* block_rows;  // row bounds of the extraction blocks
+  int64_t extract_blocks;  // 0: nothing to extract
+};
+
+// Checks the feature pointers, then enqueues the set-up: the stats slots
+// before the counters and the counters cleared, partition bounds at -1, the
+// zero words cleared, the slice and feature descriptors copied and the
+// extraction blocks' row bounds computed. One launch when the descriptors
+// fit one chunk of kernel arguments (no pageable host copy, no host
+// synchronisation); otherwise one launch per part.
+int EnqueueSetup(const scemb_feature_t* feats, int nf,
+                 const scemb_preprocess_options_t* o, const Plan& pl,
+                 int64_t counters_off, int32_t* stats, int64_t* counters,
+                 const SetupTargets& t, hipStream_t stream) {
+  std::vector<FeatureDev> fd(nf);
+  for (int f = 0; f < nf; ++f) {
+    fd[f].ids = feats[f].ids;
+    fd[f].weights = o->has_variable_weights ? feats[f].weights : nullptr;
+    fd[f].splits = feats[f].row_splits;
+    fd[f].valency = feats[f].valency;
+    fd[f].col_offset = feats[f].col_offset;
+    fd[f].col_shift = feats[f].col_shift;
+    if (feats[f].nnz > 0 && feats[f].ids == nullptr) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null ids");
+    }
+    if (o->has_variable_weights && feats[f].nnz > 0 &&
+        feats[f].weights == nullptr) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "weights required for every feature of a weighted stack");
+    }
+  }
+  const size_t slice_bytes = sizeof(SliceDesc) * pl.slices.size();
+  const size_t feat_bytes = sizeof(FeatureDev) * nf;
+  const int num_slices = static_cast<int>(pl.slices.size());
+  if (slice_bytes + feat_bytes <= sizeof(UploadChunk)) {
+    UploadChunk c;
+    std::memcpy(c.words, pl.slices.data(), slice_bytes);
+    std::memcpy(reinterpret_cast<char*>(c.words) + slice_bytes, fd.data(),
+                feat_bytes);
+    SetupArgs a;
+    a.stats = stats;
+    a.stats_words = counters_off;
+    a.counters = counters;
+    a.part_first = t.part_first;
+    a.part_last = t.part_last;
+    a.num_buckets = t.num_buckets;
+    a.split_words = t.zero_words;
+    a.num_split_words = t.zero_words != nullptr ? t.num_zero_words : 0;
+    a.slices = reinterpret_cast<uint32_t*>(t.slices);
+    a.feats = reinterpret_cast<uint32_t*>(t.feats);
+    a.slice_words = static_cast<int32_t>(slice_bytes / 4);
+    a.feat_words = static_cast<int32_t>(feat_bytes / 4);
+    a.num_slices = num_slices;
+    a.total_ids = pl.total_ids;
+    a.extract_blocks = t.extract_blocks;
+    a.block_rows = t.block_rows;
+    const int64_t work = std::max<int64_t>(
+        {int64_t{kNumCounters}, counters_off, t.num_buckets,
+         a.num_split_words,
+         static_cast<int64_t>((slice_bytes + feat_bytes) / 4),
+         a.extract_blocks});
+    hipLaunchKernelGGL(SetupKernel, dim3(CeilDiv(work, 256)), dim3(256), 0,
+                       stream, c, a);
+    SCEMB_LAUNCH_CHECK();
+    return 0;
+  }
+  hipLaunchKernelGGL(FillI32, dim3(CeilDiv(counters_off, 256)), dim3(256), 0,
+                     stream, stats, counters_off, 0);
+  SCEMB_LAUNCH_CHECK();
+  hipLaunchKernelGGL(ZeroI64, dim3(1), dim3(64), 0, stream, counters,
+                     kNumCounters);
+  SCEMB_LAUNCH_CHECK();
+  int st = UploadBytes(pl.slices.data(), slice_bytes, t.slices, stream);
+  if (st != 0) return st;
+  st = UploadBytes(fd.data(), feat_bytes, t.feats, stream);
+  if (st != 0) return st;
+  hipLaunchKernelGGL(FillI32, dim3(CeilDiv(t.num_buckets, 256)), dim3(256), 0,
+                     stream, t.part_first, t.num_buckets, -1);
+  SCEMB_LAUNCH_CHECK();
+  hipLaunchKernelGGL(FillI32, dim3(CeilDiv(t.num_buckets, 256)), dim3(256), 0,
+                     stream, t.part_last, t.num_buckets, -1);
+  SCEMB_LAUNCH_CHECK();
+  if (t.zero_words != nullptr && t.num_zero_words > 0) {
+    hipLaunchKernelGGL(FillI32, dim3(CeilDiv(t.num_zero_words, 256)),
+                       dim3(256), 0, stream, t.zero_words, t.num_zero_words,
+                       0);
+    SCEMB_LAUNCH_CHECK();
+  }
+  if (t.extract_blocks > 0) {
+    hipLaunchKernelGGL(BlockBounds, dim3(CeilDiv(t.extract_blocks, 256)),
+                       dim3(256), 0, stream, t.slices, num_slices, t.feats,
+                       pl.total_ids, t.extract_blocks, t.block_rows);
+    SCEMB_LAUNCH_CHECK();
+  }
+  return 0;
+}
+
 template <typename K>
 int RunPipeline(const scemb_feature_t* feats, int nf,
                 const scemb_preprocess_options_t* o,
@@ -1698,85 +2249,17 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
     if ((reinterpret_cast<uintptr_t>(counters) & 7u) != 0) {
       return Fail(SCEMB_ERR_INVALID_ARGUMENT, "stats buffer must be 8-byte aligned");
     }
-    std::vector<FeatureDev> fd(nf);
-    for (int f = 0; f < nf; ++f) {
-      fd[f].ids = feats[f].ids;
-      fd[f].weights = o->has_variable_weights ? feats[f].weights : nullptr;
-      fd[f].splits = feats[f].row_splits;
-      fd[f].valency = feats[f].valency;
-      fd[f].col_offset = feats[f].col_offset;
-      fd[f].col_shift = feats[f].col_shift;
-      if (feats[f].nnz > 0 && feats[f].ids == nullptr) {
-        return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null ids");
-      }
-      if (o->has_variable_weights && feats[f].nnz > 0 &&
-          feats[f].weights == nullptr) {
-        return Fail(SCEMB_ERR_INVALID_ARGUMENT,
-                    "weights required for every feature of a weighted stack");
-      }
-    }
-    // The slice and feature descriptors travel as kernel arguments: no
-    // pageable host copy, no host synchronisation.
-    bool bounds_done = false;  // BlockBounds folded into the set-up
-    const size_t slice_bytes = sizeof(SliceDesc) * pl.slices.size();
-    const size_t feat_bytes = sizeof(FeatureDev) * nf;
-    const int64_t split_words =
-        split_counts != nullptr ? split_cells * (sizeof(BucketStats) / 4) : 0;
-    if (slice_bytes + feat_bytes <= sizeof(UploadChunk)) {
-      UploadChunk c;
-      std::memcpy(c.words, pl.slices.data(), slice_bytes);
-      std::memcpy(reinterpret_cast<char*>(c.words) + slice_bytes, fd.data(),
-                  feat_bytes);
-      SetupArgs a;
-      a.stats = out->stats;
-      a.stats_words = counters_off;
-      a.counters = counters;
-      a.part_first = b.part_first;
-      a.part_last = b.part_last;
-      a.num_buckets = num_buckets;
-      a.split_words = reinterpret_cast<int32_t*>(split_counts);
-      a.num_split_words = split_words;
-      a.slices = reinterpret_cast<uint32_t*>(b.slices);
-      a.feats = reinterpret_cast<uint32_t*>(b.feats);
-      a.slice_words = static_cast<int32_t>(slice_bytes / 4);
-      a.feat_words = static_cast<int32_t>(feat_bytes / 4);
-      a.num_slices = static_cast<int32_t>(pl.slices.size());
-      a.total_ids = M;
-      a.extract_blocks = M > 0 ? extract_blocks : 0;
-      a.block_rows = b.block_rows;
-      bounds_done = true;
-      const int64_t work = std::max<int64_t>(
-          {int64_t{kNumCounters}, counters_off, num_buckets, split_words,
-           static_cast<int64_t>((slice_bytes + feat_bytes) / 4),
-           a.extract_blocks});
-      hipLaunchKernelGGL(SetupKernel, dim3(CeilDiv(work, 256)), dim3(256), 0,
-                         stream, c, a);
-      SCEMB_LAUNCH_CHECK();
-    } else {
-      hipLaunchKernelGGL(FillI32, dim3(CeilDiv(counters_off, 256)), dim3(256),
-                         0, stream, out->stats, counters_off, 0);
-      SCEMB_LAUNCH_CHECK();
-      hipLaunchKernelGGL(ZeroI64, dim3(1), dim3(64), 0, stream, counters,
-                         kNumCounters);
-      SCEMB_LAUNCH_CHECK();
-      int st = UploadBytes(pl.slices.data(), slice_bytes, b.slices, stream);
-      if (st != 0) return st;
-      st = UploadBytes(fd.data(), feat_bytes, b.feats, stream);
-      if (st != 0) return st;
-      hipLaunchKernelGGL(FillI32, dim3(CeilDiv(num_buckets, 256)), dim3(256),
-                         0, stream, b.part_first, num_buckets, -1);
-      SCEMB_LAUNCH_CHECK();
-      hipLaunchKernelGGL(FillI32, dim3(CeilDiv(num_buckets, 256)), dim3(256),
-                         0, stream, b.part_last, num_buckets, -1);
-      SCEMB_LAUNCH_CHECK();
-      if (split_counts != nullptr) {
-        hipLaunchKernelGGL(FillI32, dim3(CeilDiv(split_words, 256)),
-                           dim3(256), 0, stream,
-                           reinterpret_cast<int32_t*>(split_counts),
-                           split_words, 0);
-        SCEMB_LAUNCH_CHECK();
-      }
-    }
+    const SetupTargets tg{b.part_first, b.part_last, num_buckets,
+                          reinterpret_cast<int32_t*>(split_counts),
+                          split_counts != nullptr
+                              ? split_cells * static_cast<int64_t>(
+                                                  sizeof(BucketStats) / 4)
+                              : 0,
+                          b.slices, b.feats, b.block_rows,
+                          M > 0 ? extract_blocks : 0};
+    const int su = EnqueueSetup(feats, nf, o, pl, counters_off, out->stats,
+                                counters, tg, stream);
+    if (su != 0) return su;
     if (divisors != nullptr && pl.total_rows > 0) {
       hipLaunchKernelGGL(RowDivisors, dim3(CeilDiv(pl.total_rows, 256)),
                          dim3(256), 0, stream, b.slices,
@@ -1786,12 +2269,6 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
     }
     if (M > 0) {
       const int num_slices = static_cast<int>(pl.slices.size());
-      if (!bounds_done) {
-        hipLaunchKernelGGL(BlockBounds, dim3(CeilDiv(extract_blocks, 256)),
-                           dim3(256), 0, stream, b.slices, num_slices,
-                           b.feats, M, extract_blocks, b.block_rows);
-        SCEMB_LAUNCH_CHECK();
-      }
       hipLaunchKernelGGL((ExtractIds<K>), dim3(extract_blocks),
                          dim3(kExtractBlock), 0, stream, b.slices, num_slices,
                          b.feats, b.block_rows, M, o->combiner,
@@ -1883,7 +2360,8 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   // Without minibatching the fill plan's single block reduces the bucket
   // stats first (one launch less).
   BucketReduceArgs bra{b.part_first, b.part_last, b.flags, b.scan,
-                       b.keep_scan, minibatching ? 0 : num_buckets, b.bstats};
+                       b.keep_scan, minibatching ? 0 : num_buckets, b.bstats,
+                       nullptr};
   if (minibatching) {
     hipLaunchKernelGGL(BucketReduce, dim3(CeilDiv(num_buckets, 256)),
                        dim3(256), 0, stream, b.part_first, b.part_last,
@@ -1981,7 +2459,7 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   hipLaunchKernelGGL(WritePadding, dim3(CeilDiv(num_buckets * kAlign, 256)),
                      dim3(256), 0, stream, b.plans, num_buckets, fp,
                      out->embedding_ids, out->sample_ids, out->gains,
-                     M > 0 ? b.totals : nullptr, counters);
+                     M > 0 ? b.totals : nullptr, nullptr, counters);
   SCEMB_LAUNCH_CHECK();
   if (view.entry != nullptr) {
     hipLaunchKernelGGL(MarkEntries, dim3(CeilDiv(M + 1, 256)), dim3(256), 0,
@@ -2003,6 +2481,215 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   return 0;
 }
 
+// The route of grouping at extraction: set-up, ExtractUnique, the sample
+// view (a scan of the blocks' counts, then ViewWrite), a stable LSD radix
+// sort of the distinct (row, column) entries on the key, whose first pass
+// leaves out the sentinel keys, then GroupUnique, the fill plan,
+// ScatterUnique and the padding. Same outputs as RunPipeline for the calls
+// Preprocess routes here.
+template <typename K>
+int RunUniquePipeline(const scemb_feature_t* feats, int nf,
+                      const scemb_preprocess_options_t* o,
+                      const scemb_preprocess_output_t* out, const Plan& pl,
+                      Arena& ws, hipStream_t stream) {
+  using radix::kSortBlock;
+  using radix::kSortTile;
+  using Arr = radix::ArraySource<K, uint64_t>;
+  using Sink = radix::ArraySink<K, uint64_t>;
+  const int64_t M = pl.total_ids;
+  const int64_t num_buckets = static_cast<int64_t>(pl.L) * pl.S * pl.NS;
+  const int64_t extract_blocks = CeilDiv(M, kExtractBlock);
+  const bool view = o->build_sample_view != 0;
+  K* keys = ws.Take<K>(M);
+  K* keys_alt = ws.Take<K>(M);
+  uint64_t* pay = ws.Take<uint64_t>(M);
+  uint64_t* pay_alt = ws.Take<uint64_t>(M);
+  BlockRows* block_rows = ws.Take<BlockRows>(extract_blocks);
+  uint32_t* view_off = view ? ws.Take<uint32_t>(extract_blocks) : nullptr;
+  uint32_t* view_total = view ? ws.Take<uint32_t>(1) : nullptr;
+  int32_t* part_first = ws.Take<int32_t>(num_buckets);
+  int32_t* part_last = ws.Take<int32_t>(num_buckets);
+  int32_t* col_heads = ws.Take<int32_t>(num_buckets);
+  BucketStats* bstats = ws.Take<BucketStats>(num_buckets);
+  FillPlan* plans = ws.Take<FillPlan>(num_buckets);
+  SliceDesc* slices =
+      ws.Take<SliceDesc>(static_cast<int64_t>(pl.slices.size()));
+  FeatureDev* fdev = ws.Take<FeatureDev>(nf);
+  const int key_bits = std::max(1, pl.kl.col_bits + pl.kl.seg_bits);
+  const radix::DigitPlan dp = radix::PlanDigits(key_bits);
+  const int64_t tiles = CeilDiv(M, kSortTile);
+  uint32_t* hist = ws.Take<uint32_t>(tiles * (int64_t{1} << dp.digit));
+  uint32_t* totals = ws.Take<uint32_t>(dp.passes);
+  if (view) {
+    if (pl.L != 1 || pl.G != 1) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "the sample view needs one local and one global device");
+    }
+    if (o->table_rows <= 0 || o->table_rows % pl.NS != 0) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                  "table_rows must be a positive multiple of the partitions");
+    }
+  }
+  const int64_t view_rows = view ? o->table_rows / pl.NS : 0;
+  const bool measuring = ws.measuring();
+  const int64_t counters_off = RoundUp(2 * static_cast<int64_t>(pl.L) * pl.NS +
+                                       static_cast<int64_t>(pl.L) * pl.S, 2);
+  const int num_slices = static_cast<int>(pl.slices.size());
+  int64_t* counters = nullptr;
+  if (!measuring) {
+    if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+    if (out == nullptr || out->row_pointers == nullptr || out->stats == nullptr ||
+        out->embedding_ids == nullptr || out->sample_ids == nullptr ||
+        out->gains == nullptr) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null output buffer");
+    }
+    if (view && (out->view_keys == nullptr || out->view_entries == nullptr)) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null sample view buffer");
+    }
+    counters = reinterpret_cast<int64_t*>(out->stats + counters_off);
+    if ((reinterpret_cast<uintptr_t>(counters) & 7u) != 0) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "stats buffer must be 8-byte aligned");
+    }
+    const SetupTargets tg{part_first, part_last, num_buckets,  col_heads,
+                          num_buckets, slices,    fdev,        block_rows,
+                          M > 0 ? extract_blocks : 0};
+    const int su = EnqueueSetup(feats, nf, o, pl, counters_off, out->stats,
+                                counters, tg, stream);
+    if (su != 0) return su;
+    if (M > 0) {
+      hipLaunchKernelGGL((ExtractUnique<K>), dim3(extract_blocks),
+                         dim3(kExtractBlock), 0, stream, slices, num_slices,
+                         fdev, block_rows, M, o->combiner,
+                         o->has_variable_weights ? 1 : 0, pl.kl, view_rows,
+                         keys, pay, view_off, counters);
+      SCEMB_LAUNCH_CHECK();
+    }
+  }
+  int st = 0;
+  if (view) {
+    st = ExclusiveScan<uint32_t>(view_off, view_off, extract_blocks,
+                                 view_total, ws, stream);
+    if (st != 0) return st;
+    const int64_t n = pl.coo_size;
+    const int64_t grid = std::max(extract_blocks, CeilDiv(n, kExtractBlock));
+    if (!measuring && grid > 0) {
+      hipLaunchKernelGGL((ViewWrite<K>), dim3(grid), dim3(kExtractBlock), 0,
+                         stream, keys, pay, view_off, view_total, M, n, pl.kl,
+                         view_rows, static_cast<uint32_t>(pl.batch_for_device),
+                         out->view_keys, out->view_entries);
+      SCEMB_LAUNCH_CHECK();
+    }
+  }
+  // Sort. Pass p writes (keys_alt, pay_alt) when p is even.
+  const UniqueSource<K> first_src{keys, pay};
+  for (int pass = 0; pass < dp.passes; ++pass) {
+    const int shift = pass * dp.digit;
+    const int pbits = key_bits - shift < dp.digit ? key_bits - shift : dp.digit;
+    const uint32_t mask = (1u << pbits) - 1u;
+    const int64_t cells = tiles * (int64_t{1} << pbits);
+    const bool even = pass % 2 == 0;
+    const Arr arr{even ? keys : keys_alt, even ? pay : pay_alt};
+    const Sink sink{even ? keys_alt : keys, even ? pay_alt : pay};
+    if (!measuring && M > 0) {
+      if (pass == 0) {
+        hipLaunchKernelGGL((radix::RadixHistogramK<K, UniqueSource<K>>),
+                           dim3(tiles), dim3(kSortBlock), 0, stream, first_src,
+                           M, nullptr, shift, mask, tiles, hist);
+      } else {
+        hipLaunchKernelGGL((radix::RadixHistogramK<K, Arr>), dim3(tiles),
+                           dim3(kSortBlock), 0, stream, arr, M, totals, shift,
+                           mask, tiles, hist);
+      }
+      SCEMB_LAUNCH_CHECK();
+    }
+    st = ExclusiveScan<uint32_t>(hist, hist, cells, totals + pass, ws, stream);
+    if (st != 0) return st;
+    if (!measuring && M > 0) {
+      if (pass == 0) {
+        hipLaunchKernelGGL(
+            (radix::RadixScatterK<K, uint64_t, UniqueSource<K>, Sink>),
+            dim3(tiles), dim3(kSortBlock), 0, stream, first_src, sink, M,
+            nullptr, shift, mask, pbits, tiles, hist, totals + pass, false);
+      } else {
+        hipLaunchKernelGGL((radix::RadixScatterK<K, uint64_t, Arr, Sink>),
+                           dim3(tiles), dim3(kSortBlock), 0, stream, arr, sink,
+                           M, totals, shift, mask, pbits, tiles, hist,
+                           totals + pass, false);
+      }
+      SCEMB_LAUNCH_CHECK();
+    }
+  }
+  if (measuring) return 0;
+  if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+  const bool odd = dp.passes % 2 == 1;
+  const K* skeys = odd ? keys_alt : keys;
+  const uint64_t* spay = odd ? pay_alt : pay;
+  if (M > 0) {
+    hipLaunchKernelGGL((GroupUnique<K>),
+                       dim3(CeilDiv(M, int64_t{256} * kGroupItems)), dim3(256),
+                       0, stream, skeys, totals, pl.kl, pl.NS, part_first,
+                       part_last, col_heads);
+    SCEMB_LAUNCH_CHECK();
+  }
+  FillParams fp;
+  fp.local_devices = pl.L;
+  fp.segs_per_device = pl.S;
+  fp.num_partitions = pl.NS;
+  fp.rp_per_segment = pl.rp_per_seg;
+  fp.coo_size = pl.coo_size;
+  fp.max_ids = o->max_ids_per_partition;
+  fp.max_unique = o->max_unique_ids_per_partition;
+  fp.allow_dropping = 0;
+  fp.mb_bits = 0;
+  fp.absolute = 0;
+  fp.num_minibatches = 1;
+  for (int bkt = 0; bkt < kMaxMinibatches; ++bkt) fp.minibatch_of[bkt] = 0;
+  const BucketReduceArgs bra{part_first, part_last, nullptr,   nullptr,
+                             nullptr,    num_buckets, bstats, col_heads};
+  hipLaunchKernelGGL(FillPlanKernel, dim3(1), dim3(256), 0, stream, bstats, fp,
+                     out->row_pointers, plans, out->stats,
+                     out->stats + static_cast<int64_t>(pl.L) * pl.NS,
+                     out->stats + 2 * static_cast<int64_t>(pl.L) * pl.NS,
+                     counters, bra);
+  SCEMB_LAUNCH_CHECK();
+  if (M > 0) {
+    hipLaunchKernelGGL((ScatterUnique<K>), dim3(CeilDiv(M, 256)), dim3(256), 0,
+                       stream, skeys, spay, totals, pl.kl, fp,
+                       static_cast<int32_t>(pl.bps), part_first, plans,
+                       out->embedding_ids, out->sample_ids, out->gains);
+    SCEMB_LAUNCH_CHECK();
+  }
+  hipLaunchKernelGGL(WritePadding, dim3(CeilDiv(num_buckets * kAlign, 256)),
+                     dim3(256), 0, stream, plans, num_buckets, fp,
+                     out->embedding_ids, out->sample_ids, out->gains, nullptr,
+                     totals, counters);
+  SCEMB_LAUNCH_CHECK();
+  return 0;
+}
+
+// The most ids of one row over the stack's features: a dense feature's
+// valency, else the caller's hint, else a pass over the host row splits (the
+// caller's, or the copy MakePlan made of device-only ones).
+int64_t MaxRowLength(const scemb_feature_t* feats, int nf,
+                     const std::vector<std::vector<int64_t>>& cache) {
+  int64_t most = 0;
+  for (int f = 0; f < nf; ++f) {
+    const scemb_feature_t& ft = feats[f];
+    if (ft.row_splits == nullptr) {
+      most = std::max<int64_t>(most, ft.valency);
+    } else if (ft.max_row_length > 0) {
+      most = std::max<int64_t>(most, ft.max_row_length);
+    } else {
+      const int64_t* sp = ft.row_splits_host != nullptr ? ft.row_splits_host
+                                                        : cache[f].data();
+      for (int64_t r = 0; r < ft.num_rows; ++r) {
+        most = std::max<int64_t>(most, sp[r + 1] - sp[r]);
+      }
+    }
+  }
+  return most;
+}
+
 int Preprocess(const scemb_feature_t* feats, int nf,
                const scemb_preprocess_options_t* o,
                const scemb_preprocess_output_t* out, Arena& ws,
@@ -2011,6 +2698,25 @@ int Preprocess(const scemb_feature_t* feats, int nf,
   std::vector<std::vector<int64_t>> cache;
   int st = MakePlan(feats, nf, o, &pl, &cache);
   if (st != 0) return st;
+  // Grouping at extraction needs every (row, column) pair to come from one
+  // input row (disjoint sample rows) and keeps every entry (no id dropping,
+  // no minibatching). With the sample view it also needs a static buffer
+  // that holds any input within the limits: the view is written before the
+  // fill plan and so cannot leave out entries the buffer has no room for.
+  // Its duplicate scan costs the square of the row length, so rows longer
+  // than the LDS staging go the other way.
+  const bool at_extraction =
+      (o->flags & SCEMB_PREPROCESS_GROUP_AFTER_SORT) == 0 &&
+      !o->enable_minibatching && !o->allow_id_dropping && pl.rows_disjoint &&
+      (!o->build_sample_view ||
+       pl.coo_size >= RoundUp(o->max_ids_per_partition, kAlign) *
+                          static_cast<int64_t>(pl.S) * pl.NS) &&
+      MaxRowLength(feats, nf, cache) <= kDedupMaxRow;
+  if (at_extraction) {
+    return pl.wide_keys
+               ? RunUniquePipeline<uint64_t>(feats, nf, o, out, pl, ws, stream)
+               : RunUniquePipeline<uint32_t>(feats, nf, o, out, pl, ws, stream);
+  }
   if (pl.wide_keys) {
     return RunPipeline<uint64_t>(feats, nf, o, out, pl, ws, stream);
   }
@@ -2061,6 +2767,27 @@ int scemb_preprocess_stacked_table(const scemb_feature_t* features,
   const int rc = Preprocess(features, num_features, o, out, ws, s);
   ProfileEnd(prof, s);
   return rc;
+}
+
+int scemb_check_row_splits(const int64_t* row_splits, int64_t num_rows,
+                           int64_t nnz, int64_t* max_row_length) {
+  if (row_splits == nullptr || num_rows < 0 || max_row_length == nullptr) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null row splits");
+  }
+  int64_t most = 0;
+  bool down = false;
+  for (int64_t r = 0; r < num_rows; ++r) {
+    const int64_t len = row_splits[r + 1] - row_splits[r];
+    down |= len < 0;
+    most = len > most ? len : most;
+  }
+  if (row_splits[0] != 0 || row_splits[num_rows] != nnz || down) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "row_splits must start at 0, be non-decreasing and end at the "
+                "number of values.");
+  }
+  *max_row_length = most;
+  return 0;
 }
 
 int64_t scemb_compute_theoretical_max_coo_buffer_size(

@@ -68,6 +68,7 @@ EXPORTED_SYMBOLS = (
     "scemb_preprocess_stats_counters_offset",
     "scemb_preprocess_workspace_size",
     "scemb_preprocess_stacked_table",
+    "scemb_check_row_splits",
     "scemb_compute_theoretical_max_coo_buffer_size",
     "scemb_compute_coo_buffer_size_per_device",
     "scemb_compute_row_pointers_size_per_device",
@@ -183,6 +184,7 @@ class Feature(ctypes.Structure):
       ("row_offset", ctypes.c_int32),
       ("col_offset", ctypes.c_int32),
       ("col_shift", ctypes.c_int32),
+      ("max_row_length", ctypes.c_int64),
   ]
 
 
@@ -202,9 +204,14 @@ class PreprocessOptions(ctypes.Structure):
       ("enable_minibatching", ctypes.c_int32),
       ("table_rows", ctypes.c_int64),
       ("minibatching_pass", ctypes.c_int32),
-      ("reserved", ctypes.c_int32),
+      ("flags", ctypes.c_int32),
       ("minibatching_split", ctypes.c_uint64),
   ]
+
+
+# PreprocessOptions.flags: merge duplicates after the sort even where the
+# library would merge them at extraction (both give the same outputs).
+PREPROCESS_GROUP_AFTER_SORT = 1
 
 
 class PreprocessOutput(ctypes.Structure):
@@ -301,6 +308,9 @@ def load_library() -> ctypes.CDLL:
     lib.scemb_preprocess_stacked_table.argtypes = [
         ctypes.POINTER(Feature), i32, opts_p, ctypes.POINTER(PreprocessOutput),
         vp, sz, vp]
+    lib.scemb_check_row_splits.restype = ctypes.c_int
+    lib.scemb_check_row_splits.argtypes = [vp, i64, i64,
+                                           ctypes.POINTER(ctypes.c_int64)]
     lib.scemb_compute_theoretical_max_coo_buffer_size.restype = i64
     lib.scemb_compute_theoretical_max_coo_buffer_size.argtypes = [i32, i32,
                                                                   i32, i32]

@@ -25,6 +25,9 @@ import numpy as np
 from jax_tpu_embedding.sparsecore import _native
 
 _COMBINERS = {"sum": 0, "mean": 1, "sqrtn": 2}
+# PreprocessOptions.flags of every call (_native.PREPROCESS_*); 0 lets the
+# library pick the grouping route.
+PREPROCESS_FLAGS = 0
 
 
 class ShardingStrategy(enum.IntEnum):
@@ -171,7 +174,14 @@ class _DeviceFeature:
   nnz: int
   valency: int
   max_id: int | None  # known when the input came from host memory
-  one_id_per_row: bool = True  # no row of a ragged input holds two ids
+  max_row_length: int = 0  # most ids of one row (0: not known)
+
+  @property
+  def one_id_per_row(self) -> bool:
+    """No row holds two ids."""
+    if self.splits_host is None:
+      return self.valency <= 1
+    return self.max_row_length <= 1
 
 
 def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
@@ -205,16 +215,13 @@ def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
     # Ragged tensor (tf.RaggedTensor-like: flat values + row splits), the
     # RaggedTensorInputBatch input of ragged_tensor_input_batch.h:68-127.
     vals = feature.values
-    splits = np.asarray(feature.row_splits, np.int64).reshape(-1)
+    splits = np.ascontiguousarray(feature.row_splits,
+                                  dtype=np.int64).reshape(-1)
     if isinstance(vals, t.Tensor):
       vals = vals.reshape(-1)
     else:
       vals = np.ascontiguousarray(np.asarray(vals), dtype=np.int32).reshape(-1)
-    lens = np.diff(splits)
-    if splits.size == 0 or splits[0] != 0 or splits[-1] != vals.shape[0] or (
-        lens.size and lens.min() < 0):
-      raise ValueError("row_splits must start at 0, be non-decreasing and "
-                       "end at the number of values.")
+    max_len = _check_row_splits(splits, int(vals.shape[0]))
     w = None
     if weights is not None:
       wv = getattr(weights, "values", weights)
@@ -229,7 +236,7 @@ def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
       max_id = int(vals.max())
     return _DeviceFeature(ids, w, on_device(splits, t.int64),
                           splits, splits.size - 1, int(splits[-1]), 0, max_id,
-                          _one_id_per_row(lens, int(splits[-1])))
+                          max_len)
   arr = feature if isinstance(feature, np.ndarray) else np.asarray(
       feature, dtype=object)
   if arr.dtype != object and arr.ndim == 2:
@@ -272,12 +279,22 @@ def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
       on_device(ids_np, t.int32),
       None if w_np is None else on_device(w_np, t.float32),
       on_device(splits, t.int64), splits, len(rows),
-      int(splits[-1]), 0, max_id, _one_id_per_row(lens, int(splits[-1])))
+      int(splits[-1]), 0, max_id, int(lens.max()) if lens.size else 0)
 
 
-def _one_id_per_row(lens: np.ndarray, nnz: int) -> bool:
-  """Whether no row length exceeds 1 (more ids than rows settles it)."""
-  return nnz <= lens.size and (lens.size == 0 or int(lens.max()) <= 1)
+def _check_row_splits(splits: np.ndarray, nnz: int) -> int:
+  """The most ids of one row; raises ValueError unless the row splits start
+  at 0, do not decrease and end at `nnz` (one pass in the library)."""
+  if splits.size == 0:
+    raise ValueError("row_splits must start at 0, be non-decreasing and "
+                     "end at the number of values.")
+  out = ctypes.c_int64(0)
+  rc = _native.load_library().scemb_check_row_splits(
+      splits.ctypes.data, splits.size - 1, nnz, ctypes.byref(out))
+  if rc != 0:
+    raise ValueError("row_splits must start at 0, be non-decreasing and "
+                     "end at the number of values.")
+  return int(out.value)
 
 
 def _resolve_feature(f: _DeviceFeature) -> _DeviceFeature:
@@ -320,13 +337,14 @@ def _preprocess_stack(feats, metas, *, local_device_count,
       int(bool(allow_id_dropping)), int(bool(has_weights)), c, bound,
       int(bool(build_view)), int(bool(enable_minibatching)),
       metas[0].stack_vocab_size // global_device_count,
-      int(minibatching_pass), 0, int(minibatching_split))
+      int(minibatching_pass), PREPROCESS_FLAGS, int(minibatching_split))
   structs = (_native.Feature * len(feats))()
   for i, (f, m) in enumerate(zip(feats, metas)):
     structs[i] = _native.Feature(
         _native.ptr(f.ids), _native.ptr(f.weights), _native.ptr(f.splits),
         None if f.splits_host is None else f.splits_host.ctypes.data,
-        f.num_rows, f.nnz, f.valency, m.row_offset, m.col_offset, m.col_shift)
+        f.num_rows, f.nnz, f.valency, m.row_offset, m.col_offset, m.col_shift,
+        f.max_row_length)
   need = lib.scemb_preprocess_workspace_size(structs, len(feats),
                                              ctypes.byref(opts))
   if need == 0:

@@ -114,17 +114,63 @@ def test_primitive_validation_messages():
 
 
 def _sizing_call(build_view, local_devices, table_rows=1024,
-                 enable_minibatching=0, minibatching_pass=0, split=0):
-  """scemb_preprocess_workspace_size for one 64 x 2 dense feature (sizing
-  only: no device memory is touched)."""
+                 enable_minibatching=0, minibatching_pass=0, split=0,
+                 flags=0, valency=2, allow_dropping=0):
+  """scemb_preprocess_workspace_size for one 64 x `valency` dense feature
+  (sizing only: no device memory is touched)."""
   lib = _native.load_library()
   feat = (_native.Feature * 1)()
-  feat[0] = _native.Feature(None, None, None, None, 64, 128, 2, 0, 0, 0)
+  feat[0] = _native.Feature(None, None, None, None, 64, 64 * valency, valency,
+                            0, 0, 0)
   opts = _native.PreprocessOptions(local_devices, local_devices, 1, 0, 512,
-                                   512, 0, 0, 512, 1024, int(build_view),
-                                   enable_minibatching, table_rows,
-                                   minibatching_pass, 0, split)
+                                   512, allow_dropping, 0, 512, 1024,
+                                   int(build_view), enable_minibatching,
+                                   table_rows, minibatching_pass, flags, split)
   return int(lib.scemb_preprocess_workspace_size(feat, 1, ctypes.byref(opts)))
+
+
+def test_grouping_route_selection():
+  """The route that merges duplicates at extraction needs less workspace
+  than the after-sort route; the flag, id dropping, minibatching and rows
+  longer than 896 ids each select the after-sort route."""
+  at_extraction = _sizing_call(False, 1)
+  after_sort = _sizing_call(False, 1, flags=_native.PREPROCESS_GROUP_AFTER_SORT)
+  assert 0 < at_extraction < after_sort
+  assert _sizing_call(False, 1, allow_dropping=1) == after_sort
+  assert _sizing_call(True, 1) < _sizing_call(
+      True, 1, flags=_native.PREPROCESS_GROUP_AFTER_SORT)
+  long_rows = _sizing_call(False, 1, valency=897)
+  assert long_rows == _sizing_call(
+      False, 1, valency=897, flags=_native.PREPROCESS_GROUP_AFTER_SORT)
+  assert _sizing_call(False, 1, valency=896) < _sizing_call(
+      False, 1, valency=896, flags=_native.PREPROCESS_GROUP_AFTER_SORT)
+
+
+def test_check_row_splits():
+  """One pass over host row splits: the longest row, or the reference's
+  RaggedTensorInputBatch contract violated (start 0, non-decreasing, end at
+  the number of values)."""
+  lib = _native.load_library()
+
+  def check(splits, nnz):
+    a = np.ascontiguousarray(splits, dtype=np.int64)
+    out = ctypes.c_int64(-1)
+    rc = lib.scemb_check_row_splits(a.ctypes.data, a.size - 1, nnz,
+                                    ctypes.byref(out))
+    return rc, out.value
+
+  assert check([0, 2, 2, 7, 8], 8) == (0, 5)
+  assert check([0], 0) == (0, 0)
+  assert check([0, 0, 0], 0) == (0, 0)
+  assert check([1, 2, 3], 3)[0] == _native.SCEMB_ERR_INVALID_ARGUMENT
+  assert check([0, 3, 2, 4], 4)[0] == _native.SCEMB_ERR_INVALID_ARGUMENT
+  assert b"non-decreasing" in lib.scemb_last_error()
+  assert check([0, 2, 4], 5)[0] == _native.SCEMB_ERR_INVALID_ARGUMENT
+  assert pip._check_row_splits(np.array([0, 1, 4], np.int64), 4) == 3  # pylint: disable=protected-access
+  with pytest.raises(ValueError, match="non-decreasing"):
+    pip._check_row_splits(np.array([0, 4, 1], np.int64), 1)  # pylint: disable=protected-access
+  with pytest.raises(ValueError, match="non-decreasing"):
+    pip._check_row_splits(np.zeros(0, np.int64), 0)  # pylint: disable=protected-access
 
 
 def test_preprocess_minibatching_options():
