@@ -1427,32 +1427,88 @@ __device__ __forceinline__ bool ScanRow(const T* ids, const W* w, int n, int q,
   return before == 0;
 }
 
+// LDS hash set of a block's staged rows: slot = (row start << 11) | position
+// of the first copy of an id in that row (both relative to the staged span,
+// so below 2^11), or kSlotEmpty; a slot's key (row start, id) never changes
+// once claimed, only its position can drop (atomicMin). A 16-bit count per
+// slot tracks the copies.
+constexpr int kDedupSlots = kDedupStage;
+constexpr uint32_t kSlotEmpty = 0xffffffffu;
+static_assert(kDedupStage <= 2048, "positions must fit 11 bits");
+
+__device__ __forceinline__ uint32_t DedupHash(int32_t id, uint32_t row_start) {
+  const uint32_t h = static_cast<uint32_t>(id) * 0x9e3779b1u ^
+                     (row_start + 0x7f4a7c15u) * 0x85ebca77u;
+  return (h ^ (h >> 15)) & (kDedupSlots - 1);
+}
+
+// Inserts position x (row start rs, id) and counts the copy.
+__device__ __forceinline__ void DedupInsert(uint32_t* table, uint32_t* counts,
+                                            const int32_t* s_ids, uint32_t rs,
+                                            uint32_t x, int32_t id) {
+  const uint32_t mine = (rs << 11) | x;
+  uint32_t h = DedupHash(id, rs);
+  for (;;) {
+    uint32_t cur = table[h];
+    if (cur == kSlotEmpty) {
+      cur = atomicCAS(&table[h], kSlotEmpty, mine);
+      if (cur == kSlotEmpty) break;
+    }
+    if ((cur >> 11) == rs && s_ids[cur & 2047u] == id) {
+      atomicMin(&table[h], mine);
+      break;
+    }
+    h = (h + 1) & (kDedupSlots - 1);
+  }
+  atomicAdd(&counts[h >> 1], 1u << ((h & 1u) * 16));
+}
+
+// The slot of (row start rs, id), which is in the set.
+__device__ __forceinline__ uint32_t DedupFind(const uint32_t* table,
+                                              const int32_t* s_ids,
+                                              uint32_t rs, int32_t id) {
+  uint32_t h = DedupHash(id, rs);
+  for (;;) {
+    const uint32_t cur = table[h];
+    if ((cur >> 11) == rs && s_ids[cur & 2047u] == id) return h;
+    h = (h + 1) & (kDedupSlots - 1);
+  }
+}
+
 // One thread per extracted id, laid out as ExtractIds. The block stages the
-// ids (and weights) of the rows it spans in LDS and, for a weighted mean or
-// sqrtn, each row's divisor (one thread per row, the sequential sums of
-// RowDivisors). An id then scans its row: an earlier copy makes it a
-// duplicate; a first copy adds the gains of the later copies to its own, in
-// input order. The first copy of an id writes its key and (sample, summed
-// gain); later copies and ids outside the table write the sentinel key.
-// Blocks whose rows do not fit the staging read them from memory. With
-// `view_counts`, each block also counts its entries that enter the sample
-// view (a first copy whose local row is below `view_rows`).
-template <typename K>
+// ids of the rows it spans in LDS. With unit weights (kHashed) every staged
+// position enters an LDS hash set keyed by (row, id), which keeps the first
+// position of each key and counts its copies: an id is its row's first copy
+// when the set holds its position, and the first copy's gain is the
+// combiner's unit summed once per copy, in order. With weights (not kHashed)
+// the block also stages the weights and, for a weighted mean or sqrtn, each
+// row's divisor (one thread per row, the sequential sums of RowDivisors);
+// each id scans its row for copies (ScanRow) and a first copy adds the later
+// copies' w / divisor in input order. Blocks whose rows do not fit the
+// staging scan each row from memory. The first copy of an id writes its key
+// and (sample, summed gain); later copies and ids outside the table write
+// the sentinel key. With `view_counts`, each block also counts its entries
+// that enter the sample view (a first copy whose local row is below
+// `view_rows`).
+template <typename K, bool kHashed>
 __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
     const SliceDesc* slices, int num_slices, const FeatureDev* feats,
     const BlockRows* block_rows, int64_t total_ids, int combiner,
-    int has_weights, KeyLayout kl, int64_t view_rows, K* keys, uint64_t* pay,
+    KeyLayout kl, int64_t view_rows, K* keys, uint64_t* pay,
     uint32_t* view_counts, int64_t* counters) {
+  constexpr bool kWeighted = !kHashed;
   __shared__ int64_t s_splits[kExtractStagedSplits];
   __shared__ int32_t s_ids[kDedupStage];
-  __shared__ float s_w[kDedupStage];
-  __shared__ float s_div[kExtractStagedSplits];
+  __shared__ float s_w[kWeighted ? kDedupStage : 1];
+  __shared__ float s_div[kWeighted ? kExtractStagedSplits : 1];
+  __shared__ uint32_t s_table[kHashed ? kDedupSlots : 1];
+  __shared__ uint32_t s_counts[kHashed ? kDedupSlots / 2 : 1];
   const int64_t blk_first = static_cast<int64_t>(blockIdx.x) * blockDim.x;
   const int64_t o = blk_first + threadIdx.x;
   const BlockRows br = block_rows[blockIdx.x];
   const int block_slice = br.slice;
   const int64_t row_lo = br.lo, row_hi = br.hi;
-  const bool need_div = has_weights && combiner != 0;
+  const bool need_div = kWeighted && combiner != 0;
   bool staged = false;       // row splits [row_lo, row_hi + 1] in s_splits
   bool ids_staged = false;   // ids (and weights) [span_b, span_e) in LDS
   int64_t span_b = 0, span_e = 0;
@@ -1484,7 +1540,7 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
       const int n = static_cast<int>(span_e - span_b);
       for (int i = threadIdx.x; i < n; i += blockDim.x) {
         s_ids[i] = bf.ids[span_b + i];
-        if (has_weights) s_w[i] = bf.weights[span_b + i];
+        if constexpr (kWeighted) s_w[i] = bf.weights[span_b + i];
       }
       ids_staged = true;
       if (need_div) {
@@ -1498,22 +1554,36 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
       }
     }
   }
-  __syncthreads();
-  for (int t = threadIdx.x; t < div_rows; t += blockDim.x) {
-    const int64_t b = valency > 0 ? t * valency : s_splits[t] - span_b;
-    const int64_t e = valency > 0 ? b + valency : s_splits[t + 1] - span_b;
-    s_div[t] = RowDivisor(s_w + b, e - b, combiner);
+  // The hash set needs every staged position's row start: dense rows, or
+  // staged splits.
+  const bool hashed = kHashed && ids_staged && (valency > 0 || staged);
+  if constexpr (kHashed) {
+    if (hashed) {
+      for (int i = threadIdx.x; i < kDedupSlots; i += blockDim.x) {
+        s_table[i] = kSlotEmpty;
+      }
+      for (int i = threadIdx.x; i < kDedupSlots / 2; i += blockDim.x) {
+        s_counts[i] = 0;
+      }
+    }
   }
   __syncthreads();
-  bool bad = false;
-  bool view_entry = false;
+  if constexpr (kWeighted) {
+    for (int t = threadIdx.x; t < div_rows; t += blockDim.x) {
+      const int64_t b = valency > 0 ? t * valency : s_splits[t] - span_b;
+      const int64_t e = valency > 0 ? b + valency : s_splits[t + 1] - span_b;
+      s_div[t] = RowDivisor(s_w + b, static_cast<int>(e - b), combiner);
+    }
+  }
+  // Each id's slice and row.
+  int si = 0;
+  int64_t p = 0, r = 0, b = 0, e = 0;
   if (o < total_ids) {
-    const int si = block_slice >= 0 ? block_slice
-                                    : FindSlice(slices, num_slices, o, false);
+    si = block_slice >= 0 ? block_slice
+                          : FindSlice(slices, num_slices, o, false);
     const SliceDesc sl = slices[si];
     const FeatureDev f = feats[sl.feature];
-    const int64_t p = sl.id_begin + (o - sl.out_begin);  // input position
-    int64_t r, b, e;
+    p = sl.id_begin + (o - sl.out_begin);  // input position
     if (staged) {
       const int64_t k = LastRowAtOrBefore(s_splits, 0, row_hi - row_lo, p);
       r = row_lo + k;
@@ -1533,27 +1603,90 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
       b = r * f.valency;
       e = b + f.valency;
     }
-    // The row in LDS (a staged block holds all of its rows) or in memory;
-    // two inlined copies, so that each reads through a pointer of one
-    // address space.
+  }
+  if constexpr (kHashed) {
+    if (hashed) {
+      // The block's own ids, then the rest of its first row before them (row
+      // start 0) and of its last row after them.
+      if (o < total_ids) {
+        DedupInsert(s_table, s_counts, s_ids,
+                    static_cast<uint32_t>(b - span_b),
+                    static_cast<uint32_t>(p - span_b), s_ids[p - span_b]);
+      }
+      const SliceDesc bsl = slices[block_slice];
+      const int64_t o_last = min(blk_first + kExtractBlock, total_ids) - 1;
+      const int head = static_cast<int>(bsl.id_begin +
+                                        (blk_first - bsl.out_begin) - span_b);
+      const int tail = static_cast<int>(bsl.id_begin +
+                                        (o_last - bsl.out_begin) - span_b) + 1;
+      const int span = static_cast<int>(span_e - span_b);
+      const uint32_t last_start =
+          valency > 0
+              ? static_cast<uint32_t>((tail - 1) / valency * valency)
+              : static_cast<uint32_t>(s_splits[row_hi - row_lo] - span_b);
+      for (int x = threadIdx.x; x < head; x += blockDim.x) {
+        DedupInsert(s_table, s_counts, s_ids, 0u, static_cast<uint32_t>(x),
+                    s_ids[x]);
+      }
+      for (int x = tail + threadIdx.x; x < span; x += blockDim.x) {
+        DedupInsert(s_table, s_counts, s_ids, last_start,
+                    static_cast<uint32_t>(x), s_ids[x]);
+      }
+    }
+  }
+  __syncthreads();
+  bool bad = false;
+  bool view_entry = false;
+  if (o < total_ids) {
+    const SliceDesc sl = slices[si];
+    const FeatureDev f = feats[sl.feature];
     const int n = static_cast<int>(e - b);
     const int q = static_cast<int>(p - b);  // position in the row
-    float div = 1.0f;
-    if (need_div && r - div_row0 >= 0 && r - div_row0 < div_rows) {
-      div = s_div[r - div_row0];
-    }
-    const bool table_div = !need_div || (r - div_row0 >= 0 &&
-                                         r - div_row0 < div_rows);
     int32_t id;
     float gain;
     bool first;
-    if (ids_staged) {
-      const int64_t off = b - span_b;
-      first = ScanRow(s_ids + off, s_w + off, n, q, has_weights != 0,
-                      combiner, table_div, &div, &id, &gain);
+    if constexpr (kHashed) {
+      float unit = 1.0f;
+      if (combiner == 1) {
+        unit = 1.0f / static_cast<float>(n);
+      } else if (combiner == 2) {
+        unit = 1.0f / sqrtf(static_cast<float>(n));
+      }
+      float div = 1.0f;
+      if (hashed) {
+        id = s_ids[p - span_b];
+        const uint32_t h = DedupFind(s_table, s_ids,
+                                     static_cast<uint32_t>(b - span_b), id);
+        first = (s_table[h] & 2047u) == static_cast<uint32_t>(p - span_b);
+        const uint32_t copies =
+            (s_counts[h >> 1] >> ((h & 1u) * 16)) & 0xffffu;
+        gain = unit;
+        if (first) {
+          for (uint32_t c = 1; c < copies; ++c) gain = gain + unit;
+        }
+      } else if (ids_staged) {
+        const int64_t off = b - span_b;
+        first = ScanRow(s_ids + off, s_ids + off, n, q, false, combiner, true,
+                        &div, &id, &gain);
+      } else {
+        first = ScanRow(f.ids + b, f.ids + b, n, q, false, combiner, true,
+                        &div, &id, &gain);
+      }
     } else {
-      first = ScanRow(f.ids + b, has_weights ? f.weights + b : nullptr, n, q,
-                      has_weights != 0, combiner, table_div, &div, &id, &gain);
+      float div = 1.0f;
+      if (need_div && r - div_row0 >= 0 && r - div_row0 < div_rows) {
+        div = s_div[r - div_row0];
+      }
+      const bool table_div = !need_div || (r - div_row0 >= 0 &&
+                                           r - div_row0 < div_rows);
+      if (ids_staged) {
+        const int64_t off = b - span_b;
+        first = ScanRow(s_ids + off, s_w + off, n, q, true, combiner,
+                        table_div, &div, &id, &gain);
+      } else {
+        first = ScanRow(f.ids + b, f.weights + b, n, q, true, combiner,
+                        table_div, &div, &id, &gain);
+      }
     }
     const int32_t col = ((id + f.col_shift) & kl.ns_mask) + (id & ~kl.ns_mask) +
                         f.col_offset;
@@ -2557,11 +2690,17 @@ int RunUniquePipeline(const scemb_feature_t* feats, int nf,
                                 counters, tg, stream);
     if (su != 0) return su;
     if (M > 0) {
-      hipLaunchKernelGGL((ExtractUnique<K>), dim3(extract_blocks),
-                         dim3(kExtractBlock), 0, stream, slices, num_slices,
-                         fdev, block_rows, M, o->combiner,
-                         o->has_variable_weights ? 1 : 0, pl.kl, view_rows,
-                         keys, pay, view_off, counters);
+      if (o->has_variable_weights) {
+        hipLaunchKernelGGL((ExtractUnique<K, false>), dim3(extract_blocks),
+                           dim3(kExtractBlock), 0, stream, slices, num_slices,
+                           fdev, block_rows, M, o->combiner, pl.kl, view_rows,
+                           keys, pay, view_off, counters);
+      } else {
+        hipLaunchKernelGGL((ExtractUnique<K, true>), dim3(extract_blocks),
+                           dim3(kExtractBlock), 0, stream, slices, num_slices,
+                           fdev, block_rows, M, o->combiner, pl.kl, view_rows,
+                           keys, pay, view_off, counters);
+      }
       SCEMB_LAUNCH_CHECK();
     }
   }
