@@ -421,6 +421,12 @@ typedef struct scemb_feature {
 int scemb_check_row_splits(const int64_t* row_splits, int64_t num_rows,
                            int64_t nnz, int64_t* max_row_length);
 
+/* scemb_check_row_splits that also copies the splits to host memory dst
+ * [num_rows + 1] (a staging buffer for the upload) in the same pass. */
+int scemb_stage_row_splits(const int64_t* row_splits, int64_t num_rows,
+                           int64_t nnz, int64_t* dst,
+                           int64_t* max_row_length);
+
 /* scemb_preprocess_options_t.flags. Where the features' sample rows are
  * disjoint and neither id dropping nor minibatching is on, the library merges
  * the copies of an id within one input row while extracting (the only

@@ -46,6 +46,14 @@
 #include "scan.h"
 
 namespace scemb {
+
+// The longest row (returned) and the shortest (*least, at most 0) of host
+// row splits [num_rows + 1]; the second also copies them to dst
+// (rowsplits.cc).
+int64_t RowLengthRange(const int64_t* sp, int64_t num_rows, int64_t* least);
+int64_t CopyRowLengthRange(const int64_t* sp, int64_t num_rows, int64_t* dst,
+                           int64_t* least);
+
 namespace {
 
 constexpr uint32_t kDataMask26 = (1u << 26) - 1;
@@ -1784,9 +1792,10 @@ struct UniqueSource {
 constexpr int kGroupItems = 8;  // sorted entries per GroupUnique thread
 
 // Over the *total sorted entries: each bucket's first and last position, and
-// its distinct columns (counted per block in LDS, then one atomic per bucket
-// and block; integer sums, so the order does not matter). col_heads starts
-// at zero.
+// its distinct columns, counted per block in LDS (one add per wave while
+// the wave lies in one bucket, the usual case) and then added with one
+// atomic per bucket and block (integer sums: the order does not matter).
+// col_heads starts at zero.
 template <typename K>
 __global__ __launch_bounds__(256) void GroupUnique(
     const K* skeys, const uint32_t* total, KeyLayout kl, int num_partitions,
@@ -1803,26 +1812,52 @@ __global__ __launch_bounds__(256) void GroupUnique(
   };
   s_cnt[threadIdx.x] = 0;
   const int64_t b0 = bucket_of(skeys[base]);
-  __syncthreads();
+  // Every key this thread needs, loaded before any store (the stores could
+  // alias them as far as the compiler knows).
+  K cur[kGroupItems], prev[kGroupItems], next[kGroupItems];
+#pragma unroll
   for (int it = 0; it < kGroupItems; ++it) {
     const int64_t i = base + static_cast<int64_t>(it) * 256 + threadIdx.x;
-    if (i >= n) break;
-    const K key = skeys[i];
-    const int64_t bkt = bucket_of(key);
-    bool new_col = true, new_bucket = true;
-    if (i > 0) {
-      const K pk = skeys[i - 1];
-      new_col = pk != key;
-      new_bucket = new_col && bucket_of(pk) != bkt;
+    cur[it] = i < n ? skeys[i] : K(0);
+    prev[it] = i > 0 && i < n ? skeys[i - 1] : K(0);
+    next[it] = i + 1 < n ? skeys[i + 1] : K(0);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < kGroupItems; ++it) {
+    const int64_t i = base + static_cast<int64_t>(it) * 256 + threadIdx.x;
+    const bool active = i < n;
+    int64_t bkt = -1;
+    bool new_col = false;
+    if (active) {
+      const K key = cur[it];
+      bkt = bucket_of(key);
+      bool new_bucket = true;
+      new_col = true;
+      if (i > 0) {
+        new_col = prev[it] != key;
+        new_bucket = new_col && bucket_of(prev[it]) != bkt;
+      }
+      if (new_bucket) part_first[bkt] = static_cast<int32_t>(i);
+      bool last = i + 1 == n;
+      if (!last) last = next[it] != key && bucket_of(next[it]) != bkt;
+      if (last) part_last[bkt] = static_cast<int32_t>(i);
     }
-    if (new_bucket) part_first[bkt] = static_cast<int32_t>(i);
-    bool last = i + 1 == n;
-    if (!last) {
-      const K nk = skeys[i + 1];
-      last = nk != key && bucket_of(nk) != bkt;
-    }
-    if (last) part_last[bkt] = static_cast<int32_t>(i);
-    if (new_col) {
+    // The wave's first active lane is lane 0 (positions ascend with lanes).
+    const int64_t wave_bkt = __shfl(bkt, 0, kWave);
+    const uint64_t heads = __ballot(new_col);
+    const uint64_t other = __ballot(active && bkt != wave_bkt);
+    if (other == 0) {
+      if (__lane_id() == 0 && heads != 0) {
+        const int64_t rel = wave_bkt - b0;
+        const int c = __popcll(heads);
+        if (rel < 256) {
+          atomicAdd(&s_cnt[rel], c);
+        } else {
+          atomicAdd(&col_heads[wave_bkt], c);
+        }
+      }
+    } else if (new_col) {
       const int64_t rel = bkt - b0;  // >= 0: buckets ascend with the key
       if (rel < 256) {
         atomicAdd(&s_cnt[rel], 1);
@@ -2821,9 +2856,8 @@ int64_t MaxRowLength(const scemb_feature_t* feats, int nf,
     } else {
       const int64_t* sp = ft.row_splits_host != nullptr ? ft.row_splits_host
                                                         : cache[f].data();
-      for (int64_t r = 0; r < ft.num_rows; ++r) {
-        most = std::max<int64_t>(most, sp[r + 1] - sp[r]);
-      }
+      int64_t least = 0;
+      most = std::max<int64_t>(most, RowLengthRange(sp, ft.num_rows, &least));
     }
   }
   return most;
@@ -2913,14 +2947,27 @@ int scemb_check_row_splits(const int64_t* row_splits, int64_t num_rows,
   if (row_splits == nullptr || num_rows < 0 || max_row_length == nullptr) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null row splits");
   }
-  int64_t most = 0;
-  bool down = false;
-  for (int64_t r = 0; r < num_rows; ++r) {
-    const int64_t len = row_splits[r + 1] - row_splits[r];
-    down |= len < 0;
-    most = len > most ? len : most;
+  int64_t least = 0;
+  const int64_t most = RowLengthRange(row_splits, num_rows, &least);
+  if (row_splits[0] != 0 || row_splits[num_rows] != nnz || least < 0) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT,
+                "row_splits must start at 0, be non-decreasing and end at the "
+                "number of values.");
   }
-  if (row_splits[0] != 0 || row_splits[num_rows] != nnz || down) {
+  *max_row_length = most;
+  return 0;
+}
+
+int scemb_stage_row_splits(const int64_t* row_splits, int64_t num_rows,
+                           int64_t nnz, int64_t* dst,
+                           int64_t* max_row_length) {
+  if (row_splits == nullptr || dst == nullptr || num_rows < 0 ||
+      max_row_length == nullptr) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null row splits");
+  }
+  int64_t least = 0;
+  const int64_t most = CopyRowLengthRange(row_splits, num_rows, dst, &least);
+  if (row_splits[0] != 0 || row_splits[num_rows] != nnz || least < 0) {
     return Fail(SCEMB_ERR_INVALID_ARGUMENT,
                 "row_splits must start at 0, be non-decreasing and end at the "
                 "number of values.");

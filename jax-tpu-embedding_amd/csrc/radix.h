@@ -28,6 +28,17 @@ constexpr int kMaxDigitBits = 8;
 constexpr int kMaxRadix = 1 << kMaxDigitBits;
 constexpr int kSortWaves = kSortBlock / kWave;
 
+// Tile of block b of nb. Work-groups go to the eight XCDs round-robin
+// (block b to XCD b % 8), each with its own L2; this gives every XCD a
+// contiguous range of tiles, so that neighbouring tiles, whose histogram
+// counts and bucket writes share cache lines, share an L2.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int64_t XcdTile(int64_t b, int64_t nb) {
+  const int64_t per = nb / kXcds, rem = nb % kXcds;
+  const int64_t x = b % kXcds, j = b / kXcds;
+  return x * per + (x < rem ? x : rem) + j;
+}
+
 template <typename K>
 __device__ __forceinline__ uint32_t Digit(K key, int shift, uint32_t mask) {
   return static_cast<uint32_t>(key >> shift) & mask;
@@ -77,15 +88,24 @@ __global__ __launch_bounds__(kSortBlock) void RadixHistogramK(
   for (int d = threadIdx.x; d < radix; d += kSortBlock) h[d] = 0;
   __syncthreads();
   const int64_t m = ActiveCount(n, n_dev);
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kSortTile;
+  const int64_t tile = XcdTile(blockIdx.x, gridDim.x);
+  const int64_t base = tile * kSortTile;
   const int digit_bits = __popc(mask);
   const uint64_t lt = LaneMaskLt();
+  // All of the thread's keys first: the source reads through pointers that
+  // the compiler cannot tell apart from the LDS counters, so loads issued
+  // between the atomics would each wait for the one before.
+  K keys[kSortChunks];
+  bool act[kSortChunks];
 #pragma unroll
   for (int c = 0; c < kSortChunks; ++c) {
     const int64_t i = base + c * kSortBlock + threadIdx.x;
-    K k;
-    const bool active = i < m && src.LoadKey(i, &k);
-    const uint32_t d = active ? Digit(k, shift, mask) : 0u;
+    act[c] = i < m && src.LoadKey(i, &keys[c]);
+  }
+#pragma unroll
+  for (int c = 0; c < kSortChunks; ++c) {
+    const bool active = act[c];
+    const uint32_t d = active ? Digit(keys[c], shift, mask) : 0u;
     // Lanes of one digit add their count through one atomic (runs of equal
     // keys would otherwise serialise on one LDS address).
     uint64_t match = __ballot(active);
@@ -99,7 +119,7 @@ __global__ __launch_bounds__(kSortBlock) void RadixHistogramK(
   }
   __syncthreads();
   for (int d = threadIdx.x; d < radix; d += kSortBlock) {
-    hist[static_cast<int64_t>(d) * tiles + blockIdx.x] = h[d];
+    hist[static_cast<int64_t>(d) * tiles + tile] = h[d];
   }
 }
 
@@ -133,7 +153,7 @@ __global__ __launch_bounds__(kSortBlock) void RadixScatterK(
   const int wave = t / kWave;
   const int lane = t % kWave;
   const int radix = static_cast<int>(mask) + 1;
-  const int64_t blk = blockIdx.x;
+  const int64_t blk = XcdTile(blockIdx.x, gridDim.x);
   const int64_t base = blk * kSortTile;
   if (fill_tail) {
     const int64_t taken = static_cast<int64_t>(*total);
@@ -157,13 +177,18 @@ __global__ __launch_bounds__(kSortBlock) void RadixScatterK(
   V val[kWaveChunks];
   uint32_t dig[kWaveChunks];
   uint32_t rank[kWaveChunks];  // among the wave's elements of the digit
+  bool act[kWaveChunks];
+  // Loads first (see RadixHistogramK), then the ranking.
 #pragma unroll
   for (int c = 0; c < kWaveChunks; ++c) {
     const int li = wave * kWaveSpan + c * kWave + lane;
     key[c] = 0;
     val[c] = 0;
-    const bool active =
-        li < tile_n && src.Load(base + li, &key[c], &val[c]);
+    act[c] = li < tile_n && src.Load(base + li, &key[c], &val[c]);
+  }
+#pragma unroll
+  for (int c = 0; c < kWaveChunks; ++c) {
+    const bool active = act[c];
     const uint32_t d = active ? Digit(key[c], shift, mask) : 0u;
     uint64_t match = __ballot(active);
     for (int b = 0; b < digit_bits; ++b) {

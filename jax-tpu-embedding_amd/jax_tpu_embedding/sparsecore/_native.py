@@ -69,6 +69,7 @@ EXPORTED_SYMBOLS = (
     "scemb_preprocess_workspace_size",
     "scemb_preprocess_stacked_table",
     "scemb_check_row_splits",
+    "scemb_stage_row_splits",
     "scemb_compute_theoretical_max_coo_buffer_size",
     "scemb_compute_coo_buffer_size_per_device",
     "scemb_compute_row_pointers_size_per_device",
@@ -310,6 +311,9 @@ def load_library() -> ctypes.CDLL:
         vp, sz, vp]
     lib.scemb_check_row_splits.restype = ctypes.c_int
     lib.scemb_check_row_splits.argtypes = [vp, i64, i64,
+                                           ctypes.POINTER(ctypes.c_int64)]
+    lib.scemb_stage_row_splits.restype = ctypes.c_int
+    lib.scemb_stage_row_splits.argtypes = [vp, i64, i64, vp,
                                            ctypes.POINTER(ctypes.c_int64)]
     lib.scemb_compute_theoretical_max_coo_buffer_size.restype = i64
     lib.scemb_compute_theoretical_max_coo_buffer_size.argtypes = [i32, i32,
@@ -566,6 +570,10 @@ def as_device_tensor(x, dtype, dev=None):
   return t.from_numpy(arr).to(dev, non_blocking=False)
 
 
+ROW_SPLITS_MESSAGE = ("row_splits must start at 0, be non-decreasing and "
+                      "end at the number of values.")
+
+
 class HostUploads:
   """Host arrays bound for the device, gathered into one pinned staging
   buffer and sent with a single asynchronous copy on the current stream.
@@ -578,26 +586,38 @@ class HostUploads:
   _ALIGN = 256  # every array starts 256-byte aligned on the device
 
   class _Handle:
-    __slots__ = ("offset", "count", "dtype", "tensor")
+    __slots__ = ("offset", "count", "dtype", "tensor", "nnz",
+                 "max_row_length")
 
-    def __init__(self, offset, count, dtype):
+    def __init__(self, offset, count, dtype, nnz=None):
       self.offset, self.count, self.dtype = offset, count, dtype
       self.tensor = None
+      self.nnz = nnz  # row splits: the number of values they end at
+      self.max_row_length = None
 
   def __init__(self):
     self._items = []
     self._nbytes = 0
 
-  def add(self, x, dtype):
+  def add(self, x, dtype, nnz=None):
     t = torch()
     np_dtype = {t.int32: np.int32, t.int64: np.int64,
                 t.float32: np.float32}[dtype]
     arr = np.ascontiguousarray(np.asarray(x), dtype=np_dtype).reshape(-1)
     off = -(-self._nbytes // self._ALIGN) * self._ALIGN
     self._nbytes = off + arr.nbytes
-    h = HostUploads._Handle(off, arr.size, dtype)
+    h = HostUploads._Handle(off, arr.size, dtype, nnz)
     self._items.append((arr, h))
     return h
+
+  def add_row_splits(self, splits, nnz: int):
+    """Host row splits of a ragged feature. flush() checks them
+    (scemb_stage_row_splits: start at 0, non-decreasing, end at `nnz`) while
+    it stages them, raising ValueError if they do not hold; the handle then
+    holds their longest row in max_row_length."""
+    if np.asarray(splits).size == 0:
+      raise ValueError(ROW_SPLITS_MESSAGE)
+    return self.add(splits, torch().int64, nnz)
 
   def flush(self):
     if not self._items:
@@ -606,8 +626,19 @@ class HostUploads:
     dev = device()
     host = t.empty(self._nbytes, dtype=t.uint8, pin_memory=True)
     staged = host.numpy()
+    base = host.data_ptr()
+    lib = load_library()
+    longest = ctypes.c_int64(0)
     for arr, h in self._items:
-      staged[h.offset:h.offset + arr.nbytes] = arr.view(np.uint8)
+      if h.nnz is None:
+        staged[h.offset:h.offset + arr.nbytes] = arr.view(np.uint8)
+        continue
+      if lib.scemb_stage_row_splits(arr.ctypes.data, arr.size - 1, h.nnz,
+                                    base + h.offset, ctypes.byref(longest)):
+        self._items = []
+        self._nbytes = 0
+        raise ValueError(ROW_SPLITS_MESSAGE)
+      h.max_row_length = int(longest.value)
     dst = t.empty(self._nbytes, dtype=t.uint8, device=dev)
     dst.copy_(host, non_blocking=True)
     for arr, h in self._items:

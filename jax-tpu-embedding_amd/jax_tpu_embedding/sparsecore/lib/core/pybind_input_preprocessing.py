@@ -221,7 +221,13 @@ def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
       vals = vals.reshape(-1)
     else:
       vals = np.ascontiguousarray(np.asarray(vals), dtype=np.int32).reshape(-1)
-    max_len = _check_row_splits(splits, int(vals.shape[0]))
+    if uploads is not None:
+      # Checked while staged (flush); the longest row comes back then.
+      splits_dev = uploads.add_row_splits(splits, int(vals.shape[0]))
+      max_len = 0
+    else:
+      max_len = _check_row_splits(splits, int(vals.shape[0]))
+      splits_dev = on_device(splits, t.int64)
     w = None
     if weights is not None:
       wv = getattr(weights, "values", weights)
@@ -234,9 +240,8 @@ def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
     max_id = None
     if not isinstance(vals, t.Tensor) and vals.size:
       max_id = int(vals.max())
-    return _DeviceFeature(ids, w, on_device(splits, t.int64),
-                          splits, splits.size - 1, int(splits[-1]), 0, max_id,
-                          max_len)
+    return _DeviceFeature(ids, w, splits_dev, splits, splits.size - 1,
+                          int(splits[-1]), 0, max_id, max_len)
   arr = feature if isinstance(feature, np.ndarray) else np.asarray(
       feature, dtype=object)
   if arr.dtype != object and arr.ndim == 2:
@@ -286,18 +291,18 @@ def _check_row_splits(splits: np.ndarray, nnz: int) -> int:
   """The most ids of one row; raises ValueError unless the row splits start
   at 0, do not decrease and end at `nnz` (one pass in the library)."""
   if splits.size == 0:
-    raise ValueError("row_splits must start at 0, be non-decreasing and "
-                     "end at the number of values.")
+    raise ValueError(_native.ROW_SPLITS_MESSAGE)
   out = ctypes.c_int64(0)
   rc = _native.load_library().scemb_check_row_splits(
       splits.ctypes.data, splits.size - 1, nnz, ctypes.byref(out))
   if rc != 0:
-    raise ValueError("row_splits must start at 0, be non-decreasing and "
-                     "end at the number of values.")
+    raise ValueError(_native.ROW_SPLITS_MESSAGE)
   return int(out.value)
 
 
 def _resolve_feature(f: _DeviceFeature) -> _DeviceFeature:
+  if getattr(f.splits, "max_row_length", None) is not None:
+    f.max_row_length = f.splits.max_row_length
   f.ids = _native.HostUploads.resolve(f.ids)
   f.weights = _native.HostUploads.resolve(f.weights)
   f.splits = _native.HostUploads.resolve(f.splits)

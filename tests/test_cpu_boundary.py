@@ -173,6 +173,26 @@ def test_check_row_splits():
     pip._check_row_splits(np.zeros(0, np.int64), 0)  # pylint: disable=protected-access
 
 
+def test_stage_row_splits_copies_and_checks():
+  """The staging variant copies the splits while it checks them."""
+  lib = _native.load_library()
+  rng = np.random.default_rng(0)
+  for rows in (0, 1, 3, 4, 5, 1000, 16385):
+    src = np.zeros(rows + 1, np.int64)
+    src[1:] = np.cumsum(rng.integers(0, 9, size=rows))
+    dst = np.full(rows + 1, -7, np.int64)
+    out = ctypes.c_int64(-1)
+    assert lib.scemb_stage_row_splits(src.ctypes.data, rows, int(src[-1]),
+                                      dst.ctypes.data, ctypes.byref(out)) == 0
+    np.testing.assert_array_equal(dst, src)
+    assert out.value == (int(np.diff(src).max()) if rows else 0)
+  bad = np.array([0, 5, 3, 6], np.int64)
+  dst = np.zeros(4, np.int64)
+  assert lib.scemb_stage_row_splits(bad.ctypes.data, 3, 6, dst.ctypes.data,
+                                    ctypes.byref(out)) == \
+      _native.SCEMB_ERR_INVALID_ARGUMENT
+
+
 def test_preprocess_minibatching_options():
   """The bucket passes size 64 buckets per (SC, partition); a bad pass or a
   split of 64 bits is refused; the sample view adds its temporaries."""
