@@ -1502,7 +1502,7 @@ template <typename K, bool kHashed>
 __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
     const SliceDesc* slices, int num_slices, const FeatureDev* feats,
     const BlockRows* block_rows, int64_t total_ids, int combiner,
-    KeyLayout kl, int64_t view_rows, K* keys, uint64_t* pay,
+    int rows_of_one, KeyLayout kl, int64_t view_rows, K* keys, uint64_t* pay,
     uint32_t* view_counts, int64_t* counters) {
   constexpr bool kWeighted = !kHashed;
   __shared__ int64_t s_splits[kExtractStagedSplits];
@@ -1523,6 +1523,9 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
   int64_t div_row0 = 0;      // row of s_div[0]
   int div_rows = 0;          // rows with a divisor in s_div
   int64_t valency = 0;       // dense feature of the block
+  // With unit weights and no row of two ids there is nothing to merge: no
+  // staging, no hash set.
+  const bool stage = !(kHashed && rows_of_one);
   if (block_slice >= 0) {  // uniform over the block
     const SliceDesc bsl = slices[block_slice];
     const FeatureDev bf = feats[bsl.feature];
@@ -1544,7 +1547,7 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
       span_b = p_first / valency * valency;
       span_e = (p_last / valency + 1) * valency;
     }
-    if (span_e > span_b && span_e - span_b <= kDedupStage) {
+    if (stage && span_e > span_b && span_e - span_b <= kDedupStage) {
       const int n = static_cast<int>(span_e - span_b);
       for (int i = threadIdx.x; i < n; i += blockDim.x) {
         s_ids[i] = bf.ids[span_b + i];
@@ -1672,6 +1675,10 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
         if (first) {
           for (uint32_t c = 1; c < copies; ++c) gain = gain + unit;
         }
+      } else if (!stage) {
+        id = f.ids[p];
+        first = true;
+        gain = unit;
       } else if (ids_staged) {
         const int64_t off = b - span_b;
         first = ScanRow(s_ids + off, s_ids + off, n, q, false, combiner, true,
@@ -2725,16 +2732,24 @@ int RunUniquePipeline(const scemb_feature_t* feats, int nf,
                                 counters, tg, stream);
     if (su != 0) return su;
     if (M > 0) {
+      // Only dense features of one id per row are known to need no merging
+      // (max_row_length is a hint and may understate).
+      int rows_of_one = 1;
+      for (int f = 0; f < nf; ++f) {
+        if (feats[f].row_splits != nullptr || feats[f].valency > 1) {
+          rows_of_one = 0;
+        }
+      }
       if (o->has_variable_weights) {
         hipLaunchKernelGGL((ExtractUnique<K, false>), dim3(extract_blocks),
                            dim3(kExtractBlock), 0, stream, slices, num_slices,
-                           fdev, block_rows, M, o->combiner, pl.kl, view_rows,
-                           keys, pay, view_off, counters);
+                           fdev, block_rows, M, o->combiner, rows_of_one,
+                           pl.kl, view_rows, keys, pay, view_off, counters);
       } else {
         hipLaunchKernelGGL((ExtractUnique<K, true>), dim3(extract_blocks),
                            dim3(kExtractBlock), 0, stream, slices, num_slices,
-                           fdev, block_rows, M, o->combiner, pl.kl, view_rows,
-                           keys, pay, view_off, counters);
+                           fdev, block_rows, M, o->combiner, rows_of_one,
+                           pl.kl, view_rows, keys, pay, view_off, counters);
       }
       SCEMB_LAUNCH_CHECK();
     }

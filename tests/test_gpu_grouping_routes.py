@@ -167,8 +167,15 @@ def test_rows_longer_than_the_staging(weighted, monkeypatch):
   feats = [_ragged(rng, lens, 900)]
   weights = _weights(rng, feats) if weighted else None
   _compare(("long", weighted), feats, weights, specs)
-  monkeypatch.setattr(pip, "_check_row_splits", lambda splits, nnz: 1)
-  _compare(("long, hint 1", weighted), feats, weights, specs)
+  resolve = pip._resolve_feature  # pylint: disable=protected-access
+
+  def understated(f):
+    f = resolve(f)
+    f.max_row_length = 2
+    return f
+
+  monkeypatch.setattr(pip, "_resolve_feature", understated)
+  _compare(("long, hint 2", weighted), feats, weights, specs)
 
 
 @pytest.mark.parametrize("valency", [1, 3, 50, 3000])
