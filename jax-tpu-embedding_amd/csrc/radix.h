@@ -28,17 +28,6 @@ constexpr int kMaxDigitBits = 8;
 constexpr int kMaxRadix = 1 << kMaxDigitBits;
 constexpr int kSortWaves = kSortBlock / kWave;
 
-// Tile of block b of nb. Work-groups go to the eight XCDs round-robin
-// (block b to XCD b % 8), each with its own L2; this gives every XCD a
-// contiguous range of tiles, so that neighbouring tiles, whose histogram
-// counts and bucket writes share cache lines, share an L2.
-constexpr int kXcds = 8;
-__device__ __forceinline__ int64_t XcdTile(int64_t b, int64_t nb) {
-  const int64_t per = nb / kXcds, rem = nb % kXcds;
-  const int64_t x = b % kXcds, j = b / kXcds;
-  return x * per + (x < rem ? x : rem) + j;
-}
-
 template <typename K>
 __device__ __forceinline__ uint32_t Digit(K key, int shift, uint32_t mask) {
   return static_cast<uint32_t>(key >> shift) & mask;
@@ -88,7 +77,7 @@ __global__ __launch_bounds__(kSortBlock) void RadixHistogramK(
   for (int d = threadIdx.x; d < radix; d += kSortBlock) h[d] = 0;
   __syncthreads();
   const int64_t m = ActiveCount(n, n_dev);
-  const int64_t tile = XcdTile(blockIdx.x, gridDim.x);
+  const int64_t tile = blockIdx.x;
   const int64_t base = tile * kSortTile;
   const int digit_bits = __popc(mask);
   const uint64_t lt = LaneMaskLt();
@@ -153,7 +142,7 @@ __global__ __launch_bounds__(kSortBlock) void RadixScatterK(
   const int wave = t / kWave;
   const int lane = t % kWave;
   const int radix = static_cast<int>(mask) + 1;
-  const int64_t blk = XcdTile(blockIdx.x, gridDim.x);
+  const int64_t blk = blockIdx.x;
   const int64_t base = blk * kSortTile;
   if (fill_tail) {
     const int64_t taken = static_cast<int64_t>(*total);
