@@ -676,16 +676,23 @@ class _Workspace:
     self._captured = set()
     self._retired = []
 
-  def get(self, nbytes: int):
+  def get(self, nbytes: int, stream=None):
+    """The buffer of `stream` (default: the current stream), at least
+    `nbytes` long. A new buffer is allocated on that stream, so that the
+    allocator hands its memory to no other stream before the stream's work
+    on it is done."""
     t = torch()
     dev = device()
-    key = (dev.index, t.cuda.current_stream(dev).cuda_stream)
+    if stream is None:
+      stream = t.cuda.current_stream(dev)
+    key = (dev.index, stream.cuda_stream)
     buf = self._buf.get(key)
     if buf is None or buf.numel() < nbytes:
       if buf is not None and key in self._captured:
         self._retired.append(buf)
-      buf = t.empty(max(int(nbytes * 1.25), 1 << 20), dtype=t.uint8,
-                    device=dev)
+      with t.cuda.stream(stream):
+        buf = t.empty(max(int(nbytes * 1.25), 1 << 20), dtype=t.uint8,
+                      device=dev)
       self._buf[key] = buf
     if t.cuda.is_current_stream_capturing():
       self._captured.add(key)

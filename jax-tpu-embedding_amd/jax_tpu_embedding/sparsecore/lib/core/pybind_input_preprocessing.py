@@ -15,7 +15,6 @@ here (the reference's all-reduce across hosts is not part of this path).
 
 from __future__ import annotations
 
-import contextlib
 import ctypes
 import dataclasses
 import enum
@@ -355,15 +354,29 @@ def _preprocess_stack(feats, metas, *, local_device_count,
   if need == 0:
     _native.check(_native.SCEMB_ERR_INVALID_ARGUMENT)
   L, S = local_device_count, num_sc_per_device
+  # Outputs not given come out of one allocation (int32 words, each part
+  # 256-byte aligned): row pointers, ids, samples, gains, view keys and
+  # entries.
+  parts = []
+  if outputs is None:
+    parts += [L * S * max(ns, 8) *
+              (_native.MAX_MINIBATCHES if enable_minibatching else 1),
+              L * c, L * c, L * c]
+  if build_view and not view_outputs:
+    parts += [c, 2 * c]
+  if parts:
+    sizes = [-(-n // 64) * 64 for n in parts]
+    block = t.empty(max(sum(sizes), 1), dtype=t.int32, device=dev)
+    carved, pos = [], 0
+    for n, size in zip(parts, sizes):
+      carved.append(block[pos:pos + n])
+      pos += size
   if outputs is not None:
     rp, eid, sid, gains = outputs
   else:
-    rp = t.empty(L * S * max(ns, 8) *
-                 (_native.MAX_MINIBATCHES if enable_minibatching else 1),
-                 dtype=t.int32, device=dev)
-    eid = t.empty(L * c, dtype=t.int32, device=dev)
-    sid = t.empty(L * c, dtype=t.int32, device=dev)
-    gains = t.empty(L * c, dtype=t.float32, device=dev)
+    rp, eid, sid, gains = carved[:4]
+    gains = gains.view(t.float32)
+    carved = carved[4:]
   nstats = lib.scemb_preprocess_stats_size(ctypes.byref(opts))
   # The library initialises the whole stats block.
   if stats_out is not None:
@@ -374,19 +387,17 @@ def _preprocess_stack(feats, metas, *, local_device_count,
     stats = t.empty(nstats + 2, dtype=t.int32, device=dev)
   view = None
   if build_view:
-    view = view_outputs or (t.empty(c, dtype=t.int32, device=dev),
-                            t.empty(c, dtype=t.int64, device=dev))
+    view = view_outputs or (carved[0], carved[1].view(t.int64))
   out = _native.PreprocessOutput(
       _native.ptr(rp), _native.ptr(eid), _native.ptr(sid), _native.ptr(gains),
       _native.ptr(stats), None if view is None else _native.ptr(view[0]),
       None if view is None else _native.ptr(view[1]))
-  with (t.cuda.stream(stream) if stream is not None else
-        contextlib.nullcontext()):
-    # The workspace belongs to the stream the work is enqueued on.
-    ws = _native.WORKSPACE.get(need)
-    _native.check(lib.scemb_preprocess_stacked_table(
-        structs, len(feats), ctypes.byref(opts), ctypes.byref(out),
-        _native.ptr(ws), ws.numel(), _native.stream_handle()))
+  # The workspace belongs to the stream the work is enqueued on.
+  ws = _native.WORKSPACE.get(need, stream)
+  _native.check(lib.scemb_preprocess_stacked_table(
+      structs, len(feats), ctypes.byref(opts), ctypes.byref(out),
+      _native.ptr(ws), ws.numel(),
+      stream.cuda_stream if stream is not None else _native.stream_handle()))
   off = int(lib.scemb_preprocess_stats_counters_offset(ctypes.byref(opts)))
   # The stats stay on the device until every stack has been enqueued.
   return rp, eid, sid, gains, stats, (L, S, ns, off), view
