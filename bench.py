@@ -385,7 +385,8 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
           max_unique_ids_per_partition=spec.max_unique_ids_per_partition,
           num_sc_per_device=1,
           lookup_view=None if csr_only else p.lookup_views[name],
-          csr_num_entries=None if csr_only else p.csr_num_entries[name])
+          csr_num_entries=None if csr_only else
+          (p.csr_num_entries or {}).get(name))
 
     def update(name):
       spec = stacked[name]
@@ -396,7 +397,7 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
                 csr_sorted_by_row=None if csr_only else
                 p.csr_sorted_by_row,
                 csr_num_entries=None if csr_only else
-                p.csr_num_entries[name])
+                (p.csr_num_entries or {}).get(name))
       if a is not None:
         return ada.tpu_sparse_dense_matmul_grad_with_adagrad_primitive.bind(
             *csr_of(name), 1, t, a, g, lr, **kw)
@@ -428,9 +429,9 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
   graph_ms = _graph_steps(step, steps, warmup)
   log(f"step replayed from a HIP graph: {graph_ms:.4f} ms")
   pipelined_ms = _pipelined_steps(
-      step, lambda: embedding.preprocess_sparse_dense_matmul_input(
+      step, lambda: embedding.enqueue_preprocess_sparse_dense_matmul_input(
           feats_dev, weights_dev, w.feature_specs, 1, 1,
-          num_sc_per_device=1)[0], steps, warmup)
+          num_sc_per_device=1), steps, warmup)
   log(f"step with the next batch preprocessed alongside: "
       f"{pipelined_ms:.4f} ms")
   # Kernel durations from HIP events on the launch stream, in a second pass
@@ -504,11 +505,12 @@ def _device_tensors(obj, out):
 
 def _pipelined_steps(step, preprocess, steps, warmup):
   """Steady state of a training loop that preprocesses batch k + 1 on a
-  second stream while step k runs: each iteration enqueues the step on the
-  current stream, then preprocesses the next batch (the same synthetic
-  input, already in HBM) on the side stream; the next step waits for it.
-  The preprocessing's host work and its stats read-back (a wait on the side
-  stream only) overlap the step's kernels. ms per step."""
+  second stream while step k runs: each iteration enqueues step k on the
+  current stream, enqueues the preprocessing of the next batch (the same
+  synthetic input, already in HBM) on the side stream
+  (enqueue_preprocess_sparse_dense_matmul_input), then collects batch k's
+  stats, whose copy finished before step k could start; the next step waits
+  for the side stream. The host never waits for the step. ms per step."""
   import torch  # pylint: disable=g-import-not-at-top
 
   main = torch.cuda.current_stream()
@@ -516,24 +518,29 @@ def _pipelined_steps(step, preprocess, steps, warmup):
 
   def next_batch():
     with torch.cuda.stream(side):
-      b = preprocess()
+      b, stats = preprocess()
     # The batch is consumed on the main stream: its memory must not return
     # to the side stream's pool before the main stream is done with it.
     for t in _device_tensors(b, []):
       t.record_stream(main)
     main.wait_stream(side)
-    return b
+    return b, stats
 
-  cur = next_batch()
+  cur, stats = next_batch()
   for _ in range(warmup):
     step(False, cur)
-    cur = next_batch()
+    nxt = next_batch()
+    stats.result()
+    cur, stats = nxt
   torch.cuda.synchronize()
   t0 = time.perf_counter()
   for _ in range(steps):
     step(False, cur)
-    cur = next_batch()
+    nxt = next_batch()
+    stats.result()
+    cur, stats = nxt
   torch.cuda.synchronize()
+  stats.result()
   return (time.perf_counter() - t0) * 1e3 / steps
 
 

@@ -506,6 +506,11 @@ class PendingStats(list):
     self.num_minibatches = 1
     self.final_pass_stats = {}
     self.stats_buffer = None  # the stacks' first-pass stats, one after another
+    # Without minibatching: the stats block's copy into pinned host memory,
+    # enqueued behind the preprocessing on its stream, and the event that
+    # marks it done.
+    self.host_stats = None
+    self.host_stats_ready = None
 
 
 def _to_host(tensors) -> np.ndarray:
@@ -655,6 +660,16 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
   if enable_minibatching:
     _minibatching_passes(pending, jobs, flat,
                          sample_views if sample_views is not None else {})
+  else:
+    # The stats go to the host behind the preprocessing, on its stream:
+    # collect_stats then waits for this copy alone, not for whatever the
+    # calling stream runs later.
+    host = t.empty(pending.stats_buffer.numel(), dtype=t.int32,
+                   pin_memory=True)
+    host.copy_(pending.stats_buffer, non_blocking=True)
+    ready = t.cuda.Event()
+    ready.record()
+    pending.host_stats, pending.host_stats_ready = host, ready
   return rps, eids, sids, gns, pending
 
 
@@ -684,8 +699,13 @@ def collect_stats(pending) -> SparseDenseMatmulInputStats:
   # One wait for the first passes' stats and any later pass's counters.
   # The stacks' stats tensors are consecutive slices of stats_buffer.
   buffer = getattr(pending, "stats_buffer", None)
-  host = _to_host(([buffer] if buffer is not None else
-                   [p[1] for p in pending]) + [x[0] for x in later])
+  early = getattr(pending, "host_stats", None)
+  if early is not None and not later:
+    pending.host_stats_ready.synchronize()
+    host = early.numpy()
+  else:
+    host = _to_host(([buffer] if buffer is not None else
+                     [p[1] for p in pending]) + [x[0] for x in later])
   pos = 0
   tail = sum(p[1].numel() for p in pending)
   for name, stats_dev, L, S, ns, off, _ in pending:

@@ -292,6 +292,69 @@ def preprocess_sparse_dense_matmul_input(
   Returns (PreprocessedInput, SparseDenseMatmulInputStats); the CSR buffers
   are torch CUDA tensors.
   """
+  preprocessed, stats = enqueue_preprocess_sparse_dense_matmul_input(
+      features, features_weights, feature_specs, local_device_count,
+      global_device_count, num_sc_per_device=num_sc_per_device,
+      sharding_strategy=sharding_strategy,
+      has_leading_dimension=has_leading_dimension,
+      allow_id_dropping=allow_id_dropping, batch_number=batch_number,
+      enable_minibatching=enable_minibatching,
+      all_reduce_interface=all_reduce_interface)
+  return preprocessed, stats.result()
+
+
+class PreprocessStats:
+  """The stats of a preprocessing call still running on the device
+  (enqueue_preprocess_sparse_dense_matmul_input). result() waits for them
+  (for the copy enqueued behind the call on its stream, not for later work
+  on that stream), raises as preprocess_sparse_dense_matmul_input does on
+  ids outside a table or over the limits, records the entry counts in the
+  PreprocessedInput (the lookup picks kernel variants by them; until then
+  it sizes by the buffers) and returns SparseDenseMatmulInputStats."""
+
+  def __init__(self, pending, preprocessed, enable_minibatching):
+    self._pending = pending
+    self._preprocessed = preprocessed
+    self._minibatching = enable_minibatching
+    self._stats = None
+
+  def result(self) -> SparseDenseMatmulInputStats:
+    if self._stats is not None:
+      return self._stats
+    stats = pybind_input_preprocessing.collect_stats(self._pending)
+    pre = self._preprocessed
+    if pre.lookup_views is not None:
+      counts = dict(stats.num_entries)
+      pre.csr_num_entries = counts
+      for name, view in pre.lookup_views.items():
+        view.num_entries = counts.get(name, 0)
+        if self._minibatching and view.num_entries:
+          # The view has room for a buffer sized for 64 minibatches; past
+          # the entries it holds only unused keys.
+          used = -(-view.num_entries // 256) * 256
+          if used < view.keys.numel():
+            view.keys, view.entries = view.keys[:used], view.entries[:used]
+    self._stats = SparseDenseMatmulInputStats.from_cc(stats)
+    self._pending = None
+    return self._stats
+
+
+def enqueue_preprocess_sparse_dense_matmul_input(
+    features, features_weights, feature_specs, local_device_count: int,
+    global_device_count: int, *, num_sc_per_device: int | None = None,
+    sharding_strategy: str = "MOD", has_leading_dimension: bool = False,
+    allow_id_dropping: bool = False, batch_number: int = 0,
+    enable_minibatching: bool = False, all_reduce_interface=None):
+  """preprocess_sparse_dense_matmul_input without the wait: enqueues the
+  preprocessing on the current stream and returns (PreprocessedInput,
+  PreprocessStats) at once (no counterpart in the reference, whose
+  preprocessing runs on the host). Work enqueued later on the stream may use
+  the PreprocessedInput; a training loop can preprocess batch k + 1 on a
+  second stream during step k and call result() once step k + 1 is
+  enqueued. Arguments are checked before anything is enqueued; ids outside
+  a table and exceeded limits are raised by result(). Minibatching decides
+  between its passes on the host, so with enable_minibatching this waits
+  for the first pass."""
   num_sc_per_device = _get_num_sc_per_device(num_sc_per_device)
   _assert_same_structure(features, feature_specs, "features", "feature_specs")
   if features_weights is not None:
@@ -339,28 +402,16 @@ def preprocess_sparse_dense_matmul_input(
           one_per_row, only=missing,
           num_minibatches=(pending.num_minibatches if enable_minibatching
                            else 0)))
-  stats = pybind_input_preprocessing.collect_stats(pending)
-  counts = None
-  if local_device_count == 1:
-    counts = dict(stats.num_entries)
-    for name, view in (views or {}).items():
-      view.num_entries = counts.get(name, 0)
-      if enable_minibatching and view.num_entries:
-        # The view has room for a buffer sized for 64 minibatches; past the
-        # entries it holds only unused keys.
-        used = -(-view.num_entries // 256) * 256
-        if used < view.keys.numel():
-          view.keys, view.entries = view.keys[:used], view.entries[:used]
   minibatches = np.full(local_device_count, pending.num_minibatches,
                         dtype=np.int32)
   if has_leading_dimension:
     minibatches = minibatches.reshape(local_device_count, 1)
-  return (PreprocessedInput(SparseDenseMatmulInput(*csr), minibatches,
-                            lookup_views=views,
-                            csr_sorted_by_row=(None if local_device_count == 1
-                                               else False),
-                            csr_num_entries=counts),
-          SparseDenseMatmulInputStats.from_cc(stats))
+  preprocessed = PreprocessedInput(
+      SparseDenseMatmulInput(*csr), minibatches, lookup_views=views,
+      csr_sorted_by_row=(None if local_device_count == 1 else False),
+      csr_num_entries=None)
+  return preprocessed, PreprocessStats(pending, preprocessed,
+                                       enable_minibatching)
 
 
 def preprocess_sparse_dense_matmul_input_from_sparse_tensor(
