@@ -436,11 +436,16 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
       f"{pipelined_ms:.4f} ms")
   # Kernel durations from HIP events on the launch stream, in a second pass
   # of the same steps (the events themselves cost a few microseconds each,
-  # so the timed pass above runs without them).
+  # so the timed pass above runs without them). Stacks run one after another
+  # in this pass: side by side, each event pair would also span the other
+  # stacks' kernels sharing the GPU.
+  sides = _native.NUM_SIDE_STREAMS
+  _native.NUM_SIDE_STREAMS = 0
   _native.profile_enable(True)
   _native.profile_collect(None)
   timed(steps, False)
   _native.profile_enable(False)
+  _native.NUM_SIDE_STREAMS = sides
   api_ms = api_copy_ms = None
   if api:
     api_ms, api_copy_ms = _api_steps(w, pre, state, stacked, steps, warmup,
