@@ -719,6 +719,35 @@ def test_shared_row_in_one_entry_per_row_csr_is_flagged():
   del keep
 
 
+@pytest.mark.parametrize("shared", [False, True])
+def test_undeclared_csr_stream_is_the_stable_row_sort(shared):
+  """A small CSR with padding, not declared one entry per row, with and
+  without a row that holds two entries: the sample stream is the stable
+  sort of the valid entries by activation row, the rest holds the unused
+  key, and no status is raised for the shared row (nothing was declared)."""
+  pad = np.iinfo(np.int32).max
+  rp = np.full(8, 5, np.int32)
+  eid = np.array([1, 2, 3, 4, 6, pad, pad, pad], np.int32)
+  sid = np.array([0, 5, 7 if not shared else 0, 3, 6, pad, pad, pad],
+                 np.int32)
+  gains = np.array([1, 2, 3, 4, 5, np.nan, np.nan, np.nan], np.float32)
+  batch, rows = 8, 16
+  keep, c = _device.csr_operands(rp, eid, sid, gains, 1, 1)
+  status = torch.zeros(1, dtype=torch.int32, device="cuda")
+  v = _native.build_sample_view(c, batch, rows, device_status=status)
+  torch.cuda.synchronize()
+  order = np.argsort(sid[:5], kind="stable")
+  keys = v.keys.cpu().numpy()
+  entries = v.entries.cpu().numpy()
+  np.testing.assert_array_equal(keys[:5], sid[:5][order])
+  np.testing.assert_array_equal(
+      entries[:5], eid[:5][order].astype(np.uint64) |
+      (gains[:5][order].view(np.uint32).astype(np.uint64) << np.uint64(32)))
+  assert (keys[5:] == batch).all()
+  assert int(status.item()) == 0
+  del keep
+
+
 @pytest.mark.parametrize("num_sc", [1, 2])
 @pytest.mark.parametrize("weighted", [False, True])
 def test_preprocessing_view_groups_like_the_csr_view(num_sc, weighted):
