@@ -73,34 +73,50 @@ __global__ void FillU32(uint32_t* p, int64_t n, uint32_t v) {
 // value to make room for); the last pass fills the positions past the
 // entries with the unused key.
 
+// The loads do not report entries outside the table: an atomic between them
+// would keep the compiler from issuing one position's loads before the
+// previous position's atomic, so RadixHistogramK hands the positions it did
+// not take to Rejected once all of its loads are out.
 struct CsrRowSource {
   Csr csr;
   int64_t bps;
   int64_t rows_per_partition;
   uint32_t* status;
-  __device__ bool Valid(int64_t j, int* p, uint32_t* k) const {
-    int s = 0;
-    *p = LocateEntry(csr, j, &s);
-    if (*p < 0) return false;
-    const int32_t e = csr.eid[j];
-    const int32_t sm = csr.sid[j];
-    if (e < 0 || e >= rows_per_partition || sm < 0 || sm >= bps) {
-      if (status != nullptr) atomicOr(status, SCEMB_STATUS_BAD_ENTRY);
+  __device__ bool Entry(int s, int p, int32_t e, int32_t sm,
+                        uint32_t* k) const {
+    if (p < 0 || e < 0 || e >= rows_per_partition || sm < 0 || sm >= bps) {
       return false;
     }
     *k = static_cast<uint32_t>(s * bps + sm);
     return true;
   }
+  // Every position below the geometry's n lies inside the CSR arrays, so
+  // the loads need not wait for the partition test.
   __device__ bool LoadKey(int64_t j, uint32_t* k) const {
-    int p;
-    return Valid(j, &p, k);
+    int s = 0;
+    const int p = LocateEntry(csr, j, &s);
+    return Entry(s, p, csr.eid[j], csr.sid[j], k);
   }
   __device__ bool Load(int64_t j, uint32_t* k, uint64_t* v) const {
-    int p;
-    if (!Valid(j, &p, k)) return false;
-    *v = Pack(static_cast<uint32_t>(p * rows_per_partition + csr.eid[j]),
-              csr.gains[j]);
+    int s = 0;
+    const int p = LocateEntry(csr, j, &s);
+    const int32_t e = csr.eid[j];
+    const float g = csr.gains[j];
+    if (!Entry(s, p, e, csr.sid[j], k)) return false;
+    *v = Pack(static_cast<uint32_t>(p * rows_per_partition + e), g);
     return true;
+  }
+  // A position LoadKey declined: an entry (not padding) outside the table
+  // or the batch sets SCEMB_STATUS_BAD_ENTRY.
+  __device__ void Rejected(int64_t j) const {
+    if (status == nullptr) return;
+    int s = 0;
+    if (LocateEntry(csr, j, &s) < 0) return;
+    const int32_t e = csr.eid[j];
+    const int32_t sm = csr.sid[j];
+    if (e < 0 || e >= rows_per_partition || sm < 0 || sm >= bps) {
+      atomicOr(status, SCEMB_STATUS_BAD_ENTRY);
+    }
   }
 };
 
@@ -119,6 +135,51 @@ struct StreamSink {
   }
 };
 
+// Keys of 9 to 8 + radix::kBucketMaxBits bits: one pass on the top 8 bits
+// into (b.keys_alt, b.pay_alt), then RadixBucketSortK into (b.keys, b.pay),
+// which also fills the positions past the entries. Same result as the LSD
+// passes: each bucket's elements arrive in CSR order and keep it.
+int GroupByRowInBuckets(const CsrRowSource& src, int64_t n, int bits,
+                        int64_t batch, const SortBuffers& b, Arena& ws,
+                        hipStream_t stream) {
+  using radix::kSortBlock;
+  using radix::kSortTile;
+  constexpr int hb = radix::kMaxDigitBits;
+  const int lb = bits - hb;
+  const int buckets = 1 << hb;
+  const int64_t tiles = CeilDiv(n, kSortTile);
+  uint32_t* hist = ws.Take<uint32_t>(tiles * buckets);
+  uint32_t* total = ws.Take<uint32_t>(1);
+  const bool measuring = ws.measuring();
+  if (!measuring && ws.overflow()) {
+    return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+  }
+  const uint32_t mask = static_cast<uint32_t>(buckets - 1);
+  if (!measuring) {
+    hipLaunchKernelGGL((radix::RadixHistogramK<uint32_t, CsrRowSource>),
+                       dim3(tiles), dim3(kSortBlock), 0, stream, src, n,
+                       nullptr, lb, mask, tiles, hist);
+    SCEMB_LAUNCH_CHECK();
+  }
+  const int st = ExclusiveScan<uint32_t>(hist, hist, tiles * buckets, total,
+                                         ws, stream);
+  if (st != 0 || measuring) return st;
+  const radix::ArraySink<uint32_t, uint64_t> mid{b.keys_alt, b.pay_alt};
+  hipLaunchKernelGGL(
+      (radix::RadixScatterK<uint32_t, uint64_t, CsrRowSource,
+                            radix::ArraySink<uint32_t, uint64_t>>),
+      dim3(tiles), dim3(kSortBlock), 0, stream, src, mid, n, nullptr, lb,
+      mask, hb, tiles, hist, total, false);
+  SCEMB_LAUNCH_CHECK();
+  const StreamSink sink{b.keys, b.pay, static_cast<uint32_t>(batch)};
+  hipLaunchKernelGGL(
+      (radix::RadixBucketSortK<uint32_t, uint64_t, StreamSink>),
+      dim3(buckets), dim3(radix::kBucketBlock), 0, stream, b.keys_alt,
+      b.pay_alt, sink, hist, tiles, buckets, total, lb, n, true);
+  SCEMB_LAUNCH_CHECK();
+  return 0;
+}
+
 int GroupByRow(const scemb_csr_t* csr, const Geometry& geo, int64_t batch,
                const SortBuffers& b, Arena& ws, uint32_t* status,
                hipStream_t stream) {
@@ -127,6 +188,12 @@ int GroupByRow(const scemb_csr_t* csr, const Geometry& geo, int64_t batch,
   using Arr = radix::ArraySource<uint32_t, uint64_t>;
   const int64_t n = geo.n;
   const int bits = batch > 1 ? BitWidth(static_cast<uint64_t>(batch - 1)) : 1;
+  if (bits > radix::kMaxDigitBits &&
+      bits <= radix::kMaxDigitBits + radix::kBucketMaxBits) {
+    const CsrRowSource src{MakeCsr(csr), geo.bps, geo.rows_per_partition,
+                           status};
+    return GroupByRowInBuckets(src, n, bits, batch, b, ws, stream);
+  }
   const radix::DigitPlan plan = radix::PlanDigits(bits);
   const int64_t tiles = CeilDiv(n, kSortTile);
   uint32_t* hist = ws.Take<uint32_t>(tiles * (int64_t{1} << plan.digit));

@@ -1794,6 +1794,7 @@ struct UniqueSource {
     *v = pay[i];
     return true;
   }
+  __device__ void Rejected(int64_t) const {}
 };
 
 constexpr int kGroupItems = 8;  // sorted entries per GroupUnique thread

@@ -46,6 +46,7 @@ struct ArraySource {
     *v = vals[i];
     return true;
   }
+  __device__ void Rejected(int64_t) const {}
 };
 
 template <typename K, typename V>
@@ -67,7 +68,8 @@ __device__ __forceinline__ int64_t ActiveCount(int64_t n,
   return m < n ? m : n;
 }
 
-// hist[d * tiles + tile] = elements of digit d in the tile.
+// hist[d * tiles + tile] = elements of digit d in the tile. The positions
+// the source declines go to src.Rejected after all loads are issued.
 template <typename K, typename Src>
 __global__ __launch_bounds__(kSortBlock) void RadixHistogramK(
     Src src, int64_t n, const uint32_t* n_dev, int shift, uint32_t mask,
@@ -105,6 +107,11 @@ __global__ __launch_bounds__(kSortBlock) void RadixHistogramK(
     if (active && (match & lt) == 0) {
       atomicAdd(&h[d], static_cast<uint32_t>(__popcll(match)));
     }
+  }
+#pragma unroll
+  for (int c = 0; c < kSortChunks; ++c) {
+    const int64_t i = base + c * kSortBlock + threadIdx.x;
+    if (i < m && !act[c]) src.Rejected(i);
   }
   __syncthreads();
   for (int d = threadIdx.x; d < radix; d += kSortBlock) {
@@ -245,6 +252,273 @@ __global__ __launch_bounds__(kSortBlock) void RadixScatterK(
     const uint32_t d = Digit(k, shift, mask);
     sink.Store(global_off[d] + (static_cast<uint32_t>(j) - tile_off[d]), k,
                s_vals[j]);
+  }
+}
+
+// --- Two-stage sort: one pass on the high digit, then a sort per bucket ----
+//
+// After one RadixScatterK pass on the digit above the low `lb` key bits,
+// bucket d (the keys whose high digit is d) occupies
+// [offsets[d * tiles], offsets[(d + 1) * tiles]) of that pass's output, in
+// input order. RadixBucketSortK gives each bucket one block of 16 waves,
+// which sorts it stably by the low lb bits:
+//   - a chunk of at most kBucketChunk elements is read into LDS with
+//     coalesced loads, as (low key bits, position in the chunk) pairs;
+//   - one or two LDS passes of at most kBucketDigitMax bits sort the pairs
+//     stably: each wave ranks its own contiguous span of the chunk in order
+//     (one ballot per digit bit finds the lanes of one digit; the lowest of
+//     them bumps the wave's counter), a block scan over (digit, wave) gives
+//     the bases, and a second walk places every pair;
+//   - the sorted chunk is written out coalesced: the full key is the bucket
+//     digit over the low bits, and the value is read at its position.
+// A bucket of one chunk is then done. A larger bucket is first counted per
+// low-key value (LDS atomics and a scan give each value's start); each
+// sorted chunk then places a value's elements after the ones that earlier
+// chunks placed.
+constexpr int kBucketWaves = 16;
+constexpr int kBucketBlock = kBucketWaves * kWave;
+constexpr int kBucketChunk = 8192;
+constexpr int kBucketDigitMax = 7;
+constexpr int kBucketMaxBits = 13;  // two LDS passes; 2^13 value starts
+
+// One stable LDS pass over pairs [0, m) of (sk, si)[from] into [1 - from],
+// by bits [shift, shift + bits) of the key. Each wave ranks its span once
+// (ballots) and keeps every element's digit and rank in registers across
+// the scan, so the placement walk only adds the (digit, wave) base.
+constexpr int kBucketWaveChunks = kBucketChunk / kBucketWaves / kWave;
+
+__device__ __forceinline__ void BucketLdsPass(
+    uint16_t (*sk)[kBucketChunk], uint16_t (*si)[kBucketChunk],
+    uint16_t (*wcnt)[1 << kBucketDigitMax], uint32_t* scan_tmp, int from,
+    int m, int shift, int bits) {
+  const int t = threadIdx.x;
+  const int wave = t / kWave;
+  const int lane = t % kWave;
+  const uint32_t mask = (1u << bits) - 1u;
+  const int digits = 1 << bits;
+  const int span = ((m + kBucketWaves - 1) / kBucketWaves + kWave - 1) /
+                   kWave * kWave;
+  const int w0 = wave * span;
+  const int w1 = w0 + span < m ? w0 + span : m;
+  const uint64_t lt = LaneMaskLt();
+  for (int v = lane; v < digits; v += kWave) wcnt[wave][v] = 0;
+  uint16_t key[kBucketWaveChunks];
+  uint16_t idx[kBucketWaveChunks];
+  uint16_t dig[kBucketWaveChunks];
+  uint16_t rank[kBucketWaveChunks];
+#pragma unroll
+  for (int c = 0; c < kBucketWaveChunks; ++c) {
+    const int i = w0 + c * kWave + lane;
+    const bool active = i < w1;
+    key[c] = active ? sk[from][i] : 0;
+    idx[c] = active ? si[from][i] : 0;
+  }
+#pragma unroll
+  for (int c = 0; c < kBucketWaveChunks; ++c) {
+    if (w0 + c * kWave >= w1) break;  // uniform: the wave's span ended
+    const bool active = w0 + c * kWave + lane < w1;
+    const uint32_t v = (static_cast<uint32_t>(key[c]) >> shift) & mask;
+    uint64_t match = __ballot(active);
+    for (int b = 0; b < bits; ++b) {
+      const uint64_t bb = __ballot((v >> b) & 1u);
+      match &= ((v >> b) & 1u) ? bb : ~bb;
+    }
+    const bool leader = active && (match & lt) == 0;
+    uint32_t before = 0;
+    if (leader) {
+      before = wcnt[wave][v];
+      wcnt[wave][v] = static_cast<uint16_t>(before + __popcll(match));
+    }
+    const int src_lane =
+        active ? __ffsll(static_cast<long long>(match)) - 1 : lane;
+    before = static_cast<uint32_t>(
+        __shfl(static_cast<int>(before), src_lane, kWave));
+    dig[c] = static_cast<uint16_t>(v);
+    rank[c] = static_cast<uint16_t>(before + __popcll(match & lt));
+  }
+  __syncthreads();
+  // Exclusive scan over cells (digit, wave), digit-major: cells 2t, 2t + 1.
+  {
+    const int c0 = 2 * t;
+    const int cells = digits * kBucketWaves;
+    uint32_t a = 0, b2 = 0;
+    if (c0 < cells) a = wcnt[c0 % kBucketWaves][c0 / kBucketWaves];
+    if (c0 + 1 < cells) b2 = wcnt[(c0 + 1) % kBucketWaves][(c0 + 1) / kBucketWaves];
+    uint32_t all;
+    const uint32_t ex =
+        BlockExclusiveScan<uint32_t, kBucketBlock>(a + b2, scan_tmp, &all);
+    if (c0 < cells) {
+      wcnt[c0 % kBucketWaves][c0 / kBucketWaves] = static_cast<uint16_t>(ex);
+    }
+    if (c0 + 1 < cells) {
+      wcnt[(c0 + 1) % kBucketWaves][(c0 + 1) / kBucketWaves] =
+          static_cast<uint16_t>(ex + a);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < kBucketWaveChunks; ++c) {
+    const int i = w0 + c * kWave + lane;
+    if (i < w1) {
+      const uint32_t pos = static_cast<uint32_t>(wcnt[wave][dig[c]]) + rank[c];
+      if (pos < static_cast<uint32_t>(m)) {
+        sk[1 - from][pos] = key[c];
+        si[1 - from][pos] = idx[c];
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// One bucket [lo, hi) of digit d, by the whole block.
+template <typename K, typename V, typename Sink>
+__device__ __forceinline__ void BucketSort(
+    const K* keys, const V* vals, const Sink& sink, int64_t lo, int64_t hi,
+    int d, int lb, uint16_t (*sk)[kBucketChunk], uint16_t (*si)[kBucketChunk],
+    uint16_t (*wcnt)[1 << kBucketDigitMax], uint32_t* next, uint16_t* head,
+    uint32_t* scan_tmp) {
+  constexpr int kPer = kBucketChunk / kBucketBlock;  // elements per thread
+  const int t = threadIdx.x;
+  const int64_t size = hi - lo;
+  const uint32_t lmask = (1u << lb) - 1u;
+  const K high = static_cast<K>(static_cast<uint64_t>(d) << lb);
+  const int values = 1 << lb;
+  const bool chunked = size > kBucketChunk;
+  if (chunked) {
+    for (int v = t; v < values; v += kBucketBlock) next[v] = 0;
+    __syncthreads();
+    for (int64_t i0 = lo; i0 < hi; i0 += kBucketBlock * kPer) {
+      K k[kPer];
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int64_t i = i0 + u * kBucketBlock + t;
+        k[u] = i < hi ? keys[i] : K{0};
+      }
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        if (i0 + u * kBucketBlock + t < hi) {
+          atomicAdd(&next[static_cast<uint32_t>(k[u]) & lmask], 1u);
+        }
+      }
+    }
+    __syncthreads();
+    // Thread t scans values [t * per, (t + 1) * per).
+    const int per = (values + kBucketBlock - 1) / kBucketBlock;
+    const int v0 = t * per;
+    uint32_t sum = 0;
+    for (int v = v0; v < v0 + per && v < values; ++v) sum += next[v];
+    uint32_t all;
+    uint32_t run =
+        BlockExclusiveScan<uint32_t, kBucketBlock>(sum, scan_tmp, &all);
+    for (int v = v0; v < v0 + per && v < values; ++v) {
+      const uint32_t c = next[v];
+      next[v] = run;
+      run += c;
+    }
+  }
+  const int b0 = lb <= kBucketDigitMax ? lb : lb / 2;
+  const int b1 = lb - b0;
+  for (int64_t c0 = lo; c0 < hi; c0 += kBucketChunk) {
+    const int m = static_cast<int>(hi - c0 < kBucketChunk ? hi - c0
+                                                          : kBucketChunk);
+    __syncthreads();  // the previous chunk is out of LDS
+    {
+      K k[kPer];
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int i = u * kBucketBlock + t;
+        k[u] = i < m ? keys[c0 + i] : K{0};
+      }
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        const int i = u * kBucketBlock + t;
+        if (i < m) {
+          sk[0][i] = static_cast<uint16_t>(static_cast<uint32_t>(k[u]) & lmask);
+          si[0][i] = static_cast<uint16_t>(i);
+        }
+      }
+    }
+    __syncthreads();
+    BucketLdsPass(sk, si, wcnt, scan_tmp, 0, m, 0, b0);
+    int cur = 1;
+    if (b1 > 0) {
+      BucketLdsPass(sk, si, wcnt, scan_tmp, 1, m, b0, b1);
+      cur = 0;
+    }
+    // Every pair of [0, m) was placed; the masks below only keep LDS and
+    // value reads in range whatever the keys hold.
+    if (chunked) {
+      for (int i = t; i < m; i += kBucketBlock) {
+        const uint32_t v = sk[cur][i] & lmask;
+        if (i == 0 || (sk[cur][i - 1] & lmask) != v) {
+          head[v] = static_cast<uint16_t>(i);
+        }
+      }
+      __syncthreads();
+    }
+    V x[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int i = u * kBucketBlock + t;
+      const int j = i < m ? si[cur][i] : m;
+      x[u] = j < m ? vals[c0 + j] : V{0};
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int i = u * kBucketBlock + t;
+      if (i < m) {
+        const uint32_t v = sk[cur][i] & lmask;
+        const int64_t rel =
+            chunked ? static_cast<int64_t>(next[v]) + (i - head[v])
+                    : (c0 - lo) + i;
+        // rel < size by construction; the test keeps every store inside the
+        // bucket whatever the keys hold.
+        if (rel < size) {
+          sink.Store(static_cast<uint32_t>(lo + rel), high | static_cast<K>(v),
+                     x[u]);
+        }
+      }
+    }
+    if (chunked) {
+      __syncthreads();
+      for (int i = t; i < m; i += kBucketBlock) {
+        const uint32_t v = sk[cur][i] & lmask;
+        if (i == m - 1 || (sk[cur][i + 1] & lmask) != v) {
+          next[v] += i - head[v] + 1;
+        }
+      }
+    }
+  }
+}
+
+template <typename K, typename V, typename Sink>
+__global__ __launch_bounds__(kBucketBlock) void RadixBucketSortK(
+    const K* keys, const V* vals, Sink sink, const uint32_t* offsets,
+    int64_t tiles, int buckets, const uint32_t* total, int lb, int64_t n,
+    bool fill_tail) {
+  __shared__ uint16_t sk[2][kBucketChunk];
+  __shared__ uint16_t si[2][kBucketChunk];
+  __shared__ uint16_t wcnt[kBucketWaves][1 << kBucketDigitMax];
+  __shared__ uint32_t next[1 << kBucketMaxBits];  // buckets of several chunks
+  __shared__ uint16_t head[1 << kBucketMaxBits];
+  __shared__ uint32_t scan_tmp[kBucketWaves + 1];
+  const int t = threadIdx.x;
+  // The three bounds load together (no store before them).
+  const int d = blockIdx.x;
+  const int64_t taken = static_cast<int64_t>(*total);
+  const int64_t lo = offsets[static_cast<int64_t>(d) * tiles];
+  const int64_t hi =
+      d + 1 < buckets ? offsets[static_cast<int64_t>(d + 1) * tiles] : taken;
+  if (hi > lo) {  // uniform: the whole block
+    BucketSort<K, V, Sink>(keys, vals, sink, lo, hi, d, lb, sk, si, wcnt,
+                           next, head, scan_tmp);
+  }
+  if (fill_tail) {
+    for (int64_t i = taken + static_cast<int64_t>(blockIdx.x) * kBucketBlock +
+                     t;
+         i < n; i += static_cast<int64_t>(gridDim.x) * kBucketBlock) {
+      sink.Fill(i);
+    }
   }
 }
 

@@ -174,8 +174,30 @@ __device__ __forceinline__ float PackedGain(uint64_t p) {
 
 // Partition of position `off` of a segment whose row pointers are `rp`
 // (partitions start at 8-aligned offsets), or -1 for padding.
+constexpr int kUniformPartitions = 16;
 __device__ __forceinline__ int PartitionOf(const int32_t* rp, int nparts,
                                            int64_t per_segment, int64_t off) {
+  if (nparts <= kUniformPartitions) {
+    // The same answer from straight-line code (a fully unrolled walk with a
+    // uniform guard): the row pointer loads are uniform (scalar), and with no
+    // loop boundary a caller's own loads of several positions stay in
+    // flight together.
+    int part = -1;
+    bool found = false;
+    int64_t start = 0;
+#pragma unroll
+    for (int q = 0; q < kUniformPartitions; ++q) {
+      if (q >= nparts) break;
+      int64_t end = rp[q];
+      if (end > per_segment) end = per_segment;
+      if (!found && off < end) {
+        part = off >= start ? q : -1;
+        found = true;
+      }
+      start = (end + kAlign - 1) / kAlign * kAlign;
+    }
+    return part;
+  }
   int64_t start = 0;
   for (int q = 0; q < nparts; ++q) {
     int64_t end = rp[q];

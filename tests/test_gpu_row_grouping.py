@@ -1,0 +1,127 @@
+"""Grouping a CSR by activation row (the CSR-only forward's sample stream).
+
+The stream must be the stable sort of the CSR's valid entries by activation
+row: each row's entries in CSR order, the order in which the oracle sums.
+Activation rows of 9 to 21 key bits take one radix pass on the top 8 bits
+and a sort of each of its 256 buckets by the low bits in one block (LDS
+passes over chunks of 8,192 entries); wider keys take the LSD passes. The
+cases below cover low-bit widths of 1 to 13 (one and two LDS passes),
+buckets of one chunk and of several (a long row, and c3-sized buckets of
+about 15,600 entries), rows of thousands of entries, empty buckets, padding
+and alignment gaps, entries outside the table, and four segments.
+Expectations come from numpy's stable argsort of the same CSR.
+"""
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+  if not torch.cuda.is_available():
+    pytest.skip("no GPU")
+  torch.cuda.set_device(0)
+
+
+from jax_tpu_embedding.sparsecore import _native  # pylint: disable=g-import-not-at-top,wrong-import-position
+from jax_tpu_embedding.sparsecore.lib.core.primitives import _device  # pylint: disable=g-import-not-at-top,wrong-import-position
+
+PAD = np.iinfo(np.int32).max
+
+
+def _csr(rng, num_sc, bps, rpp, entries, heavy=0, bad=0.0):
+  """A CSR of `num_sc` segments with `num_sc` partitions each: partition
+  entries ascending by id, 8-aligned starts, padding to the segment end.
+  `heavy` entries go to sample 3 of every segment (one long row)."""
+  parts = num_sc
+  per_part = entries // (num_sc * parts)
+  per_seg = (parts * ((per_part + heavy // parts + 7) // 8 * 8) + 64)
+  eid = np.full(num_sc * per_seg, PAD, np.int32)
+  sid = np.full(num_sc * per_seg, PAD, np.int32)
+  gains = np.full(num_sc * per_seg, np.nan, np.float32)
+  rp = np.zeros((num_sc, parts), np.int32)
+  for s in range(num_sc):
+    start = 0
+    for p in range(parts):
+      c = per_part + heavy // parts
+      ids = np.sort(rng.integers(0, rpp, size=c)).astype(np.int32)
+      if bad:
+        ids[rng.random(c) < bad] = rpp + 5
+      rows = rng.integers(0, bps, size=c).astype(np.int32)
+      if heavy:
+        rows[rng.permutation(c)[:heavy // parts]] = 3
+      o = s * per_seg + start
+      eid[o:o + c] = ids
+      sid[o:o + c] = rows
+      gains[o:o + c] = rng.uniform(0.5, 1.5, size=c).astype(np.float32)
+      rp[s, p] = start + c
+      start = (start + c + 7) // 8 * 8
+  return rp.reshape(-1), eid, sid, gains, per_seg
+
+
+def _expected(rp, eid, sid, gains, num_sc, bps, rpp, per_seg):
+  parts = rp.size // num_sc
+  keys, ents = [], []
+  g = gains.view(np.uint32).astype(np.uint64)
+  for s in range(num_sc):
+    start = 0
+    for p in range(parts):
+      end = int(rp[s * parts + p])
+      sl = slice(s * per_seg + start, s * per_seg + end)
+      e, r = eid[sl], sid[sl]
+      ok = (e >= 0) & (e < rpp) & (r >= 0) & (r < bps)
+      keys.append((s * bps + r[ok]).astype(np.int64))
+      ents.append((p * rpp + e[ok]).astype(np.uint64) | (g[sl][ok] <<
+                                                          np.uint64(32)))
+      start = (end + 7) // 8 * 8
+  keys = np.concatenate(keys)
+  ents = np.concatenate(ents)
+  order = np.argsort(keys, kind="stable")
+  return keys[order], ents[order]
+
+
+def _check(rng, num_sc, batch, entries, heavy=0, bad=0.0):
+  bps = batch // num_sc
+  rpp = 5000
+  rp, eid, sid, gains, per_seg = _csr(rng, num_sc, bps, rpp, entries, heavy,
+                                      bad)
+  keep, c = _device.csr_operands(rp, eid, sid, gains, num_sc, num_sc)
+  status = torch.zeros(1, dtype=torch.int32, device="cuda")
+  v = _native.build_sample_view(c, batch, rpp * num_sc, device_status=status)
+  torch.cuda.synchronize()
+  del keep
+  ek, ee = _expected(rp, eid, sid, gains, num_sc, bps, rpp, per_seg)
+  gk = v.keys.cpu().numpy().astype(np.int64)
+  ge = v.entries.cpu().numpy().view(np.uint64)
+  total = ek.size
+  np.testing.assert_array_equal(gk[:total], ek)
+  np.testing.assert_array_equal(ge[:total], ee)
+  assert (gk[total:] == batch).all()
+  st = int(status.item())
+  assert bool(st & _native.STATUS_BAD_ENTRY) == bool(bad), st
+
+
+# (batch, entries): keys of 9-13 bits (1-5 low bits: one LDS pass), 15, 17
+# (also with buckets of two chunks), 19, 20 and 21 bits (7-13 low bits: two
+# LDS passes), then 22 bits (LSD passes).
+@pytest.mark.parametrize("batch,entries", [
+    (300, 2000), (1000, 900), (2048, 30000), (4000, 20000), (8192, 8192),
+    (20000, 100000), (100000, 400000), (70000, 4000000), (500000, 300000),
+    (1 << 20, 300000), (1703936, 1703936), (2500000, 600000)])
+def test_stream_is_the_stable_row_sort(batch, entries):
+  _check(np.random.default_rng(batch), 1, batch, entries)
+
+
+@pytest.mark.parametrize("batch", [4000, 70000, 1703936])
+def test_long_row_spans_several_bucket_chunks(batch):
+  """Row 3 holds 150,000 entries: its bucket is sorted in 19 chunks."""
+  _check(np.random.default_rng(batch + 1), 1, batch, 50000, heavy=150000)
+
+
+@pytest.mark.parametrize("batch", [512, 131072])
+def test_four_segments_and_entries_outside_the_table(batch):
+  _check(np.random.default_rng(batch + 2), 4, batch, 80000, bad=0.05)
