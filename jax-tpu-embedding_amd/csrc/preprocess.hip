@@ -280,40 +280,76 @@ struct BlockRows {
   int64_t hi;
 };
 
-// One thread per ExtractIds block: two binary searches over the row splits,
-// run for all blocks at once before the extraction, so that an extraction
-// thread only searches the few rows its block spans.
-__device__ __forceinline__ BlockRows ComputeBlockRows(
-    const SliceDesc* slices, int num_slices, const FeatureDev* feats,
-    int64_t total_ids, int64_t blk) {
+// Where an extraction block reads from, found for all blocks at once before
+// the extraction (so that an extraction thread only searches the few rows
+// its block spans), without any search over the row splits:
+//   - the thread of block b writes its slice, or -1 when its first and last
+//     output positions lie in different slices (BlockSliceOf);
+//   - the thread of input row r of a ragged slice writes r as `lo` of every
+//     block whose first position the row covers and as `hi` of every block
+//     whose last position it covers (RowBlockBounds).
+// Each output position of a ragged slice lies in exactly one non-empty row,
+// so every single-slice block of a ragged slice gets both rows from the
+// rows' own two splits. The extraction clamps them into the slice's rows
+// (ClampBlockRows), so that rows written for other input keep its reads in
+// range.
+__device__ __forceinline__ void BlockSliceOf(const SliceDesc* slices,
+                                             int num_slices,
+                                             int64_t total_ids, int64_t blk,
+                                             BlockRows* out) {
   const int64_t first = blk * kExtractBlock;
   const int64_t last = min(first + kExtractBlock, total_ids) - 1;
-  BlockRows br{-1, 0, 0, -1};
   const int sf = FindSlice(slices, num_slices, first, false);
-  if (sf == FindSlice(slices, num_slices, last, false)) {
-    br.slice = sf;
-    const SliceDesc sl = slices[sf];
-    const int64_t* splits = feats[sl.feature].splits;
-    if (splits != nullptr) {
-      const int64_t top = sl.row_start + sl.num_rows - 1;
-      br.lo = LastRowAtOrBefore(splits, sl.row_start, top,
-                                sl.id_begin + (first - sl.out_begin));
-      br.hi = LastRowAtOrBefore(splits, br.lo, top,
-                                sl.id_begin + (last - sl.out_begin));
-    }
-  }
-  return br;
+  out[blk].slice = sf == FindSlice(slices, num_slices, last, false) ? sf : -1;
 }
 
+__device__ __forceinline__ void RowBlockBounds(const SliceDesc* slices,
+                                               int num_slices,
+                                               const FeatureDev* feats,
+                                               int64_t total_ids, int64_t gr,
+                                               BlockRows* out) {
+  const int s = FindSlice(slices, num_slices, gr, true);
+  const SliceDesc sl = slices[s];
+  const int64_t* splits = feats[sl.feature].splits;
+  if (splits == nullptr) return;
+  const int64_t r = sl.row_start + (gr - sl.row_prefix);
+  const int64_t out_end =
+      s + 1 < num_slices ? slices[s + 1].out_begin : total_ids;
+  const int64_t a = max(sl.out_begin + (splits[r] - sl.id_begin),
+                        sl.out_begin);
+  const int64_t e = min(sl.out_begin + (splits[r + 1] - sl.id_begin),
+                        out_end);
+  for (int64_t blk = a / kExtractBlock; blk * kExtractBlock < e; ++blk) {
+    const int64_t first = blk * kExtractBlock;
+    const int64_t last = min(first + kExtractBlock, total_ids) - 1;
+    if (first >= a) out[blk].lo = r;
+    if (last >= a && last < e) out[blk].hi = r;
+  }
+}
+
+// The rows [*lo, *hi] of a single-slice block, clamped into its slice.
+__device__ __forceinline__ void ClampBlockRows(const BlockRows& br,
+                                               const SliceDesc& sl,
+                                               int64_t* lo, int64_t* hi) {
+  const int64_t top = sl.row_start + sl.num_rows - 1;
+  *lo = min(max(br.lo, sl.row_start), top);
+  *hi = min(max(br.hi, *lo), top);
+}
+
+// BlockSliceOf for blocks [0, num_blocks), RowBlockBounds for rows
+// [0, total_rows).
 __global__ __launch_bounds__(256) void BlockBounds(const SliceDesc* slices,
                                                    int num_slices,
                                                    const FeatureDev* feats,
                                                    int64_t total_ids,
                                                    int64_t num_blocks,
+                                                   int64_t total_rows,
                                                    BlockRows* out) {
-  const int64_t blk = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (blk >= num_blocks) return;
-  out[blk] = ComputeBlockRows(slices, num_slices, feats, total_ids, blk);
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < num_blocks) BlockSliceOf(slices, num_slices, total_ids, i, out);
+  if (i < total_rows) {
+    RowBlockBounds(slices, num_slices, feats, total_ids, i, out);
+  }
 }
 
 // One thread per extracted id (output position o, in slice order): finds its
@@ -337,9 +373,10 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractIds(
   const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const BlockRows br = block_rows[blockIdx.x];
   const int block_slice = br.slice;
-  const int64_t row_lo = br.lo, row_hi = br.hi;
+  int64_t row_lo = 0, row_hi = -1;
   bool staged = false;
   if (block_slice >= 0) {  // uniform over the block
+    ClampBlockRows(br, slices[block_slice], &row_lo, &row_hi);
     const int64_t* sp = feats[slices[block_slice].feature].splits;
     const int64_t cnt = row_hi - row_lo + 2;
     if (sp != nullptr && cnt <= kExtractStagedSplits) {
@@ -1515,7 +1552,8 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
   const int64_t o = blk_first + threadIdx.x;
   const BlockRows br = block_rows[blockIdx.x];
   const int block_slice = br.slice;
-  const int64_t row_lo = br.lo, row_hi = br.hi;
+  int64_t row_lo = 0, row_hi = -1;
+  if (block_slice >= 0) ClampBlockRows(br, slices[block_slice], &row_lo, &row_hi);
   const bool need_div = kWeighted && combiner != 0;
   bool staged = false;       // row splits [row_lo, row_hi + 1] in s_splits
   bool ids_staged = false;   // ids (and weights) [span_b, span_e) in LDS
@@ -2176,6 +2214,7 @@ struct SetupArgs {
   int32_t num_slices;
   int64_t total_ids;
   int64_t extract_blocks;
+  int64_t total_rows;
   BlockRows* block_rows;
 };
 
@@ -2194,11 +2233,17 @@ __global__ __launch_bounds__(256) void SetupKernel(UploadChunk c,
   } else if (i < a.slice_words + a.feat_words) {
     a.feats[i - a.slice_words] = c.words[i];
   }
-  if (i < a.extract_blocks) {
-    a.block_rows[i] = ComputeBlockRows(
-        reinterpret_cast<const SliceDesc*>(c.words), a.num_slices,
-        reinterpret_cast<const FeatureDev*>(c.words + a.slice_words),
-        a.total_ids, i);
+  if (a.extract_blocks > 0) {
+    const SliceDesc* sl = reinterpret_cast<const SliceDesc*>(c.words);
+    if (i < a.extract_blocks) {
+      BlockSliceOf(sl, a.num_slices, a.total_ids, i, a.block_rows);
+    }
+    if (i < a.total_rows) {
+      RowBlockBounds(
+          sl, a.num_slices,
+          reinterpret_cast<const FeatureDev*>(c.words + a.slice_words),
+          a.total_ids, i, a.block_rows);
+    }
   }
 }
 
@@ -2288,12 +2333,13 @@ int EnqueueSetup(const scemb_feature_t* feats, int nf,
     a.num_slices = num_slices;
     a.total_ids = pl.total_ids;
     a.extract_blocks = t.extract_blocks;
+    a.total_rows = t.extract_blocks > 0 ? pl.total_rows : 0;
     a.block_rows = t.block_rows;
     const int64_t work = std::max<int64_t>(
         {int64_t{kNumCounters}, counters_off, t.num_buckets,
          a.num_split_words,
          static_cast<int64_t>((slice_bytes + feat_bytes) / 4),
-         a.extract_blocks});
+         a.extract_blocks, a.total_rows});
     hipLaunchKernelGGL(SetupKernel, dim3(CeilDiv(work, 256)), dim3(256), 0,
                        stream, c, a);
     SCEMB_LAUNCH_CHECK();
@@ -2322,9 +2368,12 @@ int EnqueueSetup(const scemb_feature_t* feats, int nf,
     SCEMB_LAUNCH_CHECK();
   }
   if (t.extract_blocks > 0) {
-    hipLaunchKernelGGL(BlockBounds, dim3(CeilDiv(t.extract_blocks, 256)),
+    hipLaunchKernelGGL(BlockBounds,
+                       dim3(CeilDiv(std::max(t.extract_blocks, pl.total_rows),
+                                    256)),
                        dim3(256), 0, stream, t.slices, num_slices, t.feats,
-                       pl.total_ids, t.extract_blocks, t.block_rows);
+                       pl.total_ids, t.extract_blocks, pl.total_rows,
+                       t.block_rows);
     SCEMB_LAUNCH_CHECK();
   }
   return 0;
