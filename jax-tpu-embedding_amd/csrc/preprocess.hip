@@ -2312,6 +2312,12 @@ int EnqueueSetup(const scemb_feature_t* feats, int nf,
   const size_t slice_bytes = sizeof(SliceDesc) * pl.slices.size();
   const size_t feat_bytes = sizeof(FeatureDev) * nf;
   const int num_slices = static_cast<int>(pl.slices.size());
+  // Rows of dense features bound no block: the row-side pass runs only when
+  // some feature is ragged.
+  bool any_ragged = false;
+  for (int f = 0; f < nf; ++f) any_ragged |= feats[f].row_splits != nullptr;
+  const int64_t bound_rows =
+      t.extract_blocks > 0 && any_ragged ? pl.total_rows : 0;
   if (slice_bytes + feat_bytes <= sizeof(UploadChunk)) {
     UploadChunk c;
     std::memcpy(c.words, pl.slices.data(), slice_bytes);
@@ -2333,7 +2339,7 @@ int EnqueueSetup(const scemb_feature_t* feats, int nf,
     a.num_slices = num_slices;
     a.total_ids = pl.total_ids;
     a.extract_blocks = t.extract_blocks;
-    a.total_rows = t.extract_blocks > 0 ? pl.total_rows : 0;
+    a.total_rows = bound_rows;
     a.block_rows = t.block_rows;
     const int64_t work = std::max<int64_t>(
         {int64_t{kNumCounters}, counters_off, t.num_buckets,
@@ -2369,10 +2375,10 @@ int EnqueueSetup(const scemb_feature_t* feats, int nf,
   }
   if (t.extract_blocks > 0) {
     hipLaunchKernelGGL(BlockBounds,
-                       dim3(CeilDiv(std::max(t.extract_blocks, pl.total_rows),
+                       dim3(CeilDiv(std::max(t.extract_blocks, bound_rows),
                                     256)),
                        dim3(256), 0, stream, t.slices, num_slices, t.feats,
-                       pl.total_ids, t.extract_blocks, pl.total_rows,
+                       pl.total_ids, t.extract_blocks, bound_rows,
                        t.block_rows);
     SCEMB_LAUNCH_CHECK();
   }
