@@ -288,6 +288,30 @@ def copy_probe(dev, gib=1):
   del a, b
 
 
+def copy_rate_gbs(dev, gib=1, reps=5):
+  """HBM bytes per second of a plain device copy of `gib` GiB (read plus
+  write), median of `reps` event-timed copies: the rate a bandwidth-bound
+  kernel of this mix can reach on this box, measured in the same run."""
+  import torch  # pylint: disable=g-import-not-at-top
+
+  n = gib * (1 << 30) // 4
+  a = torch.ones(n, dtype=torch.float32, device=dev)
+  b = torch.empty_like(a)
+  b.copy_(a)
+  times = []
+  for _ in range(reps):
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    b.copy_(a)
+    e1.record()
+    e1.synchronize()
+    times.append(e0.elapsed_time(e1) / 1e3)
+  del a, b
+  torch.cuda.empty_cache()
+  return 2 * gib * (1 << 30) / float(np.median(times)) / 1e9
+
+
 def _stack_batch_ids(w: Workload):
   """Input ids (lookups) per stack."""
   out = {}
@@ -314,6 +338,8 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
   dev = torch.device("cuda", 0)
   if probe:
     copy_probe(dev)
+  copy_gbs = copy_rate_gbs(dev)
+  log(f"device copy: {copy_gbs:.1f} GB/s")
   stacked = embedding.get_stacked_table_specs(w.feature_specs)
 
   def resident(x):
@@ -486,6 +512,7 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
       "dropped": int(sum(stats.id_drop_counters.values())),
       "optimizer_bwd_ms": opt_ms,
       "minibatching": mb,
+      "copy_gbs": copy_gbs,
   }
 
 
@@ -1020,6 +1047,9 @@ def main():
       "traffic": dom_traffic,
       "kernel_ms": round(dom_ms, 4),
       "algorithmic_bytes": int(dom_bytes),
+      # The same rate against a 1 GiB device copy timed in this run.
+      "copy_gbs": round(res["copy_gbs"], 1),
+      "copy_frac": round(achieved / res["copy_gbs"], 4),
   }
   cpu = None
   if not args.no_cpu_baseline:
@@ -1057,6 +1087,8 @@ def main():
                                      1),
       "step_hbm_frac": round((fwd_bytes + bwd_bytes) / step_s / 1e9 /
                              PEAK_HBM_GBS, 4),
+      "step_copy_frac": round((fwd_bytes + bwd_bytes) / step_s / 1e9 /
+                              res["copy_gbs"], 4),
       "algorithmic_bytes_per_step": int(fwd_bytes + bwd_bytes),
       # HIP-event time per step of each kernel (summed over stacks).
       "kernel_ms_per_step": spans,

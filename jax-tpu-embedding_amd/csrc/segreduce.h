@@ -1067,6 +1067,10 @@ __global__ __launch_bounds__(kBlock) void SegFinish(int64_t num_blocks,
   const int cl = tid % G;
   const uint32_t key = r.block_keys[blk];
   int64_t c1 = -1;
+  // Most such runs end in the next block: one uniform load settles it.
+  if (blk + 1 < num_blocks && (r.block_flags[blk + 1] & kFlagHeadEnd)) {
+    c1 = blk + 1;
+  }
   for (int64_t b0 = blk + 1; b0 < num_blocks && c1 < 0; b0 += kBlock) {
     const int64_t c = b0 + tid;
     const bool is_end = c < num_blocks && (r.block_flags[c] & kFlagHeadEnd);
@@ -1121,8 +1125,10 @@ __global__ __launch_bounds__(kBlock) void SegFinish(int64_t num_blocks,
     s_part[sub][cl] = acc;
     __syncthreads();
     if (sub == 0) {
+      // Sub-groups past the m-th took no partial row.
+      const int used = m < P ? static_cast<int>(m) : P;
       T g = s_part[0][cl];
-      for (int s = 1; s < P; ++s) g = V::Add(g, s_part[s][cl]);
+      for (int s = 1; s < used; ++s) g = V::Add(g, s_part[s][cl]);
       if (col_ok) EpilogueLoad<VEC, EPI, kMapped>(r, s_map, key, col, g, H);
     }
     __syncthreads();
