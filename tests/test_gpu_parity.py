@@ -313,6 +313,41 @@ def test_forward_long_rows_and_empty_rows(dim):
     assert not act[0].any() and not act[-1].any()
 
 
+@pytest.mark.parametrize("dim", [8, 128])
+def test_forward_runs_ending_at_block_edges(dim):
+  """Activation rows laid out so that runs of the sorted stream end exactly
+  on 256-entry block edges: a run that starts in one block and ends on the
+  last entry of the next, one that fills a block, one that spans three
+  blocks, single entries at an edge. Ids are distinct within a row, so every
+  id is one entry; integer tables make the sums exact, so the forward must
+  equal the oracle bit for bit through both routes."""
+  rng = np.random.default_rng(dim + 11)
+  lengths = [200, 312, 256, 100, 412, 600, 1, 423, 0, 255, 1, 700, 40, 216,
+             256, 257, 255]
+  batch = 48
+  lengths += [int(x) for x in rng.integers(0, 300, size=batch - len(lengths))]
+  vocab = 4096
+  _, feats = _make_specs(1, [vocab], [dim], "sum",
+                         embedding_spec.SGDOptimizerSpec(0.01), batch,
+                         max_ids=1 << 16)
+  embedding.prepare_feature_specs_for_training(feats, 1, 1)
+  arr = np.empty(batch, dtype=object)
+  for i, n in enumerate(lengths):
+    arr[i] = rng.permutation(vocab)[:n].astype(np.int32)
+  ends = np.cumsum(lengths)
+  assert 512 in ends and 1280 in ends and 2304 in ends and 2560 in ends
+  name, ref = _csr_from_oracle([arr], None, feats, 1)
+  rows = feats[0].table_spec.stacked_table_spec.stack_vocab_size
+  table = rng.integers(-4, 5, size=(rows, dim)).astype(np.float32)
+  table_t = torch.from_numpy(table).cuda()
+  exp = refcpu.sparse_dense_matmul(
+      ref.row_pointers[name], ref.embedding_ids[name], ref.sample_ids[name],
+      ref.gains[name], table, batch, num_sc_per_device=1, num_scs=1)
+  for view in (None, _view(ref, name, batch, rows, 1)):
+    act = _fwd_bind(ref, name, table_t, batch, 1, view=view).cpu().numpy()
+    np.testing.assert_array_equal(act, exp)
+
+
 def test_forward_empty_batch_is_zero():
   rng = np.random.default_rng(2)
   batch = 40
