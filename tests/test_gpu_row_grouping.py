@@ -33,13 +33,16 @@ from jax_tpu_embedding.sparsecore.lib.core.primitives import _device  # pylint: 
 PAD = np.iinfo(np.int32).max
 
 
-def _csr(rng, num_sc, bps, rpp, entries, heavy=0, bad=0.0):
+def _csr(rng, num_sc, bps, rpp, entries, heavy=0, bad=0.0, tail=0):
   """A CSR of `num_sc` segments with `num_sc` partitions each: partition
   entries ascending by id, 8-aligned starts, padding to the segment end.
-  `heavy` entries go to sample 3 of every segment (one long row)."""
+  `heavy` entries go to sample 3 of every segment (one long row). `tail`:
+  that many more positions at the end of each segment, filled with entries
+  that look valid (ids and samples in range) but lie past the last
+  partition's row pointer, where the format leaves memory unwritten."""
   parts = num_sc
   per_part = entries // (num_sc * parts)
-  per_seg = (parts * ((per_part + heavy // parts + 7) // 8 * 8) + 64)
+  per_seg = (parts * ((per_part + heavy // parts + 7) // 8 * 8) + 64 + tail)
   eid = np.full(num_sc * per_seg, PAD, np.int32)
   sid = np.full(num_sc * per_seg, PAD, np.int32)
   gains = np.full(num_sc * per_seg, np.nan, np.float32)
@@ -60,6 +63,11 @@ def _csr(rng, num_sc, bps, rpp, entries, heavy=0, bad=0.0):
       gains[o:o + c] = rng.uniform(0.5, 1.5, size=c).astype(np.float32)
       rp[s, p] = start + c
       start = (start + c + 7) // 8 * 8
+    if tail:
+      o, e = s * per_seg + start, (s + 1) * per_seg
+      eid[o:e] = rng.integers(0, rpp, size=e - o)
+      sid[o:e] = rng.integers(0, bps, size=e - o)
+      gains[o:e] = 1.0
   return rp.reshape(-1), eid, sid, gains, per_seg
 
 
@@ -84,11 +92,11 @@ def _expected(rp, eid, sid, gains, num_sc, bps, rpp, per_seg):
   return keys[order], ents[order]
 
 
-def _check(rng, num_sc, batch, entries, heavy=0, bad=0.0):
+def _check(rng, num_sc, batch, entries, heavy=0, bad=0.0, tail=0):
   bps = batch // num_sc
   rpp = 5000
   rp, eid, sid, gains, per_seg = _csr(rng, num_sc, bps, rpp, entries, heavy,
-                                      bad)
+                                      bad, tail)
   keep, c = _device.csr_operands(rp, eid, sid, gains, num_sc, num_sc)
   status = torch.zeros(1, dtype=torch.int32, device="cuda")
   v = _native.build_sample_view(c, batch, rpp * num_sc, device_status=status)
@@ -125,3 +133,13 @@ def test_long_row_spans_several_bucket_chunks(batch):
 @pytest.mark.parametrize("batch", [512, 131072])
 def test_four_segments_and_entries_outside_the_table(batch):
   _check(np.random.default_rng(batch + 2), 4, batch, 80000, bad=0.05)
+
+
+@pytest.mark.parametrize("batch,num_sc", [(20000, 1), (2500000, 1),
+                                           (131072, 4)])
+def test_entries_past_the_last_row_pointer_are_ignored(batch, num_sc):
+  """Positions past each segment's last partition hold valid-looking
+  entries (a buffer sized for more ids than the batch has, its end never
+  written): the stream takes none of them, through the bucket route
+  (batch 20,000), the LSD passes (2.5M rows) and four segments."""
+  _check(np.random.default_rng(batch + 3), num_sc, batch, 60000, tail=40000)
