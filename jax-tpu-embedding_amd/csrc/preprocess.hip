@@ -267,6 +267,17 @@ __device__ __forceinline__ int64_t LastRowAtOrBefore(const int64_t* splits,
   return lo;
 }
 
+// The same over 32-bit staged offsets (rows [0, hi]).
+__device__ __forceinline__ int LastRowAtOrBefore32(const int32_t* splits,
+                                                   int hi, int32_t target) {
+  int lo = 0;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (splits[mid] <= target) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
 constexpr int kExtractBlock = 256;
 constexpr int kExtractStagedSplits = 2 * kExtractBlock + 2;
 
@@ -1383,6 +1394,11 @@ __global__ void StoreTotal(const uint64_t* totals, int64_t* counters) {
 // which fit the staging.
 constexpr int kDedupStage = 2048;
 constexpr int64_t kDedupMaxRow = 896;
+// Rows of one ExtractUnique block whose splits (as 32-bit offsets from the
+// block's first row) and divisors are staged; blocks spanning more rows (only
+// with many empty rows) read the splits from memory. Sized so that a
+// weighted block stays under 20 KB of LDS: eight blocks per CU.
+constexpr int kUniqueStagedSplits = 448;
 static_assert(kExtractBlock + 2 * (kDedupMaxRow - 1) <= kDedupStage,
               "a block's rows must fit the staging");
 
@@ -1542,10 +1558,10 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
     int rows_of_one, KeyLayout kl, int64_t view_rows, K* keys, uint64_t* pay,
     uint32_t* view_counts, int64_t* counters) {
   constexpr bool kWeighted = !kHashed;
-  __shared__ int64_t s_splits[kExtractStagedSplits];
+  __shared__ int32_t s_splits[kUniqueStagedSplits];  // splits - span_b
   __shared__ int32_t s_ids[kDedupStage];
   __shared__ float s_w[kWeighted ? kDedupStage : 1];
-  __shared__ float s_div[kWeighted ? kExtractStagedSplits : 1];
+  __shared__ float s_div[kWeighted ? kUniqueStagedSplits : 1];
   __shared__ uint32_t s_table[kHashed ? kDedupSlots : 1];
   __shared__ uint32_t s_counts[kHashed ? kDedupSlots / 2 : 1];
   const int64_t blk_first = static_cast<int64_t>(blockIdx.x) * blockDim.x;
@@ -1556,6 +1572,7 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
   if (block_slice >= 0) ClampBlockRows(br, slices[block_slice], &row_lo, &row_hi);
   const bool need_div = kWeighted && combiner != 0;
   bool staged = false;       // row splits [row_lo, row_hi + 1] in s_splits
+                             // (relative to span_b)
   bool ids_staged = false;   // ids (and weights) [span_b, span_e) in LDS
   int64_t span_b = 0, span_e = 0;
   int64_t div_row0 = 0;      // row of s_div[0]
@@ -1568,15 +1585,16 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
     const SliceDesc bsl = slices[block_slice];
     const FeatureDev bf = feats[bsl.feature];
     if (bf.splits != nullptr) {
+      span_b = bf.splits[row_lo];
+      span_e = bf.splits[row_hi + 1];
       const int64_t cnt = row_hi - row_lo + 2;
-      if (cnt <= kExtractStagedSplits) {
+      if (cnt <= kUniqueStagedSplits) {
+        // A stack holds fewer than 2^31 ids: the offsets fit 32 bits.
         for (int64_t i = threadIdx.x; i < cnt; i += blockDim.x) {
-          s_splits[i] = bf.splits[row_lo + i];
+          s_splits[i] = static_cast<int32_t>(bf.splits[row_lo + i] - span_b);
         }
         staged = true;
       }
-      span_b = bf.splits[row_lo];
-      span_e = bf.splits[row_hi + 1];
     } else if (bf.valency > 0) {
       valency = bf.valency;
       const int64_t o_last = min(blk_first + kExtractBlock, total_ids) - 1;
@@ -1596,7 +1614,7 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
         const int64_t rows =
             valency > 0 ? (span_e - span_b) / valency
                         : (staged ? row_hi - row_lo + 1 : 0);
-        if (rows <= kExtractStagedSplits) {
+        if (rows <= kUniqueStagedSplits) {
           div_rows = static_cast<int>(rows);
           div_row0 = valency > 0 ? span_b / valency : row_lo;
         }
@@ -1619,8 +1637,8 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
   __syncthreads();
   if constexpr (kWeighted) {
     for (int t = threadIdx.x; t < div_rows; t += blockDim.x) {
-      const int64_t b = valency > 0 ? t * valency : s_splits[t] - span_b;
-      const int64_t e = valency > 0 ? b + valency : s_splits[t + 1] - span_b;
+      const int64_t b = valency > 0 ? t * valency : s_splits[t];
+      const int64_t e = valency > 0 ? b + valency : s_splits[t + 1];
       s_div[t] = RowDivisor(s_w + b, static_cast<int>(e - b), combiner);
     }
   }
@@ -1634,10 +1652,12 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
     const FeatureDev f = feats[sl.feature];
     p = sl.id_begin + (o - sl.out_begin);  // input position
     if (staged) {
-      const int64_t k = LastRowAtOrBefore(s_splits, 0, row_hi - row_lo, p);
+      const int k = LastRowAtOrBefore32(
+          s_splits, static_cast<int>(row_hi - row_lo),
+          static_cast<int32_t>(p - span_b));
       r = row_lo + k;
-      b = s_splits[k];
-      e = s_splits[k + 1];
+      b = span_b + s_splits[k];
+      e = span_b + s_splits[k + 1];
     } else if (f.splits != nullptr) {
       int64_t lo = sl.row_start, hi = sl.row_start + sl.num_rows - 1;
       if (block_slice >= 0) {
@@ -1672,7 +1692,7 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
       const uint32_t last_start =
           valency > 0
               ? static_cast<uint32_t>((tail - 1) / valency * valency)
-              : static_cast<uint32_t>(s_splits[row_hi - row_lo] - span_b);
+              : static_cast<uint32_t>(s_splits[row_hi - row_lo]);
       for (int x = threadIdx.x; x < head; x += blockDim.x) {
         DedupInsert(s_table, s_counts, s_ids, 0u, static_cast<uint32_t>(x),
                     s_ids[x]);
