@@ -180,11 +180,16 @@ class UpdateProgram:
 
 
 def _fmt(x: float) -> str:
+  """The float32 value of x in decimal with 9 significant digits, which is
+  enough for the text to parse back to the same float32 bits."""
   if math.isnan(x):
     return "0x7FC00000"
   if math.isinf(x):
     return "0x7F800000" if x > 0 else "0xFF800000"
-  return f"{x:.6e}" if x != 0 or math.copysign(1, x) > 0 else "-0.000000e+00"
+  f = float(np.float32(x))
+  if math.isinf(f):  # a finite double beyond float32's range
+    return "0x7F800000" if f > 0 else "0xFF800000"
+  return f"{f:.8e}" if f != 0 or math.copysign(1, f) > 0 else "-0.00000000e+00"
 
 
 # ---------------------------------------------------------------------------

@@ -91,6 +91,45 @@ def test_wrap_stablehlo_with_limits():
       out, np.array([10.0, 5.0, 5.0 - np.float32(0.1), 0.0], np.float32))
 
 
+def _thirds(grad, param, lr):
+  return param - (lr * np.float32(1.0 / 3.0)) * grad + np.float32(0.1)
+
+
+@pytest.mark.parametrize("lo,hi", [(-0.123456789, 0.123456789),
+                                   (-1e-30, 3.4e38), (None, 2.0 / 3.0)])
+def test_printed_constants_keep_their_float32_bits(lo, hi):
+  """lower_to_stablehlo -> parse_stablehlo -> compile keeps every constant,
+  and the clip bounds, at the float32 bits trace() gives them. Seven
+  significant digits would not: 1/3 would come back as 0x3EAAAAAA and
+  0.123456789 as 0.1234567985."""
+  traced = col.trace(_thirds, 0, 1)
+  col._clip_outputs(traced, lo, hi)  # pylint: disable=protected-access
+  text = col.lower_to_stablehlo(_thirds, 4, 0, 1, min_value=lo, max_value=hi)
+  parsed = col.parse_stablehlo(text, 0, 1)
+  want = np.asarray(traced.compile()["imm"], np.float32).view(np.uint32)
+  got = np.asarray(parsed.compile()["imm"], np.float32).view(np.uint32)
+  np.testing.assert_array_equal(got, want)
+  consts = {np.float32(imm).view(np.uint32)
+            for name, _, imm in parsed.ops if name == "constant"}
+  for v in (1.0 / 3.0, 0.1, lo, hi):
+    if v is not None:
+      assert np.float32(v).view(np.uint32) in consts, v
+  # Evaluated, the parsed module clips at exactly float32(lo) / float32(hi).
+  g = np.array([-1e6, 0.0, 1e6], np.float32)
+  t = np.zeros(3, np.float32)
+  (out,) = _run_fields(parsed.compile(), [g, t, np.float32(1.0)])
+  want = _thirds(g, t, np.float32(1.0))
+  if hi is not None:
+    want = np.minimum(want, np.float32(hi))
+  if lo is not None:
+    want = np.maximum(want, np.float32(lo))
+  np.testing.assert_array_equal(out.view(np.uint32), want.view(np.uint32))
+  if hi is not None and hi < 1.0:
+    assert out[0] == np.float32(hi)
+  if lo is not None and lo > -1.0:
+    assert out[2] == np.float32(lo)
+
+
 # --- the register program ----------------------------------------------------
 
 def _op(code, x, y, z, imm):
