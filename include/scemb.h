@@ -410,7 +410,11 @@ typedef struct scemb_feature {
   /* With row_splits: the most ids of one row, or 0 when not known (the
    * library then reads it off the row splits). A hint that picks the
    * grouping route (scemb_preprocess_options_t.flags); any value gives the
-   * same outputs. */
+   * same outputs. An understated hint costs time, not correctness: a row of
+   * more than 896 ids then goes through the route that merges duplicates at
+   * extraction, where its duplicate scan runs from global memory and grows
+   * with the square of the row length (about 10^10 loads for one row of
+   * 10^5 ids). Pass 0 rather than a guess. */
   int64_t max_row_length;
 } scemb_feature_t;
 

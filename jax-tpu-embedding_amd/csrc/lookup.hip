@@ -140,7 +140,8 @@ struct StreamSink {
 // which also fills the positions past the entries. Same result as the LSD
 // passes: each bucket's elements arrive in CSR order and keep it.
 int GroupByRowInBuckets(const CsrRowSource& src, int64_t n,
-                        const uint32_t* n_dev, int bits, int64_t batch,
+                        const uint32_t* n_dev, int n_dev_words, int bits,
+                        int64_t batch,
                         const SortBuffers& b, Arena& ws, hipStream_t stream) {
   using radix::kSortBlock;
   using radix::kSortTile;
@@ -158,7 +159,7 @@ int GroupByRowInBuckets(const CsrRowSource& src, int64_t n,
   if (!measuring) {
     hipLaunchKernelGGL((radix::RadixHistogramK<uint32_t, CsrRowSource>),
                        dim3(tiles), dim3(kSortBlock), 0, stream, src, n,
-                       n_dev, lb, mask, tiles, hist);
+                       n_dev, n_dev_words, lb, mask, tiles, hist);
     SCEMB_LAUNCH_CHECK();
   }
   const int st = ExclusiveScan<uint32_t>(hist, hist, tiles * buckets, total,
@@ -168,8 +169,8 @@ int GroupByRowInBuckets(const CsrRowSource& src, int64_t n,
   hipLaunchKernelGGL(
       (radix::RadixScatterK<uint32_t, uint64_t, CsrRowSource,
                             radix::ArraySink<uint32_t, uint64_t>>),
-      dim3(tiles), dim3(kSortBlock), 0, stream, src, mid, n, n_dev, lb,
-      mask, hb, tiles, hist, total, false);
+      dim3(tiles), dim3(kSortBlock), 0, stream, src, mid, n, n_dev,
+      n_dev_words, lb, mask, hb, tiles, hist, total, false);
   SCEMB_LAUNCH_CHECK();
   const StreamSink sink{b.keys, b.pay, static_cast<uint32_t>(batch)};
   hipLaunchKernelGGL(
@@ -187,21 +188,24 @@ int GroupByRow(const scemb_csr_t* csr, const Geometry& geo, int64_t batch,
   using radix::kSortTile;
   using Arr = radix::ArraySource<uint32_t, uint64_t>;
   const int64_t n = geo.n;
-  // With one segment, no entry lies past the last partition's row pointer
-  // (partitions follow each other in order): the passes over the CSR read
-  // that word as their position bound, so a buffer sized for more ids than
-  // the batch holds is not walked to its end.
+  // With one segment, no entry lies at or past the largest of the segment's
+  // row pointers (the last one, unless they decrease): the passes over the
+  // CSR read those words and bound their positions by the largest, so a
+  // buffer sized for more ids than the batch holds is not walked to its end.
+  // The backward's walk (PartitionOf over every position) takes the same
+  // entries, whatever the row pointers' order.
+  const bool one_segment = csr->num_segments == 1 && csr->num_minibatches == 0;
   const uint32_t* csr_end =
-      csr->num_segments == 1 && csr->num_minibatches == 0
-          ? reinterpret_cast<const uint32_t*>(csr->row_pointers +
-                                              csr->num_partitions - 1)
-          : nullptr;
+      one_segment ? reinterpret_cast<const uint32_t*>(csr->row_pointers)
+                  : nullptr;
+  const int csr_end_words = one_segment ? csr->num_partitions : 0;
   const int bits = batch > 1 ? BitWidth(static_cast<uint64_t>(batch - 1)) : 1;
   if (bits > radix::kMaxDigitBits &&
       bits <= radix::kMaxDigitBits + radix::kBucketMaxBits) {
     const CsrRowSource src{MakeCsr(csr), geo.bps, geo.rows_per_partition,
                            status};
-    return GroupByRowInBuckets(src, n, csr_end, bits, batch, b, ws, stream);
+    return GroupByRowInBuckets(src, n, csr_end, csr_end_words, bits, batch, b,
+                               ws, stream);
   }
   const radix::DigitPlan plan = radix::PlanDigits(bits);
   const int64_t tiles = CeilDiv(n, kSortTile);
@@ -233,11 +237,12 @@ int GroupByRow(const scemb_csr_t* csr, const Geometry& geo, int64_t batch,
       if (first) {
         hipLaunchKernelGGL((radix::RadixHistogramK<uint32_t, CsrRowSource>),
                            dim3(tiles), dim3(kSortBlock), 0, stream, csr_src,
-                           n, csr_end, shift, mask, tiles, hist);
+                           n, csr_end, csr_end_words, shift, mask, tiles,
+                           hist);
       } else {
         hipLaunchKernelGGL((radix::RadixHistogramK<uint32_t, Arr>),
                            dim3(tiles), dim3(kSortBlock), 0, stream, arr, n,
-                           taken, shift, mask, tiles, hist);
+                           taken, 1, shift, mask, tiles, hist);
       }
       SCEMB_LAUNCH_CHECK();
     }
@@ -250,11 +255,12 @@ int GroupByRow(const scemb_csr_t* csr, const Geometry& geo, int64_t batch,
             (radix::RadixScatterK<uint32_t, uint64_t, CsrRowSource,
                                   StreamSink>),
             dim3(tiles), dim3(kSortBlock), 0, stream, csr_src, sink, n,
-            csr_end, shift, mask, pbits, tiles, hist, totals + pass, last);
+            csr_end, csr_end_words, shift, mask, pbits, tiles, hist,
+            totals + pass, last);
       } else {
         hipLaunchKernelGGL(
             (radix::RadixScatterK<uint32_t, uint64_t, Arr, StreamSink>),
-            dim3(tiles), dim3(kSortBlock), 0, stream, arr, sink, n, taken,
+            dim3(tiles), dim3(kSortBlock), 0, stream, arr, sink, n, taken, 1,
             shift, mask, pbits, tiles, hist, totals + pass, last);
       }
       SCEMB_LAUNCH_CHECK();

@@ -2859,11 +2859,11 @@ int RunUniquePipeline(const scemb_feature_t* feats, int nf,
       if (pass == 0) {
         hipLaunchKernelGGL((radix::RadixHistogramK<K, UniqueSource<K>>),
                            dim3(tiles), dim3(kSortBlock), 0, stream, first_src,
-                           M, nullptr, shift, mask, tiles, hist);
+                           M, nullptr, 0, shift, mask, tiles, hist);
       } else {
         hipLaunchKernelGGL((radix::RadixHistogramK<K, Arr>), dim3(tiles),
-                           dim3(kSortBlock), 0, stream, arr, M, totals, shift,
-                           mask, tiles, hist);
+                           dim3(kSortBlock), 0, stream, arr, M, totals, 1,
+                           shift, mask, tiles, hist);
       }
       SCEMB_LAUNCH_CHECK();
     }
@@ -2874,11 +2874,11 @@ int RunUniquePipeline(const scemb_feature_t* feats, int nf,
         hipLaunchKernelGGL(
             (radix::RadixScatterK<K, uint64_t, UniqueSource<K>, Sink>),
             dim3(tiles), dim3(kSortBlock), 0, stream, first_src, sink, M,
-            nullptr, shift, mask, pbits, tiles, hist, totals + pass, false);
+            nullptr, 0, shift, mask, pbits, tiles, hist, totals + pass, false);
       } else {
         hipLaunchKernelGGL((radix::RadixScatterK<K, uint64_t, Arr, Sink>),
                            dim3(tiles), dim3(kSortBlock), 0, stream, arr, sink,
-                           M, totals, shift, mask, pbits, tiles, hist,
+                           M, totals, 1, shift, mask, pbits, tiles, hist,
                            totals + pass, false);
       }
       SCEMB_LAUNCH_CHECK();

@@ -60,11 +60,19 @@ struct ArraySink {
   __device__ void Fill(int64_t) const {}
 };
 
-// Positions [0, n) of the source, or [0, min(n, *n_dev)) when n_dev is set.
+// Positions [0, n) of the source, or [0, min(n, max(n_dev[0, words)))) when
+// n_dev is set: one device count (words = 1), or a segment's row pointers,
+// whose largest value bounds the positions any partition covers whatever
+// their order.
 __device__ __forceinline__ int64_t ActiveCount(int64_t n,
-                                               const uint32_t* n_dev) {
+                                               const uint32_t* n_dev,
+                                               int words) {
   if (n_dev == nullptr) return n;
-  const int64_t m = static_cast<int64_t>(*n_dev);
+  int64_t m = 0;
+  for (int w = 0; w < words; ++w) {
+    const int64_t v = static_cast<int64_t>(n_dev[w]);
+    m = v > m ? v : m;
+  }
   return m < n ? m : n;
 }
 
@@ -72,13 +80,13 @@ __device__ __forceinline__ int64_t ActiveCount(int64_t n,
 // the source declines go to src.Rejected after all loads are issued.
 template <typename K, typename Src>
 __global__ __launch_bounds__(kSortBlock) void RadixHistogramK(
-    Src src, int64_t n, const uint32_t* n_dev, int shift, uint32_t mask,
-    int64_t tiles, uint32_t* hist) {
+    Src src, int64_t n, const uint32_t* n_dev, int n_dev_words, int shift,
+    uint32_t mask, int64_t tiles, uint32_t* hist) {
   __shared__ uint32_t h[kMaxRadix];
   const int radix = static_cast<int>(mask) + 1;
   for (int d = threadIdx.x; d < radix; d += kSortBlock) h[d] = 0;
   __syncthreads();
-  const int64_t m = ActiveCount(n, n_dev);
+  const int64_t m = ActiveCount(n, n_dev, n_dev_words);
   const int64_t tile = blockIdx.x;
   const int64_t base = tile * kSortTile;
   const int digit_bits = __popc(mask);
@@ -136,8 +144,8 @@ constexpr int kWaveChunks = kWaveSpan / kWave;      // 8 chunks of 64
 
 template <typename K, typename V, typename Src, typename Sink>
 __global__ __launch_bounds__(kSortBlock) void RadixScatterK(
-    Src src, Sink sink, int64_t n, const uint32_t* n_dev, int shift,
-    uint32_t mask, int digit_bits, int64_t tiles, const uint32_t* offsets,
+    Src src, Sink sink, int64_t n, const uint32_t* n_dev, int n_dev_words,
+    int shift, uint32_t mask, int digit_bits, int64_t tiles, const uint32_t* offsets,
     const uint32_t* total, bool fill_tail) {
   __shared__ uint32_t wave_cnt[kSortWaves][kMaxRadix];
   __shared__ uint32_t global_off[kMaxRadix];  // bucket start (output)
@@ -158,7 +166,7 @@ __global__ __launch_bounds__(kSortBlock) void RadixScatterK(
       if (i >= taken) sink.Fill(i);
     }
   }
-  const int64_t m = ActiveCount(n, n_dev);
+  const int64_t m = ActiveCount(n, n_dev, n_dev_words);
   if (base >= m) return;  // uniform: the whole block
   const int tile_n =
       static_cast<int>(m - base < kSortTile ? m - base : kSortTile);

@@ -207,7 +207,7 @@ int RadixSortPairs(K* keys, V* vals, K* keys_alt, V* vals_alt, int64_t n,
     if (!measuring) {
       hipLaunchKernelGGL((radix::RadixHistogramK<K, radix::ArraySource<K, V>>),
                          dim3(tiles), dim3(kSortBlock), 0, stream, src, n,
-                         nullptr, shift, mask, tiles, hist);
+                         nullptr, 0, shift, mask, tiles, hist);
       SCEMB_LAUNCH_CHECK();
     }
     const int st = ExclusiveScan<uint32_t>(hist, hist, cells, total, ws,
@@ -218,7 +218,7 @@ int RadixSortPairs(K* keys, V* vals, K* keys_alt, V* vals_alt, int64_t n,
       hipLaunchKernelGGL(
           (radix::RadixScatterK<K, V, radix::ArraySource<K, V>,
                                 radix::ArraySink<K, V>>),
-          dim3(tiles), dim3(kSortBlock), 0, stream, src, sink, n, nullptr,
+          dim3(tiles), dim3(kSortBlock), 0, stream, src, sink, n, nullptr, 0,
           shift, mask, bits, tiles, hist, total, false);
       SCEMB_LAUNCH_CHECK();
     }

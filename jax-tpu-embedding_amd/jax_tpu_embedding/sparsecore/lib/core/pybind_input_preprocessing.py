@@ -173,14 +173,15 @@ class _DeviceFeature:
   nnz: int
   valency: int
   max_id: int | None  # known when the input came from host memory
-  max_row_length: int = 0  # most ids of one row (0: not known)
+  max_row_length: int | None = None  # most ids of one row (None: not known)
 
   @property
   def one_id_per_row(self) -> bool:
-    """No row holds two ids."""
+    """No row holds two ids. False for ragged rows whose longest length is
+    not known yet (row splits staged but not checked)."""
     if self.splits_host is None:
       return self.valency <= 1
-    return self.max_row_length <= 1
+    return self.max_row_length is not None and self.max_row_length <= 1
 
 
 def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
@@ -223,7 +224,7 @@ def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
     if uploads is not None:
       # Checked while staged (flush); the longest row comes back then.
       splits_dev = uploads.add_row_splits(splits, int(vals.shape[0]))
-      max_len = 0
+      max_len = None
     else:
       max_len = _check_row_splits(splits, int(vals.shape[0]))
       splits_dev = on_device(splits, t.int64)
@@ -348,7 +349,7 @@ def _preprocess_stack(feats, metas, *, local_device_count,
         _native.ptr(f.ids), _native.ptr(f.weights), _native.ptr(f.splits),
         None if f.splits_host is None else f.splits_host.ctypes.data,
         f.num_rows, f.nnz, f.valency, m.row_offset, m.col_offset, m.col_shift,
-        f.max_row_length)
+        f.max_row_length or 0)
   need = lib.scemb_preprocess_workspace_size(structs, len(feats),
                                              ctypes.byref(opts))
   if need == 0:
@@ -680,10 +681,7 @@ def one_id_per_row(pending) -> dict:
   for name, *_, feats in pending:
     ok = True
     for f in feats:
-      if f.splits_host is not None:
-        ok = ok and f.one_id_per_row
-      else:
-        ok = ok and f.valency <= 1
+      ok = ok and f.one_id_per_row
     out[name] = ok
   return out
 

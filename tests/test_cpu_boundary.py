@@ -254,3 +254,20 @@ def test_device_status_decoding():
     _native.check_status_word(None, "op")
   finally:
     _native.set_validation(prev)
+
+
+def test_unknown_row_length_is_not_one_id_per_row():
+  """A ragged feature whose longest row is not known yet (row splits
+  staged, not checked) is not declared one id per row; 0 and 1 known ids
+  per row are; a dense feature follows its valency."""
+  splits = np.array([0, 1, 3], np.int64)
+  kw = dict(ids=None, weights=None, splits=None, splits_host=splits,
+            num_rows=2, nnz=3, valency=0, max_id=None)
+  assert not pip._DeviceFeature(**kw).one_id_per_row  # pylint: disable=protected-access
+  assert not pip._DeviceFeature(**kw, max_row_length=2).one_id_per_row  # pylint: disable=protected-access
+  assert pip._DeviceFeature(**kw, max_row_length=1).one_id_per_row  # pylint: disable=protected-access
+  assert pip._DeviceFeature(**kw, max_row_length=0).one_id_per_row  # pylint: disable=protected-access
+  kw.update(splits_host=None, valency=1)
+  assert pip._DeviceFeature(**kw).one_id_per_row  # pylint: disable=protected-access
+  kw.update(valency=3)
+  assert not pip._DeviceFeature(**kw).one_id_per_row  # pylint: disable=protected-access

@@ -143,3 +143,48 @@ def test_entries_past_the_last_row_pointer_are_ignored(batch, num_sc):
   written): the stream takes none of them, through the bucket route
   (batch 20,000), the LSD passes (2.5M rows) and four segments."""
   _check(np.random.default_rng(batch + 3), num_sc, batch, 60000, tail=40000)
+
+
+@pytest.mark.parametrize("batch", [5000, 2500000])
+def test_decreasing_row_pointers_forward_and_backward_agree(batch):
+  """Row pointers that decrease (one segment, four partitions: 1600, 800,
+  3200, 2400). A position belongs to the first partition whose row pointer
+  lies past it, unless it falls in that partition's alignment gap, so the
+  entries are positions [0, 1600) (partition 0) and [1600, 3200)
+  (partition 2), and [3200, 4096) is padding. The CSR-only forward bounds
+  its passes by the largest row pointer, not the last: it must take the
+  same entries as the backward, which walks every position. Integer tables,
+  gains and gradients make both sums exact, so the forward and the SGD
+  update are compared bit for bit with numpy over those entries, through
+  the bucket route (batch 5,000) and the LSD passes (2.5M rows)."""
+  rng = np.random.default_rng(batch + 4)
+  parts, rpp, dim, per_seg = 4, 3000, 8, 4096
+  rp = np.array([1600, 800, 3200, 2400], np.int32)
+  eid = np.sort(rng.integers(0, rpp, size=per_seg)).astype(np.int32)
+  eid[1600:3200] = np.sort(rng.integers(0, rpp, size=1600))
+  sid = rng.integers(0, batch, size=per_seg).astype(np.int32)
+  gains = rng.integers(1, 4, size=per_seg).astype(np.float32)
+  table = rng.integers(-8, 9, size=(parts * rpp, dim)).astype(np.float32)
+  grad = rng.integers(-4, 5, size=(batch, dim)).astype(np.float32)
+  part = np.full(per_seg, -1)
+  part[:1600] = 0
+  part[1600:3200] = 2
+  ok = part >= 0
+  rows = part[ok] * rpp + eid[ok]
+  exp_act = np.zeros((batch, dim), np.float64)
+  np.add.at(exp_act, sid[ok], gains[ok, None] * table[rows])
+  exp_table = table.astype(np.float64)
+  np.add.at(exp_table, rows, -gains[ok, None] * grad[sid[ok]])
+  keep, c = _device.csr_operands(rp, eid, sid, gains, 1, parts)
+  status = torch.zeros(1, dtype=torch.int32, device="cuda")
+  table_t = torch.from_numpy(table).cuda()
+  act = torch.zeros((batch, dim), dtype=torch.float32, device="cuda")
+  _native.sparse_dense_matmul(c, table_t, act, batch, device_status=status)
+  _native.sparse_dense_matmul_grad(c, torch.from_numpy(grad).cuda(), table_t,
+                                   None, 1.0, batch, device_status=status)
+  torch.cuda.synchronize()
+  del keep
+  assert int(status.item()) == 0
+  np.testing.assert_array_equal(act.cpu().numpy(), exp_act.astype(np.float32))
+  np.testing.assert_array_equal(table_t.cpu().numpy(),
+                                exp_table.astype(np.float32))
