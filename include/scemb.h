@@ -219,6 +219,29 @@ int scemb_sparse_dense_matmul_to_blocks(
     int64_t device_batch_size, void* workspace, size_t workspace_bytes,
     uint32_t* device_status, void* stream);
 
+/* ---- SparseActivationsUnstackInterleaved --------------------------------
+ * Replaces the custom call of tpu_sparse_dense_matmul_activation_unstack_
+ * primitive (lib/core/primitives/sparse_dense_matmul_activation_unstack.py:
+ * 64-96 of the reference). For each block, stacked rows [first_row,
+ * first_row + num_rows), columns [0, width), of `stacked` ([rows, dim]
+ * row-major) are copied to the block's rows. With several SparseCores a
+ * feature takes one block per SparseCore (its slice of each segment); blocks
+ * may come in any order and any number. Only enqueues on `stream`. */
+int scemb_activation_unstack(const float* stacked, int64_t rows, int32_t dim,
+                             const scemb_row_block_t* blocks,
+                             int32_t num_blocks, void* stream);
+
+/* ---- SparseGradientsStackInterleaved ------------------------------------
+ * Replaces the custom call of tpu_sparse_dense_matmul_gradient_stack_
+ * primitive (lib/core/primitives/sparse_dense_matmul_gradient_stack.py:
+ * 46-86 of the reference). Writes every row of `stacked` ([rows, dim]
+ * row-major): a row of a block gets the block's first `width` columns and
+ * zeros after them; a row in no block is zero. Blocks must not overlap.
+ * Only enqueues on `stream`. */
+int scemb_gradient_stack(const scemb_row_block_t* blocks, int32_t num_blocks,
+                         float* stacked, int64_t rows, int32_t dim,
+                         void* stream);
+
 /* Builds the sample view of a CSR into keys[coo_size] / entries[coo_size]
  * (device memory owned by the caller). Invalid entries are flagged as in the
  * forward pass and left out of the view. */

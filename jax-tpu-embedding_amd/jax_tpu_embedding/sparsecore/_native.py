@@ -55,6 +55,8 @@ EXPORTED_SYMBOLS = (
     "scemb_sparse_dense_matmul",
     "scemb_sparse_dense_matmul_no_alloc",
     "scemb_sparse_dense_matmul_to_blocks",
+    "scemb_activation_unstack",
+    "scemb_gradient_stack",
     "scemb_build_sample_view_workspace_size",
     "scemb_build_sample_view",
     "scemb_sparse_dense_matmul_grad_workspace_size",
@@ -274,6 +276,10 @@ def load_library() -> ctypes.CDLL:
     lib.scemb_sparse_dense_matmul_grad_with_adagrad_from_blocks.argtypes = [
         csr_p, blk_p, i32, i64, vp, vp, i64, i32, vp, f32, i32, f32, f32, vp,
         sz, vp, vp]
+    lib.scemb_activation_unstack.restype = ctypes.c_int
+    lib.scemb_activation_unstack.argtypes = [vp, i64, i32, blk_p, i32, vp]
+    lib.scemb_gradient_stack.restype = ctypes.c_int
+    lib.scemb_gradient_stack.argtypes = [blk_p, i32, vp, i64, i32, vp]
     lib.scemb_build_sample_view_workspace_size.restype = sz
     lib.scemb_build_sample_view_workspace_size.argtypes = [csr_p, i64, i64]
     lib.scemb_build_sample_view.restype = ctypes.c_int
@@ -833,6 +839,26 @@ def sparse_dense_matmul_to_blocks(csr: Csr | None, table, blocks, batch: int,
   check(lib.scemb_sparse_dense_matmul_to_blocks(
       csr_ref, vs_ref, ptr(table), rows, dim, arr, n, batch, ptr(ws),
       ws.numel(), ptr(device_status), stream_handle()))
+
+
+def activation_unstack(stacked, blocks) -> None:
+  """Copies each block's stacked rows (first `width` columns) out of the
+  [rows, dim] CUDA float32 matrix `stacked` into the block's tensor;
+  `blocks` as for row_blocks."""
+  arr, n = row_blocks(blocks)
+  check(load_library().scemb_activation_unstack(
+      ptr(stacked), int(stacked.shape[0]), int(stacked.shape[1]), arr, n,
+      stream_handle()))
+
+
+def gradient_stack(blocks, stacked) -> None:
+  """Writes every row of the [rows, dim] CUDA float32 matrix `stacked`: a
+  block's rows from its tensor's first `width` columns (zeros after them),
+  rows in no block zero; `blocks` as for row_blocks."""
+  arr, n = row_blocks(blocks)
+  check(load_library().scemb_gradient_stack(
+      arr, n, ptr(stacked), int(stacked.shape[0]), int(stacked.shape[1]),
+      stream_handle()))
 
 
 def _lr_args(learning_rate):

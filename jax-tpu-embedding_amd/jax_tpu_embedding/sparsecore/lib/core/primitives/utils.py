@@ -126,21 +126,45 @@ def validate_abstract_eval_params(
         f" {min_value} and {max_value}")
 
 
+class ShapedArray(tuple):
+  """Shape and dtype of a result (jax.core.ShapedArray's two fields)."""
+
+  def __new__(cls, shape, dtype):
+    return super().__new__(cls, (tuple(int(d) for d in shape),
+                                 np.dtype(dtype)))
+
+  @property
+  def shape(self):
+    return self[0]
+
+  @property
+  def dtype(self):
+    return self[1]
+
+
 class Primitive:
   """Named operation with a ``bind`` entry point, like jex.core.Primitive.
 
   ``bind`` validates operands and runs the HIP implementation eagerly on the
-  current torch stream.
+  current torch stream. ``abstract_eval`` (when the primitive defines one)
+  gives the results' ShapedArrays from the operands' shapes alone, without a
+  device.
   """
 
-  multiple_results = False
-
-  def __init__(self, name: str, impl):
+  def __init__(self, name: str, impl, abstract_eval=None,
+               multiple_results: bool = False):
     self.name = name
     self._impl = impl
+    self._abstract_eval = abstract_eval
+    self.multiple_results = multiple_results
 
   def bind(self, *args, **kwargs):
     return self._impl(*args, **kwargs)
+
+  def abstract_eval(self, *args, **kwargs):
+    if self._abstract_eval is None:
+      raise NotImplementedError(f"{self.name} has no abstract evaluation")
+    return self._abstract_eval(*args, **kwargs)
 
   def __repr__(self):
     return self.name

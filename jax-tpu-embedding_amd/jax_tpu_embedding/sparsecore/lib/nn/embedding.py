@@ -25,7 +25,10 @@ from jax_tpu_embedding.sparsecore import _native
 from jax_tpu_embedding.sparsecore import _tree
 from jax_tpu_embedding.sparsecore.lib.core import pybind_input_preprocessing
 from jax_tpu_embedding.sparsecore.lib.core.primitives import _device
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_activation_unstack
 from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_csr
+from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_gradient_stack
+from jax_tpu_embedding.sparsecore.lib.core.primitives import utils as prim_utils
 from jax_tpu_embedding.sparsecore.lib.nn import custom_optimizer_lowering
 from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec
 from jax_tpu_embedding.sparsecore.lib.nn import table_stacking
@@ -272,6 +275,47 @@ def compute_coo_buffer_size_per_device(feature_specs, global_device_count: int,
       global_device_count=global_device_count,
       num_sc_per_device=_get_num_sc_per_device(num_sc_per_device),
       enable_minibatching=enable_minibatching)
+
+
+# Shape and dtype of an array that is not materialised (the two fields of
+# jax.ShapeDtypeStruct).
+ShapeDtypeStruct = prim_utils.ShapedArray
+
+
+def eval_preprocess_sparse_dense_matmul_input_shape(
+    feature_specs, local_device_count: int, global_device_count: int, *,
+    num_sc_per_device: int | None = None, has_leading_dimension: bool = False,
+    enable_minibatching: bool = False) -> PreprocessedInput:
+  """Shapes and dtypes of preprocess_sparse_dense_matmul_input's outputs
+  from the specs alone, without input tensors or a device
+  (embedding.py:822-900): per stacked table the row pointers, embedding ids,
+  sample ids and gains as flat `(local_device_count * size,)` arrays (the
+  COO size from compute_coo_buffer_size_per_device, the row-pointer size
+  from compute_row_pointers_size_per_device, 64 times larger with
+  minibatching), and the minibatch counts as `(local_device_count,)` int32,
+  `(local_device_count, 1)` with `has_leading_dimension`. The leaves are
+  ShapeDtypeStruct records in a PreprocessedInput."""
+  coo = compute_coo_buffer_size_per_device(
+      feature_specs, global_device_count, num_sc_per_device=num_sc_per_device,
+      enable_minibatching=enable_minibatching)
+  rp_size = compute_row_pointers_size_per_device(
+      global_device_count=global_device_count,
+      num_sc_per_device=num_sc_per_device,
+      enable_minibatching=enable_minibatching)
+
+  def flat(size, dtype):
+    return ShapeDtypeStruct((local_device_count * size,), dtype)
+
+  nmb = ShapeDtypeStruct(
+      (local_device_count, 1) if has_leading_dimension else
+      (local_device_count,), np.int32)
+  return PreprocessedInput(
+      sparse_dense_matmul_input=SparseDenseMatmulInput(
+          lhs_row_pointers={k: flat(rp_size, np.int32) for k in coo},
+          lhs_embedding_ids={k: flat(n, np.int32) for k, n in coo.items()},
+          lhs_sample_ids={k: flat(n, np.int32) for k, n in coo.items()},
+          lhs_gains={k: flat(n, np.float32) for k, n in coo.items()}),
+      num_minibatches=nmb)
 
 
 def sharding_strategy_to_enum(sharding_strategy: str):
@@ -592,11 +636,46 @@ def _gradient_blocks(stack_spec, items, num_sc_per_device: int,
   return _device.RowBlocks(rows, stack_spec.stack_embedding_dim, blocks)
 
 
+def _unstack_activations_with_primitive(activations, feature_specs,
+                                        global_device_count: int,
+                                        num_sc_per_device: int):
+  """Unstacking through tpu_sparse_dense_matmul_activation_unstack_primitive
+  (embedding.py:971-1028): one call per stacked table over its features in
+  row-offset order, each feature at its table's embedding dim."""
+  flat, treedef = _tree.tree_flatten(feature_specs)
+  out = [None] * len(flat)
+  by_stack = collections.defaultdict(list)
+  for i, fs in enumerate(flat):
+    if any(d is None for d in fs.output_shape):
+      raise ValueError(
+          f"Feature {fs.name} has dynamic output shape {fs.output_shape}, "
+          "which is not supported.")
+    by_stack[fs.table_spec.stacked_table_spec.stack_name].append((i, fs))
+  for name, items in by_stack.items():
+    items.sort(key=lambda x: x[1].id_transformation.row_offset)
+    batches = tuple(int(np.prod(fs.output_shape[:-1])) // global_device_count
+                    for _, fs in items)
+    dims = tuple(fs.table_spec.embedding_dim for _, fs in items)
+    acts = (sparse_dense_matmul_activation_unstack
+            .tpu_sparse_dense_matmul_activation_unstack_primitive.bind(
+                activations[name], per_feature_batch_sizes=batches,
+                per_feature_dims=dims, num_sc_per_device=num_sc_per_device))
+    for (i, _), a in zip(items, acts):
+      out[i] = a
+  return _tree.tree_unflatten(treedef, out)
+
+
 def unstack_embedding_activations(activations, feature_specs,
                                   global_device_count: int,
                                   num_sc_per_device: int,
                                   use_activation_unstack_primitive=False):
-  del use_activation_unstack_primitive
+  """Per-feature activations from the stacked ones (embedding.py:1031-1044):
+  views of the stacked activations, or with
+  `use_activation_unstack_primitive` new tensors copied out by the
+  unstacking primitive."""
+  if use_activation_unstack_primitive:
+    return _unstack_activations_with_primitive(
+        activations, feature_specs, global_device_count, num_sc_per_device)
   return _tree.tree_map(
       lambda fs: _get_activation_for_feature(fs, activations,
                                              global_device_count,
@@ -636,7 +715,8 @@ def tpu_sparse_dense_matmul(preprocessed_inputs, embedding_variables,
     ev = embedding_variables[name]
     table = ev.table if isinstance(ev, EmbeddingVariables) else ev[0]
     fused = None
-    if perform_unstacking and len(getattr(table, "shape", ())) == 2:
+    if (perform_unstacking and not use_activation_unstack_primitive and
+        len(getattr(table, "shape", ())) == 2):
       # Unstacking fused into the kernel: activation rows go straight to
       # the per-feature outputs.
       fused = _activation_blocks(spec, by_stack[name], global_device_count,
@@ -711,9 +791,14 @@ def stack_embedding_gradients(activation_gradients, feature_specs,
                               num_sc_per_device: int,
                               global_device_count: int | None = None,
                               use_gradient_stacking_primitive: bool = False):
-  """Per-feature gradients -> one [B_stack, D] gradient per stack."""
-  del global_device_count, use_gradient_stacking_primitive
+  """Per-feature gradients -> one [B_stack, D] gradient per stack
+  (embedding.py:1220-1294): a concatenation per SparseCore slice, or with
+  `use_gradient_stacking_primitive` one call of the stacking primitive per
+  stacked table."""
   t = _native.torch()
+  if use_gradient_stacking_primitive and global_device_count is None:
+    raise ValueError("global_device_count must be provided when "
+                     "use_gradient_stacking_primitive is True")
   by_stack = collections.defaultdict(list)
   for g, fs in zip(_tree.tree_leaves(activation_gradients),
                    _tree.tree_leaves(feature_specs)):
@@ -725,9 +810,19 @@ def stack_embedding_gradients(activation_gradients, feature_specs,
   f = num_sc_per_device
   for name, items in by_stack.items():
     items.sort(key=lambda x: x[0].id_transformation.row_offset)
+    grads = [_prepare_gradient_for_stacking(g, fs, f) for fs, g in items]
+    if use_gradient_stacking_primitive:
+      spec = items[0][0].table_spec.stacked_table_spec
+      out[name] = (sparse_dense_matmul_gradient_stack
+                   .tpu_sparse_dense_matmul_gradient_stack_primitive.bind(
+                       *grads,
+                       stacked_batch_size=(spec.total_sample_count //
+                                           global_device_count),
+                       stacked_feature_dim=spec.stack_embedding_dim,
+                       num_sc_per_device=f))
+      continue
     parts = []
-    for fs, g in items:
-      g = _prepare_gradient_for_stacking(g, fs, f)
+    for g in grads:
       parts.append(g.reshape(f, g.shape[0] // f, g.shape[1]))
     cat = t.cat(parts, dim=1)
     out[name] = cat.reshape(-1, cat.shape[-1])
@@ -778,7 +873,8 @@ def tpu_sparse_dense_matmul_grad(activation_gradients, preprocessed_inputs,
       ev = embedding_variables[name]
       table = ev.table if isinstance(ev, EmbeddingVariables) else ev[0]
       blocks = None
-      if len(getattr(table, "shape", ())) == 2:
+      if (not use_gradient_stacking_primitive and
+          len(getattr(table, "shape", ())) == 2):
         blocks = _gradient_blocks(
             stacked[name], items, num_sc_per_device,
             (getattr(preprocessed_inputs, "csr_num_entries", None) or

@@ -227,11 +227,21 @@ def _check_update(before, after, eid, sid, gains, grad, rows, spec):
 
 @pytest.mark.parametrize("cfg", ["c1", "c2", "c3", "c5", "c4"])
 def test_config_full_size(cfg):
-  w = bench.WORKLOADS[cfg]()
+  w = bench.WORKLOADS[cfg](num_batches=1)
   pre, stats = embedding.preprocess_sparse_dense_matmul_input(
       w.features, w.weights, w.feature_specs, 1, 1, num_sc_per_device=1)
   ref = refcpu.preprocess(w.features, w.weights, w.feature_specs, 1, 1,
                           num_sc_per_device=1)
+  # The shapes the specs alone predict are the buffers' shapes.
+  shapes = embedding.eval_preprocess_sparse_dense_matmul_input_shape(
+      w.feature_specs, 1, 1, num_sc_per_device=1)
+  for field in ("lhs_row_pointers", "lhs_embedding_ids", "lhs_sample_ids",
+                "lhs_gains"):
+    want, got = getattr(shapes, field), getattr(pre, field)
+    assert set(want) == set(got)
+    for name, s in want.items():
+      assert tuple(got[name].shape) == s.shape, (field, name)
+      assert str(got[name].dtype) == f"torch.{s.dtype}", (field, name)
   rng = np.random.default_rng(int(cfg[1:]))
   gen = torch.Generator(device="cuda")
   gen.manual_seed(7)
