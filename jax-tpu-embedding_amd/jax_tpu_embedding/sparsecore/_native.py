@@ -244,6 +244,11 @@ def load_library() -> ctypes.CDLL:
           f"libscemb.so not found at {LIB_PATH}; build it with "
           "`python -c 'import __graft_entry__; __graft_entry__.build()'` or "
           "`make -C jax-tpu-embedding_amd/csrc`.")
+    # torch first: its wheel carries its own HIP runtime, which libscemb's
+    # libamdhip64 dependency must resolve to. Loaded the other way round, the
+    # process holds two runtimes and launches from the library find no
+    # device.
+    import torch as _  # pylint: disable=g-import-not-at-top,unused-import
     lib = ctypes.CDLL(str(LIB_PATH))
     vp, i32, i64, f32, sz = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
                              ctypes.c_float, ctypes.c_size_t)
