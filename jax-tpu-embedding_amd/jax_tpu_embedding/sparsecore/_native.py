@@ -191,6 +191,36 @@ class Feature(ctypes.Structure):
   ]
 
 
+# scemb_feature_t as a numpy record: an array of them is filled column by
+# column, far cheaper than one ctypes structure per feature.
+_FEATURE_DTYPE = np.dtype({
+    "names": [f[0] for f in Feature._fields_],
+    "formats": ["<u8", "<u8", "<u8", "<u8", "<i8", "<i8", "<i4", "<i4", "<i4",
+                "<i4", "<i8"],
+    "offsets": [getattr(Feature, f[0]).offset for f in Feature._fields_],
+    "itemsize": ctypes.sizeof(Feature)})
+
+
+class FeatureArray:
+  """scemb_feature_t[n] in numpy memory; pass `as_parameter` where the C ABI
+  takes the features (the array must outlive the call)."""
+
+  def __init__(self, rows):
+    self.array = np.array([tuple(0 if v is None else v for v in r)
+                           for r in rows], dtype=_FEATURE_DTYPE)
+    self._as_parameter_ = self.array.ctypes.data_as(ctypes.POINTER(Feature))
+
+  def __len__(self):
+    return len(self.array)
+
+
+def feature_structs(rows) -> FeatureArray:
+  """scemb_feature_t[len(rows)] from (ids, weights, row_splits,
+  row_splits_host, num_rows, nnz, valency, row_offset, col_offset,
+  col_shift, max_row_length) tuples; addresses may be None (null)."""
+  return FeatureArray(rows)
+
+
 class PreprocessOptions(ctypes.Structure):
   _fields_ = [
       ("local_device_count", ctypes.c_int32),
@@ -597,14 +627,27 @@ class HostUploads:
   _ALIGN = 256  # every array starts 256-byte aligned on the device
 
   class _Handle:
-    __slots__ = ("offset", "count", "dtype", "tensor", "nnz",
+    __slots__ = ("offset", "count", "dtype", "base", "nnz",
                  "max_row_length")
 
     def __init__(self, offset, count, dtype, nnz=None):
       self.offset, self.count, self.dtype = offset, count, dtype
-      self.tensor = None
+      self.base = None  # the device buffer, after flush()
       self.nnz = nnz  # row splits: the number of values they end at
       self.max_row_length = None
+
+    @property
+    def tensor(self):
+      if self.base is None:
+        return None
+      size = self.count * torch().empty(0, dtype=self.dtype).element_size()
+      return self.base[self.offset:self.offset + size].view(self.dtype)
+
+    @property
+    def address(self):
+      return None if self.base is None else self.base.data_ptr() + self.offset
+
+  Handle = _Handle
 
   def __init__(self):
     self._items = []
@@ -652,22 +695,36 @@ class HostUploads:
       h.max_row_length = int(longest.value)
     dst = t.empty(self._nbytes, dtype=t.uint8, device=dev)
     dst.copy_(host, non_blocking=True)
-    for arr, h in self._items:
-      h.tensor = dst[h.offset:h.offset + arr.nbytes].view(h.dtype)
+    for _, h in self._items:
+      h.base = dst
     self._items = []
     self._nbytes = 0
 
   @staticmethod
   def resolve(x):
+    """The device tensor of a handle; anything else as is."""
     if isinstance(x, HostUploads._Handle):
-      if x.tensor is None:
+      if x.base is None:
         raise RuntimeError("HostUploads.flush() has not run")
       return x.tensor
     return x
 
+  @staticmethod
+  def resolve_address(x):
+    """The device address of a handle (an int; its buffer stays alive while
+    any tensor of the call holds it, see flush); anything else as is."""
+    if isinstance(x, HostUploads._Handle):
+      if x.base is None:
+        raise RuntimeError("HostUploads.flush() has not run")
+      return x.address
+    return x
+
 
 def ptr(x) -> int | None:
-  return None if x is None else x.data_ptr()
+  """Device address of a tensor; an int address is passed through."""
+  if x is None or isinstance(x, int):
+    return x
+  return x.data_ptr()
 
 
 class _Workspace:

@@ -174,6 +174,10 @@ class _DeviceFeature:
   valency: int
   max_id: int | None  # known when the input came from host memory
   max_row_length: int | None = None  # most ids of one row (None: not known)
+  # Device buffers that staged fields live in once they are addresses: held
+  # as long as the feature (the pending call keeps its features until its
+  # stats are collected, after every kernel that reads them).
+  keep: list | None = None
 
   @property
   def one_id_per_row(self) -> bool:
@@ -193,7 +197,14 @@ def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
   dev = _native.device()
 
   def on_device(x, dtype):
-    if uploads is None or isinstance(x, t.Tensor):
+    if isinstance(x, t.Tensor):
+      # Already where it goes (the common case for inputs kept in HBM): a
+      # flat view, no copy.
+      if x.is_cuda and x.dtype == dtype and x.device == dev and (
+          x.is_contiguous()):
+        return x.view(-1)
+      return _native.as_device_tensor(x, dtype, dev)
+    if uploads is None:
       return _native.as_device_tensor(x, dtype, dev)
     return uploads.add(x, dtype)
 
@@ -301,11 +312,15 @@ def _check_row_splits(splits: np.ndarray, nnz: int) -> int:
 
 
 def _resolve_feature(f: _DeviceFeature) -> _DeviceFeature:
+  """Staged fields become device addresses (_native.ptr takes both); the
+  rows' longest length comes from the staging check."""
   if getattr(f.splits, "max_row_length", None) is not None:
     f.max_row_length = f.splits.max_row_length
-  f.ids = _native.HostUploads.resolve(f.ids)
-  f.weights = _native.HostUploads.resolve(f.weights)
-  f.splits = _native.HostUploads.resolve(f.splits)
+  f.keep = [h.base for h in (f.ids, f.weights, f.splits)
+            if isinstance(h, _native.HostUploads.Handle)]
+  f.ids = _native.HostUploads.resolve_address(f.ids)
+  f.weights = _native.HostUploads.resolve_address(f.weights)
+  f.splits = _native.HostUploads.resolve_address(f.splits)
   return f
 
 
@@ -343,13 +358,11 @@ def _preprocess_stack(feats, metas, *, local_device_count,
       int(bool(build_view)), int(bool(enable_minibatching)),
       metas[0].stack_vocab_size // global_device_count,
       int(minibatching_pass), PREPROCESS_FLAGS, int(minibatching_split))
-  structs = (_native.Feature * len(feats))()
-  for i, (f, m) in enumerate(zip(feats, metas)):
-    structs[i] = _native.Feature(
-        _native.ptr(f.ids), _native.ptr(f.weights), _native.ptr(f.splits),
-        None if f.splits_host is None else f.splits_host.ctypes.data,
+  structs = _native.feature_structs(
+      [(_native.ptr(f.ids), _native.ptr(f.weights), _native.ptr(f.splits),
+        0 if f.splits_host is None else f.splits_host.ctypes.data,
         f.num_rows, f.nnz, f.valency, m.row_offset, m.col_offset, m.col_shift,
-        f.max_row_length or 0)
+        f.max_row_length or 0) for f, m in zip(feats, metas)])
   need = lib.scemb_preprocess_workspace_size(structs, len(feats),
                                              ctypes.byref(opts))
   if need == 0:
