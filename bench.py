@@ -676,11 +676,13 @@ def _graph_steps(step, steps, warmup):
 
 # Every built-in optimizer spec with two slot variables, at its defaults.
 OTHER_OPTIMIZERS = ("adam", "adagrad_momentum", "ftrl", "laprop", "f2a")
+# The optimizer_bwd entries with one slot variable (the others have two).
+ONE_SLOT_OPTIMIZERS = ("adagrad", "custom_adagrad", "custom_adagrad_interpreted")
 
 
 def _optimizer_steps(pre, state, stacked, steps, warmup):
-  """Backward + each two-slot optimizer on the headline stack (the step's
-  backward with another update): ms per call, event-free wall time over
+  """Backward + Adagrad (built-in and custom) and each two-slot optimizer on
+  the headline stack (the step's backward with another update): ms per call, event-free wall time over
   `steps` calls. Slots start at the spec's initial values; the table is the
   step's own (updated in place, as in training)."""
   import torch  # pylint: disable=g-import-not-at-top
@@ -705,6 +707,49 @@ def _optimizer_steps(pre, state, stacked, steps, warmup):
             num_sc_per_device=1, csr_sorted_by_row=pre.csr_sorted_by_row,
             csr_num_entries=pre.csr_num_entries[name])
   out = {}
+  # The reference test's custom Adagrad (tpu_sparse_dense_matmul_grad_test.py:
+  # 1324-1486) beside the built-in Adagrad (the same bytes, one slot): its
+  # update compiled for the program at run time (compiled once, in the
+  # warmup), and interpreted.
+  from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_optimizer_grad as custom  # pylint: disable=g-import-not-at-top
+  from jax_tpu_embedding.sparsecore.lib.core.primitives import sparse_dense_matmul_grad_with_adagrad as ada  # pylint: disable=g-import-not-at-top
+  from jax_tpu_embedding.sparsecore.lib.nn import custom_optimizer_lowering  # pylint: disable=g-import-not-at-top
+
+  def adagrad_fn(grad, table, accum, lr):
+    new_accum = accum + grad * grad
+    return table - lr * grad / np.sqrt(new_accum), new_accum
+
+  text = custom_optimizer_lowering.lower_to_stablehlo(
+      adagrad_fn, int(t.shape[1]), 1, 1)
+  lr = torch.tensor(0.01, dtype=torch.float32, device=t.device)
+  acc = slots[0]
+  def custom_call():
+    custom.tpu_sparse_dense_matmul_optimizer_grad_primitive.bind(
+        *csr, 1, g, lr, t, acc, num_hyperparameters=1, stablehlo=text, **kw)
+
+  variants = {
+      "adagrad": (None, lambda: ada.tpu_sparse_dense_matmul_grad_with_adagrad_primitive
+                  .bind(*csr, 1, t, acc, g, lr, **kw)),
+      "custom_adagrad": ("compile", custom_call),
+      "custom_adagrad_interpreted": ("interpret", custom_call),
+  }
+  saved_mode = os.environ.get("SCEMB_CUSTOM_UPDATE")
+  for key, (mode, call) in variants.items():
+    if mode is not None:
+      os.environ["SCEMB_CUSTOM_UPDATE"] = mode
+    acc.fill_(0.1)
+    for _ in range(warmup):
+      call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+      call()
+    torch.cuda.synchronize()
+    out[key] = (time.perf_counter() - t0) * 1e3 / steps
+  if saved_mode is None:
+    os.environ.pop("SCEMB_CUSTOM_UPDATE", None)
+  else:
+    os.environ["SCEMB_CUSTOM_UPDATE"] = saved_mode
   for key in OTHER_OPTIMIZERS:
     opt = specs[key]
     for s, init in zip(slots, opt.slot_variables_initializers()):
@@ -1176,13 +1221,17 @@ def main():
       "cpu_baseline": cpu,
   }
   if res["optimizer_bwd_ms"]:
-    # The same backward with each two-slot optimizer: compulsory bytes
-    # 12N + 4D*Bs + 24D*U (table and two slots read and written).
+    # The same backward with each optimizer: compulsory bytes 12N + 4D*Bs +
+    # 8D*U per table or slot array read and written.
     (s,) = res["per_stack"].values()
-    two_slot = 12 * s["N"] + 4 * s["D"] * s["Bs"] + 24 * s["D"] * s["U"]
+
+    def bwd_bytes(slots):
+      return 12 * s["N"] + 4 * s["D"] * s["Bs"] + 8 * (1 + slots) * s["D"] * s["U"]
+
     out["optimizer_bwd"] = {
         k: {"ms": round(v, 4),
-            "hbm_frac": round(two_slot / (v / 1e3) / 1e9 / PEAK_HBM_GBS, 4)}
+            "hbm_frac": round(bwd_bytes(1 if k in ONE_SLOT_OPTIMIZERS else 2) /
+                              (v / 1e3) / 1e9 / PEAK_HBM_GBS, 4)}
         for k, v in res["optimizer_bwd_ms"].items()}
   if res["minibatching"]:
     # Same entries (nothing dropped), so the same compulsory bytes.

@@ -39,8 +39,10 @@
 #ifndef SCEMB_H_
 #define SCEMB_H_
 
+#ifndef __HIPCC_RTC__ /* kernels compiled at run time get these types built in */
 #include <stddef.h>
 #include <stdint.h>
+#endif
 
 #ifdef __cplusplus
 extern "C" {
@@ -361,7 +363,16 @@ int scemb_sparse_dense_matmul_grad_with_adagrad_from_blocks(
  * min(max(b, a), c)). Afterwards register out[0] is the new table value
  * (the optimizer's clipping then applies) and out[1 + k] the new value of
  * slot k. Arithmetic is float32 with correctly rounded division and square
- * root; EXP, LOG, POW, TANH, LOG1P and EXPM1 are the device library's. */
+ * root; EXP, LOG, POW, TANH, LOG1P and EXPM1 are the device library's
+ * double-precision functions rounded once to float.
+ * The first call with a program compiles it at run time (hiprtc, about a
+ * second per program and layout; kept for the process) into the kernels the
+ * built-in optimizers run, with the update inlined. The environment variable
+ * SCEMB_CUSTOM_UPDATE chooses: "auto" (default: compiled, or interpreted
+ * by the library's own kernels when hiprtc is missing or compilation
+ * fails), "compile" (fail with SCEMB_ERR_DEVICE instead of interpreting) or
+ * "interpret"; any other value is SCEMB_ERR_INVALID_ARGUMENT. Both forms give
+ * identical results. */
 #define SCEMB_PROGRAM_MAX_OPS 48
 #define SCEMB_PROGRAM_MAX_REGISTERS 24
 enum {

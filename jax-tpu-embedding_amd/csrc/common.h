@@ -1,11 +1,16 @@
-// Shared device helpers for libscemb (gfx950, wave64).
+// Shared device helpers for libscemb (gfx950, wave64). The host-side parts
+// are left out when the header is compiled at run time (__HIPCC_RTC__: the
+// kernels of a custom update program, rtc.hip).
 #pragma once
 
+#ifndef __HIPCC_RTC__
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#endif
 
 namespace scemb {
 
@@ -17,6 +22,7 @@ constexpr int kMaxMinibatches = 64;
 constexpr int32_t kPadInt = 0x7fffffff;
 constexpr uint32_t kNanBits = 0x7fc00000u;  // std::nanf("")
 
+#ifndef __HIPCC_RTC__
 // Status plumbing: every entry point returns a code and leaves a message in a
 // thread-local buffer (scemb_last_error).
 void SetError(const std::string& msg);
@@ -77,6 +83,7 @@ class Arena {
   size_t cap_;
   size_t used_ = 0;
 };
+#endif  // __HIPCC_RTC__
 
 // ---------------------------------------------------------------------------
 // Device-side helpers.

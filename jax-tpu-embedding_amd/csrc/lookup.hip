@@ -560,15 +560,7 @@ int CheckProgram(const scemb_update_program_t* p) {
       return Fail(SCEMB_ERR_INVALID_ARGUMENT,
                   "custom optimizer program: bad opcode or register");
     }
-    const bool unary = op == SCEMB_OP_NEG || op == SCEMB_OP_SQRT ||
-                       op == SCEMB_OP_RSQRT || op == SCEMB_OP_ABS ||
-                       op == SCEMB_OP_EXP || op == SCEMB_OP_LOG ||
-                       op == SCEMB_OP_SIGN || op == SCEMB_OP_TANH ||
-                       op == SCEMB_OP_LOG1P || op == SCEMB_OP_EXPM1 ||
-                       op == SCEMB_OP_FLOOR || op == SCEMB_OP_CEIL ||
-                       op == SCEMB_OP_NOT;
-    const bool ternary = op == SCEMB_OP_SELECT || op == SCEMB_OP_CLAMP;
-    const int reads = op == SCEMB_OP_CONST ? 0 : unary ? 1 : ternary ? 3 : 2;
+    const int reads = ProgReads(op);
     const uint8_t src[3] = {p->a[i], p->b[i], p->c[i]};
     for (int k = 0; k < reads; ++k) {
       if (!set[src[k]]) {
@@ -643,7 +635,9 @@ int GradEntry(const scemb_csr_t* csr, const float* activations_grad,
   c.opt.min_value = opt->min_value;
   c.opt.max_value = opt->max_value;
   c.opt.flags = opt->flags;
-  if (opt->kind == SCEMB_OPTIMIZER_CUSTOM) c.opt.prog = *opt->program;
+  if (opt->kind == SCEMB_OPTIMIZER_CUSTOM) {
+    c.opt.prog = EncodeProgram(*opt->program);
+  }
   c.ws = &ws;
   c.status = device_status;
   c.stream = static_cast<hipStream_t>(stream);

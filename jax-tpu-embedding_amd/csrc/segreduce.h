@@ -33,7 +33,9 @@
 
 #include "../../include/scemb.h"
 #include "common.h"
+#ifndef __HIPCC_RTC__
 #include "scan.h"
+#endif
 
 namespace scemb {
 
@@ -47,10 +49,69 @@ enum {
   kEpiFtrl = 5,
   kEpiLaprop = 6,
   kEpiF2a = 7,
-  kEpiCustom = 8,  // a CustomOptimizerSpec update, run as a program
+  kEpiCustom = 8,       // a CustomOptimizerSpec update, run as a program
+  kEpiCustomArith = 9,  // the same without exp/log/pow/tanh/log1p/expm1
+  kEpiRtc = 10,         // a custom update compiled for its program (rtc.hip)
 };
 
+// The interpreted forms of custom update. Kept apart because the
+// transcendental operations (double precision, inlined) take about 90 VGPRs:
+// the kernels of programs without them stay small enough for the 16-byte
+// layout, and those of programs with them run the 4-byte layout only.
+template <int EPI>
+__host__ __device__ constexpr bool IsInterpreted() {
+  return EPI == kEpiCustom || EPI == kEpiCustomArith;
+}
+// Custom updates, interpreted or compiled: slots and hyperparameters as the
+// program declares them.
+template <int EPI>
+__host__ __device__ constexpr bool IsCustom() {
+  return IsInterpreted<EPI>() || EPI == kEpiRtc;
+}
+
+// The update of a custom program compiled at run time: the source rtc.hip
+// generates for the program defines it for kEpiRtc, and only kernels
+// compiled from that source call it. Returns the new table value and updates
+// the slot values s0, s1 in place; h holds the hyperparameters.
+template <int EPI>
+__device__ float RtcUpdate(float g, float t, float& s0, float& s1,
+                           const float* h);
+
 constexpr int kMaxHyper = SCEMB_MAX_HYPERPARAMETERS;
+
+// A custom update program (scemb_update_program_t) as the kernels read it:
+// one 32-bit word per instruction, opcode in bits 0-7, then 5 bits each for
+// the registers dst, a, b and c (operands the opcode does not read are 0).
+// Each instruction is one scalar load from the kernel arguments and its
+// register indices are uniform across the wave; byte-sized fields would be
+// fetched by per-lane loads, and a register index held per lane costs a
+// loop over its distinct values at every access.
+struct DevProgram {
+  int32_t num_ops;
+  int32_t num_slots;
+  int32_t num_hyper;
+  int32_t num_regs;  // 1 + the largest register the program names
+  int32_t transcendental;  // uses exp, log, pow, tanh, log1p or expm1
+  uint32_t out;      // output register k in bits 8k .. 8k + 4
+  uint32_t code[SCEMB_PROGRAM_MAX_OPS];
+  float imm[SCEMB_PROGRAM_MAX_OPS];
+};
+
+// Interpreter registers per vector component. The register file is one
+// 32-float vector value held in VGPRs: the 16-byte layout (four components)
+// takes programs of up to 8 registers, and the host gives larger programs
+// the 4-byte layout.
+template <int VEC>
+__host__ __device__ constexpr int ProgRegs() {
+  return VEC == 4 ? 8 : SCEMB_PROGRAM_MAX_REGISTERS;
+}
+
+// Register r's component k is element r * VEC + k. A vector value rather
+// than an array: an element picked by a wave-uniform index is an indexed
+// register move, while a private array may be placed in scratch memory.
+typedef float ProgRegFile __attribute__((ext_vector_type(32)));
+static_assert(ProgRegs<4>() * 4 <= 32 && ProgRegs<1>() <= 32,
+              "register file size");
 
 // Hyperparameters of the update: value i is *ptr[i] (a device scalar, read
 // once per block) when ptr[i] is set, else value[i]. Clipping of the updated
@@ -62,7 +123,7 @@ struct OptParams {
   float min_value;
   float max_value;
   uint32_t flags;     // SCEMB_OPTIMIZER_FLAG_*
-  scemb_update_program_t prog;  // kEpiCustom only
+  DevProgram prog;    // custom updates only
 };
 
 constexpr int kMaxRowBlocks = SCEMB_MAX_ROW_BLOCKS;
@@ -81,6 +142,7 @@ struct RowMap {
   float* data[kMaxRowBlocks];
 };
 
+#ifndef __HIPCC_RTC__
 // One backward call: the CSR, the activation gradients (dense, or through
 // `map` when it is set), the table and up to two slot variables updated in
 // place, the hyperparameters, and where temporaries and problems go.
@@ -109,6 +171,26 @@ int GradWithFtrl(const GradCall& c);
 int GradWithLaprop(const GradCall& c);
 int GradWithF2a(const GradCall& c);
 int GradWithCustom(const GradCall& c);
+int GradWithCustomTranscendental(const GradCall& c);
+
+
+// A custom program's update kernels compiled at run time for one layout
+// (rtc.hip): SegReduce and SegFinish instantiated for kEpiRtc.
+struct RtcKernels {
+  hipFunction_t reduce;
+  hipFunction_t finish;
+};
+
+// The kernels of program p for layout (g, vec, src, unroll, mapped) on the
+// current device, compiled at the first request and kept for the process.
+// 0: *k is set. kRtcInterpret: interpret the program instead (compilation
+// switched off, or unavailable or failed while not required). Otherwise an
+// error code (SCEMB_ERR_*), message set: SCEMB_CUSTOM_UPDATE unknown, or
+// compilation required (SCEMB_CUSTOM_UPDATE=compile) and failed.
+constexpr int kRtcInterpret = -1;
+int RtcKernelsFor(const DevProgram& p, int g, int vec, int src, int unroll,
+                  bool mapped, RtcKernels* k);
+#endif  // __HIPCC_RTC__
 
 namespace {
 
@@ -446,13 +528,13 @@ __host__ __device__ constexpr int NumHyper() {
          : EPI == kEpiSgd || EPI == kEpiAdagrad         ? 1
          : EPI == kEpiAdam || EPI == kEpiLaprop         ? 4
          : EPI == kEpiFtrl                              ? 5
-         : EPI == kEpiCustom                            ? kMaxHyper
+         : IsCustom<EPI>()                              ? kMaxHyper
                                                         : 6;
 }
 // Whether slot k is read and written.
 template <int EPI>
 __device__ __forceinline__ bool HasSlot(const OptParams& o, int k) {
-  return NumSlots<EPI>() > k && (EPI != kEpiCustom || o.prog.num_slots > k);
+  return NumSlots<EPI>() > k && (!IsCustom<EPI>() || o.prog.num_slots > k);
 }
 
 // The hyperparameters as the update reads them, plus what is constant for
@@ -525,10 +607,10 @@ __device__ __forceinline__ Hyper LoadHyper(const OptParams& o) {
 // Transcendentals of a custom update program, evaluated in double and
 // rounded once: correctly rounded but for the rarest double-rounding ties,
 // so the result matches a correctly rounded float library (glibc's powf,
-// numpy's float32 power) rather than differing in the last bit. Kept out of
-// line: inlined for every vector element, the double-precision code would
-// double the interpreter's registers.
-__device__ __noinline__ float ProgTranscendental(int op, float x, float y) {
+// numpy's float32 power) rather than differing in the last bit. Inlined: a
+// call would make the caller save its live registers to scratch memory
+// around it.
+__device__ __forceinline__ float ProgTranscendental(int op, float x, float y) {
   const double a = static_cast<double>(x);
   switch (op) {
     case SCEMB_OP_EXP: return static_cast<float>(exp(a));
@@ -540,65 +622,221 @@ __device__ __noinline__ float ProgTranscendental(int op, float x, float y) {
   }
 }
 
-// A custom update (scemb_update_program_t): registers 0, 1 hold the summed
-// gradient and the table value, then the slot values, then the
-// hyperparameters; each instruction sets one register. The program is the
-// same for every thread (kernel arguments), so every branch is uniform.
-__device__ __forceinline__ float ProgOp(int op, float x, float y, float z,
-                                        float imm) {
-  switch (op) {
-    case SCEMB_OP_CONST: return imm;
-    case SCEMB_OP_ADD: return x + y;
-    case SCEMB_OP_SUB: return x - y;
-    case SCEMB_OP_MUL: return x * y;
-    case SCEMB_OP_DIV: return x / y;
-    case SCEMB_OP_NEG: return -x;
-    case SCEMB_OP_SQRT: return sqrtf(x);
-    case SCEMB_OP_RSQRT: return 1.0f / sqrtf(x);
-    case SCEMB_OP_ABS: return fabsf(x);
-    case SCEMB_OP_EXP:
-    case SCEMB_OP_LOG:
-    case SCEMB_OP_POW:
-    case SCEMB_OP_TANH:
-    case SCEMB_OP_LOG1P:
-    case SCEMB_OP_EXPM1:
-      return ProgTranscendental(op, x, y);
-    // maximum / minimum propagate NaN, as StableHLO's do.
-    case SCEMB_OP_MAX: return (x != x || y != y) ? x + y : fmaxf(x, y);
-    case SCEMB_OP_MIN: return (x != x || y != y) ? x + y : fminf(x, y);
-    case SCEMB_OP_SIGN: return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : x);
-    case SCEMB_OP_FLOOR: return floorf(x);
-    case SCEMB_OP_CEIL: return ceilf(x);
-    case SCEMB_OP_SELECT: return x != 0.0f ? y : z;
-    case SCEMB_OP_CMP_EQ: return x == y ? 1.0f : 0.0f;
-    case SCEMB_OP_CMP_NE: return x != y ? 1.0f : 0.0f;
-    case SCEMB_OP_CMP_LT: return x < y ? 1.0f : 0.0f;
-    case SCEMB_OP_CMP_LE: return x <= y ? 1.0f : 0.0f;
-    case SCEMB_OP_CMP_GT: return x > y ? 1.0f : 0.0f;
-    case SCEMB_OP_CMP_GE: return x >= y ? 1.0f : 0.0f;
-    case SCEMB_OP_CLAMP: return fminf(fmaxf(y, x), z);
-    case SCEMB_OP_AND: return (x != 0.0f && y != 0.0f) ? 1.0f : 0.0f;
-    case SCEMB_OP_OR: return (x != 0.0f || y != 0.0f) ? 1.0f : 0.0f;
-    default: return x == 0.0f ? 1.0f : 0.0f;  // SCEMB_OP_NOT
+// The value instruction OP (not CONST) gives for operands x, y, z: the one
+// definition of each operation, used by the interpreter and by the programs
+// compiled at run time alike. maximum / minimum propagate NaN, as
+// StableHLO's do; comparisons give 1 or 0; sign keeps zeros and NaN.
+template <int OP>
+__device__ __forceinline__ float ProgApply(float x, float y, float z) {
+  if constexpr (OP == SCEMB_OP_ADD) return x + y;
+  else if constexpr (OP == SCEMB_OP_SUB) return x - y;
+  else if constexpr (OP == SCEMB_OP_MUL) return x * y;
+  else if constexpr (OP == SCEMB_OP_DIV) return x / y;
+  else if constexpr (OP == SCEMB_OP_NEG) return -x;
+  else if constexpr (OP == SCEMB_OP_SQRT) return sqrtf(x);
+  else if constexpr (OP == SCEMB_OP_RSQRT) return 1.0f / sqrtf(x);
+  else if constexpr (OP == SCEMB_OP_ABS) return fabsf(x);
+  else if constexpr (OP == SCEMB_OP_EXP || OP == SCEMB_OP_LOG ||
+                     OP == SCEMB_OP_POW || OP == SCEMB_OP_TANH ||
+                     OP == SCEMB_OP_LOG1P || OP == SCEMB_OP_EXPM1)
+    return ProgTranscendental(OP, x, y);
+  else if constexpr (OP == SCEMB_OP_MAX)
+    return (x != x || y != y) ? x + y : fmaxf(x, y);
+  else if constexpr (OP == SCEMB_OP_MIN)
+    return (x != x || y != y) ? x + y : fminf(x, y);
+  else if constexpr (OP == SCEMB_OP_SIGN)
+    return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : x);
+  else if constexpr (OP == SCEMB_OP_FLOOR) return floorf(x);
+  else if constexpr (OP == SCEMB_OP_CEIL) return ceilf(x);
+  else if constexpr (OP == SCEMB_OP_SELECT) return x != 0.0f ? y : z;
+  else if constexpr (OP == SCEMB_OP_CMP_EQ) return x == y ? 1.0f : 0.0f;
+  else if constexpr (OP == SCEMB_OP_CMP_NE) return x != y ? 1.0f : 0.0f;
+  else if constexpr (OP == SCEMB_OP_CMP_LT) return x < y ? 1.0f : 0.0f;
+  else if constexpr (OP == SCEMB_OP_CMP_LE) return x <= y ? 1.0f : 0.0f;
+  else if constexpr (OP == SCEMB_OP_CMP_GT) return x > y ? 1.0f : 0.0f;
+  else if constexpr (OP == SCEMB_OP_CMP_GE) return x >= y ? 1.0f : 0.0f;
+  else if constexpr (OP == SCEMB_OP_CLAMP) return fminf(fmaxf(y, x), z);
+  else if constexpr (OP == SCEMB_OP_AND)
+    return (x != 0.0f && y != 0.0f) ? 1.0f : 0.0f;
+  else if constexpr (OP == SCEMB_OP_OR)
+    return (x != 0.0f || y != 0.0f) ? 1.0f : 0.0f;
+  else {
+    static_assert(OP == SCEMB_OP_NOT, "opcode");
+    return x == 0.0f ? 1.0f : 0.0f;
   }
 }
 
-__device__ __forceinline__ void RunProgram(const scemb_update_program_t& p,
-                                           float g, float& t, float& s0,
-                                           float& s1, const float* h) {
-  float R[SCEMB_PROGRAM_MAX_REGISTERS];
-  R[0] = g;
-  R[1] = t;
-  const int ns = p.num_slots;
-  if (ns >= 1) R[2] = s0;
-  if (ns >= 2) R[3] = s1;
-  for (int i = 0; i < p.num_hyperparameters; ++i) R[2 + ns + i] = h[i];
-  for (int i = 0; i < p.num_ops; ++i) {
-    R[p.dst[i]] = ProgOp(p.op[i], R[p.a[i]], R[p.b[i]], R[p.c[i]], p.imm[i]);
+// o[k] = ProgApply<OP>(x[k], y[k], z[k]) for every vector component.
+template <int OP, int VEC>
+__device__ __forceinline__ void ApplyAll(float (&o)[VEC], const float (&x)[VEC],
+                                         const float (&y)[VEC],
+                                         const float (&z)[VEC]) {
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) o[k] = ProgApply<OP>(x[k], y[k], z[k]);
+}
+
+// Register index field of an instruction word, kept inside the register
+// file whatever the word holds (the host has checked it already).
+template <int NR>
+__device__ __forceinline__ int ProgReg(uint32_t field) {
+  const int r = static_cast<int>(field & 31u);
+  return r < NR ? r : NR - 1;
+}
+
+// Hyperparameters into registers B.. (constant indices). Registers past the
+// program's inputs get values too: the program sets every register before
+// reading it, so they are never read.
+template <int B, int NR, int VEC>
+__device__ __forceinline__ void SetHyperRegs(ProgRegFile& R, const float* h) {
+#pragma unroll
+  for (int i = 0; i < kMaxHyper; ++i) {
+    if (B + i < NR) {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) R[(B + i) * VEC + k] = h[i];
+    }
   }
-  t = R[p.out[0]];
-  if (ns >= 1) s0 = R[p.out[1]];
-  if (ns >= 2) s1 = R[p.out[2]];
+}
+
+// A custom update (scemb_update_program_t) on VEC table values at once
+// (kTranscendentals: the program may use the transcendental operations;
+// without, those opcodes give NaN -- the host never sends them there):
+// registers 0, 1 hold the summed gradient and the table value, then the slot
+// values, then the hyperparameters; each instruction sets one register. The
+// program is the same for every thread (kernel arguments), so each
+// instruction is decoded and dispatched once per wave and applied to every
+// component, and its register indices are uniform.
+template <int VEC, bool kTranscendentals>
+__device__ __forceinline__ void RunProgram(const DevProgram& p,
+                                           const float (&g)[VEC],
+                                           float (&t)[VEC], float (&s0)[VEC],
+                                           float (&s1)[VEC], const float* h) {
+  constexpr int NR = ProgRegs<VEC>();
+  ProgRegFile R = {};
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    R[k] = g[k];
+    R[VEC + k] = t[k];
+  }
+  // Each slot count is its own (uniform) branch, so every input lands at a
+  // constant index.
+  const int ns = p.num_slots;
+  if (ns == 0) {
+    SetHyperRegs<2, NR, VEC>(R, h);
+  } else {
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) R[2 * VEC + k] = s0[k];
+    if (ns == 1) {
+      SetHyperRegs<3, NR, VEC>(R, h);
+    } else {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) R[3 * VEC + k] = s1[k];
+      SetHyperRegs<4, NR, VEC>(R, h);
+    }
+  }
+  const int n = p.num_ops;
+  for (int i = 0; i < n; ++i) {
+    const uint32_t w = __builtin_amdgcn_readfirstlane(p.code[i]);
+    const int op = static_cast<int>(w & 0xffu);
+    const int d = ProgReg<NR>(w >> 8) * VEC;
+    const int a = ProgReg<NR>(w >> 13) * VEC;
+    const int b = ProgReg<NR>(w >> 18) * VEC;
+    float x[VEC], y[VEC], z[VEC], o[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      x[k] = R[a + k];
+      y[k] = R[b + k];
+      z[k] = 0.0f;
+    }
+    switch (op) {
+      case SCEMB_OP_CONST: {
+        const float imm = __builtin_bit_cast(
+            float, __builtin_amdgcn_readfirstlane(
+                       __builtin_bit_cast(uint32_t, p.imm[i])));
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) o[k] = imm;
+        break;
+      }
+      case SCEMB_OP_ADD: ApplyAll<SCEMB_OP_ADD>(o, x, y, z); break;
+      case SCEMB_OP_SUB: ApplyAll<SCEMB_OP_SUB>(o, x, y, z); break;
+      case SCEMB_OP_MUL: ApplyAll<SCEMB_OP_MUL>(o, x, y, z); break;
+      case SCEMB_OP_DIV: ApplyAll<SCEMB_OP_DIV>(o, x, y, z); break;
+      case SCEMB_OP_NEG: ApplyAll<SCEMB_OP_NEG>(o, x, y, z); break;
+      case SCEMB_OP_SQRT: ApplyAll<SCEMB_OP_SQRT>(o, x, y, z); break;
+      case SCEMB_OP_RSQRT: ApplyAll<SCEMB_OP_RSQRT>(o, x, y, z); break;
+      case SCEMB_OP_ABS: ApplyAll<SCEMB_OP_ABS>(o, x, y, z); break;
+      case SCEMB_OP_EXP:
+      case SCEMB_OP_LOG:
+      case SCEMB_OP_POW:
+      case SCEMB_OP_TANH:
+      case SCEMB_OP_LOG1P:
+      case SCEMB_OP_EXPM1:
+        if constexpr (kTranscendentals) {
+          // One inlined copy: each pass takes component 0 and shifts the
+          // operands down and the results up (constant indices throughout).
+#pragma unroll 1
+          for (int k = 0; k < VEC; ++k) {
+            const float v = ProgTranscendental(op, x[0], y[0]);
+#pragma unroll
+            for (int j = 0; j + 1 < VEC; ++j) {
+              x[j] = x[j + 1];
+              y[j] = y[j + 1];
+              o[j] = o[j + 1];
+            }
+            o[VEC - 1] = v;
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) o[k] = __builtin_nanf("");
+        }
+        break;
+      case SCEMB_OP_MAX: ApplyAll<SCEMB_OP_MAX>(o, x, y, z); break;
+      case SCEMB_OP_MIN: ApplyAll<SCEMB_OP_MIN>(o, x, y, z); break;
+      case SCEMB_OP_SIGN: ApplyAll<SCEMB_OP_SIGN>(o, x, y, z); break;
+      case SCEMB_OP_FLOOR: ApplyAll<SCEMB_OP_FLOOR>(o, x, y, z); break;
+      case SCEMB_OP_CEIL: ApplyAll<SCEMB_OP_CEIL>(o, x, y, z); break;
+      case SCEMB_OP_SELECT:
+      case SCEMB_OP_CLAMP: {
+        const int c = ProgReg<NR>(w >> 23) * VEC;
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) z[k] = R[c + k];
+        if (op == SCEMB_OP_SELECT) {
+          ApplyAll<SCEMB_OP_SELECT>(o, x, y, z);
+        } else {
+          ApplyAll<SCEMB_OP_CLAMP>(o, x, y, z);
+        }
+        break;
+      }
+      case SCEMB_OP_CMP_EQ: ApplyAll<SCEMB_OP_CMP_EQ>(o, x, y, z); break;
+      case SCEMB_OP_CMP_NE: ApplyAll<SCEMB_OP_CMP_NE>(o, x, y, z); break;
+      case SCEMB_OP_CMP_LT: ApplyAll<SCEMB_OP_CMP_LT>(o, x, y, z); break;
+      case SCEMB_OP_CMP_LE: ApplyAll<SCEMB_OP_CMP_LE>(o, x, y, z); break;
+      case SCEMB_OP_CMP_GT: ApplyAll<SCEMB_OP_CMP_GT>(o, x, y, z); break;
+      case SCEMB_OP_CMP_GE: ApplyAll<SCEMB_OP_CMP_GE>(o, x, y, z); break;
+      case SCEMB_OP_AND: ApplyAll<SCEMB_OP_AND>(o, x, y, z); break;
+      case SCEMB_OP_OR: ApplyAll<SCEMB_OP_OR>(o, x, y, z); break;
+      default: ApplyAll<SCEMB_OP_NOT>(o, x, y, z); break;
+    }
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) R[d + k] = o[k];
+  }
+  const uint32_t out = __builtin_amdgcn_readfirstlane(p.out);
+  const int o0 = ProgReg<NR>(out) * VEC;
+  const int o1 = ProgReg<NR>(out >> 8) * VEC;
+  const int o2 = ProgReg<NR>(out >> 16) * VEC;
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    t[k] = R[o0 + k];
+    if (ns >= 1) s0[k] = R[o1 + k];
+    if (ns >= 2) s1[k] = R[o2 + k];
+  }
+}
+
+// The optimizer's clipping of an updated table value
+// (primitives/utils.py:24-59).
+__device__ __forceinline__ float ClipValue(const OptParams& o, float v) {
+  if (o.clip_mask & 1) v = fmaxf(o.min_value, v);
+  if (o.clip_mask & 2) v = fminf(o.max_value, v);
+  return v;
 }
 
 // Update of one table value t with its summed gradient g and slot values
@@ -619,6 +857,10 @@ template <int EPI>
 __device__ __forceinline__ float UpdateOne(float t, float& s0, float& s1,
                                            float g, const Hyper& H,
                                            const OptParams& o) {
+  static_assert(!IsInterpreted<EPI>(), "these run through RunProgram");
+  if constexpr (EPI == kEpiRtc) {
+    return ClipValue(o, RtcUpdate<EPI>(g, t, s0, s1, H.h));
+  }
   float v;
   if (EPI == kEpiSgd) {
     v = t - g * H.h[0];
@@ -672,9 +914,6 @@ __device__ __forceinline__ float UpdateOne(float t, float& s0, float& s1,
     s0 = u;
     s1 = nu;
     v = t - H.h[0] * u;
-  } else if (EPI == kEpiCustom) {
-    v = t;
-    RunProgram(o.prog, g, v, s0, s1, H.h);
   } else {
     // F2A: (lr, rho, l1, l2, max_lr_multiplier, global_step); slots
     // (accumulator, local_step). sign() keeps zeros (and NaN) as they are.
@@ -688,9 +927,7 @@ __device__ __forceinline__ float UpdateOne(float t, float& s0, float& s1,
     s1 = ls;
     v = t - H.h[0] * upd;
   }
-  if (o.clip_mask & 1) v = fmaxf(o.min_value, v);
-  if (o.clip_mask & 2) v = fminf(o.max_value, v);
-  return v;
+  return ClipValue(o, v);
 }
 
 // The row map staged in LDS by every block that reads or writes
@@ -754,14 +991,32 @@ __device__ __forceinline__ void Epilogue(const RowArgs& r,
     if (p != nullptr) StoreRow<VEC, kNtAct>(p, g);
     return;
   }
+  if constexpr (IsInterpreted<EPI>()) {
+    float tv[VEC], av[VEC], bv[VEC], gv[VEC];
 #pragma unroll
-  for (int k = 0; k < VEC; ++k) {
-    float ak = V::Get(a, k);
-    float bk = V::Get(b, k);
-    V::Set(t, k, UpdateOne<EPI>(V::Get(t, k), ak, bk, V::Get(g, k), H,
-                                r.opt));
-    V::Set(a, k, ak);
-    V::Set(b, k, bk);
+    for (int k = 0; k < VEC; ++k) {
+      tv[k] = V::Get(t, k);
+      av[k] = V::Get(a, k);
+      bv[k] = V::Get(b, k);
+      gv[k] = V::Get(g, k);
+    }
+    RunProgram<VEC, EPI == kEpiCustom>(r.opt.prog, gv, tv, av, bv, H.h);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      V::Set(t, k, ClipValue(r.opt, tv[k]));
+      V::Set(a, k, av[k]);
+      V::Set(b, k, bv[k]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      float ak = V::Get(a, k);
+      float bk = V::Get(b, k);
+      V::Set(t, k, UpdateOne<EPI>(V::Get(t, k), ak, bk, V::Get(g, k), H,
+                                  r.opt));
+      V::Set(a, k, ak);
+      V::Set(b, k, bk);
+    }
   }
   StoreRow<VEC, kNtTable>(r.dst + off, t);
   if (HasSlot<EPI>(r.opt, 0)) StoreRow<VEC, kNtTable>(r.slot0 + off, a);
@@ -955,6 +1210,7 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
       T tv[kUnroll];
       T av[kUnroll];
       T bv[kUnroll];
+      T res[kUnroll];  // interpreted updates: finished rows' gradient sums
       float gn[kUnroll];
       uint32_t kk[kUnroll];
       bool fin[kUnroll];
@@ -988,6 +1244,7 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
         tv[u] = V::Zero();
         av[u] = V::Zero();
         bv[u] = V::Zero();
+        res[u] = V::Zero();
         if (EPI != kEpiFwd && fin[u] && col_ok) {
           const int64_t off = static_cast<int64_t>(kk[u]) * dim + col;
           tv[u] = V::Load(r.dst + off);
@@ -1002,7 +1259,9 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
           acc = V::Fma(acc, gn[u], v[u]);
           if ((end_m >> idx) & 1) {
             if (fin[u]) {
-              if (col_ok) {
+              if constexpr (IsInterpreted<EPI>()) {
+                res[u] = acc;  // updated below
+              } else if (col_ok) {
                 Epilogue<VEC, EPI, kMapped>(r, s_map, kk[u], col, acc, tv[u],
                                             av[u], bv[u], H);
               }
@@ -1011,6 +1270,28 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
               s_part[head_cont && first ? 2 * sub : 2 * sub + 1][cl] = acc;
             }
             acc = V::Zero();
+          }
+        }
+      }
+      if constexpr (IsInterpreted<EPI>()) {
+        // The finished rows' updates through one inlined copy of the
+        // interpreter (its register file then stays in VGPRs, and the loop
+        // body in the instruction cache): each pass updates entry 0 and
+        // shifts the rest down, so every index stays constant.
+#pragma unroll 1
+        for (int u = 0; u < kUnroll; ++u) {
+          if (fin[0] && col_ok) {
+            Epilogue<VEC, EPI, kMapped>(r, s_map, kk[0], col, res[0], tv[0],
+                                        av[0], bv[0], H);
+          }
+#pragma unroll
+          for (int j = 0; j + 1 < kUnroll; ++j) {
+            fin[j] = fin[j + 1];
+            kk[j] = kk[j + 1];
+            res[j] = res[j + 1];
+            tv[j] = tv[j + 1];
+            av[j] = av[j + 1];
+            bv[j] = bv[j + 1];
           }
         }
       }
@@ -1135,7 +1416,7 @@ __global__ __launch_bounds__(kBlock) void SegFinish(int64_t num_blocks,
   }
 }
 
-
+#ifndef __HIPCC_RTC__
 // ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
@@ -1219,6 +1500,61 @@ Csr MakeCsr(const scemb_csr_t* csr) {
 }
 
 // Lanes per row (>= 4) and vector width for a row of `dim` floats.
+// Whether opcode op is one of the transcendental operations.
+inline bool ProgTranscendentalOp(int op) {
+  return op == SCEMB_OP_EXP || op == SCEMB_OP_LOG || op == SCEMB_OP_POW ||
+         op == SCEMB_OP_TANH || op == SCEMB_OP_LOG1P || op == SCEMB_OP_EXPM1;
+}
+
+// Registers an instruction of opcode op reads: a, then b, then c.
+inline int ProgReads(int op) {
+  switch (op) {
+    case SCEMB_OP_CONST:
+      return 0;
+    case SCEMB_OP_NEG: case SCEMB_OP_SQRT: case SCEMB_OP_RSQRT:
+    case SCEMB_OP_ABS: case SCEMB_OP_EXP: case SCEMB_OP_LOG:
+    case SCEMB_OP_SIGN: case SCEMB_OP_TANH: case SCEMB_OP_LOG1P:
+    case SCEMB_OP_EXPM1: case SCEMB_OP_FLOOR: case SCEMB_OP_CEIL:
+    case SCEMB_OP_NOT:
+      return 1;
+    case SCEMB_OP_SELECT: case SCEMB_OP_CLAMP:
+      return 3;
+    default:
+      return 2;
+  }
+}
+
+// The device form of a checked program: operands an opcode does not read
+// become register 0, and num_regs covers the inputs and every register an
+// instruction reads or sets.
+inline DevProgram EncodeProgram(const scemb_update_program_t& p) {
+  DevProgram d{};
+  d.num_ops = p.num_ops;
+  d.num_slots = p.num_slots;
+  d.num_hyper = p.num_hyperparameters;
+  int regs = 2 + p.num_slots + p.num_hyperparameters;
+  for (int i = 0; i < p.num_ops; ++i) {
+    const int reads = ProgReads(p.op[i]);
+    const uint32_t src[3] = {p.a[i], p.b[i], p.c[i]};
+    uint32_t w = static_cast<uint32_t>(p.op[i]) |
+                 (static_cast<uint32_t>(p.dst[i]) << 8);
+    regs = std::max(regs, p.dst[i] + 1);
+    for (int k = 0; k < reads; ++k) {
+      w |= src[k] << (13 + 5 * k);
+      regs = std::max(regs, static_cast<int>(src[k]) + 1);
+    }
+    d.code[i] = w;
+    d.imm[i] = p.op[i] == SCEMB_OP_CONST ? p.imm[i] : 0.0f;
+    d.transcendental |= ProgTranscendentalOp(p.op[i]);
+  }
+  for (int k = 0; k <= p.num_slots; ++k) {
+    d.out |= static_cast<uint32_t>(p.out[k]) << (8 * k);
+    regs = std::max(regs, p.out[k] + 1);
+  }
+  d.num_regs = regs;
+  return d;
+}
+
 void PickLayout(int64_t dim, bool vec4_ok, int* g, int* vec) {
   *vec = vec4_ok && dim % 4 == 0 ? 4 : 1;
   const int64_t lanes = CeilDiv(dim, *vec);
@@ -1263,6 +1599,26 @@ SegBuffers TakeSegBuffers(Arena& ws, int64_t n, int64_t dim) {
   return b;
 }
 
+// SegReduce + SegFinish compiled for a custom program (RtcKernelsFor), with
+// the arguments of the library's own kernels.
+int LaunchRtc(const RtcKernels& k, StreamArgs st, RowArgs r, int64_t num_blocks,
+              const char* reduce_span, const char* finish_span,
+              hipStream_t stream) {
+  const uint32_t grid = static_cast<uint32_t>(num_blocks);
+  void* reduce_args[] = {&st, &r};
+  int prof = ProfileBegin(reduce_span, stream);
+  SCEMB_HIP(hipModuleLaunchKernel(k.reduce, grid, 1, 1, kBlock, 1, 1, 0,
+                                  stream, reduce_args, nullptr));
+  ProfileEnd(prof, stream);
+  if (r.single_runs) return 0;
+  void* finish_args[] = {&num_blocks, &r};
+  prof = ProfileBegin(finish_span, stream);
+  SCEMB_HIP(hipModuleLaunchKernel(k.finish, grid, 1, 1, kBlock, 1, 1, 0,
+                                  stream, finish_args, nullptr));
+  ProfileEnd(prof, stream);
+  return 0;
+}
+
 template <int SRC, int EPI, bool kMapped>
 int LaunchSegMapped(const StreamArgs& st, RowArgs r, const SegBuffers& sb,
                     int g, int vec, bool one_hot, const char* reduce_span,
@@ -1272,8 +1628,21 @@ int LaunchSegMapped(const StreamArgs& st, RowArgs r, const SegBuffers& sb,
   r.partials = sb.partials;
   r.block_flags = sb.flags;
   r.block_keys = sb.keys;
+  if constexpr (IsInterpreted<EPI>()) {
+    // A custom program runs compiled for itself when it can (the same
+    // kernels with its update inlined), else through the interpreter.
+    RtcKernels k{};
+    const int rc = RtcKernelsFor(r.opt.prog, g, vec, SRC,
+                                 one_hot ? kWide : kNarrow, kMapped, &k);
+    if (rc == 0) {
+      return LaunchRtc(k, st, r, sb.num_blocks, reduce_span, finish_span,
+                       stream);
+    }
+    if (rc != kRtcInterpret) return rc;
+  }
   const dim3 grid(static_cast<uint32_t>(sb.num_blocks));
 #define SCEMB_SEG_CASE(GG, VV)                                                \
+  if constexpr (VV == 1 || EPI != kEpiCustom)                                \
   if (g == GG && vec == VV) {                                                \
     int prof = ProfileBegin(reduce_span, stream);                            \
     if (one_hot) {                                                           \
@@ -1389,7 +1758,10 @@ int GradImpl(const GradCall& c) {
              Aligned16(c.table) &&
                  (c.map != nullptr ? c.map_vec4 : Aligned16(c.act_grad)) &&
                  (c.slot0 == nullptr || Aligned16(c.slot0)) &&
-                 (c.slot1 == nullptr || Aligned16(c.slot1)),
+                 (c.slot1 == nullptr || Aligned16(c.slot1)) &&
+                 EPI != kEpiCustom &&
+                 (EPI != kEpiCustomArith ||
+                  c.opt.prog.num_regs <= ProgRegs<4>()),
              &g, &vec);
   const bool mapped = c.map != nullptr;
   if (direct) {
@@ -1399,6 +1771,8 @@ int GradImpl(const GradCall& c) {
   return LaunchSeg<kSrcSorted, EPI>(st, r, sb, g, vec, one_hot, mapped,
                                     "bwd_reduce", "bwd_finish", stream);
 }
+
+#endif  // __HIPCC_RTC__
 
 }  // namespace
 }  // namespace scemb

@@ -19,7 +19,10 @@ Transcribed from the reference (paths under jax_tpu_embedding/sparsecore/):
       out (one GPU), its closed-form expectations kept.
 Added here: custom SGD and Adagrad equal the built-in updates bit for bit on
 multi-hot weighted input (the same kernel up to the update), and a random
-custom update matches the oracle.
+custom update matches the oracle. Every test runs twice: with the programs
+compiled for themselves at run time (SCEMB_CUSTOM_UPDATE=compile, where a
+failure to compile fails the call) and interpreted; the two give identical
+bits.
 """
 
 import pathlib
@@ -37,6 +40,12 @@ def _gpu():
   if not torch.cuda.is_available():
     pytest.skip("no GPU")
   torch.cuda.set_device(0)
+
+
+@pytest.fixture(autouse=True, params=["compile", "interpret"])
+def update_mode(request, monkeypatch):
+  monkeypatch.setenv("SCEMB_CUSTOM_UPDATE", request.param)
+  return request.param
 
 
 from jax_tpu_embedding.sparsecore.lib.core import input_preprocessing  # pylint: disable=g-import-not-at-top,wrong-import-position
@@ -464,3 +473,61 @@ def test_custom_update_matches_oracle(num_sc):
   np.testing.assert_array_equal(got[0].cpu().numpy()[untouched],
                                 table[untouched])
 
+
+
+def _arith(grad, table, m, v, lr, decay):
+  """Arithmetic and comparison operations only, more than 8 registers."""
+  new_m = np.maximum(decay * m, np.abs(grad))
+  new_v = np.minimum(v + grad * grad, 4.0)
+  step = np.where(new_m > 0.5, grad / (np.sqrt(new_v) + 1e-6), -grad)
+  step = step + np.sign(table) * 0.01
+  return np.clip(table - lr * step, -3.0, 3.0), new_m, new_v
+
+
+@pytest.mark.parametrize("fn,dim", [(_adagrad, 16), (_arith, 16), (_mixed, 24),
+                                    (_adagrad, 12)])
+def test_compiled_equals_interpreted(fn, dim, monkeypatch):
+  """Compiled and interpreted updates give the same bits (16-byte layout:
+  Adagrad at dim 16; 4-byte layout: programs over 8 registers, programs with
+  transcendental operations, dims that are not multiples of 4), both within
+  the oracle's tolerance."""
+  rng, ocsr, csr = _random_csr(4, seed=13)
+  rows = 256
+  table = rng.normal(size=(rows, dim)).astype(np.float32)
+  m = rng.uniform(0.1, 1.0, size=(rows, dim)).astype(np.float32)
+  v = rng.uniform(0.1, 1.0, size=(rows, dim)).astype(np.float32)
+  grad = rng.normal(size=(128, dim)).astype(np.float32)
+  if fn is _adagrad:
+    slots, hyper = [m], [np.float32(0.1)]
+  else:
+    slots, hyper = [m, v], [np.float32(0.1), np.float32(0.9)]
+  text = col.lower_to_stablehlo(fn, dim, len(slots), len(hyper))
+  runs = {}
+  for mode in ("compile", "interpret"):
+    monkeypatch.setenv("SCEMB_CUSTOM_UPDATE", mode)
+    runs[mode] = [
+        x.cpu().numpy()
+        for x in smog.tpu_sparse_dense_matmul_optimizer_grad_primitive.bind(
+            *csr, np.int32(1), _cuda(grad), *hyper, _cuda(table),
+            *[_cuda(x) for x in slots], num_hyperparameters=len(hyper),
+            stablehlo=text, max_ids_per_partition=1024,
+            max_unique_ids_per_partition=1024, num_sc_per_device=4)]
+  for c, i in zip(runs["compile"], runs["interpret"]):
+    np.testing.assert_array_equal(c, i)
+  want = refcpu.sparse_dense_matmul_grad_custom(
+      *ocsr, grad, table, slots, update_fn=fn, hyperparameters=hyper,
+      num_sc_per_device=4, num_scs=4)
+  for g, w in zip(runs["compile"], want):
+    np.testing.assert_allclose(g, w, rtol=1e-5, atol=1e-5)
+
+
+def test_unknown_update_mode_is_an_error(monkeypatch):
+  _, _, csr = _random_csr(1)
+  monkeypatch.setenv("SCEMB_CUSTOM_UPDATE", "fast")
+  with pytest.raises(ValueError, match="SCEMB_CUSTOM_UPDATE"):
+    smog.tpu_sparse_dense_matmul_optimizer_grad_primitive.bind(
+        *csr, np.int32(1), _cuda(np.ones((128, 8))), np.float32(0.1),
+        _cuda(np.zeros((256, 8))), num_hyperparameters=1,
+        stablehlo=col.lower_to_stablehlo(_sgd, 8),
+        max_ids_per_partition=1024, max_unique_ids_per_partition=1024,
+        num_sc_per_device=1)
