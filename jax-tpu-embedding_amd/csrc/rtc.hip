@@ -154,6 +154,7 @@ std::string UpdateSource(const DevProgram& p) {
 
 struct Entry {
   int status = 1;  // 0 compiled, 1 not compiled (error says why)
+  bool retry = false;  // failed loading, not compiling: a later call retries
   RtcKernels kernels{};
   std::string error;
 };
@@ -237,7 +238,10 @@ Entry Compile(const DevProgram& p, const std::string& arch, int g, int vec,
     rc = hipModuleGetFunction(&e.kernels.finish, module, finish_name.c_str());
   }
   if (rc != hipSuccess) {
+    // For example inside a stream capture that forbids it: the program
+    // compiled, so a later call tries again.
     e.error = std::string("loading the code object: ") + hipGetErrorString(rc);
+    e.retry = true;
     return e;
   }
   e.status = 0;
@@ -277,7 +281,8 @@ int RtcKernelsFor(const DevProgram& p, int g, int vec, int src, int unroll,
     it = cache->emplace(key, Compile(p, prop.gcnArchName, g, vec, src, unroll,
                                      mapped)).first;
   }
-  const Entry& e = it->second;
+  const Entry e = it->second;
+  if (e.retry) cache->erase(it);
   if (e.status == 0) {
     *k = e.kernels;
     return 0;

@@ -27,13 +27,15 @@ from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-i
 from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top,wrong-import-position
 
 
-def _workload(one_hot, seed=0, dims=(32, 32, 32)):
+def _workload(one_hot, seed=0, dims=(32, 32, 32), optimizer=None):
   rng = np.random.default_rng(seed)
   batch = 2048
+  if optimizer is None:
+    optimizer = embedding_spec.AdagradOptimizerSpec(0.05)
   tables = [embedding_spec.TableSpec(
       name=f"t{i}", vocabulary_size=int(v), embedding_dim=dims[i],
       initializer=embedding_spec.zeros,
-      optimizer=embedding_spec.AdagradOptimizerSpec(0.05), combiner="sum",
+      optimizer=optimizer, combiner="sum",
       max_ids_per_partition=1 << 16, max_unique_ids_per_partition=1 << 16)
             for i, v in enumerate((100, 5000, 70000))]
   feats = [embedding_spec.FeatureSpec(
@@ -69,7 +71,28 @@ def _workload(one_hot, seed=0, dims=(32, 32, 32)):
 def test_graph_replays_equal_eager_steps(one_hot, dims):
   """With stacks of three widths the lookups and updates run on forked side
   streams (run_per_stack), so the graph also holds their fork and join."""
-  feats, pre, init, grads = _workload(one_hot, dims=dims)
+  _check_graph_replays(*_workload(one_hot, dims=dims))
+
+
+def _custom_adagrad(grad, table, accum, lr):
+  new_accum = accum + grad * grad
+  return table - lr * grad / np.sqrt(new_accum), new_accum
+
+
+@pytest.mark.parametrize("mode", ["compile", "interpret"])
+def test_custom_update_graph_replays_equal_eager_steps(mode, monkeypatch):
+  """A custom optimizer's update captured in the graph: compiled for its
+  program (the warm-up step compiles it; the capture records launches of
+  the loaded code object) and interpreted."""
+  monkeypatch.setenv("SCEMB_CUSTOM_UPDATE", mode)
+  spec = embedding_spec.CustomOptimizerSpec(
+      learning_rate=0.05, custom_computation_fn=_custom_adagrad,
+      slot_variable_initializers_tuple=(lambda *_: 0.1,),
+      short_name_str="custom_adagrad")
+  _check_graph_replays(*_workload(False, dims=(8, 16, 32), optimizer=spec))
+
+
+def _check_graph_replays(feats, pre, init, grads):
 
   def make_state():
     return {n: embedding.EmbeddingVariables(table=t.clone(), slot=(a.clone(),))
