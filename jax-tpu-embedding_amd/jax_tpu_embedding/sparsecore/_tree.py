@@ -53,8 +53,37 @@ def tree_unflatten(treedef, leaves) -> Any:
   return rec(treedef)
 
 
+def _flat_leaves(tree) -> bool:
+  """Whether tree is a plain list or tuple of leaves (the common case, which
+  needs no walk)."""
+  if type(tree) not in (list, tuple):
+    return False
+  for v in tree:
+    if v is None or isinstance(v, (dict, list, tuple)):
+      return False
+  return True
+
+
 def tree_leaves(tree) -> list:
-  return tree_flatten(tree)[0]
+  """The leaves of tree_flatten, without building the structure."""
+  if _flat_leaves(tree):
+    return list(tree)
+  leaves: list = []
+
+  def rec(x):
+    if x is None:
+      return
+    if isinstance(x, dict):
+      for k in sorted(x.keys()):
+        rec(x[k])
+    elif isinstance(x, (list, tuple)):  # NamedTuples included, in order
+      for v in x:
+        rec(v)
+    else:
+      leaves.append(x)
+
+  rec(tree)
+  return leaves
 
 
 def tree_structure(tree):
@@ -70,6 +99,8 @@ def tree_map(fn: Callable, tree, *rest) -> Any:
 
 def leaf_paths(tree) -> list:
   """Paths (tuples of keys / indices) of the leaves, in flattening order."""
+  if _flat_leaves(tree):
+    return [(i,) for i in range(len(tree))]
   out = []
 
   def rec(x, path):

@@ -188,40 +188,44 @@ class _DeviceFeature:
     return self.max_row_length is not None and self.max_row_length <= 1
 
 
-def _to_device_feature(feature, weights, uploads=None) -> _DeviceFeature:
+def _to_device_feature(feature, weights, uploads=None,
+                       dev=None) -> _DeviceFeature:
   """One feature's ids, weights and row splits as device tensors. With
   `uploads` (a _native.HostUploads), host arrays are staged there instead of
   copied one by one: the fields hold handles until _resolve_feature runs
-  after uploads.flush()."""
+  after uploads.flush(). `dev`: the current device, when the caller has it."""
   t = _native.require_gpu()
-  dev = _native.device()
+  if dev is None:
+    dev = _native.device()
 
   def on_device(x, dtype):
     if isinstance(x, t.Tensor):
-      # Already where it goes (the common case for inputs kept in HBM): a
-      # flat view, no copy.
-      if x.is_cuda and x.dtype == dtype and x.device == dev and (
+      # Already where it goes (the common case for inputs kept in HBM): the
+      # tensor itself, whose contiguous elements are the flat layout the
+      # library reads (a view would cost host time and change nothing).
+      if (x.is_cuda and x.dtype == dtype and x.get_device() == dev.index and
           x.is_contiguous()):
-        return x.view(-1)
-      return _native.as_device_tensor(x, dtype, dev)
+        return x
+      return _native.as_device_tensor(x.reshape(-1), dtype, dev)
     if uploads is None:
       return _native.as_device_tensor(x, dtype, dev)
     return uploads.add(x, dtype)
 
   if isinstance(feature, t.Tensor):
-    f = feature
-    if f.dim() == 1:
-      f = f.reshape(-1, 1)
-    if f.dim() != 2:
+    nd = feature.dim()
+    if nd == 1:
+      rows, cols = int(feature.shape[0]), 1
+    elif nd == 2:
+      rows, cols = int(feature.shape[0]), int(feature.shape[1])
+    else:
       raise ValueError("Only 1D and 2D inputs are supported.")
-    ids = on_device(f.reshape(-1), t.int32)
+    ids = on_device(feature, t.int32)
     w = None
     if weights is not None:
       w = on_device(
-          weights.reshape(-1) if isinstance(weights, t.Tensor) else
+          weights if isinstance(weights, t.Tensor) else
           np.asarray(weights, np.float32).reshape(-1), t.float32)
-    return _DeviceFeature(ids, w, None, None, int(f.shape[0]), int(f.numel()),
-                          int(f.shape[1]), None)
+    return _DeviceFeature(ids, w, None, None, rows, rows * cols, cols, None)
   if hasattr(feature, "values") and hasattr(feature, "row_splits"):
     # Ragged tensor (tf.RaggedTensor-like: flat values + row splits), the
     # RaggedTensorInputBatch input of ragged_tensor_input_batch.h:68-127.
@@ -618,12 +622,13 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
                 global_device_count == 1)
   # Host inputs of every stack go to the device in one copy.
   uploads = _native.HostUploads()
+  dev = _native.device()
   stack_feats = {
       name: [
           _to_device_feature(
               features[m.feature_index],
               None if feature_weights is None else
-              feature_weights[m.feature_index], uploads) for m in metas
+              feature_weights[m.feature_index], uploads, dev) for m in metas
       ] for name, metas in stacks.items()
   }
   uploads.flush()
