@@ -318,6 +318,10 @@ def _check_row_splits(splits: np.ndarray, nnz: int) -> int:
 def _resolve_feature(f: _DeviceFeature) -> _DeviceFeature:
   """Staged fields become device addresses (_native.ptr takes both); the
   rows' longest length comes from the staging check."""
+  handle = _native.HostUploads.Handle
+  if not (isinstance(f.ids, handle) or isinstance(f.weights, handle) or
+          isinstance(f.splits, handle)):
+    return f  # nothing was staged: device tensors (or None) as they are
   if getattr(f.splits, "max_row_length", None) is not None:
     f.max_row_length = f.splits.max_row_length
   f.keep = [h.base for h in (f.ids, f.weights, f.splits)
