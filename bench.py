@@ -1225,13 +1225,15 @@ def main():
     # 8D*U per table or slot array read and written.
     (s,) = res["per_stack"].values()
 
-    def bwd_bytes(slots):
-      return 12 * s["N"] + 4 * s["D"] * s["Bs"] + 8 * (1 + slots) * s["D"] * s["U"]
+    def optimizer_bwd_bytes(slots):
+      return (12 * s["N"] + 4 * s["D"] * s["Bs"] +
+              8 * (1 + slots) * s["D"] * s["U"])
 
     out["optimizer_bwd"] = {
         k: {"ms": round(v, 4),
-            "hbm_frac": round(bwd_bytes(1 if k in ONE_SLOT_OPTIMIZERS else 2) /
-                              (v / 1e3) / 1e9 / PEAK_HBM_GBS, 4)}
+            "hbm_frac": round(
+                optimizer_bwd_bytes(1 if k in ONE_SLOT_OPTIMIZERS else 2) /
+                (v / 1e3) / 1e9 / PEAK_HBM_GBS, 4)}
         for k, v in res["optimizer_bwd_ms"].items()}
   if res["minibatching"]:
     # Same entries (nothing dropped), so the same compulsory bytes.
