@@ -465,6 +465,18 @@ int scemb_stage_row_splits(const int64_t* row_splits, int64_t num_rows,
                            int64_t nnz, int64_t* dst,
                            int64_t* max_row_length);
 
+/* No counterpart in the reference (its row splits never leave the host).
+ * scemb_stage_row_splits for `count` features in one call, their rows spread
+ * over a few host threads: feature i's splits row_splits[i] [num_rows[i] + 1]
+ * are checked against nnz[i], copied to dst[i] and their longest row stored
+ * in max_row_length[i]. SCEMB_ERR_INVALID_ARGUMENT when any feature's splits
+ * do not hold; *first_bad (may be null) is then its index, else -1. */
+int scemb_stage_row_splits_batch(int32_t count,
+                                 const int64_t* const* row_splits,
+                                 const int64_t* num_rows, const int64_t* nnz,
+                                 int64_t* const* dst, int64_t* max_row_length,
+                                 int32_t* first_bad);
+
 /* scemb_preprocess_options_t.flags. Where the features' sample rows are
  * disjoint and neither id dropping nor minibatching is on, the library merges
  * the copies of an id within one input row while extracting (the only

@@ -133,6 +133,64 @@ __device__ __forceinline__ T BlockExclusiveScan(T v, T* smem, T* total) {
   return res;
 }
 
+// ---------------------------------------------------------------------------
+// Grouped launches: one kernel over several independent problems (the
+// stacked tables of one call). Every problem's arguments A travel in the
+// kernel argument block; problem p owns work-groups [first[p], first[p + 1]),
+// and A::Run(args, block, blocks) runs one of them with its index within the
+// problem. A kernel body written against (block, blocks) instead of
+// (blockIdx.x, gridDim.x) serves single and grouped launches alike.
+// ---------------------------------------------------------------------------
+constexpr int kMaxGroup = 8;
+
+template <typename A>
+struct Group {
+  int32_t n;
+  uint32_t first[kMaxGroup + 1];
+  A a[kMaxGroup];
+};
+
+template <typename A>
+__global__ __launch_bounds__(A::kBlock) void GroupedKernel(Group<A> g) {
+  int p = 0;
+  while (p + 1 < g.n && blockIdx.x >= g.first[p + 1]) ++p;
+  A::Run(g.a[p], blockIdx.x - g.first[p], g.first[p + 1] - g.first[p]);
+}
+
+#ifndef __HIPCC_RTC__
+// Enqueues GroupedKernel<A> over problems i with args[i] and blocks[i]
+// work-groups, at most kMaxGroup per launch; problems of no blocks are left
+// out.
+template <typename A>
+int LaunchGrouped(const A* args, const int64_t* blocks, int n,
+                  hipStream_t stream) {
+  static_assert(sizeof(Group<A>) <= 3584,
+                "grouped arguments must fit the kernel argument block");
+  Group<A> g;
+  g.n = 0;
+  int64_t total = 0;
+  for (int i = 0; i <= n; ++i) {
+    const bool last = i == n;
+    const int64_t b = last ? 0 : blocks[i];
+    if (!last && b <= 0) continue;
+    if (g.n > 0 && (last || g.n == kMaxGroup || total + b > 0xffffffffll)) {
+      g.first[g.n] = static_cast<uint32_t>(total);
+      hipLaunchKernelGGL(GroupedKernel<A>, dim3(static_cast<uint32_t>(total)),
+                         dim3(A::kBlock), 0, stream, g);
+      SCEMB_LAUNCH_CHECK();
+      g.n = 0;
+      total = 0;
+    }
+    if (last) break;
+    g.first[g.n] = static_cast<uint32_t>(total);
+    g.a[g.n] = args[i];
+    ++g.n;
+    total += b;
+  }
+  return 0;
+}
+#endif  // __HIPCC_RTC__
+
 // Non-coherent-free load of data written by other work-groups of the same
 // kernel after an acquire fence.
 __device__ __forceinline__ void AcquireFence() {

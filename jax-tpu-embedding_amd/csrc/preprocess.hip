@@ -714,10 +714,10 @@ struct FillParams {
 // second loop reduces device stats (max over local SCs). With
 // br.num_buckets > 0 the block first reduces the bucket stats itself
 // (BucketReduce folded in; bstats is then br.out).
-__global__ __launch_bounds__(256) void FillPlanKernel(
-    const BucketStats* bstats, FillParams fp, int32_t* rp_out,
+__device__ __forceinline__ void FillPlanBody(
+    const BucketStats* bstats, const FillParams& fp, int32_t* rp_out,
     FillPlan* plans, int32_t* stat_max_ids, int32_t* stat_max_unique,
-    int32_t* stat_required, int64_t* counters, BucketReduceArgs br) {
+    int32_t* stat_required, int64_t* counters, const BucketReduceArgs& br) {
   if (br.num_buckets > 0) {
     for (int64_t bkt = threadIdx.x; bkt < br.num_buckets; bkt += blockDim.x) {
       br.out[bkt] = br.col_heads != nullptr
@@ -819,6 +819,32 @@ __global__ __launch_bounds__(256) void FillPlanKernel(
     stat_max_unique[dp] = mu;
   }
 }
+
+__global__ __launch_bounds__(256) void FillPlanKernel(
+    const BucketStats* bstats, FillParams fp, int32_t* rp_out,
+    FillPlan* plans, int32_t* stat_max_ids, int32_t* stat_max_unique,
+    int32_t* stat_required, int64_t* counters, BucketReduceArgs br) {
+  FillPlanBody(bstats, fp, rp_out, plans, stat_max_ids, stat_max_unique,
+               stat_required, counters, br);
+}
+
+// FillPlanKernel's arguments for a grouped launch (one block per problem).
+struct FillPlanArgs {
+  static constexpr int kBlock = 256;
+  const BucketStats* bstats;
+  FillParams fp;
+  int32_t* rp_out;
+  FillPlan* plans;
+  int32_t* stat_max_ids;
+  int32_t* stat_max_unique;
+  int32_t* stat_required;
+  int64_t* counters;
+  BucketReduceArgs br;
+  __device__ static void Run(const FillPlanArgs& a, uint32_t, uint32_t) {
+    FillPlanBody(a.bstats, a.fp, a.rp_out, a.plans, a.stat_max_ids,
+                 a.stat_max_unique, a.stat_required, a.counters, a.br);
+  }
+};
 
 // The minibatching layout (input_preprocessing_util.cc:135-143, :331-473):
 // one thread per device replays FillBufferSegment over the (SC, minibatch)
@@ -1336,14 +1362,11 @@ __global__ __launch_bounds__(256) void ViewCompact(
 // Also copies the grouped-entry total into the counters when `totals` (low
 // half of a 64-bit scan total) or `total32` is not null (after the scatter,
 // which reads it).
-__global__ __launch_bounds__(256) void WritePadding(const FillPlan* plans,
-                                                    int64_t num_buckets,
-                                                    FillParams fp, int32_t* eid,
-                                                    int32_t* sid, float* gains,
-                                                    const uint64_t* totals,
-                                                    const uint32_t* total32,
-                                                    int64_t* counters) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void WritePaddingBody(
+    uint32_t blk, const FillPlan* plans, int64_t num_buckets,
+    const FillParams& fp, int32_t* eid, int32_t* sid, float* gains,
+    const uint64_t* totals, const uint32_t* total32, int64_t* counters) {
+  const int64_t t = static_cast<int64_t>(blk) * blockDim.x + threadIdx.x;
   if (t == 0 && totals != nullptr) {
     counters[3] = static_cast<int64_t>(static_cast<uint32_t>(totals[0]));
   }
@@ -1367,6 +1390,36 @@ __global__ __launch_bounds__(256) void WritePadding(const FillPlan* plans,
   sid[pos] = kPadInt;
   gains[pos] = __uint_as_float(kNanBits);
 }
+
+__global__ __launch_bounds__(256) void WritePadding(const FillPlan* plans,
+                                                    int64_t num_buckets,
+                                                    FillParams fp, int32_t* eid,
+                                                    int32_t* sid, float* gains,
+                                                    const uint64_t* totals,
+                                                    const uint32_t* total32,
+                                                    int64_t* counters) {
+  WritePaddingBody(blockIdx.x, plans, num_buckets, fp, eid, sid, gains, totals,
+                   total32, counters);
+}
+
+// WritePadding's arguments for a grouped launch.
+struct WritePaddingArgs {
+  static constexpr int kBlock = 256;
+  const FillPlan* plans;
+  int64_t num_buckets;
+  FillParams fp;
+  int32_t* eid;
+  int32_t* sid;
+  float* gains;
+  const uint64_t* totals;
+  const uint32_t* total32;
+  int64_t* counters;
+  __device__ static void Run(const WritePaddingArgs& a, uint32_t blk,
+                             uint32_t) {
+    WritePaddingBody(blk, a.plans, a.num_buckets, a.fp, a.eid, a.sid, a.gains,
+                     a.totals, a.total32, a.counters);
+  }
+};
 
 __global__ void ZeroI64(int64_t* p, int n) {
   if (threadIdx.x < n) p[threadIdx.x] = 0;
@@ -1552,11 +1605,11 @@ __device__ __forceinline__ uint32_t DedupFind(const uint32_t* table,
 // that enter the sample view (a first copy whose local row is below
 // `view_rows`).
 template <typename K, bool kHashed>
-__global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
-    const SliceDesc* slices, int num_slices, const FeatureDev* feats,
-    const BlockRows* block_rows, int64_t total_ids, int combiner,
-    int rows_of_one, KeyLayout kl, int64_t view_rows, K* keys, uint64_t* pay,
-    uint32_t* view_counts, int64_t* counters) {
+__device__ __forceinline__ void ExtractUniqueBody(
+    uint32_t blk, const SliceDesc* slices, int num_slices,
+    const FeatureDev* feats, const BlockRows* block_rows, int64_t total_ids,
+    int combiner, int rows_of_one, const KeyLayout& kl, int64_t view_rows,
+    K* keys, uint64_t* pay, uint32_t* view_counts, int64_t* counters) {
   constexpr bool kWeighted = !kHashed;
   __shared__ int32_t s_splits[kUniqueStagedSplits];  // splits - span_b
   __shared__ int32_t s_ids[kDedupStage];
@@ -1564,9 +1617,9 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
   __shared__ float s_div[kWeighted ? kUniqueStagedSplits : 1];
   __shared__ uint32_t s_table[kHashed ? kDedupSlots : 1];
   __shared__ uint32_t s_counts[kHashed ? kDedupSlots / 2 : 1];
-  const int64_t blk_first = static_cast<int64_t>(blockIdx.x) * blockDim.x;
+  const int64_t blk_first = static_cast<int64_t>(blk) * blockDim.x;
   const int64_t o = blk_first + threadIdx.x;
-  const BlockRows br = block_rows[blockIdx.x];
+  const BlockRows br = block_rows[blk];
   const int block_slice = br.slice;
   int64_t row_lo = 0, row_hi = -1;
   if (block_slice >= 0) ClampBlockRows(br, slices[block_slice], &row_lo, &row_hi);
@@ -1786,23 +1839,50 @@ __global__ __launch_bounds__(kExtractBlock) void ExtractUnique(
   }
   if (view_counts != nullptr) {
     const int c = __syncthreads_count(view_entry);
-    if (threadIdx.x == 0) view_counts[blockIdx.x] = static_cast<uint32_t>(c);
+    if (threadIdx.x == 0) view_counts[blk] = static_cast<uint32_t>(c);
   }
 }
+
+// ExtractUnique's arguments for a grouped launch: one block per
+// kExtractBlock extracted ids.
+template <typename K, bool kHashed>
+struct ExtractUniqueArgs {
+  static constexpr int kBlock = kExtractBlock;
+  const SliceDesc* slices;
+  int num_slices;
+  const FeatureDev* feats;
+  const BlockRows* block_rows;
+  int64_t total_ids;
+  int combiner;
+  int rows_of_one;
+  KeyLayout kl;
+  int64_t view_rows;
+  K* keys;
+  uint64_t* pay;
+  uint32_t* view_counts;
+  int64_t* counters;
+  __device__ static void Run(const ExtractUniqueArgs& a, uint32_t blk,
+                             uint32_t) {
+    ExtractUniqueBody<K, kHashed>(blk, a.slices, a.num_slices, a.feats,
+                                  a.block_rows, a.total_ids, a.combiner,
+                                  a.rows_of_one, a.kl, a.view_rows, a.keys,
+                                  a.pay, a.view_counts, a.counters);
+  }
+};
 
 // The sample view from ExtractUnique's arrays: the entries a block counted
 // go, in extraction order, to view_off[block] onwards (positions at or past
 // n are not written); positions from *view_total to n get the unused key.
 // The grid covers max(extraction blocks, n / 256).
 template <typename K>
-__global__ __launch_bounds__(kExtractBlock) void ViewWrite(
-    const K* keys, const uint64_t* pay, const uint32_t* view_off,
-    const uint32_t* view_total, int64_t m, int64_t n, KeyLayout kl,
+__device__ __forceinline__ void ViewWriteBody(
+    uint32_t blk, const K* keys, const uint64_t* pay, const uint32_t* view_off,
+    const uint32_t* view_total, int64_t m, int64_t n, const KeyLayout& kl,
     int64_t view_rows, uint32_t unused_key, uint32_t* vkeys,
     uint64_t* ventries) {
   __shared__ uint32_t smem[kExtractBlock / kWave + 1];
-  const int64_t o = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (static_cast<int64_t>(blockIdx.x) * blockDim.x < m) {  // uniform
+  const int64_t o = static_cast<int64_t>(blk) * blockDim.x + threadIdx.x;
+  if (static_cast<int64_t>(blk) * blockDim.x < m) {  // uniform
     bool in_view = false;
     uint32_t p = 0, local = 0;
     if (o < m) {
@@ -1819,7 +1899,7 @@ __global__ __launch_bounds__(kExtractBlock) void ViewWrite(
         BlockExclusiveScan<uint32_t, kExtractBlock>(in_view ? 1u : 0u, smem,
                                                     &count);
     if (in_view) {
-      const int64_t q = static_cast<int64_t>(view_off[blockIdx.x]) + rank;
+      const int64_t q = static_cast<int64_t>(view_off[blk]) + rank;
       if (q < n) {
         const uint64_t v = pay[o];
         vkeys[q] = static_cast<uint32_t>(v);
@@ -1834,6 +1914,26 @@ __global__ __launch_bounds__(kExtractBlock) void ViewWrite(
     ventries[o] = 0;
   }
 }
+
+template <typename K>
+struct ViewWriteArgs {
+  static constexpr int kBlock = kExtractBlock;
+  const K* keys;
+  const uint64_t* pay;
+  const uint32_t* view_off;
+  const uint32_t* view_total;
+  int64_t m;
+  int64_t n;
+  KeyLayout kl;
+  int64_t view_rows;
+  uint32_t unused_key;
+  uint32_t* vkeys;
+  uint64_t* ventries;
+  __device__ static void Run(const ViewWriteArgs& a, uint32_t blk, uint32_t) {
+    ViewWriteBody<K>(blk, a.keys, a.pay, a.view_off, a.view_total, a.m, a.n,
+                     a.kl, a.view_rows, a.unused_key, a.vkeys, a.ventries);
+  }
+};
 
 // First pass source of the sort: the extraction arrays, sentinel keys left
 // out (duplicates and ids outside the table), so that the later passes and
@@ -1863,12 +1963,13 @@ constexpr int kGroupItems = 8;  // sorted entries per GroupUnique thread
 // atomic per bucket and block (integer sums: the order does not matter).
 // col_heads starts at zero.
 template <typename K>
-__global__ __launch_bounds__(256) void GroupUnique(
-    const K* skeys, const uint32_t* total, KeyLayout kl, int num_partitions,
-    int32_t* part_first, int32_t* part_last, int32_t* col_heads) {
+__device__ __forceinline__ void GroupUniqueBody(
+    uint32_t blk, const K* skeys, const uint32_t* total, const KeyLayout& kl,
+    int num_partitions, int32_t* part_first, int32_t* part_last,
+    int32_t* col_heads) {
   __shared__ int32_t s_cnt[256];
   const int64_t n = static_cast<int64_t>(total[0]);
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * 256 * kGroupItems;
+  const int64_t base = static_cast<int64_t>(blk) * 256 * kGroupItems;
   if (base >= n) return;  // uniform
   const K col_mask = kl.col_bits >= 64 ? ~K(0) : ((K(1) << kl.col_bits) - 1);
   auto bucket_of = [&](K key) -> int64_t {
@@ -1938,15 +2039,33 @@ __global__ __launch_bounds__(256) void GroupUnique(
   }
 }
 
+template <typename K>
+struct GroupUniqueArgs {
+  static constexpr int kBlock = 256;
+  const K* skeys;
+  const uint32_t* total;
+  KeyLayout kl;
+  int num_partitions;
+  int32_t* part_first;
+  int32_t* part_last;
+  int32_t* col_heads;
+  __device__ static void Run(const GroupUniqueArgs& a, uint32_t blk,
+                             uint32_t) {
+    GroupUniqueBody<K>(blk, a.skeys, a.total, a.kl, a.num_partitions,
+                       a.part_first, a.part_last, a.col_heads);
+  }
+};
+
 // One thread per sorted entry: the CSR position is the bucket's planned
 // start plus the entry's rank in its bucket (every entry is kept; those
 // past the bucket's room in the static buffer are not written).
 template <typename K>
-__global__ __launch_bounds__(256) void ScatterUnique(
-    const K* skeys, const uint64_t* spay, const uint32_t* total, KeyLayout kl,
-    FillParams fp, int32_t bps, const int32_t* part_first,
-    const FillPlan* plans, int32_t* eid, int32_t* sid, float* gains) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void ScatterUniqueBody(
+    uint32_t blk, const K* skeys, const uint64_t* spay, const uint32_t* total,
+    const KeyLayout& kl, const FillParams& fp, int32_t bps,
+    const int32_t* part_first, const FillPlan* plans, int32_t* eid,
+    int32_t* sid, float* gains) {
+  const int64_t i = static_cast<int64_t>(blk) * blockDim.x + threadIdx.x;
   if (i >= static_cast<int64_t>(total[0])) return;
   const K key = skeys[i];
   const K col_mask = kl.col_bits >= 64 ? ~K(0) : ((K(1) << kl.col_bits) - 1);
@@ -1965,6 +2084,27 @@ __global__ __launch_bounds__(256) void ScatterUnique(
                                   static_cast<uint32_t>(bps));
   gains[pos] = __uint_as_float(static_cast<uint32_t>(v >> 32));
 }
+
+template <typename K>
+struct ScatterUniqueArgs {
+  static constexpr int kBlock = 256;
+  const K* skeys;
+  const uint64_t* spay;
+  const uint32_t* total;
+  KeyLayout kl;
+  FillParams fp;
+  int32_t bps;
+  const int32_t* part_first;
+  const FillPlan* plans;
+  int32_t* eid;
+  int32_t* sid;
+  float* gains;
+  __device__ static void Run(const ScatterUniqueArgs& a, uint32_t blk,
+                             uint32_t) {
+    ScatterUniqueBody<K>(blk, a.skeys, a.spay, a.total, a.kl, a.fp, a.bps,
+                         a.part_first, a.plans, a.eid, a.sid, a.gains);
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Host planning.
@@ -2738,39 +2878,91 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
 // leaves out the sentinel keys, then GroupUnique, the fill plan,
 // ScatterUnique and the padding. Same outputs as RunPipeline for the calls
 // Preprocess routes here.
+// One stack of the route that groups at extraction, between PrepareUnique
+// (buffers carved from the stack's workspace, checks, the set-up launch and
+// every later stage's arguments) and EnqueueUnique (the stages of several
+// stacks together, one grouped launch per stage, common.h).
 template <typename K>
-int RunUniquePipeline(const scemb_feature_t* feats, int nf,
-                      const scemb_preprocess_options_t* o,
-                      const scemb_preprocess_output_t* out, const Plan& pl,
-                      Arena& ws, hipStream_t stream) {
-  using radix::kSortBlock;
-  using radix::kSortTile;
-  using Arr = radix::ArraySource<K, uint64_t>;
-  using Sink = radix::ArraySink<K, uint64_t>;
+struct UniqueStack {
+  Arena* ws = nullptr;
+  bool measuring = true;
+  bool weighted = false;
+  int64_t M = 0;
+  int64_t extract_blocks = 0;
+  radix::DigitPlan dp{};
+  int key_bits = 0;
+  int64_t tiles = 0;
+  K* keys = nullptr;
+  K* keys_alt = nullptr;
+  uint64_t* pay = nullptr;
+  uint64_t* pay_alt = nullptr;
+  bool view = false;
+  uint32_t* view_off = nullptr;
+  uint32_t* view_total = nullptr;
+  uint32_t* view_partial = nullptr;  // null: the view scan is not grouped
+  uint32_t* hist = nullptr;
+  uint32_t* hist_partial = nullptr;  // null: the sort's scans are not grouped
+  uint32_t* totals = nullptr;        // [passes], cleared by the set-up
+  ExtractUniqueArgs<K, true> ex;     // fields shared by both variants
+  int64_t view_grid = 0;
+  ViewWriteArgs<K> vw;
+  GroupUniqueArgs<K> gu;
+  FillPlanArgs fill;
+  ScatterUniqueArgs<K> sc;
+  WritePaddingArgs pad;
+  int64_t pad_blocks = 0;
+};
+
+template <typename K>
+int PrepareUnique(const scemb_feature_t* feats, int nf,
+                  const scemb_preprocess_options_t* o,
+                  const scemb_preprocess_output_t* out, const Plan& pl,
+                  Arena& ws, hipStream_t stream, UniqueStack<K>* u) {
   const int64_t M = pl.total_ids;
   const int64_t num_buckets = static_cast<int64_t>(pl.L) * pl.S * pl.NS;
   const int64_t extract_blocks = CeilDiv(M, kExtractBlock);
   const bool view = o->build_sample_view != 0;
-  K* keys = ws.Take<K>(M);
-  K* keys_alt = ws.Take<K>(M);
-  uint64_t* pay = ws.Take<uint64_t>(M);
-  uint64_t* pay_alt = ws.Take<uint64_t>(M);
+  u->ws = &ws;
+  u->measuring = ws.measuring();
+  u->weighted = o->has_variable_weights != 0;
+  u->M = M;
+  u->extract_blocks = extract_blocks;
+  u->view = view;
+  u->keys = ws.Take<K>(M);
+  u->keys_alt = ws.Take<K>(M);
+  u->pay = ws.Take<uint64_t>(M);
+  u->pay_alt = ws.Take<uint64_t>(M);
   BlockRows* block_rows = ws.Take<BlockRows>(extract_blocks);
-  uint32_t* view_off = view ? ws.Take<uint32_t>(extract_blocks) : nullptr;
-  uint32_t* view_total = view ? ws.Take<uint32_t>(1) : nullptr;
+  u->view_off = view ? ws.Take<uint32_t>(extract_blocks) : nullptr;
   int32_t* part_first = ws.Take<int32_t>(num_buckets);
   int32_t* part_last = ws.Take<int32_t>(num_buckets);
-  int32_t* col_heads = ws.Take<int32_t>(num_buckets);
+  u->key_bits = std::max(1, pl.kl.col_bits + pl.kl.seg_bits);
+  u->dp = radix::PlanDigits(u->key_bits);
+  // Cleared by the set-up launch: the buckets' distinct-column counts, the
+  // sort's per-pass totals and the view's total, so that a stack of no ids
+  // (whose scans are not launched) reads zeros.
+  const int64_t head_words = RoundUp(num_buckets, 64);
+  const int64_t cleared = head_words + RoundUp(u->dp.passes + 1, 64);
+  int32_t* col_heads = ws.Take<int32_t>(cleared);
+  u->totals = col_heads == nullptr
+                  ? nullptr
+                  : reinterpret_cast<uint32_t*>(col_heads + head_words);
+  u->view_total = view && u->totals != nullptr ? u->totals + u->dp.passes
+                                               : nullptr;
   BucketStats* bstats = ws.Take<BucketStats>(num_buckets);
   FillPlan* plans = ws.Take<FillPlan>(num_buckets);
   SliceDesc* slices =
       ws.Take<SliceDesc>(static_cast<int64_t>(pl.slices.size()));
   FeatureDev* fdev = ws.Take<FeatureDev>(nf);
-  const int key_bits = std::max(1, pl.kl.col_bits + pl.kl.seg_bits);
-  const radix::DigitPlan dp = radix::PlanDigits(key_bits);
-  const int64_t tiles = CeilDiv(M, kSortTile);
-  uint32_t* hist = ws.Take<uint32_t>(tiles * (int64_t{1} << dp.digit));
-  uint32_t* totals = ws.Take<uint32_t>(dp.passes);
+  u->tiles = CeilDiv(M, radix::kSortTile);
+  const int64_t cells = u->tiles * (int64_t{1} << u->dp.digit);
+  u->hist = ws.Take<uint32_t>(cells);
+  // The scans' tile sums for grouped scans; a scan too long for one is left
+  // to ExclusiveScan, whose temporaries EnqueueUnique takes from ws.
+  const int64_t view_words = view ? GroupedScanPartialWords(extract_blocks) : 0;
+  const int64_t hist_words = GroupedScanPartialWords(cells);
+  u->view_partial = view_words > 0 ? ws.Take<uint32_t>(view_words) : nullptr;
+  u->hist_partial = hist_words > 0 ? ws.Take<uint32_t>(hist_words) : nullptr;
   if (view) {
     if (pl.L != 1 || pl.G != 1) {
       return Fail(SCEMB_ERR_INVALID_ARGUMENT,
@@ -2782,12 +2974,11 @@ int RunUniquePipeline(const scemb_feature_t* feats, int nf,
     }
   }
   const int64_t view_rows = view ? o->table_rows / pl.NS : 0;
-  const bool measuring = ws.measuring();
   const int64_t counters_off = RoundUp(2 * static_cast<int64_t>(pl.L) * pl.NS +
                                        static_cast<int64_t>(pl.L) * pl.S, 2);
   const int num_slices = static_cast<int>(pl.slices.size());
   int64_t* counters = nullptr;
-  if (!measuring) {
+  if (!u->measuring) {
     if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
     if (out == nullptr || out->row_pointers == nullptr || out->stats == nullptr ||
         out->embedding_ids == nullptr || out->sample_ids == nullptr ||
@@ -2801,101 +2992,40 @@ int RunUniquePipeline(const scemb_feature_t* feats, int nf,
     if ((reinterpret_cast<uintptr_t>(counters) & 7u) != 0) {
       return Fail(SCEMB_ERR_INVALID_ARGUMENT, "stats buffer must be 8-byte aligned");
     }
-    const SetupTargets tg{part_first, part_last, num_buckets,  col_heads,
-                          num_buckets, slices,    fdev,        block_rows,
+    const SetupTargets tg{part_first, part_last, num_buckets, col_heads,
+                          cleared,    slices,    fdev,        block_rows,
                           M > 0 ? extract_blocks : 0};
     const int su = EnqueueSetup(feats, nf, o, pl, counters_off, out->stats,
                                 counters, tg, stream);
     if (su != 0) return su;
-    if (M > 0) {
-      // Only dense features of one id per row are known to need no merging
-      // (max_row_length is a hint and may understate).
-      int rows_of_one = 1;
-      for (int f = 0; f < nf; ++f) {
-        if (feats[f].row_splits != nullptr || feats[f].valency > 1) {
-          rows_of_one = 0;
-        }
-      }
-      if (o->has_variable_weights) {
-        hipLaunchKernelGGL((ExtractUnique<K, false>), dim3(extract_blocks),
-                           dim3(kExtractBlock), 0, stream, slices, num_slices,
-                           fdev, block_rows, M, o->combiner, rows_of_one,
-                           pl.kl, view_rows, keys, pay, view_off, counters);
-      } else {
-        hipLaunchKernelGGL((ExtractUnique<K, true>), dim3(extract_blocks),
-                           dim3(kExtractBlock), 0, stream, slices, num_slices,
-                           fdev, block_rows, M, o->combiner, rows_of_one,
-                           pl.kl, view_rows, keys, pay, view_off, counters);
-      }
-      SCEMB_LAUNCH_CHECK();
+  }
+  // Only dense features of one id per row are known to need no merging
+  // (max_row_length is a hint and may understate).
+  int rows_of_one = 1;
+  for (int f = 0; f < nf; ++f) {
+    if (feats[f].row_splits != nullptr || feats[f].valency > 1) {
+      rows_of_one = 0;
     }
   }
-  int st = 0;
+  u->ex = ExtractUniqueArgs<K, true>{
+      slices,      num_slices,  fdev, block_rows, M,           o->combiner,
+      rows_of_one, pl.kl,       view_rows,        u->keys,     u->pay,
+      u->view_off, counters};
   if (view) {
-    st = ExclusiveScan<uint32_t>(view_off, view_off, extract_blocks,
-                                 view_total, ws, stream);
-    if (st != 0) return st;
     const int64_t n = pl.coo_size;
-    const int64_t grid = std::max(extract_blocks, CeilDiv(n, kExtractBlock));
-    if (!measuring && grid > 0) {
-      hipLaunchKernelGGL((ViewWrite<K>), dim3(grid), dim3(kExtractBlock), 0,
-                         stream, keys, pay, view_off, view_total, M, n, pl.kl,
-                         view_rows, static_cast<uint32_t>(pl.batch_for_device),
-                         out->view_keys, out->view_entries);
-      SCEMB_LAUNCH_CHECK();
-    }
+    u->view_grid = std::max(extract_blocks, CeilDiv(n, kExtractBlock));
+    u->vw = ViewWriteArgs<K>{u->keys,  u->pay, u->view_off,
+                             u->view_total, M,  n,
+                             pl.kl,    view_rows,
+                             static_cast<uint32_t>(pl.batch_for_device),
+                             out != nullptr ? out->view_keys : nullptr,
+                             out != nullptr ? out->view_entries : nullptr};
   }
-  // Sort. Pass p writes (keys_alt, pay_alt) when p is even.
-  const UniqueSource<K> first_src{keys, pay};
-  for (int pass = 0; pass < dp.passes; ++pass) {
-    const int shift = pass * dp.digit;
-    const int pbits = key_bits - shift < dp.digit ? key_bits - shift : dp.digit;
-    const uint32_t mask = (1u << pbits) - 1u;
-    const int64_t cells = tiles * (int64_t{1} << pbits);
-    const bool even = pass % 2 == 0;
-    const Arr arr{even ? keys : keys_alt, even ? pay : pay_alt};
-    const Sink sink{even ? keys_alt : keys, even ? pay_alt : pay};
-    if (!measuring && M > 0) {
-      if (pass == 0) {
-        hipLaunchKernelGGL((radix::RadixHistogramK<K, UniqueSource<K>>),
-                           dim3(tiles), dim3(kSortBlock), 0, stream, first_src,
-                           M, nullptr, 0, shift, mask, tiles, hist);
-      } else {
-        hipLaunchKernelGGL((radix::RadixHistogramK<K, Arr>), dim3(tiles),
-                           dim3(kSortBlock), 0, stream, arr, M, totals, 1,
-                           shift, mask, tiles, hist);
-      }
-      SCEMB_LAUNCH_CHECK();
-    }
-    st = ExclusiveScan<uint32_t>(hist, hist, cells, totals + pass, ws, stream);
-    if (st != 0) return st;
-    if (!measuring && M > 0) {
-      if (pass == 0) {
-        hipLaunchKernelGGL(
-            (radix::RadixScatterK<K, uint64_t, UniqueSource<K>, Sink>),
-            dim3(tiles), dim3(kSortBlock), 0, stream, first_src, sink, M,
-            nullptr, 0, shift, mask, pbits, tiles, hist, totals + pass, false);
-      } else {
-        hipLaunchKernelGGL((radix::RadixScatterK<K, uint64_t, Arr, Sink>),
-                           dim3(tiles), dim3(kSortBlock), 0, stream, arr, sink,
-                           M, totals, 1, shift, mask, pbits, tiles, hist,
-                           totals + pass, false);
-      }
-      SCEMB_LAUNCH_CHECK();
-    }
-  }
-  if (measuring) return 0;
-  if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
-  const bool odd = dp.passes % 2 == 1;
-  const K* skeys = odd ? keys_alt : keys;
-  const uint64_t* spay = odd ? pay_alt : pay;
-  if (M > 0) {
-    hipLaunchKernelGGL((GroupUnique<K>),
-                       dim3(CeilDiv(M, int64_t{256} * kGroupItems)), dim3(256),
-                       0, stream, skeys, totals, pl.kl, pl.NS, part_first,
-                       part_last, col_heads);
-    SCEMB_LAUNCH_CHECK();
-  }
+  const bool odd = u->dp.passes % 2 == 1;
+  const K* skeys = odd ? u->keys_alt : u->keys;
+  const uint64_t* spay = odd ? u->pay_alt : u->pay;
+  u->gu = GroupUniqueArgs<K>{skeys,      u->totals, pl.kl,    pl.NS,
+                             part_first, part_last, col_heads};
   FillParams fp;
   fp.local_devices = pl.L;
   fp.segs_per_device = pl.S;
@@ -2911,25 +3041,221 @@ int RunUniquePipeline(const scemb_feature_t* feats, int nf,
   for (int bkt = 0; bkt < kMaxMinibatches; ++bkt) fp.minibatch_of[bkt] = 0;
   const BucketReduceArgs bra{part_first, part_last, nullptr,   nullptr,
                              nullptr,    num_buckets, bstats, col_heads};
-  hipLaunchKernelGGL(FillPlanKernel, dim3(1), dim3(256), 0, stream, bstats, fp,
-                     out->row_pointers, plans, out->stats,
-                     out->stats + static_cast<int64_t>(pl.L) * pl.NS,
-                     out->stats + 2 * static_cast<int64_t>(pl.L) * pl.NS,
-                     counters, bra);
-  SCEMB_LAUNCH_CHECK();
-  if (M > 0) {
-    hipLaunchKernelGGL((ScatterUnique<K>), dim3(CeilDiv(M, 256)), dim3(256), 0,
-                       stream, skeys, spay, totals, pl.kl, fp,
-                       static_cast<int32_t>(pl.bps), part_first, plans,
-                       out->embedding_ids, out->sample_ids, out->gains);
-    SCEMB_LAUNCH_CHECK();
-  }
-  hipLaunchKernelGGL(WritePadding, dim3(CeilDiv(num_buckets * kAlign, 256)),
-                     dim3(256), 0, stream, plans, num_buckets, fp,
-                     out->embedding_ids, out->sample_ids, out->gains, nullptr,
-                     totals, counters);
-  SCEMB_LAUNCH_CHECK();
+  int32_t* stats = out != nullptr ? out->stats : nullptr;
+  u->fill = FillPlanArgs{
+      bstats,
+      fp,
+      out != nullptr ? out->row_pointers : nullptr,
+      plans,
+      stats,
+      stats == nullptr ? nullptr : stats + static_cast<int64_t>(pl.L) * pl.NS,
+      stats == nullptr ? nullptr
+                       : stats + 2 * static_cast<int64_t>(pl.L) * pl.NS,
+      counters,
+      bra};
+  u->sc = ScatterUniqueArgs<K>{
+      skeys,
+      spay,
+      u->totals,
+      pl.kl,
+      fp,
+      static_cast<int32_t>(pl.bps),
+      part_first,
+      plans,
+      out != nullptr ? out->embedding_ids : nullptr,
+      out != nullptr ? out->sample_ids : nullptr,
+      out != nullptr ? out->gains : nullptr};
+  u->pad = WritePaddingArgs{plans,
+                            num_buckets,
+                            fp,
+                            out != nullptr ? out->embedding_ids : nullptr,
+                            out != nullptr ? out->sample_ids : nullptr,
+                            out != nullptr ? out->gains : nullptr,
+                            nullptr,
+                            u->totals,
+                            counters};
+  u->pad_blocks = CeilDiv(num_buckets * kAlign, 256);
   return 0;
+}
+
+// The stages of every stack in `st` (all prepared for the same workspace
+// mode), in order, each one grouped launch over the stacks that have work in
+// it: extraction, the view's scan and write, the radix passes (histogram,
+// scan, scatter), grouping, the fill plan, the scatter into the CSR and the
+// padding. Measuring, only the temporaries of scans left to ExclusiveScan are
+// taken.
+template <typename K, bool kHashed>
+int EnqueueUnique(UniqueStack<K>* const* st, int n, hipStream_t stream) {
+  const bool measuring = n > 0 && st[0]->measuring;
+  std::vector<int64_t> blocks(n);
+  int rc = 0;
+  // Extraction.
+  if (!measuring) {
+    std::vector<ExtractUniqueArgs<K, kHashed>> ex(n);
+    for (int i = 0; i < n; ++i) {
+      const ExtractUniqueArgs<K, true>& e = st[i]->ex;
+      ex[i] = ExtractUniqueArgs<K, kHashed>{
+          e.slices,      e.num_slices, e.feats,     e.block_rows, e.total_ids,
+          e.combiner,    e.rows_of_one, e.kl,       e.view_rows,  e.keys,
+          e.pay,         e.view_counts, e.counters};
+      blocks[i] = st[i]->extract_blocks;
+    }
+    rc = LaunchGrouped(ex.data(), blocks.data(), n, stream);
+    if (rc != 0) return rc;
+  }
+  // The sample view: scan of the blocks' counts, then the write.
+  {
+    std::vector<ScanJob<uint32_t>> jobs;
+    for (int i = 0; i < n; ++i) {
+      UniqueStack<K>& u = *st[i];
+      if (!u.view || u.extract_blocks == 0) continue;
+      if (u.view_partial != nullptr) {
+        jobs.push_back(ScanJob<uint32_t>{u.view_off, u.view_off,
+                                         u.extract_blocks, u.view_total,
+                                         u.view_partial});
+      } else {
+        rc = ExclusiveScan<uint32_t>(u.view_off, u.view_off, u.extract_blocks,
+                                     u.view_total, *u.ws, stream);
+        if (rc != 0) return rc;
+      }
+    }
+    if (!measuring && !jobs.empty()) {
+      rc = GroupedExclusiveScan(jobs.data(), static_cast<int>(jobs.size()),
+                                stream);
+      if (rc != 0) return rc;
+    }
+    if (!measuring) {
+      std::vector<ViewWriteArgs<K>> vw(n);
+      for (int i = 0; i < n; ++i) {
+        vw[i] = st[i]->vw;
+        blocks[i] = st[i]->view ? st[i]->view_grid : 0;
+      }
+      rc = LaunchGrouped(vw.data(), blocks.data(), n, stream);
+      if (rc != 0) return rc;
+    }
+  }
+  // The sort. Pass p writes (keys_alt, pay_alt) when p is even; pass 0 reads
+  // the extraction arrays without the merged copies.
+  using Arr = radix::ArraySource<K, uint64_t>;
+  using Sink = radix::ArraySink<K, uint64_t>;
+  int max_passes = 0;
+  for (int i = 0; i < n; ++i) max_passes = std::max(max_passes, st[i]->dp.passes);
+  for (int pass = 0; pass < max_passes; ++pass) {
+    std::vector<radix::RadixHistogramArgs<K, UniqueSource<K>>> h0(n);
+    std::vector<radix::RadixHistogramArgs<K, Arr>> hn(n);
+    std::vector<radix::RadixScatterArgs<K, uint64_t, UniqueSource<K>, Sink>>
+        s0(n);
+    std::vector<radix::RadixScatterArgs<K, uint64_t, Arr, Sink>> sn(n);
+    std::vector<ScanJob<uint32_t>> jobs;
+    for (int i = 0; i < n; ++i) {
+      UniqueStack<K>& u = *st[i];
+      blocks[i] = 0;
+      if (pass >= u.dp.passes || u.M == 0) continue;
+      blocks[i] = u.tiles;
+      const int shift = pass * u.dp.digit;
+      const int pbits =
+          u.key_bits - shift < u.dp.digit ? u.key_bits - shift : u.dp.digit;
+      const uint32_t mask = (1u << pbits) - 1u;
+      const int64_t cells = u.tiles * (int64_t{1} << pbits);
+      const bool even = pass % 2 == 0;
+      const Arr arr{even ? u.keys : u.keys_alt, even ? u.pay : u.pay_alt};
+      const Sink sink{even ? u.keys_alt : u.keys, even ? u.pay_alt : u.pay};
+      const UniqueSource<K> first{u.keys, u.pay};
+      h0[i] = {first, u.M, nullptr, 0, shift, mask, u.tiles, u.hist};
+      hn[i] = {arr, u.M, u.totals, 1, shift, mask, u.tiles, u.hist};
+      s0[i] = {first, sink,  u.M,   nullptr,  0,
+               shift, mask,  pbits, u.tiles,  u.hist,
+               u.totals + pass, false};
+      sn[i] = {arr,   sink,  u.M,   u.totals, 1,
+               shift, mask,  pbits, u.tiles,  u.hist,
+               u.totals + pass, false};
+      if (u.hist_partial != nullptr) {
+        jobs.push_back(ScanJob<uint32_t>{u.hist, u.hist, cells,
+                                         u.totals + pass, u.hist_partial});
+      }
+    }
+    if (!measuring) {
+      rc = pass == 0 ? LaunchGrouped(h0.data(), blocks.data(), n, stream)
+                     : LaunchGrouped(hn.data(), blocks.data(), n, stream);
+      if (rc != 0) return rc;
+      if (!jobs.empty()) {
+        rc = GroupedExclusiveScan(jobs.data(), static_cast<int>(jobs.size()),
+                                  stream);
+        if (rc != 0) return rc;
+      }
+    }
+    for (int i = 0; i < n; ++i) {
+      UniqueStack<K>& u = *st[i];
+      if (pass >= u.dp.passes || u.M == 0 || u.hist_partial != nullptr) {
+        continue;
+      }
+      const int shift = pass * u.dp.digit;
+      const int pbits =
+          u.key_bits - shift < u.dp.digit ? u.key_bits - shift : u.dp.digit;
+      rc = ExclusiveScan<uint32_t>(u.hist, u.hist,
+                                   u.tiles * (int64_t{1} << pbits),
+                                   u.totals + pass, *u.ws, stream);
+      if (rc != 0) return rc;
+    }
+    if (!measuring) {
+      rc = pass == 0 ? LaunchGrouped(s0.data(), blocks.data(), n, stream)
+                     : LaunchGrouped(sn.data(), blocks.data(), n, stream);
+      if (rc != 0) return rc;
+    }
+  }
+  if (measuring) return 0;
+  for (int i = 0; i < n; ++i) {
+    if (st[i]->ws->overflow()) {
+      return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
+    }
+  }
+  // Grouping, the fill plan, the CSR scatter and the padding.
+  {
+    std::vector<GroupUniqueArgs<K>> gu(n);
+    for (int i = 0; i < n; ++i) {
+      gu[i] = st[i]->gu;
+      blocks[i] = CeilDiv(st[i]->M, int64_t{256} * kGroupItems);
+    }
+    rc = LaunchGrouped(gu.data(), blocks.data(), n, stream);
+    if (rc != 0) return rc;
+  }
+  {
+    std::vector<FillPlanArgs> fill(n);
+    for (int i = 0; i < n; ++i) {
+      fill[i] = st[i]->fill;
+      blocks[i] = 1;
+    }
+    rc = LaunchGrouped(fill.data(), blocks.data(), n, stream);
+    if (rc != 0) return rc;
+  }
+  {
+    std::vector<ScatterUniqueArgs<K>> sc(n);
+    for (int i = 0; i < n; ++i) {
+      sc[i] = st[i]->sc;
+      blocks[i] = CeilDiv(st[i]->M, 256);
+    }
+    rc = LaunchGrouped(sc.data(), blocks.data(), n, stream);
+    if (rc != 0) return rc;
+  }
+  std::vector<WritePaddingArgs> pad(n);
+  for (int i = 0; i < n; ++i) {
+    pad[i] = st[i]->pad;
+    blocks[i] = st[i]->pad_blocks;
+  }
+  return LaunchGrouped(pad.data(), blocks.data(), n, stream);
+}
+
+template <typename K>
+int RunUniquePipeline(const scemb_feature_t* feats, int nf,
+                      const scemb_preprocess_options_t* o,
+                      const scemb_preprocess_output_t* out, const Plan& pl,
+                      Arena& ws, hipStream_t stream) {
+  UniqueStack<K> u;
+  int rc = PrepareUnique<K>(feats, nf, o, out, pl, ws, stream, &u);
+  if (rc != 0) return rc;
+  UniqueStack<K>* one = &u;
+  return u.weighted ? EnqueueUnique<K, false>(&one, 1, stream)
+                    : EnqueueUnique<K, true>(&one, 1, stream);
 }
 
 // The most ids of one row over the stack's features: a dense feature's

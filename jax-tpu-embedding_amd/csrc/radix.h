@@ -78,16 +78,17 @@ __device__ __forceinline__ int64_t ActiveCount(int64_t n,
 
 // hist[d * tiles + tile] = elements of digit d in the tile. The positions
 // the source declines go to src.Rejected after all loads are issued.
+// The body of work-group `tile` (RadixHistogramK and grouped launches).
 template <typename K, typename Src>
-__global__ __launch_bounds__(kSortBlock) void RadixHistogramK(
-    Src src, int64_t n, const uint32_t* n_dev, int n_dev_words, int shift,
-    uint32_t mask, int64_t tiles, uint32_t* hist) {
+__device__ __forceinline__ void RadixHistogramBody(
+    uint32_t tile_index, Src src, int64_t n, const uint32_t* n_dev,
+    int n_dev_words, int shift, uint32_t mask, int64_t tiles, uint32_t* hist) {
   __shared__ uint32_t h[kMaxRadix];
   const int radix = static_cast<int>(mask) + 1;
   for (int d = threadIdx.x; d < radix; d += kSortBlock) h[d] = 0;
   __syncthreads();
   const int64_t m = ActiveCount(n, n_dev, n_dev_words);
-  const int64_t tile = blockIdx.x;
+  const int64_t tile = tile_index;
   const int64_t base = tile * kSortTile;
   const int digit_bits = __popc(mask);
   const uint64_t lt = LaneMaskLt();
@@ -127,6 +128,33 @@ __global__ __launch_bounds__(kSortBlock) void RadixHistogramK(
   }
 }
 
+template <typename K, typename Src>
+__global__ __launch_bounds__(kSortBlock) void RadixHistogramK(
+    Src src, int64_t n, const uint32_t* n_dev, int n_dev_words, int shift,
+    uint32_t mask, int64_t tiles, uint32_t* hist) {
+  RadixHistogramBody<K, Src>(blockIdx.x, src, n, n_dev, n_dev_words, shift,
+                             mask, tiles, hist);
+}
+
+// RadixHistogramK's arguments for a grouped launch (common.h).
+template <typename K, typename Src>
+struct RadixHistogramArgs {
+  static constexpr int kBlock = kSortBlock;
+  Src src;
+  int64_t n;
+  const uint32_t* n_dev;
+  int n_dev_words;
+  int shift;
+  uint32_t mask;
+  int64_t tiles;
+  uint32_t* hist;
+  __device__ static void Run(const RadixHistogramArgs& a, uint32_t blk,
+                             uint32_t) {
+    RadixHistogramBody<K, Src>(blk, a.src, a.n, a.n_dev, a.n_dev_words,
+                               a.shift, a.mask, a.tiles, a.hist);
+  }
+};
+
 // Stable scatter of one tile (kSortTile consecutive source positions) into
 // the digit buckets; `offsets` is the scanned histogram matrix. With
 // `fill_tail`, the block also hands the output positions of its tile range
@@ -143,10 +171,10 @@ constexpr int kWaveSpan = kSortTile / kSortWaves;   // 512 positions
 constexpr int kWaveChunks = kWaveSpan / kWave;      // 8 chunks of 64
 
 template <typename K, typename V, typename Src, typename Sink>
-__global__ __launch_bounds__(kSortBlock) void RadixScatterK(
-    Src src, Sink sink, int64_t n, const uint32_t* n_dev, int n_dev_words,
-    int shift, uint32_t mask, int digit_bits, int64_t tiles, const uint32_t* offsets,
-    const uint32_t* total, bool fill_tail) {
+__device__ __forceinline__ void RadixScatterBody(
+    uint32_t tile_index, Src src, Sink sink, int64_t n, const uint32_t* n_dev,
+    int n_dev_words, int shift, uint32_t mask, int digit_bits, int64_t tiles,
+    const uint32_t* offsets, const uint32_t* total, bool fill_tail) {
   __shared__ uint32_t wave_cnt[kSortWaves][kMaxRadix];
   __shared__ uint32_t global_off[kMaxRadix];  // bucket start (output)
   __shared__ uint32_t tile_off[kMaxRadix];    // bucket start (tile)
@@ -157,7 +185,7 @@ __global__ __launch_bounds__(kSortBlock) void RadixScatterK(
   const int wave = t / kWave;
   const int lane = t % kWave;
   const int radix = static_cast<int>(mask) + 1;
-  const int64_t blk = blockIdx.x;
+  const int64_t blk = tile_index;
   const int64_t base = blk * kSortTile;
   if (fill_tail) {
     const int64_t taken = static_cast<int64_t>(*total);
@@ -262,6 +290,41 @@ __global__ __launch_bounds__(kSortBlock) void RadixScatterK(
                s_vals[j]);
   }
 }
+
+template <typename K, typename V, typename Src, typename Sink>
+__global__ __launch_bounds__(kSortBlock) void RadixScatterK(
+    Src src, Sink sink, int64_t n, const uint32_t* n_dev, int n_dev_words,
+    int shift, uint32_t mask, int digit_bits, int64_t tiles, const uint32_t* offsets,
+    const uint32_t* total, bool fill_tail) {
+  RadixScatterBody<K, V, Src, Sink>(blockIdx.x, src, sink, n, n_dev,
+                                    n_dev_words, shift, mask, digit_bits,
+                                    tiles, offsets, total, fill_tail);
+}
+
+// RadixScatterK's arguments for a grouped launch (common.h).
+template <typename K, typename V, typename Src, typename Sink>
+struct RadixScatterArgs {
+  static constexpr int kBlock = kSortBlock;
+  Src src;
+  Sink sink;
+  int64_t n;
+  const uint32_t* n_dev;
+  int n_dev_words;
+  int shift;
+  uint32_t mask;
+  int digit_bits;
+  int64_t tiles;
+  const uint32_t* offsets;
+  const uint32_t* total;
+  bool fill_tail;
+  __device__ static void Run(const RadixScatterArgs& a, uint32_t blk,
+                             uint32_t) {
+    RadixScatterBody<K, V, Src, Sink>(blk, a.src, a.sink, a.n, a.n_dev,
+                                      a.n_dev_words, a.shift, a.mask,
+                                      a.digit_bits, a.tiles, a.offsets,
+                                      a.total, a.fill_tail);
+  }
+};
 
 // --- Two-stage sort: one pass on the high digit, then a sort per bucket ----
 //

@@ -10,6 +10,8 @@
 // that the writes of a tile come out bucket by bucket (radix.h).
 #include "scan.h"
 
+#include <vector>
+
 #include "radix.h"
 
 #include "../../include/scemb.h"
@@ -22,11 +24,10 @@ constexpr int kScanItems = 8;
 constexpr int kScanTile = kScanBlock * kScanItems;
 
 template <typename T>
-__global__ __launch_bounds__(kScanBlock) void ScanReduceTiles(const T* in,
-                                                               int64_t n,
-                                                               T* partial) {
+__device__ __forceinline__ void ScanReduceTilesBody(uint32_t blk, const T* in,
+                                                    int64_t n, T* partial) {
   __shared__ T smem[kScanBlock / kWave + 1];
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile +
+  const int64_t base = static_cast<int64_t>(blk) * kScanTile +
                        static_cast<int64_t>(threadIdx.x) * kScanItems;
   T s = 0;
 #pragma unroll
@@ -36,7 +37,14 @@ __global__ __launch_bounds__(kScanBlock) void ScanReduceTiles(const T* in,
   }
   T total;
   BlockExclusiveScan<T, kScanBlock>(s, smem, &total);
-  if (threadIdx.x == 0) partial[blockIdx.x] = total;
+  if (threadIdx.x == 0) partial[blk] = total;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kScanBlock) void ScanReduceTiles(const T* in,
+                                                               int64_t n,
+                                                               T* partial) {
+  ScanReduceTilesBody<T>(blockIdx.x, in, n, partial);
 }
 
 template <typename T>
@@ -75,17 +83,20 @@ __global__ __launch_bounds__(kScanBlock) void ScanTiles(const T* in, T* out,
 // before it, added up by the block itself (integer sums: any order gives the
 // same value), so that no separate scan of the partial sums is launched.
 template <typename T>
-__global__ __launch_bounds__(kScanBlock) void ScanTilesPrefix(
-    const T* in, T* out, int64_t n, const T* partial, T* total_out) {
+__device__ __forceinline__ void ScanTilesPrefixBody(uint32_t blk,
+                                                    uint32_t nblk, const T* in,
+                                                    T* out, int64_t n,
+                                                    const T* partial,
+                                                    T* total_out) {
   __shared__ T smem[kScanBlock / kWave + 1];
   T pre = 0;
-  for (int64_t j = threadIdx.x; j < static_cast<int64_t>(blockIdx.x);
+  for (int64_t j = threadIdx.x; j < static_cast<int64_t>(blk);
        j += kScanBlock) {
     pre += partial[j];
   }
   T off;
   BlockExclusiveScan<T, kScanBlock>(pre, smem, &off);
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile +
+  const int64_t base = static_cast<int64_t>(blk) * kScanTile +
                        static_cast<int64_t>(threadIdx.x) * kScanItems;
   T v[kScanItems];
   T s = 0;
@@ -103,11 +114,43 @@ __global__ __launch_bounds__(kScanBlock) void ScanTilesPrefix(
     if (i < n) out[i] = run;
     run += v[k];
   }
-  if (total_out != nullptr && threadIdx.x == 0 &&
-      blockIdx.x == gridDim.x - 1) {
+  if (total_out != nullptr && threadIdx.x == 0 && blk == nblk - 1) {
     total_out[0] = off + total;
   }
 }
+
+template <typename T>
+__global__ __launch_bounds__(kScanBlock) void ScanTilesPrefix(
+    const T* in, T* out, int64_t n, const T* partial, T* total_out) {
+  ScanTilesPrefixBody<T>(blockIdx.x, gridDim.x, in, out, n, partial,
+                         total_out);
+}
+
+// The two launches of a scan as grouped arguments (common.h).
+template <typename T>
+struct ScanReduceArgs {
+  static constexpr int kBlock = kScanBlock;
+  const T* in;
+  int64_t n;
+  T* partial;
+  __device__ static void Run(const ScanReduceArgs& a, uint32_t blk, uint32_t) {
+    ScanReduceTilesBody<T>(blk, a.in, a.n, a.partial);
+  }
+};
+
+template <typename T>
+struct ScanPrefixArgs {
+  static constexpr int kBlock = kScanBlock;
+  const T* in;
+  T* out;
+  int64_t n;
+  const T* partial;
+  T* total;
+  __device__ static void Run(const ScanPrefixArgs& a, uint32_t blk,
+                             uint32_t nblk) {
+    ScanTilesPrefixBody<T>(blk, nblk, a.in, a.out, a.n, a.partial, a.total);
+  }
+};
 
 // Up to this many tiles, each block of the second launch adds up the
 // partial sums before it (at most this many loads spread over 256 threads).
@@ -163,6 +206,35 @@ int ExclusiveScan(const T* in, T* out, int64_t n, T* total, Arena& ws,
   }
   return 0;
 }
+
+int64_t GroupedScanPartialWords(int64_t n) {
+  const int64_t tiles = std::max<int64_t>(1, CeilDiv(n, kScanTile));
+  return tiles <= kPrefixTilesMax ? tiles : 0;
+}
+
+template <typename T>
+int GroupedExclusiveScan(const ScanJob<T>* jobs, int n, hipStream_t stream) {
+  std::vector<ScanReduceArgs<T>> red(n);
+  std::vector<ScanPrefixArgs<T>> pre(n);
+  std::vector<int64_t> blocks(n);
+  for (int i = 0; i < n; ++i) {
+    const ScanJob<T>& j = jobs[i];
+    // Nothing to scan writes a zero total (one block of no elements).
+    blocks[i] = j.n > 0 ? CeilDiv(j.n, kScanTile) : (j.total != nullptr);
+    if (blocks[i] > kPrefixTilesMax) {
+      return Fail(SCEMB_ERR_INVALID_ARGUMENT, "grouped scan: too many tiles");
+    }
+    red[i] = ScanReduceArgs<T>{j.in, std::max<int64_t>(j.n, 0), j.partial};
+    pre[i] = ScanPrefixArgs<T>{j.in, j.out, std::max<int64_t>(j.n, 0),
+                               j.partial, j.total};
+  }
+  int st = LaunchGrouped(red.data(), blocks.data(), n, stream);
+  if (st != 0) return st;
+  return LaunchGrouped(pre.data(), blocks.data(), n, stream);
+}
+
+template int GroupedExclusiveScan<uint32_t>(const ScanJob<uint32_t>*, int,
+                                            hipStream_t);
 
 template int ExclusiveScan<uint32_t>(const uint32_t*, uint32_t*, int64_t,
                                      uint32_t*, Arena&, hipStream_t);

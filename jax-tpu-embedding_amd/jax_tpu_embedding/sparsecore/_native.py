@@ -73,6 +73,7 @@ EXPORTED_SYMBOLS = (
     "scemb_preprocess_stacked_table",
     "scemb_check_row_splits",
     "scemb_stage_row_splits",
+    "scemb_stage_row_splits_batch",
     "scemb_compute_theoretical_max_coo_buffer_size",
     "scemb_compute_coo_buffer_size_per_device",
     "scemb_compute_row_pointers_size_per_device",
@@ -360,6 +361,9 @@ def load_library() -> ctypes.CDLL:
     lib.scemb_stage_row_splits.restype = ctypes.c_int
     lib.scemb_stage_row_splits.argtypes = [vp, i64, i64, vp,
                                            ctypes.POINTER(ctypes.c_int64)]
+    lib.scemb_stage_row_splits_batch.restype = ctypes.c_int
+    lib.scemb_stage_row_splits_batch.argtypes = [
+        i32, vp, vp, vp, vp, vp, ctypes.POINTER(ctypes.c_int32)]
     lib.scemb_compute_theoretical_max_coo_buffer_size.restype = i64
     lib.scemb_compute_theoretical_max_coo_buffer_size.argtypes = [i32, i32,
                                                                   i32, i32]
@@ -685,18 +689,30 @@ class HostUploads:
     host = t.empty(self._nbytes, dtype=t.uint8, pin_memory=True)
     staged = host.numpy()
     base = host.data_ptr()
-    lib = load_library()
-    longest = ctypes.c_int64(0)
+    splits = []
     for arr, h in self._items:
       if h.nnz is None:
         staged[h.offset:h.offset + arr.nbytes] = arr.view(np.uint8)
-        continue
-      if lib.scemb_stage_row_splits(arr.ctypes.data, arr.size - 1, h.nnz,
-                                    base + h.offset, ctypes.byref(longest)):
+      else:
+        splits.append((arr, h))
+    if splits:
+      # Every feature's row splits checked and staged by one library call
+      # (its rows spread over a few host threads).
+      n = len(splits)
+      src = np.fromiter((a.ctypes.data for a, _ in splits), np.uint64, n)
+      rows = np.fromiter((a.size - 1 for a, _ in splits), np.int64, n)
+      nnz = np.fromiter((h.nnz for _, h in splits), np.int64, n)
+      dst = np.fromiter((base + h.offset for _, h in splits), np.uint64, n)
+      longest = np.zeros(n, np.int64)
+      bad = ctypes.c_int32(-1)
+      if load_library().scemb_stage_row_splits_batch(
+          n, src.ctypes.data, rows.ctypes.data, nnz.ctypes.data,
+          dst.ctypes.data, longest.ctypes.data, ctypes.byref(bad)):
         self._items = []
         self._nbytes = 0
         raise ValueError(ROW_SPLITS_MESSAGE)
-      h.max_row_length = int(longest.value)
+      for (_, h), most in zip(splits, longest.tolist()):
+        h.max_row_length = most
     dst = t.empty(self._nbytes, dtype=t.uint8, device=dev)
     dst.copy_(host, non_blocking=True)
     for _, h in self._items:

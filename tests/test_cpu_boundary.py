@@ -193,6 +193,59 @@ def test_stage_row_splits_copies_and_checks():
       _native.SCEMB_ERR_INVALID_ARGUMENT
 
 
+def _stage_batch(splits, nnz=None):
+  """scemb_stage_row_splits_batch over `splits`: (rc, first_bad, copies,
+  longest rows)."""
+  lib = _native.load_library()
+  n = len(splits)
+  dsts = [np.full(s.size, -7, np.int64) for s in splits]
+  src = np.array([s.ctypes.data for s in splits], np.uint64)
+  dst = np.array([d.ctypes.data for d in dsts], np.uint64)
+  rows = np.array([s.size - 1 for s in splits], np.int64)
+  nnz = np.array([int(s[-1]) for s in splits] if nnz is None else nnz,
+                 np.int64)
+  longest = np.full(n, -1, np.int64)
+  bad = ctypes.c_int32(-2)
+  rc = lib.scemb_stage_row_splits_batch(n, src.ctypes.data, rows.ctypes.data,
+                                        nnz.ctypes.data, dst.ctypes.data,
+                                        longest.ctypes.data, ctypes.byref(bad))
+  return rc, bad.value, dsts, longest
+
+
+def test_stage_row_splits_batch_matches_one_at_a_time():
+  """The batched staging copies and checks every feature as the one-feature
+  call does, with features long enough to be split over threads (the
+  longest row placed in a late chunk), and names the first bad feature."""
+  rng = np.random.default_rng(1)
+  sizes = (0, 1, 7, 1000, 16385, 32768, 32769, 200_003, 70_000, 3)
+  splits = []
+  for rows in sizes:
+    s = np.zeros(rows + 1, np.int64)
+    s[1:] = np.cumsum(rng.integers(0, 9, size=rows))
+    if rows > 100_000:
+      s[rows - 5:] += 1000  # the longest row, in the last chunk
+    splits.append(s)
+  rc, first_bad, dsts, longest = _stage_batch(splits)
+  assert rc == 0 and first_bad == -1
+  for s, d, most in zip(splits, dsts, longest.tolist()):
+    np.testing.assert_array_equal(d, s)
+    assert most == (int(np.diff(s).max()) if s.size > 1 else 0)
+  assert longest[sizes.index(200_003)] >= 1000
+  # A decrease inside a middle chunk of a long feature; a wrong end; a
+  # non-zero start.
+  dec = splits[7].copy()
+  dec[100_000] = dec[99_999] - 1
+  rc, first_bad, _, _ = _stage_batch([splits[3], dec, splits[8]])
+  assert rc == _native.SCEMB_ERR_INVALID_ARGUMENT and first_bad == 1
+  rc, first_bad, _, _ = _stage_batch(
+      [splits[3], splits[4]], nnz=[int(splits[3][-1]), int(splits[4][-1]) + 1])
+  assert rc == _native.SCEMB_ERR_INVALID_ARGUMENT and first_bad == 1
+  start = splits[2].copy() + 1
+  rc, first_bad, _, _ = _stage_batch([start])
+  assert rc == _native.SCEMB_ERR_INVALID_ARGUMENT and first_bad == 0
+  assert _stage_batch([])[0] == 0
+
+
 def test_preprocess_minibatching_options():
   """The bucket passes size 64 buckets per (SC, partition); a bad pass or a
   split of 64 bits is refused; the sample view adds its temporaries."""
