@@ -562,6 +562,26 @@ int scemb_preprocess_stacked_table(const scemb_feature_t* features,
                                    void* workspace, size_t workspace_bytes,
                                    void* stream);
 
+/* Several stacked tables of one batch in one call, as the reference's
+ * PreprocessSparseDenseMatmulInput takes them all (input_preprocessing.cc:
+ * 827-868 extracts, sorts and groups every table, then fills every table's
+ * buffers). Job i is scemb_preprocess_stacked_table's arguments for one
+ * stack, with its own workspace of scemb_preprocess_workspace_size() bytes.
+ * Each stage of the stacks that merge duplicates at extraction is one launch
+ * for all of them (those of one key width and weighting); the others run one
+ * after another. The outputs are those of one call per job. */
+typedef struct scemb_preprocess_job {
+  const scemb_feature_t* features;
+  int32_t num_features;
+  const scemb_preprocess_options_t* options;
+  const scemb_preprocess_output_t* outputs;
+  void* workspace;
+  size_t workspace_bytes;
+} scemb_preprocess_job_t;
+
+int scemb_preprocess_stacked_tables(const scemb_preprocess_job_t* jobs,
+                                    int32_t num_jobs, void* stream);
+
 /* ---- Launch timing (no counterpart in the reference) -------------------
  * For benchmarks: while enabled, the library records HIP events on the launch
  * stream around its main kernels ("fwd_reduce", "fwd_finish", "bwd_reduce",

@@ -38,6 +38,7 @@
 //                     a scatter of the kept runs.
 #include <algorithm>
 #include <cstring>
+#include <memory>
 #include <vector>
 
 #include "../../include/scemb.h"
@@ -3280,6 +3281,25 @@ int64_t MaxRowLength(const scemb_feature_t* feats, int nf,
   return most;
 }
 
+// Grouping at extraction needs every (row, column) pair to come from one
+// input row (disjoint sample rows) and keeps every entry (no id dropping, no
+// minibatching). With the sample view it also needs a static buffer that
+// holds any input within the limits: the view is written before the fill
+// plan and so cannot leave out entries the buffer has no room for. Its
+// duplicate scan costs the square of the row length, so rows longer than the
+// LDS staging go the other way.
+bool GroupsAtExtraction(const scemb_feature_t* feats, int nf,
+                        const scemb_preprocess_options_t* o, const Plan& pl,
+                        const std::vector<std::vector<int64_t>>& cache) {
+  return (o->flags & SCEMB_PREPROCESS_GROUP_AFTER_SORT) == 0 &&
+         !o->enable_minibatching && !o->allow_id_dropping &&
+         pl.rows_disjoint &&
+         (!o->build_sample_view ||
+          pl.coo_size >= RoundUp(o->max_ids_per_partition, kAlign) *
+                             static_cast<int64_t>(pl.S) * pl.NS) &&
+         MaxRowLength(feats, nf, cache) <= kDedupMaxRow;
+}
+
 int Preprocess(const scemb_feature_t* feats, int nf,
                const scemb_preprocess_options_t* o,
                const scemb_preprocess_output_t* out, Arena& ws,
@@ -3288,21 +3308,7 @@ int Preprocess(const scemb_feature_t* feats, int nf,
   std::vector<std::vector<int64_t>> cache;
   int st = MakePlan(feats, nf, o, &pl, &cache);
   if (st != 0) return st;
-  // Grouping at extraction needs every (row, column) pair to come from one
-  // input row (disjoint sample rows) and keeps every entry (no id dropping,
-  // no minibatching). With the sample view it also needs a static buffer
-  // that holds any input within the limits: the view is written before the
-  // fill plan and so cannot leave out entries the buffer has no room for.
-  // Its duplicate scan costs the square of the row length, so rows longer
-  // than the LDS staging go the other way.
-  const bool at_extraction =
-      (o->flags & SCEMB_PREPROCESS_GROUP_AFTER_SORT) == 0 &&
-      !o->enable_minibatching && !o->allow_id_dropping && pl.rows_disjoint &&
-      (!o->build_sample_view ||
-       pl.coo_size >= RoundUp(o->max_ids_per_partition, kAlign) *
-                          static_cast<int64_t>(pl.S) * pl.NS) &&
-      MaxRowLength(feats, nf, cache) <= kDedupMaxRow;
-  if (at_extraction) {
+  if (GroupsAtExtraction(feats, nf, o, pl, cache)) {
     return pl.wide_keys
                ? RunUniquePipeline<uint64_t>(feats, nf, o, out, pl, ws, stream)
                : RunUniquePipeline<uint32_t>(feats, nf, o, out, pl, ws, stream);
@@ -3311,6 +3317,69 @@ int Preprocess(const scemb_feature_t* feats, int nf,
     return RunPipeline<uint64_t>(feats, nf, o, out, pl, ws, stream);
   }
   return RunPipeline<uint32_t>(feats, nf, o, out, pl, ws, stream);
+}
+
+// The stacks of one call: those grouping at extraction are prepared in job
+// order (each one's set-up launch), then their stages are enqueued together,
+// one grouped launch per stage for the stacks of one key width and weighting;
+// the other stacks run whole, first.
+template <typename K>
+struct UniqueClasses {
+  std::vector<std::unique_ptr<UniqueStack<K>>> weighted, unit;
+  int Add(const scemb_preprocess_job_t& j, const Plan& pl, Arena& ws,
+          hipStream_t stream) {
+    auto u = std::make_unique<UniqueStack<K>>();
+    const int rc = PrepareUnique<K>(j.features, j.num_features, j.options,
+                                    j.outputs, pl, ws, stream, u.get());
+    if (rc != 0) return rc;
+    (u->weighted ? weighted : unit).push_back(std::move(u));
+    return 0;
+  }
+  int Enqueue(hipStream_t stream) {
+    std::vector<UniqueStack<K>*> w, h;
+    for (auto& u : weighted) w.push_back(u.get());
+    for (auto& u : unit) h.push_back(u.get());
+    int rc = w.empty() ? 0
+                       : EnqueueUnique<K, false>(w.data(),
+                                                 static_cast<int>(w.size()),
+                                                 stream);
+    if (rc != 0 || h.empty()) return rc;
+    return EnqueueUnique<K, true>(h.data(), static_cast<int>(h.size()), stream);
+  }
+};
+
+int PreprocessJobs(const scemb_preprocess_job_t* jobs, int n,
+                   hipStream_t stream) {
+  if (n < 0 || (n > 0 && jobs == nullptr)) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "null jobs");
+  }
+  std::vector<Arena> arenas;
+  arenas.reserve(n);  // the prepared stacks keep pointers to their arenas
+  UniqueClasses<uint32_t> narrow;
+  UniqueClasses<uint64_t> wide;
+  for (int i = 0; i < n; ++i) {
+    const scemb_preprocess_job_t& j = jobs[i];
+    if (j.workspace == nullptr) return Fail(SCEMB_ERR_WORKSPACE, "no workspace");
+    arenas.emplace_back(j.workspace, j.workspace_bytes);
+    Arena& ws = arenas.back();
+    Plan pl;
+    std::vector<std::vector<int64_t>> cache;
+    int rc = MakePlan(j.features, j.num_features, j.options, &pl, &cache);
+    if (rc != 0) return rc;
+    if (GroupsAtExtraction(j.features, j.num_features, j.options, pl, cache)) {
+      rc = pl.wide_keys ? wide.Add(j, pl, ws, stream)
+                        : narrow.Add(j, pl, ws, stream);
+    } else if (pl.wide_keys) {
+      rc = RunPipeline<uint64_t>(j.features, j.num_features, j.options,
+                                 j.outputs, pl, ws, stream);
+    } else {
+      rc = RunPipeline<uint32_t>(j.features, j.num_features, j.options,
+                                 j.outputs, pl, ws, stream);
+    }
+    if (rc != 0) return rc;
+  }
+  const int rc = narrow.Enqueue(stream);
+  return rc != 0 ? rc : wide.Enqueue(stream);
 }
 
 }  // namespace
@@ -3342,6 +3411,15 @@ size_t scemb_preprocess_workspace_size(const scemb_feature_t* features,
     return 0;
   }
   return ws.used() + 256;
+}
+
+int scemb_preprocess_stacked_tables(const scemb_preprocess_job_t* jobs,
+                                    int32_t num_jobs, void* stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int prof = ProfileBegin("preprocess_call", s);
+  const int rc = PreprocessJobs(jobs, num_jobs, s);
+  ProfileEnd(prof, s);
+  return rc;
 }
 
 int scemb_preprocess_stacked_table(const scemb_feature_t* features,

@@ -71,6 +71,7 @@ EXPORTED_SYMBOLS = (
     "scemb_preprocess_stats_counters_offset",
     "scemb_preprocess_workspace_size",
     "scemb_preprocess_stacked_table",
+    "scemb_preprocess_stacked_tables",
     "scemb_check_row_splits",
     "scemb_stage_row_splits",
     "scemb_stage_row_splits_batch",
@@ -218,6 +219,10 @@ class FeatureArray:
   def __len__(self):
     return self._n
 
+  @property
+  def address(self) -> int:
+    return ctypes.addressof(self._buffer)
+
 
 def feature_structs(rows) -> FeatureArray:
   """scemb_feature_t[len(rows)] from (ids, weights, row_splits,
@@ -261,6 +266,20 @@ class PreprocessOutput(ctypes.Structure):
       ("stats", ctypes.c_void_p),
       ("view_keys", ctypes.c_void_p),
       ("view_entries", ctypes.c_void_p),
+  ]
+
+
+class PreprocessJob(ctypes.Structure):
+  """scemb_preprocess_job_t: one stack of scemb_preprocess_stacked_tables
+  (addresses of its features, options and outputs, which the caller keeps
+  alive through the call)."""
+  _fields_ = [
+      ("features", ctypes.c_void_p),
+      ("num_features", ctypes.c_int32),
+      ("options", ctypes.c_void_p),
+      ("outputs", ctypes.c_void_p),
+      ("workspace", ctypes.c_void_p),
+      ("workspace_bytes", ctypes.c_size_t),
   ]
 
 
@@ -355,6 +374,9 @@ def load_library() -> ctypes.CDLL:
     lib.scemb_preprocess_stacked_table.argtypes = [
         ctypes.POINTER(Feature), i32, opts_p, ctypes.POINTER(PreprocessOutput),
         vp, sz, vp]
+    lib.scemb_preprocess_stacked_tables.restype = ctypes.c_int
+    lib.scemb_preprocess_stacked_tables.argtypes = [
+        ctypes.POINTER(PreprocessJob), i32, vp]
     lib.scemb_check_row_splits.restype = ctypes.c_int
     lib.scemb_check_row_splits.argtypes = [vp, i64, i64,
                                            ctypes.POINTER(ctypes.c_int64)]

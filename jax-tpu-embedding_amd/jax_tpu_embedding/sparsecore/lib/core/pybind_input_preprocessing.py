@@ -332,22 +332,69 @@ def _resolve_feature(f: _DeviceFeature) -> _DeviceFeature:
   return f
 
 
-def _preprocess_stack(feats, metas, *, local_device_count,
-                      global_device_count, num_sc_per_device,
-                      allow_id_dropping, has_weights, build_view=False,
-                      enable_minibatching=False, minibatching_pass=0,
-                      minibatching_split=0, outputs=None, view_outputs=None,
-                      stats_out=None, stream=None):
+class _StackCall:
+  """One stack's library call, prepared by _prepare_stack: its ctypes
+  arguments (held until the call) and the workspace it needs."""
+  __slots__ = ("structs", "num_features", "opts", "out", "need")
+
+  def __init__(self, structs, num_features, opts, out, need):
+    self.structs, self.num_features = structs, num_features
+    self.opts, self.out, self.need = opts, out, need
+
+
+def _preprocess_stack(feats, metas, *, stream=None, **kwargs):
   """Enqueues one stacked table (one minibatching pass of it with
-  `enable_minibatching`); returns (rp, eid, sid, gains, stats on the
-  device, (L, S, NS, counters offset), view) where view is the
-  (keys, entries) pair of the CSR's sample view when `build_view`, else
-  None. `outputs` / `view_outputs`: the (rp, eid, sid, gains) / view of an
-  earlier pass to write into. `stats_out`: an int32 device tensor of
-  _stats_words(...) slots to hold the stats (else one is allocated).
-  `stream` (may be None): the stream to enqueue on instead of the current
-  one; the outputs are still allocated on the current stream, which the
-  caller makes wait for `stream` before it uses them."""
+  `enable_minibatching`); returns what _prepare_stack does. `stream` (may be
+  None): the stream to enqueue on instead of the current one; the outputs
+  are still allocated on the current stream, which the caller makes wait for
+  `stream` before it uses them."""
+  call, result = _prepare_stack(feats, metas, **kwargs)
+  lib = _native.load_library()
+  # The workspace belongs to the stream the work is enqueued on.
+  ws = _native.WORKSPACE.get(call.need, stream)
+  _native.check(lib.scemb_preprocess_stacked_table(
+      call.structs, call.num_features, ctypes.byref(call.opts),
+      ctypes.byref(call.out), _native.ptr(ws), ws.numel(),
+      stream.cuda_stream if stream is not None else _native.stream_handle()))
+  return result
+
+
+def _preprocess_stacks(calls):
+  """Enqueues prepared stacks with one library call on the current stream
+  (scemb_preprocess_stacked_tables: one launch per stage for the stacks that
+  merge duplicates at extraction), each with its slice of one workspace."""
+  if not calls:
+    return
+  sizes = [-(-c.need // 256) * 256 for c in calls]
+  ws = _native.WORKSPACE.get(sum(sizes))
+  base = _native.ptr(ws)
+  jobs = (_native.PreprocessJob * len(calls))()
+  pos = 0
+  for job, c, size in zip(jobs, calls, sizes):
+    job.features = c.structs.address
+    job.num_features = c.num_features
+    job.options = ctypes.addressof(c.opts)
+    job.outputs = ctypes.addressof(c.out)
+    job.workspace = base + pos
+    job.workspace_bytes = size
+    pos += size
+  _native.check(_native.load_library().scemb_preprocess_stacked_tables(
+      jobs, len(calls), _native.stream_handle()))
+
+
+def _prepare_stack(feats, metas, *, local_device_count, global_device_count,
+                   num_sc_per_device, allow_id_dropping, has_weights,
+                   build_view=False, enable_minibatching=False,
+                   minibatching_pass=0, minibatching_split=0, outputs=None,
+                   view_outputs=None, stats_out=None):
+  """The library call of one stacked table (one minibatching pass of it with
+  `enable_minibatching`), not yet made, and its outputs: (call, (rp, eid,
+  sid, gains, stats on the device, (L, S, NS, counters offset), view)) where
+  view is the (keys, entries) pair of the CSR's sample view when
+  `build_view`, else None. `outputs` / `view_outputs`: the (rp, eid, sid,
+  gains) / view of an earlier pass to write into. `stats_out`: an int32
+  device tensor of _stats_words(...) slots to hold the stats (else one is
+  allocated). The outputs are allocated on the current stream."""
   t = _native.require_gpu()
   lib = _native.load_library()
   dev = _native.device()
@@ -414,15 +461,10 @@ def _preprocess_stack(feats, metas, *, local_device_count,
       _native.ptr(rp), _native.ptr(eid), _native.ptr(sid), _native.ptr(gains),
       _native.ptr(stats), None if view is None else _native.ptr(view[0]),
       None if view is None else _native.ptr(view[1]))
-  # The workspace belongs to the stream the work is enqueued on.
-  ws = _native.WORKSPACE.get(need, stream)
-  _native.check(lib.scemb_preprocess_stacked_table(
-      structs, len(feats), ctypes.byref(opts), ctypes.byref(out),
-      _native.ptr(ws), ws.numel(),
-      stream.cuda_stream if stream is not None else _native.stream_handle()))
   off = int(lib.scemb_preprocess_stats_counters_offset(ctypes.byref(opts)))
   # The stats stay on the device until every stack has been enqueued.
-  return rp, eid, sid, gains, stats, (L, S, ns, off), view
+  return (_StackCall(structs, len(feats), opts, out, need),
+          (rp, eid, sid, gains, stats, (L, S, ns, off), view))
 
 
 def _stats_words(local_device_count, global_device_count, num_sc_per_device):
@@ -643,17 +685,11 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
   t = _native.torch()
   pending.stats_buffer = t.empty(words * len(stacks), dtype=t.int32,
                                  device=_native.device())
-  # Stacks are independent: with several, each is enqueued on one of a few
-  # side streams, forked from and joined back into the current stream, so
-  # that their chains of small kernels overlap on the device.
-  sides = _native.side_streams(min(len(stacks), _native.NUM_SIDE_STREAMS)
-                               if len(stacks) > 1 else 0)
-  if sides:
-    main = t.cuda.current_stream()
-    fork = t.cuda.Event()
-    fork.record(main)
-    for s in sides:
-      s.wait_event(fork)
+  # Every stack goes to the library in one call on the current stream, which
+  # runs each stage of the stacks that merge duplicates at extraction as one
+  # launch for all of them (the kernels of one stage then fill the device
+  # together).
+  calls = []
   for i, (name, metas) in enumerate(stacks.items()):
     feats = [_resolve_feature(f) for f in stack_feats[name]]
     kwargs = dict(feats=feats, metas=metas,
@@ -663,10 +699,11 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
                   allow_id_dropping=allow_id_dropping,
                   has_weights=feature_weights is not None,
                   enable_minibatching=enable_minibatching)
-    rp, eid, sid, gains, stats_dev, (L, S, ns, off), view = _preprocess_stack(
-        **kwargs, build_view=build_view,
-        stats_out=pending.stats_buffer[i * words:(i + 1) * words],
-        stream=sides[i % len(sides)] if sides else None)
+    call, (rp, eid, sid, gains, stats_dev, (L, S, ns, off),
+           view) = _prepare_stack(
+               **kwargs, build_view=build_view,
+               stats_out=pending.stats_buffer[i * words:(i + 1) * words])
+    calls.append(call)
     if view is not None:
       sample_views[name] = view
     pending.append((name, stats_dev, L, S, ns, off, feats))
@@ -676,10 +713,7 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
       rp, eid, sid, gains = (rp.reshape(L, -1), eid.reshape(L, -1),
                              sid.reshape(L, -1), gains.reshape(L, -1))
     rps[name], eids[name], sids[name], gns[name] = rp, eid, sid, gains
-  for s in sides:
-    done = t.cuda.Event()
-    done.record(s)
-    main.wait_event(done)
+  _preprocess_stacks(calls)
   if enable_minibatching:
     _minibatching_passes(pending, jobs, flat,
                          sample_views if sample_views is not None else {})
