@@ -240,7 +240,7 @@ def test_wide_keys():
 
 
 def test_view_tail_and_many_stacks():
-  """Several stacks of one call (side streams) with their sample views."""
+  """Several stacks of one call (grouped launches) with their sample views."""
   rng = np.random.default_rng(21)
   batch = 1024
   specs = []
