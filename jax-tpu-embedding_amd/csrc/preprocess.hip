@@ -2593,8 +2593,10 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
                         ? ws.Take<float>(pl.total_rows)
                         : nullptr;
   ViewParts view{};
-  // The bucket pass writes no CSR, so no view either.
-  if (o->build_sample_view && !(minibatching && pass == 1)) {
+  // The bucket pass writes no CSR, so no view either. (Measuring, the view's
+  // buffers are null: `has_view` says whether there is one.)
+  const bool has_view = o->build_sample_view && !(minibatching && pass == 1);
+  if (has_view) {
     if (pl.L != 1 || pl.G != 1) {
       return Fail(SCEMB_ERR_INVALID_ARGUMENT,
                   "the sample view needs one local and one global device");
@@ -2743,10 +2745,9 @@ int RunPipeline(const scemb_feature_t* feats, int nf,
   if (st != 0) return st;
   if (measuring) {
     // The view's scan runs last; size its temporaries at the same point.
-    return view.entry != nullptr
-               ? ExclusiveScan<uint32_t>(nullptr, nullptr, M + 1, nullptr, ws,
-                                         stream)
-               : 0;
+    return has_view ? ExclusiveScan<uint32_t>(nullptr, nullptr, M + 1,
+                                              nullptr, ws, stream)
+                    : 0;
   }
   if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
   // Without minibatching the fill plan's single block reduces the bucket
@@ -2900,9 +2901,11 @@ struct UniqueStack {
   bool view = false;
   uint32_t* view_off = nullptr;
   uint32_t* view_total = nullptr;
-  uint32_t* view_partial = nullptr;  // null: the view scan is not grouped
+  bool view_grouped = false;  // the view's scan is a grouped scan
+  uint32_t* view_partial = nullptr;
   uint32_t* hist = nullptr;
-  uint32_t* hist_partial = nullptr;  // null: the sort's scans are not grouped
+  bool hist_grouped = false;  // so are the sort's scans
+  uint32_t* hist_partial = nullptr;
   uint32_t* totals = nullptr;        // [passes], cleared by the set-up
   ExtractUniqueArgs<K, true> ex;     // fields shared by both variants
   int64_t view_grid = 0;
@@ -2962,6 +2965,8 @@ int PrepareUnique(const scemb_feature_t* feats, int nf,
   // to ExclusiveScan, whose temporaries EnqueueUnique takes from ws.
   const int64_t view_words = view ? GroupedScanPartialWords(extract_blocks) : 0;
   const int64_t hist_words = GroupedScanPartialWords(cells);
+  u->view_grouped = view_words > 0;
+  u->hist_grouped = hist_words > 0;
   u->view_partial = view_words > 0 ? ws.Take<uint32_t>(view_words) : nullptr;
   u->hist_partial = hist_words > 0 ? ws.Take<uint32_t>(hist_words) : nullptr;
   if (view) {
@@ -3110,7 +3115,7 @@ int EnqueueUnique(UniqueStack<K>* const* st, int n, hipStream_t stream) {
     for (int i = 0; i < n; ++i) {
       UniqueStack<K>& u = *st[i];
       if (!u.view || u.extract_blocks == 0) continue;
-      if (u.view_partial != nullptr) {
+      if (u.view_grouped) {
         jobs.push_back(ScanJob<uint32_t>{u.view_off, u.view_off,
                                          u.extract_blocks, u.view_total,
                                          u.view_partial});
@@ -3170,7 +3175,7 @@ int EnqueueUnique(UniqueStack<K>* const* st, int n, hipStream_t stream) {
       sn[i] = {arr,   sink,  u.M,   u.totals, 1,
                shift, mask,  pbits, u.tiles,  u.hist,
                u.totals + pass, false};
-      if (u.hist_partial != nullptr) {
+      if (u.hist_grouped) {
         jobs.push_back(ScanJob<uint32_t>{u.hist, u.hist, cells,
                                          u.totals + pass, u.hist_partial});
       }
@@ -3187,9 +3192,7 @@ int EnqueueUnique(UniqueStack<K>* const* st, int n, hipStream_t stream) {
     }
     for (int i = 0; i < n; ++i) {
       UniqueStack<K>& u = *st[i];
-      if (pass >= u.dp.passes || u.M == 0 || u.hist_partial != nullptr) {
-        continue;
-      }
+      if (pass >= u.dp.passes || u.M == 0 || u.hist_grouped) continue;
       const int shift = pass * u.dp.digit;
       const int pbits =
           u.key_bits - shift < u.dp.digit ? u.key_bits - shift : u.dp.digit;
