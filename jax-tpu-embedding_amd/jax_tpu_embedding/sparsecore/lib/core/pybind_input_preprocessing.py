@@ -382,6 +382,67 @@ def _preprocess_stacks(calls):
       jobs, len(calls), _native.stream_handle()))
 
 
+class _StackPlan:
+  """What one stack's library call needs besides its outputs (_plan_stack):
+  the ctypes options and features (held until the call), the workspace
+  bytes, the COO buffer size per device and the stats layout."""
+  __slots__ = ("structs", "num_features", "opts", "need", "coo", "L", "S",
+               "ns", "off")
+
+
+def _plan_stack(feats, metas, *, local_device_count, global_device_count,
+                num_sc_per_device, allow_id_dropping, has_weights,
+                build_view=False, enable_minibatching=False,
+                minibatching_pass=0, minibatching_split=0) -> _StackPlan:
+  lib = _native.load_library()
+  ns = num_sc_per_device * global_device_count
+  c = _coo_buffer_size(metas[0], global_device_count, num_sc_per_device,
+                       enable_minibatching)
+  bound = max(m.stack_vocab_size for m in metas)
+  for f, m in zip(feats, metas):
+    if f.max_id is not None:
+      bound = max(bound, m.col_offset + f.max_id + ns + 1)
+  plan = _StackPlan()
+  plan.opts = _native.PreprocessOptions(
+      local_device_count, global_device_count, num_sc_per_device,
+      _COMBINERS.get(metas[0].row_combiner, 0),
+      metas[0].max_ids_per_partition, metas[0].max_unique_ids_per_partition,
+      int(bool(allow_id_dropping)), int(bool(has_weights)), c, bound,
+      int(bool(build_view)), int(bool(enable_minibatching)),
+      metas[0].stack_vocab_size // global_device_count,
+      int(minibatching_pass), PREPROCESS_FLAGS, int(minibatching_split))
+  plan.structs = _native.feature_structs(
+      [(_native.ptr(f.ids), _native.ptr(f.weights), _native.ptr(f.splits),
+        0 if f.splits_host is None else f.splits_host.ctypes.data,
+        f.num_rows, f.nnz, f.valency, m.row_offset, m.col_offset, m.col_shift,
+        f.max_row_length or 0) for f, m in zip(feats, metas)])
+  plan.num_features = len(feats)
+  plan.need = lib.scemb_preprocess_workspace_size(plan.structs, len(feats),
+                                                  ctypes.byref(plan.opts))
+  if plan.need == 0:
+    _native.check(_native.SCEMB_ERR_INVALID_ARGUMENT)
+  plan.coo, plan.L, plan.S, plan.ns = c, local_device_count, num_sc_per_device, ns
+  # The stats block's int64 counters follow the per-partition stats
+  # (scemb_preprocess_stats_counters_offset).
+  stats = 2 * plan.L * ns + plan.L * plan.S
+  plan.off = stats + stats % 2
+  return plan
+
+
+def _output_words(plan, enable_minibatching, build_view, outputs=True):
+  """int32 words of a stack's outputs, in order: row pointers, ids, samples,
+  gains (unless `outputs` is false), then view keys and entries."""
+  L, S, c = plan.L, plan.S, plan.coo
+  parts = []
+  if outputs:
+    parts += [L * S * max(plan.ns, 8) *
+              (_native.MAX_MINIBATCHES if enable_minibatching else 1),
+              L * c, L * c, L * c]
+  if build_view:
+    parts += [c, 2 * c]
+  return parts
+
+
 def _prepare_stack(feats, metas, *, local_device_count, global_device_count,
                    num_sc_per_device, allow_id_dropping, has_weights,
                    build_view=False, enable_minibatching=False,
@@ -396,43 +457,19 @@ def _prepare_stack(feats, metas, *, local_device_count, global_device_count,
   device tensor of _stats_words(...) slots to hold the stats (else one is
   allocated). The outputs are allocated on the current stream."""
   t = _native.require_gpu()
-  lib = _native.load_library()
   dev = _native.device()
-  ns = num_sc_per_device * global_device_count
-  c = _coo_buffer_size(metas[0], global_device_count, num_sc_per_device,
-                       enable_minibatching)
-  bound = max(m.stack_vocab_size for m in metas)
-  for f, m in zip(feats, metas):
-    if f.max_id is not None:
-      bound = max(bound, m.col_offset + f.max_id + ns + 1)
-  opts = _native.PreprocessOptions(
-      local_device_count, global_device_count, num_sc_per_device,
-      _COMBINERS.get(metas[0].row_combiner, 0),
-      metas[0].max_ids_per_partition, metas[0].max_unique_ids_per_partition,
-      int(bool(allow_id_dropping)), int(bool(has_weights)), c, bound,
-      int(bool(build_view)), int(bool(enable_minibatching)),
-      metas[0].stack_vocab_size // global_device_count,
-      int(minibatching_pass), PREPROCESS_FLAGS, int(minibatching_split))
-  structs = _native.feature_structs(
-      [(_native.ptr(f.ids), _native.ptr(f.weights), _native.ptr(f.splits),
-        0 if f.splits_host is None else f.splits_host.ctypes.data,
-        f.num_rows, f.nnz, f.valency, m.row_offset, m.col_offset, m.col_shift,
-        f.max_row_length or 0) for f, m in zip(feats, metas)])
-  need = lib.scemb_preprocess_workspace_size(structs, len(feats),
-                                             ctypes.byref(opts))
-  if need == 0:
-    _native.check(_native.SCEMB_ERR_INVALID_ARGUMENT)
-  L, S = local_device_count, num_sc_per_device
+  plan = _plan_stack(
+      feats, metas, local_device_count=local_device_count,
+      global_device_count=global_device_count,
+      num_sc_per_device=num_sc_per_device,
+      allow_id_dropping=allow_id_dropping, has_weights=has_weights,
+      build_view=build_view, enable_minibatching=enable_minibatching,
+      minibatching_pass=minibatching_pass,
+      minibatching_split=minibatching_split)
   # Outputs not given come out of one allocation (int32 words, each part
-  # 256-byte aligned): row pointers, ids, samples, gains, view keys and
-  # entries.
-  parts = []
-  if outputs is None:
-    parts += [L * S * max(ns, 8) *
-              (_native.MAX_MINIBATCHES if enable_minibatching else 1),
-              L * c, L * c, L * c]
-  if build_view and not view_outputs:
-    parts += [c, 2 * c]
+  # 256-byte aligned).
+  parts = _output_words(plan, enable_minibatching,
+                        build_view and not view_outputs, outputs is None)
   if parts:
     sizes = [-(-n // 64) * 64 for n in parts]
     block = t.empty(max(sum(sizes), 1), dtype=t.int32, device=dev)
@@ -446,7 +483,7 @@ def _prepare_stack(feats, metas, *, local_device_count, global_device_count,
     rp, eid, sid, gains = carved[:4]
     gains = gains.view(t.float32)
     carved = carved[4:]
-  nstats = lib.scemb_preprocess_stats_size(ctypes.byref(opts))
+  nstats = plan.off + 2 * _NUM_COUNTERS
   # The library initialises the whole stats block.
   if stats_out is not None:
     if int(stats_out.numel()) < nstats:
@@ -461,10 +498,11 @@ def _prepare_stack(feats, metas, *, local_device_count, global_device_count,
       _native.ptr(rp), _native.ptr(eid), _native.ptr(sid), _native.ptr(gains),
       _native.ptr(stats), None if view is None else _native.ptr(view[0]),
       None if view is None else _native.ptr(view[1]))
-  off = int(lib.scemb_preprocess_stats_counters_offset(ctypes.byref(opts)))
   # The stats stay on the device until every stack has been enqueued.
-  return (_StackCall(structs, len(feats), opts, out, need),
-          (rp, eid, sid, gains, stats, (L, S, ns, off), view))
+  return (_StackCall(plan.structs, plan.num_features, plan.opts, out,
+                     plan.need),
+          (rp, eid, sid, gains, stats, (plan.L, plan.S, plan.ns, plan.off),
+           view))
 
 
 def _stats_words(local_device_count, global_device_count, num_sc_per_device):
@@ -688,9 +726,10 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
   # Every stack goes to the library in one call on the current stream, which
   # runs each stage of the stacks that merge duplicates at extraction as one
   # launch for all of them (the kernels of one stage then fill the device
-  # together).
-  calls = []
-  for i, (name, metas) in enumerate(stacks.items()):
+  # together). The call takes the outputs' addresses in one block for all
+  # stacks; their tensors are made while the device works.
+  plans, layout, total = [], [], 0
+  for name, metas in stacks.items():
     feats = [_resolve_feature(f) for f in stack_feats[name]]
     kwargs = dict(feats=feats, metas=metas,
                   local_device_count=local_device_count,
@@ -699,11 +738,41 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
                   allow_id_dropping=allow_id_dropping,
                   has_weights=feature_weights is not None,
                   enable_minibatching=enable_minibatching)
-    call, (rp, eid, sid, gains, stats_dev, (L, S, ns, off),
-           view) = _prepare_stack(
-               **kwargs, build_view=build_view,
-               stats_out=pending.stats_buffer[i * words:(i + 1) * words])
-    calls.append(call)
+    plan = _plan_stack(**kwargs, build_view=build_view)
+    if plan.off + 2 * _NUM_COUNTERS > words:
+      raise ValueError("stats buffer too small")
+    parts = _output_words(plan, enable_minibatching, build_view)
+    offs = []
+    for n in parts:
+      offs.append(total)
+      total += -(-n // 64) * 64  # 256-byte aligned parts
+    plans.append((name, kwargs, plan))
+    layout.append((parts, offs))
+  block = t.empty(max(total, 1), dtype=t.int32, device=_native.device())
+  base = _native.ptr(block)
+  stats_base = _native.ptr(pending.stats_buffer)
+  calls = []
+  for i, ((name, kwargs, plan), (parts, offs)) in enumerate(zip(plans,
+                                                                layout)):
+    addr = [base + 4 * o for o in offs]
+    out = _native.PreprocessOutput(
+        addr[0], addr[1], addr[2], addr[3], stats_base + 4 * i * words,
+        addr[4] if build_view else None, addr[5] if build_view else None)
+    calls.append(_StackCall(plan.structs, plan.num_features, plan.opts, out,
+                            plan.need))
+  _preprocess_stacks(calls)
+  for i, ((name, kwargs, plan), (parts, offs)) in enumerate(zip(plans,
+                                                                layout)):
+    rp, eid, sid, gains = (block[o:o + n] for o, n in zip(offs[:4],
+                                                           parts[:4]))
+    gains = gains.view(t.float32)
+    view = None
+    if build_view:
+      view = (block[offs[4]:offs[4] + parts[4]],
+              block[offs[5]:offs[5] + parts[5]].view(t.int64))
+    stats_dev = pending.stats_buffer[i * words:(i + 1) * words]
+    L, S, ns, off = plan.L, plan.S, plan.ns, plan.off
+    feats = kwargs["feats"]
     if view is not None:
       sample_views[name] = view
     pending.append((name, stats_dev, L, S, ns, off, feats))
@@ -713,7 +782,6 @@ def enqueue_preprocessing(features, feature_weights, feature_specs,
       rp, eid, sid, gains = (rp.reshape(L, -1), eid.reshape(L, -1),
                              sid.reshape(L, -1), gains.reshape(L, -1))
     rps[name], eids[name], sids[name], gns[name] = rp, eid, sid, gains
-  _preprocess_stacks(calls)
   if enable_minibatching:
     _minibatching_passes(pending, jobs, flat,
                          sample_views if sample_views is not None else {})
