@@ -1,8 +1,9 @@
 // Stable LSD radix sort passes over a source and into a sink (gfx950).
 //
 // One pass sorts by one digit of at most kMaxDigitBits bits:
-//   RadixHistogramK  per-tile digit histograms (LDS atomics, one per digit
-//                    and wave), digit-major
+//   RadixHistogramK  per-tile digit histograms (LDS atomics: one per wave
+//                    whose lanes share a digit, else one per lane),
+//                    digit-major
 //   ExclusiveScan    of the histogram matrix (scan.h), with the total
 //   RadixScatterK    stable scatter of each tile into the digit buckets
 // The source decides which input positions take part (a position it
@@ -90,8 +91,6 @@ __device__ __forceinline__ void RadixHistogramBody(
   const int64_t m = ActiveCount(n, n_dev, n_dev_words);
   const int64_t tile = tile_index;
   const int64_t base = tile * kSortTile;
-  const int digit_bits = __popc(mask);
-  const uint64_t lt = LaneMaskLt();
   // All of the thread's keys first: the source reads through pointers that
   // the compiler cannot tell apart from the LDS counters, so loads issued
   // between the atomics would each wait for the one before.
@@ -106,15 +105,20 @@ __device__ __forceinline__ void RadixHistogramBody(
   for (int c = 0; c < kSortChunks; ++c) {
     const bool active = act[c];
     const uint32_t d = active ? Digit(keys[c], shift, mask) : 0u;
-    // Lanes of one digit add their count through one atomic (runs of equal
-    // keys would otherwise serialise on one LDS address).
-    uint64_t match = __ballot(active);
-    for (int b = 0; b < digit_bits; ++b) {
-      const uint64_t bits = __ballot((d >> b) & 1u);
-      match &= ((d >> b) & 1u) ? bits : ~bits;
-    }
-    if (active && (match & lt) == 0) {
-      atomicAdd(&h[d], static_cast<uint32_t>(__popcll(match)));
+    // A wave whose active lanes share one digit (a run of equal keys, as the
+    // later passes see them) adds its count with one atomic; otherwise each
+    // lane adds one, which costs less than finding the lanes of each digit.
+    const uint64_t live = __ballot(active);
+    if (live == 0) continue;  // uniform
+    const int first = __ffsll(static_cast<long long>(live)) - 1;
+    const uint32_t d0 = static_cast<uint32_t>(
+        __shfl(static_cast<int>(d), first, kWave));
+    if (__ballot(active && d == d0) == live) {
+      if (LaneId() == first) {
+        atomicAdd(&h[d0], static_cast<uint32_t>(__popcll(live)));
+      }
+    } else if (active) {
+      atomicAdd(&h[d], 1u);
     }
   }
 #pragma unroll
