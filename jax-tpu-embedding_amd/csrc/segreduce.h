@@ -458,7 +458,26 @@ struct StreamArgs {
   int64_t rows_per_partition;
   int64_t bps;
   int64_t n;
+  // kSrcCsr: entries of hot runs, which the hot-run kernels reduce instead
+  // (null: none). Per block of kBlock entries, hot_head holds the count of
+  // leading entries that belong to a hot run and hot_tail the index from
+  // which the trailing ones do, each with that run's index in the upper 16
+  // bits; a run whose entries failed their check (run_bad) stays here.
+  const uint32_t* hot_head;
+  const uint32_t* hot_tail;
+  const uint32_t* run_bad;
 };
+
+// The entries [0, *lead) and [*trail, kBlock) of block b belong to hot runs.
+__device__ __forceinline__ void HotSpan(const StreamArgs& s, int64_t b,
+                                        int* lead, int* trail) {
+  const uint32_t h = s.hot_head[b];
+  const uint32_t t = s.hot_tail[b];
+  *lead = (h & 0xffffu) != 0 && s.run_bad[h >> 16] == 0
+              ? static_cast<int>(h & 0xffffu) : 0;
+  *trail = (t & 0xffffu) < kBlock && s.run_bad[t >> 16] == 0
+               ? static_cast<int>(t & 0xffffu) : kBlock;
+}
 
 // What the reduction reads and writes.
 struct RowArgs {
@@ -480,6 +499,38 @@ struct RowArgs {
   bool single_runs;
 };
 
+// Key of CSR position e (partition * rows_per_partition + embedding id) and
+// its sample in *sample, or kSkip for padding and invalid entries (reported
+// through `status` when it is set).
+__device__ __forceinline__ uint32_t CsrKeySample(const StreamArgs& s,
+                                                 int64_t e, int32_t* sample,
+                                                 uint32_t* status) {
+  *sample = 0;
+  int seg = 0;
+  const int p = s.csr.num_minibatches > 0
+                    ? LocateEntry(s.csr, e, &seg)
+                    : PartitionOf(s.csr.rp, s.csr.num_partitions,
+                                  s.csr.per_segment, e);
+  if (p < 0) return kSkip;
+  const int32_t id = s.csr.eid[e];
+  const int32_t sm = s.csr.sid[e];
+  if (id < 0 || id >= s.rows_per_partition || sm < 0 || sm >= s.bps) {
+    if (status != nullptr) atomicOr(status, SCEMB_STATUS_BAD_ENTRY);
+    return kSkip;
+  }
+  *sample = sm;
+  return static_cast<uint32_t>(p * s.rows_per_partition + id);
+}
+
+// The same with the sample and gain packed in *ent (0 for kSkip).
+__device__ __forceinline__ uint32_t CsrKey(const StreamArgs& s, int64_t e,
+                                           uint64_t* ent, uint32_t* status) {
+  int32_t sm;
+  const uint32_t k = CsrKeySample(s, e, &sm, status);
+  *ent = k == kSkip ? 0 : Pack(static_cast<uint32_t>(sm), s.csr.gains[e]);
+  return k;
+}
+
 template <int SRC>
 __device__ __forceinline__ uint32_t FetchEntry(const StreamArgs& s, int64_t e,
                                                uint64_t* ent,
@@ -495,21 +546,7 @@ __device__ __forceinline__ uint32_t FetchEntry(const StreamArgs& s, int64_t e,
     }
     return k;
   } else {
-    *ent = 0;
-    int seg = 0;
-    const int p = s.csr.num_minibatches > 0
-                      ? LocateEntry(s.csr, e, &seg)
-                      : PartitionOf(s.csr.rp, s.csr.num_partitions,
-                                    s.csr.per_segment, e);
-    if (p < 0) return kSkip;
-    const int32_t id = s.csr.eid[e];
-    const int32_t sm = s.csr.sid[e];
-    if (id < 0 || id >= s.rows_per_partition || sm < 0 || sm >= s.bps) {
-      if (status != nullptr) atomicOr(status, SCEMB_STATUS_BAD_ENTRY);
-      return kSkip;
-    }
-    *ent = Pack(static_cast<uint32_t>(sm), s.csr.gains[e]);
-    return static_cast<uint32_t>(p * s.rows_per_partition + id);
+    return CsrKey(s, e, ent, status);
   }
 }
 
@@ -1095,22 +1132,46 @@ __global__ __launch_bounds__(kBlock) void SegReduce(StreamArgs st, RowArgs r) {
       return;
     }
   }
+  // Entries of hot runs read as outside any run; a block of nothing else
+  // has no work.
+  const bool hot = SRC == kSrcCsr && st.hot_head != nullptr;
+  int lead = 0, trail = kBlock;
+  if (hot) {
+    HotSpan(st, blk, &lead, &trail);
+    if (lead >= trail) {
+      if (tid == 0) r.block_flags[blk] = 0;
+      return;
+    }
+  }
   if (kMapped) StageRowMap(r.act, &s_map);
   {
     uint64_t en = 0;
     uint32_t k = kSkip;
-    if (cb + tid < n) k = FetchEntry<SRC>(st, cb + tid, &en, r.status);
+    if (cb + tid < n && tid >= lead && tid < trail) {
+      k = FetchEntry<SRC>(st, cb + tid, &en, r.status);
+    }
     s_key[tid + 1] = k;
     s_ent[tid] = en;
     if (tid == 0) {
       uint64_t d;
-      s_key[0] = cb > 0 ? FetchEntry<SRC>(st, cb - 1, &d, nullptr) : kSkip;
+      bool skip = cb == 0;
+      if (!skip && hot) {
+        int l, t;
+        HotSpan(st, blk - 1, &l, &t);
+        skip = kBlock - 1 < l || kBlock - 1 >= t;
+      }
+      s_key[0] = skip ? kSkip : FetchEntry<SRC>(st, cb - 1, &d, nullptr);
     }
     if (tid == kBlock - 1) {
       uint64_t d;
+      bool skip = cb + kBlock >= n;
+      if (!skip && hot) {
+        int l, t;
+        HotSpan(st, blk + 1, &l, &t);
+        skip = 0 < l || 0 >= t;
+      }
       s_key[kBlock + 1] =
-          cb + kBlock < n ? FetchEntry<SRC>(st, cb + kBlock, &d, nullptr)
-                          : kSkip;
+          skip ? kSkip : FetchEntry<SRC>(st, cb + kBlock, &d, nullptr);
     }
   }
   __syncthreads();
@@ -1418,6 +1479,635 @@ __global__ __launch_bounds__(kBlock) void SegFinish(int64_t num_blocks,
 
 #ifndef __HIPCC_RTC__
 // ---------------------------------------------------------------------------
+// Hot runs of the backward: the CSR read in place (one segment, no
+// minibatching) with several entries per activation row. SegReduce gathers
+// one activation-gradient row per entry, and the long runs of the hottest
+// table rows spread over every sample: together they sweep the whole
+// gradient matrix many times, from beyond the L2. A run longer than about
+// a few times the number of sample tiles is reduced per tile instead. A
+// block stages one tile of gradient rows in LDS, then the CSR entries its
+// group's runs hold in that tile, and adds the rows up from LDS: each
+// gradient row is read from memory once per (tile, group) rather than once
+// per entry, and the reduction waits on no global load.
+//
+// The CSR holds a run's entries contiguously and ascending by sample (the
+// grouping key's low bits are the sample row, input_preprocessing_util.cc
+// and coo_format.h GetGroupingKey), so a run's entries in one tile form a
+// contiguous range. Every entry of a candidate run is checked; a run that
+// fails stays with SegReduce.
+//   HotPoints  the key of every q-th position; a run holding two such
+//              positions is hot. Bit masks of each run's first and last
+//              sampled position, counts per 256 positions, and the
+//              SegReduce blocks' hot marks cleared.
+//   HotPlan    one block per run: which sampled positions are its first and
+//              last, its exact bounds, the SegReduce blocks' hot marks.
+//   HotCheck   one thread per marked entry: same key, samples strictly
+//              ascending; the first entry of each tile.
+//   HotTile    one block per (tile, group): a partial row per (run, tile),
+//              its entries spread over kHotAcc chains joined by a tree.
+//   HotCombine kHotCombineSplit blocks per run, each over a range of tiles
+//              (strided over sub-groups, joined by a tree).
+//   HotUpdate  one sub-group per run: the HotCombine rows in order, then the
+//              optimizer update. (A ticket for the last HotCombine block of
+//              a run needs device-scope fences, which write back and
+//              invalidate the per-XCD L2s: a launch is cheaper.)
+// Run-to-run identical: every sum has a fixed order and no float atomics.
+// ---------------------------------------------------------------------------
+constexpr int kHotPointBlock = 256;  // sampled positions per HotPoints block
+constexpr int kHotPlanBlock = 256;
+constexpr int kHotTileBlock = 512;
+// LDS of a HotTile block: one tile of gradient rows, a pass's runs and the
+// CSR entries staged per pass; two blocks fit a CU, so that one block's
+// loads overlap the other's arithmetic.
+constexpr int kHotTileBytes = 64 * 1024;
+constexpr int kHotStage = 1408;
+constexpr int kHotPassRuns = 256;
+constexpr int kHotMaxPointBlocks = 4 * kHotPlanBlock;  // HotPlan's scan
+constexpr int kHotMaxRuns = 1 << 16;  // run index in 16 bits of a mark
+// Accumulators per sub-group in HotTile. A run has at most one entry per
+// sample (checked) and a tile at most kHotChain * kHotAcc samples, so each
+// chain adds at most kHotChain entries; HotCombine then adds at most
+// tiles / (kHotCombineSplit * kHotCombineBlock / G) partial rows per chain,
+// joins its sub-groups by a tree and its kHotCombineSplit blocks' rows in
+// order, like the error bound of the other reductions.
+constexpr int kHotAcc = 8;
+constexpr int kHotChain = 64;
+static_assert(kHotChain * kHotAcc <= kHotStage,
+              "a pass must hold one run's entries in a full tile");
+constexpr int kHotCombineBlock = 1024;
+constexpr int kHotCombineSplit = 8;  // HotCombine blocks per run
+constexpr int kHotLoadUnroll = 8;  // loads per thread issued together
+
+struct HotArgs {
+  int64_t q;           // spacing of the sampled positions (multiple of kBlock)
+  int64_t points;      // sampled positions: ceil(n / q)
+  int64_t seg_blocks;  // SegReduce blocks: ceil(n / kBlock)
+  int32_t max_runs;
+  int32_t tile_rows;   // activation rows per tile
+  int32_t num_tiles;
+  int32_t num_groups;  // runs r, r + num_groups, ... share a HotTile block
+  uint64_t* first_mask;   // [4 * point blocks]
+  uint64_t* last_mask;
+  uint32_t* first_count;  // [point blocks]
+  uint32_t* last_count;
+  uint32_t* count;        // runs taken: min(found, max_runs)
+  uint32_t* run_key;      // [max_runs]
+  int32_t* run_start;
+  int32_t* run_end;
+  uint32_t* run_bad;
+  uint32_t* hot_head;     // [seg_blocks], as StreamArgs
+  uint32_t* hot_tail;
+  int32_t* tile_off;      // [max_runs][num_tiles + 1]: first entry per tile
+  float* partials;        // [max_runs][num_tiles][dim]
+  float* partials2;       // [max_runs][kHotCombineSplit][dim]
+};
+
+__global__ __launch_bounds__(kHotPointBlock) void HotPoints(StreamArgs st,
+                                                            HotArgs h) {
+  __shared__ uint32_t s_k[kHotPointBlock + 2];
+  __shared__ uint32_t s_cnt[2][kHotPointBlock / kWave];
+  const int tid = threadIdx.x;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kHotPointBlock + tid;
+  const int64_t per = h.q / kBlock;
+  for (int64_t b = i * per; b < (i + 1) * per && b < h.seg_blocks; ++b) {
+    h.hot_head[b] = 0;
+    h.hot_tail[b] = kBlock;
+  }
+  int32_t d;
+  s_k[tid + 1] =
+      i < h.points ? CsrKeySample(st, i * h.q, &d, nullptr) : kSkip;
+  if (tid == 0) {
+    s_k[0] = i > 0 ? CsrKeySample(st, (i - 1) * h.q, &d, nullptr) : kSkip;
+  }
+  if (tid == kHotPointBlock - 1) {
+    s_k[kHotPointBlock + 1] =
+        i + 1 < h.points ? CsrKeySample(st, (i + 1) * h.q, &d, nullptr)
+                         : kSkip;
+  }
+  __syncthreads();
+  const uint32_t k = s_k[tid + 1];
+  const uint32_t kp = s_k[tid];
+  const uint32_t kn = s_k[tid + 2];
+  const uint64_t fm = __ballot(k != kSkip && k == kn && k != kp);
+  const uint64_t lm = __ballot(k != kSkip && k == kp && k != kn);
+  const int wave = tid / kWave;
+  if (tid % kWave == 0) {
+    h.first_mask[i / kWave] = fm;
+    h.last_mask[i / kWave] = lm;
+    s_cnt[0][wave] = static_cast<uint32_t>(__popcll(fm));
+    s_cnt[1][wave] = static_cast<uint32_t>(__popcll(lm));
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t a = 0, b = 0;
+    for (int w = 0; w < kHotPointBlock / kWave; ++w) {
+      a += s_cnt[0][w];
+      b += s_cnt[1][w];
+    }
+    h.first_count[blockIdx.x] = a;
+    h.last_count[blockIdx.x] = b;
+  }
+}
+
+__global__ __launch_bounds__(kHotPlanBlock) void HotPlan(StreamArgs st,
+                                                         HotArgs h,
+                                                         int64_t point_blocks,
+                                                         uint32_t* status) {
+  constexpr int kWaves = kHotPlanBlock / kWave;
+  __shared__ uint32_t s_scan[kWaves + 1];
+  __shared__ int64_t s_point[2];
+  __shared__ int32_t s_red[2];
+  const int tid = threadIdx.x;
+  const uint32_t r = blockIdx.x;
+  if (tid == 0) {
+    s_point[0] = -1;
+    s_point[1] = -1;
+  }
+  uint32_t runs = 0;
+  for (int which = 0; which < 2; ++which) {
+    const uint32_t* cnt = which == 0 ? h.first_count : h.last_count;
+    const uint64_t* mask = which == 0 ? h.first_mask : h.last_mask;
+    uint32_t c[4];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t idx = static_cast<int64_t>(tid) * 4 + u;
+      c[u] = idx < point_blocks ? cnt[idx] : 0u;
+      sum += c[u];
+    }
+    uint32_t total;
+    uint32_t base =
+        BlockExclusiveScan<uint32_t, kHotPlanBlock>(sum, s_scan, &total);
+    if (which == 0) runs = total;
+    if (r >= base && r < base + sum) {
+      int u = 0;
+      while (r >= base + c[u]) base += c[u++];
+      uint32_t rank = r - base;
+      const int64_t pb = static_cast<int64_t>(tid) * 4 + u;
+      for (int w = 0; w < kHotPointBlock / kWave; ++w) {
+        uint64_t m = mask[pb * (kHotPointBlock / kWave) + w];
+        const uint32_t pc = static_cast<uint32_t>(__popcll(m));
+        if (rank < pc) {
+          for (uint32_t q = 0; q < rank; ++q) m &= m - 1;
+          s_point[which] = pb * kHotPointBlock + w * kWave +
+                           (__ffsll(static_cast<long long>(m)) - 1);
+          break;
+        }
+        rank -= pc;
+      }
+    }
+    __syncthreads();
+  }
+  const uint32_t taken =
+      runs < static_cast<uint32_t>(h.max_runs) ? runs : h.max_runs;
+  if (r == 0 && tid == 0) *h.count = taken;
+  if (r >= taken) return;
+  if (s_point[0] < 0 || s_point[1] <= s_point[0]) {
+    if (tid == 0) h.run_bad[r] = 1;  // no marks: the run stays with SegReduce
+    return;
+  }
+  const int64_t pf = s_point[0] * h.q;
+  const int64_t pl = s_point[1] * h.q;
+  int32_t d;
+  const uint32_t key = CsrKeySample(st, pf, &d, nullptr);
+  // The run's first entry lies in (pf - q, pf], its end in [pl, pl + q).
+  // Each is the first position of a window where a predicate turns true
+  // (wave 0: key == K; wave 1: key != K, or the window's end): rounds of 64
+  // probes, each narrowing the window 64-fold (two rounds for q <= 4096).
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  if (wave < 2) {
+    int64_t lo = wave == 0 ? (pf - h.q + 1 > 0 ? pf - h.q + 1 : 0) : pl;
+    int64_t hi = wave == 0 ? pf + 1 : (pl + h.q < st.n ? pl + h.q : st.n);
+    while (lo < hi) {
+      const int64_t step = (hi - lo + kWave - 1) / kWave;
+      const int64_t p = lo + lane * step;
+      bool pred = false;
+      if (p < hi) {
+        const uint32_t k = CsrKeySample(st, p, &d, nullptr);
+        pred = wave == 0 ? k == key : k != key;
+      }
+      const uint64_t m = __ballot(pred);
+      if (m != 0) {
+        const int64_t l = __ffsll(static_cast<long long>(m)) - 1;
+        hi = lo + l * step;
+        lo = l > 0 ? lo + (l - 1) * step + 1 : lo;
+      } else {
+        lo = lo + (hi - 1 - lo) / step * step + 1;
+      }
+    }
+    if (lane == 0) s_red[wave] = static_cast<int32_t>(hi);
+  }
+  __syncthreads();
+  const int32_t s = s_red[0];
+  const int32_t e = s_red[1];
+  // A run holds two sampled positions, so it spans more than q entries and
+  // at least two SegReduce blocks; anything else is not a sorted run.
+  const bool ok = key != kSkip && s <= pf && e > pl &&
+                  static_cast<int64_t>(e) - s > h.q;
+  if (tid == 0) {
+    h.run_key[r] = key;
+    h.run_start[r] = s;
+    h.run_end[r] = e;
+    h.run_bad[r] = ok ? 0u : 1u;
+    // SegReduce no longer compares the keys on either side of the run.
+    if (ok && status != nullptr) {
+      const uint32_t kb =
+          s > 0 ? CsrKeySample(st, s - 1, &d, nullptr) : kSkip;
+      const uint32_t ka =
+          e < st.n ? CsrKeySample(st, e, &d, nullptr) : kSkip;
+      if ((kb != kSkip && kb > key) || (ka != kSkip && ka < key)) {
+        atomicOr(status, SCEMB_STATUS_UNSORTED);
+      }
+    }
+  }
+  if (!ok) return;
+  const int64_t b0 = s / kBlock;
+  const int64_t b1 = (e - 1) / kBlock;
+  const uint32_t tag = r << 16;
+  for (int64_t b = b0 + tid; b <= b1; b += kHotPlanBlock) {
+    if (b == b0) {
+      h.hot_tail[b] = static_cast<uint32_t>(s - b0 * kBlock) | tag;
+    } else if (b == b1) {
+      h.hot_head[b] = static_cast<uint32_t>(e - b1 * kBlock) | tag;
+    } else {
+      h.hot_head[b] = static_cast<uint32_t>(kBlock) | tag;
+    }
+  }
+}
+
+// Each thread checks kHotCheckPer consecutive positions of one SegReduce
+// block, their ids and samples read as 16-byte vectors.
+constexpr int kHotCheckPer = 8;
+constexpr int kHotCheckSpan = kBlock * kHotCheckPer;  // positions per block
+
+__global__ __launch_bounds__(kBlock) void HotCheck(StreamArgs st, HotArgs h) {
+  constexpr int K = kHotCheckPer;
+  const int tid = threadIdx.x;
+  const int64_t j0 = static_cast<int64_t>(blockIdx.x) * kHotCheckSpan +
+                     static_cast<int64_t>(tid) * K;
+  const int64_t b = j0 / kBlock;
+  if (b >= h.seg_blocks) return;
+  const uint32_t hw = h.hot_head[b];
+  const uint32_t tw = h.hot_tail[b];
+  const int lead = static_cast<int>(hw & 0xffffu);
+  const int trail = static_cast<int>(tw & 0xffffu);
+  const int i0 = static_cast<int>(j0 - b * kBlock);
+  if (i0 >= lead && i0 + K <= trail) return;  // no position in a hot range
+  if (lead > trail && i0 < lead && i0 + K > trail) {
+    h.run_bad[hw >> 16] = 1;  // marks of two runs overlap: not sorted runs
+    h.run_bad[tw >> 16] = 1;
+    return;
+  }
+  int32_t eid[K], sid[K];
+  // Vector loads where both arrays are 16-byte aligned at j0 (the CSR may be
+  // slices of one buffer at any 4-byte offset).
+  const bool vec = j0 + K <= st.n &&
+                   ((reinterpret_cast<uintptr_t>(st.csr.eid + j0) |
+                     reinterpret_cast<uintptr_t>(st.csr.sid + j0)) & 15u) == 0;
+  if (vec) {
+    const int4* pe = reinterpret_cast<const int4*>(st.csr.eid + j0);
+    const int4* ps = reinterpret_cast<const int4*>(st.csr.sid + j0);
+#pragma unroll
+    for (int v = 0; v < K / 4; ++v) {
+      const int4 e4 = pe[v];
+      const int4 s4 = ps[v];
+      eid[4 * v] = e4.x;
+      eid[4 * v + 1] = e4.y;
+      eid[4 * v + 2] = e4.z;
+      eid[4 * v + 3] = e4.w;
+      sid[4 * v] = s4.x;
+      sid[4 * v + 1] = s4.y;
+      sid[4 * v + 2] = s4.z;
+      sid[4 * v + 3] = s4.w;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      eid[k] = j0 + k < st.n ? st.csr.eid[j0 + k] : -1;
+      sid[k] = j0 + k < st.n ? st.csr.sid[j0 + k] : -1;
+    }
+  }
+  const int32_t before = j0 > 0 ? st.csr.sid[j0 - 1] : -1;
+  const uint32_t rl = hw >> 16;
+  const uint32_t rt = tw >> 16;
+  const uint32_t key_l = h.run_key[rl];
+  const int32_t s_l = h.run_start[rl];
+  const int32_t e_l = h.run_end[rl];
+  const uint32_t key_t = h.run_key[rt];
+  const int32_t s_t = h.run_start[rt];
+  const int32_t e_t = h.run_end[rt];
+  const int32_t rows = h.tile_rows;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int i = i0 + k;
+    const bool in_lead = i < lead;
+    if (!in_lead && i < trail) continue;
+    const uint32_t r = in_lead ? rl : rt;
+    const uint32_t want = in_lead ? key_l : key_t;
+    const int32_t s = in_lead ? s_l : s_t;
+    const int32_t e = in_lead ? e_l : e_t;
+    const int64_t j = j0 + k;
+    // The key as CsrKeySample forms it (one segment, no minibatching).
+    const int p = j < st.n ? PartitionOf(st.csr.rp, st.csr.num_partitions,
+                                         st.csr.per_segment, j)
+                           : -1;
+    const int32_t sm = sid[k];
+    const bool valid = p >= 0 && eid[k] >= 0 &&
+                       eid[k] < st.rows_per_partition && sm >= 0 &&
+                       sm < st.bps;
+    const uint32_t key =
+        valid ? static_cast<uint32_t>(p * st.rows_per_partition + eid[k])
+              : kSkip;
+    const int32_t sp = k == 0 ? before : sid[k - 1];
+    // Strictly ascending: a run has at most one entry per sample, so at
+    // most tile_rows per tile.
+    const bool ok = key == want && j >= s && j < e &&
+                    (j == s || (sp >= 0 && sp < sm));
+    if (!ok) {
+      h.run_bad[r] = 1;
+      continue;
+    }
+    const int32_t tj = sm / rows;
+    int32_t* off = h.tile_off + static_cast<int64_t>(r) * (h.num_tiles + 1);
+    for (int32_t t = j == s ? 0 : sp / rows + 1; t <= tj; ++t) {
+      off[t] = static_cast<int32_t>(j);
+    }
+    if (j == e - 1) {
+      for (int32_t t = tj + 1; t <= h.num_tiles; ++t) off[t] = e;
+    }
+  }
+}
+
+template <int G, int VEC, bool kMapped>
+__global__ __launch_bounds__(kHotTileBlock) void HotTile(StreamArgs st,
+                                                         HotArgs h,
+                                                         RowArgs r) {
+  using V = Vec<VEC>;
+  using T = typename V::T;
+  constexpr int P = kHotTileBlock / G;
+  constexpr int kWaves = kHotTileBlock / kWave;
+  constexpr int U = kHotLoadUnroll;
+  __shared__ float s_tile[kHotTileBytes / sizeof(float)];
+  __shared__ int32_t s_j0[kHotPassRuns];       // a pass's runs: first entry,
+  __shared__ int32_t s_len[kHotPassRuns];      // entries in the tile,
+  __shared__ int32_t s_pos[kHotPassRuns + 1];  // staged at [pos, pos')
+  // Staged entries: the entry's row in s_tile (as a float index) and its
+  // gain. Each run's entries are padded to a multiple of kHotAcc with
+  // (row 0, gain 0), which adds 0 to its sum.
+  __shared__ __align__(16) uint32_t s_row[kHotStage];
+  __shared__ __align__(16) float s_gain[kHotStage];
+  __shared__ int32_t s_scan[kWaves + 1];
+  __shared__ RowMapLds s_map;
+  const int tid = threadIdx.x;
+  const int32_t t = static_cast<int32_t>(blockIdx.x) / h.num_groups;
+  const int32_t g = static_cast<int32_t>(blockIdx.x) % h.num_groups;
+  const int32_t ng = h.num_groups;
+  const int32_t runs = static_cast<int32_t>(*h.count);
+  const int32_t mine = runs > g ? (runs - g + ng - 1) / ng : 0;
+  const int64_t dim = r.dim;
+  const int64_t row0 = static_cast<int64_t>(t) * h.tile_rows;
+  const int32_t rows = static_cast<int32_t>(
+      r.batch - row0 < h.tile_rows ? r.batch - row0 : h.tile_rows);
+  const int64_t stride = h.num_tiles + 1;
+  const int sub = tid / G;
+  const int cl = tid % G;
+  bool staged = false;
+  // The group's runs (g, g + ng, ...) in passes: each pass takes the
+  // longest prefix of the remaining runs whose padded entries in this tile
+  // fit the staging area (a run has at most one entry per sample, so at
+  // most tile_rows, and kHotStage holds that padded: every pass takes one
+  // run at least).
+  for (int32_t base = 0; base < mine;) {
+    const int32_t avail = mine - base < kHotPassRuns ? mine - base
+                                                     : kHotPassRuns;
+    int32_t j0 = 0, len = 0;
+    if (tid < avail) {
+      const int32_t run = g + (base + tid) * ng;
+      if (h.run_bad[run] == 0) {
+        const int32_t* off = h.tile_off + run * stride;
+        j0 = off[t];
+        len = off[t + 1] - j0;
+      }
+    }
+    const int32_t padded = (len + kHotAcc - 1) / kHotAcc * kHotAcc;
+    int32_t total;
+    const int32_t excl =
+        BlockExclusiveScan<int32_t, kHotTileBlock>(padded, s_scan, &total);
+    const int32_t nk =
+        __syncthreads_count(tid < avail && excl + padded <= kHotStage);
+    if (tid <= nk) s_pos[tid] = excl;  // thread nk holds the pass's end
+    if (tid < nk) {
+      s_j0[tid] = j0;
+      s_len[tid] = len;
+    }
+    __syncthreads();
+    const int32_t staged_entries = s_pos[nk];
+    if (staged_entries > 0) {
+      if (!staged) {
+        staged = true;
+        if (kMapped) {
+          StageRowMap(r.act, &s_map);
+          __syncthreads();
+        }
+        // Every thread's loads of the tile are issued before its stores.
+        const int32_t vecs = static_cast<int32_t>(dim / VEC);
+        const int32_t cells = rows * vecs;
+        for (int32_t x0 = 0; x0 < cells; x0 += U * kHotTileBlock) {
+          T v[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int32_t x = x0 + u * kHotTileBlock + tid;
+            v[u] = V::Zero();
+            if (x < cells) {
+              const int32_t row = x / vecs;
+              const float* p = ActAddr<kMapped>(
+                  s_map, const_cast<float*>(r.src), dim, row0 + row,
+                  static_cast<int64_t>(x - row * vecs) * VEC);
+              if (p != nullptr) v[u] = V::Load(p);
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int32_t x = x0 + u * kHotTileBlock + tid;
+            if (x < cells) {
+              V::Store(&s_tile[static_cast<int64_t>(x) * VEC], v[u]);
+            }
+          }
+        }
+      }
+      // The pass's entries: staged position x belongs to the run k with
+      // s_pos[k] <= x < s_pos[k + 1] (a search in LDS); all of a thread's
+      // loads are issued before its stores.
+      for (int32_t x0 = 0; x0 < staged_entries; x0 += U * kHotTileBlock) {
+        int32_t sv[U];
+        float gv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int32_t x = x0 + u * kHotTileBlock + tid;
+          sv[u] = -1;
+          gv[u] = 0.0f;
+          if (x < staged_entries) {
+            int32_t lo = 0, hi = nk;  // last k with s_pos[k] <= x
+            while (hi - lo > 1) {
+              const int32_t mid = (lo + hi) >> 1;
+              if (s_pos[mid] <= x) lo = mid; else hi = mid;
+            }
+            const int32_t i = x - s_pos[lo];
+            if (i < s_len[lo]) {
+              const int64_t e = s_j0[lo] + i;
+              sv[u] = st.csr.sid[e];
+              gv[u] = st.csr.gains[e];
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int32_t x = x0 + u * kHotTileBlock + tid;
+          if (x < staged_entries) {
+            // Checked entries lie in the tile; padding and anything else
+            // add 0.
+            const int64_t rel = sv[u] - row0;
+            const bool in = sv[u] >= 0 && rel >= 0 && rel < rows;
+            s_row[x] = in ? static_cast<uint32_t>(rel * dim) : 0u;
+            s_gain[x] = in ? gv[u] : 0.0f;
+          }
+        }
+      }
+      __syncthreads();
+      for (int64_t col0 = 0; col0 < dim;
+           col0 += static_cast<int64_t>(G) * VEC) {
+        const int64_t col = col0 + static_cast<int64_t>(cl) * VEC;
+        const bool col_ok = col < dim;
+        const float* tile_col = s_tile + (col_ok ? col : 0);
+        for (int32_t kk = sub; kk < nk; kk += P) {
+          const int32_t p0 = s_pos[kk];
+          const int32_t p1 = s_pos[kk + 1];
+          if (p1 <= p0) continue;
+          // Entry i of the run goes to accumulator i % kHotAcc:
+          // independent chains, joined by a tree at the end. An
+          // accumulator starts at +0 and so is never -0: adding a padding
+          // entry's 0 leaves it unchanged.
+          T acc[kHotAcc];
+#pragma unroll
+          for (int u = 0; u < kHotAcc; ++u) acc[u] = V::Zero();
+          for (int32_t q = p0; q < p1; q += kHotAcc) {
+            uint32_t ro[kHotAcc];
+            float gu[kHotAcc];
+#pragma unroll
+            for (int u = 0; u < kHotAcc; ++u) {
+              ro[u] = s_row[q + u];
+              gu[u] = s_gain[q + u];
+            }
+            T v[kHotAcc];
+#pragma unroll
+            for (int u = 0; u < kHotAcc; ++u) v[u] = V::Load(tile_col + ro[u]);
+#pragma unroll
+            for (int u = 0; u < kHotAcc; ++u) {
+              acc[u] = V::Fma(acc[u], gu[u], v[u]);
+            }
+          }
+#pragma unroll
+          for (int w = kHotAcc / 2; w > 0; w /= 2) {
+#pragma unroll
+            for (int u = 0; u < w; ++u) acc[u] = V::Add(acc[u], acc[u + w]);
+          }
+          if (col_ok) {
+            const int32_t run = g + (base + kk) * ng;
+            V::Store(h.partials +
+                         (static_cast<int64_t>(run) * h.num_tiles + t) * dim +
+                         col,
+                     acc[0]);
+          }
+        }
+      }
+    }
+    __syncthreads();  // the next pass overwrites the staging area
+    base += nk;
+  }
+}
+
+template <int G, int VEC>
+__global__ __launch_bounds__(kHotCombineBlock) void HotCombine(HotArgs h,
+                                                               RowArgs r) {
+  using V = Vec<VEC>;
+  using T = typename V::T;
+  constexpr int P = kHotCombineBlock / G;
+  __shared__ T s_part[P][G];
+  const int32_t run = static_cast<int32_t>(blockIdx.x) / kHotCombineSplit;
+  const int part = static_cast<int>(blockIdx.x) % kHotCombineSplit;
+  if (run >= static_cast<int32_t>(*h.count) || h.run_bad[run] != 0) return;
+  const int tid = threadIdx.x;
+  const int sub = tid / G;
+  const int cl = tid % G;
+  const int32_t* off = h.tile_off + static_cast<int64_t>(run) *
+                                        (h.num_tiles + 1);
+  const int64_t dim = r.dim;
+  const float* part_rows = h.partials + static_cast<int64_t>(run) *
+                                            h.num_tiles * dim;
+  const int32_t chunk = (h.num_tiles + kHotCombineSplit - 1) / kHotCombineSplit;
+  const int32_t t0 = part * chunk;
+  const int32_t t1 = t0 + chunk < h.num_tiles ? t0 + chunk : h.num_tiles;
+  float* mid = h.partials2 + (static_cast<int64_t>(run) * kHotCombineSplit +
+                              part) * dim;
+  // This block's tiles: strided over the sub-groups (every partial row is
+  // loaded, its offsets settle whether it is added, so a thread's loads
+  // overlap), then the sub-groups joined by a tree.
+  for (int64_t col0 = 0; col0 < dim; col0 += static_cast<int64_t>(G) * VEC) {
+    const int64_t col = col0 + static_cast<int64_t>(cl) * VEC;
+    const bool col_ok = col < dim;
+    T acc = V::Zero();
+    if (col_ok) {
+#pragma unroll 4
+      for (int32_t t = t0 + sub; t < t1; t += P) {
+        const bool has = off[t + 1] > off[t];
+        const T v = V::Load(part_rows + static_cast<int64_t>(t) * dim + col);
+        acc = has ? V::Add(acc, v) : acc;
+      }
+    }
+    s_part[sub][cl] = acc;
+    __syncthreads();
+#pragma unroll
+    for (int w = P / 2; w > 0; w /= 2) {
+      if (sub < w) s_part[sub][cl] = V::Add(s_part[sub][cl], s_part[sub + w][cl]);
+      __syncthreads();
+    }
+    if (sub == 0 && col_ok) V::Store(mid + col, s_part[0][cl]);
+    __syncthreads();
+  }
+}
+
+// The kHotCombineSplit rows of each run in order, then the update.
+template <int G, int VEC, int EPI>
+__global__ __launch_bounds__(kBlock) void HotUpdate(HotArgs h, RowArgs r) {
+  using V = Vec<VEC>;
+  using T = typename V::T;
+  constexpr int P = kBlock / G;
+  __shared__ RowMapLds s_map;  // not read: the backward stores no activations
+  const int32_t run = static_cast<int32_t>(blockIdx.x) * P +
+                      static_cast<int32_t>(threadIdx.x) / G;
+  if (run >= static_cast<int32_t>(*h.count) || h.run_bad[run] != 0) return;
+  const int cl = threadIdx.x % G;
+  const int64_t dim = r.dim;
+  const uint32_t key = h.run_key[run];
+  const Hyper H = LoadHyper<EPI>(r.opt);
+  const float* rows = h.partials2 + static_cast<int64_t>(run) *
+                                        kHotCombineSplit * dim;
+  for (int64_t col0 = 0; col0 < dim; col0 += static_cast<int64_t>(G) * VEC) {
+    const int64_t col = col0 + static_cast<int64_t>(cl) * VEC;
+    if (col >= dim) continue;
+    T gsum = V::Load(rows + col);
+#pragma unroll
+    for (int k = 1; k < kHotCombineSplit; ++k) {
+      gsum = V::Add(gsum, V::Load(rows + k * dim + col));
+    }
+    EpilogueLoad<VEC, EPI, false>(r, s_map, key, col, gsum, H);
+  }
+}
+#endif  // __HIPCC_RTC__
+
+#ifndef __HIPCC_RTC__
+// ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------
 
@@ -1670,6 +2360,160 @@ int LaunchSegMapped(const StreamArgs& st, RowArgs r, const SegBuffers& sb,
   return Fail(SCEMB_ERR_INVALID_ARGUMENT, "unsupported layout");
 }
 
+// Hot-run reduction of a backward call (HotPoints ... HotCombine).
+// SCEMB_HOT_RUNS=0 switches it off, =1 on for every call that qualifies;
+// otherwise it runs when the activation gradients exceed kHotMinGradBytes
+// (the gathers of smaller ones are mostly served by the caches: at c3's
+// 33.5 MB per stack SegReduce saved 41 us for 102 us of hot-run kernels)
+// and a tile holds kHotMinTileRows samples at least (fewer make a run's
+// partial row per tile cost about what its gathers did).
+constexpr int64_t kHotMinGradBytes = 64ll << 20;
+constexpr int64_t kHotMinTileRows = 128;
+constexpr int64_t kHotPartialBudget = 128ll << 20;
+constexpr int64_t kHotTargetBlocks = 1024;
+constexpr int64_t kHotEntriesPerTile = 4;
+
+struct HotBuffers {
+  bool on = false;
+  int64_t point_blocks = 0;
+  HotArgs a{};
+};
+
+inline int HotRunsMode() {
+  const char* e = std::getenv("SCEMB_HOT_RUNS");
+  if (e == nullptr || *e == '\0') return -1;
+  return e[0] == '0' ? 0 : 1;
+}
+
+// Decides whether the call reduces hot runs and carves their buffers.
+// `eligible`: the CSR is read in place with one segment and no minibatching,
+// about more than one entry per activation row, and a built-in update.
+HotBuffers TakeHotBuffers(Arena& ws, bool eligible, int64_t n, int64_t batch,
+                          int64_t dim) {
+  HotBuffers hb;
+  const int mode = HotRunsMode();
+  const int64_t row_bytes = dim * static_cast<int64_t>(sizeof(float));
+  if (!eligible || mode == 0 || n <= 0 || batch <= 0 ||
+      row_bytes > kHotTileBytes ||
+      (mode < 0 && batch * row_bytes < kHotMinGradBytes)) {
+    return hb;
+  }
+  HotArgs& a = hb.a;
+  const int64_t tile_rows = std::min<int64_t>(
+      {batch, kHotTileBytes / row_bytes, kHotChain * kHotAcc});
+  if (mode < 0 && tile_rows < kHotMinTileRows) return hb;
+  const int64_t tiles = CeilDiv(batch, tile_rows);
+  // A run's partial row per tile (written, then read) costs about what two
+  // gathered rows do: runs of a few entries per tile on average pay off.
+  const int64_t q = std::min<int64_t>(
+      RoundUp(std::max<int64_t>(kHotEntriesPerTile * tiles, kBlock), kBlock),
+      1 << 16);
+  const int64_t points = CeilDiv(n, q);
+  const int64_t point_blocks = CeilDiv(points, kHotPointBlock);
+  // Each run holds two sampled positions.
+  int64_t max_runs = std::min<int64_t>(
+      {kHotMaxRuns - 1, kHotPartialBudget / (tiles * row_bytes),
+       points / 2 + 1});
+  // SCEMB_HOT_MAX_RUNS: fewer runs per call (the rest stay with SegReduce).
+  if (const char* e = std::getenv("SCEMB_HOT_MAX_RUNS")) {
+    if (*e != '\0') max_runs = std::min<int64_t>(max_runs, std::atoll(e));
+  }
+  if (point_blocks > kHotMaxPointBlocks || max_runs < 1 ||
+      n >= (int64_t{1} << 31)) {
+    return hb;
+  }
+  hb.on = true;
+  hb.point_blocks = point_blocks;
+  a.q = q;
+  a.points = points;
+  a.seg_blocks = CeilDiv(n, kBlock);
+  a.max_runs = static_cast<int32_t>(max_runs);
+  a.tile_rows = static_cast<int32_t>(tile_rows);
+  a.num_tiles = static_cast<int32_t>(tiles);
+  a.num_groups = static_cast<int32_t>(std::min<int64_t>(
+      CeilDiv(kHotTargetBlocks, tiles), max_runs));
+  const int64_t words = point_blocks * (kHotPointBlock / kWave);
+  a.first_mask = ws.Take<uint64_t>(words);
+  a.last_mask = ws.Take<uint64_t>(words);
+  a.first_count = ws.Take<uint32_t>(point_blocks);
+  a.last_count = ws.Take<uint32_t>(point_blocks);
+  a.count = ws.Take<uint32_t>(1);
+  a.run_key = ws.Take<uint32_t>(max_runs);
+  a.run_start = ws.Take<int32_t>(max_runs);
+  a.run_end = ws.Take<int32_t>(max_runs);
+  a.run_bad = ws.Take<uint32_t>(max_runs);
+  a.hot_head = ws.Take<uint32_t>(a.seg_blocks);
+  a.hot_tail = ws.Take<uint32_t>(a.seg_blocks);
+  a.tile_off = ws.Take<int32_t>(max_runs * (tiles + 1));
+  a.partials = ws.Take<float>(max_runs * tiles * dim);
+  a.partials2 = ws.Take<float>(max_runs * kHotCombineSplit * dim);
+  return hb;
+}
+
+// Finds the hot runs and marks their entries for SegReduce (before it).
+inline int LaunchHotPlan(StreamArgs* st, const HotBuffers& hb, uint32_t* status,
+                         hipStream_t stream) {
+  const HotArgs& a = hb.a;
+  int prof = ProfileBegin("bwd_hot_plan", stream);
+  hipLaunchKernelGGL(HotPoints, dim3(static_cast<uint32_t>(hb.point_blocks)),
+                     dim3(kHotPointBlock), 0, stream, *st, a);
+  SCEMB_LAUNCH_CHECK();
+  hipLaunchKernelGGL(HotPlan, dim3(static_cast<uint32_t>(a.max_runs)),
+                     dim3(kHotPlanBlock), 0, stream, *st, a, hb.point_blocks,
+                     status);
+  SCEMB_LAUNCH_CHECK();
+  const int64_t check_blocks = CeilDiv(a.seg_blocks * kBlock, kHotCheckSpan);
+  hipLaunchKernelGGL(HotCheck, dim3(static_cast<uint32_t>(check_blocks)),
+                     dim3(kBlock), 0, stream, *st, a);
+  SCEMB_LAUNCH_CHECK();
+  ProfileEnd(prof, stream);
+  st->hot_head = a.hot_head;
+  st->hot_tail = a.hot_tail;
+  st->run_bad = a.run_bad;
+  return 0;
+}
+
+// Reduces the hot runs and updates their rows (after SegReduce, or before:
+// the two touch disjoint table rows).
+template <int EPI>
+int LaunchHotReduce(const StreamArgs& st, const RowArgs& r,
+                    const HotBuffers& hb, int g, int vec, bool mapped,
+                    hipStream_t stream) {
+  const HotArgs& a = hb.a;
+  const dim3 tiles(static_cast<uint32_t>(a.num_tiles * a.num_groups));
+  const dim3 runs(static_cast<uint32_t>(a.max_runs * kHotCombineSplit));
+  const dim3 updates(static_cast<uint32_t>(CeilDiv(a.max_runs, kBlock / g)));
+  int prof = ProfileBegin("bwd_hot_reduce", stream);
+#define SCEMB_HOT_CASE(GG, VV)                                              \
+  if (g == GG && vec == VV) {                                               \
+    if (mapped) {                                                           \
+      hipLaunchKernelGGL((HotTile<GG, VV, true>), tiles, dim3(kHotTileBlock), \
+                         0, stream, st, a, r);                              \
+    } else {                                                                \
+      hipLaunchKernelGGL((HotTile<GG, VV, false>), tiles,                   \
+                         dim3(kHotTileBlock), 0, stream, st, a, r);         \
+    }                                                                       \
+    SCEMB_LAUNCH_CHECK();                                                   \
+    hipLaunchKernelGGL((HotCombine<GG, VV>), runs, dim3(kHotCombineBlock),  \
+                       0, stream, a, r);                                    \
+    SCEMB_LAUNCH_CHECK();                                                   \
+    hipLaunchKernelGGL((HotUpdate<GG, VV, EPI>), updates, dim3(kBlock), 0,  \
+                       stream, a, r);                                       \
+    SCEMB_LAUNCH_CHECK();                                                   \
+    ProfileEnd(prof, stream);                                               \
+    return 0;                                                               \
+  }
+  if constexpr (!IsCustom<EPI>()) {
+    SCEMB_HOT_CASE(4, 1) SCEMB_HOT_CASE(8, 1) SCEMB_HOT_CASE(16, 1)
+    SCEMB_HOT_CASE(32, 1) SCEMB_HOT_CASE(64, 1) SCEMB_HOT_CASE(4, 4)
+    SCEMB_HOT_CASE(8, 4) SCEMB_HOT_CASE(16, 4) SCEMB_HOT_CASE(32, 4)
+    SCEMB_HOT_CASE(64, 4)
+  }
+#undef SCEMB_HOT_CASE
+  ProfileEnd(prof, stream);
+  return Fail(SCEMB_ERR_INVALID_ARGUMENT, "unsupported layout");
+}
+
 // Launches SegReduce + SegFinish for the layout picked for `dim`; `one_hot`
 // selects the wide unroll, `mapped` the kernels that address activations
 // through the row map in `r.act` (which may hold no block at all).
@@ -1735,6 +2579,13 @@ int GradImpl(const GradCall& c) {
     st.src_rows = batch;
   }
   const SegBuffers sb = TakeSegBuffers(ws, n, dim);
+  // Entries per activation row: how often each gradient row is gathered.
+  const int64_t entries =
+      csr->num_entries > 0 && csr->num_entries < n ? csr->num_entries : n;
+  const bool one_hot = entries <= kOneHotMaxEntriesPerRow * batch;
+  const HotBuffers hb = TakeHotBuffers(
+      ws, direct && csr->num_minibatches == 0 && !one_hot && !IsCustom<EPI>(),
+      n, batch, dim);
   if (ws.measuring()) return 0;
   if (ws.overflow()) return Fail(SCEMB_ERR_WORKSPACE, "workspace too small");
   if (n == 0 || batch == 0) return 0;
@@ -1748,10 +2599,6 @@ int GradImpl(const GradCall& c) {
   r.opt = c.opt;
   r.status = c.status;
   if (c.map != nullptr) r.act = *c.map;
-  // Entries per activation row: how often each gradient row is gathered.
-  const int64_t entries =
-      csr->num_entries > 0 && csr->num_entries < n ? csr->num_entries : n;
-  const bool one_hot = entries <= kOneHotMaxEntriesPerRow * batch;
   r.stream_src = one_hot;
   int g, vec;
   PickLayout(dim,
@@ -1765,8 +2612,14 @@ int GradImpl(const GradCall& c) {
              &g, &vec);
   const bool mapped = c.map != nullptr;
   if (direct) {
-    return LaunchSeg<kSrcCsr, EPI>(st, r, sb, g, vec, one_hot, mapped,
-                                   "bwd_reduce", "bwd_finish", stream);
+    if (hb.on) {
+      rc = LaunchHotPlan(&st, hb, c.status, stream);
+      if (rc != 0) return rc;
+    }
+    rc = LaunchSeg<kSrcCsr, EPI>(st, r, sb, g, vec, one_hot, mapped,
+                                 "bwd_reduce", "bwd_finish", stream);
+    if (rc != 0 || !hb.on) return rc;
+    return LaunchHotReduce<EPI>(st, r, hb, g, vec, mapped, stream);
   }
   return LaunchSeg<kSrcSorted, EPI>(st, r, sb, g, vec, one_hot, mapped,
                                     "bwd_reduce", "bwd_finish", stream);
