@@ -396,6 +396,14 @@ struct Vec<4> {
     const NativeF4 w = {v.x, v.y, v.z, v.w};
     __builtin_nontemporal_store(w, reinterpret_cast<NativeF4*>(p));
   }
+  // acc + g * v with one rounding per component (the hot-run reduction).
+  __device__ static T Fused(T acc, float g, T v) {
+    acc.x = __builtin_fmaf(g, v.x, acc.x);
+    acc.y = __builtin_fmaf(g, v.y, acc.y);
+    acc.z = __builtin_fmaf(g, v.z, acc.z);
+    acc.w = __builtin_fmaf(g, v.w, acc.w);
+    return acc;
+  }
   __device__ static T Fma(T acc, float g, T v) {
     acc.x = acc.x + g * v.x;
     acc.y = acc.y + g * v.y;
@@ -429,6 +437,9 @@ struct Vec<1> {
     __builtin_nontemporal_store(v, p);
   }
   __device__ static T Fma(T acc, float g, T v) { return acc + g * v; }
+  __device__ static T Fused(T acc, float g, T v) {
+    return __builtin_fmaf(g, v, acc);
+  }
   __device__ static T Add(T a, T b) { return a + b; }
   __device__ static float Get(const T& v, int) { return v; }
   __device__ static void Set(T& v, int, float x) { v = x; }
@@ -1872,36 +1883,63 @@ __global__ __launch_bounds__(kHotTileBlock) void HotTile(StreamArgs st,
   const int64_t stride = h.num_tiles + 1;
   const int sub = tid / G;
   const int cl = tid % G;
-  bool staged = false;
-  // The group's runs (g, g + ng, ...) in passes: each pass takes the
-  // longest prefix of the remaining runs whose padded entries in this tile
+  // Dense rows of 16-byte vectors: the tile is one contiguous range of the
+  // gradient matrix, copied into LDS by DMA loads (global_load_lds, 16
+  // bytes per lane to the wave's LDS base + 16 * lane) while the block
+  // reads its runs' ranges; the copy is waited for before the reduction.
+  const bool dma = !kMapped && VEC == 4 &&
+                   (reinterpret_cast<uintptr_t>(r.src) & 15u) == 0;
+  bool staged = dma;
+  if (dma) {
+    constexpr int kChunk = kWave * 16;  // bytes one wave copies at once
+    const int64_t bytes = static_cast<int64_t>(rows) * dim * sizeof(float);
+    const char* src = reinterpret_cast<const char*>(r.src + row0 * dim);
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    for (int64_t c = static_cast<int64_t>(wave) * kChunk; c < bytes;
+         c += static_cast<int64_t>(kWaves) * kChunk) {
+      if (c + lane * 16 < bytes) {
+        __builtin_amdgcn_global_load_lds(
+            src + c + lane * 16, reinterpret_cast<char*>(s_tile) + c, 16, 0,
+            0);
+      }
+    }
+  }
+  // The group's runs (g, g + ng, ...), up to kHotTileBlock at a time, one
+  // per thread (its entry range in this tile read once), in passes: each
+  // pass takes the longest prefix of the remaining runs whose padded entries
   // fit the staging area (a run has at most one entry per sample, so at
   // most tile_rows, and kHotStage holds that padded: every pass takes one
   // run at least).
-  for (int32_t base = 0; base < mine;) {
-    const int32_t avail = mine - base < kHotPassRuns ? mine - base
-                                                     : kHotPassRuns;
+  for (int32_t chunk = 0; chunk < mine; chunk += kHotTileBlock) {
+    const int32_t avail = mine - chunk < kHotTileBlock ? mine - chunk
+                                                       : kHotTileBlock;
     int32_t j0 = 0, len = 0;
     if (tid < avail) {
-      const int32_t run = g + (base + tid) * ng;
+      const int32_t run = g + (chunk + tid) * ng;
       if (h.run_bad[run] == 0) {
         const int32_t* off = h.tile_off + run * stride;
         j0 = off[t];
         len = off[t + 1] - j0;
       }
     }
-    const int32_t padded = (len + kHotAcc - 1) / kHotAcc * kHotAcc;
+  for (int32_t lo = 0; lo < avail;) {
+    const int32_t mine_k = tid - lo;  // this thread's run within the pass
+    const bool live = tid >= lo && tid < avail && mine_k < kHotPassRuns;
+    const int32_t padded =
+        live ? (len + kHotAcc - 1) / kHotAcc * kHotAcc : 0;
     int32_t total;
     const int32_t excl =
         BlockExclusiveScan<int32_t, kHotTileBlock>(padded, s_scan, &total);
-    const int32_t nk =
-        __syncthreads_count(tid < avail && excl + padded <= kHotStage);
-    if (tid <= nk) s_pos[tid] = excl;  // thread nk holds the pass's end
-    if (tid < nk) {
-      s_j0[tid] = j0;
-      s_len[tid] = len;
+    const int32_t nk = __syncthreads_count(live && excl + padded <= kHotStage);
+    if (live && mine_k < nk) {
+      s_pos[mine_k] = excl;
+      if (mine_k == nk - 1) s_pos[nk] = excl + padded;  // the pass's end
+      s_j0[mine_k] = j0;
+      s_len[mine_k] = len;
     }
     __syncthreads();
+    const int32_t base = chunk + lo;
     const int32_t staged_entries = s_pos[nk];
     if (staged_entries > 0) {
       if (!staged) {
@@ -1974,6 +2012,7 @@ __global__ __launch_bounds__(kHotTileBlock) void HotTile(StreamArgs st,
           }
         }
       }
+      if (dma) __builtin_amdgcn_s_waitcnt(0);  // this wave's tile copies
       __syncthreads();
       for (int64_t col0 = 0; col0 < dim;
            col0 += static_cast<int64_t>(G) * VEC) {
@@ -2004,7 +2043,7 @@ __global__ __launch_bounds__(kHotTileBlock) void HotTile(StreamArgs st,
             for (int u = 0; u < kHotAcc; ++u) v[u] = V::Load(tile_col + ro[u]);
 #pragma unroll
             for (int u = 0; u < kHotAcc; ++u) {
-              acc[u] = V::Fma(acc[u], gu[u], v[u]);
+              acc[u] = V::Fused(acc[u], gu[u], v[u]);
             }
           }
 #pragma unroll
@@ -2023,8 +2062,11 @@ __global__ __launch_bounds__(kHotTileBlock) void HotTile(StreamArgs st,
       }
     }
     __syncthreads();  // the next pass overwrites the staging area
-    base += nk;
+    lo += nk;
   }
+  }
+  // A block with nothing to add still waits for its copies before it ends.
+  if (dma) __builtin_amdgcn_s_waitcnt(0);
 }
 
 template <int G, int VEC>
