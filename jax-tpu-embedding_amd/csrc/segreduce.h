@@ -1916,12 +1916,15 @@ __global__ __launch_bounds__(kHotTileBlock) void HotTile(StreamArgs st,
                                                        : kHotTileBlock;
     int32_t j0 = 0, len = 0;
     if (tid < avail) {
+      // The three loads together: a bad run's offsets are in the buffer
+      // (possibly stale) and dropped after.
       const int32_t run = g + (chunk + tid) * ng;
-      if (h.run_bad[run] == 0) {
-        const int32_t* off = h.tile_off + run * stride;
-        j0 = off[t];
-        len = off[t + 1] - j0;
-      }
+      const int32_t* off = h.tile_off + run * stride;
+      const uint32_t bad = h.run_bad[run];
+      const int32_t a = off[t];
+      const int32_t z = off[t + 1];
+      j0 = bad == 0 ? a : 0;
+      len = bad == 0 ? z - a : 0;
     }
   for (int32_t lo = 0; lo < avail;) {
     const int32_t mine_k = tid - lo;  // this thread's run within the pass
@@ -2409,7 +2412,7 @@ int LaunchSegMapped(const StreamArgs& st, RowArgs r, const SegBuffers& sb,
 // 33.5 MB per stack SegReduce saved 41 us for 102 us of hot-run kernels)
 // and a tile holds kHotMinTileRows samples at least (fewer make a run's
 // partial row per tile cost about what its gathers did).
-constexpr int64_t kHotMinGradBytes = 64ll << 20;
+constexpr int64_t kHotMinGradBytes = 64'000'000;
 constexpr int64_t kHotMinTileRows = 128;
 constexpr int64_t kHotPartialBudget = 128ll << 20;
 constexpr int64_t kHotTargetBlocks = 1024;
