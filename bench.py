@@ -559,7 +559,7 @@ def run_gpu(w: Workload, steps: int, warmup: int, probe: bool = False,
         f"dropped {mb['dropped']}")
   spans = {}
   for k in ("fwd_reduce", "fwd_finish", "bwd_reduce", "bwd_finish",
-            "fwd_call", "bwd_call"):
+            "bwd_hot_plan", "bwd_hot_reduce", "fwd_call", "bwd_call"):
     ms, n = _native.profile_collect(k)
     # Per step, summed over the stacks (one launch per stack and step).
     spans[k] = (ms / steps if n else 0.0, n)
@@ -1139,14 +1139,18 @@ def main():
   step_s = res["ms_per_step"] / 1e3
   sp = res["spans"]
   # Each op is one SegReduce launch plus one SegFinish launch (the finish
-  # kernel completes the rows whose entries span several blocks).
+  # kernel completes the rows whose entries span several blocks); the
+  # backward adds its hot-run launches where they run (0 otherwise).
   fwd_ms = sp["fwd_reduce"][0] + sp["fwd_finish"][0]
-  bwd_ms = sp["bwd_reduce"][0] + sp["bwd_finish"][0]
+  hot_ms = sp["bwd_hot_plan"][0] + sp["bwd_hot_reduce"][0]
+  bwd_ms = sp["bwd_reduce"][0] + sp["bwd_finish"][0] + hot_ms
   traffic = profiled_traffic() if w.name == "dlrm26" else None
   opts = sorted({s["optimizer"] for s in res["per_stack"].values()})
   if bwd_ms >= fwd_ms:
+    hot = " + hot runs" if hot_ms > 0 else ""
     dom, dom_ms, dom_bytes = (
-        f"bwd: SegReduce+SegFinish ({'/'.join(opts)})", bwd_ms, bwd_bytes)
+        f"bwd: SegReduce+SegFinish{hot} ({'/'.join(opts)})", bwd_ms,
+        bwd_bytes)
     dom_traffic = traffic["bwd"] if traffic else None
   else:
     dom, dom_ms, dom_bytes = "fwd: SegReduce+SegFinish", fwd_ms, fwd_bytes
