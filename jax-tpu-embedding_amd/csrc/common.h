@@ -33,6 +33,14 @@ int Fail(int code, const std::string& msg);
 int ProfileBegin(const char* name, hipStream_t stream);
 void ProfileEnd(int token, hipStream_t stream);
 
+// Runs work beside `stream`: *side (a stream of the current device, created
+// once, default priority) first waits for what `stream` has enqueued so far.
+// After enqueueing on *side, call JoinSide(stream) so that `stream` waits for
+// it. Returns 0 or an error code. One side stream per device: the calls that
+// fork from several streams share it and run one after another on it.
+int ForkSide(hipStream_t stream, hipStream_t* side);
+int JoinSide(hipStream_t stream);
+
 #define SCEMB_HIP(expr)                                                     \
   do {                                                                      \
     hipError_t e_ = (expr);                                                 \

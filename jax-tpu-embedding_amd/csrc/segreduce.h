@@ -2657,14 +2657,23 @@ int GradImpl(const GradCall& c) {
              &g, &vec);
   const bool mapped = c.map != nullptr;
   if (direct) {
-    if (hb.on) {
-      rc = LaunchHotPlan(&st, hb, c.status, stream);
-      if (rc != 0) return rc;
+    if (!hb.on) {
+      return LaunchSeg<kSrcCsr, EPI>(st, r, sb, g, vec, one_hot, mapped,
+                                     "bwd_reduce", "bwd_finish", stream);
     }
-    rc = LaunchSeg<kSrcCsr, EPI>(st, r, sb, g, vec, one_hot, mapped,
-                                 "bwd_reduce", "bwd_finish", stream);
-    if (rc != 0 || !hb.on) return rc;
-    return LaunchHotReduce<EPI>(st, r, hb, g, vec, mapped, stream);
+    rc = LaunchHotPlan(&st, hb, c.status, stream);
+    if (rc != 0) return rc;
+    // The hot runs and the cold entries update disjoint table rows: the
+    // hot-run reduction (LDS and ALU bound) runs beside SegReduce (memory
+    // bound) on a side stream, joined before the call returns.
+    hipStream_t side = nullptr;
+    rc = ForkSide(stream, &side);
+    if (rc != 0) return rc;
+    rc = LaunchHotReduce<EPI>(st, r, hb, g, vec, mapped, side);
+    const int rc_seg = LaunchSeg<kSrcCsr, EPI>(
+        st, r, sb, g, vec, one_hot, mapped, "bwd_reduce", "bwd_finish", stream);
+    const int rc_join = JoinSide(stream);
+    return rc != 0 ? rc : rc_seg != 0 ? rc_seg : rc_join;
   }
   return LaunchSeg<kSrcSorted, EPI>(st, r, sb, g, vec, one_hot, mapped,
                                     "bwd_reduce", "bwd_finish", stream);

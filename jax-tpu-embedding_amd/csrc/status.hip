@@ -59,6 +59,54 @@ void ProfileEnd(int token, hipStream_t stream) {
   }
 }
 
+namespace {
+constexpr int kMaxSideDevices = 64;
+struct SideState {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t join = nullptr;
+};
+std::mutex g_side_mu;
+SideState g_side[kMaxSideDevices];
+
+int SideOf(SideState** out) {
+  int dev = 0;
+  SCEMB_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxSideDevices) {
+    return Fail(SCEMB_ERR_INVALID_ARGUMENT, "device index out of range");
+  }
+  SideState& st = g_side[dev];
+  if (st.stream == nullptr) {
+    SCEMB_HIP(hipStreamCreateWithFlags(&st.stream, hipStreamNonBlocking));
+    SCEMB_HIP(hipEventCreateWithFlags(&st.fork, hipEventDisableTiming));
+    SCEMB_HIP(hipEventCreateWithFlags(&st.join, hipEventDisableTiming));
+  }
+  *out = &st;
+  return 0;
+}
+}  // namespace
+
+int ForkSide(hipStream_t stream, hipStream_t* side) {
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  SideState* st = nullptr;
+  const int rc = SideOf(&st);
+  if (rc != 0) return rc;
+  SCEMB_HIP(hipEventRecord(st->fork, stream));
+  SCEMB_HIP(hipStreamWaitEvent(st->stream, st->fork, 0));
+  *side = st->stream;
+  return 0;
+}
+
+int JoinSide(hipStream_t stream) {
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  SideState* st = nullptr;
+  const int rc = SideOf(&st);
+  if (rc != 0) return rc;
+  SCEMB_HIP(hipEventRecord(st->join, st->stream));
+  SCEMB_HIP(hipStreamWaitEvent(stream, st->join, 0));
+  return 0;
+}
+
 }  // namespace scemb
 
 extern "C" {

@@ -27,7 +27,8 @@ from jax_tpu_embedding.sparsecore.lib.nn import embedding  # pylint: disable=g-i
 from jax_tpu_embedding.sparsecore.lib.nn import embedding_spec  # pylint: disable=g-import-not-at-top,wrong-import-position
 
 
-def _workload(one_hot, seed=0, dims=(32, 32, 32), optimizer=None):
+def _workload(one_hot, seed=0, dims=(32, 32, 32), optimizer=None,
+              vocabs=(100, 5000, 70000)):
   rng = np.random.default_rng(seed)
   batch = 2048
   if optimizer is None:
@@ -37,7 +38,7 @@ def _workload(one_hot, seed=0, dims=(32, 32, 32), optimizer=None):
       initializer=embedding_spec.zeros,
       optimizer=optimizer, combiner="sum",
       max_ids_per_partition=1 << 16, max_unique_ids_per_partition=1 << 16)
-            for i, v in enumerate((100, 5000, 70000))]
+            for i, v in enumerate(vocabs)]
   feats = [embedding_spec.FeatureSpec(
       name=f"f{i}", table_spec=t, input_shape=[batch, 1],
       output_shape=[batch, t.embedding_dim]) for i, t in enumerate(tables)]
@@ -72,6 +73,32 @@ def test_graph_replays_equal_eager_steps(one_hot, dims):
   """With stacks of three widths the lookups and updates run on forked side
   streams (run_per_stack), so the graph also holds their fork and join."""
   _check_graph_replays(*_workload(one_hot, dims=dims))
+
+
+def test_graph_replays_with_hot_runs(monkeypatch):
+  """The backward's hot-run reduction forced on (a table of 8 ids holds runs
+  of hundreds of entries): its side stream's fork and join are captured
+  too, and every replay equals the eager step."""
+  monkeypatch.setenv("SCEMB_HOT_RUNS", "1")
+  from jax_tpu_embedding.sparsecore import _native  # pylint: disable=g-import-not-at-top
+  feats, pre, init, grads = _workload(False, seed=3, vocabs=(8, 5000, 70000))
+  _check_graph_replays(feats, pre, init, grads)
+  # The reduction ran: one eager backward with the launch spans on (not
+  # during capture, which would record the spans' events into the graph).
+  variables = {n: embedding.EmbeddingVariables(table=t.clone(),
+                                               slot=(a.clone(),))
+               for n, (t, a) in init.items()}
+  _native.profile_enable(True)
+  _native.profile_collect(None)
+  try:
+    embedding.tpu_sparse_dense_matmul_grad(
+        grads, pre, variables, feats, global_device_count=1,
+        num_sc_per_device=1)
+    torch.cuda.synchronize()
+    assert _native.profile_collect("bwd_hot_reduce")[1] > 0
+  finally:
+    _native.profile_collect(None)
+    _native.profile_enable(False)
 
 
 def _custom_adagrad(grad, table, accum, lr):
