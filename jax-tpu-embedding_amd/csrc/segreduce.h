@@ -2669,9 +2669,9 @@ int GradImpl(const GradCall& c) {
     hipStream_t side = nullptr;
     rc = ForkSide(stream, &side);
     if (rc != 0) return rc;
-    rc = LaunchHotReduce<EPI>(st, r, hb, g, vec, mapped, side);
     const int rc_seg = LaunchSeg<kSrcCsr, EPI>(
         st, r, sb, g, vec, one_hot, mapped, "bwd_reduce", "bwd_finish", stream);
+    rc = LaunchHotReduce<EPI>(st, r, hb, g, vec, mapped, side);
     const int rc_join = JoinSide(stream);
     return rc != 0 ? rc : rc_seg != 0 ? rc_seg : rc_join;
   }
