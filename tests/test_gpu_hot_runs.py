@@ -20,7 +20,7 @@ runs in seconds, check through a profiling span that it ran, and compare:
     or bad samples keep a run with the per-entry reduction: exact, the bad
     entry reported as without the hot path); a key order violation next to
     a hot run, still reported; fewer runs taken than found
-    (SCEMB_HOT_MAX_RUNS); a buffer of padding only.
+    (SCEMB_HOT_MAX_RUNS); two partitions; a buffer of padding only.
 """
 
 import numpy as np
@@ -352,6 +352,48 @@ def test_fewer_runs_taken_than_found(hot, max_runs):
     (got, exp), = _grad("sgd", csr, grad, table0, None, 0.25)
   assert h.count == 1
   np.testing.assert_array_equal(got, exp)
+
+
+def test_two_partitions(hot):
+  """Hot runs in both partitions of one segment, with the alignment gap
+  between them: keys are partition * rows_per_partition + id."""
+  rng = np.random.default_rng(71)
+  batch, dim, rpp = 2048, 8, 32
+  parts = [[(2, _sorted_samples(rng, batch, 1500)),
+            (5, _sorted_samples(rng, batch, 40)),
+            (7, _sorted_samples(rng, batch, 1500))],
+           [(1, _sorted_samples(rng, batch, 1500)),
+            (9, _sorted_samples(rng, batch, 1200))]]
+  eid, sid, rp = [], [], []
+  for runs in parts:
+    start = (len(eid) + 7) // 8 * 8
+    pad = start - len(eid)
+    eid += [np.iinfo(np.int32).max] * pad
+    sid += [np.iinfo(np.int32).max] * pad
+    for r, samples in runs:
+      eid += [r] * len(samples)
+      sid += list(samples)
+    rp.append(len(eid))
+  rp = np.array(rp + [rp[-1]] * (8 - len(rp)), np.int32)
+  eid = np.array(eid, np.int32)
+  sid = np.array(sid, np.int32)
+  gains = np.ones(len(eid), np.float32)
+  assert len(eid) > 2 * batch  # the multi-hot kernels
+  table0, grad = _integer_case(rng, batch, dim, 2 * rpp)
+  keep, c = _device.csr_operands(rp, eid, sid, gains, 1, 2,
+                                 sorted_by_row=True, num_entries=len(eid))
+  table = torch.from_numpy(table0.copy()).cuda()
+  status = torch.zeros(1, dtype=torch.int32, device="cuda")
+  with _HotLaunches() as h:
+    _native.sparse_dense_matmul_grad(c, torch.from_numpy(grad).cuda(), table,
+                                     None, 0.5, batch, device_status=status)
+  assert h.count == 1
+  del keep
+  assert int(status.item()) == 0
+  exp = refcpu.sparse_dense_matmul_grad(
+      rp, eid, sid, gains, grad, table0, None, learning_rate=0.5,
+      num_sc_per_device=1, num_scs=2)
+  np.testing.assert_array_equal(table.cpu().numpy(), exp)
 
 
 def test_padding_only(hot):
