@@ -2114,7 +2114,9 @@ __global__ __launch_bounds__(kHotCombineBlock) void HotCombine(HotArgs h,
     __syncthreads();
 #pragma unroll
     for (int w = P / 2; w > 0; w /= 2) {
-      if (sub < w) s_part[sub][cl] = V::Add(s_part[sub][cl], s_part[sub + w][cl]);
+      if (sub < w) {
+        s_part[sub][cl] = V::Add(s_part[sub][cl], s_part[sub + w][cl]);
+      }
       __syncthreads();
     }
     if (sub == 0 && col_ok) V::Store(mid + col, s_part[0][cl]);
