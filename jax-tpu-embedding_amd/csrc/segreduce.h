@@ -1508,8 +1508,8 @@ __global__ __launch_bounds__(kBlock) void SegFinish(int64_t num_blocks,
 // fails stays with SegReduce.
 //   HotPoints  the key of every q-th position; a run holding two such
 //              positions is hot. Bit masks of each run's first and last
-//              sampled position, counts per 256 positions, and the
-//              SegReduce blocks' hot marks cleared.
+//              sampled position and counts per 256 positions; one thread
+//              per SegReduce block clears its hot marks.
 //   HotPlan    one block per run: which sampled positions are its first and
 //              last, its exact bounds, the SegReduce blocks' hot marks.
 //   HotCheck   one thread per marked entry: same key, samples strictly
@@ -1579,11 +1579,13 @@ __global__ __launch_bounds__(kHotPointBlock) void HotPoints(StreamArgs st,
   __shared__ uint32_t s_cnt[2][kHotPointBlock / kWave];
   const int tid = threadIdx.x;
   const int64_t i = static_cast<int64_t>(blockIdx.x) * kHotPointBlock + tid;
-  const int64_t per = h.q / kBlock;
-  for (int64_t b = i * per; b < (i + 1) * per && b < h.seg_blocks; ++b) {
-    h.hot_head[b] = 0;
-    h.hot_tail[b] = kBlock;
+  // One thread per SegReduce block clears its marks (the grid covers the
+  // larger of the two counts); the first blocks also sample the keys.
+  if (i < h.seg_blocks) {
+    h.hot_head[i] = 0;
+    h.hot_tail[i] = kBlock;
   }
+  if (static_cast<int64_t>(blockIdx.x) * kHotPointBlock >= h.points) return;
   int32_t d;
   s_k[tid + 1] =
       i < h.points ? CsrKeySample(st, i * h.q, &d, nullptr) : kSkip;
@@ -2502,7 +2504,9 @@ inline int LaunchHotPlan(StreamArgs* st, const HotBuffers& hb, uint32_t* status,
                          hipStream_t stream) {
   const HotArgs& a = hb.a;
   int prof = ProfileBegin("bwd_hot_plan", stream);
-  hipLaunchKernelGGL(HotPoints, dim3(static_cast<uint32_t>(hb.point_blocks)),
+  const int64_t point_grid =
+      std::max<int64_t>(hb.point_blocks, CeilDiv(a.seg_blocks, kHotPointBlock));
+  hipLaunchKernelGGL(HotPoints, dim3(static_cast<uint32_t>(point_grid)),
                      dim3(kHotPointBlock), 0, stream, *st, a);
   SCEMB_LAUNCH_CHECK();
   hipLaunchKernelGGL(HotPlan, dim3(static_cast<uint32_t>(a.max_runs)),
