@@ -269,7 +269,15 @@ int scemb_build_sample_view(const scemb_csr_t* csr, int64_t device_batch_size,
  * row's gradient is summed in a fixed order (pieces of consecutive entries,
  * added in a fixed tree) and the row is updated once. With
  * SCEMB_CSR_SORTED_BY_ROW and one segment the CSR is read in place; else the
- * call sorts a copy of the entries by table row. */
+ * call sorts a copy of the entries by table row. A CSR read in place
+ * without minibatching, with several entries per activation row, may have
+ * its long runs (entries ascending by sample, checked) reduced per sample
+ * tile instead. The tile sums use fused multiply-adds: the same fixed-order
+ * guarantee, different rounding. The environment variables
+ * SCEMB_HOT_RUNS (0 off, 1 whenever eligible, unset: activation gradients
+ * over 64 MB and tiles of 128 samples or more) and SCEMB_HOT_MAX_RUNS decide
+ * it. The workspace size then includes its buffers, so they must not change
+ * between sizing and the call. */
 size_t scemb_sparse_dense_matmul_grad_workspace_size(const scemb_csr_t* csr,
                                                      int64_t device_batch_size,
                                                      int64_t table_rows,
