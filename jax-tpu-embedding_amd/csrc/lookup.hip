@@ -141,7 +141,7 @@ struct StreamSink {
 // passes: each bucket's elements arrive in CSR order and keep it.
 int GroupByRowInBuckets(const CsrRowSource& src, int64_t n,
                         const uint32_t* n_dev, int n_dev_words, int bits,
-                        int64_t batch,
+                        int64_t batch, bool try_unique,
                         const SortBuffers& b, Arena& ws, hipStream_t stream) {
   using radix::kSortBlock;
   using radix::kSortTile;
@@ -176,7 +176,7 @@ int GroupByRowInBuckets(const CsrRowSource& src, int64_t n,
   hipLaunchKernelGGL(
       (radix::RadixBucketSortK<uint32_t, uint64_t, StreamSink>),
       dim3(buckets), dim3(radix::kBucketBlock), 0, stream, b.keys_alt,
-      b.pay_alt, sink, hist, tiles, buckets, total, lb, n, true);
+      b.pay_alt, sink, hist, tiles, buckets, total, lb, n, true, try_unique);
   SCEMB_LAUNCH_CHECK();
   return 0;
 }
@@ -204,8 +204,13 @@ int GroupByRow(const scemb_csr_t* csr, const Geometry& geo, int64_t batch,
       bits <= radix::kMaxDigitBits + radix::kBucketMaxBits) {
     const CsrRowSource src{MakeCsr(csr), geo.bps, geo.rows_per_partition,
                            status};
-    return GroupByRowInBuckets(src, n, csr_end, csr_end_words, bits, batch, b,
-                               ws, stream);
+    // No more entries than activation rows: the buckets first try to place
+    // entries by key (RadixBucketSortK), which needs no ranking when no key
+    // repeats.
+    const int64_t entries =
+        csr->num_entries > 0 && csr->num_entries < n ? csr->num_entries : n;
+    return GroupByRowInBuckets(src, n, csr_end, csr_end_words, bits, batch,
+                               entries <= batch, b, ws, stream);
   }
   const radix::DigitPlan plan = radix::PlanDigits(bits);
   const int64_t tiles = CeilDiv(n, kSortTile);

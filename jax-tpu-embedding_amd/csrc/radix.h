@@ -451,7 +451,7 @@ __device__ __forceinline__ void BucketSort(
     const K* keys, const V* vals, const Sink& sink, int64_t lo, int64_t hi,
     int d, int lb, uint16_t (*sk)[kBucketChunk], uint16_t (*si)[kBucketChunk],
     uint16_t (*wcnt)[1 << kBucketDigitMax], uint32_t* next, uint16_t* head,
-    uint32_t* scan_tmp) {
+    uint32_t* scan_tmp, bool try_unique) {
   constexpr int kPer = kBucketChunk / kBucketBlock;  // elements per thread
   const int t = threadIdx.x;
   const int64_t size = hi - lo;
@@ -514,11 +514,46 @@ __device__ __forceinline__ void BucketSort(
       }
     }
     __syncthreads();
-    BucketLdsPass(sk, si, wcnt, scan_tmp, 0, m, 0, b0);
+    // A bucket of one chunk whose low keys never repeat (at most one entry
+    // per activation row) needs no ranking: a count per low key, then each
+    // present key's place is the number of present keys below it. Any
+    // repeat falls back to the ranked passes, with the same result.
+    bool placed = false;
+    if (try_unique && !chunked) {
+      for (int v = t; v < values; v += kBucketBlock) next[v] = 0;
+      __syncthreads();
+      bool dup = false;
+      for (int i = t; i < m; i += kBucketBlock) {
+        const uint32_t v = sk[0][i] & lmask;
+        dup = dup || atomicAdd(&next[v], 1u) != 0;
+        head[v] = static_cast<uint16_t>(i);
+      }
+      if (!__syncthreads_or(dup)) {
+        const int per = (values + kBucketBlock - 1) / kBucketBlock;
+        const int v0 = t * per;
+        uint32_t sum = 0;
+        for (int v = v0; v < v0 + per && v < values; ++v) sum += next[v];
+        uint32_t all;
+        uint32_t pos =
+            BlockExclusiveScan<uint32_t, kBucketBlock>(sum, scan_tmp, &all);
+        for (int v = v0; v < v0 + per && v < values; ++v) {
+          if (next[v] != 0 && pos < static_cast<uint32_t>(m)) {
+            sk[1][pos] = static_cast<uint16_t>(v);
+            si[1][pos] = head[v];
+            ++pos;
+          }
+        }
+        __syncthreads();
+        placed = true;
+      }
+    }
     int cur = 1;
-    if (b1 > 0) {
-      BucketLdsPass(sk, si, wcnt, scan_tmp, 1, m, b0, b1);
-      cur = 0;
+    if (!placed) {
+      BucketLdsPass(sk, si, wcnt, scan_tmp, 0, m, 0, b0);
+      if (b1 > 0) {
+        BucketLdsPass(sk, si, wcnt, scan_tmp, 1, m, b0, b1);
+        cur = 0;
+      }
     }
     // Every pair of [0, m) was placed; the masks below only keep LDS and
     // value reads in range whatever the keys hold.
@@ -570,7 +605,7 @@ template <typename K, typename V, typename Sink>
 __global__ __launch_bounds__(kBucketBlock) void RadixBucketSortK(
     const K* keys, const V* vals, Sink sink, const uint32_t* offsets,
     int64_t tiles, int buckets, const uint32_t* total, int lb, int64_t n,
-    bool fill_tail) {
+    bool fill_tail, bool try_unique) {
   __shared__ uint16_t sk[2][kBucketChunk];
   __shared__ uint16_t si[2][kBucketChunk];
   __shared__ uint16_t wcnt[kBucketWaves][1 << kBucketDigitMax];
@@ -586,7 +621,7 @@ __global__ __launch_bounds__(kBucketBlock) void RadixBucketSortK(
       d + 1 < buckets ? offsets[static_cast<int64_t>(d + 1) * tiles] : taken;
   if (hi > lo) {  // uniform: the whole block
     BucketSort<K, V, Sink>(keys, vals, sink, lo, hi, d, lb, sk, si, wcnt,
-                           next, head, scan_tmp);
+                           next, head, scan_tmp, try_unique);
   }
   if (fill_tail) {
     for (int64_t i = taken + static_cast<int64_t>(blockIdx.x) * kBucketBlock +

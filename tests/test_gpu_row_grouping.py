@@ -33,13 +33,16 @@ from jax_tpu_embedding.sparsecore.lib.core.primitives import _device  # pylint: 
 PAD = np.iinfo(np.int32).max
 
 
-def _csr(rng, num_sc, bps, rpp, entries, heavy=0, bad=0.0, tail=0):
+def _csr(rng, num_sc, bps, rpp, entries, heavy=0, bad=0.0, tail=0,
+         unique=False, repeat=False):
   """A CSR of `num_sc` segments with `num_sc` partitions each: partition
   entries ascending by id, 8-aligned starts, padding to the segment end.
   `heavy` entries go to sample 3 of every segment (one long row). `tail`:
   that many more positions at the end of each segment, filled with entries
   that look valid (ids and samples in range) but lie past the last
-  partition's row pointer, where the format leaves memory unwritten."""
+  partition's row pointer, where the format leaves memory unwritten.
+  `unique`: every activation row at most once per segment (one-hot rows);
+  `repeat` then gives one row a second entry."""
   parts = num_sc
   per_part = entries // (num_sc * parts)
   per_seg = (parts * ((per_part + heavy // parts + 7) // 8 * 8) + 64 + tail)
@@ -49,12 +52,18 @@ def _csr(rng, num_sc, bps, rpp, entries, heavy=0, bad=0.0, tail=0):
   rp = np.zeros((num_sc, parts), np.int32)
   for s in range(num_sc):
     start = 0
+    perm = rng.permutation(bps).astype(np.int32) if unique else None
     for p in range(parts):
       c = per_part + heavy // parts
       ids = np.sort(rng.integers(0, rpp, size=c)).astype(np.int32)
       if bad:
         ids[rng.random(c) < bad] = rpp + 5
-      rows = rng.integers(0, bps, size=c).astype(np.int32)
+      if unique:
+        rows = perm[p * c:(p + 1) * c].copy()
+        if repeat and p == 0:
+          rows[1] = rows[0]
+      else:
+        rows = rng.integers(0, bps, size=c).astype(np.int32)
       if heavy:
         rows[rng.permutation(c)[:heavy // parts]] = 3
       o = s * per_seg + start
@@ -92,11 +101,12 @@ def _expected(rp, eid, sid, gains, num_sc, bps, rpp, per_seg):
   return keys[order], ents[order]
 
 
-def _check(rng, num_sc, batch, entries, heavy=0, bad=0.0, tail=0):
+def _check(rng, num_sc, batch, entries, heavy=0, bad=0.0, tail=0,
+           unique=False, repeat=False):
   bps = batch // num_sc
   rpp = 5000
   rp, eid, sid, gains, per_seg = _csr(rng, num_sc, bps, rpp, entries, heavy,
-                                      bad, tail)
+                                      bad, tail, unique, repeat)
   keep, c = _device.csr_operands(rp, eid, sid, gains, num_sc, num_sc)
   status = torch.zeros(1, dtype=torch.int32, device="cuda")
   v = _native.build_sample_view(c, batch, rpp * num_sc, device_status=status)
@@ -122,6 +132,17 @@ def _check(rng, num_sc, batch, entries, heavy=0, bad=0.0, tail=0):
     (1 << 20, 300000), (1703936, 1703936), (2500000, 600000)])
 def test_stream_is_the_stable_row_sort(batch, entries):
   _check(np.random.default_rng(batch), 1, batch, entries)
+
+
+@pytest.mark.parametrize("repeat", [False, True])
+@pytest.mark.parametrize("batch,entries", [
+    (1000, 900), (8192, 8192), (500000, 300000), (1703936, 1703936)])
+def test_rows_of_one_entry(batch, entries, repeat):
+  """At most one entry per activation row: the buckets place entries by key
+  without ranking. One repeated row sends its bucket back to the ranked
+  passes (the others are still placed), with the same stream."""
+  _check(np.random.default_rng(batch + 5), 1, batch, entries, unique=True,
+         repeat=repeat)
 
 
 @pytest.mark.parametrize("batch", [4000, 70000, 1703936])
